@@ -1,0 +1,71 @@
+// Shared device/host helpers for the gfx950 K-quant kernels.
+// Compiled with -ffp-contract=off: every fp32 expression below rounds each
+// operation separately unless an fma builtin is written explicitly.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/kq_capi.h"
+
+#define KQ_QK 256
+
+typedef _Float16 kq_half;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+// 16-byte loads at addresses that are only 2-byte aligned (Q6_K / IQ2_XXS
+// blocks of 210 / 66 bytes): gfx950 global loads accept them.
+typedef uint32_t u32x4_a2 __attribute__((ext_vector_type(4), aligned(2)));
+typedef uint32_t u32x2_a2 __attribute__((ext_vector_type(2), aligned(2)));
+typedef uint32_t u32_a2 __attribute__((aligned(2)));
+
+__host__ __device__ constexpr int kq_block_bytes(int codec) {
+    return codec == KQ_CODEC_Q4_K ? 144 : codec == KQ_CODEC_Q6_K ? 210 : codec == KQ_CODEC_IQ2_XXS ? 66 : 0;
+}
+
+__device__ __forceinline__ float kq_f16_bits_to_f32(uint32_t bits16) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+
+__device__ __forceinline__ uint32_t kq_f32_to_f16_bits(float f) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// fp32 -> bf16 round-to-nearest-even (NaN kept quiet).
+__host__ __device__ __forceinline__ uint16_t kq_f32_to_bf16_bits(float f) {
+    uint32_t u = __builtin_bit_cast(uint32_t, f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float kq_bf16_bits_to_f32(uint32_t b) {
+    return __builtin_bit_cast(float, b << 16);
+}
+
+__device__ __forceinline__ void kq_store_out(void *out, int dtype, int64_t i, float v) {
+    if (dtype == KQ_DTYPE_F32) {
+        ((float *)out)[i] = v;
+    } else if (dtype == KQ_DTYPE_F16) {
+        ((_Float16 *)out)[i] = (_Float16)v;
+    } else {
+        ((uint16_t *)out)[i] = kq_f32_to_bf16_bits(v);
+    }
+}
+
+// Packed fp16 pair from two bytes already in [0, 63]: lanes hold 1024 + byte.
+// sel picks the two source bytes (0..3) for the low / high half.
+__device__ __forceinline__ uint32_t kq_bytes_to_h2_biased(uint32_t bytes, uint32_t sel) {
+    return __builtin_amdgcn_perm(0x64646464u, bytes, sel);
+}
+// selectors: result byte0 = src byte a, byte1 = 0x64, byte2 = src byte b, byte3 = 0x64
+#define KQ_SEL_B01 0x04010400u
+#define KQ_SEL_B23 0x04030402u
+
+__device__ __forceinline__ half2_t kq_as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+__device__ __forceinline__ uint32_t kq_h2_bits(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+
+// Wave-level helpers (wave64).
+__device__ __forceinline__ int kq_lane() { return (int)__lane_id(); }

@@ -1,0 +1,610 @@
+// Dequant-fused quantized matmul: dense grouped problems (KQuantLinear /
+// kq.quantized_matmul) and the MoE expert gather family (kq.gather_qmm,
+// kq.moe_glu_gather_kq, kq.gather_qmv_kq, mix, router top-k).
+//
+// Work decomposition (one wave = one work unit, 64-thread workgroups so even
+// a 1024-row matrix spreads over all 256 CUs):
+//   unit = (problem, 16-row weight tile, K split), grid.y = 64-row batch chunk.
+// A unit streams its weight rows once for the whole batch chunk; K splits of
+// one tile are reduced deterministically: every split writes its fp32 partial
+// to the workspace, and the last split to arrive (agent-scope counter) sums
+// the partials in split order and writes the output.
+#include <stdlib.h>
+
+#include "kq_mma.h"
+
+namespace {
+
+using namespace kqmma;
+
+constexpr int kMaxChunk = 64;  // batch rows per grid.y chunk (4 m-tiles)
+
+struct DenseProblem {
+    const uint8_t *w;
+    const char *x;
+    void *y;
+    int64_t w_row_bytes, x_stride, y_stride;
+    int32_t M, N, K, codec;
+    int32_t n_tiles, k_splits, steps_per_split;
+    int32_t unit_begin;   // first unit id of this problem
+    int64_t part_off;     // float offset of this problem's partials in the workspace
+    int64_t ctr_off;      // u32 offset of this problem's counters
+};
+
+struct DenseArgs {
+    DenseProblem p[KQ_MAX_GROUP];
+    int32_t n_problems;
+    int32_t y_dtype;
+    float *parts;
+    uint32_t *ctrs;
+};
+
+__device__ __forceinline__ void store_tile(void *y, int y_dtype, int64_t y_stride, int m0, int M,
+                                           int n, bool n_valid, const floatx4 &c) {
+    const int lane = kq_lane();
+    if (!n_valid) return;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int m = m0 + 4 * (lane >> 4) + e;
+        if (m < M) kq_store_out(y, y_dtype, (int64_t)m * y_stride + n, c[e]);
+    }
+}
+
+// Split-K reduction for one unit's MT m-tiles.  Returns true when this wave
+// holds the final sums in `acc` (single split, or last arrival).
+template <int MT>
+__device__ __forceinline__ bool splitk_reduce(floatx4 (&acc)[MT], int k_splits, int ks,
+                                              float *part, uint32_t *ctr) {
+    if (k_splits == 1) return true;
+    const int lane = kq_lane();
+    float *mine = part + (int64_t)ks * (MT * 256);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) mine[(mt * 4 + e) * 64 + lane] = acc[mt][e];
+    __threadfence();
+    uint32_t old = 0;
+    if (lane == 0) old = atomicAdd(ctr, 1u);
+    old = __shfl(old, 0);
+    if (old != (uint32_t)(k_splits - 1)) return false;
+    __threadfence();
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = floatx4{0, 0, 0, 0};
+    for (int s = 0; s < k_splits; ++s) {
+        const float *src = part + (int64_t)s * (MT * 256);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                acc[mt][e] += __hip_atomic_load(src + (mt * 4 + e) * 64 + lane, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (lane == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+}
+
+template <int CODEC, int MT, int XT>
+__device__ __forceinline__ void dense_unit(const DenseArgs &a, const DenseProblem &p, int local_unit) {
+    const int lane = kq_lane();
+    const int r = lane & 15;
+    const int nt = local_unit / p.k_splits;
+    const int ks = local_unit - nt * p.k_splits;
+    const int mc = blockIdx.y;
+    const int m0 = mc * kMaxChunk;
+    if (m0 >= p.M) return;
+    const int n = nt * 16 + r;
+    const bool n_valid = n < p.N;
+    const int nb = p.K / KQ_QK;
+    const int kb0 = ks * p.steps_per_split * 4;
+    const int kb1 = min(nb, kb0 + p.steps_per_split * 4);
+    const uint8_t *wrow[1] = {p.w + (int64_t)(n_valid ? n : 0) * p.w_row_bytes};
+    const char *xrow[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const int m = m0 + 16 * mt + r;
+        xrow[mt] = m < p.M ? p.x + (int64_t)m * p.x_stride * x_elem_bytes<XT>() : nullptr;
+    }
+    floatx4 acc[1][MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[0][mt] = floatx4{0, 0, 0, 0};
+    tile_accumulate<CODEC, MT, XT, 1>(wrow, n_valid, kb0, kb1, xrow, acc);
+
+    const int64_t tile_id = (int64_t)mc * p.n_tiles + nt;
+    float *part = a.parts + p.part_off + tile_id * (int64_t)p.k_splits * (MT * 256);
+    uint32_t *ctr = a.ctrs + p.ctr_off + tile_id;
+    if (!splitk_reduce<MT>(acc[0], p.k_splits, ks, part, ctr)) return;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+        store_tile(p.y, a.y_dtype, p.y_stride, m0 + 16 * mt, p.M, n, n_valid, acc[0][mt]);
+}
+
+template <int MT, int XT>
+__global__ __launch_bounds__(64) void kq_dense_grouped_kernel(DenseArgs a) {
+    const int unit = blockIdx.x;
+    // Select the problem with static indices only: dynamic indexing of the
+    // by-value argument array would copy it to scratch memory.
+    DenseProblem p = a.p[0];
+#pragma unroll
+    for (int i = 1; i < KQ_MAX_GROUP; ++i)
+        if (i < a.n_problems && unit >= a.p[i].unit_begin) p = a.p[i];
+    const int local = unit - p.unit_begin;
+    switch (p.codec) {
+    case KQ_CODEC_Q4_K: dense_unit<KQ_CODEC_Q4_K, MT, XT>(a, p, local); break;
+    case KQ_CODEC_Q6_K: dense_unit<KQ_CODEC_Q6_K, MT, XT>(a, p, local); break;
+    default: dense_unit<KQ_CODEC_IQ2_XXS, MT, XT>(a, p, local); break;
+    }
+}
+
+// ---------------------------------------------------------------- MoE
+
+struct GatherArgs {
+    const char *x;
+    const uint8_t *w0, *w1;   // expert stacks (w1: up for the fused GLU)
+    void *y;                  // [n_pairs, N] (f32 for the GLU)
+    const int32_t *seg_info;  // [0] = S, then seg_expert[E], seg_start[E+1]
+    const int32_t *pair_order;
+    int64_t x_stride, w_expert_bytes, w_row_bytes, y_stride;
+    int32_t x_pair_div, N, K, n_pairs, n_experts, n_tiles, y_dtype, act;
+};
+
+__device__ __forceinline__ float act_apply(int act, float g) {
+    if (act == 0) return g / (1.0f + __expf(-g));  // silu
+    // gelu, tanh approximation
+    const float k0 = 0.7978845608028654f, k1 = 0.044715f;
+    const float u = k0 * (g + k1 * g * g * g);
+    return 0.5f * g * (1.0f + tanhf(u));
+}
+
+template <int CODEC, int MT, int XT, int NW>
+__global__ __launch_bounds__(64) void kq_gather_kernel(GatherArgs a) {
+    const int lane = kq_lane();
+    const int r = lane & 15;
+    const int slot = blockIdx.x / a.n_tiles;
+    const int nt = blockIdx.x - slot * a.n_tiles;
+    const int S = a.seg_info[0];
+    if (slot >= S) return;
+    const int expert = a.seg_info[1 + slot];
+    const int seg_begin = a.seg_info[1 + a.n_experts + slot];
+    const int seg_end = a.seg_info[1 + a.n_experts + slot + 1];
+    const int n = nt * 16 + r;
+    const bool n_valid = n < a.N;
+    const int nb = a.K / KQ_QK;
+    const uint8_t *wrow[NW];
+    wrow[0] = a.w0 + (int64_t)expert * a.w_expert_bytes + (int64_t)(n_valid ? n : 0) * a.w_row_bytes;
+    if constexpr (NW == 2)
+        wrow[1] = a.w1 + (int64_t)expert * a.w_expert_bytes + (int64_t)(n_valid ? n : 0) * a.w_row_bytes;
+    for (int c0 = seg_begin; c0 < seg_end; c0 += 16 * MT) {
+        const char *xrow[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const int ri = c0 + 16 * mt + r;
+            xrow[mt] = ri < seg_end
+                           ? a.x + (int64_t)(a.pair_order[ri] / a.x_pair_div) * a.x_stride * x_elem_bytes<XT>()
+                           : nullptr;
+        }
+        floatx4 acc[NW][MT];
+#pragma unroll
+        for (int i = 0; i < NW; ++i)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc[i][mt] = floatx4{0, 0, 0, 0};
+        tile_accumulate<CODEC, MT, XT, NW>(wrow, n_valid, 0, nb, xrow, acc);
+        if (!n_valid) continue;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int ri = c0 + 16 * mt + 4 * (lane >> 4) + e;
+                if (ri >= seg_end) continue;
+                const int pair = a.pair_order[ri];
+                float v = acc[0][mt][e];
+                if constexpr (NW == 2) v = act_apply(a.act, v) * acc[1][mt][e];
+                kq_store_out(a.y, a.y_dtype, (int64_t)pair * a.y_stride + n, v);
+            }
+        }
+    }
+}
+
+// Zero the outputs of pairs whose expert id is out of range (never routed).
+__global__ void kq_gather_zero_invalid(const int32_t *idx_sorted_flag, int32_t n_pairs, int32_t N,
+                                       void *y, int y_dtype, int64_t y_stride) {
+    const int p = blockIdx.x;
+    if (idx_sorted_flag[p] >= 0) return;
+    for (int n = threadIdx.x; n < N; n += blockDim.x) kq_store_out(y, y_dtype, (int64_t)p * y_stride + n, 0.f);
+}
+
+// Routing: one workgroup, counting sort of pairs by expert (stable by pair id).
+// seg_info = [S, seg_expert[E], seg_start[E+1]]; pair_order[n_pairs];
+// valid_flag[n_pairs] (appended after pair_order) = expert or -1.
+__global__ __launch_bounds__(1024) void kq_route_kernel(const int32_t *__restrict__ idx, int32_t n_pairs,
+                                                        int32_t n_experts, int32_t *__restrict__ seg_info,
+                                                        int32_t *__restrict__ pair_order) {
+    extern __shared__ int32_t sm[];
+    int32_t *count = sm;                 // [E]
+    int32_t *start = sm + n_experts;     // [E]
+    const int tid = threadIdx.x;
+    for (int e = tid; e < n_experts; e += blockDim.x) count[e] = 0;
+    __syncthreads();
+    for (int p = tid; p < n_pairs; p += blockDim.x) {
+        const int e = idx[p];
+        if (e >= 0 && e < n_experts) atomicAdd(&count[e], 1);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int acc = 0, s = 0;
+        for (int e = 0; e < n_experts; ++e) {
+            start[e] = acc;
+            if (count[e] > 0) {
+                seg_info[1 + s] = e;
+                seg_info[1 + n_experts + s] = acc;
+                ++s;
+            }
+            acc += count[e];
+        }
+        seg_info[0] = s;
+        for (int i = s; i <= n_experts; ++i) seg_info[1 + n_experts + i] = acc;
+        for (int i = s; i < n_experts; ++i) seg_info[1 + i] = -1;
+    }
+    __syncthreads();
+    int32_t *flag = pair_order + n_pairs;
+    for (int p = tid; p < n_pairs; p += blockDim.x) {
+        const int e = idx[p];
+        if (e < 0 || e >= n_experts) {
+            flag[p] = -1;
+            continue;
+        }
+        flag[p] = e;
+        int rank = 0;
+        for (int q = 0; q < p; ++q) rank += (idx[q] == e);
+        pair_order[start[e] + rank] = p;
+    }
+}
+
+__global__ void kq_mix_kernel(const float *__restrict__ yp, const float *__restrict__ sc, int32_t T,
+                              int32_t k, int32_t N, void *y, int y_dtype) {
+    const int t = blockIdx.y;
+    const int n = blockIdx.x * blockDim.x + threadIdx.x;
+    if (n >= N) return;
+    float acc = 0.f;
+    for (int s = 0; s < k; ++s) acc += sc[t * k + s] * yp[((int64_t)t * k + s) * N + n];
+    kq_store_out(y, y_dtype, (int64_t)t * N + n, acc);
+}
+
+// Router: one wave per token.  softmax over E logits in fp32, top-k by repeated
+// arg-max (ties -> lower expert id), optional renormalisation.
+__global__ __launch_bounds__(64) void kq_router_kernel(const void *logits, int ldt, int32_t E, int32_t k,
+                                                       int norm, int32_t *inds, float *scores) {
+    const int t = blockIdx.x;
+    const int lane = kq_lane();
+    constexpr int kMaxPerLane = 16;  // E <= 1024
+    float v[kMaxPerLane];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < kMaxPerLane; ++i) {
+        const int e = lane + 64 * i;
+        float x = -INFINITY;
+        if (e < E) {
+            const int64_t o = (int64_t)t * E + e;
+            x = ldt == KQ_DTYPE_F32 ? ((const float *)logits)[o]
+                : ldt == KQ_DTYPE_F16 ? (float)((const _Float16 *)logits)[o]
+                                      : kq_bf16_bits_to_f32(((const uint16_t *)logits)[o]);
+        }
+        v[i] = x;
+        mx = fmaxf(mx, x);
+    }
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < kMaxPerLane; ++i) {
+        const int e = lane + 64 * i;
+        v[i] = e < E ? expf(v[i] - mx) : -1.f;
+        if (e < E) sum += v[i];
+    }
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+#pragma unroll
+    for (int i = 0; i < kMaxPerLane; ++i)
+        if (lane + 64 * i < E) v[i] = v[i] / sum;
+    float picked_sum = 0.f;
+    for (int j = 0; j < k; ++j) {
+        float best = -2.f;
+        int bi = 0x7FFFFFFF;
+#pragma unroll
+        for (int i = 0; i < kMaxPerLane; ++i) {
+            const int e = lane + 64 * i;
+            if (e < E && (v[i] > best || (v[i] == best && e < bi))) {
+                best = v[i];
+                bi = e;
+            }
+        }
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ob = __shfl_xor(best, off);
+            const int oi = __shfl_xor(bi, off);
+            if (ob > best || (ob == best && oi < bi)) {
+                best = ob;
+                bi = oi;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kMaxPerLane; ++i)
+            if (lane + 64 * i == bi) v[i] = -1.f;
+        picked_sum += best;
+        if (lane == 0) {
+            inds[(int64_t)t * k + j] = bi;
+            scores[(int64_t)t * k + j] = best;
+        }
+    }
+    if (norm && lane == 0) {
+        for (int j = 0; j < k; ++j) scores[(int64_t)t * k + j] = scores[(int64_t)t * k + j] / picked_sum;
+    }
+}
+
+// ---------------------------------------------------------------- host
+
+int env_int(const char *name, int dflt) {
+    const char *s = getenv(name);
+    if (!s || !*s) return dflt;
+    char *end = nullptr;
+    const long v = strtol(s, &end, 10);
+    return (end && *end == 0 && v > 0 && v < (1 << 24)) ? (int)v : dflt;
+}
+
+struct Plan {
+    int n_tiles, k_splits, steps_per_split, mt, chunks;
+};
+
+Plan plan_problem(const kq_matmul_problem &q) {
+    Plan pl;
+    pl.n_tiles = (q.N + 15) / 16;
+    const int nb = q.K / KQ_QK;
+    const int steps = (nb + 3) / 4;
+    // Target enough waves per problem to keep every CU streaming.
+    const int target = env_int("GMLX_KQ_MM_WAVES", 1024);
+    int ks = (target + pl.n_tiles - 1) / pl.n_tiles;
+    ks = ks < 1 ? 1 : (ks > steps ? steps : ks);
+    pl.steps_per_split = (steps + ks - 1) / ks;
+    pl.k_splits = (steps + pl.steps_per_split - 1) / pl.steps_per_split;
+    const int mrows = q.M < kMaxChunk ? q.M : kMaxChunk;
+    pl.mt = (mrows + 15) / 16;
+    pl.chunks = (q.M + kMaxChunk - 1) / kMaxChunk;
+    return pl;
+}
+
+int validate_problem(const kq_matmul_problem &q) {
+    if (!q.w || !q.x || !q.y) return KQ_ERR_NULL_POINTER;
+    if (kq_block_bytes(q.codec) == 0) return KQ_ERR_UNSUPPORTED_CODEC;
+    if (q.M < 0 || q.N < 0 || q.K <= 0) return KQ_ERR_BAD_SHAPE;
+    if (q.K % KQ_QK) return KQ_ERR_BAD_SHAPE;
+    const int64_t need = (int64_t)(q.K / KQ_QK) * kq_block_bytes(q.codec);
+    if (q.w_row_bytes < need) return KQ_ERR_BAD_SHAPE;
+    if (q.x_row_stride < q.K || q.y_row_stride < q.N) return KQ_ERR_BAD_SHAPE;
+    if (((uintptr_t)q.x & 15) || (q.x_row_stride & 7)) return KQ_ERR_BAD_ALIGN;
+    if (q.codec == KQ_CODEC_Q4_K && (((uintptr_t)q.w & 15) || (q.w_row_bytes & 15))) return KQ_ERR_BAD_ALIGN;
+    if (((uintptr_t)q.w & 1) || (q.w_row_bytes & 1)) return KQ_ERR_BAD_ALIGN;
+    return KQ_OK;
+}
+
+size_t workspace_for(const kq_matmul_problem *ps, int n, int64_t *part_off, int64_t *ctr_off,
+                     size_t *ctr_bytes_out) {
+    int64_t floats = 0, ctrs = 0;
+    for (int i = 0; i < n; ++i) {
+        const Plan pl = plan_problem(ps[i]);
+        if (part_off) part_off[i] = floats;
+        if (ctr_off) ctr_off[i] = ctrs;
+        if (pl.k_splits > 1) {
+            floats += (int64_t)pl.chunks * pl.n_tiles * pl.k_splits * pl.mt * 256;
+            ctrs += (int64_t)pl.chunks * pl.n_tiles;
+        }
+    }
+    // counters first (zeroed region), then partials, 256-byte aligned
+    const size_t ctr_bytes = ((size_t)ctrs * 4 + 255) & ~(size_t)255;
+    if (ctr_bytes_out) *ctr_bytes_out = ctr_bytes;
+    return ctr_bytes + (size_t)floats * 4;
+}
+
+template <int MT, int XT>
+void launch_dense(const DenseArgs &a, int units, int chunks, hipStream_t s) {
+    hipLaunchKernelGGL((kq_dense_grouped_kernel<MT, XT>), dim3(units, chunks), dim3(64), 0, s, a);
+}
+
+template <int CODEC, int XT, int NW>
+void launch_gather_codec(int mt, const GatherArgs &a, int grid, hipStream_t s) {
+    switch (mt) {
+    case 1: hipLaunchKernelGGL((kq_gather_kernel<CODEC, 1, XT, NW>), dim3(grid), dim3(64), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((kq_gather_kernel<CODEC, 2, XT, NW>), dim3(grid), dim3(64), 0, s, a); break;
+    default: hipLaunchKernelGGL((kq_gather_kernel<CODEC, 4, XT, NW>), dim3(grid), dim3(64), 0, s, a); break;
+    }
+}
+
+template <int XT, int NW>
+void launch_gather(int codec, int mt, const GatherArgs &a, int grid, hipStream_t s) {
+    if (codec == KQ_CODEC_Q4_K) launch_gather_codec<KQ_CODEC_Q4_K, XT, NW>(mt, a, grid, s);
+    else if (codec == KQ_CODEC_Q6_K) launch_gather_codec<KQ_CODEC_Q6_K, XT, NW>(mt, a, grid, s);
+    else launch_gather_codec<KQ_CODEC_IQ2_XXS, XT, NW>(mt, a, grid, s);
+}
+
+int gather_common(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pair_div, const void *w0,
+                  const void *w1, int64_t w_expert_bytes, int64_t w_row_bytes, int32_t N, int32_t K,
+                  int codec, int act, const int32_t *seg_info, const int32_t *pair_order,
+                  int32_t n_pairs, int32_t n_experts, void *y, int y_dtype, int64_t y_row_stride,
+                  hipStream_t s) {
+    if (!x || !w0 || !seg_info || !pair_order || !y) return KQ_ERR_NULL_POINTER;
+    if (kq_block_bytes(codec) == 0) return KQ_ERR_UNSUPPORTED_CODEC;
+    if (x_dtype != KQ_DTYPE_F16 && x_dtype != KQ_DTYPE_BF16 && x_dtype != KQ_DTYPE_F32)
+        return KQ_ERR_UNSUPPORTED_DTYPE;
+    if (y_dtype != KQ_DTYPE_F32 && y_dtype != KQ_DTYPE_F16 && y_dtype != KQ_DTYPE_BF16)
+        return KQ_ERR_UNSUPPORTED_DTYPE;
+    if (N <= 0 || K <= 0 || K % KQ_QK || n_pairs < 0 || n_experts <= 0 || x_pair_div <= 0)
+        return KQ_ERR_BAD_SHAPE;
+    if (n_pairs == 0) return KQ_OK;
+    const int64_t need = (int64_t)(K / KQ_QK) * kq_block_bytes(codec);
+    if (w_row_bytes < need || w_expert_bytes < w_row_bytes * N) return KQ_ERR_BAD_SHAPE;
+    if (x_row_stride < K || y_row_stride < N) return KQ_ERR_BAD_SHAPE;
+    if (((uintptr_t)x & 15) || (x_row_stride & (x_dtype == KQ_DTYPE_F32 ? 3 : 7))) return KQ_ERR_BAD_ALIGN;
+    if (codec == KQ_CODEC_Q4_K && (((uintptr_t)w0 & 15) || (w_row_bytes & 15) || (w_expert_bytes & 15) ||
+                                   (w1 && ((uintptr_t)w1 & 15))))
+        return KQ_ERR_BAD_ALIGN;
+    if (((uintptr_t)w0 & 1) || (w_row_bytes & 1) || (w_expert_bytes & 1)) return KQ_ERR_BAD_ALIGN;
+    GatherArgs a;
+    a.x = (const char *)x;
+    a.w0 = (const uint8_t *)w0;
+    a.w1 = (const uint8_t *)w1;
+    a.y = y;
+    a.seg_info = seg_info;
+    a.pair_order = pair_order;
+    a.x_stride = x_row_stride;
+    a.w_expert_bytes = w_expert_bytes;
+    a.w_row_bytes = w_row_bytes;
+    a.y_stride = y_row_stride;
+    a.x_pair_div = x_pair_div;
+    a.N = N;
+    a.K = K;
+    a.n_pairs = n_pairs;
+    a.n_experts = n_experts;
+    a.n_tiles = (N + 15) / 16;
+    a.y_dtype = y_dtype;
+    a.act = act;
+    // rows per expert segment are bounded by the number of pairs
+    const int rows = n_pairs < kMaxChunk ? n_pairs : kMaxChunk;
+    const int mt = rows <= 16 ? 1 : rows <= 32 ? 2 : 4;
+    const int slots = n_experts < n_pairs ? n_experts : n_pairs;
+    const int grid = slots * a.n_tiles;
+    if (w1) {
+        if (x_dtype == KQ_DTYPE_F16) launch_gather<0, 2>(codec, mt, a, grid, s);
+        else if (x_dtype == KQ_DTYPE_BF16) launch_gather<1, 2>(codec, mt, a, grid, s);
+        else launch_gather<2, 2>(codec, mt, a, grid, s);
+    } else {
+        if (x_dtype == KQ_DTYPE_F16) launch_gather<0, 1>(codec, mt, a, grid, s);
+        else if (x_dtype == KQ_DTYPE_BF16) launch_gather<1, 1>(codec, mt, a, grid, s);
+        else launch_gather<2, 1>(codec, mt, a, grid, s);
+    }
+    if (hipGetLastError() != hipSuccess) return KQ_ERR_LAUNCH_FAILED;
+    hipLaunchKernelGGL(kq_gather_zero_invalid, dim3(n_pairs), dim3(256), 0, s, pair_order + n_pairs,
+                       n_pairs, N, y, y_dtype, y_row_stride);
+    return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t kq_matmul_workspace_bytes(const kq_matmul_problem *problems, int n_problems) {
+    if (!problems || n_problems <= 0) return 0;
+    for (int i = 0; i < n_problems; ++i)
+        if (validate_problem(problems[i]) != KQ_OK) return 0;
+    return workspace_for(problems, n_problems, nullptr, nullptr, nullptr);
+}
+
+int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problems, int x_dtype,
+                                int y_dtype, void *workspace, size_t workspace_bytes,
+                                kq_stream_t stream) {
+    if (!problems) return KQ_ERR_NULL_POINTER;
+    if (n_problems <= 0) return KQ_ERR_BAD_ARGUMENT;
+    if (n_problems > KQ_MAX_GROUP) return KQ_ERR_TOO_MANY_PROBLEMS;
+    if (x_dtype != KQ_DTYPE_F16 && x_dtype != KQ_DTYPE_BF16) return KQ_ERR_UNSUPPORTED_DTYPE;
+    if (y_dtype != KQ_DTYPE_F32 && y_dtype != KQ_DTYPE_F16 && y_dtype != KQ_DTYPE_BF16)
+        return KQ_ERR_UNSUPPORTED_DTYPE;
+    DenseArgs a;
+    int64_t part_off[KQ_MAX_GROUP], ctr_off[KQ_MAX_GROUP];
+    for (int i = 0; i < n_problems; ++i) {
+        const int rc = validate_problem(problems[i]);
+        if (rc != KQ_OK) return rc;
+    }
+    size_t ctr_bytes = 0;
+    const size_t need = workspace_for(problems, n_problems, part_off, ctr_off, &ctr_bytes);
+    if (need > 0 && (!workspace || workspace_bytes < need)) return KQ_ERR_WORKSPACE_TOO_SMALL;
+    int units = 0, max_mt = 1, max_chunks = 0;
+    int np = 0;
+    for (int i = 0; i < n_problems; ++i) {
+        const kq_matmul_problem &q = problems[i];
+        if (q.M == 0 || q.N == 0) continue;
+        const Plan pl = plan_problem(q);
+        DenseProblem &p = a.p[np++];
+        p.w = (const uint8_t *)q.w;
+        p.x = (const char *)q.x;
+        p.y = q.y;
+        p.w_row_bytes = q.w_row_bytes;
+        p.x_stride = q.x_row_stride;
+        p.y_stride = q.y_row_stride;
+        p.M = q.M;
+        p.N = q.N;
+        p.K = q.K;
+        p.codec = q.codec;
+        p.n_tiles = pl.n_tiles;
+        p.k_splits = pl.k_splits;
+        p.steps_per_split = pl.steps_per_split;
+        p.unit_begin = units;
+        p.part_off = part_off[i];
+        p.ctr_off = ctr_off[i];
+        units += pl.n_tiles * pl.k_splits;
+        if (pl.mt > max_mt) max_mt = pl.mt;
+        if (pl.chunks > max_chunks) max_chunks = pl.chunks;
+    }
+    if (np == 0) return KQ_OK;
+    a.n_problems = np;
+    a.y_dtype = y_dtype;
+    a.ctrs = (uint32_t *)workspace;
+    a.parts = (float *)((char *)workspace + ctr_bytes);
+    hipStream_t s = (hipStream_t)stream;
+    const bool bf = x_dtype == KQ_DTYPE_BF16;
+    const int mt = max_mt <= 1 ? 1 : max_mt <= 2 ? 2 : 4;
+    if (mt == 1) bf ? launch_dense<1, 1>(a, units, max_chunks, s) : launch_dense<1, 0>(a, units, max_chunks, s);
+    else if (mt == 2) bf ? launch_dense<2, 1>(a, units, max_chunks, s) : launch_dense<2, 0>(a, units, max_chunks, s);
+    else bf ? launch_dense<4, 1>(a, units, max_chunks, s) : launch_dense<4, 0>(a, units, max_chunks, s);
+    return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
+}
+
+int kq_moe_route(const int32_t *idx, int32_t n_pairs, int32_t n_experts, int32_t *seg_info,
+                 int32_t *pair_order, kq_stream_t stream) {
+    if (!idx || !seg_info || !pair_order) return KQ_ERR_NULL_POINTER;
+    if (n_pairs < 0 || n_experts <= 0 || n_experts > 4096) return KQ_ERR_BAD_SHAPE;
+    const size_t smem = (size_t)2 * n_experts * sizeof(int32_t);
+    hipLaunchKernelGGL(kq_route_kernel, dim3(1), dim3(1024), smem, (hipStream_t)stream, idx, n_pairs,
+                       n_experts, seg_info, pair_order);
+    return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
+}
+
+int kq_gather_qmm(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pair_div, const void *w,
+                  int64_t w_expert_bytes, int64_t w_row_bytes, int32_t N, int32_t K, int codec,
+                  const int32_t *seg_info, const int32_t *pair_order, int32_t n_pairs,
+                  int32_t n_experts, void *y, int y_dtype, int64_t y_row_stride, kq_stream_t stream) {
+    return gather_common(x, x_dtype, x_row_stride, x_pair_div, w, nullptr, w_expert_bytes, w_row_bytes,
+                         N, K, codec, 0, seg_info, pair_order, n_pairs, n_experts, y, y_dtype,
+                         y_row_stride, (hipStream_t)stream);
+}
+
+int kq_moe_glu_gather(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pair_div,
+                      const void *w_gate, const void *w_up, int64_t w_expert_bytes, int64_t w_row_bytes,
+                      int32_t N, int32_t K, int codec, int act, const int32_t *seg_info,
+                      const int32_t *pair_order, int32_t n_pairs, int32_t n_experts, float *h,
+                      kq_stream_t stream) {
+    if (!w_up) return KQ_ERR_NULL_POINTER;
+    if (act != 0 && act != 1) return KQ_ERR_BAD_ARGUMENT;
+    return gather_common(x, x_dtype, x_row_stride, x_pair_div, w_gate, w_up, w_expert_bytes, w_row_bytes,
+                         N, K, codec, act, seg_info, pair_order, n_pairs, n_experts, h, KQ_DTYPE_F32, N,
+                         (hipStream_t)stream);
+}
+
+int kq_moe_mix(const float *y_pairs, const float *scores, int32_t T, int32_t top_k, int32_t N, void *y,
+               int y_dtype, kq_stream_t stream) {
+    if (!y_pairs || !scores || !y) return KQ_ERR_NULL_POINTER;
+    if (T < 0 || top_k <= 0 || N <= 0) return KQ_ERR_BAD_SHAPE;
+    if (y_dtype != KQ_DTYPE_F32 && y_dtype != KQ_DTYPE_F16 && y_dtype != KQ_DTYPE_BF16)
+        return KQ_ERR_UNSUPPORTED_DTYPE;
+    if (T == 0) return KQ_OK;
+    hipLaunchKernelGGL(kq_mix_kernel, dim3((N + 255) / 256, T), dim3(256), 0, (hipStream_t)stream, y_pairs,
+                       scores, T, top_k, N, y, y_dtype);
+    return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
+}
+
+int kq_moe_router_topk(const void *logits, int logits_dtype, int32_t T, int32_t E, int32_t k,
+                       int norm_topk_prob, int32_t *inds, float *scores, kq_stream_t stream) {
+    if (!logits || !inds || !scores) return KQ_ERR_NULL_POINTER;
+    if (T < 0 || E <= 0 || E > 1024 || k <= 0 || k > 32 || k > E) return KQ_ERR_BAD_SHAPE;
+    if (logits_dtype != KQ_DTYPE_F32 && logits_dtype != KQ_DTYPE_F16 && logits_dtype != KQ_DTYPE_BF16)
+        return KQ_ERR_UNSUPPORTED_DTYPE;
+    if (T == 0) return KQ_OK;
+    hipLaunchKernelGGL(kq_router_kernel, dim3(T), dim3(64), 0, (hipStream_t)stream, logits, logits_dtype, E,
+                       k, norm_topk_prob, inds, scores);
+    return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
+}
+
+}  // extern "C"

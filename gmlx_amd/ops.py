@@ -1,0 +1,518 @@
+"""K-quant ops on torch tensors, mirroring the mlx_kquant op surface gmlx binds.
+
+Every op validates on the host, allocates its output with torch on the input's
+device, and launches the gfx950 kernels of libgmlx_amd.so on the current torch
+stream.  There is no CPU path: CPU tensors, a missing library or an
+unsupported shape raise.  Reference call sites are cited per op.
+
+Op names and argument orders follow the reference's calls:
+  dequantize(w, scales, codec, dtype)            gmlx/modules.py:1461
+  quantize(w, codec) -> (wire, scales)           tests/test_dequant_unattachable.py:36
+  quantized_matmul(x, w, scales, codec, transpose=True)   gmlx/occupancy_fuse.py:162-165
+  gather_qmm / KQuantSwitchLinear                tests/test_native_fp.py:420-428
+  moe_glu_gather_kq(x, gate_w, up_w, codec, idx, act=)    gmlx/modules.py:557-588
+  gather_qmv_kq(h, down_w, codec, idx)           gmlx/modules.py:595-597
+  gather_qmv_mix_ns_kq(h, down_w, codec, idx, scores)     gmlx/modules.py:591-593
+  moe_router_topk(logits, k, norm_topk_prob)     gmlx/modules.py:750-752
+  sdpa_decode_gqa(q, k, v, scale, starts=)       gmlx/gemma4_batched_sdpa.py:221-222
+  ragged_decode_attention(q, k, v, pads, scale)  gmlx/qwen35_attn.py:395-493
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from collections import OrderedDict
+
+import torch
+
+from . import _lib
+from ._lib import CODEC_ID, DTYPE_BF16, DTYPE_F16, DTYPE_F32, KQError, MatmulProblem, check, lib
+
+QK_K = 256
+BLOCK_BYTES = {"q4_k": 144, "q6_k": 210, "iq2_xxs": 66}
+_TORCH_DTYPE = {torch.float32: DTYPE_F32, torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16}
+
+__all__ = [
+    "codecs", "codec_has_matmul", "codec_has_moe_glu", "dequantize", "quantize", "quantized_matmul",
+    "quantized_matmul_grouped", "moe_route", "gather_qmm", "moe_glu_gather_kq", "gather_qmv_kq",
+    "gather_qmv_mix_ns_kq", "moe_router_topk", "sdpa_decode_ragged", "sdpa_decode_gqa",
+    "ragged_decode_attention", "wire_k",
+]
+
+
+# ------------------------------------------------------------------ helpers
+
+def _fault(op):
+    """GMLX_HIP_FAULT=<op>[,<op>...] makes that op reject the call before any
+    launch (tests exercise the callers' decline paths on CPU with it)."""
+    names = os.environ.get("GMLX_HIP_FAULT", "")
+    if names and (op in names.split(",") or names == "all"):
+        raise KQError(op, _lib.KQ_ERR_LAUNCH_FAILED, "fault injected by GMLX_HIP_FAULT")
+
+
+def _stream(t):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _require_gpu(*ts):
+    for t in ts:
+        if not isinstance(t, torch.Tensor) or not t.is_cuda:
+            raise ValueError("gmlx_amd ops run on the GPU only: got a non-CUDA tensor")
+
+
+def _codec_id(codec):
+    try:
+        return CODEC_ID[codec]
+    except KeyError:
+        raise ValueError(f"unsupported codec {codec!r}; have {tuple(CODEC_ID)}") from None
+
+
+def _dt(dtype):
+    try:
+        return _TORCH_DTYPE[dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {dtype}") from None
+
+
+def wire_k(wire_cols, codec):
+    """Logical K of a wire row of `wire_cols` bytes (-1 if not whole blocks);
+    the rule of gmlx/modules.py:_kq_wire_k (:253-257)."""
+    bpb = BLOCK_BYTES[codec]
+    return (wire_cols // bpb) * QK_K if wire_cols % bpb == 0 else -1
+
+
+def _rows_view(x):
+    """2-D [M, K] view of x[..., K] with unit inner stride, 16-byte aligned
+    base and 8-element aligned row stride (copying when needed)."""
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K)
+    if (x2.stride(1) != 1 or x2.data_ptr() % 16 or (x2.shape[0] > 1 and x2.stride(0) % 8)
+            or x2.stride(0) < K):
+        x2 = x2.contiguous()
+    return x2
+
+
+class _Workspaces:
+    """Zero-filled scratch per (device, stream), grown on demand.  Kernels
+    leave their counters zeroed, so a workspace is reusable by later calls on
+    the same stream."""
+
+    def __init__(self):
+        self._ws = {}
+
+    def get(self, device, stream_handle, nbytes):
+        key = (device.index, stream_handle)
+        cur = self._ws.get(key)
+        if cur is None or cur.numel() < nbytes:
+            cur = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+            self._ws[key] = cur
+        return cur
+
+
+_WS = _Workspaces()
+
+
+# ------------------------------------------------------------ capabilities
+
+def codecs():
+    """Codecs with kernels here (kq.codecs(), gmlx/modules.py:179-181)."""
+    return tuple(CODEC_ID)
+
+
+def codec_has_matmul(codec):
+    return codec in CODEC_ID and bool(lib().kq_supports(_lib.OP_MATMUL, CODEC_ID[codec], DTYPE_F16))
+
+
+def codec_has_moe_glu(codec):
+    return codec in CODEC_ID and bool(lib().kq_supports(_lib.OP_MOE_GLU, CODEC_ID[codec], DTYPE_F16))
+
+
+# ------------------------------------------------------- dequant / quantize
+
+def dequantize(w, scales=None, codec="q4_k", dtype=torch.float32):
+    """Wire bytes [..., nb*bpb] -> [..., nb*256] of `dtype`.  float32 output is
+    bit-exact to the GGML dequantize_row_* definition.  `scales` is the
+    reference's vestigial placeholder and is ignored."""
+    _fault("dequantize")
+    _require_gpu(w)
+    cid = _codec_id(codec)
+    if w.dtype != torch.uint8:
+        raise ValueError("wire bytes must be uint8")
+    bpb = BLOCK_BYTES[codec]
+    if w.shape[-1] % bpb:
+        raise ValueError(f"wire width {w.shape[-1]} is not a whole number of {codec} blocks")
+    w = w.contiguous()
+    nb = w.numel() // bpb
+    out = torch.empty((*w.shape[:-1], (w.shape[-1] // bpb) * QK_K), dtype=dtype, device=w.device)
+    check("kq_dequantize", lib().kq_dequantize(w.data_ptr(), nb, cid, out.data_ptr(), _dt(dtype), _stream(w)))
+    return out
+
+
+def quantize(w, codec):
+    """fp32 weights [..., K] -> (wire uint8 [..., K/256*bpb], scales placeholder
+    uint8[1]) on the GPU.  Q4_K/Q6_K follow llama.cpp's reference quantizers."""
+    _fault("quantize")
+    _require_gpu(w)
+    cid = _codec_id(codec)
+    K = w.shape[-1]
+    if K % QK_K:
+        raise ValueError(f"K={K} is not a multiple of {QK_K}")
+    w2 = w.reshape(-1, K).to(torch.float32).contiguous()
+    rows = w2.shape[0]
+    bpb = BLOCK_BYTES[codec]
+    wire = torch.empty((rows, (K // QK_K) * bpb), dtype=torch.uint8, device=w.device)
+    check("kq_quantize", lib().kq_quantize(w2.data_ptr(), rows, K, w2.stride(0), cid, wire.data_ptr(),
+                                           _stream(w)))
+    return wire.reshape(*w.shape[:-1], wire.shape[-1]), torch.zeros(1, dtype=torch.uint8, device=w.device)
+
+
+# ------------------------------------------------------------------ matmul
+
+def _problem(x2, w, codec, y2):
+    N = w.shape[0]
+    K = x2.shape[1]
+    if wire_k(w.shape[-1], codec) != K:
+        raise ValueError(f"x has K={K} but the {codec} wire rows hold {wire_k(w.shape[-1], codec)} values")
+    if w.stride(-1) != 1:
+        raise ValueError("wire rows must be contiguous bytes")
+    return MatmulProblem(w.data_ptr(), w.stride(0), x2.data_ptr(), x2.stride(0), y2.data_ptr(), y2.stride(0),
+                         x2.shape[0], N, K, _codec_id(codec))
+
+
+def _launch_grouped(probs, x_dt, y_dt, device, stream):
+    arr = (MatmulProblem * len(probs))(*probs)
+    L = lib()
+    need = L.kq_matmul_workspace_bytes(arr, len(probs))
+    ws = _WS.get(device, stream.value, need)
+    check("kq_quantized_matmul_grouped",
+          L.kq_quantized_matmul_grouped(arr, len(probs), x_dt, y_dt, ws.data_ptr(), ws.numel(), stream))
+
+
+def quantized_matmul(x, w, scales=None, codec="q4_k", transpose=True, out_dtype=None):
+    """y[..., N] = x[..., K] . dequant(w[N, K])^T with fp32 accumulation
+    (KQuantLinear forward).  Output dtype = x dtype unless `out_dtype`."""
+    _fault("quantized_matmul")
+    if not transpose:
+        raise ValueError("only transpose=True (y = x . W^T) is supported, as gmlx calls it")
+    _require_gpu(x, w)
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"activations must be float16 or bfloat16, got {x.dtype}")
+    if w.dim() != 2 or w.dtype != torch.uint8:
+        raise ValueError("w must be a uint8 wire matrix [N, K/256*block_bytes]")
+    x2 = _rows_view(x)
+    out_dtype = out_dtype or x.dtype
+    y = torch.empty((x2.shape[0], w.shape[0]), dtype=out_dtype, device=x.device)
+    if x2.shape[0] > 0 and w.shape[0] > 0:
+        s = _stream(x)
+        _launch_grouped([_problem(x2, w, codec, y)], _dt(x.dtype), _dt(out_dtype), x.device, s)
+    return y.reshape(*x.shape[:-1], w.shape[0])
+
+
+def quantized_matmul_grouped(items, out_dtype=None):
+    """Run up to 8 independent quantized matmuls in ONE launch.
+
+    items: sequence of (x, w, codec); every x shares one dtype (f16/bf16).
+    Returns the list of outputs.  This is the launch-level form of the
+    reference's occupancy fusion (gmlx/occupancy_fuse.py:141-344, q|k|v and
+    gate|up concatenated wires): codecs may differ (Q4_K q/k with Q6_K v) and
+    no wire bytes are concatenated."""
+    _fault("quantized_matmul")
+    if not items or len(items) > _lib.MAX_GROUP:
+        raise ValueError(f"need 1..{_lib.MAX_GROUP} problems")
+    x0 = items[0][0]
+    out_dtype = out_dtype or x0.dtype
+    probs, outs = [], []
+    for x, w, codec in items:
+        _require_gpu(x, w)
+        if x.dtype != x0.dtype:
+            raise ValueError("all activations of a group must share a dtype")
+        x2 = _rows_view(x)
+        y = torch.empty((x2.shape[0], w.shape[0]), dtype=out_dtype, device=x.device)
+        outs.append(y.reshape(*x.shape[:-1], w.shape[0]))
+        if x2.shape[0] and w.shape[0]:
+            probs.append(_problem(x2, w, codec, y))
+    if probs:
+        _launch_grouped(probs, _dt(x0.dtype), _dt(out_dtype), x0.device, _stream(x0))
+    return outs
+
+
+# --------------------------------------------------------------------- MoE
+
+def moe_route(idx, n_experts):
+    """Group (token, slot) pairs by expert on the device.  Returns (seg_info,
+    pair_order) int32 tensors as documented for kq_moe_route."""
+    _require_gpu(idx)
+    idx32 = idx.reshape(-1).to(torch.int32).contiguous()
+    P = idx32.numel()
+    seg = torch.empty(2 + 2 * n_experts, dtype=torch.int32, device=idx.device)
+    order = torch.empty(max(2 * P, 1), dtype=torch.int32, device=idx.device)
+    check("kq_moe_route", lib().kq_moe_route(idx32.data_ptr(), P, n_experts, seg.data_ptr(), order.data_ptr(),
+                                             _stream(idx)))
+    return seg, order
+
+
+def _expert_stack(w, codec, K):
+    if w.dim() != 3 or w.dtype != torch.uint8:
+        raise ValueError("expert weights must be a uint8 wire stack [E, N, K/256*block_bytes]")
+    if wire_k(w.shape[-1], codec) != K:
+        raise ValueError(f"activations have K={K} but the wire rows hold {wire_k(w.shape[-1], codec)}")
+    if w.stride(-1) != 1 or w.stride(1) < w.shape[-1] or w.stride(0) < w.stride(1) * w.shape[1]:
+        w = w.contiguous()
+    return w
+
+
+def _x_dt(x):
+    if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise ValueError(f"unsupported activation dtype {x.dtype}")
+    return _dt(x.dtype)
+
+
+def _gather(x2, x_pair_div, w, codec, idx2, out, out_dt, w_up=None, act=0):
+    E, N, _ = w.shape
+    K = x2.shape[1]
+    seg, order = moe_route(idx2, E)
+    P = idx2.numel()
+    L = lib()
+    s = _stream(x2)
+    if w_up is None:
+        rc = L.kq_gather_qmm(x2.data_ptr(), _x_dt(x2), x2.stride(0), x_pair_div, w.data_ptr(), w.stride(0),
+                             w.stride(1), N, K, _codec_id(codec), seg.data_ptr(), order.data_ptr(), P, E,
+                             out.data_ptr(), out_dt, out.stride(0), s)
+        check("kq_gather_qmm", rc)
+    else:
+        rc = L.kq_moe_glu_gather(x2.data_ptr(), _x_dt(x2), x2.stride(0), x_pair_div, w.data_ptr(),
+                                 w_up.data_ptr(), w.stride(0), w.stride(1), N, K, _codec_id(codec), act,
+                                 seg.data_ptr(), order.data_ptr(), P, E, out.data_ptr(), s)
+        check("kq_moe_glu_gather", rc)
+
+
+def gather_qmm(x, w, scales=None, codec="q4_k", indices=None, sorted_indices=False, out_dtype=None):
+    """KQuantSwitchLinear forward: x (T, 1, 1, K) or (T, K), indices (T, k)
+    -> (T, k, 1, N) with y[t, s] = dequant(w[indices[t, s]]) . x[t].
+    `sorted_indices` is accepted for signature parity; grouping by expert
+    always happens on the device."""
+    _fault("gather_qmm")
+    _require_gpu(x, w, indices)
+    K = x.shape[-1]
+    T, k = indices.shape[0], indices.shape[-1]
+    x2 = _rows_view(x)
+    if x2.shape[0] != T:
+        raise ValueError(f"x has {x2.shape[0]} rows for {T} index rows")
+    w = _expert_stack(w, codec, K)
+    out_dtype = out_dtype or x.dtype
+    y = torch.empty((T * k, w.shape[1]), dtype=out_dtype, device=x.device)
+    if T * k:
+        _gather(x2, k, w, codec, indices.reshape(T, k), y, _dt(out_dtype))
+    return y.reshape(T, k, 1, w.shape[1])
+
+
+_ACTS = {"silu": 0, "gelu": 1}
+
+
+def moe_glu_gather_kq(x, gate_w, up_w, codec, idx, act="silu"):
+    """Fused MoE GLU gather: h[t, s] = act(Wg[e] . x[t]) * (Wu[e] . x[t]),
+    e = idx[t, s], fp32 epilogue -> h (t, k, I) float32."""
+    _fault("moe_glu_gather_kq")
+    _require_gpu(x, gate_w, up_w, idx)
+    if act not in _ACTS:
+        raise ValueError(f"act {act!r} has no kernel epilogue; have {tuple(_ACTS)}")
+    K = x.shape[-1]
+    t, k = idx.shape[0], idx.shape[-1]
+    x2 = _rows_view(x)
+    gate_w = _expert_stack(gate_w, codec, K)
+    up_w = _expert_stack(up_w, codec, K)
+    if gate_w.shape != up_w.shape or gate_w.stride() != up_w.stride():
+        raise ValueError("gate and up stacks must share shape and layout")
+    h = torch.empty((t * k, gate_w.shape[1]), dtype=torch.float32, device=x.device)
+    if t * k:
+        _gather(x2, k, gate_w, codec, idx.reshape(t, k), h, DTYPE_F32, w_up=up_w, act=_ACTS[act])
+    return h.reshape(t, k, gate_w.shape[1])
+
+
+def gather_qmv_kq(h, down_w, codec, idx, bias=None, out_dtype=torch.float32):
+    """Per-pair down projection: y[t, s] = dequant(Wd[idx[t, s]]) . h[t, s]
+    -> (t, k, N).  h (t, k, I) float32/float16/bfloat16."""
+    _fault("gather_qmv_kq")
+    if bias is not None:
+        raise ValueError("biased expert stacks are not supported by the K-quant kernels")
+    _require_gpu(h, down_w, idx)
+    t, k = idx.shape[0], idx.shape[-1]
+    I = h.shape[-1]
+    h2 = _rows_view(h)
+    if h2.shape[0] != t * k:
+        raise ValueError("h must hold one row per (token, slot) pair")
+    down_w = _expert_stack(down_w, codec, I)
+    y = torch.empty((t * k, down_w.shape[1]), dtype=out_dtype, device=h.device)
+    if t * k:
+        _gather(h2, 1, down_w, codec, idx.reshape(t, k), y, _dt(out_dtype))
+    return y.reshape(t, k, down_w.shape[1])
+
+
+def gather_qmv_mix_ns_kq(h, down_w, codec, idx, scores, out_dtype=torch.float32):
+    """Down projection with the routing mix folded in:
+    y[t] = sum_s scores[t, s] * (Wd[idx[t, s]] . h[t, s]), fp32, slots summed
+    in order."""
+    _fault("gather_qmv_mix_ns_kq")
+    _require_gpu(h, down_w, idx, scores)
+    t, k = idx.shape[0], idx.shape[-1]
+    yp = gather_qmv_kq(h, down_w, codec, idx, out_dtype=torch.float32).reshape(t * k, -1)
+    N = yp.shape[1]
+    sc = scores.reshape(t, k).to(torch.float32).contiguous()
+    y = torch.empty((t, N), dtype=out_dtype, device=h.device)
+    if t:
+        check("kq_moe_mix", lib().kq_moe_mix(yp.data_ptr(), sc.data_ptr(), t, k, N, y.data_ptr(),
+                                             _dt(out_dtype), _stream(h)))
+    return y
+
+
+def moe_router_topk(logits, k, norm_topk_prob=True):
+    """softmax(fp32) -> top-k (descending, ties to the lower expert id) ->
+    optional renormalisation (stock form gmlx/modules.py:754-760).
+    Returns (inds int32 (t, k), scores float32 (t, k))."""
+    _fault("moe_router_topk")
+    _require_gpu(logits)
+    E = logits.shape[-1]
+    l2 = logits.reshape(-1, E).contiguous()
+    t = l2.shape[0]
+    inds = torch.empty((t, k), dtype=torch.int32, device=logits.device)
+    scores = torch.empty((t, k), dtype=torch.float32, device=logits.device)
+    if t:
+        check("kq_moe_router_topk", lib().kq_moe_router_topk(l2.data_ptr(), _dt(l2.dtype), t, E, k,
+                                                             int(bool(norm_topk_prob)), inds.data_ptr(),
+                                                             scores.data_ptr(), _stream(logits)))
+    return inds.reshape(*logits.shape[:-1], k), scores.reshape(*logits.shape[:-1], k)
+
+
+# --------------------------------------------------------------- attention
+
+_TABLES = OrderedDict()  # memoised device row tables, like the reference's pads cache
+
+
+def _row_tables(device, kv_off, head_stride, row_len):
+    key = (device.index, tuple(kv_off), tuple(head_stride), tuple(row_len))
+    hit = _TABLES.get(key)
+    if hit is not None:
+        _TABLES.move_to_end(key)
+        return hit
+    t = (torch.tensor(kv_off, dtype=torch.int64, device=device),
+         torch.tensor(head_stride, dtype=torch.int64, device=device),
+         torch.tensor(row_len, dtype=torch.int32, device=device))
+    _TABLES[key] = t
+    if len(_TABLES) > 128:
+        _TABLES.popitem(last=False)
+    return t
+
+
+def sdpa_decode_ragged(q, k, v, kv_off, head_stride, row_len, n_kv_heads, scale, max_len):
+    """Ragged GQA decode attention over per-row KV regions (device tables).
+
+    q (B, Hq, D); k, v flat-addressable tensors of q's dtype sharing one
+    layout; row b's kv head h tokens start at element
+    kv_off[b] + h * head_stride[b], D contiguous elements per token,
+    row_len[b] tokens (rows longer than max_len are clamped to it).
+    kv_off / head_stride are int64 and row_len int32 device tensors.
+    Returns (B, Hq, D) in q's dtype."""
+    _fault("sdpa_decode_ragged")
+    _require_gpu(q, k, v, kv_off, head_stride, row_len)
+    B, Hq, D = q.shape
+    dt = q.dtype
+    if dt not in (torch.float16, torch.bfloat16) or k.dtype != dt or v.dtype != dt:
+        raise ValueError("q, k, v must share dtype float16 or bfloat16")
+    if Hq % n_kv_heads:
+        raise ValueError("Hq must be a multiple of Hkv")
+    if kv_off.dtype != torch.int64 or head_stride.dtype != torch.int64 or row_len.dtype != torch.int32:
+        raise ValueError("kv_off / head_stride must be int64 and row_len int32")
+    if kv_off.numel() != B or head_stride.numel() != B or row_len.numel() != B:
+        raise ValueError("one table entry per row")
+    q = q.contiguous()
+    out = torch.empty_like(q)
+    tabs = (kv_off.contiguous(), head_stride.contiguous(), row_len.contiguous())
+    return _sdpa_launch(q, k, v, tabs, int(n_kv_heads), scale, int(max_len), out)
+
+
+def _sdpa_launch(q, k, v, tabs, Hkv, scale, max_len, out):
+    B, Hq, D = q.shape
+    L = lib()
+    need = L.kq_sdpa_workspace_bytes(B, Hq, Hkv, D, max_len)
+    s = _stream(q)
+    ws = _WS.get(q.device, s.value, need)
+    rc = L.kq_sdpa_decode_ragged(q.data_ptr(), k.data_ptr(), v.data_ptr(), tabs[0].data_ptr(),
+                                 tabs[1].data_ptr(), tabs[2].data_ptr(), B, Hq, Hkv, D, max_len,
+                                 float(scale), _dt(q.dtype), out.data_ptr(), ws.data_ptr(), ws.numel(), s)
+    check("kq_sdpa_decode_ragged", rc)
+    return out
+
+
+def sdpa_decode_slabs(q, k_cache, v_cache, row_offsets, row_lens, n_kv_heads, scale, max_len=None):
+    """C-config layout: row b's KV is a contiguous slab [Hkv, len_b, D] at
+    element offset row_offsets[b] of the flat caches.  row_offsets /
+    row_lens are host sequences (memoised to device tables)."""
+    _fault("sdpa_decode_ragged")
+    _require_gpu(q, k_cache, v_cache)
+    B, Hq, D = q.shape
+    if Hq % n_kv_heads:
+        raise ValueError("Hq must be a multiple of Hkv")
+    row_lens = [int(x) for x in row_lens]
+    offs = [int(x) for x in row_offsets]
+    hstride = [l * D for l in row_lens]
+    tabs = _row_tables(q.device, offs, hstride, row_lens)
+    max_len = int(max_len if max_len is not None else (max(row_lens) if row_lens else 0))
+    out = torch.empty_like(q.contiguous())
+    return _sdpa_launch(q.contiguous(), k_cache, v_cache, tabs, n_kv_heads, scale, max_len, out)
+
+
+def sdpa_decode_gqa(q, k, v, scale, starts=None):
+    """kq.sdpa_decode_gqa with per-row `starts` (gmlx/gemma4_batched_sdpa.py:
+    210-226): q (B, Hq, 1, D), k/v (B, Hkv, L, D); row b attends keys
+    [starts[b], L).  `starts` may be a host sequence or an int tensor."""
+    B = q.shape[0]
+    if starts is None:
+        pads = [0] * B
+    elif isinstance(starts, torch.Tensor):
+        pads = [int(x) for x in starts.tolist()]
+    else:
+        pads = [int(x) for x in starts]
+    out = ragged_decode_attention(q, k, v, pads, scale)
+    if out is None:
+        raise ValueError("sdpa_decode_gqa: unsupported shape/dtype for the ragged kernel")
+    return out
+
+
+def ragged_decode_attention(queries, keys, values, pads, scale):
+    """Ragged left-padded S=1 decode (gmlx/qwen35_attn.py:395-493).
+
+    queries (B, Hq, 1, D); keys/values (B, Hkv, L, D); row b's visible keys
+    are [pads[b], L).  Declines (returns None) exactly where the reference's
+    guard rails do (:412-431): non-4-D inputs, S != 1, dtype other than
+    float16/bfloat16 or mismatched, len(pads) != B, negative pads,
+    Hq % Hkv != 0, D != V, D not in (64, 96, 128, 256), pad >= L."""
+    if any(not isinstance(t, torch.Tensor) for t in (queries, keys, values)):
+        return None
+    if (queries.dim() != 4 or keys.dim() != 4 or values.dim() != 4 or queries.shape[2] != 1
+            or queries.dtype not in (torch.float16, torch.bfloat16) or keys.dtype != queries.dtype
+            or values.dtype != queries.dtype):
+        return None
+    B, Hq, _, D = queries.shape
+    pads = tuple(int(p) for p in pads)
+    if len(pads) != B or any(p < 0 for p in pads):
+        return None
+    Hkv, L = keys.shape[1], keys.shape[2]
+    Dv = values.shape[-1]
+    if Hq % Hkv != 0 or D != Dv or D not in (64, 96, 128, 256) or any(p >= L for p in pads):
+        return None
+    if Hq // Hkv > 16 or tuple(values.shape) != tuple(keys.shape):
+        return None
+    _fault("ragged_decode_attention")
+    _require_gpu(queries, keys, values)
+    k = keys if keys.stride(3) == 1 and keys.stride(2) == D else keys.contiguous()
+    v = values if values.stride() == k.stride() else values.contiguous()
+    if v.stride() != k.stride():
+        k, v = k.contiguous(), v.contiguous()
+    kv_off = [b * k.stride(0) + p * D for b, p in enumerate(pads)]
+    hstride = [k.stride(1)] * B
+    lens = [L - p for p in pads]
+    tabs = _row_tables(queries.device, kv_off, hstride, lens)
+    q3 = queries.reshape(B, Hq, D).contiguous()
+    out = torch.empty_like(q3)
+    _sdpa_launch(q3, k, v, tabs, Hkv, scale, L, out)
+    return out.reshape(B, Hq, 1, D)

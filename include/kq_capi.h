@@ -1,0 +1,193 @@
+/*
+ * kq_capi.h -- C ABI of libgmlx_amd.so, the MI355X (gfx950) K-quant
+ * batched-decode hot path: GGUF Q4_K / Q6_K / IQ2_XXS dequant-fused matmuls
+ * (dense, grouped, MoE expert gather) and ragged GQA decode attention.
+ *
+ * Every entry point replaces one op of the un-vendored mlx-kquant package that
+ * gmlx binds (pyproject.toml:26-34); the reference call site each replaces is
+ * cited beside it.  Conventions:
+ *   - all pointers are device pointers unless stated; the caller owns every
+ *     buffer (outputs and workspace included); the library never allocates,
+ *     frees or synchronizes;
+ *   - weights are GGUF wire bytes, consumed unchanged: row n of a matrix
+ *     starts at w + n * w_row_bytes and holds K/256 consecutive super-blocks;
+ *   - every call takes a hipStream_t (pass the caller's current stream) and
+ *     launches asynchronously;
+ *   - return value: KQ_OK (0) or a negative kq_status; kq_strerror() names it.
+ *     Validation happens on the host before any launch, so a rejected call
+ *     launches nothing.
+ */
+#ifndef KQ_CAPI_H
+#define KQ_CAPI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t *kq_stream_t; /* == hipStream_t */
+
+typedef enum {
+    KQ_OK = 0,
+    KQ_ERR_NULL_POINTER = -1,
+    KQ_ERR_BAD_SHAPE = -2,
+    KQ_ERR_BAD_ALIGN = -3,
+    KQ_ERR_UNSUPPORTED_CODEC = -4,
+    KQ_ERR_UNSUPPORTED_DTYPE = -5,
+    KQ_ERR_WORKSPACE_TOO_SMALL = -6,
+    KQ_ERR_LAUNCH_FAILED = -7,
+    KQ_ERR_TOO_MANY_PROBLEMS = -8,
+    KQ_ERR_BAD_ARGUMENT = -9
+} kq_status;
+
+/* Codec ids are the GGML type ids (gguf GGMLQuantizationType). */
+enum { KQ_CODEC_Q4_K = 12, KQ_CODEC_Q6_K = 14, KQ_CODEC_IQ2_XXS = 16 };
+/* Element types of activations / outputs. */
+enum { KQ_DTYPE_F32 = 0, KQ_DTYPE_F16 = 1, KQ_DTYPE_BF16 = 2 };
+/* Op ids for kq_supports. */
+enum {
+    KQ_OP_DEQUANTIZE = 0,
+    KQ_OP_QUANTIZE = 1,
+    KQ_OP_MATMUL = 2,
+    KQ_OP_GATHER = 3,
+    KQ_OP_MOE_GLU = 4,
+    KQ_OP_SDPA = 5
+};
+
+/* ---- identity and capability probes ---------------------------------- */
+/* Capability probes replace kq.codecs() / kq.codec_has_matmul(c) /
+ * kq.codec_has_moe_glu(c) (gmlx/modules.py:179-181, gmlx/loader.py:1443-1456). */
+const char *kq_version(void);
+const char *kq_strerror(int code);
+/* Bytes per 256-value super-block of a codec (144 / 210 / 66), else 0. */
+int kq_codec_block_bytes(int codec);
+/* 1 when `op` supports `codec` (ignored for KQ_OP_SDPA) with activation
+ * `dtype`, else 0. */
+int kq_supports(int op, int codec, int dtype);
+/* Host copy of the IQ2_XXS grid the kernels use (256 x u64, byte j = value j). */
+const uint64_t *kq_iq2xxs_grid_host(void);
+
+/* ---- dequantize / quantize ------------------------------------------- */
+/* kq.dequantize(w, scales, codec, dtype) (gmlx/modules.py:1461,
+ * gmlx/dsv32_patches.py:229): n_blocks super-blocks at `wire` (contiguous)
+ * -> n_blocks*256 values of out_dtype.  fp32 output is bit-exact to the GGML
+ * dequantize_row_* definition; f16/bf16 outputs are that value rounded to
+ * nearest even. */
+int kq_dequantize(const void *wire, int64_t n_blocks, int codec, void *out, int out_dtype,
+                  kq_stream_t stream);
+
+/* kq.quantize(w, codec) (tests/test_dequant_unattachable.py:36,
+ * gmlx/mtp_load.py:290): fp32 w [n_rows, K] (row stride w_row_stride
+ * elements), K % 256 == 0 -> wire [n_rows, K/256*block_bytes].  Q4_K / Q6_K
+ * follow llama.cpp's reference quantizers; IQ2_XXS uses an exhaustive-grid
+ * search.  Deterministic. */
+int kq_quantize(const float *w, int64_t n_rows, int64_t K, int64_t w_row_stride, int codec,
+                void *wire, kq_stream_t stream);
+
+/* ---- dense quantized matmul ------------------------------------------ */
+/* One problem y[M, N] = x[M, K] . dequant(W[N, K])^T, fp32 accumulation. */
+typedef struct {
+    const void *w;       /* wire bytes */
+    int64_t w_row_bytes; /* byte stride between weight rows (>= K/256*bpb) */
+    const void *x;       /* activations [M, K] of x_dtype */
+    int64_t x_row_stride;/* elements */
+    void *y;             /* output [M, N] of y_dtype */
+    int64_t y_row_stride;/* elements */
+    int32_t M, N, K;
+    int32_t codec;
+} kq_matmul_problem;
+
+/* Workspace bytes kq_quantized_matmul_grouped needs for these problems
+ * (split-K partials + arrival counters).  The workspace must be zero-filled
+ * once when allocated; calls leave it zeroed.  Calls that share a workspace
+ * must be ordered (same stream). */
+size_t kq_matmul_workspace_bytes(const kq_matmul_problem *problems, int n_problems);
+
+/* kq.quantized_matmul(x, w, scales, codec, transpose=True) -- the
+ * KQuantLinear forward (gmlx/modules.py:1535-1539; direct calls at
+ * gmlx/occupancy_fuse.py:162-165, 224-227, 290-293, 312-315).  Up to
+ * KQ_MAX_GROUP independent problems (any codec mix, shared x_dtype/y_dtype)
+ * run in ONE launch: the row-concatenated q|k|v and gate|up wires of
+ * gmlx/occupancy_fuse.py:141-344 become one call without concatenating
+ * bytes.  x_dtype: f16 or bf16.  y_dtype: f16, bf16 or f32. */
+#define KQ_MAX_GROUP 8
+int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problems,
+                                int x_dtype, int y_dtype, void *workspace,
+                                size_t workspace_bytes, kq_stream_t stream);
+
+/* ---- MoE expert gather ------------------------------------------------- */
+/* Device-side routing of (token, slot) pairs to experts.  idx [n_pairs]
+ * int32 expert ids (row-major [T, k]).  Writes:
+ *   seg_info  int32 [3 + 2*n_experts]: [0] = number of non-empty experts S,
+ *             then seg_expert[n_experts], seg_start[n_experts + 1];
+ *   pair_order int32 [n_pairs]: pair ids grouped by expert (ascending expert,
+ *             ascending pair id inside an expert) -- the stable sort gmlx's
+ *             SwitchGLU applies at indices.size >= 64
+ *             (gmlx/modules.py:1308-1310).
+ * Expert ids outside [0, n_experts) are rejected on device: they are routed
+ * to no segment and their outputs are written as zeros. */
+int kq_moe_route(const int32_t *idx, int32_t n_pairs, int32_t n_experts, int32_t *seg_info,
+                 int32_t *pair_order, kq_stream_t stream);
+
+/* KQuantSwitchLinear / kq.gather_qmm (gmlx/modules.py:1549-1552,
+ * tests/test_native_fp.py:420-428) and kq.gather_qmv_kq (gmlx/modules.py:595-597):
+ * for every pair p = t*k + s with expert e = idx[p]:
+ *   y[p, :] = x_row(p) . dequant(W[e])^T
+ * x_row(p) = x[p / x_pair_div]: x_pair_div = top_k for gather_qmm (one x row
+ * per token), 1 for gather_qmv (one h row per pair).  W: [n_experts, N, K]
+ * wire with expert stride w_expert_bytes.  seg_info / pair_order come from
+ * kq_moe_route.  y [n_pairs, N] of y_dtype (f32/f16/bf16). */
+int kq_gather_qmm(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pair_div,
+                  const void *w, int64_t w_expert_bytes, int64_t w_row_bytes, int32_t N,
+                  int32_t K, int codec, const int32_t *seg_info, const int32_t *pair_order,
+                  int32_t n_pairs, int32_t n_experts, void *y, int y_dtype,
+                  int64_t y_row_stride, kq_stream_t stream);
+
+/* kq.moe_glu_gather_kq(x, gate_w, up_w, codec, idx, act) (gmlx/modules.py:557-588):
+ * h[p, :] = act(x_row(p) . Wg[e]^T) * (x_row(p) . Wu[e]^T) in fp32, act 0 =
+ * silu, 1 = gelu (tanh approximation).  h [n_pairs, N] fp32. */
+int kq_moe_glu_gather(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pair_div,
+                      const void *w_gate, const void *w_up, int64_t w_expert_bytes,
+                      int64_t w_row_bytes, int32_t N, int32_t K, int codec, int act,
+                      const int32_t *seg_info, const int32_t *pair_order, int32_t n_pairs,
+                      int32_t n_experts, float *h, kq_stream_t stream);
+
+/* The routing mix of kq.gather_qmv_mix_ns_kq (gmlx/modules.py:591-593):
+ * y[t, :] = sum_s scores[t, s] * y_pairs[t*k + s, :], fp32, slots summed in
+ * order s = 0..k-1.  y_pairs fp32 [T*k, N]; scores fp32 [T, k]; y of y_dtype. */
+int kq_moe_mix(const float *y_pairs, const float *scores, int32_t T, int32_t top_k, int32_t N,
+               void *y, int y_dtype, kq_stream_t stream);
+
+/* kq.moe_router_topk(logits, k, norm_topk_prob) (gmlx/modules.py:750-752),
+ * stock form gmlx/modules.py:754-760: softmax in fp32 -> top-k (descending,
+ * ties to the lower expert id) -> optional renormalisation.  logits [T, E] of
+ * logits_dtype; inds int32 [T, k]; scores fp32 [T, k].  E <= 1024, k <= 32. */
+int kq_moe_router_topk(const void *logits, int logits_dtype, int32_t T, int32_t E, int32_t k,
+                       int norm_topk_prob, int32_t *inds, float *scores, kq_stream_t stream);
+
+/* ---- ragged GQA decode attention ----------------------------------------- */
+/* ragged_decode_attention(q, k, v, pads, scale) (gmlx/qwen35_attn.py:395-493)
+ * and kq.sdpa_decode_gqa(q, k, v, scale, starts=) (gmlx/gemma4_batched_sdpa.py:
+ * 210-226), one query token per row:
+ *   out[b, hq, :] = softmax(scale * q[b, hq] . K_b,h^T) . V_b,h,  h = hq / (Hq/Hkv)
+ * over the row's visible keys.  Row b's keys for kv head h are the row_len[b]
+ * tokens starting at element kv_off[b] + h * head_stride[b] of k (and v), each
+ * token D contiguous elements.  Both the packed per-row slab layout
+ * ([Hkv, len_b, D] at a row offset) and the reference's padded
+ * [B, Hkv, L, D] + per-row start layout are expressible.
+ * q [B, Hq, D] (contiguous), out [B, Hq, D]; q/k/v/out share dtype (f16 or
+ * bf16).  D in {64, 96, 128, 256}; Hq % Hkv == 0; Hq/Hkv <= 16.
+ * max_len >= every row_len[b] (sizes the split table and workspace). */
+size_t kq_sdpa_workspace_bytes(int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t max_len);
+int kq_sdpa_decode_ragged(const void *q, const void *k, const void *v, const int64_t *kv_off,
+                          const int64_t *head_stride, const int32_t *row_len, int32_t B,
+                          int32_t Hq, int32_t Hkv, int32_t D, int32_t max_len, float scale,
+                          int dtype, void *out, void *workspace, size_t workspace_bytes,
+                          kq_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KQ_CAPI_H */

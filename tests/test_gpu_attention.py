@@ -1,0 +1,125 @@
+"""Ragged GQA decode attention parity (kq_sdpa_decode_ragged through the C
+ABI) against the fp64 per-row reference: the reference's construction is
+per-row SDPA over each row's unpadded keys (tests/test_ragged_decode.py:48-58).
+Pad poisoning must not leak (:126-148); outputs are deterministic."""
+import numpy as np
+import pytest
+
+from helpers import BF16_TOL, TOL, attention_ref
+from oracle import kquant as okq
+
+pytestmark = pytest.mark.gpu
+
+
+def _slabs(rng, lens, Hkv, D, dtype=np.float16):
+    offs, ks, vs, off = [], [], [], 0
+    for L in lens:
+        ks.append(rng.normal(0, 1, size=(Hkv, L, D)).astype(dtype))
+        vs.append(rng.normal(0, 1, size=(Hkv, L, D)).astype(dtype))
+        offs.append(off)
+        off += Hkv * L * D
+    kflat = np.concatenate([k.reshape(-1) for k in ks] + [np.zeros(8, dtype)])
+    vflat = np.concatenate([v.reshape(-1) for v in vs] + [np.zeros(8, dtype)])
+    return offs, ks, vs, kflat, vflat
+
+
+@pytest.mark.parametrize("D,Hq,Hkv", [(128, 32, 8), (64, 8, 8), (96, 12, 3), (256, 16, 1), (128, 16, 2)])
+def test_ragged_slabs_fp16(D, Hq, Hkv):
+    import torch
+    from gmlx_amd import ops
+    rng = np.random.default_rng(D + Hq)
+    lens = [1, 31, 33, 513, 1500, 0, 64]
+    offs, ks, vs, kf, vf = _slabs(rng, lens, Hkv, D)
+    q = rng.normal(0, 1, size=(len(lens), Hq, D)).astype(np.float16)
+    scale = D ** -0.5
+    out = ops.sdpa_decode_slabs(torch.from_numpy(q).cuda(), torch.from_numpy(kf).cuda(),
+                                torch.from_numpy(vf).cuda(), offs, lens, Hkv, scale).float().cpu().numpy()
+    ref = np.stack([attention_ref(q[b], ks[b], vs[b], scale) for b in range(len(lens))])
+    assert okq.max_rel(out, ref) <= TOL, okq.max_rel(out, ref)
+    assert np.all(out[5] == 0)          # empty row -> zeros (sum_exp == 0 branch of the reference)
+
+
+def test_long_row_many_splits_and_determinism():
+    import torch
+    from gmlx_amd import ops
+    rng = np.random.default_rng(5)
+    lens = [9000, 3, 4100]
+    offs, ks, vs, kf, vf = _slabs(rng, lens, 2, 128)
+    q = rng.normal(0, 1, size=(3, 8, 128)).astype(np.float16)
+    args = (torch.from_numpy(q).cuda(), torch.from_numpy(kf).cuda(), torch.from_numpy(vf).cuda(), offs, lens, 2,
+            128 ** -0.5)
+    outs = [ops.sdpa_decode_slabs(*args).cpu().numpy() for _ in range(3)]
+    for o in outs[1:]:
+        assert np.array_equal(o.view(np.uint16), outs[0].view(np.uint16))
+    ref = np.stack([attention_ref(q[b], ks[b], vs[b], 128 ** -0.5) for b in range(3)])
+    assert okq.max_rel(outs[0].astype(np.float32), ref) <= TOL
+
+
+def test_split_size_invariance(monkeypatch):
+    import torch
+    from gmlx_amd import ops
+    rng = np.random.default_rng(6)
+    lens = [2000, 700]
+    offs, ks, vs, kf, vf = _slabs(rng, lens, 4, 128)
+    q = rng.normal(0, 1, size=(2, 16, 128)).astype(np.float16)
+    ref = np.stack([attention_ref(q[b], ks[b], vs[b], 128 ** -0.5) for b in range(2)])
+    for split in ("32", "96", "512", "4096"):
+        monkeypatch.setenv("GMLX_KQ_SDPA_SPLIT", split)
+        out = ops.sdpa_decode_slabs(torch.from_numpy(q).cuda(), torch.from_numpy(kf).cuda(),
+                                    torch.from_numpy(vf).cuda(), offs, lens, 4, 128 ** -0.5)
+        assert okq.max_rel(out.float().cpu().numpy(), ref) <= TOL, split
+
+
+def _padded(rng, B, Hq, Hkv, L, D, dtype):
+    import torch
+    q = torch.from_numpy(rng.normal(0, 1, size=(B, Hq, 1, D)).astype(np.float32)).to(dtype)
+    k = torch.from_numpy(rng.normal(0, 1, size=(B, Hkv, L, D)).astype(np.float32)).to(dtype)
+    v = torch.from_numpy(rng.normal(0, 1, size=(B, Hkv, L, D)).astype(np.float32)).to(dtype)
+    return q, k, v
+
+
+@pytest.mark.parametrize("dtype_name", ["float16", "bfloat16"])
+def test_reference_layout_with_pads(dtype_name):
+    """ragged_decode_attention(q, k, v, pads, scale) on [B, Hkv, L, D]."""
+    import torch
+    from gmlx_amd import ops
+    dtype = getattr(torch, dtype_name)
+    rng = np.random.default_rng(21)
+    B, Hq, Hkv, L, D = 3, 16, 2, 4096, 256
+    pads = [0, 1000, 2000]
+    q, k, v = _padded(rng, B, Hq, Hkv, L, D, dtype)
+    got = ops.ragged_decode_attention(q.cuda(), k.cuda(), v.cuda(), pads, D ** -0.5)
+    assert got is not None and got.shape == (B, Hq, 1, D)
+    qf, kf, vf = q.float().numpy(), k.float().numpy(), v.float().numpy()
+    ref = np.stack([attention_ref(qf[b, :, 0], kf[b, :, pads[b]:], vf[b, :, pads[b]:], D ** -0.5)
+                    for b in range(B)])
+    tol = TOL if dtype == torch.float16 else BF16_TOL
+    assert okq.max_rel(got.float().cpu().numpy()[:, :, 0], ref) <= tol
+
+
+def test_pads_are_honored():
+    """Poisoning the pad region cannot change the output (bit-exact)."""
+    import torch
+    from gmlx_amd import ops
+    rng = np.random.default_rng(1)
+    B, Hq, Hkv, L, D = 2, 16, 2, 4096, 128
+    pads = [512, 0]
+    q, k, v = _padded(rng, B, Hq, Hkv, L, D, torch.bfloat16)
+    clean = ops.ragged_decode_attention(q.cuda(), k.cuda(), v.cuda(), pads, D ** -0.5)
+    k2 = k.clone()
+    k2[0, :, :pads[0]] = 40.0
+    v2 = v.clone()
+    v2[0, :, :pads[0]] = -40.0
+    dirty = ops.ragged_decode_attention(q.cuda(), k2.cuda(), v2.cuda(), pads, D ** -0.5)
+    assert torch.equal(clean.cpu(), dirty.cpu())
+
+
+def test_sdpa_decode_gqa_starts():
+    import torch
+    from gmlx_amd import ops
+    rng = np.random.default_rng(3)
+    q, k, v = _padded(rng, 2, 8, 1, 640, 64, torch.float16)
+    starts = torch.tensor([0, 100], dtype=torch.int32)
+    got = ops.sdpa_decode_gqa(q.cuda(), k.cuda(), v.cuda(), 0.125, starts=starts)
+    ref = ops.ragged_decode_attention(q.cuda(), k.cuda(), v.cuda(), [0, 100], 0.125)
+    assert torch.equal(got.cpu(), ref.cpu())

@@ -1,0 +1,157 @@
+"""Dequant-fused quantized matmul parity (kq_quantized_matmul_grouped through
+the C ABI): max-rel <= 2e-3 against the fp64 oracle, plus the reference's
+structural properties (row independence of concatenated wires,
+gmlx/occupancy_fuse.py:32-34; B=1 inside a batch equals M=1,
+tests/test_batch_parity.py:147-159; permutation; determinism)."""
+import os
+
+import numpy as np
+import pytest
+
+from helpers import TOL, fp16_rows, quantized_weights
+from oracle import kquant as okq
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _mm(x16, wire, codec, **kw):
+    from gmlx_amd import ops
+    return ops.quantized_matmul(_dev(x16), _dev(wire), None, codec, **kw)
+
+
+def test_config1_q4k_matvec():
+    """Q4_K 3072x1024 from N(0, 0.02), x fp16 [1, 1024] N(0, 1), seed 0."""
+    rng = np.random.default_rng(0)
+    w = rng.normal(0.0, 0.02, size=(3072, 1024)).astype(np.float32)
+    wire = okq.quantize(w, "q4_k")
+    x = rng.normal(0.0, 1.0, size=(1, 1024)).astype(np.float16)
+    ref = okq.qmm_ref(x, wire, "q4_k")
+    got = _mm(x, wire, "q4_k").float().cpu().numpy()
+    assert got.shape == (1, 3072)
+    assert okq.max_rel(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("codec", ["q4_k", "q6_k", "iq2_xxs"])
+@pytest.mark.parametrize("M", [1, 2, 3, 5, 8, 13, 16, 17, 31, 33, 64, 65])
+def test_small_m_parity(codec, M):
+    rng = np.random.default_rng(100 + M)
+    N, K = 200, 1280                # N not a multiple of 16, K = 5 blocks (partial 4-block step)
+    wire = quantized_weights(rng, codec, N, K) if codec != "iq2_xxs" else okq.random_valid_blocks(
+        rng, codec, N * K // 256).reshape(N, -1)
+    x = fp16_rows(rng, M, K)
+    ref = okq.qmm_ref(x, wire, codec)
+    got = _mm(x, wire, codec).float().cpu().numpy()
+    assert okq.max_rel(got, ref) <= TOL, okq.max_rel(got, ref)
+
+
+@pytest.mark.parametrize("codec", ["q4_k", "q6_k"])
+def test_config2_shapes_b8(codec):
+    """Config 2 geometry (K 4096 and 12288) at B=8."""
+    rng = np.random.default_rng(7)
+    for N, K in [(1024, 4096), (512, 12288)]:
+        wire = quantized_weights(rng, codec, N, K)
+        x = fp16_rows(rng, 8, K)
+        ref = okq.qmm_ref(x, wire, codec)
+        got = _mm(x, wire, codec).float().cpu().numpy()
+        assert okq.max_rel(got, ref) <= TOL
+
+
+def test_bf16_activations_and_f32_out():
+    import torch
+    from gmlx_amd import ops
+    rng = np.random.default_rng(8)
+    wire = quantized_weights(rng, "q4_k", 96, 512)
+    x32 = rng.normal(0, 1, size=(4, 512)).astype(np.float32)
+    xb = torch.from_numpy(x32).to(torch.bfloat16)
+    ref = okq.qmm_ref(xb.float().numpy(), wire, "q4_k")
+    got = ops.quantized_matmul(xb.cuda(), _dev(wire), None, "q4_k").float().cpu().numpy()
+    assert okq.max_rel(got, ref) <= TOL
+    got32 = ops.quantized_matmul(xb.cuda(), _dev(wire), None, "q4_k", out_dtype=torch.float32)
+    assert got32.dtype == torch.float32
+    assert okq.max_rel(got32.cpu().numpy(), ref) <= TOL
+
+
+def test_grouped_equals_separate_bitwise():
+    """q|k|v with mixed codecs in one launch == three separate launches."""
+    from gmlx_amd import ops
+    rng = np.random.default_rng(9)
+    K = 1024
+    wq = quantized_weights(rng, "q4_k", 256, K)
+    wk = quantized_weights(rng, "q4_k", 64, K)
+    wv = quantized_weights(rng, "q6_k", 64, K)
+    x = _dev(fp16_rows(rng, 4, K))
+    outs = ops.quantized_matmul_grouped([(x, _dev(wq), "q4_k"), (x, _dev(wk), "q4_k"), (x, _dev(wv), "q6_k")])
+    for o, (w, c) in zip(outs, [(wq, "q4_k"), (wk, "q4_k"), (wv, "q6_k")]):
+        sep = ops.quantized_matmul(x, _dev(w), None, c)
+        assert np.array_equal(o.cpu().numpy().view(np.uint16), sep.cpu().numpy().view(np.uint16))
+
+
+def test_row_concatenated_wire_is_row_independent():
+    """Output rows of a row-concatenated wire equal the separate matmuls."""
+    rng = np.random.default_rng(10)
+    K = 512
+    wa = quantized_weights(rng, "q4_k", 48, K)
+    wb = quantized_weights(rng, "q4_k", 80, K)
+    x = fp16_rows(rng, 3, K)
+    cat = _mm(x, np.concatenate([wa, wb]), "q4_k").cpu().numpy()
+    a = _mm(x, wa, "q4_k").cpu().numpy()
+    b = _mm(x, wb, "q4_k").cpu().numpy()
+    # k-splitting depends on N, so compare within tolerance and exactly when plans agree
+    ref = okq.qmm_ref(x, np.concatenate([wa, wb]), "q4_k")
+    assert okq.max_rel(cat.astype(np.float32), ref) <= TOL
+    assert okq.max_rel(np.concatenate([a, b], axis=1).astype(np.float32), ref) <= TOL
+
+
+def test_batch_row_equals_single_row_and_permutation():
+    rng = np.random.default_rng(12)
+    wire = quantized_weights(rng, "q4_k", 160, 2048)
+    x = fp16_rows(rng, 8, 2048)
+    full = _mm(x, wire, "q4_k").cpu().numpy()
+    one = _mm(x[3:4], wire, "q4_k").cpu().numpy()
+    assert np.array_equal(full[3:4].view(np.uint16), one.view(np.uint16))
+    perm = rng.permutation(8)
+    pm = _mm(x[perm], wire, "q4_k").cpu().numpy()
+    assert np.array_equal(pm.view(np.uint16), full[perm].view(np.uint16))
+
+
+def test_deterministic_split_k():
+    rng = np.random.default_rng(13)
+    wire = quantized_weights(rng, "q6_k", 64, 4096)   # few tiles -> k split across waves
+    x = fp16_rows(rng, 5, 4096)
+    outs = [_mm(x, wire, "q6_k").cpu().numpy() for _ in range(4)]
+    for o in outs[1:]:
+        assert np.array_equal(o.view(np.uint16), outs[0].view(np.uint16))
+    ref = okq.qmm_ref(x, wire, "q6_k")
+    assert okq.max_rel(outs[0].astype(np.float32), ref) <= TOL
+
+
+def test_split_plan_invariance(monkeypatch):
+    """Changing the K-split plan changes summation order only (tolerance)."""
+    rng = np.random.default_rng(14)
+    wire = quantized_weights(rng, "q4_k", 64, 4096)
+    x = fp16_rows(rng, 2, 4096)
+    ref = okq.qmm_ref(x, wire, "q4_k")
+    for waves in ("1", "64", "100000"):
+        monkeypatch.setenv("GMLX_KQ_MM_WAVES", waves)
+        got = _mm(x, wire, "q4_k").float().cpu().numpy()
+        assert okq.max_rel(got, ref) <= TOL, waves
+
+
+def test_module_forward():
+    import torch
+    from gmlx_amd.nn import KQuantLinear
+    rng = np.random.default_rng(15)
+    wire = quantized_weights(rng, "q4_k", 128, 512)
+    mod = KQuantLinear(512, 128, bias=True, codec="q4_k").cuda()
+    mod.weight.copy_(_dev(wire))
+    with torch.no_grad():
+        mod.bias.copy_(torch.linspace(-1, 1, 128))
+    x = fp16_rows(rng, 3, 512)
+    got = mod(_dev(x).reshape(3, 1, 512)).float().cpu().numpy().reshape(3, 128)
+    ref = okq.qmm_ref(x, wire, "q4_k") + np.linspace(-1, 1, 128)
+    assert okq.max_rel(got, ref) <= TOL

@@ -1,0 +1,150 @@
+"""MoE expert-gather family parity through the C ABI: routing, gather_qmm
+(KQuantSwitchLinear, tests/test_native_fp.py:420-428 convention), the fused
+GLU gather, the per-pair down gather, the routing mix (fp32, slots in order),
+and the router top-k (gmlx/modules.py:754-760 stock form)."""
+import numpy as np
+import pytest
+
+from helpers import TOL, fp16_rows, quantized_weights
+from oracle import kquant as okq
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _experts(rng, codec, E, N, K):
+    if codec == "iq2_xxs":
+        return okq.random_valid_blocks(rng, codec, E * N * K // 256).reshape(E, N, -1)
+    return np.stack([quantized_weights(rng, codec, N, K) for _ in range(E)])
+
+
+def test_route_groups_pairs_stably():
+    import torch
+    from gmlx_amd import ops
+    rng = np.random.default_rng(0)
+    idx = rng.integers(0, 16, size=(37, 4)).astype(np.int32)
+    seg, order = ops.moe_route(_dev(idx), 16)
+    seg, order = seg.cpu().numpy(), order.cpu().numpy()
+    flat = idx.reshape(-1)
+    P = flat.size
+    S = seg[0]
+    uniq = np.unique(flat)
+    assert S == len(uniq)
+    assert list(seg[1:1 + S]) == list(uniq)
+    assert np.array_equal(order[:P], np.argsort(flat, kind="stable"))
+    assert np.array_equal(order[P:2 * P], flat)
+
+
+@pytest.mark.parametrize("codec", ["q4_k", "q6_k", "iq2_xxs"])
+def test_gather_qmm(codec):
+    from gmlx_amd import ops
+    rng = np.random.default_rng(1)
+    E, N, K, T, k = 12, 80, 512, 9, 3
+    w = _experts(rng, codec, E, N, K)
+    deq = okq.dequantize(w, codec).astype(np.float64)
+    x = fp16_rows(rng, T, K)
+    idx = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    got = ops.gather_qmm(_dev(x).reshape(T, 1, 1, K), _dev(w), None, codec, indices=_dev(idx))
+    assert tuple(got.shape) == (T, k, 1, N)
+    ref = np.stack([[deq[idx[t, s]] @ x[t].astype(np.float64) for s in range(k)] for t in range(T)])
+    assert okq.max_rel(got.float().cpu().numpy()[:, :, 0], ref) <= TOL
+
+
+def test_gather_many_rows_per_expert():
+    """Segments larger than one 64-row chunk (prefill-sized)."""
+    from gmlx_amd import ops
+    rng = np.random.default_rng(2)
+    E, N, K, T, k = 3, 48, 256, 150, 2
+    w = _experts(rng, "q4_k", E, N, K)
+    deq = okq.dequantize(w, "q4_k").astype(np.float64)
+    x = fp16_rows(rng, T, K)
+    idx = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    got = ops.gather_qmm(_dev(x), _dev(w), None, "q4_k", indices=_dev(idx)).float().cpu().numpy()[:, :, 0]
+    ref = np.stack([[deq[idx[t, s]] @ x[t].astype(np.float64) for s in range(k)] for t in range(T)])
+    assert okq.max_rel(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("act", ["silu", "gelu"])
+def test_moe_glu_then_down_then_mix(act):
+    import torch
+    from gmlx_amd import ops
+    rng = np.random.default_rng(3)
+    E, D, I, T, k = 16, 512, 256, 5, 4
+    gw = _experts(rng, "q4_k", E, I, D)
+    uw = _experts(rng, "q4_k", E, I, D)
+    dw = _experts(rng, "q6_k", E, D, I)
+    x = fp16_rows(rng, T, D)
+    logits = rng.normal(0, 1, size=(T, E)).astype(np.float32)
+    inds, scores = ops.moe_router_topk(_dev(logits), k, True)
+    idx = inds.cpu().numpy()
+    sc = scores.cpu().numpy()
+    h = ops.moe_glu_gather_kq(_dev(x), _dev(gw), _dev(uw), "q4_k", inds, act=act)
+    assert h.dtype == torch.float32 and tuple(h.shape) == (T, k, I)
+    g_deq = okq.dequantize(gw, "q4_k").astype(np.float64)
+    u_deq = okq.dequantize(uw, "q4_k").astype(np.float64)
+    d_deq = okq.dequantize(dw, "q6_k").astype(np.float64)
+    xf = x.astype(np.float64)
+
+    def actf(z):
+        if act == "silu":
+            return z / (1 + np.exp(-z))
+        return 0.5 * z * (1 + np.tanh(0.7978845608028654 * (z + 0.044715 * z ** 3)))
+
+    href = np.stack([[actf(g_deq[idx[t, s]] @ xf[t]) * (u_deq[idx[t, s]] @ xf[t]) for s in range(k)]
+                     for t in range(T)])
+    assert okq.max_rel(h.cpu().numpy(), href) <= TOL
+    y = ops.gather_qmv_kq(h, _dev(dw), "q6_k", inds)
+    yref = np.stack([[d_deq[idx[t, s]] @ href[t, s] for s in range(k)] for t in range(T)])
+    assert okq.max_rel(y.cpu().numpy(), yref) <= TOL
+    mixed = ops.gather_qmv_mix_ns_kq(h, _dev(dw), "q6_k", inds, scores)
+    mref = np.einsum("tk,tkn->tn", sc.astype(np.float64), yref)
+    assert okq.max_rel(mixed.cpu().numpy(), mref) <= TOL
+    # mix == sum over slots of the per-pair outputs (fp32, in order)
+    manual = (y.cpu().numpy() * sc[..., None]).sum(1)
+    assert np.allclose(mixed.cpu().numpy(), manual, rtol=1e-5, atol=1e-6)
+
+
+def test_router_topk_matches_numpy():
+    from gmlx_amd import ops
+    rng = np.random.default_rng(4)
+    for E, k, norm in [(128, 8, True), (256, 8, False), (60, 4, True)]:
+        logits = rng.normal(0, 1, size=(17, E)).astype(np.float32)
+        inds, scores = ops.moe_router_topk(_dev(logits), k, norm)
+        p = np.exp(logits - logits.max(-1, keepdims=True))
+        p /= p.sum(-1, keepdims=True)
+        order = np.argsort(-p, axis=-1, kind="stable")[:, :k]
+        assert np.array_equal(inds.cpu().numpy(), order)
+        sel = np.take_along_axis(p, order, -1)
+        if norm:
+            sel = sel / sel.sum(-1, keepdims=True)
+        assert np.allclose(scores.cpu().numpy(), sel, rtol=1e-5, atol=1e-7)
+
+
+def test_out_of_range_expert_gives_zeros():
+    from gmlx_amd import ops
+    rng = np.random.default_rng(5)
+    w = _experts(rng, "q4_k", 4, 32, 256)
+    x = fp16_rows(rng, 3, 256)
+    idx = np.array([[0, 9], [1, 2], [-1, 3]], np.int32)
+    got = ops.gather_qmm(_dev(x), _dev(w), None, "q4_k", indices=_dev(idx)).float().cpu().numpy()
+    assert np.all(got[0, 1] == 0) and np.all(got[2, 0] == 0)
+    deq = okq.dequantize(w, "q4_k").astype(np.float64)
+    assert okq.max_rel(got[1, 0, 0], deq[1] @ x[1].astype(np.float64)) <= TOL
+
+
+def test_switch_linear_module():
+    from gmlx_amd.nn import KQuantSwitchLinear
+    rng = np.random.default_rng(6)
+    w = _experts(rng, "q6_k", 6, 64, 512)
+    mod = KQuantSwitchLinear(6, 64, 512, False, "q6_k").cuda()
+    mod.weight.copy_(_dev(w))
+    x = fp16_rows(rng, 4, 512)
+    idx = np.array([[0, 5], [1, 1 + 1], [3, 4], [5, 0]], np.int32)
+    got = mod(_dev(x).reshape(4, 1, 1, 512), _dev(idx)).float().cpu().numpy()
+    deq = okq.dequantize(w, "q6_k").astype(np.float64)
+    ref = np.stack([[deq[idx[t, s]] @ x[t].astype(np.float64) for s in range(2)] for t in range(4)])
+    assert okq.max_rel(got[:, :, 0], ref) <= TOL

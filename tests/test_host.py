@@ -1,0 +1,159 @@
+"""Host-side checks that need no GPU: the C-ABI library loads and exports
+every symbol include/kq_capi.h declares, capability probes and error strings,
+the ops' CPU-side validation and decline rails, fault injection, the wire-K
+rule, and the leaf-module swap."""
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _header_symbols():
+    text = open(os.path.join(ROOT, "include", "kq_capi.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(kq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    from gmlx_amd import _lib
+    L = _lib.lib()
+    declared = _header_symbols()
+    assert declared, "no declarations parsed"
+    for name in declared:
+        assert hasattr(L, name), name
+    assert set(declared) == set(_lib.EXPORTS)
+
+
+def test_version_strerror_and_capabilities():
+    from gmlx_amd import _lib, ops
+    assert "gfx950" in _lib.version()
+    L = _lib.lib()
+    assert L.kq_strerror(0) == b"ok"
+    assert b"workspace" in L.kq_strerror(_lib.KQ_ERR_WORKSPACE_TOO_SMALL)
+    assert L.kq_codec_block_bytes(12) == 144 and L.kq_codec_block_bytes(14) == 210
+    assert L.kq_codec_block_bytes(16) == 66 and L.kq_codec_block_bytes(2) == 0
+    assert ops.codecs() == ("q4_k", "q6_k", "iq2_xxs")
+    assert all(ops.codec_has_matmul(c) and ops.codec_has_moe_glu(c) for c in ops.codecs())
+    assert not ops.codec_has_matmul("q8_0")
+    assert L.kq_supports(_lib.OP_SDPA, 0, _lib.DTYPE_F32) == 0
+
+
+def test_library_grid_table_is_pinned():
+    from gmlx_amd import _lib
+    from oracle import kquant as okq
+    ptr = _lib.lib().kq_iq2xxs_grid_host()
+    assert [ptr[i] for i in range(256)] == okq.iq2xxs_grid()
+
+
+def test_host_validation_rejects_before_launch():
+    """Bad shapes / codecs / workspaces are refused by the C ABI with status
+    codes and nothing is launched (null stream, no GPU needed)."""
+    import ctypes
+    from gmlx_amd import _lib
+    L = _lib.lib()
+    P = _lib.MatmulProblem
+    good = dict(w=16, w_row_bytes=144 * 4, x=16, x_row_stride=1024, y=16, y_row_stride=64, M=2, N=64, K=1024,
+                codec=12)
+
+    def call(**over):
+        d = dict(good, **over)
+        arr = (P * 1)(P(**d))
+        return L.kq_quantized_matmul_grouped(arr, 1, _lib.DTYPE_F16, _lib.DTYPE_F16, None, 0, None)
+
+    assert call(K=1000) == _lib.KQ_ERR_BAD_SHAPE
+    assert call(codec=3) == _lib.KQ_ERR_UNSUPPORTED_CODEC
+    assert call(w_row_bytes=100) == _lib.KQ_ERR_BAD_SHAPE
+    assert call(x=18) == _lib.KQ_ERR_BAD_ALIGN
+    assert call(w=0) == _lib.KQ_ERR_NULL_POINTER
+    arr = (P * 1)(P(**good))
+    assert L.kq_quantized_matmul_grouped(arr, 1, _lib.DTYPE_F32, _lib.DTYPE_F16, None, 0, None) == \
+        _lib.KQ_ERR_UNSUPPORTED_DTYPE
+    assert L.kq_quantized_matmul_grouped(arr, 9, _lib.DTYPE_F16, _lib.DTYPE_F16, None, 0, None) == \
+        _lib.KQ_ERR_TOO_MANY_PROBLEMS
+    # a K-split plan needs workspace: refuse a null / short one
+    small_n = dict(good, N=16, K=4096, w_row_bytes=144 * 16, x_row_stride=4096)
+    arr = (P * 1)(P(**small_n))
+    need = L.kq_matmul_workspace_bytes(arr, 1)
+    assert need > 0
+    assert L.kq_quantized_matmul_grouped(arr, 1, _lib.DTYPE_F16, _lib.DTYPE_F16, None, 0, None) == \
+        _lib.KQ_ERR_WORKSPACE_TOO_SMALL
+    assert L.kq_sdpa_decode_ragged(16, 16, 16, 16, 16, 16, 2, 8, 3, 128, 100, 0.1, _lib.DTYPE_F16, 16, 16,
+                                   1 << 20, None) == _lib.KQ_ERR_BAD_SHAPE
+    assert L.kq_sdpa_decode_ragged(16, 16, 16, 16, 16, 16, 2, 8, 2, 80, 100, 0.1, _lib.DTYPE_F16, 16, 16,
+                                   1 << 20, None) == _lib.KQ_ERR_BAD_SHAPE
+    assert L.kq_sdpa_decode_ragged(16, 16, 16, 16, 16, 16, 2, 8, 2, 128, 100, 0.1, _lib.DTYPE_F16, 16, 16,
+                                   16, None) == _lib.KQ_ERR_WORKSPACE_TOO_SMALL
+    assert L.kq_moe_router_topk(16, 0, 4, 2000, 8, 1, 16, 16, None) == _lib.KQ_ERR_BAD_SHAPE
+    assert L.kq_dequantize(16, 4, 99, 16, 0, None) == _lib.KQ_ERR_UNSUPPORTED_CODEC
+    assert L.kq_quantize(16, 2, 100, 100, 12, 16, None) == _lib.KQ_ERR_BAD_SHAPE
+    _ = ctypes
+
+
+def test_ops_refuse_cpu_tensors():
+    from gmlx_amd import ops
+    x = torch.zeros(2, 256, dtype=torch.float16)
+    w = torch.zeros(16, 144, dtype=torch.uint8)
+    with pytest.raises(ValueError, match="GPU only"):
+        ops.quantized_matmul(x, w, None, "q4_k")
+    with pytest.raises(ValueError, match="GPU only"):
+        ops.dequantize(w, None, "q4_k")
+
+
+def test_ragged_attention_declines_like_the_reference():
+    """Guard rails return None before any GPU work (gmlx/qwen35_attn.py:412-431)."""
+    from gmlx_amd import ops
+    q = torch.zeros(2, 16, 1, 80, dtype=torch.bfloat16)
+    k = torch.zeros(2, 2, 512, 80, dtype=torch.bfloat16)
+    assert ops.ragged_decode_attention(q, k, k, [0, 0], 80 ** -0.5) is None        # head dim 80
+    q = torch.zeros(2, 16, 1, 128, dtype=torch.float16)
+    k = torch.zeros(2, 2, 512, 128, dtype=torch.float16)
+    assert ops.ragged_decode_attention(q, k, k, [0], 0.1) is None                    # pads != B
+    assert ops.ragged_decode_attention(q, k, k, [0, -1], 0.1) is None                # negative pad
+    assert ops.ragged_decode_attention(q, k, k, [0, 512], 0.1) is None               # pad >= L
+    assert ops.ragged_decode_attention(q.float(), k.float(), k.float(), [0, 0], 0.1) is None
+    q2 = torch.zeros(2, 16, 2, 128, dtype=torch.float16)
+    assert ops.ragged_decode_attention(q2, k, k, [0, 0], 0.1) is None                # S != 1
+    k3 = torch.zeros(2, 3, 512, 128, dtype=torch.float16)
+    assert ops.ragged_decode_attention(q, k3, k3, [0, 0], 0.1) is None               # Hq % Hkv
+
+
+def test_fault_injection(monkeypatch):
+    from gmlx_amd import KQError, ops
+    monkeypatch.setenv("GMLX_HIP_FAULT", "quantized_matmul,moe_router_topk")
+    x = torch.zeros(2, 256, dtype=torch.float16)
+    w = torch.zeros(16, 144, dtype=torch.uint8)
+    with pytest.raises(KQError, match="fault injected"):
+        ops.quantized_matmul(x, w, None, "q4_k")
+    with pytest.raises(KQError):
+        ops.moe_router_topk(torch.zeros(2, 8), 2)
+    # an injected fault on the attention route reads as a decline upstream
+    monkeypatch.setenv("GMLX_HIP_FAULT", "ragged_decode_attention")
+    q = torch.zeros(1, 8, 1, 64, dtype=torch.float16)
+    k = torch.zeros(1, 2, 64, 64, dtype=torch.float16)
+    with pytest.raises(KQError):
+        ops.ragged_decode_attention(q, k, k, [0], 0.1)
+
+
+def test_wire_k_rule():
+    from gmlx_amd.ops import wire_k
+    assert wire_k(144 * 16, "q4_k") == 4096
+    assert wire_k(210 * 48, "q6_k") == 12288
+    assert wire_k(66 * 28, "iq2_xxs") == 7168
+    assert wire_k(145, "q4_k") == -1
+
+
+def test_install_kquant_modules_swaps_linear_leaves():
+    from gmlx_amd.nn import KQuantLinear, install_kquant_modules
+    model = torch.nn.Sequential(torch.nn.Linear(512, 64), torch.nn.ReLU(), torch.nn.Linear(64, 8))
+    n = install_kquant_modules(model, {"0.weight": "q6_k"})
+    assert n == 1
+    assert isinstance(model[0], KQuantLinear) and model[0].kquant_type == "q6_k"
+    assert tuple(model[0].weight.shape) == (64, 2 * 210) and model[0].bias is not None
+    assert isinstance(model[2], torch.nn.Linear)
+    with pytest.raises(ValueError, match="no recognized module"):
+        install_kquant_modules(model, {"1.weight": "q4_k"})
+    _ = np
