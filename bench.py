@@ -1,0 +1,323 @@
+#!/usr/bin/env python3
+"""Benchmark of the K-quant batched-decode hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch B]
+
+Headline: one decode step through the linear layers of a
+Qwen3-8B Q4_K_M stack -- 36 layers, each q 4096x4096, k 1024x4096,
+o 4096x4096, gate/up 12288x4096 in Q4_K and v 1024x4096, down 4096x12288 in
+Q6_K -- at B rows of fp16 activations.  Per layer the launches follow the
+decode data flow: q|k|v grouped (one launch), o, gate|up grouped, down.
+Every layer has its own weight bytes (4.41 GB per step), so nothing is served
+from the 256 MB MALL.  A step is replayed from a HIP graph (the launches are
+5-10 us each; eager Python launching would measure the host).
+
+`value` = algorithmic weight + activation bytes per step / step time (GB/s).
+The `roofline` object is for the dense grouped matmul kernel (every launch of
+the step): achieved = algorithmic bytes per launch / average launch duration,
+both over the timed region.  Extra fields: the per-B sweep (B = 1..64, same
+stack), ragged GQA decode attention at BASELINE config 3 (KV GB/s, KV tokens/s)
+and the CPU baseline (the repository's OpenMP C restatement of the same
+dequant-fused matmul, timed on a bounded sample of the same workload).
+
+Inputs: numpy default_rng(seed) draws, N(0, 0.02) weights quantised on the GPU
+by kq_quantize (byte-identical to the llama.cpp-style reference quantiser in
+oracle/), fp16 N(0, 1) activations.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "Q4_K_M decode matmul GB/s (% HBM peak) at B=1..64; ragged SDPA tokens/s"
+
+HIDDEN, INTER, LAYERS = 4096, 12288, 36
+# (name, N, K, codec) of one Qwen3-8B layer under the Q4_K_M mix
+LAYER = [("q", 4096, 4096, "q4_k"), ("k", 1024, 4096, "q4_k"), ("v", 1024, 4096, "q6_k"),
+         ("o", 4096, 4096, "q4_k"), ("gate", INTER, 4096, "q4_k"), ("up", INTER, 4096, "q4_k"),
+         ("down", 4096, INTER, "q6_k")]
+BPB = {"q4_k": 144, "q6_k": 210}
+C3_LENS_SEED = 0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def wire_bytes(N, K, codec):
+    return N * (K // 256) * BPB[codec]
+
+
+def layer_bytes(B):
+    """Algorithmic bytes of one layer at B rows: weights + fp16 x in + fp16 y out."""
+    tot = 0
+    for _, N, K, codec in LAYER:
+        tot += wire_bytes(N, K, codec) + B * K * 2 + B * N * 2
+    return tot
+
+
+# ------------------------------------------------------------------ weights
+
+def make_stack(torch, ops, layers, seed=0):
+    """`layers` distinct layers of wire bytes on the GPU.  The first layer is
+    quantised from numpy draws (seed, draw order q, k, v, o, gate, up, down);
+    the others are byte copies at their own addresses."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    base = {}
+    for name, N, K, codec in LAYER:
+        w = torch.from_numpy(rng.normal(0.0, 0.02, size=(N, K)).astype(np.float32)).cuda()
+        base[name] = ops.quantize(w, codec)[0]
+        del w
+    stack = [base]
+    for _ in range(layers - 1):
+        stack.append({k: v.clone() for k, v in base.items()})
+    torch.cuda.synchronize()
+    return stack, rng
+
+
+def make_inputs(torch, rng, B):
+    import numpy as np
+    x = torch.from_numpy(rng.normal(0.0, 1.0, size=(B, HIDDEN)).astype(np.float16)).cuda()
+    xd = torch.from_numpy(rng.normal(0.0, 1.0, size=(B, INTER)).astype(np.float16)).cuda()
+    return x, xd
+
+
+def step_fn(ops, stack, x, xd):
+    """One decode step of the linear stack: 4 launches per layer."""
+    outs = []
+    for L in stack:
+        q, k, v = ops.quantized_matmul_grouped([(x, L["q"], "q4_k"), (x, L["k"], "q4_k"), (x, L["v"], "q6_k")])
+        o = ops.quantized_matmul(x, L["o"], None, "q4_k")
+        g, u = ops.quantized_matmul_grouped([(x, L["gate"], "q4_k"), (x, L["up"], "q4_k")])
+        d = ops.quantized_matmul(xd, L["down"], None, "q6_k")
+        outs = [q, k, v, o, g, u, d]
+    return outs
+
+
+def capture(torch, fn):
+    fn()  # eager warm-up: grows the workspace outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = fn()
+    torch.cuda.synchronize()
+    return g, outs
+
+
+def time_graph(torch, g, steps, warmup):
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps  # ms per replay
+
+
+# ---------------------------------------------------------------- attention
+
+def c3_lengths(seed=C3_LENS_SEED, B=16):
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    return np.exp(rng.uniform(math.log(1024), math.log(131072), B)).astype(np.int64), rng
+
+
+def bench_sdpa(torch, ops, iters=20):
+    """32 q heads / 8 kv heads, D 128, B 16 ragged rows in
+    per-row [Hkv, len, D] slabs (offset table), fp16, scale 1/sqrt(128)."""
+    import numpy as np
+    lens, rng = c3_lengths()
+    B, Hq, Hkv, D = 16, 32, 8, 128
+    offs = np.concatenate([[0], np.cumsum(lens * Hkv * D)[:-1]]).astype(np.int64)
+    total = int(lens.sum()) * Hkv * D
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    k = torch.randn(total, generator=gen, device="cuda", dtype=torch.float32).half()
+    v = torch.randn(total, generator=gen, device="cuda", dtype=torch.float32).half()
+    q = torch.from_numpy(rng.normal(0, 1, size=(B, Hq, D)).astype(np.float16)).cuda()
+    scale = 1.0 / math.sqrt(D)
+    run = lambda: ops.sdpa_decode_slabs(q, k, v, offs.tolist(), lens.tolist(), Hkv, scale)  # noqa: E731
+    out = run()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    for _ in range(3):
+        run()
+    e0.record()
+    for _ in range(iters):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / iters
+    kv_bytes = 2 * total * 2
+    qo_bytes = 2 * B * Hq * D * 2
+    # spot-check two heads of the shortest and longest rows against fp64
+    chk = 0.0
+    for b in (int(np.argmin(lens)), int(np.argmax(lens))):
+        L = int(lens[b])
+        for hq in (0, Hq - 1):
+            h = hq // (Hq // Hkv)
+            base = int(offs[b]) + h * L * D
+            kb = k[base:base + L * D].view(L, D).double().cpu().numpy()
+            vb = v[base:base + L * D].view(L, D).double().cpu().numpy()
+            s = kb @ q[b, hq].double().cpu().numpy() * scale
+            p = np.exp(s - s.max())
+            ref = p @ vb / p.sum()
+            got = out[b, hq].double().cpu().numpy()
+            chk = max(chk, float(np.abs(got - ref).max() / np.abs(ref).max()))
+    del k, v
+    return {
+        "workload": "C3 ragged GQA decode, 32q/8kv heads, D=128, B=16, lens log-uniform 1k..128k (seed 0), fp16",
+        "kv_tokens": int(lens.sum()),
+        "ms": round(ms, 4),
+        "kv_gbs": round(kv_bytes / ms / 1e6, 1),
+        "frac_hbm": round(kv_bytes / ms / 1e6 / HBM_PEAK_GBS, 4),
+        "kv_tokens_per_s": round(int(lens.sum()) / ms * 1e3, 1),
+        "rows_per_s": round(B / ms * 1e3, 1),
+        "algorithmic_bytes": kv_bytes + qo_bytes,
+        "max_rel_spot": chk,
+    }
+
+
+# -------------------------------------------------------------- CPU baseline
+
+def cpu_baseline(layer_wires, B, budget_s=12.0):
+    """The oracle's OpenMP dequant-fused fp32 matmul (oracle/kq_oracle.c
+    kqo_qmm_f32) on one C2 layer at B rows, repeated until ~budget_s.
+    layer_wires: {name: uint8 numpy wire} of one layer."""
+    import numpy as np
+    from oracle import kquant as okq
+    rng = np.random.default_rng(1)
+    layer = [(layer_wires[name], K, codec) for name, N, K, codec in LAYER]
+    xs = {K: rng.normal(0, 1, size=(B, K)).astype(np.float16) for K in (HIDDEN, INTER)}
+    cores = len(os.sched_getaffinity(0))
+    nthreads = min(cores, 16)
+    done, t0 = 0, time.perf_counter()
+    while True:
+        for wire, K, codec in layer:
+            okq.qmm_f32_cpu(xs[K], wire, codec, nthreads=nthreads)
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or done >= 50:
+            break
+    gbs = done * layer_bytes(B) / el / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": nthreads, "kind": "port",
+            "sample": f"{done} pass(es) of one C2 layer (7 matrices, 122.6 MB of wire) at B={B}, "
+                      f"{el:.1f} s, oracle/kq_oracle.c kqo_qmm_f32 (OpenMP, fp32)"}
+
+
+# --------------------------------------------------------------------- main
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--batch", type=int, default=8)
+    ap.add_argument("--layers", type=int, default=LAYERS)
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-sdpa", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from gmlx_amd import ops
+    import gmlx_amd
+    gmlx_amd.lib()  # fails loudly when the HIP library is missing
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+
+    log(f"[bench] building {args.layers}-layer Q4_K_M stack on {torch.cuda.get_device_name(0)}")
+    stack, rng = make_stack(torch, ops, args.layers)
+    B = args.batch
+    x, xd = make_inputs(torch, rng, B)
+    g, outs = capture(torch, lambda: step_fn(ops, stack, x, xd))
+    # graph replays must reproduce the eager result bit for bit
+    g.replay()
+    torch.cuda.synchronize()
+    eager = step_fn(ops, stack, x, xd)
+    torch.cuda.synchronize()
+    replay_ok = all(torch.equal(a, b) for a, b in zip(outs, eager))
+    log(f"[bench] graph captured, replay==eager: {replay_ok}")
+
+    torch.cuda.synchronize()
+    ms = time_graph(torch, g, args.steps, args.warmup)
+    step_bytes = args.layers * layer_bytes(B)
+    value = step_bytes / ms / 1e6
+    launches = 4 * args.layers
+    log(f"[bench] B={B}: {ms:.3f} ms/step, {value:.1f} GB/s")
+
+    per_batch = {}
+    if not args.no_sweep:
+        for b in (1, 2, 4, 8, 16, 32, 64):
+            xb, xdb = make_inputs(torch, rng, b)
+            gb, _ = capture(torch, lambda: step_fn(ops, stack, xb, xdb))
+            msb = time_graph(torch, gb, max(5, args.steps // 2), 2)
+            gbs = args.layers * layer_bytes(b) / msb / 1e6
+            per_batch[str(b)] = {"ms_per_step": round(msb, 4), "gbs": round(gbs, 1),
+                                 "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                                 "tflops": round(2 * b * args.layers * sum(N * K for _, N, K, _ in LAYER)
+                                                 / msb / 1e9, 2)}
+            log(f"[bench] sweep B={b}: {msb:.3f} ms/step, {gbs:.1f} GB/s")
+            del gb
+
+    sdpa = None
+    if not args.no_sdpa:
+        sdpa = bench_sdpa(torch, ops)
+        log(f"[bench] sdpa C3: {sdpa['ms']} ms, {sdpa['kv_gbs']} GB/s, {sdpa['kv_tokens_per_s']:.3e} tok/s")
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline({k: v.cpu().numpy() for k, v in stack[0].items()}, B)
+        log(f"[bench] cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads")
+
+    achieved = (step_bytes / launches) / (ms / launches) / 1e6
+    res = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": f"C2 Qwen3-8B Q4_K_M linear stack: {args.layers} layers x "
+                               "(q|k|v, o, gate|up, down), distinct weights per layer",
+                   "batch": B, "layers": args.layers, "hidden": HIDDEN, "intermediate": INTER,
+                   "weights_per_step_bytes": args.layers * sum(wire_bytes(N, K, c) for _, N, K, c in LAYER),
+                   "launches_per_step": launches, "graph_replay_equals_eager": replay_ok},
+        "roofline": {"bound": "hbm", "kernel": "kq_dense_grouped_kernel",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "per_batch": per_batch,
+        "sdpa": sdpa,
+    }
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -5,16 +5,24 @@
 // 210-226): per (row b, q head hq) softmax(scale * q . K^T) . V over the row's
 // visible keys, kv head h = hq / (Hq/Hkv), fp32 online softmax.
 //
-// Work unit = one wave = (row b, kv head h, split s of C tokens): the wave
-// streams its K/V tokens once for all G = Hq/Hkv query heads of the group
-// (GQA sharing), 32 tokens per tile, both products on v_mfma_f32_16x16x32:
-//   S^T[tok, head]  = K_tile[tok, d] . q^T[d, head]      (A = K rows as loaded)
-//   O^T[d, head]   += V^T[d, tok]  . P^T[tok, head]      (A = V^T via v_perm)
-// Lane l = 16*g + r: in the score tile it holds head r at tokens
-// {4g..4g+3, 16+4g..16+4g+3}; the P.V B-operand wants exactly those tokens
-// in the same lane, so P never leaves its lane.  Splits of one (b, h) are
-// merged by the last split to finish (agent-scope counter), in split order,
-// so the result does not depend on scheduling.
+// Two launches (flash-decoding):
+//  1. split pass: work unit = one wave = (row b, kv head h, split s of C
+//     tokens).  The wave streams its K/V tokens once for all G = Hq/Hkv query
+//     heads of the group (GQA sharing), 32 tokens per tile, both products on
+//     v_mfma_f32_16x16x32:
+//       S^T[tok, head] = K_tile[tok, d] . q^T[d, head]   (A = K rows as loaded)
+//       O^T[d, head]  += V^T[d, tok] . P^T[tok, head]    (A = V^T via v_perm)
+//     Lane l = 16*g + r: in the score tile it holds head r at tokens
+//     {4g..4g+3, 16+4g..16+4g+3}; the P.V B-operand wants exactly those
+//     tokens in the same lane, so P never leaves its lane.  K/V tiles are
+//     double-buffered in registers: the next tile's loads are in flight
+//     while the current one is multiplied.  A row with one split writes its
+//     output directly; otherwise the split stores (O unnormalised, m, l).
+//  2. merge pass: one workgroup per (row, q head) with nsplit > 1 rescales
+//     the splits to the common max and sums them in split order (the
+//     two-pass merge of gmlx/qwen35_attn.py:255-282), so the result does not
+//     depend on scheduling.
+// No cross-workgroup synchronisation happens inside a launch.
 #include "kq_common.h"
 
 namespace {
@@ -24,9 +32,8 @@ struct SdpaArgs {
     uint16_t *out;
     const int64_t *kv_off, *head_stride;
     const int32_t *row_len;
-    float *part;          // [B][Hkv][max_splits][G][D] O partials, then m/l
-    float *ml;            // [B][Hkv][max_splits][G][2]
-    uint32_t *ctr;        // [B][Hkv]
+    float *part;          // [B][Hkv][max_splits][G][D] O partials
+    float *ml;            // [B][Hkv][max_splits][G][2] (m, l)
     int32_t B, Hq, Hkv, G, split, max_splits, max_len;
     float scale_log2;     // scale * log2(e)
 };
@@ -53,32 +60,26 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
 }
 
 template <bool BF>
-__device__ __forceinline__ float to_f32(uint16_t h) {
-    if constexpr (!BF) return (float)__builtin_bit_cast(_Float16, h);
-    else return kq_bf16_bits_to_f32(h);
-}
-
-template <bool BF>
 __device__ __forceinline__ uint16_t from_f32(float f) {
     if constexpr (!BF) return __builtin_bit_cast(uint16_t, (_Float16)f);
     else return kq_f32_to_bf16_bits(f);
 }
 
-// Map unit u to (b, h, s).  Each row contributes max(1, ceil(len/C)) splits
-// per kv head.  Returns false when u is past the last unit.
+__device__ __forceinline__ int row_splits(int len, int split) {
+    return len <= 0 ? 1 : (len + split - 1) / split;
+}
+
+// Map unit u to (b, h, s).  Each row contributes row_splits(len) splits per
+// kv head.  Returns false when u is past the last unit.
 __device__ __forceinline__ bool map_unit(const SdpaArgs &a, int u, int &b, int &h, int &s, int &nsplit) {
     const int lane = kq_lane();
     int base = 0;
     for (int c0 = 0; c0 < a.B; c0 += 64) {
         const int row = c0 + lane;
         int n = 0;
-        if (row < a.B) {
-            const int len = min(a.row_len[row], a.max_len);
-            n = len <= 0 ? 1 : (len + a.split - 1) / a.split;
-        }
+        if (row < a.B) n = row_splits(min(a.row_len[row], a.max_len), a.split);
         const int units = n * a.Hkv;
-        // inclusive scan across the wave
-        int inc = units;
+        int inc = units;  // inclusive scan across the wave
         for (int off = 1; off < 64; off <<= 1) {
             const int t = __shfl_up(inc, off);
             if (lane >= off) inc += t;
@@ -100,10 +101,112 @@ __device__ __forceinline__ bool map_unit(const SdpaArgs &a, int u, int &b, int &
     return false;
 }
 
+// One 32-token K/V tile in registers.
+template <int D>
+struct KVTile {
+    static constexpr int NC = D / 32;            // 32-wide d chunks for Q.K
+    static constexpr int NG = (D + 127) / 128;   // 128-wide d groups for P.V
+    u32x4 k[2][NC];   // token t0 + 16*ch + r, d = 32c + 8g .. +7
+    u32x4 v[NG][8];   // token t0 + {4g+i | 16+4g+i-4}, d = 128dg + 8r .. +7
+
+    // Tokens past t_end are read from the row's last token (a valid address);
+    // their scores are masked to -inf, so they contribute p = 0.
+    __device__ __forceinline__ void load(const uint16_t *kp, const uint16_t *vp, int t0, int t_end) {
+        const int lane = kq_lane();
+        const int r = lane & 15, g = lane >> 4;
+#pragma unroll
+        for (int ch = 0; ch < 2; ++ch) {
+            const int tok = min(t0 + 16 * ch + r, t_end - 1);
+#pragma unroll
+            for (int c = 0; c < NC; ++c) k[ch][c] = *(const u32x4 *)(kp + (int64_t)tok * D + 32 * c + 8 * g);
+        }
+#pragma unroll
+        for (int dg = 0; dg < NG; ++dg) {
+            const int d0 = min(128 * dg + 8 * r, D - 8);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int tok = min(t0 + (i < 4 ? 4 * g + i : 16 + 4 * g + (i - 4)), t_end - 1);
+                v[dg][i] = *(const u32x4 *)(vp + (int64_t)tok * D + d0);
+            }
+        }
+    }
+};
+
 template <int D, bool BF>
-__global__ __launch_bounds__(64) void kq_sdpa_kernel(SdpaArgs a) {
-    constexpr int NC = D / 32;               // 32-wide d chunks for Q.K
-    constexpr int NG = (D + 127) / 128;      // 128-wide d groups for P.V
+struct SplitState {
+    static constexpr int NC = D / 32;
+    static constexpr int NG = (D + 127) / 128;
+    half8_t qf[NC];
+    floatx4 o[NG][8];
+    float m_run;   // running max (log2 domain), same on the 4 lanes of a head
+    float l_part;  // this lane's share of the running sum
+
+    __device__ __forceinline__ void tile(const KVTile<D> &kv, int t0, int t_end, bool head_ok, float scale_log2) {
+        const int lane = kq_lane();
+        const int g = lane >> 4;
+        // ---- S = K . q^T for tokens t0 + [0, 32)
+        floatx4 sc[2];
+#pragma unroll
+        for (int ch = 0; ch < 2; ++ch) {
+            floatx4 acc = {0, 0, 0, 0};
+#pragma unroll
+            for (int c = 0; c < NC; ++c) acc = mfma<BF>(__builtin_bit_cast(half8_t, kv.k[ch][c]), qf[c], acc);
+            sc[ch] = acc;
+        }
+        // ---- online softmax over this lane's 8 scores (head r)
+        float sv[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int ta = t0 + 4 * g + e, tb = t0 + 16 + 4 * g + e;
+            sv[e] = (ta < t_end && head_ok) ? sc[0][e] * scale_log2 : -INFINITY;
+            sv[4 + e] = (tb < t_end && head_ok) ? sc[1][e] * scale_log2 : -INFINITY;
+        }
+        float tmax = sv[0];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) tmax = fmaxf(tmax, sv[i]);
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        const float m_new = fmaxf(m_run, tmax);
+        // m_new == -inf only for heads >= G
+        const float alpha = (m_new == -INFINITY) ? 1.f : exp2f(m_run - m_new);
+        float p[8];
+        float psum = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            p[i] = (m_new == -INFINITY) ? 0.f : exp2f(sv[i] - m_new);
+            psum += p[i];
+        }
+        l_part = l_part * alpha + psum;
+        m_run = m_new;
+        const half8_t pf = __builtin_bit_cast(
+            half8_t, u32x4{pack2<BF>(p[0], p[1]), pack2<BF>(p[2], p[3]), pack2<BF>(p[4], p[5]),
+                           pack2<BF>(p[6], p[7])});
+        // ---- O^T += V^T . P^T
+#pragma unroll
+        for (int dg = 0; dg < NG; ++dg) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+                u32x4 f;
+                f.x = __builtin_amdgcn_perm(kv.v[dg][1][j >> 1], kv.v[dg][0][j >> 1], sel);
+                f.y = __builtin_amdgcn_perm(kv.v[dg][3][j >> 1], kv.v[dg][2][j >> 1], sel);
+                f.z = __builtin_amdgcn_perm(kv.v[dg][5][j >> 1], kv.v[dg][4][j >> 1], sel);
+                f.w = __builtin_amdgcn_perm(kv.v[dg][7][j >> 1], kv.v[dg][6][j >> 1], sel);
+                const floatx4 acc = o[dg][j] * alpha;
+                o[dg][j] = mfma<BF>(__builtin_bit_cast(half8_t, f), pf, acc);
+            }
+        }
+        // o is read by VALU at the next tile (rescale) or after the loop
+        kq_mfma_drain();
+    }
+};
+
+template <int D, bool BF>
+__global__ __launch_bounds__(64) void kq_sdpa_split_kernel(SdpaArgs a) {
+    constexpr int NC = D / 32;
+    constexpr int NG = (D + 127) / 128;
+    // D = 256 tiles are 128 VGPRs: one buffer only
+    constexpr bool kDouble = D <= 128;
     const int lane = kq_lane();
     const int r = lane & 15, g = lane >> 4;
 
@@ -119,202 +222,116 @@ __global__ __launch_bounds__(64) void kq_sdpa_kernel(SdpaArgs a) {
         const uint16_t *kp = a.k + kvbase;
         const uint16_t *vp = a.v + kvbase;
         const bool head_ok = r < a.G;
-        const int hq = h * a.G + r;
+        const int hq = h * a.G + (head_ok ? r : 0);
 
+        SplitState<D, BF> st;
         // q^T fragments: lane (head r, group g) holds q[hq][32c + 8g .. +7]
-        half8_t qf[NC];
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            if (head_ok) {
-                qf[c] = __builtin_bit_cast(half8_t, *(const u32x4 *)(a.q + ((int64_t)b * a.Hq + hq) * D + 32 * c + 8 * g));
-            } else {
-                qf[c] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
-            }
+        for (int c = 0; c < NC; ++c)
+            st.qf[c] = __builtin_bit_cast(half8_t, *(const u32x4 *)(a.q + ((int64_t)b * a.Hq + hq) * D + 32 * c + 8 * g));
+        if (!head_ok) {
+#pragma unroll
+            for (int c = 0; c < NC; ++c) st.qf[c] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
         }
-
-        floatx4 o[NG][8];
 #pragma unroll
         for (int dg = 0; dg < NG; ++dg)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) o[dg][j] = floatx4{0, 0, 0, 0};
-        float m_run = -INFINITY;   // running max (log2 domain), same on the 4 lanes of a head
-        float l_part = 0.f;        // this lane's share of the running sum
+            for (int j = 0; j < 8; ++j) st.o[dg][j] = floatx4{0, 0, 0, 0};
+        st.m_run = -INFINITY;
+        st.l_part = 0.f;
 
-        for (int t0 = t_begin; t0 < t_end; t0 += 32) {
-            // ---- S = K . q^T for tokens t0 + [0, 32)
-            floatx4 sc[2];
-#pragma unroll
-            for (int ch = 0; ch < 2; ++ch) {
-                const int tok = t0 + 16 * ch + r;
-                const bool tv = tok < t_end;
-                floatx4 acc = {0, 0, 0, 0};
-#pragma unroll
-                for (int c = 0; c < NC; ++c) {
-                    half8_t kf = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
-                    if (tv) kf = __builtin_bit_cast(half8_t, *(const u32x4 *)(kp + (int64_t)tok * D + 32 * c + 8 * g));
-                    acc = mfma<BF>(kf, qf[c], acc);
+        if (t_end > t_begin) {  // wave-uniform
+            if constexpr (kDouble) {
+                KVTile<D> ta, tb;
+                ta.load(kp, vp, t_begin, t_end);
+                for (int t0 = t_begin; t0 < t_end; t0 += 64) {
+                    const bool more = t0 + 32 < t_end;
+                    if (more) tb.load(kp, vp, t0 + 32, t_end);
+                    __builtin_amdgcn_sched_barrier(0);
+                    st.tile(ta, t0, t_end, head_ok, a.scale_log2);
+                    if (!more) break;
+                    if (t0 + 64 < t_end) ta.load(kp, vp, t0 + 64, t_end);
+                    __builtin_amdgcn_sched_barrier(0);
+                    st.tile(tb, t0 + 32, t_end, head_ok, a.scale_log2);
                 }
-                sc[ch] = acc;
-            }
-            // ---- V rows for this lane's 8 tokens, d = 128*dg + 8*r .. +7
-            u32x4 vr[NG][8];
-#pragma unroll
-            for (int dg = 0; dg < NG; ++dg) {
-                const int d0 = 128 * dg + 8 * r;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const int tok = t0 + (i < 4 ? 4 * g + i : 16 + 4 * g + (i - 4));
-                    if (tok < t_end && d0 < D) vr[dg][i] = *(const u32x4 *)(vp + (int64_t)tok * D + d0);
-                    else vr[dg][i] = u32x4{0, 0, 0, 0};
-                }
-            }
-            // ---- online softmax over this lane's 8 scores (head r)
-            float sv[8];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int ta = t0 + 4 * g + e, tb = t0 + 16 + 4 * g + e;
-                sv[e] = (ta < t_end && head_ok) ? sc[0][e] * a.scale_log2 : -INFINITY;
-                sv[4 + e] = (tb < t_end && head_ok) ? sc[1][e] * a.scale_log2 : -INFINITY;
-            }
-            float tmax = sv[0];
-#pragma unroll
-            for (int i = 1; i < 8; ++i) tmax = fmaxf(tmax, sv[i]);
-            tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-            tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-            const float m_new = fmaxf(m_run, tmax);
-            // m_new == -inf only for heads >= G or fully masked tiles
-            const float alpha = (m_new == -INFINITY) ? 1.f : exp2f(m_run - m_new);
-            float p[8];
-            float psum = 0.f;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                p[i] = (m_new == -INFINITY) ? 0.f : exp2f(sv[i] - m_new);
-                psum += p[i];
-            }
-            l_part = l_part * alpha + psum;
-            m_run = m_new;
-            const half8_t pf = __builtin_bit_cast(
-                half8_t, u32x4{pack2<BF>(p[0], p[1]), pack2<BF>(p[2], p[3]), pack2<BF>(p[4], p[5]),
-                               pack2<BF>(p[6], p[7])});
-            // ---- O^T += V^T . P^T
-#pragma unroll
-            for (int dg = 0; dg < NG; ++dg) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-                    u32x4 f;
-                    f.x = __builtin_amdgcn_perm(vr[dg][1][j >> 1], vr[dg][0][j >> 1], sel);
-                    f.y = __builtin_amdgcn_perm(vr[dg][3][j >> 1], vr[dg][2][j >> 1], sel);
-                    f.z = __builtin_amdgcn_perm(vr[dg][5][j >> 1], vr[dg][4][j >> 1], sel);
-                    f.w = __builtin_amdgcn_perm(vr[dg][7][j >> 1], vr[dg][6][j >> 1], sel);
-                    floatx4 acc = o[dg][j] * alpha;
-                    o[dg][j] = mfma<BF>(__builtin_bit_cast(half8_t, f), pf, acc);
+            } else {
+                KVTile<D> ta;
+                for (int t0 = t_begin; t0 < t_end; t0 += 32) {
+                    ta.load(kp, vp, t0, t_end);
+                    st.tile(ta, t0, t_end, head_ok, a.scale_log2);
                 }
             }
         }
 
         // Lane (head r, g) now holds O[hq][d] for d = 128*dg + 32*g + 8*e + j
         // (element e of o[dg][j]); l is split over the 4 lanes of a head.
-        float l_tot = l_part + __shfl_xor(l_part, 16);
+        float l_tot = st.l_part + __shfl_xor(st.l_part, 16);
         l_tot += __shfl_xor(l_tot, 32);
+        if (!head_ok) continue;
 
         if (nsplit == 1) {
-            if (head_ok) {
-                const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-                uint16_t *op = a.out + ((int64_t)b * a.Hq + hq) * D;
-#pragma unroll
-                for (int dg = 0; dg < NG; ++dg)
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int d0 = 128 * dg + 32 * g + 8 * e;
-                        if (d0 >= D) continue;
-                        u32x4 w;
-                        w.x = (uint32_t)from_f32<BF>(o[dg][0][e] * inv) | ((uint32_t)from_f32<BF>(o[dg][1][e] * inv) << 16);
-                        w.y = (uint32_t)from_f32<BF>(o[dg][2][e] * inv) | ((uint32_t)from_f32<BF>(o[dg][3][e] * inv) << 16);
-                        w.z = (uint32_t)from_f32<BF>(o[dg][4][e] * inv) | ((uint32_t)from_f32<BF>(o[dg][5][e] * inv) << 16);
-                        w.w = (uint32_t)from_f32<BF>(o[dg][6][e] * inv) | ((uint32_t)from_f32<BF>(o[dg][7][e] * inv) << 16);
-                        *(u32x4 *)(op + d0) = w;
-                    }
-            }
-            continue;
-        }
-
-        // ---- split partial: O (unnormalised), m, l
-        const int64_t slot = ((int64_t)b * a.Hkv + h) * a.max_splits;
-        if (head_ok) {
-            float *po = a.part + ((slot + s) * a.G + r) * D;
+            const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+            uint16_t *op = a.out + ((int64_t)b * a.Hq + hq) * D;
 #pragma unroll
             for (int dg = 0; dg < NG; ++dg)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int d0 = 128 * dg + 32 * g + 8 * e;
                     if (d0 >= D) continue;
-                    float4 *dst = (float4 *)(po + d0);
-                    dst[0] = make_float4(o[dg][0][e], o[dg][1][e], o[dg][2][e], o[dg][3][e]);
-                    dst[1] = make_float4(o[dg][4][e], o[dg][5][e], o[dg][6][e], o[dg][7][e]);
-                }
-            if (g == 0) {
-                float *pml = a.ml + ((slot + s) * a.G + r) * 2;
-                pml[0] = m_run;
-                pml[1] = l_tot;
-            }
-        }
-        __threadfence();
-        uint32_t old = 0;
-        uint32_t *ctr = a.ctr + (int64_t)b * a.Hkv + h;
-        if (lane == 0) old = atomicAdd(ctr, 1u);
-        old = __shfl(old, 0);
-        if (old != (uint32_t)(nsplit - 1)) continue;
-        __threadfence();
-        // ---- last split: merge all splits of (b, h) in split order
-        if (head_ok) {
-            float M = -INFINITY;
-            for (int si = 0; si < nsplit; ++si)
-                M = fmaxf(M, __hip_atomic_load(a.ml + ((slot + si) * a.G + r) * 2, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT));
-            // lane handles d = 32*g' + [0, 32) within each 128 group, g' = g
-            float acc[NG][32];
-            float L = 0.f;
-#pragma unroll
-            for (int dg = 0; dg < NG; ++dg)
-#pragma unroll
-                for (int i = 0; i < 32; ++i) acc[dg][i] = 0.f;
-            for (int si = 0; si < nsplit; ++si) {
-                const float ms = __hip_atomic_load(a.ml + ((slot + si) * a.G + r) * 2, __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_AGENT);
-                const float ls = __hip_atomic_load(a.ml + ((slot + si) * a.G + r) * 2 + 1, __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_AGENT);
-                const float f = (ms == -INFINITY) ? 0.f : exp2f(ms - M);
-                L += ls * f;
-                const float *po = a.part + ((slot + si) * a.G + r) * D;
-#pragma unroll
-                for (int dg = 0; dg < NG; ++dg) {
-                    const int d0 = 128 * dg + 32 * g;
-                    if (d0 >= D) continue;
-#pragma unroll
-                    for (int i = 0; i < 32; ++i)
-                        acc[dg][i] += f * __hip_atomic_load(po + d0 + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
-            }
-            const float inv = L > 0.f ? 1.f / L : 0.f;
-            uint16_t *op = a.out + ((int64_t)b * a.Hq + hq) * D;
-#pragma unroll
-            for (int dg = 0; dg < NG; ++dg) {
-                const int d0 = 128 * dg + 32 * g;
-                if (d0 >= D) continue;
-#pragma unroll
-                for (int i = 0; i < 32; i += 8) {
                     u32x4 w;
-                    w.x = (uint32_t)from_f32<BF>(acc[dg][i] * inv) | ((uint32_t)from_f32<BF>(acc[dg][i + 1] * inv) << 16);
-                    w.y = (uint32_t)from_f32<BF>(acc[dg][i + 2] * inv) | ((uint32_t)from_f32<BF>(acc[dg][i + 3] * inv) << 16);
-                    w.z = (uint32_t)from_f32<BF>(acc[dg][i + 4] * inv) | ((uint32_t)from_f32<BF>(acc[dg][i + 5] * inv) << 16);
-                    w.w = (uint32_t)from_f32<BF>(acc[dg][i + 6] * inv) | ((uint32_t)from_f32<BF>(acc[dg][i + 7] * inv) << 16);
-                    *(u32x4 *)(op + d0 + i) = w;
+                    w.x = (uint32_t)from_f32<BF>(st.o[dg][0][e] * inv) | ((uint32_t)from_f32<BF>(st.o[dg][1][e] * inv) << 16);
+                    w.y = (uint32_t)from_f32<BF>(st.o[dg][2][e] * inv) | ((uint32_t)from_f32<BF>(st.o[dg][3][e] * inv) << 16);
+                    w.z = (uint32_t)from_f32<BF>(st.o[dg][4][e] * inv) | ((uint32_t)from_f32<BF>(st.o[dg][5][e] * inv) << 16);
+                    w.w = (uint32_t)from_f32<BF>(st.o[dg][6][e] * inv) | ((uint32_t)from_f32<BF>(st.o[dg][7][e] * inv) << 16);
+                    *(u32x4 *)(op + d0) = w;
                 }
-            }
+            continue;
         }
-        if (lane == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+        // ---- split partial: O (unnormalised), m, l
+        const int64_t slot = ((int64_t)b * a.Hkv + h) * a.max_splits + s;
+        float *po = a.part + (slot * a.G + r) * D;
+#pragma unroll
+        for (int dg = 0; dg < NG; ++dg)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int d0 = 128 * dg + 32 * g + 8 * e;
+                if (d0 >= D) continue;
+                float4 *dst = (float4 *)(po + d0);
+                dst[0] = make_float4(st.o[dg][0][e], st.o[dg][1][e], st.o[dg][2][e], st.o[dg][3][e]);
+                dst[1] = make_float4(st.o[dg][4][e], st.o[dg][5][e], st.o[dg][6][e], st.o[dg][7][e]);
+            }
+        if (g == 0) {
+            float *pml = a.ml + (slot * a.G + r) * 2;
+            pml[0] = st.m_run;
+            pml[1] = l_tot;
+        }
     }
+}
+
+// One workgroup of D threads per (row b, q head hq); rows with a single split
+// were finished by the split pass.
+template <int D, bool BF>
+__global__ __launch_bounds__(256) void kq_sdpa_merge_kernel(SdpaArgs a) {
+    const int b = blockIdx.x / a.Hq;
+    const int hq = blockIdx.x - b * a.Hq;
+    const int len = max(min(a.row_len[b], a.max_len), 0);
+    const int nsplit = row_splits(len, a.split);
+    if (nsplit == 1) return;
+    const int h = hq / a.G, r = hq - h * a.G;
+    const int d = threadIdx.x;
+    const int64_t slot0 = ((int64_t)b * a.Hkv + h) * a.max_splits;
+    float M = -INFINITY;
+    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, a.ml[((slot0 + s) * a.G + r) * 2]);
+    float acc = 0.f, L = 0.f;
+    for (int s = 0; s < nsplit; ++s) {
+        const float *pml = a.ml + ((slot0 + s) * a.G + r) * 2;
+        const float f = (pml[0] == -INFINITY) ? 0.f : exp2f(pml[0] - M);
+        L += pml[1] * f;
+        acc += f * a.part[((slot0 + s) * a.G + r) * D + d];
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    a.out[((int64_t)b * a.Hq + hq) * D + d] = from_f32<BF>(acc * inv);
 }
 
 int env_int(const char *name, int dflt) {
@@ -325,6 +342,7 @@ int env_int(const char *name, int dflt) {
     return (end && *end == 0 && v > 0 && v < (1 << 24)) ? (int)v : dflt;
 }
 
+// Tokens per split (a multiple of the 32-token tile).
 int split_tokens() {
     int c = env_int("GMLX_KQ_SDPA_SPLIT", 512);
     c = (c + 31) / 32 * 32;
@@ -332,7 +350,7 @@ int split_tokens() {
 }
 
 struct WsLayout {
-    size_t ctr_bytes, part_bytes, ml_bytes;
+    size_t part_bytes, ml_bytes;
 };
 
 WsLayout ws_layout(int B, int Hq, int Hkv, int D, int max_len) {
@@ -340,15 +358,15 @@ WsLayout ws_layout(int B, int Hq, int Hkv, int D, int max_len) {
     const int C = split_tokens();
     const int64_t ms = max_len <= 0 ? 1 : (max_len + C - 1) / C;
     WsLayout w;
-    w.ctr_bytes = (((size_t)B * Hkv * 4) + 255) & ~(size_t)255;
     w.part_bytes = (((size_t)B * Hkv * ms * G * D * 4) + 255) & ~(size_t)255;
     w.ml_bytes = (size_t)B * Hkv * ms * G * 2 * 4;
     return w;
 }
 
 template <int D, bool BF>
-void launch(const SdpaArgs &a, int grid, hipStream_t s) {
-    hipLaunchKernelGGL((kq_sdpa_kernel<D, BF>), dim3(grid), dim3(64), 0, s, a);
+void launch(const SdpaArgs &a, int grid, bool merge, hipStream_t s) {
+    hipLaunchKernelGGL((kq_sdpa_split_kernel<D, BF>), dim3(grid), dim3(64), 0, s, a);
+    if (merge) hipLaunchKernelGGL((kq_sdpa_merge_kernel<D, BF>), dim3(a.B * a.Hq), dim3(D), 0, s, a);
 }
 
 }  // namespace
@@ -358,7 +376,7 @@ extern "C" {
 size_t kq_sdpa_workspace_bytes(int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t max_len) {
     if (B <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv || D <= 0) return 0;
     const WsLayout w = ws_layout(B, Hq, Hkv, D, max_len);
-    return w.ctr_bytes + w.part_bytes + w.ml_bytes;
+    return w.part_bytes + w.ml_bytes;
 }
 
 int kq_sdpa_decode_ragged(const void *q, const void *k, const void *v, const int64_t *kv_off,
@@ -369,6 +387,7 @@ int kq_sdpa_decode_ragged(const void *q, const void *k, const void *v, const int
     if (!q || !k || !v || !kv_off || !head_stride || !row_len || !out) return KQ_ERR_NULL_POINTER;
     if (B < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || Hq / Hkv > 16 || max_len < 0) return KQ_ERR_BAD_SHAPE;
     if (D != 64 && D != 96 && D != 128 && D != 256) return KQ_ERR_BAD_SHAPE;
+    if ((int64_t)B * Hq > (1 << 30)) return KQ_ERR_BAD_SHAPE;
     if (dtype != KQ_DTYPE_F16 && dtype != KQ_DTYPE_BF16) return KQ_ERR_UNSUPPORTED_DTYPE;
     if (((uintptr_t)q & 15) || ((uintptr_t)k & 15) || ((uintptr_t)v & 15) || ((uintptr_t)out & 15))
         return KQ_ERR_BAD_ALIGN;
@@ -383,9 +402,8 @@ int kq_sdpa_decode_ragged(const void *q, const void *k, const void *v, const int
     a.kv_off = kv_off;
     a.head_stride = head_stride;
     a.row_len = row_len;
-    a.ctr = (uint32_t *)workspace;
-    a.part = (float *)((char *)workspace + w.ctr_bytes);
-    a.ml = (float *)((char *)workspace + w.ctr_bytes + w.part_bytes);
+    a.part = (float *)workspace;
+    a.ml = (float *)((char *)workspace + w.part_bytes);
     a.B = B;
     a.Hq = Hq;
     a.Hkv = Hkv;
@@ -394,16 +412,18 @@ int kq_sdpa_decode_ragged(const void *q, const void *k, const void *v, const int
     a.max_splits = max_len <= 0 ? 1 : (max_len + a.split - 1) / a.split;
     a.max_len = max_len;
     a.scale_log2 = scale * 1.4426950408889634f;
+    // one wave per unit; the unit count is bounded by B * Hkv * max_splits
+    // (rows are shorter on the device side), extra waves exit at once
     const int64_t upper = (int64_t)B * Hkv * a.max_splits;
-    const int64_t cap = env_int("GMLX_KQ_SDPA_GRID", 256 * 12);
-    const int grid = (int)(upper < cap ? upper : cap);
+    const int grid = (int)(upper < (1 << 22) ? upper : (1 << 22));
+    const bool merge = a.max_splits > 1;
     hipStream_t s = (hipStream_t)stream;
     const bool bf = dtype == KQ_DTYPE_BF16;
     switch (D) {
-    case 64: bf ? launch<64, true>(a, grid, s) : launch<64, false>(a, grid, s); break;
-    case 96: bf ? launch<96, true>(a, grid, s) : launch<96, false>(a, grid, s); break;
-    case 128: bf ? launch<128, true>(a, grid, s) : launch<128, false>(a, grid, s); break;
-    default: bf ? launch<256, true>(a, grid, s) : launch<256, false>(a, grid, s); break;
+    case 64: bf ? launch<64, true>(a, grid, merge, s) : launch<64, false>(a, grid, merge, s); break;
+    case 96: bf ? launch<96, true>(a, grid, merge, s) : launch<96, false>(a, grid, merge, s); break;
+    case 128: bf ? launch<128, true>(a, grid, merge, s) : launch<128, false>(a, grid, merge, s); break;
+    default: bf ? launch<256, true>(a, grid, merge, s) : launch<256, false>(a, grid, merge, s); break;
     }
     return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
 }

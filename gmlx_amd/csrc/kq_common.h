@@ -69,3 +69,15 @@ __device__ __forceinline__ uint32_t kq_h2_bits(half2_t h) { return __builtin_bit
 
 // Wave-level helpers (wave64).
 __device__ __forceinline__ int kq_lane() { return (int)__lane_id(); }
+
+// Ordering point between the MFMAs of an accumulation loop body and any VALU
+// / accvgpr read of their accumulators after the loop's back edge: 24
+// explicit wait states, more than any 16x16x32 MFMA result latency.  Placed at
+// the end of the loop body.  Where the read followed the back edge directly,
+// the compiler has been seen to leave one wait state, and the read returned
+// the accumulator without the final MFMA's contribution.
+__device__ __forceinline__ void kq_mfma_drain() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}

@@ -2,13 +2,13 @@
 // kq.quantized_matmul) and the MoE expert gather family (kq.gather_qmm,
 // kq.moe_glu_gather_kq, kq.gather_qmv_kq, mix, router top-k).
 //
-// Work decomposition (one wave = one work unit, 64-thread workgroups so even
-// a 1024-row matrix spreads over all 256 CUs):
-//   unit = (problem, 16-row weight tile, K split), grid.y = 64-row batch chunk.
-// A unit streams its weight rows once for the whole batch chunk; K splits of
-// one tile are reduced deterministically: every split writes its fp32 partial
-// to the workspace, and the last split to arrive (agent-scope counter) sums
-// the partials in split order and writes the output.
+// Dense work decomposition: one 256-thread workgroup per (problem, 16-row
+// weight tile, 64-row batch chunk).  The 4 waves of a workgroup split the
+// tile's K range (wave w takes 4-block steps w, w+4, ...), each wave keeps
+// its own MFMA accumulators, and the workgroup sums them through LDS in wave
+// order.  The reduction never leaves the workgroup, so there are no global
+// partials, counters or device-scope fences, and the result does not depend
+// on scheduling.
 #include <stdlib.h>
 
 #include "kq_mma.h"
@@ -19,24 +19,22 @@ using namespace kqmma;
 
 constexpr int kMaxChunk = 64;  // batch rows per grid.y chunk (4 m-tiles)
 
+constexpr int kWaves = 4;      // waves per dense workgroup (K split)
+
 struct DenseProblem {
     const uint8_t *w;
     const char *x;
     void *y;
     int64_t w_row_bytes, x_stride, y_stride;
     int32_t M, N, K, codec;
-    int32_t n_tiles, k_splits, steps_per_split;
-    int32_t unit_begin;   // first unit id of this problem
-    int64_t part_off;     // float offset of this problem's partials in the workspace
-    int64_t ctr_off;      // u32 offset of this problem's counters
+    int32_t n_tiles;
+    int32_t unit_begin;   // first workgroup id of this problem
 };
 
 struct DenseArgs {
     DenseProblem p[KQ_MAX_GROUP];
     int32_t n_problems;
     int32_t y_dtype;
-    float *parts;
-    uint32_t *ctrs;
 };
 
 __device__ __forceinline__ void store_tile(void *y, int y_dtype, int64_t y_stride, int m0, int M,
@@ -50,76 +48,32 @@ __device__ __forceinline__ void store_tile(void *y, int y_dtype, int64_t y_strid
     }
 }
 
-// Split-K reduction for one unit's MT m-tiles.  Returns true when this wave
-// holds the final sums in `acc` (single split, or last arrival).
-template <int MT>
-__device__ __forceinline__ bool splitk_reduce(floatx4 (&acc)[MT], int k_splits, int ks,
-                                              float *part, uint32_t *ctr) {
-    if (k_splits == 1) return true;
-    const int lane = kq_lane();
-    float *mine = part + (int64_t)ks * (MT * 256);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) mine[(mt * 4 + e) * 64 + lane] = acc[mt][e];
-    __threadfence();
-    uint32_t old = 0;
-    if (lane == 0) old = atomicAdd(ctr, 1u);
-    old = __shfl(old, 0);
-    if (old != (uint32_t)(k_splits - 1)) return false;
-    __threadfence();
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[mt] = floatx4{0, 0, 0, 0};
-    for (int s = 0; s < k_splits; ++s) {
-        const float *src = part + (int64_t)s * (MT * 256);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                acc[mt][e] += __hip_atomic_load(src + (mt * 4 + e) * 64 + lane, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT);
-    }
-    if (lane == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return true;
-}
-
 template <int CODEC, int MT, int XT>
-__device__ __forceinline__ void dense_unit(const DenseArgs &a, const DenseProblem &p, int local_unit) {
+__device__ __forceinline__ void dense_tile(const DenseProblem &p, int nt, int wave, floatx4 (&acc)[MT]) {
     const int lane = kq_lane();
     const int r = lane & 15;
-    const int nt = local_unit / p.k_splits;
-    const int ks = local_unit - nt * p.k_splits;
-    const int mc = blockIdx.y;
-    const int m0 = mc * kMaxChunk;
-    if (m0 >= p.M) return;
-    const int n = nt * 16 + r;
-    const bool n_valid = n < p.N;
+    const int m0 = blockIdx.y * kMaxChunk;
+    const int n = min(nt * 16 + r, p.N - 1);
     const int nb = p.K / KQ_QK;
-    const int kb0 = ks * p.steps_per_split * 4;
-    const int kb1 = min(nb, kb0 + p.steps_per_split * 4);
-    const uint8_t *wrow[1] = {p.w + (int64_t)(n_valid ? n : 0) * p.w_row_bytes};
+    const uint8_t *wrow[1] = {p.w + (int64_t)n * p.w_row_bytes};
     const char *xrow[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-        const int m = m0 + 16 * mt + r;
-        xrow[mt] = m < p.M ? p.x + (int64_t)m * p.x_stride * x_elem_bytes<XT>() : nullptr;
+        const int m = min(m0 + 16 * mt + r, p.M - 1);
+        xrow[mt] = p.x + (int64_t)m * p.x_stride * x_elem_bytes<XT>();
     }
-    floatx4 acc[1][MT];
+    floatx4 a1[1][MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[0][mt] = floatx4{0, 0, 0, 0};
-    tile_accumulate<CODEC, MT, XT, 1>(wrow, n_valid, kb0, kb1, xrow, acc);
-
-    const int64_t tile_id = (int64_t)mc * p.n_tiles + nt;
-    float *part = a.parts + p.part_off + tile_id * (int64_t)p.k_splits * (MT * 256);
-    uint32_t *ctr = a.ctrs + p.ctr_off + tile_id;
-    if (!splitk_reduce<MT>(acc[0], p.k_splits, ks, part, ctr)) return;
+    for (int mt = 0; mt < MT; ++mt) a1[0][mt] = floatx4{0, 0, 0, 0};
+    for (int kb = 4 * wave; kb < nb; kb += 4 * kWaves)
+        tile_accumulate<CODEC, MT, XT, 1>(wrow, kb, min(nb, kb + 4), xrow, a1);
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-        store_tile(p.y, a.y_dtype, p.y_stride, m0 + 16 * mt, p.M, n, n_valid, acc[0][mt]);
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = a1[0][mt];
 }
 
 template <int MT, int XT>
-__global__ __launch_bounds__(64) void kq_dense_grouped_kernel(DenseArgs a) {
+__global__ __launch_bounds__(64 * kWaves) void kq_dense_grouped_kernel(DenseArgs a) {
+    __shared__ floatx4 red[kWaves - 1][MT][64];
     const int unit = blockIdx.x;
     // Select the problem with static indices only: dynamic indexing of the
     // by-value argument array would copy it to scratch memory.
@@ -127,12 +81,31 @@ __global__ __launch_bounds__(64) void kq_dense_grouped_kernel(DenseArgs a) {
 #pragma unroll
     for (int i = 1; i < KQ_MAX_GROUP; ++i)
         if (i < a.n_problems && unit >= a.p[i].unit_begin) p = a.p[i];
-    const int local = unit - p.unit_begin;
+    const int nt = unit - p.unit_begin;
+    const int wave = threadIdx.x >> 6;
+    const int lane = kq_lane();
+    const int m0 = blockIdx.y * kMaxChunk;
+    if (m0 >= p.M) return;  // uniform over the workgroup
+    floatx4 acc[MT];
     switch (p.codec) {
-    case KQ_CODEC_Q4_K: dense_unit<KQ_CODEC_Q4_K, MT, XT>(a, p, local); break;
-    case KQ_CODEC_Q6_K: dense_unit<KQ_CODEC_Q6_K, MT, XT>(a, p, local); break;
-    default: dense_unit<KQ_CODEC_IQ2_XXS, MT, XT>(a, p, local); break;
+    case KQ_CODEC_Q4_K: dense_tile<KQ_CODEC_Q4_K, MT, XT>(p, nt, wave, acc); break;
+    case KQ_CODEC_Q6_K: dense_tile<KQ_CODEC_Q6_K, MT, XT>(p, nt, wave, acc); break;
+    default: dense_tile<KQ_CODEC_IQ2_XXS, MT, XT>(p, nt, wave, acc); break;
     }
+    if (wave > 0) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) red[wave - 1][mt][lane] = acc[mt];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int w = 0; w < kWaves - 1; ++w)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt] += red[w][mt][lane];
+    const int n = nt * 16 + (lane & 15);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+        store_tile(p.y, a.y_dtype, p.y_stride, m0 + 16 * mt, p.M, n, n < p.N, acc[mt]);
 }
 
 // ---------------------------------------------------------------- MoE
@@ -168,26 +141,25 @@ __global__ __launch_bounds__(64) void kq_gather_kernel(GatherArgs a) {
     const int seg_end = a.seg_info[1 + a.n_experts + slot + 1];
     const int n = nt * 16 + r;
     const bool n_valid = n < a.N;
+    const int nc = n_valid ? n : a.N - 1;
     const int nb = a.K / KQ_QK;
     const uint8_t *wrow[NW];
-    wrow[0] = a.w0 + (int64_t)expert * a.w_expert_bytes + (int64_t)(n_valid ? n : 0) * a.w_row_bytes;
+    wrow[0] = a.w0 + (int64_t)expert * a.w_expert_bytes + (int64_t)nc * a.w_row_bytes;
     if constexpr (NW == 2)
-        wrow[1] = a.w1 + (int64_t)expert * a.w_expert_bytes + (int64_t)(n_valid ? n : 0) * a.w_row_bytes;
+        wrow[1] = a.w1 + (int64_t)expert * a.w_expert_bytes + (int64_t)nc * a.w_row_bytes;
     for (int c0 = seg_begin; c0 < seg_end; c0 += 16 * MT) {
         const char *xrow[MT];
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-            const int ri = c0 + 16 * mt + r;
-            xrow[mt] = ri < seg_end
-                           ? a.x + (int64_t)(a.pair_order[ri] / a.x_pair_div) * a.x_stride * x_elem_bytes<XT>()
-                           : nullptr;
+            const int ri = min(c0 + 16 * mt + r, seg_end - 1);
+            xrow[mt] = a.x + (int64_t)(a.pair_order[ri] / a.x_pair_div) * a.x_stride * x_elem_bytes<XT>();
         }
         floatx4 acc[NW][MT];
 #pragma unroll
         for (int i = 0; i < NW; ++i)
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) acc[i][mt] = floatx4{0, 0, 0, 0};
-        tile_accumulate<CODEC, MT, XT, NW>(wrow, n_valid, 0, nb, xrow, acc);
+        tile_accumulate<CODEC, MT, XT, NW>(wrow, 0, nb, xrow, acc);
         if (!n_valid) continue;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
@@ -339,29 +311,14 @@ __global__ __launch_bounds__(64) void kq_router_kernel(const void *logits, int l
 
 // ---------------------------------------------------------------- host
 
-int env_int(const char *name, int dflt) {
-    const char *s = getenv(name);
-    if (!s || !*s) return dflt;
-    char *end = nullptr;
-    const long v = strtol(s, &end, 10);
-    return (end && *end == 0 && v > 0 && v < (1 << 24)) ? (int)v : dflt;
-}
 
 struct Plan {
-    int n_tiles, k_splits, steps_per_split, mt, chunks;
+    int n_tiles, mt, chunks;
 };
 
 Plan plan_problem(const kq_matmul_problem &q) {
     Plan pl;
     pl.n_tiles = (q.N + 15) / 16;
-    const int nb = q.K / KQ_QK;
-    const int steps = (nb + 3) / 4;
-    // Target enough waves per problem to keep every CU streaming.
-    const int target = env_int("GMLX_KQ_MM_WAVES", 1024);
-    int ks = (target + pl.n_tiles - 1) / pl.n_tiles;
-    ks = ks < 1 ? 1 : (ks > steps ? steps : ks);
-    pl.steps_per_split = (steps + ks - 1) / ks;
-    pl.k_splits = (steps + pl.steps_per_split - 1) / pl.steps_per_split;
     const int mrows = q.M < kMaxChunk ? q.M : kMaxChunk;
     pl.mt = (mrows + 15) / 16;
     pl.chunks = (q.M + kMaxChunk - 1) / kMaxChunk;
@@ -382,27 +339,21 @@ int validate_problem(const kq_matmul_problem &q) {
     return KQ_OK;
 }
 
-size_t workspace_for(const kq_matmul_problem *ps, int n, int64_t *part_off, int64_t *ctr_off,
-                     size_t *ctr_bytes_out) {
-    int64_t floats = 0, ctrs = 0;
+// m-tiles per wave of one grouped launch: the largest any live problem needs
+// (the kernel is instantiated once for the whole group).
+int group_mt(const kq_matmul_problem *ps, int n) {
+    int mt = 1;
     for (int i = 0; i < n; ++i) {
+        if (ps[i].M == 0 || ps[i].N == 0) continue;
         const Plan pl = plan_problem(ps[i]);
-        if (part_off) part_off[i] = floats;
-        if (ctr_off) ctr_off[i] = ctrs;
-        if (pl.k_splits > 1) {
-            floats += (int64_t)pl.chunks * pl.n_tiles * pl.k_splits * pl.mt * 256;
-            ctrs += (int64_t)pl.chunks * pl.n_tiles;
-        }
+        if (pl.mt > mt) mt = pl.mt;
     }
-    // counters first (zeroed region), then partials, 256-byte aligned
-    const size_t ctr_bytes = ((size_t)ctrs * 4 + 255) & ~(size_t)255;
-    if (ctr_bytes_out) *ctr_bytes_out = ctr_bytes;
-    return ctr_bytes + (size_t)floats * 4;
+    return mt <= 1 ? 1 : mt <= 2 ? 2 : 4;
 }
 
 template <int MT, int XT>
 void launch_dense(const DenseArgs &a, int units, int chunks, hipStream_t s) {
-    hipLaunchKernelGGL((kq_dense_grouped_kernel<MT, XT>), dim3(units, chunks), dim3(64), 0, s, a);
+    hipLaunchKernelGGL((kq_dense_grouped_kernel<MT, XT>), dim3(units, chunks), dim3(64 * kWaves), 0, s, a);
 }
 
 template <int CODEC, int XT, int NW>
@@ -487,32 +438,28 @@ int gather_common(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pa
 extern "C" {
 
 size_t kq_matmul_workspace_bytes(const kq_matmul_problem *problems, int n_problems) {
-    if (!problems || n_problems <= 0) return 0;
-    for (int i = 0; i < n_problems; ++i)
-        if (validate_problem(problems[i]) != KQ_OK) return 0;
-    return workspace_for(problems, n_problems, nullptr, nullptr, nullptr);
+    (void)problems;
+    (void)n_problems;
+    return 0;  // K splits are reduced inside a workgroup
 }
 
 int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problems, int x_dtype,
                                 int y_dtype, void *workspace, size_t workspace_bytes,
                                 kq_stream_t stream) {
+    (void)workspace;
+    (void)workspace_bytes;
     if (!problems) return KQ_ERR_NULL_POINTER;
     if (n_problems <= 0) return KQ_ERR_BAD_ARGUMENT;
     if (n_problems > KQ_MAX_GROUP) return KQ_ERR_TOO_MANY_PROBLEMS;
     if (x_dtype != KQ_DTYPE_F16 && x_dtype != KQ_DTYPE_BF16) return KQ_ERR_UNSUPPORTED_DTYPE;
     if (y_dtype != KQ_DTYPE_F32 && y_dtype != KQ_DTYPE_F16 && y_dtype != KQ_DTYPE_BF16)
         return KQ_ERR_UNSUPPORTED_DTYPE;
-    DenseArgs a;
-    int64_t part_off[KQ_MAX_GROUP], ctr_off[KQ_MAX_GROUP];
     for (int i = 0; i < n_problems; ++i) {
         const int rc = validate_problem(problems[i]);
         if (rc != KQ_OK) return rc;
     }
-    size_t ctr_bytes = 0;
-    const size_t need = workspace_for(problems, n_problems, part_off, ctr_off, &ctr_bytes);
-    if (need > 0 && (!workspace || workspace_bytes < need)) return KQ_ERR_WORKSPACE_TOO_SMALL;
-    int units = 0, max_mt = 1, max_chunks = 0;
-    int np = 0;
+    DenseArgs a;
+    int units = 0, max_chunks = 0, np = 0;
     for (int i = 0; i < n_problems; ++i) {
         const kq_matmul_problem &q = problems[i];
         if (q.M == 0 || q.N == 0) continue;
@@ -529,23 +476,17 @@ int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problem
         p.K = q.K;
         p.codec = q.codec;
         p.n_tiles = pl.n_tiles;
-        p.k_splits = pl.k_splits;
-        p.steps_per_split = pl.steps_per_split;
         p.unit_begin = units;
-        p.part_off = part_off[i];
-        p.ctr_off = ctr_off[i];
-        units += pl.n_tiles * pl.k_splits;
-        if (pl.mt > max_mt) max_mt = pl.mt;
+        units += pl.n_tiles;
         if (pl.chunks > max_chunks) max_chunks = pl.chunks;
     }
     if (np == 0) return KQ_OK;
+    if (max_chunks > 65535) return KQ_ERR_BAD_SHAPE;
     a.n_problems = np;
     a.y_dtype = y_dtype;
-    a.ctrs = (uint32_t *)workspace;
-    a.parts = (float *)((char *)workspace + ctr_bytes);
     hipStream_t s = (hipStream_t)stream;
     const bool bf = x_dtype == KQ_DTYPE_BF16;
-    const int mt = max_mt <= 1 ? 1 : max_mt <= 2 ? 2 : 4;
+    const int mt = group_mt(problems, n_problems);
     if (mt == 1) bf ? launch_dense<1, 1>(a, units, max_chunks, s) : launch_dense<1, 0>(a, units, max_chunks, s);
     else if (mt == 2) bf ? launch_dense<2, 1>(a, units, max_chunks, s) : launch_dense<2, 0>(a, units, max_chunks, s);
     else bf ? launch_dense<4, 1>(a, units, max_chunks, s) : launch_dense<4, 0>(a, units, max_chunks, s);

@@ -71,15 +71,16 @@ struct Block<KQ_CODEC_Q4_K> {
     u32x4 raw[9];
     half2_t dsc[8], ndm[8];
 
-    __device__ __forceinline__ void load(const uint8_t *blk, bool valid) {
+    __device__ __forceinline__ void load(const uint8_t *blk) {
         const u32x4 *p = (const u32x4 *)blk;
 #pragma unroll
-        for (int i = 0; i < 9; ++i) raw[i] = valid ? p[i] : u32x4{0, 0, 0, 0};
+        for (int i = 0; i < 9; ++i) raw[i] = p[i];
     }
-    __device__ __forceinline__ void prep() {
+    // valid == false zeroes every weight of the block (a padding block).
+    __device__ __forceinline__ void prep(bool valid) {
         const uint32_t h0 = raw[0].x;
-        const float d = kq_f16_bits_to_f32(h0 & 0xFFFF);
-        const float dmin = kq_f16_bits_to_f32(h0 >> 16);
+        const float d = valid ? kq_f16_bits_to_f32(h0 & 0xFFFF) : 0.f;
+        const float dmin = valid ? kq_f16_bits_to_f32(h0 >> 16) : 0.f;
         // scales bytes s[0..11] = raw[0].y, .z, .w
         const uint32_t s0 = raw[0].y, s1 = raw[0].z, s2 = raw[0].w;
 #pragma unroll
@@ -130,21 +131,17 @@ struct Block<KQ_CODEC_Q6_K> {
     uint32_t dbits;
     half2_t dsc[16];
 
-    __device__ __forceinline__ void load(const uint8_t *blk, bool valid) {
+    __device__ __forceinline__ void load(const uint8_t *blk) {
         const u32x4_a2 *p = (const u32x4_a2 *)blk;
 #pragma unroll
         for (int i = 0; i < 13; ++i) {
-            if (valid) {
-                const u32x4_a2 v = p[i];
-                raw[i] = u32x4{v.x, v.y, v.z, v.w};
-            } else {
-                raw[i] = u32x4{0, 0, 0, 0};
-            }
+            const u32x4_a2 v = p[i];
+            raw[i] = u32x4{v.x, v.y, v.z, v.w};
         }
-        dbits = valid ? (uint32_t)*(const uint16_t *)(blk + 208) : 0u;
+        dbits = (uint32_t)*(const uint16_t *)(blk + 208);
     }
-    __device__ __forceinline__ void prep() {
-        const float d = kq_f16_bits_to_f32(dbits);
+    __device__ __forceinline__ void prep(bool valid) {
+        const float d = valid ? kq_f16_bits_to_f32(dbits) : 0.f;
         const uint32_t *sw = (const uint32_t *)&raw[12];  // bytes 192..207
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -190,21 +187,17 @@ struct Block<KQ_CODEC_IQ2_XXS> {
     uint32_t dbits;
     half2_t db[8];
 
-    __device__ __forceinline__ void load(const uint8_t *blk, bool valid) {
+    __device__ __forceinline__ void load(const uint8_t *blk) {
         const u32x4_a2 *p = (const u32x4_a2 *)(blk + 2);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            if (valid) {
-                const u32x4_a2 v = p[i];
-                raw[i] = u32x4{v.x, v.y, v.z, v.w};
-            } else {
-                raw[i] = u32x4{0, 0, 0, 0};
-            }
+            const u32x4_a2 v = p[i];
+            raw[i] = u32x4{v.x, v.y, v.z, v.w};
         }
-        dbits = valid ? (uint32_t)*(const uint16_t *)blk : 0u;
+        dbits = (uint32_t)*(const uint16_t *)blk;
     }
-    __device__ __forceinline__ void prep() {
-        const float d = kq_f16_bits_to_f32(dbits);
+    __device__ __forceinline__ void prep(bool valid) {
+        const float d = valid ? kq_f16_bits_to_f32(dbits) : 0.f;
         const uint32_t *g = (const uint32_t *)&raw[0];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -260,13 +253,15 @@ __device__ __forceinline__ half8_t load_x8(const char *p) {
 
 // Accumulate over super-blocks [kb_begin, kb_end) of NW weight matrices
 // (NW = 2: gate and up share the activations).  wrow[i] points at this
-// lane's weight row (row n0 + lane%16) of matrix i, or is unused when
-// !row_valid.  xrow[mt] points (as bytes) at this lane's activation row
-// (m-tile mt, row lane%16) or is null for padding rows.
+// lane's weight row (row n0 + lane%16 of matrix i, clamped to a valid row by
+// the caller).  xrow[mt] points (as bytes) at this lane's activation row of
+// m-tile mt, clamped to a valid row: rows past M compute throw-away outputs
+// that are never stored, so no load is conditional.  Blocks past kb_end (the
+// last, partial 4-block step) are read from a clamped valid address and
+// zeroed through their scales.
 template <int CODEC, int MT, int XT, int NW>
-__device__ __forceinline__ void tile_accumulate(const uint8_t *const (&wrow)[NW], bool row_valid,
-                                                int kb_begin, int kb_end,
-                                                const char *const (&xrow)[MT],
+__device__ __forceinline__ void tile_accumulate(const uint8_t *const (&wrow)[NW], int kb_begin,
+                                                int kb_end, const char *const (&xrow)[MT],
                                                 floatx4 (&acc)[NW][MT]) {
     constexpr int XS = x_elem_bytes<XT>();
     constexpr int BPB = kq_block_bytes(CODEC);
@@ -274,30 +269,42 @@ __device__ __forceinline__ void tile_accumulate(const uint8_t *const (&wrow)[NW]
     for (int kb = kb_begin; kb < kb_end; kb += 4) {
         const int blk = kb + g;
         const bool bvalid = blk < kb_end;
+        const int blk_c = bvalid ? blk : kb_end - 1;
         Block<CODEC> wb[NW];
 #pragma unroll
-        for (int i = 0; i < NW; ++i) wb[i].load(wrow[i] + (int64_t)blk * BPB, bvalid && row_valid);
+        for (int i = 0; i < NW; ++i) wb[i].load(wrow[i] + (int64_t)blk_c * BPB);
 #pragma unroll
-        for (int i = 0; i < NW; ++i) wb[i].prep();
+        for (int i = 0; i < NW; ++i) wb[i].prep(bvalid);
+        const int64_t xoff = (int64_t)blk_c * KQ_QK * XS;
+        // Activation fragments are issued in chunks of TC MFMA steps (128
+        // VGPRs of fp16 operands) before any of them is consumed, so their
+        // L2 latency overlaps instead of stalling every MFMA.
+        constexpr int TC = 32 / MT;
 #pragma unroll
-        for (int t = 0; t < 32; ++t) {
-            half8_t a[MT];
+        for (int t0 = 0; t0 < 32; t0 += TC) {
+            half8_t a[TC][MT];
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-                if (xrow[mt] != nullptr && bvalid) {
-                    a[mt] = load_x8<XT>(xrow[mt] + ((int64_t)blk * KQ_QK + 8 * t) * XS);
-                } else {
-                    a[mt] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < NW; ++i) {
-                const half8_t b = wb[i].frag(t);
+            for (int tt = 0; tt < TC; ++tt)
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt)
-                    acc[i][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mt], b, acc[i][mt], 0, 0, 0);
+                    a[tt][mt] = load_x8<XT>(xrow[mt] + xoff + 8 * (t0 + tt) * XS);
+            // keep the whole batch of loads ahead of the first consumer (the
+            // scheduler would otherwise sink each load next to its MFMA)
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int tt = 0; tt < TC; ++tt) {
+#pragma unroll
+                for (int i = 0; i < NW; ++i) {
+                    const half8_t b = wb[i].frag(t0 + tt);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+                        acc[i][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tt][mt], b, acc[i][mt], 0, 0, 0);
+                }
             }
         }
+        // inside the loop: the accumulator copies at the loop exit must come
+        // after these wait states
+        kq_mfma_drain();
     }
 }
 

@@ -34,7 +34,9 @@ class KQuantLinear(nn.Module):
         self.register_buffer("weight", torch.zeros(out_dims, _wire_cols(in_dims, codec), dtype=torch.uint8,
                                                    device=device))
         self.register_buffer("scales", torch.zeros(1, dtype=torch.uint8, device=device))
-        self.bias = nn.Parameter(torch.zeros(out_dims, device=device)) if bias else None
+        # inference leaf: the quantized matmul has no backward, so nothing here
+        # takes part in autograd
+        self.bias = nn.Parameter(torch.zeros(out_dims, device=device), requires_grad=False) if bias else None
 
     def forward(self, x):
         y = ops.quantized_matmul(x, self.weight, self.scales, self.kquant_type, transpose=True)

@@ -93,15 +93,17 @@ def _rows_view(x):
 
 
 class _Workspaces:
-    """Zero-filled scratch per (device, stream), grown on demand.  Kernels
-    leave their counters zeroed, so a workspace is reusable by later calls on
-    the same stream."""
+    """Zero-filled scratch per (op family, device, stream), grown on demand.
+    Kernels leave their counters zeroed, so a workspace is reusable by later
+    calls of the same family on the same stream.  Families never share one:
+    the matmul's partials would land on the attention's counters and vice
+    versa."""
 
     def __init__(self):
         self._ws = {}
 
-    def get(self, device, stream_handle, nbytes):
-        key = (device.index, stream_handle)
+    def get(self, kind, device, stream_handle, nbytes):
+        key = (kind, device.index, stream_handle)
         cur = self._ws.get(key)
         if cur is None or cur.numel() < nbytes:
             cur = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
@@ -183,9 +185,12 @@ def _launch_grouped(probs, x_dt, y_dt, device, stream):
     arr = (MatmulProblem * len(probs))(*probs)
     L = lib()
     need = L.kq_matmul_workspace_bytes(arr, len(probs))
-    ws = _WS.get(device, stream.value, need)
+    ws_ptr, ws_len = None, 0
+    if need:
+        ws = _WS.get("matmul", device, stream.value, need)
+        ws_ptr, ws_len = ws.data_ptr(), ws.numel()
     check("kq_quantized_matmul_grouped",
-          L.kq_quantized_matmul_grouped(arr, len(probs), x_dt, y_dt, ws.data_ptr(), ws.numel(), stream))
+          L.kq_quantized_matmul_grouped(arr, len(probs), x_dt, y_dt, ws_ptr, ws_len, stream))
 
 
 def quantized_matmul(x, w, scales=None, codec="q4_k", transpose=True, out_dtype=None):
@@ -435,7 +440,7 @@ def _sdpa_launch(q, k, v, tabs, Hkv, scale, max_len, out):
     L = lib()
     need = L.kq_sdpa_workspace_bytes(B, Hq, Hkv, D, max_len)
     s = _stream(q)
-    ws = _WS.get(q.device, s.value, need)
+    ws = _WS.get("sdpa", q.device, s.value, need)
     rc = L.kq_sdpa_decode_ragged(q.data_ptr(), k.data_ptr(), v.data_ptr(), tabs[0].data_ptr(),
                                  tabs[1].data_ptr(), tabs[2].data_ptr(), B, Hq, Hkv, D, max_len,
                                  float(scale), _dt(q.dtype), out.data_ptr(), ws.data_ptr(), ws.numel(), s)

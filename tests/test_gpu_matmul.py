@@ -8,7 +8,7 @@ import os
 import numpy as np
 import pytest
 
-from helpers import TOL, fp16_rows, quantized_weights
+from helpers import BF16_TOL, TOL, fp16_rows, quantized_weights
 from oracle import kquant as okq
 
 pytestmark = pytest.mark.gpu
@@ -70,7 +70,8 @@ def test_bf16_activations_and_f32_out():
     xb = torch.from_numpy(x32).to(torch.bfloat16)
     ref = okq.qmm_ref(xb.float().numpy(), wire, "q4_k")
     got = ops.quantized_matmul(xb.cuda(), _dev(wire), None, "q4_k").float().cpu().numpy()
-    assert okq.max_rel(got, ref) <= TOL
+    # a bf16 output carries 8 mantissa bits: its rounding alone is up to 2^-9 relative
+    assert okq.max_rel(got, ref) <= BF16_TOL
     got32 = ops.quantized_matmul(xb.cuda(), _dev(wire), None, "q4_k", out_dtype=torch.float32)
     assert got32.dtype == torch.float32
     assert okq.max_rel(got32.cpu().numpy(), ref) <= TOL
@@ -130,16 +131,18 @@ def test_deterministic_split_k():
     assert okq.max_rel(outs[0].astype(np.float32), ref) <= TOL
 
 
-def test_split_plan_invariance(monkeypatch):
-    """Changing the K-split plan changes summation order only (tolerance)."""
-    rng = np.random.default_rng(14)
-    wire = quantized_weights(rng, "q4_k", 64, 4096)
-    x = fp16_rows(rng, 2, 4096)
-    ref = okq.qmm_ref(x, wire, "q4_k")
-    for waves in ("1", "64", "100000"):
-        monkeypatch.setenv("GMLX_KQ_MM_WAVES", waves)
-        got = _mm(x, wire, "q4_k").float().cpu().numpy()
-        assert okq.max_rel(got, ref) <= TOL, waves
+@pytest.mark.parametrize("nb", [1, 2, 3, 4, 5, 8, 16, 17, 48])
+def test_k_block_counts(nb):
+    """Every K split shape of the 4-wave workgroup: waves with no step,
+    partial last steps, several steps per wave."""
+    rng = np.random.default_rng(14 + nb)
+    K = 256 * nb
+    for codec in ("q4_k", "q6_k"):
+        wire = quantized_weights(rng, codec, 40, K)
+        x = fp16_rows(rng, 3, K)
+        ref = okq.qmm_ref(x, wire, codec)
+        got = _mm(x, wire, codec).float().cpu().numpy()
+        assert okq.max_rel(got, ref) <= TOL, (codec, nb)
 
 
 def test_module_forward():
