@@ -309,26 +309,58 @@ __global__ __launch_bounds__(64) void kq_sdpa_split_kernel(SdpaArgs a) {
     }
 }
 
-// One workgroup of D threads per (row b, q head hq); rows with a single split
-// were finished by the split pass.
+// One 256-thread workgroup per (row b, q head hq); rows with a single split
+// were finished by the split pass.  Thread t handles output element
+// d = t % D for the splits s = p, p + P, ... (p = t / D, P = 256 / D parts),
+// then the P partial sums are added in part order through LDS: a fixed
+// summation order, so the merge is deterministic.
 template <int D, bool BF>
 __global__ __launch_bounds__(256) void kq_sdpa_merge_kernel(SdpaArgs a) {
+    constexpr int P = 256 / D;
+    __shared__ float red_m[4];
+    __shared__ float red_acc[P][D];
+    __shared__ float red_l[P];
     const int b = blockIdx.x / a.Hq;
     const int hq = blockIdx.x - b * a.Hq;
     const int len = max(min(a.row_len[b], a.max_len), 0);
     const int nsplit = row_splits(len, a.split);
-    if (nsplit == 1) return;
+    if (nsplit == 1) return;  // uniform over the workgroup
     const int h = hq / a.G, r = hq - h * a.G;
-    const int d = threadIdx.x;
+    const int t = threadIdx.x;
+    const int d = t % D, part = t / D;
     const int64_t slot0 = ((int64_t)b * a.Hkv + h) * a.max_splits;
+    const float *ml = a.ml + (slot0 * a.G + r) * 2;        // split s at ml[s * G * 2]
+    const float *po = a.part + (slot0 * a.G + r) * D + d;  // split s at po[s * G * D]
+    const int64_t ml_stride = (int64_t)a.G * 2, po_stride = (int64_t)a.G * D;
+    // common max over the splits
     float M = -INFINITY;
-    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, a.ml[((slot0 + s) * a.G + r) * 2]);
+    for (int s = t; s < nsplit; s += 256) M = fmaxf(M, ml[s * ml_stride]);
+    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+    if ((t & 63) == 0) red_m[t >> 6] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
+    // D = 96: threads 192..255 hold no (d, part) pair
+    const bool active = part < P;
     float acc = 0.f, L = 0.f;
-    for (int s = 0; s < nsplit; ++s) {
-        const float *pml = a.ml + ((slot0 + s) * a.G + r) * 2;
-        const float f = (pml[0] == -INFINITY) ? 0.f : exp2f(pml[0] - M);
-        L += pml[1] * f;
-        acc += f * a.part[((slot0 + s) * a.G + r) * D + d];
+    if (active) {
+#pragma unroll 4
+        for (int s = part; s < nsplit; s += P) {
+            const float ms = ml[s * ml_stride], ls = ml[s * ml_stride + 1];
+            const float f = (ms == -INFINITY) ? 0.f : exp2f(ms - M);
+            L += ls * f;
+            acc += f * po[s * po_stride];
+        }
+        red_acc[part][d] = acc;
+        if (d == 0) red_l[part] = L;
+    }
+    __syncthreads();
+    if (part != 0) return;
+    acc = red_acc[0][d];
+    L = red_l[0];
+#pragma unroll
+    for (int q = 1; q < P; ++q) {
+        acc += red_acc[q][d];
+        L += red_l[q];
     }
     const float inv = L > 0.f ? 1.f / L : 0.f;
     a.out[((int64_t)b * a.Hq + hq) * D + d] = from_f32<BF>(acc * inv);
@@ -366,7 +398,7 @@ WsLayout ws_layout(int B, int Hq, int Hkv, int D, int max_len) {
 template <int D, bool BF>
 void launch(const SdpaArgs &a, int grid, bool merge, hipStream_t s) {
     hipLaunchKernelGGL((kq_sdpa_split_kernel<D, BF>), dim3(grid), dim3(64), 0, s, a);
-    if (merge) hipLaunchKernelGGL((kq_sdpa_merge_kernel<D, BF>), dim3(a.B * a.Hq), dim3(D), 0, s, a);
+    if (merge) hipLaunchKernelGGL((kq_sdpa_merge_kernel<D, BF>), dim3(a.B * a.Hq), dim3(256), 0, s, a);
 }
 
 }  // namespace

@@ -13,6 +13,12 @@
 
 #include "kq_mma.h"
 
+// kq_qmv.hip: persistent small-batch launch (problems validated, all live,
+// sharing codec / x / M <= 16 / K <= 8192).
+int kq_qmv_persistent_launch(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype, hipStream_t s);
+// workgroups one persistent launch of this problem's codec / K would use
+int kq_qmv_persistent_grid(const kq_matmul_problem &q);
+
 namespace {
 
 using namespace kqmma;
@@ -48,8 +54,10 @@ __device__ __forceinline__ void store_tile(void *y, int y_dtype, int64_t y_strid
     }
 }
 
+// Wave `wave` of the workgroup takes super-blocks wave, wave + kWaves, ...
 template <int CODEC, int MT, int XT>
-__device__ __forceinline__ void dense_tile(const DenseProblem &p, int nt, int wave, floatx4 (&acc)[MT]) {
+__device__ __forceinline__ void dense_tile(const DenseProblem &p, int nt, int wave, floatx4 (&acc)[MT],
+                                           const Iq2Tables &tab) {
     const int lane = kq_lane();
     const int r = lane & 15;
     const int m0 = blockIdx.y * kMaxChunk;
@@ -65,8 +73,7 @@ __device__ __forceinline__ void dense_tile(const DenseProblem &p, int nt, int wa
     floatx4 a1[1][MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) a1[0][mt] = floatx4{0, 0, 0, 0};
-    for (int kb = 4 * wave; kb < nb; kb += 4 * kWaves)
-        tile_accumulate<CODEC, MT, XT, 1>(wrow, kb, min(nb, kb + 4), xrow, a1);
+    tile_accumulate<CODEC, MT, XT, 1>(wrow, wave, kWaves, nb, xrow, a1, tab);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = a1[0][mt];
 }
@@ -74,6 +81,7 @@ __device__ __forceinline__ void dense_tile(const DenseProblem &p, int nt, int wa
 template <int MT, int XT>
 __global__ __launch_bounds__(64 * kWaves) void kq_dense_grouped_kernel(DenseArgs a) {
     __shared__ floatx4 red[kWaves - 1][MT][64];
+    __shared__ Iq2Tables iq2_tab;
     const int unit = blockIdx.x;
     // Select the problem with static indices only: dynamic indexing of the
     // by-value argument array would copy it to scratch memory.
@@ -88,9 +96,12 @@ __global__ __launch_bounds__(64 * kWaves) void kq_dense_grouped_kernel(DenseArgs
     if (m0 >= p.M) return;  // uniform over the workgroup
     floatx4 acc[MT];
     switch (p.codec) {
-    case KQ_CODEC_Q4_K: dense_tile<KQ_CODEC_Q4_K, MT, XT>(p, nt, wave, acc); break;
-    case KQ_CODEC_Q6_K: dense_tile<KQ_CODEC_Q6_K, MT, XT>(p, nt, wave, acc); break;
-    default: dense_tile<KQ_CODEC_IQ2_XXS, MT, XT>(p, nt, wave, acc); break;
+    case KQ_CODEC_Q4_K: dense_tile<KQ_CODEC_Q4_K, MT, XT>(p, nt, wave, acc, iq2_tab); break;
+    case KQ_CODEC_Q6_K: dense_tile<KQ_CODEC_Q6_K, MT, XT>(p, nt, wave, acc, iq2_tab); break;
+    default:
+        load_iq2_tables(iq2_tab);
+        dense_tile<KQ_CODEC_IQ2_XXS, MT, XT>(p, nt, wave, acc, iq2_tab);
+        break;
     }
     if (wave > 0) {
 #pragma unroll
@@ -130,6 +141,8 @@ __device__ __forceinline__ float act_apply(int act, float g) {
 
 template <int CODEC, int MT, int XT, int NW>
 __global__ __launch_bounds__(64) void kq_gather_kernel(GatherArgs a) {
+    __shared__ Iq2Tables iq2_tab;
+    if constexpr (CODEC == KQ_CODEC_IQ2_XXS) load_iq2_tables(iq2_tab);
     const int lane = kq_lane();
     const int r = lane & 15;
     const int slot = blockIdx.x / a.n_tiles;
@@ -159,7 +172,7 @@ __global__ __launch_bounds__(64) void kq_gather_kernel(GatherArgs a) {
         for (int i = 0; i < NW; ++i)
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) acc[i][mt] = floatx4{0, 0, 0, 0};
-        tile_accumulate<CODEC, MT, XT, NW>(wrow, 0, nb, xrow, acc);
+        tile_accumulate<CODEC, MT, XT, NW>(wrow, 0, 1, nb, xrow, acc, iq2_tab);
         if (!n_valid) continue;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
@@ -351,6 +364,26 @@ int group_mt(const kq_matmul_problem *ps, int n) {
     return mt <= 1 ? 1 : mt <= 2 ? 2 : 4;
 }
 
+int env_flag(const char *name, int dflt) {
+    const char *s = getenv(name);
+    if (!s || !*s) return dflt;
+    return !(s[0] == '0' && s[1] == 0);
+}
+
+// The persistent small-batch path (kq_qmv.hip) serves a set of problems that
+// share one codec, x, x stride, M <= 16 and K <= 8192 (Q6_K: K <= 4096).
+bool qmv_eligible(const kq_matmul_problem *ps, const int *idx, int n) {
+    if (n == 0) return false;
+    const kq_matmul_problem &q0 = ps[idx[0]];
+    if (q0.M > 16 || q0.K > (q0.codec == KQ_CODEC_Q6_K ? 4096 : 8192)) return false;
+    for (int i = 1; i < n; ++i) {
+        const kq_matmul_problem &q = ps[idx[i]];
+        if (q.x != q0.x || q.x_row_stride != q0.x_row_stride || q.M != q0.M || q.K != q0.K || q.codec != q0.codec)
+            return false;
+    }
+    return true;
+}
+
 template <int MT, int XT>
 void launch_dense(const DenseArgs &a, int units, int chunks, hipStream_t s) {
     hipLaunchKernelGGL((kq_dense_grouped_kernel<MT, XT>), dim3(units, chunks), dim3(64 * kWaves), 0, s, a);
@@ -457,6 +490,40 @@ int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problem
     for (int i = 0; i < n_problems; ++i) {
         const int rc = validate_problem(problems[i]);
         if (rc != KQ_OK) return rc;
+    }
+    // small batches: one persistent launch per codec when every codec's
+    // problems share their activations (q|k|v, gate|up of one layer)
+    if (env_flag("GMLX_KQ_PERSISTENT", 1)) {
+        int by_codec[3][KQ_MAX_GROUP], cnt[3] = {0, 0, 0};
+        const int codecs[3] = {KQ_CODEC_Q4_K, KQ_CODEC_Q6_K, KQ_CODEC_IQ2_XXS};
+        int live = 0;
+        for (int i = 0; i < n_problems; ++i) {
+            if (problems[i].M == 0 || problems[i].N == 0) continue;
+            ++live;
+            for (int c = 0; c < 3; ++c)
+                if (problems[i].codec == codecs[c]) by_codec[c][cnt[c]++] = i;
+        }
+        bool ok = live > 0;
+        for (int c = 0; c < 3 && ok; ++c)
+            if (cnt[c] && !qmv_eligible(problems, by_codec[c], cnt[c])) ok = false;
+        // persistence pays only when a workgroup walks several tiles: every
+        // codec's launch needs at least two tiles per workgroup
+        for (int c = 0; c < 3 && ok; ++c) {
+            if (!cnt[c]) continue;
+            int tiles = 0;
+            for (int i = 0; i < cnt[c]; ++i) tiles += (problems[by_codec[c][i]].N + 15) / 16;
+            if (tiles < 2 * kq_qmv_persistent_grid(problems[by_codec[c][0]])) ok = false;
+        }
+        if (ok) {
+            for (int c = 0; c < 3; ++c) {
+                if (!cnt[c]) continue;
+                kq_matmul_problem sub[KQ_MAX_GROUP];
+                for (int i = 0; i < cnt[c]; ++i) sub[i] = problems[by_codec[c][i]];
+                const int rc = kq_qmv_persistent_launch(sub, cnt[c], x_dtype, y_dtype, (hipStream_t)stream);
+                if (rc != KQ_OK) return rc;
+            }
+            return KQ_OK;
+        }
     }
     DenseArgs a;
     int units = 0, max_chunks = 0, np = 0;

@@ -1,15 +1,18 @@
 // Wave-level dequant-fused MFMA tile for GGUF K-quant weights (gfx950).
 //
-// Tile: one wave computes C[16*MT batch rows, 16 weight rows] over a range of
+// Tile: one wave computes C[16*MT batch rows, 16 weight rows] over a set of
 // super-blocks with v_mfma_f32_16x16x32_f16 (A = activations, B = weights^T).
 // Lane l = 16*g + r: r selects the weight row (B column) and the activation
-// row (A row) the lane feeds; g selects WHICH super-block of the current
-// 4-block step the lane owns.  A lane therefore decodes one whole super-block
-// per step -- all of its scales are local -- and feeds 32 MFMAs of 8 values
-// each (values 8t..8t+7 of its block).  The MFMA sums over the 4 lane groups,
-// i.e. over 4 different blocks at once; that is valid because every weight
-// fragment is already fully scaled (w = dequant(q) in fp16), so no per-block
-// factor has to be applied to the accumulator.
+// row (A row) the lane feeds; g selects which 8 of the MFMA's 32 k values.
+// One MFMA covers 32 consecutive values of ONE super-block (MFMA step t of a
+// block = values 32t .. 32t+31; lane group g holds 32t + 8g .. +7), so:
+//   - an activation fragment is 16 contiguous bytes and the 4 lane groups of
+//     one activation row read 64 contiguous bytes (one cache line);
+//   - a lane reads only the quant bytes of its 8-value slices (Q4_K: 4 x 8 B
+//     of qs per block) plus the block's scale header, which the 4 lanes of a
+//     row share.
+// Every weight fragment is fully scaled before the MFMA (w = dequant(q) in
+// fp16), so the accumulator needs no per-block factor.
 //
 // Dequant to fp16 in registers, per pair of values:
 //   Q4_K : h = perm(0x64.., nibbles)  (= 1024+q, exact)
@@ -56,33 +59,55 @@ constexpr Iq2Tables make_iq2_tables() {
 
 __device__ const Iq2Tables kIq2 = make_iq2_tables();
 
-// ---- per-codec block decoders --------------------------------------------
+// Copy the IQ2_XXS tables into a workgroup's LDS (6 KB); every thread of the
+// workgroup must call it, and it ends with a workgroup barrier.
+__device__ __forceinline__ void load_iq2_tables(Iq2Tables &dst) {
+    const u32x4 *src = (const u32x4 *)&kIq2;
+    u32x4 *d = (u32x4 *)&dst;
+    constexpr int n = (int)(sizeof(Iq2Tables) / 16);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) d[i] = src[i];
+    __syncthreads();
+}
+
+// ---- per-codec block decoders (the lane's view of one super-block) -------
 
 __device__ __forceinline__ half2_t h2b(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
-__device__ __forceinline__ uint32_t b2h(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
 __device__ __forceinline__ half2_t bcast(_Float16 v) { return half2_t{v, v}; }
+
+// 8 bytes (two dwords, each value in [0, 63]) -> 8 fp16 (1024 + byte)
+struct Bias8 {
+    half2_t p0, p1, p2, p3;
+    __device__ __forceinline__ Bias8(uint32_t w0, uint32_t w1)
+        : p0(h2b(kq_bytes_to_h2_biased(w0, KQ_SEL_B01))), p1(h2b(kq_bytes_to_h2_biased(w0, KQ_SEL_B23))),
+          p2(h2b(kq_bytes_to_h2_biased(w1, KQ_SEL_B01))), p3(h2b(kq_bytes_to_h2_biased(w1, KQ_SEL_B23))) {}
+};
+
+__device__ __forceinline__ half8_t cat8(half2_t a, half2_t b, half2_t c, half2_t d) {
+    return half8_t{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+}
 
 template <int CODEC>
 struct Block;
 
-// Q4_K: 144 B = header (d, dmin, 12 B scales) + 128 B qs; 16-B aligned.
+// Q4_K (144 B = d, dmin, 12 B packed scales, 128 B qs; 16-B aligned).
+// Step t = sub-block t: chunk c = t/2 (qs bytes 32c .. 32c+31), low nibbles
+// for even t, high for odd t; lane group g takes bytes 32c + 8g .. +7.
 template <>
 struct Block<KQ_CODEC_Q4_K> {
-    u32x4 raw[9];
+    u32x4 hdr;
+    u32x2 q[4];
     half2_t dsc[8], ndm[8];
 
-    __device__ __forceinline__ void load(const uint8_t *blk) {
-        const u32x4 *p = (const u32x4 *)blk;
+    __device__ __forceinline__ void load(const uint8_t *blk, int g) {
+        hdr = *(const u32x4 *)blk;
 #pragma unroll
-        for (int i = 0; i < 9; ++i) raw[i] = p[i];
+        for (int c = 0; c < 4; ++c) q[c] = *(const u32x2 *)(blk + 16 + 32 * c + 8 * g);
     }
-    // valid == false zeroes every weight of the block (a padding block).
-    __device__ __forceinline__ void prep(bool valid) {
-        const uint32_t h0 = raw[0].x;
-        const float d = valid ? kq_f16_bits_to_f32(h0 & 0xFFFF) : 0.f;
-        const float dmin = valid ? kq_f16_bits_to_f32(h0 >> 16) : 0.f;
-        // scales bytes s[0..11] = raw[0].y, .z, .w
-        const uint32_t s0 = raw[0].y, s1 = raw[0].z, s2 = raw[0].w;
+    __device__ __forceinline__ void prep(int g) {
+        (void)g;
+        const float d = kq_f16_bits_to_f32(hdr.x & 0xFFFF);
+        const float dmin = kq_f16_bits_to_f32(hdr.x >> 16);
+        const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;  // scales bytes 0..11
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             uint32_t sc, mn;
@@ -90,9 +115,9 @@ struct Block<KQ_CODEC_Q4_K> {
                 sc = (s0 >> (8 * j)) & 63;
                 mn = (s1 >> (8 * j)) & 63;
             } else {
-                const uint32_t bj4 = (s2 >> (8 * (j - 4))) & 0xFF;     // s[j+4]
-                const uint32_t bjm4 = (s0 >> (8 * (j - 4))) & 0xFF;    // s[j-4]
-                const uint32_t bj = (s1 >> (8 * (j - 4))) & 0xFF;      // s[j]
+                const uint32_t bj4 = (s2 >> (8 * (j - 4))) & 0xFF;   // s[j+4]
+                const uint32_t bjm4 = (s0 >> (8 * (j - 4))) & 0xFF;  // s[j-4]
+                const uint32_t bj = (s1 >> (8 * (j - 4))) & 0xFF;    // s[j]
                 sc = (bj4 & 0xF) | ((bjm4 >> 6) << 4);
                 mn = (bj4 >> 4) | ((bj >> 6) << 4);
             }
@@ -100,124 +125,124 @@ struct Block<KQ_CODEC_Q4_K> {
             ndm[j] = bcast((_Float16)(-(dmin * (float)mn)));
         }
     }
-    // values 8t .. 8t+7 of the block (t = 0..31)
-    __device__ __forceinline__ half8_t frag(int t) const {
-        const int sub = t >> 2, c = sub >> 1, j = t & 3;
-        const uint32_t *qs = (const uint32_t *)&raw[1];
-        uint32_t w0 = qs[8 * c + 2 * j], w1 = qs[8 * c + 2 * j + 1];
-        if (sub & 1) {
+    __device__ __forceinline__ half8_t frag(int t, int g, const Iq2Tables &) const {
+        (void)g;
+        uint32_t w0 = q[t >> 1].x, w1 = q[t >> 1].y;
+        if (t & 1) {
             w0 >>= 4;
             w1 >>= 4;
         }
-        w0 &= 0x0F0F0F0Fu;
-        w1 &= 0x0F0F0F0Fu;
+        const Bias8 h(w0 & 0x0F0F0F0Fu, w1 & 0x0F0F0F0Fu);
         const half2_t k1024 = {(_Float16)1024.f, (_Float16)1024.f};
-        half2_t p0 = h2b(kq_bytes_to_h2_biased(w0, KQ_SEL_B01)) - k1024;
-        half2_t p1 = h2b(kq_bytes_to_h2_biased(w0, KQ_SEL_B23)) - k1024;
-        half2_t p2 = h2b(kq_bytes_to_h2_biased(w1, KQ_SEL_B01)) - k1024;
-        half2_t p3 = h2b(kq_bytes_to_h2_biased(w1, KQ_SEL_B23)) - k1024;
-        p0 = __builtin_elementwise_fma(p0, dsc[sub], ndm[sub]);
-        p1 = __builtin_elementwise_fma(p1, dsc[sub], ndm[sub]);
-        p2 = __builtin_elementwise_fma(p2, dsc[sub], ndm[sub]);
-        p3 = __builtin_elementwise_fma(p3, dsc[sub], ndm[sub]);
-        return half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+        return cat8(__builtin_elementwise_fma(h.p0 - k1024, dsc[t], ndm[t]),
+                    __builtin_elementwise_fma(h.p1 - k1024, dsc[t], ndm[t]),
+                    __builtin_elementwise_fma(h.p2 - k1024, dsc[t], ndm[t]),
+                    __builtin_elementwise_fma(h.p3 - k1024, dsc[t], ndm[t]));
     }
 };
 
-// Q6_K: 210 B = ql[128] qh[64] scales[16] d; only 2-byte aligned.
+// Q6_K (210 B = ql[128] qh[64] scales[16] d; only 2-byte aligned).
+// Step t: half h = t/4, quarter q = t%4 (values 128h + 32q + l, l = 0..31);
+// lane group g takes l = 8g .. 8g+7: ql bytes 64h + 32(q&1) + 8g (high
+// nibbles for q >= 2), qh bytes 32h + 8g (bits 2q, 2q+1), one int8 scale
+// sc[8h + 2q + g/2].
 template <>
 struct Block<KQ_CODEC_Q6_K> {
-    u32x4 raw[13];        // bytes 0..207
+    u32x2 ql[4];  // [2h + p]
+    u32x2 qh[2];  // [h]
+    u32x4 sc;     // scales[16]
     uint32_t dbits;
-    half2_t dsc[16];
+    half2_t dsc[8];
 
-    __device__ __forceinline__ void load(const uint8_t *blk) {
-        const u32x4_a2 *p = (const u32x4_a2 *)blk;
+    __device__ __forceinline__ void load(const uint8_t *blk, int g) {
 #pragma unroll
-        for (int i = 0; i < 13; ++i) {
-            const u32x4_a2 v = p[i];
-            raw[i] = u32x4{v.x, v.y, v.z, v.w};
+        for (int i = 0; i < 4; ++i) {
+            const u32x2_a2 v = *(const u32x2_a2 *)(blk + 64 * (i >> 1) + 32 * (i & 1) + 8 * g);
+            ql[i] = u32x2{v.x, v.y};
         }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const u32x2_a2 v = *(const u32x2_a2 *)(blk + 128 + 32 * h + 8 * g);
+            qh[h] = u32x2{v.x, v.y};
+        }
+        const u32x4_a2 s = *(const u32x4_a2 *)(blk + 192);
+        sc = u32x4{s.x, s.y, s.z, s.w};
         dbits = (uint32_t)*(const uint16_t *)(blk + 208);
     }
-    __device__ __forceinline__ void prep(bool valid) {
-        const float d = valid ? kq_f16_bits_to_f32(dbits) : 0.f;
-        const uint32_t *sw = (const uint32_t *)&raw[12];  // bytes 192..207
+    __device__ __forceinline__ void prep(int g) {
+        const float d = kq_f16_bits_to_f32(dbits);
+        const int sh = 8 * (g >> 1);
+        const uint32_t w[4] = {sc.x, sc.y, sc.z, sc.w};
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int8_t sc = (int8_t)((sw[i >> 2] >> (8 * (i & 3))) & 0xFF);
-            dsc[i] = bcast((_Float16)(d * (float)sc));
+        for (int t = 0; t < 8; ++t) {
+            // scale index 8h + 2q + g/2 = 2t + g/2: byte (2t + g/2) of the 16
+            const int bi = 2 * t;
+            const int8_t s = (int8_t)((w[bi >> 2] >> (8 * (bi & 3) + sh)) & 0xFF);
+            dsc[t] = bcast((_Float16)(d * (float)s));
         }
     }
-    __device__ __forceinline__ half8_t frag(int t) const {
-        const int h = t >> 4, quarter = (t >> 2) & 3, j = t & 3;
-        const uint32_t *ql = (const uint32_t *)&raw[0];   // 32 dwords
-        const uint32_t *qh = (const uint32_t *)&raw[8];   // 16 dwords
-        uint32_t l0 = ql[16 * h + 8 * (quarter & 1) + 2 * j];
-        uint32_t l1 = ql[16 * h + 8 * (quarter & 1) + 2 * j + 1];
-        uint32_t q0 = qh[8 * h + 2 * j], q1 = qh[8 * h + 2 * j + 1];
-        if (quarter >= 2) {
+    __device__ __forceinline__ half8_t frag(int t, int g, const Iq2Tables &) const {
+        (void)g;
+        const int h = t >> 2, q = t & 3;
+        uint32_t l0 = ql[2 * h + (q & 1)].x, l1 = ql[2 * h + (q & 1)].y;
+        if (q >= 2) {
             l0 >>= 4;
             l1 >>= 4;
         }
-        // 6-bit codes: low nibble | (2 high bits << 4)
-        const int hs = 2 * quarter;
+        const uint32_t hq0 = qh[h].x, hq1 = qh[h].y;
+        const int hs = 2 * q;
         uint32_t c0, c1;
         if (hs <= 4) {
-            c0 = (l0 & 0x0F0F0F0Fu) | ((q0 << (4 - hs)) & 0x30303030u);
-            c1 = (l1 & 0x0F0F0F0Fu) | ((q1 << (4 - hs)) & 0x30303030u);
+            c0 = (l0 & 0x0F0F0F0Fu) | ((hq0 << (4 - hs)) & 0x30303030u);
+            c1 = (l1 & 0x0F0F0F0Fu) | ((hq1 << (4 - hs)) & 0x30303030u);
         } else {
-            c0 = (l0 & 0x0F0F0F0Fu) | ((q0 >> (hs - 4)) & 0x30303030u);
-            c1 = (l1 & 0x0F0F0F0Fu) | ((q1 >> (hs - 4)) & 0x30303030u);
+            c0 = (l0 & 0x0F0F0F0Fu) | ((hq0 >> (hs - 4)) & 0x30303030u);
+            c1 = (l1 & 0x0F0F0F0Fu) | ((hq1 >> (hs - 4)) & 0x30303030u);
         }
+        const Bias8 b(c0, c1);
         const half2_t k1056 = {(_Float16)1056.f, (_Float16)1056.f};
-        const half2_t s = dsc[t >> 1];
-        const half2_t p0 = (h2b(kq_bytes_to_h2_biased(c0, KQ_SEL_B01)) - k1056) * s;
-        const half2_t p1 = (h2b(kq_bytes_to_h2_biased(c0, KQ_SEL_B23)) - k1056) * s;
-        const half2_t p2 = (h2b(kq_bytes_to_h2_biased(c1, KQ_SEL_B01)) - k1056) * s;
-        const half2_t p3 = (h2b(kq_bytes_to_h2_biased(c1, KQ_SEL_B23)) - k1056) * s;
-        return half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+        const half2_t s = dsc[t];
+        return cat8((b.p0 - k1056) * s, (b.p1 - k1056) * s, (b.p2 - k1056) * s, (b.p3 - k1056) * s);
     }
 };
 
-// IQ2_XXS: 66 B = d + 8 groups x (4 grid indices, u32 signs|scale).
+// IQ2_XXS (66 B = d + 8 groups of 8 B: 4 grid indices, u32 signs|scale).
+// Step t = group t; lane group g takes grid index byte g (values 8g .. 8g+7)
+// and the group's sign / scale dword.  The grid and sign tables are read
+// from LDS.
 template <>
 struct Block<KQ_CODEC_IQ2_XXS> {
-    u32x4 raw[4];         // bytes 2..65 (the 8 groups)
+    u32x4 raw[4];  // bytes 2..65 (the 8 groups)
     uint32_t dbits;
     half2_t db[8];
 
-    __device__ __forceinline__ void load(const uint8_t *blk) {
-        const u32x4_a2 *p = (const u32x4_a2 *)(blk + 2);
+    __device__ __forceinline__ void load(const uint8_t *blk, int g) {
+        (void)g;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const u32x4_a2 v = p[i];
+            const u32x4_a2 v = *(const u32x4_a2 *)(blk + 2 + 16 * i);
             raw[i] = u32x4{v.x, v.y, v.z, v.w};
         }
         dbits = (uint32_t)*(const uint16_t *)blk;
     }
-    __device__ __forceinline__ void prep(bool valid) {
-        const float d = valid ? kq_f16_bits_to_f32(dbits) : 0.f;
-        const uint32_t *g = (const uint32_t *)&raw[0];
+    __device__ __forceinline__ void prep(int g) {
+        (void)g;
+        const float d = kq_f16_bits_to_f32(dbits);
+        const uint32_t *w = (const uint32_t *)&raw[0];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float v = d * (0.5f + (float)(g[2 * i + 1] >> 28)) * 0.25f;
-            db[i] = bcast((_Float16)v);
+        for (int t = 0; t < 8; ++t) {
+            const float v = d * (0.5f + (float)(w[2 * t + 1] >> 28)) * 0.25f;
+            db[t] = bcast((_Float16)v);
         }
     }
-    __device__ __forceinline__ half8_t frag(int t) const {
-        const int grp = t >> 2, l = t & 3;
-        const uint32_t *g = (const uint32_t *)&raw[0];
-        const uint32_t idx = (g[2 * grp] >> (8 * l)) & 0xFF;
-        const uint32_t s7 = (g[2 * grp + 1] >> (7 * l)) & 127u;
-        const u32x4 gm = *(const u32x4 *)kIq2.grid_h2[idx];
-        const u32x4 sm = *(const u32x4 *)kIq2.sign_x2[s7];
-        const half2_t s = db[grp];
-        const half2_t p0 = h2b(gm.x ^ sm.x) * s;
-        const half2_t p1 = h2b(gm.y ^ sm.y) * s;
-        const half2_t p2 = h2b(gm.z ^ sm.z) * s;
-        const half2_t p3 = h2b(gm.w ^ sm.w) * s;
-        return half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+    __device__ __forceinline__ half8_t frag(int t, int g, const Iq2Tables &tab) const {
+        const uint32_t *w = (const uint32_t *)&raw[0];
+        const uint32_t idx = (w[2 * t] >> (8 * g)) & 0xFF;
+        const uint32_t s7 = (w[2 * t + 1] >> (7 * g)) & 127u;
+        const u32x4 gm = *(const u32x4 *)tab.grid_h2[idx];
+        const u32x4 sm = *(const u32x4 *)tab.sign_x2[s7];
+        const half2_t s = db[t];
+        return cat8(h2b(gm.x ^ sm.x) * s, h2b(gm.y ^ sm.y) * s, h2b(gm.z ^ sm.z) * s, h2b(gm.w ^ sm.w) * s);
     }
 };
 
@@ -251,60 +276,95 @@ __device__ __forceinline__ half8_t load_x8(const char *p) {
     }
 }
 
-// Accumulate over super-blocks [kb_begin, kb_end) of NW weight matrices
-// (NW = 2: gate and up share the activations).  wrow[i] points at this
-// lane's weight row (row n0 + lane%16 of matrix i, clamped to a valid row by
-// the caller).  xrow[mt] points (as bytes) at this lane's activation row of
-// m-tile mt, clamped to a valid row: rows past M compute throw-away outputs
-// that are never stored, so no load is conditional.  Blocks past kb_end (the
-// last, partial 4-block step) are read from a clamped valid address and
-// zeroed through their scales.
+// One super-block's operands for a wave: NW weight blocks and the 8 MFMA
+// steps' activation fragments of MT m-tiles.
 template <int CODEC, int MT, int XT, int NW>
-__device__ __forceinline__ void tile_accumulate(const uint8_t *const (&wrow)[NW], int kb_begin,
-                                                int kb_end, const char *const (&xrow)[MT],
-                                                floatx4 (&acc)[NW][MT]) {
-    constexpr int XS = x_elem_bytes<XT>();
-    constexpr int BPB = kq_block_bytes(CODEC);
-    const int g = kq_lane() >> 4;
-    for (int kb = kb_begin; kb < kb_end; kb += 4) {
-        const int blk = kb + g;
-        const bool bvalid = blk < kb_end;
-        const int blk_c = bvalid ? blk : kb_end - 1;
-        Block<CODEC> wb[NW];
+struct Stage {
+    Block<CODEC> w[NW];
+    half8_t x[8][MT];
+
+    __device__ __forceinline__ void load(const uint8_t *const (&wrow)[NW], const char *const (&xrow)[MT], int kb,
+                                         int g) {
+        constexpr int XS = x_elem_bytes<XT>();
+        constexpr int BPB = kq_block_bytes(CODEC);
 #pragma unroll
-        for (int i = 0; i < NW; ++i) wb[i].load(wrow[i] + (int64_t)blk_c * BPB);
+        for (int i = 0; i < NW; ++i) w[i].load(wrow[i] + (int64_t)kb * BPB, g);
+        const int64_t xoff = ((int64_t)kb * KQ_QK + 8 * g) * XS;
 #pragma unroll
-        for (int i = 0; i < NW; ++i) wb[i].prep(bvalid);
-        const int64_t xoff = (int64_t)blk_c * KQ_QK * XS;
-        // Activation fragments are issued in chunks of TC MFMA steps (128
-        // VGPRs of fp16 operands) before any of them is consumed, so their
-        // L2 latency overlaps instead of stalling every MFMA.
-        constexpr int TC = 32 / MT;
+        for (int t = 0; t < 8; ++t)
 #pragma unroll
-        for (int t0 = 0; t0 < 32; t0 += TC) {
-            half8_t a[TC][MT];
+            for (int mt = 0; mt < MT; ++mt) x[t][mt] = load_x8<XT>(xrow[mt] + xoff + 32 * t * XS);
+    }
+
+    __device__ __forceinline__ void compute(floatx4 (&acc)[NW][MT], int g, const Iq2Tables &tab) {
 #pragma unroll
-            for (int tt = 0; tt < TC; ++tt)
+        for (int i = 0; i < NW; ++i) w[i].prep(g);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+#pragma unroll
+            for (int i = 0; i < NW; ++i) {
+                const half8_t b = w[i].frag(t, g, tab);
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt)
-                    a[tt][mt] = load_x8<XT>(xrow[mt] + xoff + 8 * (t0 + tt) * XS);
-            // keep the whole batch of loads ahead of the first consumer (the
-            // scheduler would otherwise sink each load next to its MFMA)
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int tt = 0; tt < TC; ++tt) {
-#pragma unroll
-                for (int i = 0; i < NW; ++i) {
-                    const half8_t b = wb[i].frag(t0 + tt);
-#pragma unroll
-                    for (int mt = 0; mt < MT; ++mt)
-                        acc[i][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tt][mt], b, acc[i][mt], 0, 0, 0);
-                }
+                    acc[i][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x[t][mt], b, acc[i][mt], 0, 0, 0);
             }
         }
-        // inside the loop: the accumulator copies at the loop exit must come
-        // after these wait states
-        kq_mfma_drain();
+    }
+};
+
+// Accumulate super-blocks kb_first, kb_first + kb_step, ... < kb_end of NW
+// weight matrices (NW = 2: gate and up share the activations).  wrow[i]
+// points at this lane's weight row (row n0 + lane%16 of matrix i, clamped to
+// a valid row by the caller).  xrow[mt] points (as bytes) at this lane's
+// activation row of m-tile mt, clamped to a valid row: rows past M compute
+// throw-away outputs that are never stored, so no load is conditional.  The
+// next block's loads are issued before the current block is multiplied
+// (register double buffer).
+template <int CODEC, int MT, int XT, int NW>
+__device__ __forceinline__ void tile_accumulate(const uint8_t *const (&wrow)[NW], int kb_first, int kb_step,
+                                                int kb_end, const char *const (&xrow)[MT],
+                                                floatx4 (&acc)[NW][MT], const Iq2Tables &tab) {
+    const int g = kq_lane() >> 4;
+    int kb = kb_first;
+    if (kb >= kb_end) return;
+    if constexpr (MT * NW > 2) {
+        // wide tiles: one stage (two would not fit the register file)
+        Stage<CODEC, MT, XT, NW> st;
+        for (;;) {
+            st.load(wrow, xrow, kb, g);
+            __builtin_amdgcn_sched_barrier(0);
+            st.compute(acc, g, tab);
+            kb += kb_step;
+            if (kb >= kb_end) {
+                kq_mfma_drain();
+                break;
+            }
+        }
+        return;
+    }
+    Stage<CODEC, MT, XT, NW> s0, s1;
+    s0.load(wrow, xrow, kb, g);
+    for (;;) {
+        const int k1 = kb + kb_step;
+        if (k1 < kb_end) s1.load(wrow, xrow, k1, g);
+        __builtin_amdgcn_sched_barrier(0);
+        s0.compute(acc, g, tab);
+        // at the exits: wait out the last MFMA's result latency inside the
+        // loop body, ahead of the accumulator copies the compiler places at
+        // the loop exit
+        if (k1 >= kb_end) {
+            kq_mfma_drain();
+            break;
+        }
+        const int k2 = k1 + kb_step;
+        if (k2 < kb_end) s0.load(wrow, xrow, k2, g);
+        __builtin_amdgcn_sched_barrier(0);
+        s1.compute(acc, g, tab);
+        if (k2 >= kb_end) {
+            kq_mfma_drain();
+            break;
+        }
+        kb = k2;
     }
 }
 

@@ -158,3 +158,58 @@ def test_module_forward():
     got = mod(_dev(x).reshape(3, 1, 512)).float().cpu().numpy().reshape(3, 128)
     ref = okq.qmm_ref(x, wire, "q4_k") + np.linspace(-1, 1, 128)
     assert okq.max_rel(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("codec,N,K,M", [
+    ("q4_k", 9000, 4096, 5),       # 563 tiles > persistent grid: several tiles per workgroup, odd count
+    ("q4_k", 777, 3328, 16),       # 13 blocks: partial last k-step, 4 waves
+    ("q6_k", 1040, 4096, 8),       # Q6_K persistent limit K = 4096
+    ("iq2_xxs", 520, 7168, 3),     # 28 blocks: 7 waves
+    ("q4_k", 64, 256, 1),          # single block, single wave
+])
+def test_persistent_path_shapes(codec, N, K, M, monkeypatch):
+    """The persistent small-batch path (M <= 16) and the general path both
+    match the fp64 reference on the same inputs."""
+    rng = np.random.default_rng(N + K + M)
+    if codec == "iq2_xxs":
+        wire = okq.random_valid_blocks(rng, codec, N * K // 256).reshape(N, -1)
+    else:
+        wire = quantized_weights(rng, codec, N, K)
+    x = fp16_rows(rng, M, K)
+    ref = okq.qmm_ref(x, wire, codec)
+    got = _mm(x, wire, codec).float().cpu().numpy()
+    assert okq.max_rel(got, ref) <= TOL, ("persistent, default grid", okq.max_rel(got, ref))
+    # a small persistent grid: every shape takes the persistent path, and each
+    # workgroup walks many tiles
+    monkeypatch.setenv("GMLX_KQ_QMV_WGS", "3")
+    got3 = _mm(x, wire, codec).float().cpu().numpy()
+    assert okq.max_rel(got3, ref) <= TOL, ("persistent, 3 workgroups", okq.max_rel(got3, ref))
+    monkeypatch.delenv("GMLX_KQ_QMV_WGS")
+    monkeypatch.setenv("GMLX_KQ_PERSISTENT", "0")
+    got0 = _mm(x, wire, codec).float().cpu().numpy()
+    assert okq.max_rel(got0, ref) <= TOL, ("general", okq.max_rel(got0, ref))
+
+
+def test_persistent_mixed_codec_group_and_determinism():
+    """q|k (Q4_K) and v (Q6_K) sharing x: one persistent launch per codec;
+    repeated calls are bitwise identical."""
+    from gmlx_amd import ops
+    rng = np.random.default_rng(21)
+    K = 4096
+    wq = quantized_weights(rng, "q4_k", 512, K)
+    wk = quantized_weights(rng, "q4_k", 128, K)
+    wv = quantized_weights(rng, "q6_k", 128, K)
+    x16 = fp16_rows(rng, 8, K)
+    x = _dev(x16)
+    import os
+    os.environ["GMLX_KQ_QMV_WGS"] = "4"
+    try:
+        outs = [ops.quantized_matmul_grouped([(x, _dev(wq), "q4_k"), (x, _dev(wk), "q4_k"), (x, _dev(wv), "q6_k")])
+                for _ in range(3)]
+    finally:
+        del os.environ["GMLX_KQ_QMV_WGS"]
+    for o in outs[1:]:
+        for a, b in zip(o, outs[0]):
+            assert np.array_equal(a.cpu().numpy().view(np.uint16), b.cpu().numpy().view(np.uint16))
+    for o, (w, c) in zip(outs[0], [(wq, "q4_k"), (wk, "q4_k"), (wv, "q6_k")]):
+        assert okq.max_rel(o.float().cpu().numpy(), okq.qmm_ref(x16, w, c)) <= TOL
