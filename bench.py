@@ -58,11 +58,9 @@ def wire_bytes(N, K, codec):
 
 
 def layer_bytes(B):
-    """Algorithmic bytes of one layer at B rows: weights + fp16 x in + fp16 y out."""
-    tot = 0
-    for _, N, K, codec in LAYER:
-        tot += wire_bytes(N, K, codec) + B * K * 2 + B * N * 2
-    return tot
+    """Algorithmic bytes of one layer at B rows: weights + fp16 x in (once per
+    launch) + fp16 y out."""
+    return sum(launch_bytes(launch, B) for launch, _ in LAUNCHES)
 
 
 # ------------------------------------------------------------------ weights
@@ -92,15 +90,49 @@ def make_inputs(torch, rng, B):
     return x, xd
 
 
-def step_fn(ops, stack, x, xd):
-    """One decode step of the linear stack: 4 launches per layer."""
+# The launches of one layer: (name, matrices).  At B <= 16 the gate|up launch
+# (1536 tiles) takes the persistent small-batch kernel and the other three the
+# general dense kernel; at B > 16 every launch takes the general kernel.
+LAUNCHES = [("qkv", ("q", "k", "v")), ("o", ("o",)), ("gate_up", ("gate", "up")), ("down", ("down",))]
+CODEC = {name: codec for name, _, _, codec in LAYER}
+DIMS = {name: (N, K) for name, N, K, _ in LAYER}
+
+
+def kernel_of(launch, B):
+    if B <= 16 and launch == "gate_up":
+        return "kq_qmv_persistent_kernel<12, 0>"
+    return f"kq_dense_grouped_kernel<{1 if B <= 16 else 2 if B <= 32 else 4}, 0>"
+
+
+def launch_bytes(launch, B):
+    """Algorithmic bytes of one launch: wire bytes + fp16 x in + fp16 y out."""
+    tot = 0
+    for m in dict(LAUNCHES)[launch]:
+        N, K = DIMS[m]
+        tot += wire_bytes(N, K, CODEC[m]) + B * N * 2
+    N, K = DIMS[dict(LAUNCHES)[launch][0]]
+    return tot + B * K * 2  # x read once per launch (shared by grouped problems)
+
+
+def run_launch(ops, L, launch, x, xd):
+    if launch == "qkv":
+        return ops.quantized_matmul_grouped([(x, L["q"], "q4_k"), (x, L["k"], "q4_k"), (x, L["v"], "q6_k")])
+    if launch == "o":
+        return [ops.quantized_matmul(x, L["o"], None, "q4_k")]
+    if launch == "gate_up":
+        return ops.quantized_matmul_grouped([(x, L["gate"], "q4_k"), (x, L["up"], "q4_k")])
+    return [ops.quantized_matmul(xd, L["down"], None, "q6_k")]
+
+
+def step_fn(ops, stack, x, xd, only=None):
+    """One decode step of the linear stack: 4 launches per layer (or only the
+    launches named in `only`)."""
     outs = []
     for L in stack:
-        q, k, v = ops.quantized_matmul_grouped([(x, L["q"], "q4_k"), (x, L["k"], "q4_k"), (x, L["v"], "q6_k")])
-        o = ops.quantized_matmul(x, L["o"], None, "q4_k")
-        g, u = ops.quantized_matmul_grouped([(x, L["gate"], "q4_k"), (x, L["up"], "q4_k")])
-        d = ops.quantized_matmul(xd, L["down"], None, "q6_k")
-        outs = [q, k, v, o, g, u, d]
+        outs = []
+        for launch, _ in LAUNCHES:
+            if only is None or launch in only:
+                outs += run_launch(ops, L, launch, x, xd)
     return outs
 
 
@@ -219,6 +251,76 @@ def cpu_baseline(layer_wires, B, budget_s=12.0):
                       f"{el:.1f} s, oracle/kq_oracle.c kqo_qmm_f32 (OpenMP, fp32)"}
 
 
+# ------------------------------------------------------------ HBM traffic
+
+COPY_BYTES = 256 << 20
+
+
+def pmc_pass(args):
+    """Body of one rocprofv3 --pmc child run: a few steps of the same
+    launches over a 4-layer stack, then one plain 256 MiB device copy whose
+    counter value calibrates the counter."""
+    import torch
+    from gmlx_amd import ops
+    stack, rng = make_stack(torch, ops, 4)
+    x, xd = make_inputs(torch, rng, args.batch)
+    for _ in range(3):
+        step_fn(ops, stack, x, xd)
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print("pmc pass done", flush=True)
+
+
+def measure_traffic(batch, timeout=240):
+    """HBM bytes per launch of each kernel from two rocprofv3 --pmc runs
+    (FETCH_SIZE, WRITE_SIZE; KiB per dispatch), each scaled by what the same
+    counter reads for the 256 MiB copy.  Runs before this process touches
+    the GPU.  Returns {kernel: {"fetch": B, "write": B}} or None."""
+    import csv
+    import glob
+    import shutil
+    import subprocess
+    import tempfile
+    if shutil.which("rocprofv3") is None:
+        return None
+    out = {}
+    for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = tempfile.mkdtemp(prefix="kq_pmc_")
+        cmd = ["rocprofv3", "--pmc", ctr, "--output-format", "csv", "-d", d, "-o", "pmc", "--",
+               sys.executable, os.path.abspath(__file__), "--pmc-pass", "--batch", str(batch)]
+        try:
+            r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout)
+        except subprocess.TimeoutExpired:
+            shutil.rmtree(d, ignore_errors=True)
+            return None
+        files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+        if r.returncode != 0 or not files:
+            shutil.rmtree(d, ignore_errors=True)
+            return None
+        per = {}
+        copy_kib = []
+        for row in csv.DictReader(open(files[0])):
+            name, v = row.get("Kernel_Name", ""), float(row["Counter_Value"])
+            if "copyBuffer" in name or "copy" in name.lower() and int(row.get("Grid_Size", "0")) >= COPY_BYTES // 64:
+                copy_kib.append(v)
+            for k in ("kq_qmv_persistent_kernel", "kq_dense_grouped_kernel"):
+                if k in name:
+                    per.setdefault(k, []).append(v)
+        shutil.rmtree(d, ignore_errors=True)
+        if not copy_kib:
+            return None
+        # the copy reads and writes COPY_BYTES once each
+        scale = COPY_BYTES / (max(copy_kib) * 1024.0)
+        for k, vals in per.items():
+            out.setdefault(k, {})["fetch" if ctr == "FETCH_SIZE" else "write"] = \
+                sum(vals) / len(vals) * 1024.0 * scale
+            out[k]["scale_" + ctr.lower()] = round(scale, 4)
+    return out
+
+
 # --------------------------------------------------------------------- main
 
 def main():
@@ -231,12 +333,22 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-sdpa", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 --pmc passes")
+    ap.add_argument("--pmc-pass", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.pmc_pass:
+        return pmc_pass(args)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
+
+    # HBM traffic counters come from child processes started before this
+    # process touches the GPU
+    traffic = None if args.no_traffic else measure_traffic(args.batch)
+    if traffic is not None:
+        log(f"[bench] pmc traffic per launch: { {k: {kk: round(vv) for kk, vv in v.items()} for k, v in traffic.items()} }")
 
     import torch
     from gmlx_amd import ops
@@ -265,6 +377,24 @@ def main():
     value = step_bytes / ms / 1e6
     launches = 4 * args.layers
     log(f"[bench] B={B}: {ms:.3f} ms/step, {value:.1f} GB/s")
+    del g
+
+    # per-kernel launch durations: each kernel's launches of the step, alone
+    # in a graph, timed with HIP events on the replay stream
+    kernels = {}
+    for launch, _ in LAUNCHES:
+        kernels.setdefault(kernel_of(launch, B), []).append(launch)
+    per_kernel = {}
+    for kname, lset in kernels.items():
+        gk, _ = capture(torch, lambda: step_fn(ops, stack, x, xd, only=set(lset)))
+        msk = time_graph(torch, gk, args.steps, args.warmup)
+        n = args.layers * len(lset)
+        byts = args.layers * sum(launch_bytes(l, B) for l in lset)
+        per_kernel[kname] = {"launches": lset, "launches_per_step": n, "avg_launch_us": round(msk * 1e3 / n, 3),
+                             "bytes_per_launch": byts // n, "gbs": round(byts / msk / 1e6, 1)}
+        log(f"[bench] {kname} ({'+'.join(lset)}): {msk * 1e3 / n:.2f} us/launch, {byts / msk / 1e6:.1f} GB/s")
+        del gk
+    dominant = max(per_kernel, key=lambda k: per_kernel[k]["avg_launch_us"] * per_kernel[k]["launches_per_step"])
 
     per_batch = {}
     if not args.no_sweep:
@@ -290,7 +420,13 @@ def main():
         cpu = cpu_baseline({k: v.cpu().numpy() for k, v in stack[0].items()}, B)
         log(f"[bench] cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads")
 
-    achieved = (step_bytes / launches) / (ms / launches) / 1e6
+    dk = per_kernel[dominant]
+    achieved = dk["bytes_per_launch"] / dk["avg_launch_us"] / 1e3
+    tr = None
+    if traffic is not None:
+        base = dominant.split("<")[0]
+        if base in traffic and "fetch" in traffic[base] and "write" in traffic[base]:
+            tr = round(traffic[base]["fetch"] + traffic[base]["write"])
     res = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -309,9 +445,13 @@ def main():
                    "batch": B, "layers": args.layers, "hidden": HIDDEN, "intermediate": INTER,
                    "weights_per_step_bytes": args.layers * sum(wire_bytes(N, K, c) for _, N, K, c in LAYER),
                    "launches_per_step": launches, "graph_replay_equals_eager": replay_ok},
-        "roofline": {"bound": "hbm", "kernel": "kq_dense_grouped_kernel",
+        "roofline": {"bound": "hbm", "kernel": dominant,
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": tr,
+                     "algorithmic_bytes_per_launch": dk["bytes_per_launch"],
+                     "avg_launch_us": dk["avg_launch_us"]},
+        "kernels": per_kernel,
+        "traffic_per_launch": traffic,
         "cpu_baseline": cpu,
         "per_batch": per_batch,
         "sdpa": sdpa,

@@ -99,19 +99,23 @@ typedef struct {
     int32_t codec;
 } kq_matmul_problem;
 
-/* Workspace bytes kq_quantized_matmul_grouped needs for these problems
- * (split-K partials + arrival counters).  The workspace must be zero-filled
- * once when allocated; calls leave it zeroed.  Calls that share a workspace
- * must be ordered (same stream). */
+/* Workspace bytes kq_quantized_matmul_grouped needs for these problems.
+ * This build reduces K splits inside a workgroup and returns 0; the
+ * workspace arguments stay in the signature so a later split-K plan can use
+ * them without an ABI change (pass NULL / 0). */
 size_t kq_matmul_workspace_bytes(const kq_matmul_problem *problems, int n_problems);
 
 /* kq.quantized_matmul(x, w, scales, codec, transpose=True) -- the
  * KQuantLinear forward (gmlx/modules.py:1535-1539; direct calls at
  * gmlx/occupancy_fuse.py:162-165, 224-227, 290-293, 312-315).  Up to
  * KQ_MAX_GROUP independent problems (any codec mix, shared x_dtype/y_dtype)
- * run in ONE launch: the row-concatenated q|k|v and gate|up wires of
+ * run in one call: the row-concatenated q|k|v and gate|up wires of
  * gmlx/occupancy_fuse.py:141-344 become one call without concatenating
- * bytes.  x_dtype: f16 or bf16.  y_dtype: f16, bf16 or f32. */
+ * bytes.  The call is one launch, except that problems sharing x with
+ * M <= 16 and enough rows for every workgroup to walk several 16-row tiles
+ * take one persistent launch per codec.  x_dtype: f16 or bf16.
+ * y_dtype: f16, bf16 or f32.  Results do not depend on scheduling: repeated
+ * calls on the same inputs are bitwise identical. */
 #define KQ_MAX_GROUP 8
 int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problems,
                                 int x_dtype, int y_dtype, void *workspace,
@@ -168,7 +172,11 @@ int kq_moe_router_topk(const void *logits, int logits_dtype, int32_t T, int32_t 
                        int norm_topk_prob, int32_t *inds, float *scores, kq_stream_t stream);
 
 /* ---- ragged GQA decode attention ----------------------------------------- */
-/* ragged_decode_attention(q, k, v, pads, scale) (gmlx/qwen35_attn.py:395-493)
+/* Workspace of kq_sdpa_decode_ragged: fp32 split partials (O, m, l) for
+ * B * Hkv * ceil(max_len / split) splits; no zero-fill needed.  Calls that
+ * share a workspace must be ordered (same stream).
+ *
+ * ragged_decode_attention(q, k, v, pads, scale) (gmlx/qwen35_attn.py:395-493)
  * and kq.sdpa_decode_gqa(q, k, v, scale, starts=) (gmlx/gemma4_batched_sdpa.py:
  * 210-226), one query token per row:
  *   out[b, hq, :] = softmax(scale * q[b, hq] . K_b,h^T) . V_b,h,  h = hq / (Hq/Hkv)
