@@ -91,17 +91,23 @@ def make_inputs(torch, rng, B):
 
 
 # The launches of one layer: (name, matrices).  At B <= 16 the gate|up launch
-# (1536 tiles) takes the persistent small-batch kernel and the other three the
-# general dense kernel; at B > 16 every launch takes the general kernel.
+# (1536 tiles, six per CU) takes the LDS-staged persistent small-batch kernel
+# and the other three (one tile per CU or less, or K = 12288 Q6_K) the general
+# dense kernel; at B > 16 every launch takes the general kernel.
 LAUNCHES = [("qkv", ("q", "k", "v")), ("o", ("o",)), ("gate_up", ("gate", "up")), ("down", ("down",))]
 CODEC = {name: codec for name, _, _, codec in LAYER}
 DIMS = {name: (N, K) for name, N, K, _ in LAYER}
+# kernel families, as rocprofv3 names them (template arguments: codec / m-tiles,
+# activation type, blocks per wave / waves)
+KERNEL_FAMILIES = ("kq_mv_kernel", "kq_qmv_persistent_kernel", "kq_dense_grouped_kernel")
 
 
 def kernel_of(launch, B):
     if B <= 16 and launch == "gate_up":
-        return "kq_qmv_persistent_kernel<12, 0>"
-    return f"kq_dense_grouped_kernel<{1 if B <= 16 else 2 if B <= 32 else 4}, 0>"
+        return "kq_mv_kernel<12, 0, 1>"
+    if B <= 16:
+        return "kq_dense_grouped_kernel<1, 0, 16>"
+    return f"kq_dense_grouped_kernel<{2 if B <= 32 else 4}, 0, 4>"
 
 
 def launch_bytes(launch, B):
@@ -306,7 +312,7 @@ def measure_traffic(batch, timeout=240):
             name, v = row.get("Kernel_Name", ""), float(row["Counter_Value"])
             if "copyBuffer" in name or "copy" in name.lower() and int(row.get("Grid_Size", "0")) >= COPY_BYTES // 64:
                 copy_kib.append(v)
-            for k in ("kq_qmv_persistent_kernel", "kq_dense_grouped_kernel"):
+            for k in KERNEL_FAMILIES:
                 if k in name:
                     per.setdefault(k, []).append(v)
         shutil.rmtree(d, ignore_errors=True)
@@ -395,6 +401,16 @@ def main():
         log(f"[bench] {kname} ({'+'.join(lset)}): {msk * 1e3 / n:.2f} us/launch, {byts / msk / 1e6:.1f} GB/s")
         del gk
     dominant = max(per_kernel, key=lambda k: per_kernel[k]["avg_launch_us"] * per_kernel[k]["launches_per_step"])
+    # and each launch of a layer alone
+    per_launch = {}
+    for launch, _ in LAUNCHES:
+        gl, _ = capture(torch, lambda: step_fn(ops, stack, x, xd, only={launch}))
+        msl = time_graph(torch, gl, args.steps, args.warmup)
+        byts = args.layers * launch_bytes(launch, B)
+        per_launch[launch] = {"kernel": kernel_of(launch, B), "avg_us": round(msl * 1e3 / args.layers, 3),
+                              "bytes": launch_bytes(launch, B), "gbs": round(byts / msl / 1e6, 1)}
+        log(f"[bench]   {launch}: {msl * 1e3 / args.layers:.2f} us, {byts / msl / 1e6:.1f} GB/s")
+        del gl
 
     per_batch = {}
     if not args.no_sweep:
@@ -451,6 +467,7 @@ def main():
                      "algorithmic_bytes_per_launch": dk["bytes_per_launch"],
                      "avg_launch_us": dk["avg_launch_us"]},
         "kernels": per_kernel,
+        "launches": per_launch,
         "traffic_per_launch": traffic,
         "cpu_baseline": cpu,
         "per_batch": per_batch,

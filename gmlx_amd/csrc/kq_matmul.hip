@@ -2,22 +2,30 @@
 // kq.quantized_matmul) and the MoE expert gather family (kq.gather_qmm,
 // kq.moe_glu_gather_kq, kq.gather_qmv_kq, mix, router top-k).
 //
-// Dense work decomposition: one 256-thread workgroup per (problem, 16-row
-// weight tile, 64-row batch chunk).  The 4 waves of a workgroup split the
-// tile's K range (wave w takes 4-block steps w, w+4, ...), each wave keeps
-// its own MFMA accumulators, and the workgroup sums them through LDS in wave
-// order.  The reduction never leaves the workgroup, so there are no global
-// partials, counters or device-scope fences, and the result does not depend
-// on scheduling.
+// Dense work decomposition: one workgroup per (problem, 16-row weight tile,
+// 64-row batch chunk).  The WV waves of a workgroup split the tile's K range
+// (wave w takes super-blocks w, w+WV, ...), each wave keeps its own MFMA
+// accumulators, and the workgroup sums them through LDS in wave order.  The
+// reduction never leaves the workgroup, so there are no global partials,
+// counters or device-scope fences, and the result does not depend on
+// scheduling.  Small batches (one 16-row m-tile) use 16 waves per tile: each
+// wave then holds one or a few blocks and little register state, and the many
+// resident waves hide the memory latency behind the dequant work; wider batch
+// chunks use 4 waves with more m-tiles each.
 #include <stdlib.h>
 
 #include "kq_mma.h"
 
+// kq_mv.hip: LDS-staged small-batch launch (problems validated, all live,
+// one codec, sharing x / M <= 16, x rows fitting in LDS).
+bool kq_mv_eligible(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype);
+int kq_mv_launch(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype, hipStream_t s);
 // kq_qmv.hip: persistent small-batch launch (problems validated, all live,
 // sharing codec / x / M <= 16 / K <= 8192).
 int kq_qmv_persistent_launch(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype, hipStream_t s);
 // workgroups one persistent launch of this problem's codec / K would use
 int kq_qmv_persistent_grid(const kq_matmul_problem &q);
+int device_cus();
 
 namespace {
 
@@ -25,7 +33,6 @@ using namespace kqmma;
 
 constexpr int kMaxChunk = 64;  // batch rows per grid.y chunk (4 m-tiles)
 
-constexpr int kWaves = 4;      // waves per dense workgroup (K split)
 
 struct DenseProblem {
     const uint8_t *w;
@@ -54,8 +61,8 @@ __device__ __forceinline__ void store_tile(void *y, int y_dtype, int64_t y_strid
     }
 }
 
-// Wave `wave` of the workgroup takes super-blocks wave, wave + kWaves, ...
-template <int CODEC, int MT, int XT>
+// Wave `wave` of the workgroup takes super-blocks wave, wave + WV, ...
+template <int CODEC, int MT, int XT, int WV>
 __device__ __forceinline__ void dense_tile(const DenseProblem &p, int nt, int wave, floatx4 (&acc)[MT],
                                            const Iq2Tables &tab) {
     const int lane = kq_lane();
@@ -64,23 +71,18 @@ __device__ __forceinline__ void dense_tile(const DenseProblem &p, int nt, int wa
     const int n = min(nt * 16 + r, p.N - 1);
     const int nb = p.K / KQ_QK;
     const uint8_t *wrow[1] = {p.w + (int64_t)n * p.w_row_bytes};
-    const char *xrow[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-        const int m = min(m0 + 16 * mt + r, p.M - 1);
-        xrow[mt] = p.x + (int64_t)m * p.x_stride * x_elem_bytes<XT>();
-    }
+    const XRowsBuf<MT> xrow = x_rows_buf<MT, XT>(p.x, p.x_stride, p.M, p.K, m0, r);
     floatx4 a1[1][MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) a1[0][mt] = floatx4{0, 0, 0, 0};
-    tile_accumulate<CODEC, MT, XT, 1>(wrow, wave, kWaves, nb, xrow, a1, tab);
+    tile_accumulate<CODEC, MT, XT, 1, XRowsBuf<MT>, (WV < 16)>(wrow, wave, WV, nb, xrow, a1, tab);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = a1[0][mt];
 }
 
-template <int MT, int XT>
-__global__ __launch_bounds__(64 * kWaves) void kq_dense_grouped_kernel(DenseArgs a) {
-    __shared__ floatx4 red[kWaves - 1][MT][64];
+template <int MT, int XT, int WV>
+__global__ __launch_bounds__(64 * WV) void kq_dense_grouped_kernel(DenseArgs a) {
+    __shared__ floatx4 red[WV - 1][MT][64];
     __shared__ Iq2Tables iq2_tab;
     const int unit = blockIdx.x;
     // Select the problem with static indices only: dynamic indexing of the
@@ -90,17 +92,17 @@ __global__ __launch_bounds__(64 * kWaves) void kq_dense_grouped_kernel(DenseArgs
     for (int i = 1; i < KQ_MAX_GROUP; ++i)
         if (i < a.n_problems && unit >= a.p[i].unit_begin) p = a.p[i];
     const int nt = unit - p.unit_begin;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lane = kq_lane();
     const int m0 = blockIdx.y * kMaxChunk;
     if (m0 >= p.M) return;  // uniform over the workgroup
     floatx4 acc[MT];
     switch (p.codec) {
-    case KQ_CODEC_Q4_K: dense_tile<KQ_CODEC_Q4_K, MT, XT>(p, nt, wave, acc, iq2_tab); break;
-    case KQ_CODEC_Q6_K: dense_tile<KQ_CODEC_Q6_K, MT, XT>(p, nt, wave, acc, iq2_tab); break;
+    case KQ_CODEC_Q4_K: dense_tile<KQ_CODEC_Q4_K, MT, XT, WV>(p, nt, wave, acc, iq2_tab); break;
+    case KQ_CODEC_Q6_K: dense_tile<KQ_CODEC_Q6_K, MT, XT, WV>(p, nt, wave, acc, iq2_tab); break;
     default:
         load_iq2_tables(iq2_tab);
-        dense_tile<KQ_CODEC_IQ2_XXS, MT, XT>(p, nt, wave, acc, iq2_tab);
+        dense_tile<KQ_CODEC_IQ2_XXS, MT, XT, WV>(p, nt, wave, acc, iq2_tab);
         break;
     }
     if (wave > 0) {
@@ -110,7 +112,7 @@ __global__ __launch_bounds__(64 * kWaves) void kq_dense_grouped_kernel(DenseArgs
     __syncthreads();
     if (wave != 0) return;
 #pragma unroll
-    for (int w = 0; w < kWaves - 1; ++w)
+    for (int w = 0; w < WV - 1; ++w)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[mt] += red[w][mt][lane];
     const int n = nt * 16 + (lane & 15);
@@ -161,11 +163,11 @@ __global__ __launch_bounds__(64) void kq_gather_kernel(GatherArgs a) {
     if constexpr (NW == 2)
         wrow[1] = a.w1 + (int64_t)expert * a.w_expert_bytes + (int64_t)nc * a.w_row_bytes;
     for (int c0 = seg_begin; c0 < seg_end; c0 += 16 * MT) {
-        const char *xrow[MT];
+        XRowPtrs<MT> xrow;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
             const int ri = min(c0 + 16 * mt + r, seg_end - 1);
-            xrow[mt] = a.x + (int64_t)(a.pair_order[ri] / a.x_pair_div) * a.x_stride * x_elem_bytes<XT>();
+            xrow.row[mt] = a.x + (int64_t)(a.pair_order[ri] / a.x_pair_div) * a.x_stride * x_elem_bytes<XT>();
         }
         floatx4 acc[NW][MT];
 #pragma unroll
@@ -346,6 +348,8 @@ int validate_problem(const kq_matmul_problem &q) {
     const int64_t need = (int64_t)(q.K / KQ_QK) * kq_block_bytes(q.codec);
     if (q.w_row_bytes < need) return KQ_ERR_BAD_SHAPE;
     if (q.x_row_stride < q.K || q.y_row_stride < q.N) return KQ_ERR_BAD_SHAPE;
+    // activation rows are addressed with 32-bit byte offsets inside a 64-row chunk
+    if (q.x_row_stride > (1 << 22)) return KQ_ERR_BAD_SHAPE;
     if (((uintptr_t)q.x & 15) || (q.x_row_stride & 7)) return KQ_ERR_BAD_ALIGN;
     if (q.codec == KQ_CODEC_Q4_K && (((uintptr_t)q.w & 15) || (q.w_row_bytes & 15))) return KQ_ERR_BAD_ALIGN;
     if (((uintptr_t)q.w & 1) || (q.w_row_bytes & 1)) return KQ_ERR_BAD_ALIGN;
@@ -370,6 +374,14 @@ int env_flag(const char *name, int dflt) {
     return !(s[0] == '0' && s[1] == 0);
 }
 
+// "0" -> 0, "2" -> 2, anything else set -> 1, unset -> dflt
+int env_int_flag(const char *name, int dflt) {
+    const char *s = getenv(name);
+    if (!s || !*s) return dflt;
+    if (s[1] == 0 && (s[0] == '0' || s[0] == '2')) return s[0] - '0';
+    return 1;
+}
+
 // The persistent small-batch path (kq_qmv.hip) serves a set of problems that
 // share one codec, x, x stride, M <= 16 and K <= 8192 (Q6_K: K <= 4096).
 bool qmv_eligible(const kq_matmul_problem *ps, const int *idx, int n) {
@@ -384,9 +396,11 @@ bool qmv_eligible(const kq_matmul_problem *ps, const int *idx, int n) {
     return true;
 }
 
+// 16 waves per tile for one m-tile, 4 waves for wider chunks
 template <int MT, int XT>
 void launch_dense(const DenseArgs &a, int units, int chunks, hipStream_t s) {
-    hipLaunchKernelGGL((kq_dense_grouped_kernel<MT, XT>), dim3(units, chunks), dim3(64 * kWaves), 0, s, a);
+    constexpr int WV = MT == 1 ? 16 : 4;
+    hipLaunchKernelGGL((kq_dense_grouped_kernel<MT, XT, WV>), dim3(units, chunks), dim3(64 * WV), 0, s, a);
 }
 
 template <int CODEC, int XT, int NW>
@@ -491,18 +505,47 @@ int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problem
         const int rc = validate_problem(problems[i]);
         if (rc != KQ_OK) return rc;
     }
-    // small batches: one persistent launch per codec when every codec's
-    // problems share their activations (q|k|v, gate|up of one layer)
-    if (env_flag("GMLX_KQ_PERSISTENT", 1)) {
-        int by_codec[3][KQ_MAX_GROUP], cnt[3] = {0, 0, 0};
+    // live problems by codec (the small-batch paths launch once per codec)
+    int by_codec[3][KQ_MAX_GROUP], cnt[3] = {0, 0, 0};
+    int live = 0;
+    {
         const int codecs[3] = {KQ_CODEC_Q4_K, KQ_CODEC_Q6_K, KQ_CODEC_IQ2_XXS};
-        int live = 0;
         for (int i = 0; i < n_problems; ++i) {
             if (problems[i].M == 0 || problems[i].N == 0) continue;
             ++live;
             for (int c = 0; c < 3; ++c)
                 if (problems[i].codec == codecs[c]) by_codec[c][cnt[c]++] = i;
         }
+    }
+    // small batches with activations that fit in LDS: one LDS-staged launch per
+    // codec when every codec's problems share their activations.  Staging x
+    // pays when every workgroup walks several tiles (GMLX_KQ_MV=2 forces the
+    // path for any tile count).
+    const int mv_mode = env_int_flag("GMLX_KQ_MV", 1);
+    if (live > 0 && mv_mode) {
+        bool ok = true;
+        kq_matmul_problem sub[3][KQ_MAX_GROUP];
+        for (int c = 0; c < 3 && ok; ++c) {
+            if (!cnt[c]) continue;
+            int tiles = 0;
+            for (int i = 0; i < cnt[c]; ++i) {
+                sub[c][i] = problems[by_codec[c][i]];
+                tiles += (sub[c][i].N + 15) / 16;
+            }
+            ok = kq_mv_eligible(sub[c], cnt[c], x_dtype, y_dtype) && (mv_mode == 2 || tiles >= 4 * device_cus());
+        }
+        if (ok) {
+            for (int c = 0; c < 3; ++c) {
+                if (!cnt[c]) continue;
+                const int rc = kq_mv_launch(sub[c], cnt[c], x_dtype, y_dtype, (hipStream_t)stream);
+                if (rc != KQ_OK) return rc;
+            }
+            return KQ_OK;
+        }
+    }
+    // small batches: one persistent launch per codec when every codec's
+    // problems share their activations (q|k|v, gate|up of one layer)
+    if (env_flag("GMLX_KQ_PERSISTENT", 1)) {
         bool ok = live > 0;
         for (int c = 0; c < 3 && ok; ++c)
             if (cnt[c] && !qmv_eligible(problems, by_codec[c], cnt[c])) ok = false;

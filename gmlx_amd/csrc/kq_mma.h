@@ -4,22 +4,20 @@
 // super-blocks with v_mfma_f32_16x16x32_f16 (A = activations, B = weights^T).
 // Lane l = 16*g + r: r selects the weight row (B column) and the activation
 // row (A row) the lane feeds; g selects which 8 of the MFMA's 32 k values.
-// One MFMA covers 32 consecutive values of ONE super-block (MFMA step t of a
-// block = values 32t .. 32t+31; lane group g holds 32t + 8g .. +7), so:
-//   - an activation fragment is 16 contiguous bytes and the 4 lane groups of
-//     one activation row read 64 contiguous bytes (one cache line);
-//   - a lane reads only the quant bytes of its 8-value slices (Q4_K: 4 x 8 B
-//     of qs per block) plus the block's scale header, which the 4 lanes of a
-//     row share.
-// Every weight fragment is fully scaled before the MFMA (w = dequant(q) in
-// fp16), so the accumulator needs no per-block factor.
+// One super-block takes 8 MFMA steps t = 0..7; step t covers the 32 values
+// 32t .. 32t+31 of the block and lane group g feeds values 32t + 8g .. +7
+// (Block<>::x_elem).  The activation fragment of a step is the 8 activations at
+// the same value indices, so the 4 lane groups of one activation row read one
+// contiguous 64-byte run.  Every weight fragment is fully scaled before the
+// MFMA (w = dequant(q) in fp16), so the accumulator needs no per-block factor.
 //
 // Dequant to fp16 in registers, per pair of values:
-//   Q4_K : h = perm(0x64.., nibbles)  (= 1024+q, exact)
-//          w = fma(h - 1024, dsc, -dm)          single rounding
-//   Q6_K : w = (h - 1056) * dsc                 single rounding (q-32 exact)
-//   IQ2  : w = (grid ^ signmask) * db           single rounding
-// dsc / dm / db are the fp32 sub-block scales rounded once to fp16.
+//   Q4_K : q = cvt_fp8(nibble byte) exact integer, w = fma(q, dsc, -dm)
+//   Q6_K : h = perm(0x64.., 6-bit byte) (= 1024+q), w = (h - 1056) * dsc
+//   IQ2  : w = (grid ^ signmask) * db
+// each with a single rounding; dsc / dm / db are the sub-block scales rounded
+// once to fp16 (Q4_K: the fp16 product d * sc of an fp16 d and an exact
+// integer sc, the same value as rounding the exact fp32 product).
 #pragma once
 #include "kq_common.h"
 #include "kq_tables.h"
@@ -90,14 +88,22 @@ template <int CODEC>
 struct Block;
 
 // Q4_K (144 B = d, dmin, 12 B packed scales, 128 B qs; 16-B aligned).
-// Step t = sub-block t: chunk c = t/2 (qs bytes 32c .. 32c+31), low nibbles
-// for even t, high for odd t; lane group g takes bytes 32c + 8g .. +7.
+// Step t = sub-block t: qs chunk c = t/2 (bytes 32c .. 32c+31), low nibbles for
+// even t, high for odd t; lane group g takes bytes 32c + 8g .. +7.
+// The 8 six-bit scales and mins are unpacked four at a time as bytes:
+//   sub-blocks 0..3: sc = s[j] & 63,                    m = s[j+4] & 63
+//   sub-blocks 4..7: sc = s[j+4] & 15 | (s[j-4] >> 6) << 4,
+//                    m  = s[j+4] >> 4 | (s[j] >> 6) << 4
+// then turned into fp16 through the 1024-bias (exact) and multiplied by d / dmin.
+// A nibble byte q <= 15 read as fp8 E4M3 is q * 2^-9; the converter's scale 2^9
+// (a power of two, the only part of the scale it applies) returns q exactly.
 template <>
 struct Block<KQ_CODEC_Q4_K> {
     u32x4 hdr;
     u32x2 q[4];
-    half2_t dsc[8], ndm[8];
+    half2_t dsc[4], ndm[4];  // [i] = sub-blocks 2i, 2i+1
 
+    __device__ static constexpr int x_elem(int t, int g) { return 32 * t + 8 * g; }
     __device__ __forceinline__ void load(const uint8_t *blk, int g) {
         hdr = *(const u32x4 *)blk;
 #pragma unroll
@@ -105,24 +111,19 @@ struct Block<KQ_CODEC_Q4_K> {
     }
     __device__ __forceinline__ void prep(int g) {
         (void)g;
-        const float d = kq_f16_bits_to_f32(hdr.x & 0xFFFF);
-        const float dmin = kq_f16_bits_to_f32(hdr.x >> 16);
-        const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;  // scales bytes 0..11
+        const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;  // scale bytes 0..3, 4..7, 8..11
+        const uint32_t sc_lo = s0 & 0x3F3F3F3Fu, m_lo = s1 & 0x3F3F3F3Fu;
+        const uint32_t sc_hi = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
+        const uint32_t m_hi = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
+        const half2_t k1024 = {(_Float16)1024.f, (_Float16)1024.f};
+        const half2_t dd = h2b(hdr.x);  // (d, dmin)
+        const half2_t d2 = bcast(dd.x), nm2 = bcast(-dd.y);
+        const uint32_t scw[2] = {sc_lo, sc_hi}, mw[2] = {m_lo, m_hi};
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            uint32_t sc, mn;
-            if (j < 4) {
-                sc = (s0 >> (8 * j)) & 63;
-                mn = (s1 >> (8 * j)) & 63;
-            } else {
-                const uint32_t bj4 = (s2 >> (8 * (j - 4))) & 0xFF;   // s[j+4]
-                const uint32_t bjm4 = (s0 >> (8 * (j - 4))) & 0xFF;  // s[j-4]
-                const uint32_t bj = (s1 >> (8 * (j - 4))) & 0xFF;    // s[j]
-                sc = (bj4 & 0xF) | ((bjm4 >> 6) << 4);
-                mn = (bj4 >> 4) | ((bj >> 6) << 4);
-            }
-            dsc[j] = bcast((_Float16)(d * (float)sc));
-            ndm[j] = bcast((_Float16)(-(dmin * (float)mn)));
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t sel = (i & 1) ? KQ_SEL_B23 : KQ_SEL_B01;
+            dsc[i] = (h2b(__builtin_amdgcn_perm(0x64646464u, scw[i >> 1], sel)) - k1024) * d2;
+            ndm[i] = (h2b(__builtin_amdgcn_perm(0x64646464u, mw[i >> 1], sel)) - k1024) * nm2;
         }
     }
     __device__ __forceinline__ half8_t frag(int t, int g, const Iq2Tables &) const {
@@ -132,12 +133,16 @@ struct Block<KQ_CODEC_Q4_K> {
             w0 >>= 4;
             w1 >>= 4;
         }
-        const Bias8 h(w0 & 0x0F0F0F0Fu, w1 & 0x0F0F0F0Fu);
-        const half2_t k1024 = {(_Float16)1024.f, (_Float16)1024.f};
-        return cat8(__builtin_elementwise_fma(h.p0 - k1024, dsc[t], ndm[t]),
-                    __builtin_elementwise_fma(h.p1 - k1024, dsc[t], ndm[t]),
-                    __builtin_elementwise_fma(h.p2 - k1024, dsc[t], ndm[t]),
-                    __builtin_elementwise_fma(h.p3 - k1024, dsc[t], ndm[t]));
+        w0 &= 0x0F0F0F0Fu;
+        w1 &= 0x0F0F0F0Fu;
+        const half2_t sc = bcast((t & 1) ? dsc[t >> 1].y : dsc[t >> 1].x);
+        const half2_t mn = bcast((t & 1) ? ndm[t >> 1].y : ndm[t >> 1].x);
+        const half2_t a0 = h2b(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 512.f, false)));
+        const half2_t a1 = h2b(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 512.f, true)));
+        const half2_t a2 = h2b(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 512.f, false)));
+        const half2_t a3 = h2b(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 512.f, true)));
+        return cat8(__builtin_elementwise_fma(a0, sc, mn), __builtin_elementwise_fma(a1, sc, mn),
+                    __builtin_elementwise_fma(a2, sc, mn), __builtin_elementwise_fma(a3, sc, mn));
     }
 };
 
@@ -154,6 +159,7 @@ struct Block<KQ_CODEC_Q6_K> {
     uint32_t dbits;
     half2_t dsc[8];
 
+    __device__ static constexpr int x_elem(int t, int g) { return 32 * t + 8 * g; }
     __device__ __forceinline__ void load(const uint8_t *blk, int g) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -208,14 +214,15 @@ struct Block<KQ_CODEC_Q6_K> {
 
 // IQ2_XXS (66 B = d + 8 groups of 8 B: 4 grid indices, u32 signs|scale).
 // Step t = group t; lane group g takes grid index byte g (values 8g .. 8g+7)
-// and the group's sign / scale dword.  The grid and sign tables are read
-// from LDS.
+// and the group's sign / scale dword.  The grid and sign tables are read from
+// LDS.
 template <>
 struct Block<KQ_CODEC_IQ2_XXS> {
     u32x4 raw[4];  // bytes 2..65 (the 8 groups)
     uint32_t dbits;
     half2_t db[8];
 
+    __device__ static constexpr int x_elem(int t, int g) { return 32 * t + 8 * g; }
     __device__ __forceinline__ void load(const uint8_t *blk, int g) {
         (void)g;
 #pragma unroll
@@ -252,14 +259,13 @@ struct Block<KQ_CODEC_IQ2_XXS> {
 template <int XT>
 constexpr int x_elem_bytes() { return XT == 2 ? 4 : 2; }
 
-// 8 consecutive activations as fp16.  bf16 / fp32 inputs are converted
-// (exact for bf16 in the fp16 normal range; fp32 rounds to nearest).
+// Raw 16 bytes -> 8 activations as fp16 (bf16 is converted, exact in the fp16
+// normal range).
 template <int XT>
-__device__ __forceinline__ half8_t load_x8(const char *p) {
+__device__ __forceinline__ half8_t x8_from_bits(u32x4 v) {
     if constexpr (XT == 0) {
-        return __builtin_bit_cast(half8_t, *(const u32x4 *)p);
-    } else if constexpr (XT == 1) {
-        const u32x4 v = *(const u32x4 *)p;
+        return __builtin_bit_cast(half8_t, v);
+    } else {
         half8_t h;
         const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -268,12 +274,79 @@ __device__ __forceinline__ half8_t load_x8(const char *p) {
             h[2 * i + 1] = (_Float16)__builtin_bit_cast(float, w[i] & 0xFFFF0000u);
         }
         return h;
+    }
+}
+
+// 8 consecutive activations as fp16.  bf16 / fp32 inputs are converted
+// (fp32 rounds to nearest).
+template <int XT>
+__device__ __forceinline__ half8_t load_x8(const char *p) {
+    if constexpr (XT != 2) {
+        return x8_from_bits<XT>(*(const u32x4 *)p);
     } else {
         const float4 a = *(const float4 *)p;
         const float4 b = *(const float4 *)(p + 16);
         return half8_t{(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w,
                        (_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};
     }
+}
+
+// Activation rows addressed by pointer (one per m-tile, already clamped to a
+// valid row): the MoE gather, whose rows come from a pair table.
+template <int MT>
+struct XRowPtrs {
+    const char *row[MT];
+    template <int XT>
+    __device__ __forceinline__ half8_t load(int mt, int elem) const {
+        return load_x8<XT>(row[mt] + (int64_t)elem * x_elem_bytes<XT>());
+    }
+};
+
+// Activation rows of a contiguous [rows, K] block read through a buffer
+// resource whose size covers only the valid rows: a lane whose row is past
+// the end gets an offset at the end of the buffer, and the hardware returns
+// zeros without touching memory, so padding rows of a 16-row tile cost no
+// memory traffic and need no branch.  Offsets are 32-bit bytes.
+template <int MT>
+struct XRowsBuf {
+    __amdgpu_buffer_rsrc_t rsrc;
+    uint32_t row_off[MT];
+    template <int XT>
+    __device__ __forceinline__ half8_t load(int mt, int elem) const {
+        const uint32_t off = row_off[mt] + (uint32_t)elem * (uint32_t)x_elem_bytes<XT>();
+        if constexpr (XT != 2) {
+            return x8_from_bits<XT>(__builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0)));
+        } else {
+            const u32x4 a = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0));
+            const u32x4 b = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off + 16, 0, 0));
+            return half8_t{(_Float16)__builtin_bit_cast(float, a.x), (_Float16)__builtin_bit_cast(float, a.y),
+                           (_Float16)__builtin_bit_cast(float, a.z), (_Float16)__builtin_bit_cast(float, a.w),
+                           (_Float16)__builtin_bit_cast(float, b.x), (_Float16)__builtin_bit_cast(float, b.y),
+                           (_Float16)__builtin_bit_cast(float, b.z), (_Float16)__builtin_bit_cast(float, b.w)};
+        }
+    }
+};
+
+// Buffer resource over `bytes` bytes at `base` (raw, 32-bit data format).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t kq_buffer(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// XRowsBuf for rows [m0, m0 + 16*MT) of x[M, K] (row stride in elements):
+// lane row m0 + 16*mt + r; rows >= M read as zeros.
+template <int MT, int XT>
+__device__ __forceinline__ XRowsBuf<MT> x_rows_buf(const char *x, int64_t stride, int M, int K, int m0, int r) {
+    constexpr int XS = x_elem_bytes<XT>();
+    XRowsBuf<MT> xr;
+    const int rows = min(M - m0, 16 * MT);
+    const uint32_t bytes = (uint32_t)(((int64_t)(rows - 1) * stride + K) * XS);
+    xr.rsrc = kq_buffer(x + (int64_t)m0 * stride * XS, bytes);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const int m = 16 * mt + r;
+        xr.row_off[mt] = m < rows ? (uint32_t)((int64_t)m * stride * XS) : bytes;
+    }
+    return xr;
 }
 
 // One super-block's operands for a wave: NW weight blocks and the 8 MFMA
@@ -283,17 +356,16 @@ struct Stage {
     Block<CODEC> w[NW];
     half8_t x[8][MT];
 
-    __device__ __forceinline__ void load(const uint8_t *const (&wrow)[NW], const char *const (&xrow)[MT], int kb,
-                                         int g) {
-        constexpr int XS = x_elem_bytes<XT>();
+    template <class XS>
+    __device__ __forceinline__ void load(const uint8_t *const (&wrow)[NW], const XS &xs, int kb, int g) {
         constexpr int BPB = kq_block_bytes(CODEC);
 #pragma unroll
         for (int i = 0; i < NW; ++i) w[i].load(wrow[i] + (int64_t)kb * BPB, g);
-        const int64_t xoff = ((int64_t)kb * KQ_QK + 8 * g) * XS;
 #pragma unroll
         for (int t = 0; t < 8; ++t)
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) x[t][mt] = load_x8<XT>(xrow[mt] + xoff + 32 * t * XS);
+            for (int mt = 0; mt < MT; ++mt)
+                x[t][mt] = xs.template load<XT>(mt, kb * KQ_QK + Block<CODEC>::x_elem(t, g));
     }
 
     __device__ __forceinline__ void compute(floatx4 (&acc)[NW][MT], int g, const Iq2Tables &tab) {
@@ -315,20 +387,31 @@ struct Stage {
 // Accumulate super-blocks kb_first, kb_first + kb_step, ... < kb_end of NW
 // weight matrices (NW = 2: gate and up share the activations).  wrow[i]
 // points at this lane's weight row (row n0 + lane%16 of matrix i, clamped to
-// a valid row by the caller).  xrow[mt] points (as bytes) at this lane's
-// activation row of m-tile mt, clamped to a valid row: rows past M compute
-// throw-away outputs that are never stored, so no load is conditional.  The
-// next block's loads are issued before the current block is multiplied
-// (register double buffer).
-template <int CODEC, int MT, int XT, int NW>
+// a valid row by the caller).  xrow (XRowPtrs / XRowsBuf) yields this lane's
+// activation fragments of each m-tile; rows past M feed outputs that are
+// never stored.  With PREFETCH (and MT * NW <= 2) the next block's loads are
+// issued before the current block is multiplied (register double buffer);
+// without it each block is loaded and multiplied in turn, and the latency is
+// hidden by the other resident waves.
+template <int CODEC, int MT, int XT, int NW, class XS, bool PREFETCH = true>
 __device__ __forceinline__ void tile_accumulate(const uint8_t *const (&wrow)[NW], int kb_first, int kb_step,
-                                                int kb_end, const char *const (&xrow)[MT],
-                                                floatx4 (&acc)[NW][MT], const Iq2Tables &tab) {
+                                                int kb_end, const XS &xrow, floatx4 (&acc)[NW][MT],
+                                                const Iq2Tables &tab) {
     const int g = kq_lane() >> 4;
     int kb = kb_first;
     if (kb >= kb_end) return;
-    if constexpr (MT * NW > 2) {
-        // wide tiles: one stage (two would not fit the register file)
+    if (kb + kb_step >= kb_end) {
+        // a single block for this wave: no prefetch stage
+        Stage<CODEC, MT, XT, NW> st;
+        st.load(wrow, xrow, kb, g);
+        __builtin_amdgcn_sched_barrier(0);
+        st.compute(acc, g, tab);
+        kq_mfma_drain();
+        return;
+    }
+    if constexpr (MT * NW > 2 || !PREFETCH) {
+        // wide tiles: one stage (two would not fit the register file); or the
+        // caller relies on many resident waves instead of a prefetch stage
         Stage<CODEC, MT, XT, NW> st;
         for (;;) {
             st.load(wrow, xrow, kb, g);
@@ -342,11 +425,15 @@ __device__ __forceinline__ void tile_accumulate(const uint8_t *const (&wrow)[NW]
         }
         return;
     }
+    // The prefetch loads are unconditional (past the end they re-read the
+    // current block): a load under a branch makes the compiler's wait-count
+    // merge at the join assume the short path and wait for the prefetch
+    // before the current block's math, which serialises the pipeline.
     Stage<CODEC, MT, XT, NW> s0, s1;
     s0.load(wrow, xrow, kb, g);
     for (;;) {
         const int k1 = kb + kb_step;
-        if (k1 < kb_end) s1.load(wrow, xrow, k1, g);
+        s1.load(wrow, xrow, k1 < kb_end ? k1 : kb, g);
         __builtin_amdgcn_sched_barrier(0);
         s0.compute(acc, g, tab);
         // at the exits: wait out the last MFMA's result latency inside the
@@ -357,7 +444,7 @@ __device__ __forceinline__ void tile_accumulate(const uint8_t *const (&wrow)[NW]
             break;
         }
         const int k2 = k1 + kb_step;
-        if (k2 < kb_end) s0.load(wrow, xrow, k2, g);
+        s0.load(wrow, xrow, k2 < kb_end ? k2 : k1, g);
         __builtin_amdgcn_sched_barrier(0);
         s1.compute(acc, g, tab);
         if (k2 >= kb_end) {

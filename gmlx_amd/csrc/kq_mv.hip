@@ -1,0 +1,478 @@
+// Small-batch dequant-fused matmul (M <= 16 activation rows) for problems that
+// share their activations (the q|k, o, gate|up calls of a decode step).
+//
+// y[M, N] = x[M, K] . dequant(W[N, K])^T
+//
+// One persistent workgroup of 16 waves per CU.  The workgroup first copies x
+// into LDS with coalesced direct-to-LDS loads (1 KB per instruction, rows
+// padded by 16 bytes so that the 16 rows of an MFMA operand fall in different
+// LDS banks; one extra zero row stands in for rows M..15), so activations
+// cost the memory pipeline one pass per workgroup instead of one pass per
+// weight tile.  It then walks 16-row weight tiles t = blockIdx.x,
+// blockIdx.x + gridDim.x, ...; wave w dequantizes super-blocks w, w + 16, ...
+// of the tile, reads the matching activation fragments from LDS and runs
+// v_mfma_f32_16x16x32_f16.  Each wave keeps a register ring of DEPTH tiles,
+// so DEPTH - 1 tiles are in flight while one is multiplied.
+//
+// The weights are read with buffer loads whose range is the problem's matrix:
+// rows past N and the ring's requests past the workgroup's last tile use an
+// offset outside the range, which reads zeros without a memory access.  So
+// every ring step issues the same loads and stores with no branch around
+// them, and the compiler's wait counts follow the ring exactly.  The 16
+// partial tiles are summed through LDS in wave order (each wave sums and
+// stores one sixteenth of the tile, again with out-of-range offsets for the
+// lanes that store nothing), so results are deterministic.
+//
+// Lane views (lane l = 16g + r feeds weight row r):
+//   Q4_K, IQ2_XXS : lane group g owns the quarter 64g .. 64g+63 of a block;
+//                   MFMA step t covers values 64g + 8t .. +7.
+//   Q6_K          : lane group g owns half h = g/2 of the block and the
+//                   positions l = 16(g%2) .. +15 of its four 32-value runs;
+//                   step t covers run t/2, positions 16(g%2) + 8(t%2) .. +7.
+#include <stdlib.h>
+
+#include "kq_mma.h"
+
+int device_cus();
+
+namespace {
+
+using namespace kqmma;
+
+constexpr int WV = 16;                 // waves per workgroup
+constexpr int kLdsBytes = 160 * 1024;  // LDS of one CU
+constexpr uint32_t kOut = 0x80000000u; // buffer offset past every range (reads 0, writes dropped)
+#define LDSP(T) __attribute__((address_space(3))) T *
+
+struct MvProblem {
+    const uint8_t *w;
+    void *y;
+    int64_t y_stride;        // elements
+    uint32_t w_bytes;        // N * row_bytes (< 2^31)
+    uint32_t row_bytes;
+    uint32_t y_bytes;        // ((M - 1) * y_stride + N) * element size (< 2^31)
+    int32_t N;
+};
+
+struct MvArgs {
+    int32_t tile_begin[KQ_MAX_GROUP];  // first tile of each problem; unused: INT_MAX
+    MvProblem p[KQ_MAX_GROUP];
+    const char *x;
+    int64_t x_stride;                  // elements
+    int32_t M, K, y_dtype, total_tiles;
+    int32_t xrow;                      // LDS bytes per staged activation row (2K + 16)
+    int32_t red_off, red_bufs;         // reduction area: byte offset in LDS, 1 or 2 buffers
+};
+
+__device__ __forceinline__ int problem_of(const MvArgs *A, int tile) {
+    int pi = 0;
+#pragma unroll
+    for (int i = 1; i < KQ_MAX_GROUP; ++i) pi = tile >= A->tile_begin[i] ? i : pi;
+    return __builtin_amdgcn_readfirstlane(pi);
+}
+
+__device__ __forceinline__ u32x4 ld128(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+}
+
+// ---- lane views ----------------------------------------------------------------
+
+template <int CODEC>
+struct WB;
+
+// Q4_K quarter view: header (d, dmin, scales) + qs bytes 32g .. 32g+31.
+// Sub-block 2g in the low nibbles, 2g+1 in the high nibbles.  Scales and mins
+// are unpacked as bytes four at a time (sub-blocks 0..3 and 4..7), the lane's
+// two are picked with a lane-constant mask, and become fp16 through the
+// 1024-bias (exact) times d / dmin.  Nibble bytes become exact fp16 integers
+// through the fp8 converter (q <= 15 read as E4M3 is q * 2^-9, scale 2^9).
+template <>
+struct WB<KQ_CODEC_Q4_K> {
+    u32x4 hdr, q0, q1;
+    __device__ static constexpr int x_elem(int t, int g) { return 64 * g + 8 * t; }
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, uint32_t off, int g) {
+        hdr = ld128(rs, off);
+        q0 = ld128(rs, off + 16 + 32 * g);
+        q1 = ld128(rs, off + 32 + 32 * g);
+    }
+    template <class XF>
+    __device__ __forceinline__ void mma(floatx4 &acc, const XF &xf, int g, const Iq2Tables &) const {
+        const uint32_t hmask = g >= 2 ? 0xFFFFFFFFu : 0u;
+        const uint32_t ssel = (g & 1) ? KQ_SEL_B23 : KQ_SEL_B01;
+        const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;
+        const uint32_t sc_hi = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
+        const uint32_t m_hi = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
+        const uint32_t scb = (sc_hi & hmask) | (s0 & 0x3F3F3F3Fu & ~hmask);
+        const uint32_t mb = (m_hi & hmask) | (s1 & 0x3F3F3F3Fu & ~hmask);
+        const half2_t k1024 = {(_Float16)1024.f, (_Float16)1024.f};
+        const half2_t dd = h2b(hdr.x);
+        const half2_t dsc = (h2b(__builtin_amdgcn_perm(0x64646464u, scb, ssel)) - k1024) * bcast(dd.x);
+        const half2_t ndm = (h2b(__builtin_amdgcn_perm(0x64646464u, mb, ssel)) - k1024) * bcast(-dd.y);
+        const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+        for (int tp = 0; tp < 4; ++tp) {
+            const uint32_t lo0 = qw[2 * tp] & 0x0F0F0F0Fu, lo1 = qw[2 * tp + 1] & 0x0F0F0F0Fu;
+            const uint32_t hi0 = (qw[2 * tp] >> 4) & 0x0F0F0F0Fu, hi1 = (qw[2 * tp + 1] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const uint32_t w0 = e ? hi0 : lo0, w1 = e ? hi1 : lo1;
+                const half2_t sc = bcast(e ? dsc.y : dsc.x), mn = bcast(e ? ndm.y : ndm.x);
+                const half2_t a0 = h2b(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 512.f, false)));
+                const half2_t a1 = h2b(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 512.f, true)));
+                const half2_t a2 = h2b(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 512.f, false)));
+                const half2_t a3 = h2b(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 512.f, true)));
+                const half8_t bf = cat8(__builtin_elementwise_fma(a0, sc, mn), __builtin_elementwise_fma(a1, sc, mn),
+                                        __builtin_elementwise_fma(a2, sc, mn), __builtin_elementwise_fma(a3, sc, mn));
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf(4 * e + tp), bf, acc, 0, 0, 0);
+            }
+        }
+    }
+};
+
+// Q6_K half view (210 B: ql[128], qh[64], scales[16], d).  Lane group g:
+// h = g / 2, c = g % 2.  Value 128h + 32q + l (l = 16c .. 16c+15) is
+// (ql[64h + 32(q%2) + l] nibble q/2) | (qh[32h + l] bits 2q, 2q+1) << 4,
+// minus 32, times d * scales[8h + 2q + c].  Loads: the two ql runs and the qh
+// run of the lane (16 B each), the 16 scales and d.
+template <>
+struct WB<KQ_CODEC_Q6_K> {
+    u32x4 qa, qb, qh, sc;
+    uint32_t dbits;
+    __device__ static constexpr int x_elem(int t, int g) {
+        return 128 * (g >> 1) + 32 * (t >> 1) + 16 * (g & 1) + 8 * (t & 1);
+    }
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, uint32_t off, int g) {
+        const uint32_t h = (uint32_t)(g >> 1), c = (uint32_t)(g & 1);
+        qa = ld128(rs, off + 64 * h + 16 * c);
+        qb = ld128(rs, off + 64 * h + 32 + 16 * c);
+        qh = ld128(rs, off + 128 + 32 * h + 16 * c);
+        sc = ld128(rs, off + 192);
+        dbits = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, off + 208, 0, 0);
+    }
+    template <class XF>
+    __device__ __forceinline__ void mma(floatx4 &acc, const XF &xf, int g, const Iq2Tables &) const {
+        const float d = kq_f16_bits_to_f32(dbits);
+        // scales 8h + 2q + c: q = 0, 1 in word 2h, q = 2, 3 in word 2h + 1, byte 2(q%2) + c
+        const uint32_t sw0 = g >= 2 ? sc.z : sc.x, sw1 = g >= 2 ? sc.w : sc.y;
+        const uint32_t cs = 8u * (uint32_t)(g & 1);
+        half2_t dsc[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t w = q < 2 ? sw0 : sw1;
+            const int s = __builtin_amdgcn_sbfe((int)w, (int)(16u * (q & 1) + cs), 8);
+            dsc[q] = bcast((_Float16)(d * (float)s));
+        }
+        const half2_t k1056 = {(_Float16)1056.f, (_Float16)1056.f};
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const int q = t >> 1, sub = t & 1;
+            const u32x4 &lq = (q & 1) ? qb : qa;
+            uint32_t l0 = sub ? lq.z : lq.x, l1 = sub ? lq.w : lq.y;
+            if (q >= 2) {
+                l0 >>= 4;
+                l1 >>= 4;
+            }
+            const uint32_t h0 = sub ? qh.z : qh.x, h1 = sub ? qh.w : qh.y;
+            uint32_t c0, c1;
+            if (q <= 2) {
+                c0 = (l0 & 0x0F0F0F0Fu) | ((h0 << (4 - 2 * q)) & 0x30303030u);
+                c1 = (l1 & 0x0F0F0F0Fu) | ((h1 << (4 - 2 * q)) & 0x30303030u);
+            } else {
+                c0 = (l0 & 0x0F0F0F0Fu) | ((h0 >> 2) & 0x30303030u);
+                c1 = (l1 & 0x0F0F0F0Fu) | ((h1 >> 2) & 0x30303030u);
+            }
+            const Bias8 b(c0, c1);
+            const half2_t s = dsc[q];
+            const half8_t bf = cat8((b.p0 - k1056) * s, (b.p1 - k1056) * s, (b.p2 - k1056) * s, (b.p3 - k1056) * s);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf(t), bf, acc, 0, 0, 0);
+        }
+    }
+};
+
+// IQ2_XXS quarter view: groups 2g, 2g+1 (bytes 2 + 16g .. +15) and d; grid and
+// sign tables from LDS.
+template <>
+struct WB<KQ_CODEC_IQ2_XXS> {
+    u32x4 raw;
+    uint32_t dbits;
+    __device__ static constexpr int x_elem(int t, int g) { return 64 * g + 8 * t; }
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, uint32_t off, int g) {
+        raw = ld128(rs, off + 2 + 16 * g);
+        dbits = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0);
+    }
+    template <class XF>
+    __device__ __forceinline__ void mma(floatx4 &acc, const XF &xf, int g, const Iq2Tables &tab) const {
+        (void)g;
+        const float d = kq_f16_bits_to_f32(dbits);
+        const half2_t db0 = bcast((_Float16)(d * (0.5f + (float)(raw.y >> 28)) * 0.25f));
+        const half2_t db1 = bcast((_Float16)(d * (0.5f + (float)(raw.w >> 28)) * 0.25f));
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const int e = t >> 2, l = t & 3;
+            const uint32_t gw = e ? raw.z : raw.x, aux = e ? raw.w : raw.y;
+            const uint32_t idx = (gw >> (8 * l)) & 0xFF;
+            const uint32_t s7 = (aux >> (7 * l)) & 127u;
+            const u32x4 gm = *(const u32x4 *)tab.grid_h2[idx];
+            const u32x4 sm = *(const u32x4 *)tab.sign_x2[s7];
+            const half2_t s = e ? db1 : db0;
+            const half8_t bf =
+                cat8(h2b(gm.x ^ sm.x) * s, h2b(gm.y ^ sm.y) * s, h2b(gm.z ^ sm.z) * s, h2b(gm.w ^ sm.w) * s);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf(t), bf, acc, 0, 0, 0);
+        }
+    }
+};
+
+// IQ2_XXS kernels keep the fp16 grid / sign tables in LDS; other codecs
+// allocate nothing.
+template <int CODEC>
+struct Tables {
+    __device__ static const Iq2Tables *get() { return nullptr; }
+};
+template <>
+struct Tables<KQ_CODEC_IQ2_XXS> {
+    __device__ static const Iq2Tables *get() {
+        __shared__ Iq2Tables t;
+        load_iq2_tables(t);
+        return &t;
+    }
+};
+
+template <int CODEC, int NBW>
+struct Ring {
+    // register ring depth: as many tiles in flight as the 128 registers of a
+    // lane at 16 waves per CU allow
+    static constexpr int depth = NBW == 1 ? 4 : 2;
+};
+
+// ---- kernel ---------------------------------------------------------------------
+
+// NBW: blocks per wave per tile (K <= 256 * 16 * NBW).  XT: 0 fp16, 1 bf16.
+template <int CODEC, int XT, int NBW>
+__global__ __launch_bounds__(64 * WV) void kq_mv_kernel(MvArgs a_) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const MvArgs *A = (const MvArgs *)__builtin_amdgcn_kernarg_segment_ptr();
+    const Iq2Tables *tab = Tables<CODEC>::get();
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = kq_lane(), r = lane & 15, g = lane >> 4;
+    const int G = (int)gridDim.x, B0 = (int)blockIdx.x;
+    const int my_tiles = (A->total_tiles - B0 + G - 1) / G;
+    if (my_tiles <= 0) return;  // uniform over the workgroup
+    const int M = A->M, K = A->K, nb = K / KQ_QK;
+    const int xrow = A->xrow;
+    constexpr int BPB = kq_block_bytes(CODEC);
+
+    // ---- stage x rows [0, M) into LDS (1 KB per instruction, row m at m * xrow)
+    //      and clear row M, read by the lanes of rows M..15
+    {
+        const int rowb = 2 * K, segs = (rowb + 1023) >> 10;
+        const int total = M * segs;
+        for (int i = wave; i < total; i += WV) {
+            const int m = i / segs, sg = i - m * segs;
+            const int off = sg * 1024 + lane * 16;
+            if (off < rowb)
+                __builtin_amdgcn_global_load_lds(A->x + (int64_t)m * A->x_stride * 2 + off,
+                                                 (LDSP(void))(smem + m * xrow + sg * 1024), 16, 0, 0);
+        }
+        for (int i = (int)threadIdx.x; i < xrow / 16; i += 64 * WV)
+            *(u32x4 *)(smem + M * xrow + 16 * i) = u32x4{0, 0, 0, 0};
+    }
+
+    // ---- ring step k: tile B0 + k * G, this wave's blocks kb = wave + WV * i
+    auto load_tile = [&](WB<CODEC> (&b)[NBW], int k) {
+        const bool live = k < my_tiles;
+        const int tile = B0 + min(k, my_tiles - 1) * G;
+        const int pi = problem_of(A, tile);
+        const int row0 = (tile - A->tile_begin[pi]) * 16;
+        const MvProblem &p = A->p[pi];
+        const __amdgpu_buffer_rsrc_t rs = kq_buffer(p.w, p.w_bytes);
+        // rows past N fall outside the range; so does every row of a dead step
+        const uint32_t base = live ? (uint32_t)(row0 + r) * p.row_bytes : kOut;
+#pragma unroll
+        for (int i = 0; i < NBW; ++i) {
+            const int kb = wave + WV * i;  // past nb: out of range too
+            b[i].load(rs, kb < nb ? base + (uint32_t)(kb * BPB) : kOut, g);
+        }
+    };
+
+    float *red = (float *)(smem + A->red_off);  // [bufs][WV][64 lanes][4]
+    const int bufs = A->red_bufs;
+    const uint32_t xr_base = (uint32_t)(uintptr_t)(LDSP(const void))(smem + (r < M ? r : M) * xrow);
+    // reduction slice of this wave: source lane 4 * wave + lane / 4, element
+    // lane % 4 (lanes 16..63 store nothing)
+    const int src_lane = 4 * wave + ((lane >> 2) & 3), src_e = lane & 3;
+    const int out_n = src_lane & 15, out_m = 4 * (src_lane >> 4) + src_e;
+    const bool out_lane = lane < 16 && out_m < M;
+
+    auto compute_tile = [&](WB<CODEC> (&b)[NBW], int k) {
+        floatx4 acc = floatx4{0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < NBW; ++i) {
+            const int kb = wave + WV * i;
+            if (kb < nb) {
+                // activation fragment of step t: x[r][kb * 256 + x_elem(t, g)] (zero row for r >= M)
+                auto xf = [&](int t) -> half8_t {
+                    const int e = kb * KQ_QK + WB<CODEC>::x_elem(t, g);
+                    return x8_from_bits<XT>(*(const LDSP(u32x4))(uintptr_t)(xr_base + e * 2));
+                };
+                b[i].mma(acc, xf, g, *tab);
+            }
+        }
+        kq_mfma_drain();
+        // ---- sum the WV partials in wave order; every wave stores its slice
+        const int buf = bufs == 2 ? (k & 1) : 0;
+        float *rb = red + (size_t)buf * WV * 256;
+        *(floatx4 *)(rb + 4 * (wave * 64 + lane)) = acc;
+        __syncthreads();
+        float sum = rb[4 * src_lane + src_e];
+#pragma unroll
+        for (int w = 1; w < WV; ++w) sum += rb[4 * (w * 64 + src_lane) + src_e];
+        const int tile = B0 + k * G;
+        const int pi = problem_of(A, tile);
+        const MvProblem &p = A->p[pi];
+        const int n = (tile - A->tile_begin[pi]) * 16 + out_n;
+        const __amdgpu_buffer_rsrc_t ys = kq_buffer(p.y, p.y_bytes);
+        const int es = A->y_dtype == KQ_DTYPE_F32 ? 4 : 2;
+        const uint32_t yo = (out_lane && n < p.N) ? (uint32_t)(out_m * p.y_stride + n) * es : kOut;
+        if (A->y_dtype == KQ_DTYPE_F32)
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, sum), ys, yo, 0, 0);
+        else if (A->y_dtype == KQ_DTYPE_F16)
+            __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (_Float16)sum), ys, yo, 0, 0);
+        else
+            __builtin_amdgcn_raw_buffer_store_b16(kq_f32_to_bf16_bits(sum), ys, yo, 0, 0);
+        if (bufs == 1) __syncthreads();  // the buffer is reused by the next tile
+    };
+
+    constexpr int DEPTH = Ring<CODEC, NBW>::depth;
+    WB<CODEC> bq[DEPTH][NBW];
+#pragma unroll
+    for (int d = 0; d < DEPTH - 1; ++d) load_tile(bq[d], d);
+    // x must have landed before the first activation read; the wait also
+    // covers the first DEPTH - 1 tiles, whose latency overlaps the staging
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    // ring step k requests tile k + DEPTH - 1 and multiplies tile k; the loop
+    // runs whole rounds of DEPTH steps (steps past the last tile only issue
+    // their out-of-range requests)
+    const int rounds = (my_tiles + DEPTH - 1) / DEPTH;
+    for (int k0 = 0; k0 < rounds * DEPTH; k0 += DEPTH) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) {
+            const int k = k0 + d;
+            load_tile(bq[(d + DEPTH - 1) % DEPTH], k + DEPTH - 1);
+            __builtin_amdgcn_sched_barrier(0);
+            if (k < my_tiles) compute_tile(bq[d], k);  // uniform over the workgroup
+        }
+    }
+}
+
+// Launch with `lds` bytes of dynamic LDS; the kernel's limit is raised to the
+// CU's LDS once per instantiation (the default limit is lower).
+template <int CODEC, int XT, int NBW>
+int launch_one(const MvArgs &a, int grid, size_t lds, hipStream_t s) {
+    static bool raised = false;
+    if (!raised) {
+        const size_t tables = CODEC == KQ_CODEC_IQ2_XXS ? sizeof(Iq2Tables) : 0;
+        if (hipFuncSetAttribute((const void *)kq_mv_kernel<CODEC, XT, NBW>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)(kLdsBytes - tables)) != hipSuccess)
+            return KQ_ERR_LAUNCH_FAILED;
+        raised = true;
+    }
+    hipLaunchKernelGGL((kq_mv_kernel<CODEC, XT, NBW>), dim3(grid), dim3(64 * WV), lds, s, a);
+    return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
+}
+
+template <int CODEC, int XT>
+int launch_nbw(const MvArgs &a, int nbw, int grid, size_t lds, hipStream_t s) {
+    switch (nbw) {
+    case 1: return launch_one<CODEC, XT, 1>(a, grid, lds, s);
+    case 2: return launch_one<CODEC, XT, 2>(a, grid, lds, s);
+    case 3: return launch_one<CODEC, XT, 3>(a, grid, lds, s);
+    default: return KQ_ERR_BAD_SHAPE;
+    }
+}
+
+int env_int(const char *name, int dflt) {
+    const char *s = getenv(name);
+    if (!s || !*s) return dflt;
+    char *end = nullptr;
+    const long v = strtol(s, &end, 10);
+    return (end && *end == 0 && v > 0 && v < (1 << 24)) ? (int)v : dflt;
+}
+
+// Bytes of LDS the launch needs: staged x rows and the zero row, the
+// reduction buffers.
+size_t mv_lds(const kq_matmul_problem &q, int bufs) {
+    const size_t xrow = 2 * (size_t)q.K + 16;
+    return (size_t)(q.M + 1) * xrow + (size_t)bufs * WV * 64 * sizeof(floatx4);
+}
+
+int y_elem_bytes(int y_dtype) { return y_dtype == KQ_DTYPE_F32 ? 4 : 2; }
+
+}  // namespace
+
+// Eligibility of a set of problems for the LDS-staged small-batch path: one
+// codec, shared x / stride / M / K, M <= 16, fp16 or bf16 activations, x rows
+// that fit in LDS, at most 3 blocks per wave, weights and outputs addressable
+// with 31-bit buffer offsets.
+bool kq_mv_eligible(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype) {
+    if (n <= 0) return false;
+    if (x_dtype != KQ_DTYPE_F16 && x_dtype != KQ_DTYPE_BF16) return false;
+    const kq_matmul_problem &q0 = ps[0];
+    if (q0.M < 1 || q0.M > 16) return false;
+    const int nb = q0.K / KQ_QK;
+    if (nb > 3 * WV) return false;
+    if (q0.codec == KQ_CODEC_Q6_K && nb > 2 * WV) return false;  // three Q6_K blocks per wave spill
+    const size_t tables = q0.codec == KQ_CODEC_IQ2_XXS ? sizeof(Iq2Tables) : 0;
+    if (mv_lds(q0, 1) + tables > (size_t)kLdsBytes) return false;
+    for (int i = 0; i < n; ++i) {
+        const kq_matmul_problem &q = ps[i];
+        if (q.x != q0.x || q.x_row_stride != q0.x_row_stride || q.M != q0.M || q.K != q0.K || q.codec != q0.codec)
+            return false;
+        if ((int64_t)(q.N + 16) * q.w_row_bytes >= (int64_t)kOut) return false;
+        if (((int64_t)(q.M - 1) * q.y_row_stride + q.N) * y_elem_bytes(y_dtype) >= (int64_t)kOut) return false;
+    }
+    return true;
+}
+
+// Problems validated and eligible (kq_mv_eligible), all live.
+int kq_mv_launch(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype, hipStream_t s) {
+    MvArgs a;
+    int tiles = 0;
+    for (int i = 0; i < n; ++i) {
+        MvProblem &p = a.p[i];
+        p.w = (const uint8_t *)ps[i].w;
+        p.y = ps[i].y;
+        p.y_stride = ps[i].y_row_stride;
+        p.row_bytes = (uint32_t)ps[i].w_row_bytes;
+        p.w_bytes = (uint32_t)(ps[i].N * ps[i].w_row_bytes);
+        p.y_bytes = (uint32_t)(((int64_t)(ps[i].M - 1) * ps[i].y_row_stride + ps[i].N) * y_elem_bytes(y_dtype));
+        p.N = ps[i].N;
+        a.tile_begin[i] = tiles;
+        tiles += (ps[i].N + 15) / 16;
+    }
+    for (int i = n; i < KQ_MAX_GROUP; ++i) {
+        a.p[i] = a.p[0];
+        a.tile_begin[i] = 0x7FFFFFFF;
+    }
+    const kq_matmul_problem &q0 = ps[0];
+    a.x = (const char *)q0.x;
+    a.x_stride = q0.x_row_stride;
+    a.M = q0.M;
+    a.K = q0.K;
+    a.y_dtype = y_dtype;
+    a.total_tiles = tiles;
+    a.xrow = 2 * q0.K + 16;
+    a.red_off = (q0.M + 1) * a.xrow;
+    const size_t tables = q0.codec == KQ_CODEC_IQ2_XXS ? sizeof(Iq2Tables) : 0;
+    a.red_bufs = mv_lds(q0, 2) + tables <= (size_t)kLdsBytes ? 2 : 1;
+    const size_t lds = mv_lds(q0, a.red_bufs);
+    int grid = env_int("GMLX_KQ_MV_WGS", device_cus());
+    if (grid > tiles) grid = tiles;
+    const int nbw = (q0.K / KQ_QK + WV - 1) / WV;
+    const bool bf = x_dtype == KQ_DTYPE_BF16;
+    switch (q0.codec) {
+    case KQ_CODEC_Q4_K: return bf ? launch_nbw<KQ_CODEC_Q4_K, 1>(a, nbw, grid, lds, s) : launch_nbw<KQ_CODEC_Q4_K, 0>(a, nbw, grid, lds, s);
+    case KQ_CODEC_Q6_K: return bf ? launch_nbw<KQ_CODEC_Q6_K, 1>(a, nbw, grid, lds, s) : launch_nbw<KQ_CODEC_Q6_K, 0>(a, nbw, grid, lds, s);
+    default: return bf ? launch_nbw<KQ_CODEC_IQ2_XXS, 1>(a, nbw, grid, lds, s) : launch_nbw<KQ_CODEC_IQ2_XXS, 0>(a, nbw, grid, lds, s);
+    }
+}

@@ -233,13 +233,13 @@ __global__ __launch_bounds__(64 * max_waves<CODEC>()) void kq_qmv_persistent_ker
     int tile = blockIdx.x;
     if (tile >= a.total_tiles) return;  // uniform over the workgroup
 
-    // this wave's activation fragments: row min(r, M-1), block kb_c, values 8t..8t+7
-    constexpr int XS = x_elem_bytes<XT>();
+    // this wave's activation fragments: row r (zeros for r >= M, no memory
+    // access), block kb_c, values 8t..8t+7
     half8_t xa[32];
     {
-        const char *xr = a.x + ((int64_t)min(r, a.M - 1) * a.x_stride + (int64_t)kb_c * KQ_QK) * XS;
+        const XRowsBuf<1> xr = x_rows_buf<1, XT>(a.x, a.x_stride, a.M, a.K, 0, r);
 #pragma unroll
-        for (int t = 0; t < 32; ++t) xa[t] = load_x8<XT>(xr + 8 * t * XS);
+        for (int t = 0; t < 32; ++t) xa[t] = xr.template load<XT>(0, kb_c * KQ_QK + 8 * t);
     }
     QmvProblem pc, pn;
     BlockL<CODEC> b0, b1;
@@ -247,9 +247,11 @@ __global__ __launch_bounds__(64 * max_waves<CODEC>()) void kq_qmv_persistent_ker
     int it = 0;
     for (;;) {
         // ---- even half: compute b0 while b1 loads
+        // unconditional prefetch (the last one re-reads the current tile): a
+        // load under a branch makes the compiler wait for it before the math
         int tn = tile + gridDim.x;
         bool more = tn < a.total_tiles;
-        if (more) b1.load(tile_block<CODEC>(a, tn, r, kb_c, pn));
+        b1.load(tile_block<CODEC>(a, more ? tn : tile, r, kb_c, pn));
         __builtin_amdgcn_sched_barrier(0);
         floatx4 acc;
         b0.prep(kvalid);
@@ -275,7 +277,7 @@ __global__ __launch_bounds__(64 * max_waves<CODEC>()) void kq_qmv_persistent_ker
         // ---- odd half: compute b1 while b0 loads
         tn = tile + gridDim.x;
         more = tn < a.total_tiles;
-        if (more) b0.load(tile_block<CODEC>(a, tn, r, kb_c, pn));
+        b0.load(tile_block<CODEC>(a, more ? tn : tile, r, kb_c, pn));
         __builtin_amdgcn_sched_barrier(0);
         b1.prep(kvalid);
         tile_mma<CODEC, XT>(b1, xa, acc, iq2_tab);

@@ -92,7 +92,7 @@ typedef struct {
     const void *w;       /* wire bytes */
     int64_t w_row_bytes; /* byte stride between weight rows (>= K/256*bpb) */
     const void *x;       /* activations [M, K] of x_dtype */
-    int64_t x_row_stride;/* elements */
+    int64_t x_row_stride;/* elements, K <= stride <= 2^22 */
     void *y;             /* output [M, N] of y_dtype */
     int64_t y_row_stride;/* elements */
     int32_t M, N, K;

@@ -160,16 +160,31 @@ def test_module_forward():
     assert okq.max_rel(got, ref) <= TOL
 
 
+# The three small-batch paths of kq_quantized_matmul_grouped, forced in turn:
+# the LDS-staged persistent path (kq_mv), the register persistent path
+# (kq_qmv) and the general tiled path.  Small grids make every workgroup walk
+# many tiles, with partial ring rounds.
+SMALL_BATCH_PATHS = [
+    ("default routing", {}),
+    ("mv, default grid", {"GMLX_KQ_MV": "2"}),
+    ("mv, 3 workgroups", {"GMLX_KQ_MV": "2", "GMLX_KQ_MV_WGS": "3"}),
+    ("mv, 7 workgroups", {"GMLX_KQ_MV": "2", "GMLX_KQ_MV_WGS": "7"}),
+    ("persistent, 3 workgroups", {"GMLX_KQ_MV": "0", "GMLX_KQ_QMV_WGS": "3"}),
+    ("general", {"GMLX_KQ_MV": "0", "GMLX_KQ_PERSISTENT": "0"}),
+]
+
+
 @pytest.mark.parametrize("codec,N,K,M", [
-    ("q4_k", 9000, 4096, 5),       # 563 tiles > persistent grid: several tiles per workgroup, odd count
-    ("q4_k", 777, 3328, 16),       # 13 blocks: partial last k-step, 4 waves
-    ("q6_k", 1040, 4096, 8),       # Q6_K persistent limit K = 4096
-    ("iq2_xxs", 520, 7168, 3),     # 28 blocks: 7 waves
+    ("q4_k", 9000, 4096, 5),       # 563 tiles: several tiles per workgroup, odd count
+    ("q4_k", 777, 3328, 16),       # 13 blocks: waves past the last block
+    ("q4_k", 300, 12288, 3),       # 48 blocks: three blocks per wave
+    ("q6_k", 1040, 4096, 8),
+    ("q6_k", 200, 8192, 2),        # 32 blocks: two Q6_K blocks per wave
+    ("iq2_xxs", 520, 7168, 3),     # 28 blocks
     ("q4_k", 64, 256, 1),          # single block, single wave
 ])
-def test_persistent_path_shapes(codec, N, K, M, monkeypatch):
-    """The persistent small-batch path (M <= 16) and the general path both
-    match the fp64 reference on the same inputs."""
+def test_small_batch_paths(codec, N, K, M, monkeypatch):
+    """Every small-batch path matches the fp64 reference on the same inputs."""
     rng = np.random.default_rng(N + K + M)
     if codec == "iq2_xxs":
         wire = okq.random_valid_blocks(rng, codec, N * K // 256).reshape(N, -1)
@@ -177,22 +192,38 @@ def test_persistent_path_shapes(codec, N, K, M, monkeypatch):
         wire = quantized_weights(rng, codec, N, K)
     x = fp16_rows(rng, M, K)
     ref = okq.qmm_ref(x, wire, codec)
-    got = _mm(x, wire, codec).float().cpu().numpy()
-    assert okq.max_rel(got, ref) <= TOL, ("persistent, default grid", okq.max_rel(got, ref))
-    # a small persistent grid: every shape takes the persistent path, and each
-    # workgroup walks many tiles
-    monkeypatch.setenv("GMLX_KQ_QMV_WGS", "3")
-    got3 = _mm(x, wire, codec).float().cpu().numpy()
-    assert okq.max_rel(got3, ref) <= TOL, ("persistent, 3 workgroups", okq.max_rel(got3, ref))
-    monkeypatch.delenv("GMLX_KQ_QMV_WGS")
-    monkeypatch.setenv("GMLX_KQ_PERSISTENT", "0")
-    got0 = _mm(x, wire, codec).float().cpu().numpy()
-    assert okq.max_rel(got0, ref) <= TOL, ("general", okq.max_rel(got0, ref))
+    for name, env in SMALL_BATCH_PATHS:
+        for k in ("GMLX_KQ_MV", "GMLX_KQ_MV_WGS", "GMLX_KQ_QMV_WGS", "GMLX_KQ_PERSISTENT"):
+            monkeypatch.delenv(k, raising=False)
+        for k, v in env.items():
+            monkeypatch.setenv(k, v)
+        got = _mm(x, wire, codec).float().cpu().numpy()
+        assert okq.max_rel(got, ref) <= TOL, (name, okq.max_rel(got, ref))
 
 
-def test_persistent_mixed_codec_group_and_determinism():
-    """q|k (Q4_K) and v (Q6_K) sharing x: one persistent launch per codec;
-    repeated calls are bitwise identical."""
+@pytest.mark.parametrize("y_dtype", ["float32", "bfloat16"])
+def test_small_batch_output_dtypes(y_dtype, monkeypatch):
+    """bf16 activations and f32 / bf16 outputs through the LDS-staged path."""
+    import torch
+    from gmlx_amd import ops
+    rng = np.random.default_rng(31)
+    N, K, M = 333, 2048, 6
+    wire = quantized_weights(rng, "q4_k", N, K)
+    x32 = rng.normal(0.0, 1.0, size=(M, K)).astype(np.float32)
+    xb = torch.from_numpy(x32).to(torch.bfloat16)
+    ref = okq.qmm_ref(xb.float().numpy(), wire, "q4_k")
+    monkeypatch.setenv("GMLX_KQ_MV", "2")
+    monkeypatch.setenv("GMLX_KQ_MV_WGS", "5")
+    out, = ops.quantized_matmul_grouped([(xb.cuda(), _dev(wire), "q4_k")], out_dtype=getattr(torch, y_dtype))
+    assert out.dtype == getattr(torch, y_dtype)
+    assert okq.max_rel(out.float().cpu().numpy(), ref) <= BF16_TOL
+
+
+@pytest.mark.parametrize("mv", ["2", "0"])
+def test_persistent_mixed_codec_group_and_determinism(mv, monkeypatch):
+    """q|k (Q4_K) and v (Q6_K) sharing x: one small-batch launch per codec
+    (LDS-staged path forced, or the register persistent path); repeated calls
+    are bitwise identical."""
     from gmlx_amd import ops
     rng = np.random.default_rng(21)
     K = 4096
@@ -201,13 +232,11 @@ def test_persistent_mixed_codec_group_and_determinism():
     wv = quantized_weights(rng, "q6_k", 128, K)
     x16 = fp16_rows(rng, 8, K)
     x = _dev(x16)
-    import os
-    os.environ["GMLX_KQ_QMV_WGS"] = "4"
-    try:
-        outs = [ops.quantized_matmul_grouped([(x, _dev(wq), "q4_k"), (x, _dev(wk), "q4_k"), (x, _dev(wv), "q6_k")])
-                for _ in range(3)]
-    finally:
-        del os.environ["GMLX_KQ_QMV_WGS"]
+    monkeypatch.setenv("GMLX_KQ_QMV_WGS", "4")
+    monkeypatch.setenv("GMLX_KQ_MV_WGS", "4")
+    monkeypatch.setenv("GMLX_KQ_MV", mv)
+    outs = [ops.quantized_matmul_grouped([(x, _dev(wq), "q4_k"), (x, _dev(wk), "q4_k"), (x, _dev(wv), "q6_k")])
+            for _ in range(3)]
     for o in outs[1:]:
         for a, b in zip(o, outs[0]):
             assert np.array_equal(a.cpu().numpy().view(np.uint16), b.cpu().numpy().view(np.uint16))
