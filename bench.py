@@ -13,9 +13,11 @@ from the 256 MB MALL.  A step is replayed from a HIP graph (the launches are
 5-10 us each; eager Python launching would measure the host).
 
 `value` = algorithmic weight + activation bytes per step / step time (GB/s).
-The `roofline` object is for the dense grouped matmul kernel (every launch of
-the step): achieved = algorithmic bytes per launch / average launch duration,
-both over the timed region.  Extra fields: the per-B sweep (B = 1..64, same
+The `roofline` object is for the kernel family with the largest share of the
+step (its launches of the step alone, replayed from a graph): achieved =
+algorithmic bytes per launch / average launch duration, both over the timed
+region; `traffic` = HBM bytes per launch of the same family from the
+FETCH_SIZE / WRITE_SIZE counters.  Extra fields: the per-B sweep (B = 1..64, same
 stack), ragged GQA decode attention at BASELINE config 3 (KV GB/s, KV tokens/s)
 and the CPU baseline (the repository's OpenMP C restatement of the same
 dequant-fused matmul, timed on a bounded sample of the same workload).
@@ -90,24 +92,38 @@ def make_inputs(torch, rng, B):
     return x, xd
 
 
-# The launches of one layer: (name, matrices).  At B <= 16 the gate|up launch
-# (1536 tiles, six per CU) takes the LDS-staged persistent small-batch kernel
-# and the other three (one tile per CU or less, or K = 12288 Q6_K) the general
-# dense kernel; at B > 16 every launch takes the general kernel.
+# The launches of one layer: (name, matrices), and the kernel that serves
+# each (kq_quantized_matmul_grouped's routing): at B <= 16 every launch takes
+# the LDS-staged persistent small-batch kernel (q|k|v: Q4_K and Q6_K tiles in
+# one launch, 1.5 tiles per CU, ring of 2; o: one tile per CU, ring of 1;
+# gate|up: six tiles per CU, ring of 3; down: K = 12288 Q6_K, three blocks
+# per wave, the last 4096 columns of x in registers at B > 4, LDS-staged only
+# up to B = 8); at B > 16 every launch takes the general kernel.
 LAUNCHES = [("qkv", ("q", "k", "v")), ("o", ("o",)), ("gate_up", ("gate", "up")), ("down", ("down",))]
 CODEC = {name: codec for name, _, _, codec in LAYER}
 DIMS = {name: (N, K) for name, N, K, _ in LAYER}
-# kernel families, as rocprofv3 names them (template arguments: codec / m-tiles,
-# activation type, blocks per wave / waves)
+# kernel families, as rocprofv3 names them
 KERNEL_FAMILIES = ("kq_mv_kernel", "kq_qmv_persistent_kernel", "kq_dense_grouped_kernel")
 
 
 def kernel_of(launch, B):
-    if B <= 16 and launch == "gate_up":
-        return "kq_mv_kernel<12, 0, 1>"
-    if B <= 16:
-        return "kq_dense_grouped_kernel<1, 0, 16>"
-    return f"kq_dense_grouped_kernel<{2 if B <= 32 else 4}, 0, 4>"
+    """Kernel (with template arguments) that serves `launch` at B rows."""
+    dense = f"kq_dense_grouped_kernel<{1 if B <= 16 else 2 if B <= 32 else 4}, 0, {16 if B <= 16 else 4}>"
+    if B > 16:
+        return dense
+    if launch == "qkv":  # Q4_K q|k with Q6_K v: the mixed form (codec id 127), 1.5 tiles per CU
+        return "kq_mv_kernel<127, 0, 1, 2, false>"
+    if launch == "o":
+        return "kq_mv_kernel<12, 0, 1, 1, false>"
+    if launch == "gate_up":
+        return "kq_mv_kernel<12, 0, 1, 3, false>"
+    if B <= 8:
+        return f"kq_mv_kernel<14, 0, 3, 1, {'true' if B > 4 else 'false'}>"
+    return dense
+
+
+def family(kernel):
+    return kernel.split("<")[0]
 
 
 def launch_bytes(launch, B):
@@ -389,14 +405,15 @@ def main():
     # in a graph, timed with HIP events on the replay stream
     kernels = {}
     for launch, _ in LAUNCHES:
-        kernels.setdefault(kernel_of(launch, B), []).append(launch)
+        kernels.setdefault(family(kernel_of(launch, B)), []).append(launch)
     per_kernel = {}
     for kname, lset in kernels.items():
         gk, _ = capture(torch, lambda: step_fn(ops, stack, x, xd, only=set(lset)))
         msk = time_graph(torch, gk, args.steps, args.warmup)
         n = args.layers * len(lset)
         byts = args.layers * sum(launch_bytes(l, B) for l in lset)
-        per_kernel[kname] = {"launches": lset, "launches_per_step": n, "avg_launch_us": round(msk * 1e3 / n, 3),
+        per_kernel[kname] = {"launches": lset, "instances": sorted({kernel_of(l, B) for l in lset}),
+                             "launches_per_step": n, "avg_launch_us": round(msk * 1e3 / n, 3),
                              "bytes_per_launch": byts // n, "gbs": round(byts / msk / 1e6, 1)}
         log(f"[bench] {kname} ({'+'.join(lset)}): {msk * 1e3 / n:.2f} us/launch, {byts / msk / 1e6:.1f} GB/s")
         del gk
@@ -440,9 +457,8 @@ def main():
     achieved = dk["bytes_per_launch"] / dk["avg_launch_us"] / 1e3
     tr = None
     if traffic is not None:
-        base = dominant.split("<")[0]
-        if base in traffic and "fetch" in traffic[base] and "write" in traffic[base]:
-            tr = round(traffic[base]["fetch"] + traffic[base]["write"])
+        if dominant in traffic and "fetch" in traffic[dominant] and "write" in traffic[dominant]:
+            tr = round(traffic[dominant]["fetch"] + traffic[dominant]["write"])
     res = {
         "metric": METRIC,
         "value": round(value, 1),

@@ -517,13 +517,23 @@ int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problem
                 if (problems[i].codec == codecs[c]) by_codec[c][cnt[c]++] = i;
         }
     }
-    // small batches with activations that fit in LDS: one LDS-staged launch per
-    // codec when every codec's problems share their activations.  Staging x
-    // pays when every workgroup walks several tiles (GMLX_KQ_MV=2 forces the
-    // path for any tile count).
+    // small batches with activations that fit in LDS: the LDS-staged path.
+    // Other codec mixes (IQ2_XXS with K-quants) take one launch per codec
+    // only when every codec's launch is large (four tiles per CU); otherwise
+    // one dense launch serves the whole group (GMLX_KQ_MV=2 forces the path).
     const int mv_mode = env_int_flag("GMLX_KQ_MV", 1);
     if (live > 0 && mv_mode) {
+        // one launch for the whole group: one codec, or Q4_K with Q6_K
+        kq_matmul_problem all[KQ_MAX_GROUP];
+        int na = 0;
+        for (int i = 0; i < n_problems; ++i)
+            if (problems[i].M != 0 && problems[i].N != 0) all[na++] = problems[i];
+        if (kq_mv_eligible(all, na, x_dtype, y_dtype))
+            return kq_mv_launch(all, na, x_dtype, y_dtype, (hipStream_t)stream);
+    }
+    if (live > 0 && mv_mode) {
         bool ok = true;
+        const int n_codecs = (cnt[0] > 0) + (cnt[1] > 0) + (cnt[2] > 0);
         kq_matmul_problem sub[3][KQ_MAX_GROUP];
         for (int c = 0; c < 3 && ok; ++c) {
             if (!cnt[c]) continue;
@@ -532,7 +542,8 @@ int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problem
                 sub[c][i] = problems[by_codec[c][i]];
                 tiles += (sub[c][i].N + 15) / 16;
             }
-            ok = kq_mv_eligible(sub[c], cnt[c], x_dtype, y_dtype) && (mv_mode == 2 || tiles >= 4 * device_cus());
+            ok = kq_mv_eligible(sub[c], cnt[c], x_dtype, y_dtype) &&
+                 (mv_mode == 2 || n_codecs == 1 || tiles >= 4 * device_cus());
         }
         if (ok) {
             for (int c = 0; c < 3; ++c) {

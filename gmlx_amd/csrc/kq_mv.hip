@@ -6,13 +6,18 @@
 // One persistent workgroup of 16 waves per CU.  The workgroup first copies x
 // into LDS with coalesced direct-to-LDS loads (1 KB per instruction, rows
 // padded by 16 bytes so that the 16 rows of an MFMA operand fall in different
-// LDS banks; one extra zero row stands in for rows M..15), so activations
-// cost the memory pipeline one pass per workgroup instead of one pass per
-// weight tile.  It then walks 16-row weight tiles t = blockIdx.x,
-// blockIdx.x + gridDim.x, ...; wave w dequantizes super-blocks w, w + 16, ...
-// of the tile, reads the matching activation fragments from LDS and runs
-// v_mfma_f32_16x16x32_f16.  Each wave keeps a register ring of DEPTH tiles,
-// so DEPTH - 1 tiles are in flight while one is multiplied.
+// LDS banks), so activations cost the memory pipeline one pass per workgroup
+// instead of one pass per weight tile.  It then walks 16-row weight tiles
+// t = blockIdx.x, blockIdx.x + gridDim.x, ...; wave w dequantizes super-blocks
+// w, w + 16, ... of the tile, reads the matching activation fragments from
+// LDS and runs v_mfma_f32_16x16x32_f16.  A wave always works on the same
+// super-blocks, so when x does not fit in LDS (K = 12288 at M = 5..8) the
+// last 4096 columns stay in registers instead (XR): each wave loads its
+// fragments of them once.  Lanes of rows M..15 read row M - 1: they feed only
+// output rows that are never stored.  Each wave keeps a register ring of
+// DEPTH tiles, so DEPTH - 1 tiles are in flight while one is multiplied (the
+// host picks DEPTH from the tiles per workgroup: a ring deeper than the work
+// only adds dead requests to the first wait).
 //
 // The weights are read with buffer loads whose range is the problem's matrix:
 // rows past N and the ring's requests past the workgroup's last tile use an
@@ -52,6 +57,7 @@ struct MvProblem {
     uint32_t row_bytes;
     uint32_t y_bytes;        // ((M - 1) * y_stride + N) * element size (< 2^31)
     int32_t N;
+    int32_t codec;           // KQ_CODEC_*
 };
 
 struct MvArgs {
@@ -60,7 +66,8 @@ struct MvArgs {
     const char *x;
     int64_t x_stride;                  // elements
     int32_t M, K, y_dtype, total_tiles;
-    int32_t xrow;                      // LDS bytes per staged activation row (2K + 16)
+    int32_t kl;                        // columns of x staged in LDS (K, or K - 4096 with XR)
+    int32_t xrow;                      // LDS bytes per staged activation row (2 kl + 16)
     int32_t red_off, red_bufs;         // reduction area: byte offset in LDS, 1 or 2 buffers
 };
 
@@ -90,13 +97,13 @@ template <>
 struct WB<KQ_CODEC_Q4_K> {
     u32x4 hdr, q0, q1;
     __device__ static constexpr int x_elem(int t, int g) { return 64 * g + 8 * t; }
-    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, uint32_t off, int g) {
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, uint32_t off, int g, bool) {
         hdr = ld128(rs, off);
         q0 = ld128(rs, off + 16 + 32 * g);
         q1 = ld128(rs, off + 32 + 32 * g);
     }
     template <class XF>
-    __device__ __forceinline__ void mma(floatx4 &acc, const XF &xf, int g, const Iq2Tables &) const {
+    __device__ __forceinline__ void mma(floatx4 &acc, const XF &xf, int g, const Iq2Tables &, bool = false) const {
         const uint32_t hmask = g >= 2 ? 0xFFFFFFFFu : 0u;
         const uint32_t ssel = (g & 1) ? KQ_SEL_B23 : KQ_SEL_B01;
         const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;
@@ -123,7 +130,7 @@ struct WB<KQ_CODEC_Q4_K> {
                 const half2_t a3 = h2b(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 512.f, true)));
                 const half8_t bf = cat8(__builtin_elementwise_fma(a0, sc, mn), __builtin_elementwise_fma(a1, sc, mn),
                                         __builtin_elementwise_fma(a2, sc, mn), __builtin_elementwise_fma(a3, sc, mn));
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf(4 * e + tp), bf, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf(4 * e + tp, x_elem(4 * e + tp, g)), bf, acc, 0, 0, 0);
             }
         }
     }
@@ -141,7 +148,7 @@ struct WB<KQ_CODEC_Q6_K> {
     __device__ static constexpr int x_elem(int t, int g) {
         return 128 * (g >> 1) + 32 * (t >> 1) + 16 * (g & 1) + 8 * (t & 1);
     }
-    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, uint32_t off, int g) {
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, uint32_t off, int g, bool) {
         const uint32_t h = (uint32_t)(g >> 1), c = (uint32_t)(g & 1);
         qa = ld128(rs, off + 64 * h + 16 * c);
         qb = ld128(rs, off + 64 * h + 32 + 16 * c);
@@ -150,7 +157,7 @@ struct WB<KQ_CODEC_Q6_K> {
         dbits = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, off + 208, 0, 0);
     }
     template <class XF>
-    __device__ __forceinline__ void mma(floatx4 &acc, const XF &xf, int g, const Iq2Tables &) const {
+    __device__ __forceinline__ void mma(floatx4 &acc, const XF &xf, int g, const Iq2Tables &, bool = false) const {
         const float d = kq_f16_bits_to_f32(dbits);
         // scales 8h + 2q + c: q = 0, 1 in word 2h, q = 2, 3 in word 2h + 1, byte 2(q%2) + c
         const uint32_t sw0 = g >= 2 ? sc.z : sc.x, sw1 = g >= 2 ? sc.w : sc.y;
@@ -184,7 +191,7 @@ struct WB<KQ_CODEC_Q6_K> {
             const Bias8 b(c0, c1);
             const half2_t s = dsc[q];
             const half8_t bf = cat8((b.p0 - k1056) * s, (b.p1 - k1056) * s, (b.p2 - k1056) * s, (b.p3 - k1056) * s);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf(t), bf, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf(t, x_elem(t, g)), bf, acc, 0, 0, 0);
         }
     }
 };
@@ -196,12 +203,12 @@ struct WB<KQ_CODEC_IQ2_XXS> {
     u32x4 raw;
     uint32_t dbits;
     __device__ static constexpr int x_elem(int t, int g) { return 64 * g + 8 * t; }
-    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, uint32_t off, int g) {
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, uint32_t off, int g, bool) {
         raw = ld128(rs, off + 2 + 16 * g);
         dbits = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0);
     }
     template <class XF>
-    __device__ __forceinline__ void mma(floatx4 &acc, const XF &xf, int g, const Iq2Tables &tab) const {
+    __device__ __forceinline__ void mma(floatx4 &acc, const XF &xf, int g, const Iq2Tables &tab, bool = false) const {
         (void)g;
         const float d = kq_f16_bits_to_f32(dbits);
         const half2_t db0 = bcast((_Float16)(d * (0.5f + (float)(raw.y >> 28)) * 0.25f));
@@ -217,7 +224,48 @@ struct WB<KQ_CODEC_IQ2_XXS> {
             const half2_t s = e ? db1 : db0;
             const half8_t bf =
                 cat8(h2b(gm.x ^ sm.x) * s, h2b(gm.y ^ sm.y) * s, h2b(gm.z ^ sm.z) * s, h2b(gm.w ^ sm.w) * s);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf(t), bf, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf(t, x_elem(t, g)), bf, acc, 0, 0, 0);
+        }
+    }
+};
+
+// Q4_K and Q6_K problems in one launch (the q|k and v of a Q4_K_M layer).
+// Every ring slot issues the loads of the Q6_K view (four 16-B runs and d);
+// a Q4_K tile fills the first three with the Q4_K view and sends the other
+// two out of range, so both codecs issue the same instructions and the wait
+// counts do not depend on the tile.  The tile's codec (uniform over the
+// workgroup) picks the dequantization.
+constexpr int KQ_MIX = 0x7F;
+
+template <>
+struct WB<KQ_MIX> {
+    u32x4 v0, v1, v2, v3;
+    uint32_t dbits;
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, uint32_t off, int g, bool q6) {
+        const uint32_t h = (uint32_t)(g >> 1), c = (uint32_t)(g & 1);
+        const bool dead = off >= kOut;
+        v0 = ld128(rs, q6 ? off + 64 * h + 16 * c : off);
+        v1 = ld128(rs, q6 ? off + 64 * h + 32 + 16 * c : off + 16 + 32 * g);
+        v2 = ld128(rs, q6 ? off + 128 + 32 * h + 16 * c : off + 32 + 32 * g);
+        v3 = ld128(rs, q6 && !dead ? off + 192 : kOut);
+        dbits = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, q6 && !dead ? off + 208 : kOut, 0, 0);
+    }
+    template <class XF>
+    __device__ __forceinline__ void mma(floatx4 &acc, const XF &xf, int g, const Iq2Tables &tab, bool q6) const {
+        if (q6) {
+            WB<KQ_CODEC_Q6_K> b;
+            b.qa = v0;
+            b.qb = v1;
+            b.qh = v2;
+            b.sc = v3;
+            b.dbits = dbits;
+            b.mma(acc, xf, g, tab);
+        } else {
+            WB<KQ_CODEC_Q4_K> b;
+            b.hdr = v0;
+            b.q0 = v1;
+            b.q1 = v2;
+            b.mma(acc, xf, g, tab);
         }
     }
 };
@@ -237,17 +285,12 @@ struct Tables<KQ_CODEC_IQ2_XXS> {
     }
 };
 
-template <int CODEC, int NBW>
-struct Ring {
-    // register ring depth: as many tiles in flight as the 128 registers of a
-    // lane at 16 waves per CU allow
-    static constexpr int depth = NBW == 1 ? 4 : 2;
-};
-
 // ---- kernel ---------------------------------------------------------------------
 
 // NBW: blocks per wave per tile (K <= 256 * 16 * NBW).  XT: 0 fp16, 1 bf16.
-template <int CODEC, int XT, int NBW>
+// DEPTH: register ring depth in tiles.  XR: block NBW - 1 of every wave takes
+// its activations from registers.
+template <int CODEC, int XT, int NBW, int DEPTH, bool XR>
 __global__ __launch_bounds__(64 * WV) void kq_mv_kernel(MvArgs a_) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const MvArgs *A = (const MvArgs *)__builtin_amdgcn_kernarg_segment_ptr();
@@ -259,12 +302,11 @@ __global__ __launch_bounds__(64 * WV) void kq_mv_kernel(MvArgs a_) {
     if (my_tiles <= 0) return;  // uniform over the workgroup
     const int M = A->M, K = A->K, nb = K / KQ_QK;
     const int xrow = A->xrow;
-    constexpr int BPB = kq_block_bytes(CODEC);
 
-    // ---- stage x rows [0, M) into LDS (1 KB per instruction, row m at m * xrow)
-    //      and clear row M, read by the lanes of rows M..15
+    // ---- stage columns [0, kl) of x rows [0, M) into LDS (1 KB per
+    //      instruction, row m at m * xrow)
     {
-        const int rowb = 2 * K, segs = (rowb + 1023) >> 10;
+        const int rowb = 2 * A->kl, segs = (rowb + 1023) >> 10;
         const int total = M * segs;
         for (int i = wave; i < total; i += WV) {
             const int m = i / segs, sg = i - m * segs;
@@ -273,8 +315,15 @@ __global__ __launch_bounds__(64 * WV) void kq_mv_kernel(MvArgs a_) {
                 __builtin_amdgcn_global_load_lds(A->x + (int64_t)m * A->x_stride * 2 + off,
                                                  (LDSP(void))(smem + m * xrow + sg * 1024), 16, 0, 0);
         }
-        for (int i = (int)threadIdx.x; i < xrow / 16; i += 64 * WV)
-            *(u32x4 *)(smem + M * xrow + 16 * i) = u32x4{0, 0, 0, 0};
+    }
+    // ---- XR: this wave's fragments of block wave + WV * (NBW - 1) (rows >= M read zeros)
+    half8_t xreg[XR ? 8 : 1];
+    if constexpr (XR) {
+        const XRowsBuf<1> xb = x_rows_buf<1, XT>(A->x, A->x_stride, M, K, 0, r);
+        const int kb = wave + WV * (NBW - 1);
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+            xreg[t] = xb.template load<XT>(0, min(kb, nb - 1) * KQ_QK + WB<CODEC>::x_elem(t, g));
     }
 
     // ---- ring step k: tile B0 + k * G, this wave's blocks kb = wave + WV * i
@@ -285,18 +334,20 @@ __global__ __launch_bounds__(64 * WV) void kq_mv_kernel(MvArgs a_) {
         const int row0 = (tile - A->tile_begin[pi]) * 16;
         const MvProblem &p = A->p[pi];
         const __amdgpu_buffer_rsrc_t rs = kq_buffer(p.w, p.w_bytes);
+        const bool q6 = CODEC == KQ_MIX && p.codec == KQ_CODEC_Q6_K;
+        const uint32_t bpb = CODEC == KQ_MIX ? (q6 ? 210u : 144u) : (uint32_t)kq_block_bytes(CODEC);
         // rows past N fall outside the range; so does every row of a dead step
         const uint32_t base = live ? (uint32_t)(row0 + r) * p.row_bytes : kOut;
 #pragma unroll
         for (int i = 0; i < NBW; ++i) {
             const int kb = wave + WV * i;  // past nb: out of range too
-            b[i].load(rs, kb < nb ? base + (uint32_t)(kb * BPB) : kOut, g);
+            b[i].load(rs, kb < nb ? base + (uint32_t)kb * bpb : kOut, g, q6);
         }
     };
 
     float *red = (float *)(smem + A->red_off);  // [bufs][WV][64 lanes][4]
     const int bufs = A->red_bufs;
-    const uint32_t xr_base = (uint32_t)(uintptr_t)(LDSP(const void))(smem + (r < M ? r : M) * xrow);
+    const uint32_t xr_base = (uint32_t)(uintptr_t)(LDSP(const void))(smem + min(r, M - 1) * xrow);
     // reduction slice of this wave: source lane 4 * wave + lane / 4, element
     // lane % 4 (lanes 16..63 store nothing)
     const int src_lane = 4 * wave + ((lane >> 2) & 3), src_e = lane & 3;
@@ -304,17 +355,25 @@ __global__ __launch_bounds__(64 * WV) void kq_mv_kernel(MvArgs a_) {
     const bool out_lane = lane < 16 && out_m < M;
 
     auto compute_tile = [&](WB<CODEC> (&b)[NBW], int k) {
+        const int tile = B0 + k * G;
+        const int pi = problem_of(A, tile);
+        const MvProblem &p = A->p[pi];
+        const bool q6 = CODEC == KQ_MIX && p.codec == KQ_CODEC_Q6_K;
         floatx4 acc = floatx4{0, 0, 0, 0};
 #pragma unroll
         for (int i = 0; i < NBW; ++i) {
             const int kb = wave + WV * i;
             if (kb < nb) {
-                // activation fragment of step t: x[r][kb * 256 + x_elem(t, g)] (zero row for r >= M)
-                auto xf = [&](int t) -> half8_t {
-                    const int e = kb * KQ_QK + WB<CODEC>::x_elem(t, g);
-                    return x8_from_bits<XT>(*(const LDSP(u32x4))(uintptr_t)(xr_base + e * 2));
-                };
-                b[i].mma(acc, xf, g, *tab);
+                if (XR && i == NBW - 1) {
+                    auto xf = [&](int t, int) -> half8_t { return xreg[XR ? t : 0]; };
+                    b[i].mma(acc, xf, g, *tab, q6);
+                } else {
+                    // activation fragment at element e of the block: x[r][kb * 256 + e]
+                    auto xf = [&](int, int e) -> half8_t {
+                        return x8_from_bits<XT>(*(const LDSP(u32x4))(uintptr_t)(xr_base + (kb * KQ_QK + e) * 2));
+                    };
+                    b[i].mma(acc, xf, g, *tab, q6);
+                }
             }
         }
         kq_mfma_drain();
@@ -326,9 +385,6 @@ __global__ __launch_bounds__(64 * WV) void kq_mv_kernel(MvArgs a_) {
         float sum = rb[4 * src_lane + src_e];
 #pragma unroll
         for (int w = 1; w < WV; ++w) sum += rb[4 * (w * 64 + src_lane) + src_e];
-        const int tile = B0 + k * G;
-        const int pi = problem_of(A, tile);
-        const MvProblem &p = A->p[pi];
         const int n = (tile - A->tile_begin[pi]) * 16 + out_n;
         const __amdgpu_buffer_rsrc_t ys = kq_buffer(p.y, p.y_bytes);
         const int es = A->y_dtype == KQ_DTYPE_F32 ? 4 : 2;
@@ -342,7 +398,6 @@ __global__ __launch_bounds__(64 * WV) void kq_mv_kernel(MvArgs a_) {
         if (bufs == 1) __syncthreads();  // the buffer is reused by the next tile
     };
 
-    constexpr int DEPTH = Ring<CODEC, NBW>::depth;
     WB<CODEC> bq[DEPTH][NBW];
 #pragma unroll
     for (int d = 0; d < DEPTH - 1; ++d) load_tile(bq[d], d);
@@ -367,28 +422,53 @@ __global__ __launch_bounds__(64 * WV) void kq_mv_kernel(MvArgs a_) {
 
 // Launch with `lds` bytes of dynamic LDS; the kernel's limit is raised to the
 // CU's LDS once per instantiation (the default limit is lower).
-template <int CODEC, int XT, int NBW>
+template <int CODEC, int XT, int NBW, int DEPTH, bool XR>
 int launch_one(const MvArgs &a, int grid, size_t lds, hipStream_t s) {
     static bool raised = false;
     if (!raised) {
         const size_t tables = CODEC == KQ_CODEC_IQ2_XXS ? sizeof(Iq2Tables) : 0;
-        if (hipFuncSetAttribute((const void *)kq_mv_kernel<CODEC, XT, NBW>,
+        if (hipFuncSetAttribute((const void *)kq_mv_kernel<CODEC, XT, NBW, DEPTH, XR>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)(kLdsBytes - tables)) != hipSuccess)
             return KQ_ERR_LAUNCH_FAILED;
         raised = true;
     }
-    hipLaunchKernelGGL((kq_mv_kernel<CODEC, XT, NBW>), dim3(grid), dim3(64 * WV), lds, s, a);
+    hipLaunchKernelGGL((kq_mv_kernel<CODEC, XT, NBW, DEPTH, XR>), dim3(grid), dim3(64 * WV), lds, s, a);
     return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
 }
 
+// Instantiated shapes (registers of a lane at 16 waves per CU: 128): one
+// block per wave with rings of 1..3 tiles; two or three blocks per wave with
+// rings of 1..2 tiles, except three Q6_K blocks and the XR form (ring of 1).
 template <int CODEC, int XT>
-int launch_nbw(const MvArgs &a, int nbw, int grid, size_t lds, hipStream_t s) {
-    switch (nbw) {
-    case 1: return launch_one<CODEC, XT, 1>(a, grid, lds, s);
-    case 2: return launch_one<CODEC, XT, 2>(a, grid, lds, s);
-    case 3: return launch_one<CODEC, XT, 3>(a, grid, lds, s);
-    default: return KQ_ERR_BAD_SHAPE;
+int launch_shape(const MvArgs &a, int nbw, int depth, bool xr, int grid, size_t lds, hipStream_t s) {
+    if constexpr (CODEC == KQ_MIX) {
+        // mixed Q4_K / Q6_K: up to two blocks per wave, x in LDS
+        if (xr || nbw > 2) return KQ_ERR_BAD_SHAPE;
+        if (nbw == 2) return depth == 1 ? launch_one<CODEC, XT, 2, 1, false>(a, grid, lds, s)
+                                        : launch_one<CODEC, XT, 2, 2, false>(a, grid, lds, s);
+        if (depth == 1) return launch_one<CODEC, XT, 1, 1, false>(a, grid, lds, s);
+        if (depth == 2) return launch_one<CODEC, XT, 1, 2, false>(a, grid, lds, s);
+        return launch_one<CODEC, XT, 1, 3, false>(a, grid, lds, s);
+    } else {
+        if (nbw == 1) {
+            if (depth == 1) return launch_one<CODEC, XT, 1, 1, false>(a, grid, lds, s);
+            if (depth == 2) return launch_one<CODEC, XT, 1, 2, false>(a, grid, lds, s);
+            return launch_one<CODEC, XT, 1, 3, false>(a, grid, lds, s);
+        }
+        if (nbw == 2) {
+            if (xr) return launch_one<CODEC, XT, 2, 1, true>(a, grid, lds, s);
+            if (depth == 1) return launch_one<CODEC, XT, 2, 1, false>(a, grid, lds, s);
+            return launch_one<CODEC, XT, 2, 2, false>(a, grid, lds, s);
+        }
+        if (nbw == 3) {
+            if (xr) return launch_one<CODEC, XT, 3, 1, true>(a, grid, lds, s);
+            if constexpr (CODEC != KQ_CODEC_Q6_K) {
+                if (depth >= 2) return launch_one<CODEC, XT, 3, 2, false>(a, grid, lds, s);
+            }
+            return launch_one<CODEC, XT, 3, 1, false>(a, grid, lds, s);
+        }
     }
+    return KQ_ERR_BAD_SHAPE;
 }
 
 int env_int(const char *name, int dflt) {
@@ -399,21 +479,46 @@ int env_int(const char *name, int dflt) {
     return (end && *end == 0 && v > 0 && v < (1 << 24)) ? (int)v : dflt;
 }
 
-// Bytes of LDS the launch needs: staged x rows and the zero row, the
-// reduction buffers.
-size_t mv_lds(const kq_matmul_problem &q, int bufs) {
-    const size_t xrow = 2 * (size_t)q.K + 16;
-    return (size_t)(q.M + 1) * xrow + (size_t)bufs * WV * 64 * sizeof(floatx4);
+// Columns of x staged in LDS: all of K, or with XR all but the last block
+// of every wave.
+int mv_kl(const kq_matmul_problem &q, bool xr) {
+    const int nbw = (q.K / KQ_QK + WV - 1) / WV;
+    return xr ? (nbw - 1) * WV * KQ_QK : q.K;
+}
+
+// Bytes of LDS the launch needs: staged x rows and the reduction buffers.
+size_t mv_lds(const kq_matmul_problem &q, bool xr, int bufs) {
+    const size_t xrow = 2 * (size_t)mv_kl(q, xr) + 16;
+    return (size_t)q.M * xrow + (size_t)bufs * WV * 64 * sizeof(floatx4);
+}
+
+size_t mv_tables(const kq_matmul_problem &q) { return q.codec == KQ_CODEC_IQ2_XXS ? sizeof(Iq2Tables) : 0; }
+
+// x in LDS when it fits with one reduction buffer, else XR (two or more
+// blocks per wave); -1: neither fits.
+int mv_xr(const kq_matmul_problem &q) {
+    const size_t avail = (size_t)kLdsBytes - mv_tables(q);
+    if (mv_lds(q, false, 1) <= avail) return 0;
+    if (q.K / KQ_QK > WV && mv_lds(q, true, 1) <= avail) return 1;
+    return -1;
 }
 
 int y_elem_bytes(int y_dtype) { return y_dtype == KQ_DTYPE_F32 ? 4 : 2; }
 
+// A set of problems of one codec, or of Q4_K and Q6_K together (KQ_MIX).
+bool mv_mixed(const kq_matmul_problem *ps, int n) {
+    for (int i = 1; i < n; ++i)
+        if (ps[i].codec != ps[0].codec) return true;
+    return false;
+}
+
 }  // namespace
 
 // Eligibility of a set of problems for the LDS-staged small-batch path: one
-// codec, shared x / stride / M / K, M <= 16, fp16 or bf16 activations, x rows
-// that fit in LDS, at most 3 blocks per wave, weights and outputs addressable
-// with 31-bit buffer offsets.
+// codec (or Q4_K and Q6_K together, K <= 8192, x all in LDS), shared x /
+// stride / M / K, M <= 16, fp16 or bf16 activations, x rows that fit in LDS
+// (all but the last 4096 columns, when K > 4096), at most 3 blocks per wave,
+// weights and outputs addressable with 31-bit buffer offsets.
 bool kq_mv_eligible(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype) {
     if (n <= 0) return false;
     if (x_dtype != KQ_DTYPE_F16 && x_dtype != KQ_DTYPE_BF16) return false;
@@ -421,13 +526,14 @@ bool kq_mv_eligible(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype
     if (q0.M < 1 || q0.M > 16) return false;
     const int nb = q0.K / KQ_QK;
     if (nb > 3 * WV) return false;
-    if (q0.codec == KQ_CODEC_Q6_K && nb > 2 * WV) return false;  // three Q6_K blocks per wave spill
-    const size_t tables = q0.codec == KQ_CODEC_IQ2_XXS ? sizeof(Iq2Tables) : 0;
-    if (mv_lds(q0, 1) + tables > (size_t)kLdsBytes) return false;
+    const int xr = mv_xr(q0);
+    if (xr < 0) return false;
+    const bool mixed = mv_mixed(ps, n);
+    if (mixed && (xr || nb > 2 * WV)) return false;
     for (int i = 0; i < n; ++i) {
         const kq_matmul_problem &q = ps[i];
-        if (q.x != q0.x || q.x_row_stride != q0.x_row_stride || q.M != q0.M || q.K != q0.K || q.codec != q0.codec)
-            return false;
+        if (q.x != q0.x || q.x_row_stride != q0.x_row_stride || q.M != q0.M || q.K != q0.K) return false;
+        if (mixed ? (q.codec != KQ_CODEC_Q4_K && q.codec != KQ_CODEC_Q6_K) : q.codec != q0.codec) return false;
         if ((int64_t)(q.N + 16) * q.w_row_bytes >= (int64_t)kOut) return false;
         if (((int64_t)(q.M - 1) * q.y_row_stride + q.N) * y_elem_bytes(y_dtype) >= (int64_t)kOut) return false;
     }
@@ -447,6 +553,7 @@ int kq_mv_launch(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype, h
         p.w_bytes = (uint32_t)(ps[i].N * ps[i].w_row_bytes);
         p.y_bytes = (uint32_t)(((int64_t)(ps[i].M - 1) * ps[i].y_row_stride + ps[i].N) * y_elem_bytes(y_dtype));
         p.N = ps[i].N;
+        p.codec = ps[i].codec;
         a.tile_begin[i] = tiles;
         tiles += (ps[i].N + 15) / 16;
     }
@@ -461,18 +568,33 @@ int kq_mv_launch(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype, h
     a.K = q0.K;
     a.y_dtype = y_dtype;
     a.total_tiles = tiles;
-    a.xrow = 2 * q0.K + 16;
-    a.red_off = (q0.M + 1) * a.xrow;
-    const size_t tables = q0.codec == KQ_CODEC_IQ2_XXS ? sizeof(Iq2Tables) : 0;
-    a.red_bufs = mv_lds(q0, 2) + tables <= (size_t)kLdsBytes ? 2 : 1;
-    const size_t lds = mv_lds(q0, a.red_bufs);
+    const bool xr = mv_xr(q0) == 1;
+    a.kl = mv_kl(q0, xr);
+    a.xrow = 2 * a.kl + 16;
+    a.red_off = q0.M * a.xrow;
+    a.red_bufs = mv_lds(q0, xr, 2) + mv_tables(q0) <= (size_t)kLdsBytes ? 2 : 1;
+    const size_t lds = mv_lds(q0, xr, a.red_bufs);
     int grid = env_int("GMLX_KQ_MV_WGS", device_cus());
     if (grid > tiles) grid = tiles;
     const int nbw = (q0.K / KQ_QK + WV - 1) / WV;
+    // ring depth: the tiles each workgroup walks, at most 3 (one block per
+    // wave) or 2 (more blocks: register budget; launch_shape lowers it further
+    // where the registers run out)
+    const int per_wg = (tiles + grid - 1) / grid;
+    const int depth = env_int("GMLX_KQ_MV_DEPTH", per_wg >= 4 ? 3 : per_wg >= 2 ? 2 : 1);
+    const int d = min(depth, nbw == 1 ? 3 : 2);
     const bool bf = x_dtype == KQ_DTYPE_BF16;
+    if (mv_mixed(ps, n))
+        return bf ? launch_shape<KQ_MIX, 1>(a, nbw, d, xr, grid, lds, s) : launch_shape<KQ_MIX, 0>(a, nbw, d, xr, grid, lds, s);
     switch (q0.codec) {
-    case KQ_CODEC_Q4_K: return bf ? launch_nbw<KQ_CODEC_Q4_K, 1>(a, nbw, grid, lds, s) : launch_nbw<KQ_CODEC_Q4_K, 0>(a, nbw, grid, lds, s);
-    case KQ_CODEC_Q6_K: return bf ? launch_nbw<KQ_CODEC_Q6_K, 1>(a, nbw, grid, lds, s) : launch_nbw<KQ_CODEC_Q6_K, 0>(a, nbw, grid, lds, s);
-    default: return bf ? launch_nbw<KQ_CODEC_IQ2_XXS, 1>(a, nbw, grid, lds, s) : launch_nbw<KQ_CODEC_IQ2_XXS, 0>(a, nbw, grid, lds, s);
+    case KQ_CODEC_Q4_K:
+        return bf ? launch_shape<KQ_CODEC_Q4_K, 1>(a, nbw, d, xr, grid, lds, s)
+                  : launch_shape<KQ_CODEC_Q4_K, 0>(a, nbw, d, xr, grid, lds, s);
+    case KQ_CODEC_Q6_K:
+        return bf ? launch_shape<KQ_CODEC_Q6_K, 1>(a, nbw, d, xr, grid, lds, s)
+                  : launch_shape<KQ_CODEC_Q6_K, 0>(a, nbw, d, xr, grid, lds, s);
+    default:
+        return bf ? launch_shape<KQ_CODEC_IQ2_XXS, 1>(a, nbw, d, xr, grid, lds, s)
+                  : launch_shape<KQ_CODEC_IQ2_XXS, 0>(a, nbw, d, xr, grid, lds, s);
     }
 }

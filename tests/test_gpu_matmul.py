@@ -77,19 +77,32 @@ def test_bf16_activations_and_f32_out():
     assert okq.max_rel(got32.cpu().numpy(), ref) <= TOL
 
 
-def test_grouped_equals_separate_bitwise():
-    """q|k|v with mixed codecs in one launch == three separate launches."""
+@pytest.mark.parametrize("path", [{"GMLX_KQ_MV": "0", "GMLX_KQ_PERSISTENT": "0"}, {"GMLX_KQ_MV": "2"}, {}])
+def test_grouped_equals_separate_bitwise(path, monkeypatch):
+    """q|k|v with mixed codecs in one launch == three separate launches:
+    bitwise when both take the same kernel (the general or the LDS-staged
+    path forced), within tolerance under the default routing (a mixed-codec
+    group and a single matrix may take different kernels, whose k-order
+    differs)."""
     from gmlx_amd import ops
+    for k, v in path.items():
+        monkeypatch.setenv(k, v)
     rng = np.random.default_rng(9)
     K = 1024
     wq = quantized_weights(rng, "q4_k", 256, K)
     wk = quantized_weights(rng, "q4_k", 64, K)
     wv = quantized_weights(rng, "q6_k", 64, K)
-    x = _dev(fp16_rows(rng, 4, K))
+    x16 = fp16_rows(rng, 4, K)
+    x = _dev(x16)
     outs = ops.quantized_matmul_grouped([(x, _dev(wq), "q4_k"), (x, _dev(wk), "q4_k"), (x, _dev(wv), "q6_k")])
     for o, (w, c) in zip(outs, [(wq, "q4_k"), (wk, "q4_k"), (wv, "q6_k")]):
         sep = ops.quantized_matmul(x, _dev(w), None, c)
-        assert np.array_equal(o.cpu().numpy().view(np.uint16), sep.cpu().numpy().view(np.uint16))
+        if path:
+            assert np.array_equal(o.cpu().numpy().view(np.uint16), sep.cpu().numpy().view(np.uint16))
+        else:
+            ref = okq.qmm_ref(x16, w, c)
+            assert okq.max_rel(o.float().cpu().numpy(), ref) <= TOL
+            assert okq.max_rel(sep.float().cpu().numpy(), ref) <= TOL
 
 
 def test_row_concatenated_wire_is_row_independent():
@@ -168,7 +181,8 @@ SMALL_BATCH_PATHS = [
     ("default routing", {}),
     ("mv, default grid", {"GMLX_KQ_MV": "2"}),
     ("mv, 3 workgroups", {"GMLX_KQ_MV": "2", "GMLX_KQ_MV_WGS": "3"}),
-    ("mv, 7 workgroups", {"GMLX_KQ_MV": "2", "GMLX_KQ_MV_WGS": "7"}),
+    ("mv, 7 workgroups, ring 2", {"GMLX_KQ_MV": "2", "GMLX_KQ_MV_WGS": "7", "GMLX_KQ_MV_DEPTH": "2"}),
+    ("mv, 5 workgroups, ring 1", {"GMLX_KQ_MV": "2", "GMLX_KQ_MV_WGS": "5", "GMLX_KQ_MV_DEPTH": "1"}),
     ("persistent, 3 workgroups", {"GMLX_KQ_MV": "0", "GMLX_KQ_QMV_WGS": "3"}),
     ("general", {"GMLX_KQ_MV": "0", "GMLX_KQ_PERSISTENT": "0"}),
 ]
@@ -182,6 +196,10 @@ SMALL_BATCH_PATHS = [
     ("q6_k", 200, 8192, 2),        # 32 blocks: two Q6_K blocks per wave
     ("iq2_xxs", 520, 7168, 3),     # 28 blocks
     ("q4_k", 64, 256, 1),          # single block, single wave
+    ("q6_k", 600, 12288, 8),       # x past LDS: last 4096 columns in registers
+    ("q4_k", 500, 12288, 6),
+    ("q4_k", 300, 8192, 16),       # two blocks per wave, the second from registers
+    ("iq2_xxs", 256, 12288, 7),
 ])
 def test_small_batch_paths(codec, N, K, M, monkeypatch):
     """Every small-batch path matches the fp64 reference on the same inputs."""
@@ -193,12 +211,41 @@ def test_small_batch_paths(codec, N, K, M, monkeypatch):
     x = fp16_rows(rng, M, K)
     ref = okq.qmm_ref(x, wire, codec)
     for name, env in SMALL_BATCH_PATHS:
-        for k in ("GMLX_KQ_MV", "GMLX_KQ_MV_WGS", "GMLX_KQ_QMV_WGS", "GMLX_KQ_PERSISTENT"):
+        for k in ("GMLX_KQ_MV", "GMLX_KQ_MV_WGS", "GMLX_KQ_MV_DEPTH", "GMLX_KQ_QMV_WGS", "GMLX_KQ_PERSISTENT"):
             monkeypatch.delenv(k, raising=False)
         for k, v in env.items():
             monkeypatch.setenv(k, v)
         got = _mm(x, wire, codec).float().cpu().numpy()
         assert okq.max_rel(got, ref) <= TOL, (name, okq.max_rel(got, ref))
+
+
+@pytest.mark.parametrize("K,M", [(4096, 8), (8192, 3), (1280, 16), (2048, 1)])
+def test_mixed_codec_group_paths(K, M, monkeypatch):
+    """q|k (Q4_K) with v (Q6_K) in one launch: the mixed LDS-staged kernel
+    (rings of 1..3 tiles, small grids) and the general path match the fp64
+    reference; an IQ2_XXS member routes the group elsewhere."""
+    from gmlx_amd import ops
+    rng = np.random.default_rng(K + M)
+    wq = quantized_weights(rng, "q4_k", 300, K)
+    wk = quantized_weights(rng, "q4_k", 70, K)
+    wv = quantized_weights(rng, "q6_k", 90, K)
+    wi = okq.random_valid_blocks(rng, "iq2_xxs", 40 * K // 256).reshape(40, -1)
+    x16 = fp16_rows(rng, M, K)
+    x = _dev(x16)
+    mats = [(wq, "q4_k"), (wk, "q4_k"), (wv, "q6_k")]
+    refs = [okq.qmm_ref(x16, w, c) for w, c in mats]
+    ref_i = okq.qmm_ref(x16, wi, "iq2_xxs")
+    for name, env in SMALL_BATCH_PATHS:
+        for k in ("GMLX_KQ_MV", "GMLX_KQ_MV_WGS", "GMLX_KQ_MV_DEPTH", "GMLX_KQ_QMV_WGS", "GMLX_KQ_PERSISTENT"):
+            monkeypatch.delenv(k, raising=False)
+        for k, v in env.items():
+            monkeypatch.setenv(k, v)
+        outs = ops.quantized_matmul_grouped([(x, _dev(w), c) for w, c in mats])
+        for o, ref in zip(outs, refs):
+            assert okq.max_rel(o.float().cpu().numpy(), ref) <= TOL, name
+        outs = ops.quantized_matmul_grouped([(x, _dev(w), c) for w, c in mats] + [(x, _dev(wi), "iq2_xxs")])
+        for o, ref in zip(outs, refs + [ref_i]):
+            assert okq.max_rel(o.float().cpu().numpy(), ref) <= TOL, (name, "with iq2_xxs")
 
 
 @pytest.mark.parametrize("y_dtype", ["float32", "bfloat16"])
