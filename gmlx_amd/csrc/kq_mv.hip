@@ -316,6 +316,7 @@ __global__ __launch_bounds__(64 * WV) void kq_mv_kernel(MvArgs a_) {
                                                  (LDSP(void))(smem + m * xrow + sg * 1024), 16, 0, 0);
         }
     }
+    __builtin_amdgcn_sched_barrier(0);  // the copies go first (see the wait below)
     // ---- XR: this wave's fragments of block wave + WV * (NBW - 1) (rows >= M read zeros)
     half8_t xreg[XR ? 8 : 1];
     if constexpr (XR) {
@@ -399,10 +400,14 @@ __global__ __launch_bounds__(64 * WV) void kq_mv_kernel(MvArgs a_) {
     };
 
     WB<CODEC> bq[DEPTH][NBW];
+    // A ring requests its first DEPTH - 1 tiles before the wait for the x
+    // copies, so their latency overlaps the staging.  A single slot requests
+    // its tile after the staging (measured faster for one tile per
+    // workgroup).
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int d = 0; d < DEPTH - 1; ++d) load_tile(bq[d], d);
-    // x must have landed before the first activation read; the wait also
-    // covers the first DEPTH - 1 tiles, whose latency overlaps the staging
+    __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     // ring step k requests tile k + DEPTH - 1 and multiplies tile k; the loop
