@@ -18,8 +18,9 @@ step (its launches of the step alone, replayed from a graph): achieved =
 algorithmic bytes per launch / average launch duration, both over the timed
 region; `traffic` = HBM bytes per launch of the same family from the
 FETCH_SIZE / WRITE_SIZE counters.  Extra fields: the per-B sweep (B = 1..64, same
-stack), ragged GQA decode attention at BASELINE config 3 (KV GB/s, KV tokens/s)
-and the CPU baseline (the repository's OpenMP C restatement of the same
+stack), ragged GQA decode attention at BASELINE config 3 (KV GB/s, KV tokens/s),
+one MoE decode layer at BASELINE configs 4 and 5 (GB/s over the touched
+experts' bytes) and the CPU baseline (the repository's OpenMP C restatement of the same
 dequant-fused matmul, timed on a bounded sample of the same workload).
 
 Inputs: numpy default_rng(seed) draws, N(0, 0.02) weights quantised on the GPU
@@ -246,6 +247,72 @@ def bench_sdpa(torch, ops, iters=20):
     }
 
 
+# ------------------------------------------------------------------- MoE
+
+MOE_CONFIGS = {
+    # name: (experts, hidden, expert intermediate, top-k, tokens, gate/up codec, down codec)
+    "C4": (128, 2048, 768, 8, 32, "q4_k", "q6_k"),
+    "C5": (256, 7168, 2048, 8, 8, "iq2_xxs", "iq2_xxs"),
+}
+BLOCK_BYTES = {"q4_k": 144, "q6_k": 210, "iq2_xxs": 66}
+
+
+def bench_moe(torch, ops, which, iters=20):
+    """BASELINE configs 4 and 5: one MoE decode layer (router top-k, fused
+    gate|up GLU gather, down gather with the routing mix folded in) over
+    the tokens' ragged per-expert segments.  Router logits and x are numpy
+    default_rng(0) draws; C4 weights are N(0, 0.02) drawn on the GPU (torch
+    generator, seed 0) and quantised by kq_quantize; C5 weights are random
+    valid IQ2_XXS blocks (d = 1e-3) -- the kernels' work does not depend on
+    the values.  C4 rotates two copies of the expert stacks (783 MB, > 2x the
+    256 MB MALL); C5's touched experts alone exceed it."""
+    import numpy as np
+    E, H, I, topk, T, cgu, cd = MOE_CONFIGS[which]
+    rng = np.random.default_rng(0)
+    logits = torch.from_numpy(rng.normal(0.0, 1.0, size=(T, E)).astype(np.float32)).cuda()
+    x = torch.from_numpy(rng.normal(0.0, 1.0, size=(T, H)).astype(np.float16)).cuda()
+    gen = torch.Generator(device="cuda").manual_seed(0)
+
+    def stack(N, K, codec):
+        nb, bpb = K // 256, BLOCK_BYTES[codec]
+        if codec == "iq2_xxs":
+            w = torch.randint(0, 256, (E, N, nb, bpb), generator=gen, device="cuda", dtype=torch.uint8)
+            w[..., 0:2] = torch.full((E, N, nb), 1e-3, device="cuda").half().view(torch.uint8).view(E, N, nb, 2)
+            return w.view(E, N, nb * bpb)
+        out = torch.empty((E, N, nb * bpb), dtype=torch.uint8, device="cuda")
+        for e0 in range(0, E, 32):  # quantise 32 experts at a time
+            w = torch.randn((min(32, E - e0) * N, K), generator=gen, device="cuda") * 0.02
+            out[e0:e0 + 32].view(-1, nb * bpb).copy_(ops.quantize(w, codec)[0])
+            del w
+        return out
+
+    copies = 2 if which == "C4" else 1
+    sets = [(stack(I, H, cgu), stack(I, H, cgu), stack(H, I, cd)) for _ in range(copies)]
+
+    def step(g, u, d):
+        idx, sc = ops.moe_router_topk(logits, topk)
+        h = ops.moe_glu_gather_kq(x, g, u, cgu, idx)
+        return ops.gather_qmv_mix_ns_kq(h, d, cd, idx, sc)
+
+    g, _ = capture(torch, lambda: [step(*st) for st in sets])
+    ms = time_graph(torch, g, iters, 3) / copies
+    del g
+    idx, _ = ops.moe_router_topk(logits, topk)
+    uniq = int(torch.unique(idx).numel())
+    per_expert = 2 * I * (H // 256) * BLOCK_BYTES[cgu] + H * (I // 256) * BLOCK_BYTES[cd]
+    act_bytes = T * H * 2 + 2 * T * topk * I * 4 + T * topk * H * 4 * 2 + T * H * 4
+    byts = uniq * per_expert + act_bytes
+    del sets
+    torch.cuda.empty_cache()
+    return {
+        "workload": f"{which} MoE decode layer: {E} experts, hidden {H}, expert intermediate {I}, top-{topk}, "
+                    f"{T} tokens, gate/up {cgu}, down {cd}",
+        "unique_experts": uniq, "ms": round(ms, 4), "algorithmic_bytes": byts,
+        "gbs": round(byts / ms / 1e6, 1), "frac_hbm": round(byts / ms / 1e6 / HBM_PEAK_GBS, 4),
+        "tokens_per_s": round(T / ms * 1e3, 1),
+    }
+
+
 # -------------------------------------------------------------- CPU baseline
 
 def cpu_baseline(layer_wires, B, budget_s=12.0):
@@ -354,6 +421,7 @@ def main():
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-sdpa", action="store_true")
+    ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 --pmc passes")
     ap.add_argument("--pmc-pass", action="store_true", help=argparse.SUPPRESS)
@@ -443,6 +511,14 @@ def main():
             log(f"[bench] sweep B={b}: {msb:.3f} ms/step, {gbs:.1f} GB/s")
             del gb
 
+    moe = None
+    if not args.no_moe:
+        moe = {}
+        for which in MOE_CONFIGS:
+            moe[which] = bench_moe(torch, ops, which)
+            log(f"[bench] moe {which}: {moe[which]['ms']} ms, {moe[which]['gbs']} GB/s over "
+                f"{moe[which]['unique_experts']} touched experts")
+
     sdpa = None
     if not args.no_sdpa:
         sdpa = bench_sdpa(torch, ops)
@@ -488,6 +564,7 @@ def main():
         "cpu_baseline": cpu,
         "per_batch": per_batch,
         "sdpa": sdpa,
+        "moe": moe,
     }
     print(json.dumps(res), flush=True)
 
