@@ -141,16 +141,40 @@ __device__ __forceinline__ float act_apply(int act, float g) {
     return 0.5f * g * (1.0f + tanhf(u));
 }
 
+// One workgroup of kGatherWaves waves per (expert segment, 16-row weight
+// tile): the waves split the super-blocks (wave w takes w, w + kGatherWaves,
+// ...) like the dense kernel, and wave 0 sums their tiles in wave order (so
+// the result is deterministic) before the epilogue.  A segment longer than
+// 16 * MT rows is walked in chunks.
+constexpr int kGatherWaves = 4;
+
+// Register budget: four waves per SIMD (128 VGPRs) up to two m-tiles, two
+// (256) for four m-tiles.
+template <int MT>
+constexpr int gather_waves_per_simd() { return MT <= 2 ? 4 : 2; }
+
 template <int CODEC, int MT, int XT, int NW>
-__global__ __launch_bounds__(64) void kq_gather_kernel(GatherArgs a) {
+__global__ __launch_bounds__(64 * kGatherWaves)
+__attribute__((amdgpu_waves_per_eu(gather_waves_per_simd<MT>()))) void kq_gather_kernel(GatherArgs a) {
+    __shared__ floatx4 red[kGatherWaves - 1][NW][MT][64];
     __shared__ Iq2Tables iq2_tab;
     if constexpr (CODEC == KQ_CODEC_IQ2_XXS) load_iq2_tables(iq2_tab);
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lane = kq_lane();
     const int r = lane & 15;
     const int slot = blockIdx.x / a.n_tiles;
     const int nt = blockIdx.x - slot * a.n_tiles;
+    if (slot == 0) {
+        // pairs whose expert id is out of range (never routed) get zeros in
+        // this tile's columns
+        const int32_t *flag = a.pair_order + a.n_pairs;
+        const int c = nt * 16 + (threadIdx.x & 15);
+        if (c < a.N)
+            for (int p = threadIdx.x >> 4; p < a.n_pairs; p += 4 * kGatherWaves)
+                if (flag[p] < 0) kq_store_out(a.y, a.y_dtype, (int64_t)p * a.y_stride + c, 0.f);
+    }
     const int S = a.seg_info[0];
-    if (slot >= S) return;
+    if (slot >= S) return;  // uniform over the workgroup
     const int expert = a.seg_info[1 + slot];
     const int seg_begin = a.seg_info[1 + a.n_experts + slot];
     const int seg_end = a.seg_info[1 + a.n_experts + slot + 1];
@@ -174,75 +198,142 @@ __global__ __launch_bounds__(64) void kq_gather_kernel(GatherArgs a) {
         for (int i = 0; i < NW; ++i)
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) acc[i][mt] = floatx4{0, 0, 0, 0};
-        tile_accumulate<CODEC, MT, XT, NW>(wrow, 0, 1, nb, xrow, acc, iq2_tab);
-        if (!n_valid) continue;
+        // no prefetch stage: resident waves hide the latency
+        tile_accumulate<CODEC, MT, XT, NW, XRowPtrs<MT>, false>(wrow, wave, kGatherWaves, nb, xrow, acc, iq2_tab);
+        if (wave > 0) {
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
+            for (int i = 0; i < NW; ++i)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int ri = c0 + 16 * mt + 4 * (lane >> 4) + e;
-                if (ri >= seg_end) continue;
-                const int pair = a.pair_order[ri];
-                float v = acc[0][mt][e];
-                if constexpr (NW == 2) v = act_apply(a.act, v) * acc[1][mt][e];
-                kq_store_out(a.y, a.y_dtype, (int64_t)pair * a.y_stride + n, v);
+                for (int mt = 0; mt < MT; ++mt) red[wave - 1][i][mt][lane] = acc[i][mt];
+        }
+        __syncthreads();
+        if (wave == 0 && n_valid) {
+#pragma unroll
+            for (int w = 0; w < kGatherWaves - 1; ++w)
+#pragma unroll
+                for (int i = 0; i < NW; ++i)
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) acc[i][mt] += red[w][i][mt][lane];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int ri = c0 + 16 * mt + 4 * (lane >> 4) + e;
+                    if (ri >= seg_end) continue;
+                    const int pair = a.pair_order[ri];
+                    float v = acc[0][mt][e];
+                    if constexpr (NW == 2) v = act_apply(a.act, v) * acc[1][mt][e];
+                    kq_store_out(a.y, a.y_dtype, (int64_t)pair * a.y_stride + n, v);
+                }
             }
         }
+        __syncthreads();  // red is reused by the next chunk
     }
 }
 
-// Zero the outputs of pairs whose expert id is out of range (never routed).
-__global__ void kq_gather_zero_invalid(const int32_t *idx_sorted_flag, int32_t n_pairs, int32_t N,
-                                       void *y, int y_dtype, int64_t y_stride) {
-    const int p = blockIdx.x;
-    if (idx_sorted_flag[p] >= 0) return;
-    for (int n = threadIdx.x; n < N; n += blockDim.x) kq_store_out(y, y_dtype, (int64_t)p * y_stride + n, 0.f);
-}
 
 // Routing: one workgroup, counting sort of pairs by expert (stable by pair id).
 // seg_info = [S, seg_expert[E], seg_start[E+1]]; pair_order[n_pairs];
 // valid_flag[n_pairs] (appended after pair_order) = expert or -1.
-__global__ __launch_bounds__(1024) void kq_route_kernel(const int32_t *__restrict__ idx, int32_t n_pairs,
-                                                        int32_t n_experts, int32_t *__restrict__ seg_info,
-                                                        int32_t *__restrict__ pair_order) {
-    extern __shared__ int32_t sm[];
-    int32_t *count = sm;                 // [E]
-    int32_t *start = sm + n_experts;     // [E]
-    const int tid = threadIdx.x;
-    for (int e = tid; e < n_experts; e += blockDim.x) count[e] = 0;
-    __syncthreads();
-    for (int p = tid; p < n_pairs; p += blockDim.x) {
-        const int e = idx[p];
-        if (e >= 0 && e < n_experts) atomicAdd(&count[e], 1);
+constexpr int kRouteThreads = 1024;
+constexpr int kRouteLdsInts = 15360;  // counts, starts and (when they fit) the pairs' expert ids: 60 KB
+
+__host__ __device__ inline bool route_staged(int n_pairs, int n_experts) {
+    return 2 * n_experts + n_pairs <= kRouteLdsInts;
+}
+
+// Exclusive prefix sum of one int per thread over the workgroup
+// (kRouteThreads threads); *total receives the sum.
+__device__ int route_block_scan(int v, int *wsum, int *total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr int NWAVE = kRouteThreads / 64;
+    int x = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(x, d, 64);
+        if (lane >= d) x += y;
     }
+    if (lane == 63) wsum[wave] = x;
     __syncthreads();
-    if (tid == 0) {
-        int acc = 0, s = 0;
-        for (int e = 0; e < n_experts; ++e) {
-            start[e] = acc;
-            if (count[e] > 0) {
-                seg_info[1 + s] = e;
-                seg_info[1 + n_experts + s] = acc;
-                ++s;
-            }
-            acc += count[e];
+    if (threadIdx.x == 0) {
+        int acc = 0;
+        for (int w = 0; w < NWAVE; ++w) {
+            const int t = wsum[w];
+            wsum[w] = acc;
+            acc += t;
         }
-        seg_info[0] = s;
-        for (int i = s; i <= n_experts; ++i) seg_info[1 + n_experts + i] = acc;
-        for (int i = s; i < n_experts; ++i) seg_info[1 + i] = -1;
+        *total = acc;
     }
+    __syncthreads();
+    const int r = x - v + wsum[wave];
+    __syncthreads();  // wsum is reused by the next scan
+    return r;
+}
+
+// Stable counting sort of (token, slot) pairs by expert id (the SwitchGLU
+// order): counts in LDS, one workgroup-wide scan for the segment starts and
+// the segment list, then one wave per expert walks the pairs in order and
+// writes its segment, so pairs keep their original order within it.
+__global__ __launch_bounds__(kRouteThreads) void kq_route_kernel(const int32_t *__restrict__ idx, int32_t n_pairs,
+                                                                 int32_t n_experts, int32_t *__restrict__ seg_info,
+                                                                 int32_t *__restrict__ pair_order) {
+    extern __shared__ int32_t sm[];
+    int32_t *count = sm;                    // [E]
+    int32_t *start = sm + n_experts;        // [E]
+    int32_t *ids = sm + 2 * n_experts;      // [n_pairs] when staged
+    __shared__ int wsum[kRouteThreads / 64];
+    __shared__ int tot_pairs, tot_segs;
+    const int tid = threadIdx.x;
+    const bool staged = route_staged(n_pairs, n_experts);
+    for (int e = tid; e < n_experts; e += kRouteThreads) count[e] = 0;
     __syncthreads();
     int32_t *flag = pair_order + n_pairs;
-    for (int p = tid; p < n_pairs; p += blockDim.x) {
-        const int e = idx[p];
-        if (e < 0 || e >= n_experts) {
-            flag[p] = -1;
-            continue;
-        }
+    for (int p = tid; p < n_pairs; p += kRouteThreads) {
+        int e = idx[p];
+        if (e < 0 || e >= n_experts) e = -1;
+        else atomicAdd(&count[e], 1);
         flag[p] = e;
-        int rank = 0;
-        for (int q = 0; q < p; ++q) rank += (idx[q] == e);
-        pair_order[start[e] + rank] = p;
+        if (staged) ids[p] = e;
+    }
+    __syncthreads();
+    // thread t owns experts [t * per, t * per + per)
+    const int per = (n_experts + kRouteThreads - 1) / kRouteThreads;
+    const int e0 = tid * per, e1 = min(e0 + per, n_experts);
+    int c = 0, nz = 0;
+    for (int e = e0; e < e1; ++e) {
+        c += count[e];
+        nz += count[e] > 0;
+    }
+    int acc = route_block_scan(c, wsum, &tot_pairs);
+    int sg = route_block_scan(nz, wsum, &tot_segs);
+    for (int e = e0; e < e1; ++e) {
+        start[e] = acc;
+        if (count[e] > 0) {
+            seg_info[1 + sg] = e;
+            seg_info[1 + n_experts + sg] = acc;
+            ++sg;
+        }
+        acc += count[e];
+    }
+    const int S = tot_segs, P = tot_pairs;
+    if (tid == 0) seg_info[0] = S;
+    for (int i = S + tid; i <= n_experts; i += kRouteThreads) seg_info[1 + n_experts + i] = P;
+    for (int i = S + tid; i < n_experts; i += kRouteThreads) seg_info[1 + i] = -1;
+    __syncthreads();
+    // wave w writes the segments of experts w, w + 16, ...: 64 pairs per step,
+    // each hit at its rank among the step's hits (ballot prefix count)
+    const int wave = tid >> 6, lane = tid & 63;
+    const uint64_t below = (lane ? ~0ull >> (64 - lane) : 0ull);
+    for (int e = wave; e < n_experts; e += kRouteThreads / 64) {
+        if (count[e] == 0) continue;  // uniform over the wave
+        int w = start[e];
+        for (int q0 = 0; q0 < n_pairs; q0 += 64) {
+            const int q = q0 + lane;
+            const bool hit = q < n_pairs && (staged ? ids[q] : flag[q]) == e;
+            const uint64_t m = __ballot(hit);
+            if (hit) pair_order[w + __popcll(m & below)] = q;
+            w += __popcll(m);
+        }
     }
 }
 
@@ -406,9 +497,9 @@ void launch_dense(const DenseArgs &a, int units, int chunks, hipStream_t s) {
 template <int CODEC, int XT, int NW>
 void launch_gather_codec(int mt, const GatherArgs &a, int grid, hipStream_t s) {
     switch (mt) {
-    case 1: hipLaunchKernelGGL((kq_gather_kernel<CODEC, 1, XT, NW>), dim3(grid), dim3(64), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((kq_gather_kernel<CODEC, 2, XT, NW>), dim3(grid), dim3(64), 0, s, a); break;
-    default: hipLaunchKernelGGL((kq_gather_kernel<CODEC, 4, XT, NW>), dim3(grid), dim3(64), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((kq_gather_kernel<CODEC, 1, XT, NW>), dim3(grid), dim3(64 * kGatherWaves), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((kq_gather_kernel<CODEC, 2, XT, NW>), dim3(grid), dim3(64 * kGatherWaves), 0, s, a); break;
+    default: hipLaunchKernelGGL((kq_gather_kernel<CODEC, 4, XT, NW>), dim3(grid), dim3(64 * kGatherWaves), 0, s, a); break;
     }
 }
 
@@ -460,10 +551,12 @@ int gather_common(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pa
     a.n_tiles = (N + 15) / 16;
     a.y_dtype = y_dtype;
     a.act = act;
-    // rows per expert segment are bounded by the number of pairs
-    const int rows = n_pairs < kMaxChunk ? n_pairs : kMaxChunk;
-    const int mt = rows <= 16 ? 1 : rows <= 32 ? 2 : 4;
+    // m-tiles per chunk from the mean segment length (pairs spread over the
+    // experts): decode batches leave a few rows per expert; longer segments
+    // are walked in chunks of 16 * mt rows
     const int slots = n_experts < n_pairs ? n_experts : n_pairs;
+    const int rows = (n_pairs + slots - 1) / slots;
+    const int mt = rows <= 16 ? 1 : rows <= 32 ? 2 : 4;
     const int grid = slots * a.n_tiles;
     if (w1) {
         if (x_dtype == KQ_DTYPE_F16) launch_gather<0, 2>(codec, mt, a, grid, s);
@@ -474,9 +567,6 @@ int gather_common(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pa
         else if (x_dtype == KQ_DTYPE_BF16) launch_gather<1, 1>(codec, mt, a, grid, s);
         else launch_gather<2, 1>(codec, mt, a, grid, s);
     }
-    if (hipGetLastError() != hipSuccess) return KQ_ERR_LAUNCH_FAILED;
-    hipLaunchKernelGGL(kq_gather_zero_invalid, dim3(n_pairs), dim3(256), 0, s, pair_order + n_pairs,
-                       n_pairs, N, y, y_dtype, y_row_stride);
     return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
 }
 
@@ -618,8 +708,8 @@ int kq_moe_route(const int32_t *idx, int32_t n_pairs, int32_t n_experts, int32_t
                  int32_t *pair_order, kq_stream_t stream) {
     if (!idx || !seg_info || !pair_order) return KQ_ERR_NULL_POINTER;
     if (n_pairs < 0 || n_experts <= 0 || n_experts > 4096) return KQ_ERR_BAD_SHAPE;
-    const size_t smem = (size_t)2 * n_experts * sizeof(int32_t);
-    hipLaunchKernelGGL(kq_route_kernel, dim3(1), dim3(1024), smem, (hipStream_t)stream, idx, n_pairs,
+    const size_t smem = ((size_t)2 * n_experts + (route_staged(n_pairs, n_experts) ? n_pairs : 0)) * sizeof(int32_t);
+    hipLaunchKernelGGL(kq_route_kernel, dim3(1), dim3(kRouteThreads), smem, (hipStream_t)stream, idx, n_pairs,
                        n_experts, seg_info, pair_order);
     return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
 }

@@ -4,11 +4,13 @@
 // super-blocks with v_mfma_f32_16x16x32_f16 (A = activations, B = weights^T).
 // Lane l = 16*g + r: r selects the weight row (B column) and the activation
 // row (A row) the lane feeds; g selects which 8 of the MFMA's 32 k values.
-// One super-block takes 8 MFMA steps t = 0..7; step t covers the 32 values
-// 32t .. 32t+31 of the block and lane group g feeds values 32t + 8g .. +7
-// (Block<>::x_elem).  The activation fragment of a step is the 8 activations at
-// the same value indices, so the 4 lane groups of one activation row read one
-// contiguous 64-byte run.  Every weight fragment is fully scaled before the
+// One super-block takes 8 MFMA steps t = 0..7.  Q4_K and Q6_K: step t covers
+// the 32 values 32t .. 32t+31 of the block and lane group g feeds values
+// 32t + 8g .. +7, so the 4 lane groups of one activation row read one
+// contiguous 64-byte run.  IQ2_XXS: lane group g owns the quarter 64g .. 64g+63
+// (one 16-byte load of the block per lane) and feeds 64g + 8t .. +7.  The
+// activation fragment of a step is the 8 activations at the same value
+// indices (Block<>::x_elem).  Every weight fragment is fully scaled before the
 // MFMA (w = dequant(q) in fp16), so the accumulator needs no per-block factor.
 //
 // Dequant to fp16 in registers, per pair of values:
@@ -213,42 +215,37 @@ struct Block<KQ_CODEC_Q6_K> {
 };
 
 // IQ2_XXS (66 B = d + 8 groups of 8 B: 4 grid indices, u32 signs|scale).
-// Step t = group t; lane group g takes grid index byte g (values 8g .. 8g+7)
-// and the group's sign / scale dword.  The grid and sign tables are read from
+// Lane group g owns groups 2g and 2g+1 (bytes 2 + 16g .. +15: one 16-B load
+// per lane) and the values 64g .. 64g+63; step t covers values 64g + 8t .. +7
+// (group 2g + t/4, grid index t%4).  The grid and sign tables are read from
 // LDS.
 template <>
 struct Block<KQ_CODEC_IQ2_XXS> {
-    u32x4 raw[4];  // bytes 2..65 (the 8 groups)
+    u32x4 raw;  // index word, sign|scale word of group 2g, then of group 2g+1
     uint32_t dbits;
-    half2_t db[8];
+    half2_t db[2];
 
-    __device__ static constexpr int x_elem(int t, int g) { return 32 * t + 8 * g; }
+    __device__ static constexpr int x_elem(int t, int g) { return 64 * g + 8 * t; }
     __device__ __forceinline__ void load(const uint8_t *blk, int g) {
-        (void)g;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const u32x4_a2 v = *(const u32x4_a2 *)(blk + 2 + 16 * i);
-            raw[i] = u32x4{v.x, v.y, v.z, v.w};
-        }
+        const u32x4_a2 v = *(const u32x4_a2 *)(blk + 2 + 16 * g);
+        raw = u32x4{v.x, v.y, v.z, v.w};
         dbits = (uint32_t)*(const uint16_t *)blk;
     }
     __device__ __forceinline__ void prep(int g) {
         (void)g;
         const float d = kq_f16_bits_to_f32(dbits);
-        const uint32_t *w = (const uint32_t *)&raw[0];
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const float v = d * (0.5f + (float)(w[2 * t + 1] >> 28)) * 0.25f;
-            db[t] = bcast((_Float16)v);
-        }
+        db[0] = bcast((_Float16)(d * (0.5f + (float)(raw.y >> 28)) * 0.25f));
+        db[1] = bcast((_Float16)(d * (0.5f + (float)(raw.w >> 28)) * 0.25f));
     }
     __device__ __forceinline__ half8_t frag(int t, int g, const Iq2Tables &tab) const {
-        const uint32_t *w = (const uint32_t *)&raw[0];
-        const uint32_t idx = (w[2 * t] >> (8 * g)) & 0xFF;
-        const uint32_t s7 = (w[2 * t + 1] >> (7 * g)) & 127u;
+        (void)g;
+        const int e = t >> 2, l = t & 3;
+        const uint32_t gw = e ? raw.z : raw.x, aux = e ? raw.w : raw.y;
+        const uint32_t idx = (gw >> (8 * l)) & 0xFF;
+        const uint32_t s7 = (aux >> (7 * l)) & 127u;
         const u32x4 gm = *(const u32x4 *)tab.grid_h2[idx];
         const u32x4 sm = *(const u32x4 *)tab.sign_x2[s7];
-        const half2_t s = db[t];
+        const half2_t s = db[e];
         return cat8(h2b(gm.x ^ sm.x) * s, h2b(gm.y ^ sm.y) * s, h2b(gm.z ^ sm.z) * s, h2b(gm.w ^ sm.w) * s);
     }
 };

@@ -22,21 +22,30 @@ def _experts(rng, codec, E, N, K):
     return np.stack([quantized_weights(rng, codec, N, K) for _ in range(E)])
 
 
-def test_route_groups_pairs_stably():
-    import torch
+@pytest.mark.parametrize("E,T,k", [(16, 37, 4), (128, 32, 8), (2000, 300, 8), (4096, 1250, 8), (256, 1, 8)])
+def test_route_groups_pairs_stably(E, T, k):
+    """Stable counting sort by expert: segment list, starts and pair order
+    (ids in LDS, more experts than threads, ids past LDS, out-of-range ids)."""
     from gmlx_amd import ops
-    rng = np.random.default_rng(0)
-    idx = rng.integers(0, 16, size=(37, 4)).astype(np.int32)
-    seg, order = ops.moe_route(_dev(idx), 16)
+    rng = np.random.default_rng(E + T)
+    idx = rng.integers(0, E, size=(T, k)).astype(np.int32)
+    if T > 1:
+        idx[0, 0], idx[-1, -1] = -1, E + 5  # never routed
+    seg, order = ops.moe_route(_dev(idx), E)
     seg, order = seg.cpu().numpy(), order.cpu().numpy()
     flat = idx.reshape(-1)
     P = flat.size
+    valid = (flat >= 0) & (flat < E)
     S = seg[0]
-    uniq = np.unique(flat)
+    uniq = np.unique(flat[valid])
     assert S == len(uniq)
     assert list(seg[1:1 + S]) == list(uniq)
-    assert np.array_equal(order[:P], np.argsort(flat, kind="stable"))
-    assert np.array_equal(order[P:2 * P], flat)
+    counts = np.array([(flat == e).sum() for e in uniq])
+    starts = np.concatenate([[0], np.cumsum(counts)])
+    assert list(seg[1 + E:1 + E + S + 1]) == list(starts)
+    want = np.argsort(np.where(valid, flat, E + 10), kind="stable")[:valid.sum()]
+    assert np.array_equal(order[:valid.sum()], want)
+    assert np.array_equal(order[P:2 * P], np.where(valid, flat, -1))
 
 
 @pytest.mark.parametrize("codec", ["q4_k", "q6_k", "iq2_xxs"])
