@@ -66,17 +66,16 @@ struct MvArgs {
     const char *x;
     int64_t x_stride;                  // elements
     int32_t M, K, y_dtype, total_tiles;
+    int32_t n_problems;
     int32_t kl;                        // columns of x staged in LDS (K, or K - 4096 with XR)
     int32_t xrow;                      // LDS bytes per staged activation row (2 kl + 16)
     int32_t red_off, red_bufs;         // reduction area: byte offset in LDS, 1 or 2 buffers
 };
 
-__device__ __forceinline__ int problem_of(const MvArgs *A, int tile) {
-    int pi = 0;
-#pragma unroll
-    for (int i = 1; i < KQ_MAX_GROUP; ++i) pi = tile >= A->tile_begin[i] ? i : pi;
-    return __builtin_amdgcn_readfirstlane(pi);
-}
+// Kernel arguments read in place through the constant address space, so the
+// compiler may keep them in scalar registers across the loop.
+typedef const __attribute__((address_space(4))) MvArgs *KArgs;
+
 
 __device__ __forceinline__ u32x4 ld128(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
@@ -293,7 +292,7 @@ struct Tables<KQ_CODEC_IQ2_XXS> {
 template <int CODEC, int XT, int NBW, int DEPTH, bool XR>
 __global__ __launch_bounds__(64 * WV) void kq_mv_kernel(MvArgs a_) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const MvArgs *A = (const MvArgs *)__builtin_amdgcn_kernarg_segment_ptr();
+    const KArgs A = (KArgs)__builtin_amdgcn_kernarg_segment_ptr();
     const Iq2Tables *tab = Tables<CODEC>::get();
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lane = kq_lane(), r = lane & 15, g = lane >> 4;
@@ -328,17 +327,60 @@ __global__ __launch_bounds__(64 * WV) void kq_mv_kernel(MvArgs a_) {
     }
 
     // ---- ring step k: tile B0 + k * G, this wave's blocks kb = wave + WV * i
+    // Tiles are walked in increasing order, so the problem of the next tile is
+    // found by advancing a cursor from the previous one, and the fields a step
+    // needs stay in scalar registers, reloaded only when the cursor moves (at
+    // most once per problem).  The load side (tile k + DEPTH - 1) and the
+    // multiply/store side (tile k) keep a cursor each.
+    struct LoadCursor {
+        int pi, begin, next;  // problem, its first tile, the next problem's first tile
+        const uint8_t *w;
+        uint32_t w_bytes, row_bytes;
+        int codec;
+    };
+    struct StoreCursor {
+        int pi, begin, next;
+        void *y;
+        int64_t y_stride;
+        uint32_t y_bytes;
+        int N, codec;
+    };
+    auto next_begin = [&](int pi) { return pi + 1 < A->n_problems ? A->tile_begin[pi + 1] : 0x7FFFFFFF; };
+    LoadCursor lc{0, 0, next_begin(0), A->p[0].w, A->p[0].w_bytes, A->p[0].row_bytes, A->p[0].codec};
+    StoreCursor sc{0, 0, next_begin(0), A->p[0].y, A->p[0].y_stride, A->p[0].y_bytes, A->p[0].N, A->p[0].codec};
+    auto load_at = [&](int tile) {
+        while (tile >= lc.next) {  // uniform over the workgroup
+            ++lc.pi;
+            lc.begin = lc.next;
+            lc.next = next_begin(lc.pi);
+            lc.w = A->p[lc.pi].w;
+            lc.w_bytes = A->p[lc.pi].w_bytes;
+            lc.row_bytes = A->p[lc.pi].row_bytes;
+            lc.codec = A->p[lc.pi].codec;
+        }
+    };
+    auto store_at = [&](int tile) {
+        while (tile >= sc.next) {
+            ++sc.pi;
+            sc.begin = sc.next;
+            sc.next = next_begin(sc.pi);
+            sc.y = A->p[sc.pi].y;
+            sc.y_stride = A->p[sc.pi].y_stride;
+            sc.y_bytes = A->p[sc.pi].y_bytes;
+            sc.N = A->p[sc.pi].N;
+            sc.codec = A->p[sc.pi].codec;
+        }
+    };
     auto load_tile = [&](WB<CODEC> (&b)[NBW], int k) {
         const bool live = k < my_tiles;
         const int tile = B0 + min(k, my_tiles - 1) * G;
-        const int pi = problem_of(A, tile);
-        const int row0 = (tile - A->tile_begin[pi]) * 16;
-        const MvProblem &p = A->p[pi];
-        const __amdgpu_buffer_rsrc_t rs = kq_buffer(p.w, p.w_bytes);
-        const bool q6 = CODEC == KQ_MIX && p.codec == KQ_CODEC_Q6_K;
+        load_at(tile);
+        const int row0 = (tile - lc.begin) * 16;
+        const __amdgpu_buffer_rsrc_t rs = kq_buffer(lc.w, lc.w_bytes);
+        const bool q6 = CODEC == KQ_MIX && lc.codec == KQ_CODEC_Q6_K;
         const uint32_t bpb = CODEC == KQ_MIX ? (q6 ? 210u : 144u) : (uint32_t)kq_block_bytes(CODEC);
         // rows past N fall outside the range; so does every row of a dead step
-        const uint32_t base = live ? (uint32_t)(row0 + r) * p.row_bytes : kOut;
+        const uint32_t base = live ? (uint32_t)(row0 + r) * lc.row_bytes : kOut;
 #pragma unroll
         for (int i = 0; i < NBW; ++i) {
             const int kb = wave + WV * i;  // past nb: out of range too
@@ -355,11 +397,11 @@ __global__ __launch_bounds__(64 * WV) void kq_mv_kernel(MvArgs a_) {
     const int out_n = src_lane & 15, out_m = 4 * (src_lane >> 4) + src_e;
     const bool out_lane = lane < 16 && out_m < M;
 
+    const bool y_f32 = A->y_dtype == KQ_DTYPE_F32, y_bf16 = A->y_dtype == KQ_DTYPE_BF16;
     auto compute_tile = [&](WB<CODEC> (&b)[NBW], int k) {
         const int tile = B0 + k * G;
-        const int pi = problem_of(A, tile);
-        const MvProblem &p = A->p[pi];
-        const bool q6 = CODEC == KQ_MIX && p.codec == KQ_CODEC_Q6_K;
+        store_at(tile);
+        const bool q6 = CODEC == KQ_MIX && sc.codec == KQ_CODEC_Q6_K;
         floatx4 acc = floatx4{0, 0, 0, 0};
 #pragma unroll
         for (int i = 0; i < NBW; ++i) {
@@ -386,16 +428,14 @@ __global__ __launch_bounds__(64 * WV) void kq_mv_kernel(MvArgs a_) {
         float sum = rb[4 * src_lane + src_e];
 #pragma unroll
         for (int w = 1; w < WV; ++w) sum += rb[4 * (w * 64 + src_lane) + src_e];
-        const int n = (tile - A->tile_begin[pi]) * 16 + out_n;
-        const __amdgpu_buffer_rsrc_t ys = kq_buffer(p.y, p.y_bytes);
-        const int es = A->y_dtype == KQ_DTYPE_F32 ? 4 : 2;
-        const uint32_t yo = (out_lane && n < p.N) ? (uint32_t)(out_m * p.y_stride + n) * es : kOut;
-        if (A->y_dtype == KQ_DTYPE_F32)
+        const int n = (tile - sc.begin) * 16 + out_n;
+        const __amdgpu_buffer_rsrc_t ys = kq_buffer(sc.y, sc.y_bytes);
+        const uint32_t yo = (out_lane && n < sc.N) ? (uint32_t)(out_m * sc.y_stride + n) * (y_f32 ? 4u : 2u) : kOut;
+        if (y_f32)
             __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, sum), ys, yo, 0, 0);
-        else if (A->y_dtype == KQ_DTYPE_F16)
-            __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (_Float16)sum), ys, yo, 0, 0);
         else
-            __builtin_amdgcn_raw_buffer_store_b16(kq_f32_to_bf16_bits(sum), ys, yo, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b16(
+                y_bf16 ? kq_f32_to_bf16_bits(sum) : __builtin_bit_cast(uint16_t, (_Float16)sum), ys, yo, 0, 0);
         if (bufs == 1) __syncthreads();  // the buffer is reused by the next tile
     };
 
@@ -573,6 +613,7 @@ int kq_mv_launch(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype, h
     a.K = q0.K;
     a.y_dtype = y_dtype;
     a.total_tiles = tiles;
+    a.n_problems = n;
     const bool xr = mv_xr(q0) == 1;
     a.kl = mv_kl(q0, xr);
     a.xrow = 2 * a.kl + 16;
