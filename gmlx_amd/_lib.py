@@ -36,6 +36,7 @@ EXPORTS = (
     "kq_dequantize", "kq_quantize", "kq_matmul_workspace_bytes", "kq_quantized_matmul_grouped",
     "kq_moe_route", "kq_gather_qmm", "kq_moe_glu_gather", "kq_moe_mix", "kq_moe_router_topk",
     "kq_sdpa_workspace_bytes", "kq_sdpa_decode_ragged",
+    "kq_sdpa_cascade_workspace_bytes", "kq_sdpa_decode_gqa_cascade",
 )
 
 
@@ -92,6 +93,9 @@ _SIGS = {
     "kq_sdpa_workspace_bytes": ([_i32, _i32, _i32, _i32, _i32], _sz),
     "kq_sdpa_decode_ragged": ([_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _f32, _int, _vp,
                                _vp, _sz, _vp], _int),
+    "kq_sdpa_cascade_workspace_bytes": ([_i32, _i32, _i32, _i32, _i32, _i32, _i32], _sz),
+    "kq_sdpa_decode_gqa_cascade": ([_vp, _vp, _vp, _i64, _i32, _vp, _vp, _i64, _i64, _i32, _vp, _i32, _i32,
+                                    _i32, _i32, _i32, _f32, _int, _vp, _vp, _sz, _vp], _int),
 }
 
 

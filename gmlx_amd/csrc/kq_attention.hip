@@ -32,9 +32,18 @@ struct SdpaArgs {
     uint16_t *out;
     const int64_t *kv_off, *head_stride;
     const int32_t *row_len;
+    // cascade mode (cascade != 0): k/v hold the shared prefix [Hkv][P][D]
+    // (head stride shared_head_stride) seen by every row in full; k2/v2 the
+    // private slabs [seq][Hkv][S][D], where row r (token i = r % qL of
+    // sequence r / qL) sees keys [starts[seq], S - qL + i] after the prefix
+    const int32_t *starts;
+    const uint16_t *k2, *v2;
+    int64_t shared_head_stride, priv_batch_stride, priv_head_stride;
+    int32_t cascade, P, S, n1;  // n1 = prefix splits of every row
     float *part;          // [B][Hkv][max_splits][G][D] O partials
     float *ml;            // [B][Hkv][max_splits][G][2] (m, l)
     int32_t B, Hq, Hkv, G, split, max_splits, max_len;
+    int32_t qL;           // query tokens per sequence: row r is token r % qL of sequence r / qL
     float scale_log2;     // scale * log2(e)
 };
 
@@ -65,19 +74,50 @@ __device__ __forceinline__ uint16_t from_f32(float f) {
     else return kq_f32_to_bf16_bits(f);
 }
 
+// Element index / D of (row, q head) in q and out, laid out [seq][Hq][qL][D]
+// (qL = 1: [row][Hq][D]).
+__device__ __forceinline__ int64_t qo_index(const SdpaArgs &a, int row, int hq) {
+    const int sq = row / a.qL, i = row - sq * a.qL;
+    return ((int64_t)sq * a.Hq + hq) * a.qL + i;
+}
+
 __device__ __forceinline__ int row_splits(int len, int split) {
     return len <= 0 ? 1 : (len + split - 1) / split;
 }
 
-// Map unit u to (b, h, s).  Each row contributes row_splits(len) splits per
+__device__ __forceinline__ int cascade_start(const SdpaArgs &a, int sq) {
+    return a.starts ? min(max(a.starts[sq], 0), a.S) : 0;
+}
+
+// Private keys of cascade row r: [start, S - qL + i] (end-aligned causal).
+__device__ __forceinline__ int cascade_len2(const SdpaArgs &a, int r) {
+    const int sq = r / a.qL, i = r - sq * a.qL;
+    return max(a.S - a.qL + i + 1 - cascade_start(a, sq), 0);
+}
+
+// Splits that map_unit hands out per (row, kv head): ragged mode, the row's
+// splits; cascade mode, the private slab's (the prefix units are counted
+// apart).  A row with no keys keeps one (empty) split.
+__device__ __forceinline__ int row_unit_splits(const SdpaArgs &a, int b) {
+    if (!a.cascade) return row_splits(max(min(a.row_len[b], a.max_len), 0), a.split);
+    const int n2 = (cascade_len2(a, b) + a.split - 1) / a.split;
+    return a.n1 == 0 ? max(n2, 1) : n2;
+}
+
+// All splits of row b (the merge's count).
+__device__ __forceinline__ int row_nsplit(const SdpaArgs &a, int b) {
+    return a.cascade ? a.n1 + row_unit_splits(a, b) : row_unit_splits(a, b);
+}
+
+// Map unit u to (b, h, s).  Each row contributes row_unit_splits splits per
 // kv head.  Returns false when u is past the last unit.
-__device__ __forceinline__ bool map_unit(const SdpaArgs &a, int u, int &b, int &h, int &s, int &nsplit) {
+__device__ __forceinline__ bool map_unit(const SdpaArgs &a, int u, int &b, int &h, int &s) {
     const int lane = kq_lane();
     int base = 0;
     for (int c0 = 0; c0 < a.B; c0 += 64) {
         const int row = c0 + lane;
         int n = 0;
-        if (row < a.B) n = row_splits(min(a.row_len[row], a.max_len), a.split);
+        if (row < a.B) n = row_unit_splits(a, row);
         const int units = n * a.Hkv;
         int inc = units;  // inclusive scan across the wave
         for (int off = 1; off < 64; off <<= 1) {
@@ -90,7 +130,7 @@ __device__ __forceinline__ bool map_unit(const SdpaArgs &a, int u, int &b, int &
             const uint64_t hit = __ballot(row < a.B && u >= base + excl && u < base + inc);
             const int src = __builtin_ctzll(hit);
             b = c0 + src;
-            nsplit = __shfl(n, src);
+            const int nsplit = __shfl(n, src);
             const int local = u - base - __shfl(excl, src);
             h = local / nsplit;
             s = local - h * nsplit;
@@ -201,110 +241,164 @@ struct SplitState {
     }
 };
 
+// One split of one KV head over one token range [t_begin, t_end) of the
+// buffers kp/vp.  Lane l = 16g + r holds query vector r: row `row`, q head
+// h * G + head (ok == false: an idle column, its scores are -inf and it
+// stores nothing).  The wave reads each K/V tile once for all 16 columns.
 template <int D, bool BF>
-__global__ __launch_bounds__(64) void kq_sdpa_split_kernel(SdpaArgs a) {
+__device__ __forceinline__ void split_unit(const SdpaArgs &a, const uint16_t *kp, const uint16_t *vp, int t_begin,
+                                           int t_end, int h, int s, int row, int head, bool ok) {
     constexpr int NC = D / 32;
     constexpr int NG = (D + 127) / 128;
     // D = 256 tiles are 128 VGPRs: one buffer only
     constexpr bool kDouble = D <= 128;
     const int lane = kq_lane();
-    const int r = lane & 15, g = lane >> 4;
+    const int g = lane >> 4;
+    const int hq = h * a.G + head;
 
-    for (int u = blockIdx.x;; u += gridDim.x) {
-        int b, h, s, nsplit;
-        if (!map_unit(a, u, b, h, s, nsplit)) return;
-        // rows longer than max_len are clamped to it (the workspace holds
-        // max_len / split splits per (row, head))
-        const int len = max(min(a.row_len[b], a.max_len), 0);
-        const int t_begin = s * a.split;
-        const int t_end = min(len, t_begin + a.split);
-        const int64_t kvbase = a.kv_off[b] + (int64_t)h * a.head_stride[b];
-        const uint16_t *kp = a.k + kvbase;
-        const uint16_t *vp = a.v + kvbase;
-        const bool head_ok = r < a.G;
-        const int hq = h * a.G + (head_ok ? r : 0);
+    SplitState<D, BF> st;
+    // q^T fragments: lane (column r, group g) holds q[32c + 8g .. +7]
+    const uint16_t *qp = a.q + qo_index(a, row, hq) * D;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) st.qf[c] = __builtin_bit_cast(half8_t, *(const u32x4 *)(qp + 32 * c + 8 * g));
+    if (!ok) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) st.qf[c] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int dg = 0; dg < NG; ++dg)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) st.o[dg][j] = floatx4{0, 0, 0, 0};
+    st.m_run = -INFINITY;
+    st.l_part = 0.f;
 
-        SplitState<D, BF> st;
-        // q^T fragments: lane (head r, group g) holds q[hq][32c + 8g .. +7]
-#pragma unroll
-        for (int c = 0; c < NC; ++c)
-            st.qf[c] = __builtin_bit_cast(half8_t, *(const u32x4 *)(a.q + ((int64_t)b * a.Hq + hq) * D + 32 * c + 8 * g));
-        if (!head_ok) {
-#pragma unroll
-            for (int c = 0; c < NC; ++c) st.qf[c] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
-        }
-#pragma unroll
-        for (int dg = 0; dg < NG; ++dg)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) st.o[dg][j] = floatx4{0, 0, 0, 0};
-        st.m_run = -INFINITY;
-        st.l_part = 0.f;
-
-        if (t_end > t_begin) {  // wave-uniform
-            if constexpr (kDouble) {
-                KVTile<D> ta, tb;
-                ta.load(kp, vp, t_begin, t_end);
-                for (int t0 = t_begin; t0 < t_end; t0 += 64) {
-                    const bool more = t0 + 32 < t_end;
-                    if (more) tb.load(kp, vp, t0 + 32, t_end);
-                    __builtin_amdgcn_sched_barrier(0);
-                    st.tile(ta, t0, t_end, head_ok, a.scale_log2);
-                    if (!more) break;
-                    if (t0 + 64 < t_end) ta.load(kp, vp, t0 + 64, t_end);
-                    __builtin_amdgcn_sched_barrier(0);
-                    st.tile(tb, t0 + 32, t_end, head_ok, a.scale_log2);
-                }
-            } else {
-                KVTile<D> ta;
-                for (int t0 = t_begin; t0 < t_end; t0 += 32) {
-                    ta.load(kp, vp, t0, t_end);
-                    st.tile(ta, t0, t_end, head_ok, a.scale_log2);
-                }
+    if (t_end > t_begin) {  // wave-uniform
+        if constexpr (kDouble) {
+            KVTile<D> ta, tb;
+            ta.load(kp, vp, t_begin, t_end);
+            for (int t0 = t_begin; t0 < t_end; t0 += 64) {
+                const bool more = t0 + 32 < t_end;
+                if (more) tb.load(kp, vp, t0 + 32, t_end);
+                __builtin_amdgcn_sched_barrier(0);
+                st.tile(ta, t0, t_end, ok, a.scale_log2);
+                if (!more) break;
+                if (t0 + 64 < t_end) ta.load(kp, vp, t0 + 64, t_end);
+                __builtin_amdgcn_sched_barrier(0);
+                st.tile(tb, t0 + 32, t_end, ok, a.scale_log2);
+            }
+        } else {
+            KVTile<D> ta;
+            for (int t0 = t_begin; t0 < t_end; t0 += 32) {
+                ta.load(kp, vp, t0, t_end);
+                st.tile(ta, t0, t_end, ok, a.scale_log2);
             }
         }
+    }
 
-        // Lane (head r, g) now holds O[hq][d] for d = 128*dg + 32*g + 8*e + j
-        // (element e of o[dg][j]); l is split over the 4 lanes of a head.
-        float l_tot = st.l_part + __shfl_xor(st.l_part, 16);
-        l_tot += __shfl_xor(l_tot, 32);
-        if (!head_ok) continue;
+    // Lane (column r, g) now holds O[d] for d = 128*dg + 32*g + 8*e + j
+    // (element e of o[dg][j]); l is split over the 4 lanes of a column.
+    float l_tot = st.l_part + __shfl_xor(st.l_part, 16);
+    l_tot += __shfl_xor(l_tot, 32);
+    if (!ok) return;
 
-        if (nsplit == 1) {
-            const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-            uint16_t *op = a.out + ((int64_t)b * a.Hq + hq) * D;
-#pragma unroll
-            for (int dg = 0; dg < NG; ++dg)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int d0 = 128 * dg + 32 * g + 8 * e;
-                    if (d0 >= D) continue;
-                    u32x4 w;
-                    w.x = (uint32_t)from_f32<BF>(st.o[dg][0][e] * inv) | ((uint32_t)from_f32<BF>(st.o[dg][1][e] * inv) << 16);
-                    w.y = (uint32_t)from_f32<BF>(st.o[dg][2][e] * inv) | ((uint32_t)from_f32<BF>(st.o[dg][3][e] * inv) << 16);
-                    w.z = (uint32_t)from_f32<BF>(st.o[dg][4][e] * inv) | ((uint32_t)from_f32<BF>(st.o[dg][5][e] * inv) << 16);
-                    w.w = (uint32_t)from_f32<BF>(st.o[dg][6][e] * inv) | ((uint32_t)from_f32<BF>(st.o[dg][7][e] * inv) << 16);
-                    *(u32x4 *)(op + d0) = w;
-                }
-            continue;
-        }
-
-        // ---- split partial: O (unnormalised), m, l
-        const int64_t slot = ((int64_t)b * a.Hkv + h) * a.max_splits + s;
-        float *po = a.part + (slot * a.G + r) * D;
+    if (row_nsplit(a, row) == 1) {
+        const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+        uint16_t *op = a.out + qo_index(a, row, hq) * D;
 #pragma unroll
         for (int dg = 0; dg < NG; ++dg)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int d0 = 128 * dg + 32 * g + 8 * e;
                 if (d0 >= D) continue;
-                float4 *dst = (float4 *)(po + d0);
-                dst[0] = make_float4(st.o[dg][0][e], st.o[dg][1][e], st.o[dg][2][e], st.o[dg][3][e]);
-                dst[1] = make_float4(st.o[dg][4][e], st.o[dg][5][e], st.o[dg][6][e], st.o[dg][7][e]);
+                u32x4 w;
+                w.x = (uint32_t)from_f32<BF>(st.o[dg][0][e] * inv) | ((uint32_t)from_f32<BF>(st.o[dg][1][e] * inv) << 16);
+                w.y = (uint32_t)from_f32<BF>(st.o[dg][2][e] * inv) | ((uint32_t)from_f32<BF>(st.o[dg][3][e] * inv) << 16);
+                w.z = (uint32_t)from_f32<BF>(st.o[dg][4][e] * inv) | ((uint32_t)from_f32<BF>(st.o[dg][5][e] * inv) << 16);
+                w.w = (uint32_t)from_f32<BF>(st.o[dg][6][e] * inv) | ((uint32_t)from_f32<BF>(st.o[dg][7][e] * inv) << 16);
+                *(u32x4 *)(op + d0) = w;
             }
-        if (g == 0) {
-            float *pml = a.ml + (slot * a.G + r) * 2;
-            pml[0] = st.m_run;
-            pml[1] = l_tot;
+        return;
+    }
+
+    // ---- split partial: O (unnormalised), m, l
+    const int64_t slot = ((int64_t)row * a.Hkv + h) * a.max_splits + s;
+    float *po = a.part + (slot * a.G + head) * D;
+#pragma unroll
+    for (int dg = 0; dg < NG; ++dg)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int d0 = 128 * dg + 32 * g + 8 * e;
+            if (d0 >= D) continue;
+            float4 *dst = (float4 *)(po + d0);
+            dst[0] = make_float4(st.o[dg][0][e], st.o[dg][1][e], st.o[dg][2][e], st.o[dg][3][e]);
+            dst[1] = make_float4(st.o[dg][4][e], st.o[dg][5][e], st.o[dg][6][e], st.o[dg][7][e]);
+        }
+    if (g == 0) {
+        float *pml = a.ml + (slot * a.G + head) * 2;
+        pml[0] = st.m_run;
+        pml[1] = l_tot;
+    }
+}
+
+// Ragged mode: unit = one wave = (row b, kv head h, split s), the G q heads
+// of the group in columns 0..G-1.
+template <int D, bool BF>
+__global__ __launch_bounds__(64) void kq_sdpa_split_kernel(SdpaArgs a) {
+    const int r = kq_lane() & 15;
+    for (int u = blockIdx.x;; u += gridDim.x) {
+        int b, h, s;
+        if (!map_unit(a, u, b, h, s)) return;
+        // rows longer than max_len are clamped to it (the workspace holds
+        // max_len / split splits per (row, head))
+        const int len = max(min(a.row_len[b], a.max_len), 0);
+        const int t_begin = s * a.split;
+        const int t_end = min(len, t_begin + a.split);
+        const int64_t kvbase = a.kv_off[b] + (int64_t)h * a.head_stride[b];
+        split_unit<D, BF>(a, a.k + kvbase, a.v + kvbase, t_begin, t_end, h, s, b, r < a.G ? r : 0, r < a.G);
+    }
+}
+
+// Cascade mode.  Units [0, U1): the shared prefix, unit = (kv head h, prefix
+// split s, block of R = 16 / G rows); the R rows' G heads fill the 16 MFMA
+// columns, so each prefix tile is read once per R rows, and consecutive
+// units (the row blocks of one (h, s)) run on one XCD, where they share L2.
+// Units [U1, ...): the private slab, one wave per (row, h, split) as in
+// ragged mode; splits 0..n1-1 of a row are the prefix's, n1.. the slab's.
+template <int D, bool BF>
+__global__ __launch_bounds__(64) void kq_sdpa_cascade_kernel(SdpaArgs a) {
+    const int r = kq_lane() & 15;
+    const int R = 16 / a.G;
+    const int nrb = (a.B + R - 1) / R;
+    const int64_t U1 = (int64_t)a.Hkv * a.n1 * nrb;
+    // workgroups are dispatched to the 8 XCDs round robin: renumber so that
+    // the first pass of the grid hands each XCD a contiguous run of units
+    const int per_xcd = gridDim.x / 8;
+    const int first = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    for (int64_t u = first;; u += gridDim.x) {
+        if (u < U1) {
+            const int rb = (int)(u % nrb);
+            const int64_t hs = u / nrb;
+            const int s = (int)(hs % a.n1), h = (int)(hs / a.n1);
+            const int jr = r / a.G;
+            const int row = rb * R + jr;
+            const bool ok = jr < R && row < a.B;
+            const int64_t kvbase = (int64_t)h * a.shared_head_stride;
+            const int t_begin = s * a.split;
+            split_unit<D, BF>(a, a.k + kvbase, a.v + kvbase, t_begin, min(a.P, t_begin + a.split), h, s,
+                              ok ? row : 0, ok ? r - jr * a.G : 0, ok);
+        } else {
+            const int64_t u2 = u - U1;
+            if (u2 >= (int64_t)1 << 30) return;
+            int b, h, s;
+            if (!map_unit(a, (int)u2, b, h, s)) return;
+            const int sq = b / a.qL;
+            const int st = cascade_start(a, sq);
+            const int t_begin = s * a.split;
+            const int t_end = min(cascade_len2(a, b), t_begin + a.split);
+            const int64_t kvbase = (int64_t)sq * a.priv_batch_stride + (int64_t)h * a.priv_head_stride +
+                                   (int64_t)st * D;
+            split_unit<D, BF>(a, a.k2 + kvbase, a.v2 + kvbase, t_begin, t_end, h, a.n1 + s, b,
+                              r < a.G ? r : 0, r < a.G);
         }
     }
 }
@@ -322,8 +416,7 @@ __global__ __launch_bounds__(256) void kq_sdpa_merge_kernel(SdpaArgs a) {
     __shared__ float red_l[P];
     const int b = blockIdx.x / a.Hq;
     const int hq = blockIdx.x - b * a.Hq;
-    const int len = max(min(a.row_len[b], a.max_len), 0);
-    const int nsplit = row_splits(len, a.split);
+    const int nsplit = row_nsplit(a, b);
     if (nsplit == 1) return;  // uniform over the workgroup
     const int h = hq / a.G, r = hq - h * a.G;
     const int t = threadIdx.x;
@@ -363,7 +456,7 @@ __global__ __launch_bounds__(256) void kq_sdpa_merge_kernel(SdpaArgs a) {
         L += red_l[q];
     }
     const float inv = L > 0.f ? 1.f / L : 0.f;
-    a.out[((int64_t)b * a.Hq + hq) * D + d] = from_f32<BF>(acc * inv);
+    a.out[qo_index(a, b, hq) * D + d] = from_f32<BF>(acc * inv);
 }
 
 int env_int(const char *name, int dflt) {
@@ -397,7 +490,10 @@ WsLayout ws_layout(int B, int Hq, int Hkv, int D, int max_len) {
 
 template <int D, bool BF>
 void launch(const SdpaArgs &a, int grid, bool merge, hipStream_t s) {
-    hipLaunchKernelGGL((kq_sdpa_split_kernel<D, BF>), dim3(grid), dim3(64), 0, s, a);
+    if (a.cascade)
+        hipLaunchKernelGGL((kq_sdpa_cascade_kernel<D, BF>), dim3(grid), dim3(64), 0, s, a);
+    else
+        hipLaunchKernelGGL((kq_sdpa_split_kernel<D, BF>), dim3(grid), dim3(64), 0, s, a);
     if (merge) hipLaunchKernelGGL((kq_sdpa_merge_kernel<D, BF>), dim3(a.B * a.Hq), dim3(256), 0, s, a);
 }
 
@@ -434,6 +530,11 @@ int kq_sdpa_decode_ragged(const void *q, const void *k, const void *v, const int
     a.kv_off = kv_off;
     a.head_stride = head_stride;
     a.row_len = row_len;
+    a.starts = nullptr;
+    a.k2 = a.v2 = nullptr;
+    a.shared_head_stride = a.priv_batch_stride = a.priv_head_stride = 0;
+    a.cascade = a.P = a.S = a.n1 = 0;
+    a.qL = 1;
     a.part = (float *)workspace;
     a.ml = (float *)((char *)workspace + w.part_bytes);
     a.B = B;
@@ -456,6 +557,91 @@ int kq_sdpa_decode_ragged(const void *q, const void *k, const void *v, const int
     case 96: bf ? launch<96, true>(a, grid, merge, s) : launch<96, false>(a, grid, merge, s); break;
     case 128: bf ? launch<128, true>(a, grid, merge, s) : launch<128, false>(a, grid, merge, s); break;
     default: bf ? launch<256, true>(a, grid, merge, s) : launch<256, false>(a, grid, merge, s); break;
+    }
+    return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
+}
+
+// Cascade splits per (row, kv head): the prefix's, then the private slab's.
+static int cascade_max_splits(int P, int S) {
+    const int C = split_tokens();
+    const int n = (P + C - 1) / C + (S + C - 1) / C;
+    return n > 0 ? n : 1;
+}
+
+size_t kq_sdpa_cascade_workspace_bytes(int32_t B, int32_t qL, int32_t Hq, int32_t Hkv, int32_t D, int32_t P,
+                                       int32_t S) {
+    if (B <= 0 || qL <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv || D <= 0 || P < 0 || S < 0) return 0;
+    const int64_t slots = (int64_t)B * qL * Hkv * cascade_max_splits(P, S) * (Hq / Hkv);
+    return (((size_t)slots * D * 4 + 255) & ~(size_t)255) + (size_t)slots * 2 * 4;
+}
+
+int kq_sdpa_decode_gqa_cascade(const void *q, const void *k_shared, const void *v_shared,
+                               int64_t shared_head_stride, int32_t P, const void *k_priv, const void *v_priv,
+                               int64_t priv_batch_stride, int64_t priv_head_stride, int32_t S,
+                               const int32_t *starts, int32_t B, int32_t qL, int32_t Hq, int32_t Hkv, int32_t D,
+                               float scale, int dtype, void *out, void *workspace, size_t workspace_bytes,
+                               kq_stream_t stream) {
+    if (B == 0) return KQ_OK;
+    if (!q || !k_shared || !v_shared || !k_priv || !v_priv || !out) return KQ_ERR_NULL_POINTER;
+    if (B < 0 || qL < 1 || qL > 64 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || Hq / Hkv > 16 || P < 0 || S < 0)
+        return KQ_ERR_BAD_SHAPE;
+    if (D != 64 && D != 96 && D != 128 && D != 256) return KQ_ERR_BAD_SHAPE;
+    if ((int64_t)B * qL * Hq > (1 << 24)) return KQ_ERR_BAD_SHAPE;
+    if (shared_head_stride < (int64_t)P * D || priv_head_stride < (int64_t)S * D ||
+        priv_batch_stride < priv_head_stride * Hkv)
+        return KQ_ERR_BAD_SHAPE;
+    if (dtype != KQ_DTYPE_F16 && dtype != KQ_DTYPE_BF16) return KQ_ERR_UNSUPPORTED_DTYPE;
+    if (((uintptr_t)q & 15) || ((uintptr_t)k_shared & 15) || ((uintptr_t)v_shared & 15) ||
+        ((uintptr_t)k_priv & 15) || ((uintptr_t)v_priv & 15) || ((uintptr_t)out & 15) ||
+        (shared_head_stride & 7) || (priv_head_stride & 7) || (priv_batch_stride & 7))
+        return KQ_ERR_BAD_ALIGN;
+    const size_t need = kq_sdpa_cascade_workspace_bytes(B, qL, Hq, Hkv, D, P, S);
+    if (!workspace || workspace_bytes < need) return KQ_ERR_WORKSPACE_TOO_SMALL;
+    const int rows = B * qL;
+    SdpaArgs a;
+    a.q = (const uint16_t *)q;
+    a.k = (const uint16_t *)k_shared;
+    a.v = (const uint16_t *)v_shared;
+    a.out = (uint16_t *)out;
+    a.kv_off = a.head_stride = nullptr;
+    a.row_len = nullptr;
+    a.starts = starts;
+    a.k2 = (const uint16_t *)k_priv;
+    a.v2 = (const uint16_t *)v_priv;
+    a.shared_head_stride = shared_head_stride;
+    a.priv_batch_stride = priv_batch_stride;
+    a.priv_head_stride = priv_head_stride;
+    a.cascade = 1;
+    a.P = P;
+    a.S = S;
+    a.qL = qL;
+    a.B = rows;
+    a.Hq = Hq;
+    a.Hkv = Hkv;
+    a.G = Hq / Hkv;
+    a.split = split_tokens();
+    a.n1 = (P + a.split - 1) / a.split;
+    a.max_splits = cascade_max_splits(P, S);
+    a.max_len = P > S ? P : S;
+    a.part = (float *)workspace;
+    const int64_t slots = (int64_t)rows * Hkv * a.max_splits * a.G;
+    a.ml = (float *)((char *)workspace + (((size_t)slots * D * 4 + 255) & ~(size_t)255));
+    a.scale_log2 = scale * 1.4426950408889634f;
+    // prefix units + private units (an upper bound; extra waves exit at
+    // once), a multiple of 8 for the XCD renumbering
+    const int R = 16 / a.G;
+    const int64_t upper = (int64_t)Hkv * a.n1 * ((rows + R - 1) / R) +
+                          (int64_t)rows * Hkv * (a.max_splits - a.n1 > 0 ? a.max_splits - a.n1 : 1);
+    int64_t grid = upper < (1 << 22) ? upper : (1 << 22);
+    grid = (grid + 7) / 8 * 8;
+    const bool merge = a.max_splits > 1;
+    const bool bf = dtype == KQ_DTYPE_BF16;
+    hipStream_t s = (hipStream_t)stream;
+    switch (D) {
+    case 64: bf ? launch<64, true>(a, (int)grid, merge, s) : launch<64, false>(a, (int)grid, merge, s); break;
+    case 96: bf ? launch<96, true>(a, (int)grid, merge, s) : launch<96, false>(a, (int)grid, merge, s); break;
+    case 128: bf ? launch<128, true>(a, (int)grid, merge, s) : launch<128, false>(a, (int)grid, merge, s); break;
+    default: bf ? launch<256, true>(a, (int)grid, merge, s) : launch<256, false>(a, (int)grid, merge, s); break;
     }
     return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
 }

@@ -521,3 +521,109 @@ def ragged_decode_attention(queries, keys, values, pads, scale):
     out = torch.empty_like(q3)
     _sdpa_launch(q3, k, v, tabs, Hkv, scale, L, out)
     return out.reshape(B, Hq, 1, D)
+
+
+_STARTS = OrderedDict()  # memoised device starts rows for host sequences
+
+
+def _starts_table(device, starts):
+    key = (str(device), tuple(starts))
+    hit = _STARTS.get(key)
+    if hit is not None:
+        _STARTS.move_to_end(key)
+        return hit
+    t = torch.tensor(key[1], dtype=torch.int32, device=device)
+    _STARTS[key] = t
+    if len(_STARTS) > 128:
+        _STARTS.popitem(last=False)
+    return t
+
+
+def _kv_pair(k, v, name):
+    """k/v as views whose tokens are D contiguous elements and which share
+    strides; copies only when they do not."""
+    D = k.shape[-1]
+    if k.stride(3) != 1 or k.stride(2) != D:
+        k = k.contiguous()
+    if v.stride() != k.stride():
+        v = v.contiguous()
+        if v.stride() != k.stride():
+            k = k.contiguous()
+    if any(int(x) % 8 for x in k.stride()[:2]) or k.data_ptr() % 16 or v.data_ptr() % 16:
+        k, v = k.contiguous(), v.contiguous()
+        if k.data_ptr() % 16 or v.data_ptr() % 16:
+            raise ValueError(f"{name}: K/V must be 16-byte aligned")
+    return k, v
+
+
+def sdpa_decode_gqa_cascade(queries, k_shared, v_shared, k_priv, v_priv, scale, starts=None,
+                            **quant_kv):
+    """kq.sdpa_decode_gqa_cascade (gmlx/cascade_sdpa.py:238-248): decode with a
+    prefix shared by every sequence, held once.
+
+    queries (B, Hq, qL, D); k_shared/v_shared (1, Hkv, P, D), the common
+    prefix; k_priv/v_priv (B, Hkv, S, D), each sequence's keys after it.
+    Query token i of sequence b attends the whole prefix and private keys
+    [starts[b], S - qL + i] (left padding plus the end-aligned causal mask of
+    a verify block, qL 2..8 in the reference).  `starts` is an int32 device
+    tensor (read on the device, no host sync) or a host sequence; None = 0.
+    Strided views (slices of a larger cache, as the reference passes) are
+    used in place when the last two dims are contiguous.  Returns
+    (B, Hq, qL, D) in the queries' dtype.  The reference's affine-quantised
+    KV form (the *_scales / *_biases keywords) is not implemented here and
+    raises NotImplementedError, which the reference's claim treats as a
+    decline."""
+    if quant_kv:
+        raise NotImplementedError("sdpa_decode_gqa_cascade: quantised KV is not supported")
+    _fault("sdpa_decode_gqa_cascade")
+    _require_gpu(queries, k_shared, v_shared, k_priv, v_priv)
+    if queries.dim() != 4 or k_shared.dim() != 4 or k_priv.dim() != 4:
+        raise ValueError("queries, k_shared, k_priv must be 4-D")
+    B, Hq, qL, D = queries.shape
+    dt = queries.dtype
+    if dt not in (torch.float16, torch.bfloat16) or any(t.dtype != dt for t in (k_shared, v_shared, k_priv, v_priv)):
+        raise ValueError("queries and K/V must share dtype float16 or bfloat16")
+    if tuple(v_shared.shape) != tuple(k_shared.shape) or tuple(v_priv.shape) != tuple(k_priv.shape):
+        raise ValueError("K and V shapes differ")
+    if k_shared.shape[0] != 1 or k_priv.shape[0] != B:
+        raise ValueError("k_shared must have batch 1 and k_priv batch B")
+    Hkv, P = k_shared.shape[1], k_shared.shape[2]
+    S = k_priv.shape[2]
+    if k_priv.shape[1] != Hkv or k_shared.shape[3] != D or k_priv.shape[3] != D:
+        raise ValueError("head count / head dim mismatch")
+    if Hq % Hkv or Hq // Hkv > 16 or D not in (64, 96, 128, 256) or not 1 <= qL <= 64:
+        raise ValueError("unsupported cascade shape")
+    if S < qL:
+        raise ValueError("the private slab must hold the query block (S >= qL)")
+    ks, vs = _kv_pair(k_shared, v_shared, "sdpa_decode_gqa_cascade")
+    kp, vp = _kv_pair(k_priv, v_priv, "sdpa_decode_gqa_cascade")
+    if starts is None:
+        st = None
+    elif isinstance(starts, torch.Tensor):
+        st = starts
+        if not st.is_cuda:
+            st = _starts_table(queries.device, [int(x) for x in st.tolist()])
+        elif st.dtype != torch.int32 or not st.is_contiguous():
+            st = st.to(torch.int32).contiguous()
+        if st.numel() < B:
+            raise ValueError("one start per sequence")
+    else:
+        st = _starts_table(queries.device, [int(x) for x in starts])
+        if st.numel() < B:
+            raise ValueError("one start per sequence")
+    q = queries.contiguous()
+    out = torch.empty_like(q)
+    L = lib()
+    need = L.kq_sdpa_cascade_workspace_bytes(B, qL, Hq, Hkv, D, P, S)
+    s = _stream(q)
+    ws = _WS.get("sdpa_cascade", q.device, s.value, need)
+    # strides of size-1 dims are never used: give them their packed values
+    shs = ks.stride(1) if Hkv > 1 else P * D
+    phs = kp.stride(1) if Hkv > 1 else S * D
+    pbs = kp.stride(0) if B > 1 else Hkv * phs
+    rc = L.kq_sdpa_decode_gqa_cascade(
+        q.data_ptr(), ks.data_ptr(), vs.data_ptr(), shs, P, kp.data_ptr(), vp.data_ptr(),
+        pbs, phs, S, None if st is None else st.data_ptr(), B, qL, Hq, Hkv, D,
+        float(scale), _dt(dt), out.data_ptr(), ws.data_ptr(), ws.numel(), s)
+    check("kq_sdpa_decode_gqa_cascade", rc)
+    return out

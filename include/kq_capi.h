@@ -195,6 +195,31 @@ int kq_sdpa_decode_ragged(const void *q, const void *k, const void *v, const int
                           int dtype, void *out, void *workspace, size_t workspace_bytes,
                           kq_stream_t stream);
 
+/* ---- cascade (shared-prefix) decode attention ---------------------------- */
+/* kq.sdpa_decode_gqa_cascade(q, k_shared, v_shared, k_priv, v_priv, scale,
+ * starts=) as called at gmlx/cascade_sdpa.py:238-248 (claim gates :171-215):
+ * B sequences share a prefix of P tokens held once; each has a private slab
+ * of S tokens after it.  Query token i < qL of sequence b attends
+ *   the whole prefix k_shared/v_shared [Hkv, P, D] (element h * shared_head_stride
+ *   + t * D), then private keys [starts[b], S - qL + i] of k_priv/v_priv
+ *   (element b * priv_batch_stride + h * priv_head_stride + t * D):
+ * left padding plus the end-aligned causal mask of the query block.
+ * starts == NULL means 0 for every sequence; starts are clamped to [0, S].
+ * q, out [B, Hq, qL, D] contiguous; all tensors share dtype (f16 or bf16).
+ * qL in 1..64, D in {64, 96, 128, 256}, Hq % Hkv == 0, Hq/Hkv <= 16.
+ * Each prefix tile is loaded once per 16 / (Hq/Hkv) query rows (the rows'
+ * heads share the MFMA's 16 columns), so the prefix costs P, not B * P,
+ * bytes per head in the common case (B * qL * Hq / Hkv <= 16). */
+size_t kq_sdpa_cascade_workspace_bytes(int32_t B, int32_t qL, int32_t Hq, int32_t Hkv, int32_t D,
+                                       int32_t P, int32_t S);
+int kq_sdpa_decode_gqa_cascade(const void *q, const void *k_shared, const void *v_shared,
+                               int64_t shared_head_stride, int32_t P, const void *k_priv,
+                               const void *v_priv, int64_t priv_batch_stride,
+                               int64_t priv_head_stride, int32_t S, const int32_t *starts,
+                               int32_t B, int32_t qL, int32_t Hq, int32_t Hkv, int32_t D,
+                               float scale, int dtype, void *out, void *workspace,
+                               size_t workspace_bytes, kq_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
