@@ -22,6 +22,13 @@
 //     the splits to the common max and sums them in split order (the
 //     two-pass merge of gmlx/qwen35_attn.py:255-282), so the result does not
 //     depend on scheduling.
+// Cascade mode (kq.sdpa_decode_gqa_cascade, gmlx/cascade_sdpa.py:136-260):
+// a prefix shared by all sequences plus a private slab per sequence, and qL
+// query tokens per sequence (rows).  A prefix unit puts 16 / G rows' heads
+// in the 16 MFMA columns and the row blocks of one prefix split run as the
+// waves of one workgroup, so each prefix tile is fetched from HBM about
+// once for all rows; private splits are ragged-mode units.  The merge sees
+// one split list per row: prefix splits, then private ones.
 // No cross-workgroup synchronisation happens inside a launch.
 #include "kq_common.h"
 
@@ -40,6 +47,7 @@ struct SdpaArgs {
     const uint16_t *k2, *v2;
     int64_t shared_head_stride, priv_batch_stride, priv_head_stride;
     int32_t cascade, P, S, n1;  // n1 = prefix splits of every row
+    int32_t split1;             // tokens per prefix split
     float *part;          // [B][Hkv][max_splits][G][D] O partials
     float *ml;            // [B][Hkv][max_splits][G][2] (m, l)
     int32_t B, Hq, Hkv, G, split, max_splits, max_len;
@@ -245,13 +253,11 @@ struct SplitState {
 // buffers kp/vp.  Lane l = 16g + r holds query vector r: row `row`, q head
 // h * G + head (ok == false: an idle column, its scores are -inf and it
 // stores nothing).  The wave reads each K/V tile once for all 16 columns.
-template <int D, bool BF>
+template <int D, bool BF, int NBUF>
 __device__ __forceinline__ void split_unit(const SdpaArgs &a, const uint16_t *kp, const uint16_t *vp, int t_begin,
                                            int t_end, int h, int s, int row, int head, bool ok) {
     constexpr int NC = D / 32;
     constexpr int NG = (D + 127) / 128;
-    // D = 256 tiles are 128 VGPRs: one buffer only
-    constexpr bool kDouble = D <= 128;
     const int lane = kq_lane();
     const int g = lane >> 4;
     const int hq = h * a.G + head;
@@ -273,24 +279,18 @@ __device__ __forceinline__ void split_unit(const SdpaArgs &a, const uint16_t *kp
     st.l_part = 0.f;
 
     if (t_end > t_begin) {  // wave-uniform
-        if constexpr (kDouble) {
-            KVTile<D> ta, tb;
-            ta.load(kp, vp, t_begin, t_end);
-            for (int t0 = t_begin; t0 < t_end; t0 += 64) {
-                const bool more = t0 + 32 < t_end;
-                if (more) tb.load(kp, vp, t0 + 32, t_end);
+        // Ring of NBUF tiles: tile j + NBUF - 1 is loaded while tile j is
+        // multiplied.  Loads are issued unconditionally (tokens past t_end
+        // read the last valid token), so the wait counts are static.
+        KVTile<D> ring[NBUF];
+#pragma unroll
+        for (int j = 0; j < NBUF - 1; ++j) ring[j].load(kp, vp, t_begin + 32 * j, t_end);
+        for (int t0 = t_begin; t0 < t_end; t0 += 32 * NBUF) {
+#pragma unroll
+            for (int j = 0; j < NBUF; ++j) {
+                ring[(j + NBUF - 1) % NBUF].load(kp, vp, t0 + 32 * (j + NBUF - 1), t_end);
                 __builtin_amdgcn_sched_barrier(0);
-                st.tile(ta, t0, t_end, ok, a.scale_log2);
-                if (!more) break;
-                if (t0 + 64 < t_end) ta.load(kp, vp, t0 + 64, t_end);
-                __builtin_amdgcn_sched_barrier(0);
-                st.tile(tb, t0 + 32, t_end, ok, a.scale_log2);
-            }
-        } else {
-            KVTile<D> ta;
-            for (int t0 = t_begin; t0 < t_end; t0 += 32) {
-                ta.load(kp, vp, t0, t_end);
-                st.tile(ta, t0, t_end, ok, a.scale_log2);
+                if (t0 + 32 * j < t_end) st.tile(ring[j], t0 + 32 * j, t_end, ok, a.scale_log2);
             }
         }
     }
@@ -342,7 +342,7 @@ __device__ __forceinline__ void split_unit(const SdpaArgs &a, const uint16_t *kp
 
 // Ragged mode: unit = one wave = (row b, kv head h, split s), the G q heads
 // of the group in columns 0..G-1.
-template <int D, bool BF>
+template <int D, bool BF, int NBUF>
 __global__ __launch_bounds__(64) void kq_sdpa_split_kernel(SdpaArgs a) {
     const int r = kq_lane() & 15;
     for (int u = blockIdx.x;; u += gridDim.x) {
@@ -354,40 +354,42 @@ __global__ __launch_bounds__(64) void kq_sdpa_split_kernel(SdpaArgs a) {
         const int t_begin = s * a.split;
         const int t_end = min(len, t_begin + a.split);
         const int64_t kvbase = a.kv_off[b] + (int64_t)h * a.head_stride[b];
-        split_unit<D, BF>(a, a.k + kvbase, a.v + kvbase, t_begin, t_end, h, s, b, r < a.G ? r : 0, r < a.G);
+        split_unit<D, BF, NBUF>(a, a.k + kvbase, a.v + kvbase, t_begin, t_end, h, s, b, r < a.G ? r : 0,
+                                r < a.G);
     }
 }
 
-// Cascade mode.  Units [0, U1): the shared prefix, unit = (kv head h, prefix
-// split s, block of R = 16 / G rows); the R rows' G heads fill the 16 MFMA
-// columns, so each prefix tile is read once per R rows, and consecutive
-// units (the row blocks of one (h, s)) run on one XCD, where they share L2.
-// Units [U1, ...): the private slab, one wave per (row, h, split) as in
-// ragged mode; splits 0..n1-1 of a row are the prefix's, n1.. the slab's.
-template <int D, bool BF>
-__global__ __launch_bounds__(64) void kq_sdpa_cascade_kernel(SdpaArgs a) {
+// Cascade mode, W = blockDim / 64 waves per workgroup.
+//  - Workgroup units [0, Hkv * n1): the shared prefix, unit = (kv head h,
+//    prefix split s).  Wave w takes row blocks w, w + W, ... of R = 16 / G
+//    rows each: the block's R rows x G heads fill the 16 MFMA columns, and
+//    the W waves of one workgroup stream the same tiles on one CU, so a
+//    prefix tile comes from HBM about once for all rows.
+//  - Later workgroup units: the private slabs, W consecutive units (row,
+//    h, split) per workgroup, one per wave, as in ragged mode.  Splits
+//    0..n1-1 of a row are the prefix's, n1.. the slab's.
+template <int D, bool BF, int NBUF>
+__global__ __launch_bounds__(256) void kq_sdpa_cascade_kernel(SdpaArgs a) {
     const int r = kq_lane() & 15;
+    const int W = blockDim.x >> 6, w = threadIdx.x >> 6;
     const int R = 16 / a.G;
     const int nrb = (a.B + R - 1) / R;
-    const int64_t U1 = (int64_t)a.Hkv * a.n1 * nrb;
-    // workgroups are dispatched to the 8 XCDs round robin: renumber so that
-    // the first pass of the grid hands each XCD a contiguous run of units
-    const int per_xcd = gridDim.x / 8;
-    const int first = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-    for (int64_t u = first;; u += gridDim.x) {
-        if (u < U1) {
-            const int rb = (int)(u % nrb);
-            const int64_t hs = u / nrb;
-            const int s = (int)(hs % a.n1), h = (int)(hs / a.n1);
+    const int64_t U1 = (int64_t)a.Hkv * a.n1;
+    for (int64_t bu = blockIdx.x;; bu += gridDim.x) {
+        if (bu < U1) {
+            const int s = (int)(bu % a.n1), h = (int)(bu / a.n1);
             const int jr = r / a.G;
-            const int row = rb * R + jr;
-            const bool ok = jr < R && row < a.B;
             const int64_t kvbase = (int64_t)h * a.shared_head_stride;
-            const int t_begin = s * a.split;
-            split_unit<D, BF>(a, a.k + kvbase, a.v + kvbase, t_begin, min(a.P, t_begin + a.split), h, s,
-                              ok ? row : 0, ok ? r - jr * a.G : 0, ok);
+            const int t_begin = s * a.split1;
+            const int t_end = min(a.P, t_begin + a.split1);
+            for (int rb = w; rb < nrb; rb += W) {
+                const int row = rb * R + jr;
+                const bool ok = jr < R && row < a.B;
+                split_unit<D, BF, NBUF>(a, a.k + kvbase, a.v + kvbase, t_begin, t_end, h, s, ok ? row : 0,
+                                        ok ? r - jr * a.G : 0, ok);
+            }
         } else {
-            const int64_t u2 = u - U1;
+            const int64_t u2 = (bu - U1) * W + w;
             if (u2 >= (int64_t)1 << 30) return;
             int b, h, s;
             if (!map_unit(a, (int)u2, b, h, s)) return;
@@ -397,8 +399,8 @@ __global__ __launch_bounds__(64) void kq_sdpa_cascade_kernel(SdpaArgs a) {
             const int t_end = min(cascade_len2(a, b), t_begin + a.split);
             const int64_t kvbase = (int64_t)sq * a.priv_batch_stride + (int64_t)h * a.priv_head_stride +
                                    (int64_t)st * D;
-            split_unit<D, BF>(a, a.k2 + kvbase, a.v2 + kvbase, t_begin, t_end, h, a.n1 + s, b,
-                              r < a.G ? r : 0, r < a.G);
+            split_unit<D, BF, NBUF>(a, a.k2 + kvbase, a.v2 + kvbase, t_begin, t_end, h, a.n1 + s, b,
+                                    r < a.G ? r : 0, r < a.G);
         }
     }
 }
@@ -488,13 +490,21 @@ WsLayout ws_layout(int B, int Hq, int Hkv, int D, int max_len) {
     return w;
 }
 
-template <int D, bool BF>
-void launch(const SdpaArgs &a, int grid, bool merge, hipStream_t s) {
+template <int D, bool BF, int NBUF>
+void launch_n(const SdpaArgs &a, int grid, int block, bool merge, hipStream_t s) {
     if (a.cascade)
-        hipLaunchKernelGGL((kq_sdpa_cascade_kernel<D, BF>), dim3(grid), dim3(64), 0, s, a);
+        hipLaunchKernelGGL((kq_sdpa_cascade_kernel<D, BF, NBUF>), dim3(grid), dim3(block), 0, s, a);
     else
-        hipLaunchKernelGGL((kq_sdpa_split_kernel<D, BF>), dim3(grid), dim3(64), 0, s, a);
+        hipLaunchKernelGGL((kq_sdpa_split_kernel<D, BF, NBUF>), dim3(grid), dim3(64), 0, s, a);
     if (merge) hipLaunchKernelGGL((kq_sdpa_merge_kernel<D, BF>), dim3(a.B * a.Hq), dim3(256), 0, s, a);
+}
+
+// Tiles in flight per wave: 2 (D = 256 tiles are 128 VGPRs: 1).  Deeper
+// rings put tiles in AGPRs, whose copies wait for the loads: measured no
+// faster on the C3 ragged batch and the cascade shapes.
+template <int D, bool BF>
+void launch(const SdpaArgs &a, int grid, int block, bool merge, hipStream_t s) {
+    launch_n<D, BF, D == 256 ? 1 : 2>(a, grid, block, merge, s);
 }
 
 }  // namespace
@@ -533,7 +543,7 @@ int kq_sdpa_decode_ragged(const void *q, const void *k, const void *v, const int
     a.starts = nullptr;
     a.k2 = a.v2 = nullptr;
     a.shared_head_stride = a.priv_batch_stride = a.priv_head_stride = 0;
-    a.cascade = a.P = a.S = a.n1 = 0;
+    a.cascade = a.P = a.S = a.n1 = a.split1 = 0;
     a.qL = 1;
     a.part = (float *)workspace;
     a.ml = (float *)((char *)workspace + w.part_bytes);
@@ -553,25 +563,36 @@ int kq_sdpa_decode_ragged(const void *q, const void *k, const void *v, const int
     hipStream_t s = (hipStream_t)stream;
     const bool bf = dtype == KQ_DTYPE_BF16;
     switch (D) {
-    case 64: bf ? launch<64, true>(a, grid, merge, s) : launch<64, false>(a, grid, merge, s); break;
-    case 96: bf ? launch<96, true>(a, grid, merge, s) : launch<96, false>(a, grid, merge, s); break;
-    case 128: bf ? launch<128, true>(a, grid, merge, s) : launch<128, false>(a, grid, merge, s); break;
-    default: bf ? launch<256, true>(a, grid, merge, s) : launch<256, false>(a, grid, merge, s); break;
+    case 64: bf ? launch<64, true>(a, grid, 64, merge, s) : launch<64, false>(a, grid, 64, merge, s); break;
+    case 96: bf ? launch<96, true>(a, grid, 64, merge, s) : launch<96, false>(a, grid, 64, merge, s); break;
+    case 128: bf ? launch<128, true>(a, grid, 64, merge, s) : launch<128, false>(a, grid, 64, merge, s); break;
+    default: bf ? launch<256, true>(a, grid, 64, merge, s) : launch<256, false>(a, grid, 64, merge, s); break;
     }
     return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
 }
 
+// Tokens per prefix split (GMLX_KQ_CASCADE_SPLIT, else the ragged split).
+// Shorter prefix splits give more waves but cost partials
+// (rows * G * D * 4 bytes written and merged per split); measured on
+// B 2..16, P 16k-32k, 512 tokens was fastest.
+static int cascade_split1(int P, int rows, int Hkv, int G) {
+    (void)P, (void)rows, (void)Hkv, (void)G;
+    const int env = env_int("GMLX_KQ_CASCADE_SPLIT", 0);
+    if (env > 0) return env < 32 ? 32 : (env + 31) / 32 * 32;
+    return split_tokens();
+}
+
 // Cascade splits per (row, kv head): the prefix's, then the private slab's.
-static int cascade_max_splits(int P, int S) {
-    const int C = split_tokens();
-    const int n = (P + C - 1) / C + (S + C - 1) / C;
+static int cascade_max_splits(int P, int S, int rows, int Hkv, int G) {
+    const int C = split_tokens(), C1 = cascade_split1(P, rows, Hkv, G);
+    const int n = (P + C1 - 1) / C1 + (S + C - 1) / C;
     return n > 0 ? n : 1;
 }
 
 size_t kq_sdpa_cascade_workspace_bytes(int32_t B, int32_t qL, int32_t Hq, int32_t Hkv, int32_t D, int32_t P,
                                        int32_t S) {
     if (B <= 0 || qL <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv || D <= 0 || P < 0 || S < 0) return 0;
-    const int64_t slots = (int64_t)B * qL * Hkv * cascade_max_splits(P, S) * (Hq / Hkv);
+    const int64_t slots = (int64_t)B * qL * Hkv * cascade_max_splits(P, S, B * qL, Hkv, Hq / Hkv) * (Hq / Hkv);
     return (((size_t)slots * D * 4 + 255) & ~(size_t)255) + (size_t)slots * 2 * 4;
 }
 
@@ -620,28 +641,36 @@ int kq_sdpa_decode_gqa_cascade(const void *q, const void *k_shared, const void *
     a.Hkv = Hkv;
     a.G = Hq / Hkv;
     a.split = split_tokens();
-    a.n1 = (P + a.split - 1) / a.split;
-    a.max_splits = cascade_max_splits(P, S);
+    a.split1 = cascade_split1(P, rows, Hkv, a.G);
+    a.n1 = (P + a.split1 - 1) / a.split1;
+    a.max_splits = cascade_max_splits(P, S, rows, Hkv, a.G);
     a.max_len = P > S ? P : S;
     a.part = (float *)workspace;
     const int64_t slots = (int64_t)rows * Hkv * a.max_splits * a.G;
     a.ml = (float *)((char *)workspace + (((size_t)slots * D * 4 + 255) & ~(size_t)255));
     a.scale_log2 = scale * 1.4426950408889634f;
-    // prefix units + private units (an upper bound; extra waves exit at
-    // once), a multiple of 8 for the XCD renumbering
+    // W waves per workgroup: up to 4 row blocks of a prefix split share a
+    // workgroup.  Grid: the prefix's Hkv * n1 units, then the private
+    // units W at a time (an upper bound; extra waves exit at once).
     const int R = 16 / a.G;
-    const int64_t upper = (int64_t)Hkv * a.n1 * ((rows + R - 1) / R) +
-                          (int64_t)rows * Hkv * (a.max_splits - a.n1 > 0 ? a.max_splits - a.n1 : 1);
-    int64_t grid = upper < (1 << 22) ? upper : (1 << 22);
-    grid = (grid + 7) / 8 * 8;
+    const int nrb = (rows + R - 1) / R;
+    const int W = nrb < 4 ? nrb : 4;
+    const int64_t priv = (int64_t)rows * Hkv * (a.max_splits - a.n1 > 0 ? a.max_splits - a.n1 : 1);
+    const int64_t upper = (int64_t)Hkv * a.n1 + (priv + W - 1) / W;
+    const int grid = (int)(upper < (1 << 22) ? upper : (1 << 22));
+    const int block = 64 * W;
     const bool merge = a.max_splits > 1;
     const bool bf = dtype == KQ_DTYPE_BF16;
     hipStream_t s = (hipStream_t)stream;
     switch (D) {
-    case 64: bf ? launch<64, true>(a, (int)grid, merge, s) : launch<64, false>(a, (int)grid, merge, s); break;
-    case 96: bf ? launch<96, true>(a, (int)grid, merge, s) : launch<96, false>(a, (int)grid, merge, s); break;
-    case 128: bf ? launch<128, true>(a, (int)grid, merge, s) : launch<128, false>(a, (int)grid, merge, s); break;
-    default: bf ? launch<256, true>(a, (int)grid, merge, s) : launch<256, false>(a, (int)grid, merge, s); break;
+    case 64: bf ? launch<64, true>(a, grid, block, merge, s) : launch<64, false>(a, grid, block, merge, s); break;
+    case 96: bf ? launch<96, true>(a, grid, block, merge, s) : launch<96, false>(a, grid, block, merge, s); break;
+    case 128:
+        bf ? launch<128, true>(a, grid, block, merge, s) : launch<128, false>(a, grid, block, merge, s);
+        break;
+    default:
+        bf ? launch<256, true>(a, grid, block, merge, s) : launch<256, false>(a, grid, block, merge, s);
+        break;
     }
     return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
 }

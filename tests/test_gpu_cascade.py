@@ -135,10 +135,11 @@ def test_split_size_invariance(monkeypatch):
     kt, vt, qt = (torch.from_numpy(a).half().cuda() for a in (kb, vb, q))
     ref = _masked_ref(qt.float().cpu().numpy(), kt.float().cpu().numpy(), vt.float().cpu().numpy(), pads,
                       128 ** -0.5)
-    for split in ("32", "96", "512", "4096"):
+    for split, split1 in (("32", "0"), ("96", "64"), ("512", "0"), ("512", "1100"), ("4096", "2048")):
         monkeypatch.setenv("GMLX_KQ_SDPA_SPLIT", split)
+        monkeypatch.setenv("GMLX_KQ_CASCADE_SPLIT", split1)
         out = _cascade(torch, ops, qt, kt, vt, pads, P, 128 ** -0.5).float().cpu().numpy()
-        assert okq.max_rel(out, ref) <= TOL, split
+        assert okq.max_rel(out, ref) <= TOL, (split, split1)
 
 
 def test_rejects_bad_shapes():
@@ -153,3 +154,55 @@ def test_rejects_bad_shapes():
         ops.sdpa_decode_gqa_cascade(q[..., :80], ks[..., :80], ks[..., :80], kp[..., :80], kp[..., :80], 0.1)
     with pytest.raises(NotImplementedError):
         ops.sdpa_decode_gqa_cascade(q, ks, ks, kp, kp, 0.1, k_shared_scales=ks)
+
+
+# ------------------------------------------------ through the host route
+
+class _StampedCache:
+    def __init__(self, pads, P=None):
+        import torch
+        self.left_padding = torch.tensor(pads)
+        self._right_padding = None
+        if P is not None:
+            self._gmlx_cascade = {"P": P, "tok": ()}
+
+
+def _route_case(B, qL, pads, P=1024, sp=96, seed=21):
+    import torch
+    rng = np.random.default_rng(seed)
+    kb, vb, L = _shared_batch(rng, B, 8, P, sp, pads, 128, np.float32)
+    q = rng.normal(0, 1, size=(B, 16, qL, 128)).astype(np.float32)
+    kt, vt, qt = (torch.from_numpy(a).half().cuda() for a in (kb, vb, q))
+    ref = _masked_ref(qt.float().cpu().numpy(), kt.float().cpu().numpy(), vt.float().cpu().numpy(), pads, 0.125)
+    return qt, kt, vt, ref
+
+
+@pytest.mark.parametrize("qL,mask,pads", [(1, None, [0, 64, 128, 32]), (4, "causal", [0, 64, 32]),
+                                           (8, "causal", [0, 0, 0])])
+def test_route_claims_stamped_calls(qL, mask, pads):
+    from gmlx_amd import decode_route as dr
+
+    def stock(*a, **k):
+        raise AssertionError("a claimable stamped call fell through")
+
+    qt, kt, vt, ref = _route_case(len(pads), qL, pads)
+    route = dr.make_route(stock)
+    n0 = dr.claims()
+    out = route(qt, kt, vt, cache=_StampedCache(pads, P=1024), scale=0.125, mask=mask)
+    assert dr.claims() == n0 + 1
+    assert okq.max_rel(out.float().cpu().numpy(), ref) <= TOL
+
+
+def test_left_padded_route_order():
+    """Stamped batch: the cascade claims; unstamped: the ragged kernel runs.
+    Both agree with the masked reference."""
+    from gmlx_amd import decode_route as dr
+    pads = [0, 64, 128, 32]
+    qt, kt, vt, ref = _route_case(4, 1, pads)
+    n0 = dr.claims()
+    casc = dr.left_padded_attention(qt, kt, vt, cache=_StampedCache(pads, P=1024), scale=0.125)
+    assert dr.claims() == n0 + 1
+    rag = dr.left_padded_attention(qt, kt, vt, cache=_StampedCache(pads), scale=0.125)
+    assert dr.claims() == n0 + 1
+    for out in (casc, rag):
+        assert okq.max_rel(out.float().cpu().numpy(), ref) <= TOL
