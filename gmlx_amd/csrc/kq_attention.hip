@@ -250,33 +250,39 @@ struct SplitState {
 };
 
 // One split of one KV head over one token range [t_begin, t_end) of the
-// buffers kp/vp.  Lane l = 16g + r holds query vector r: row `row`, q head
-// h * G + head (ok == false: an idle column, its scores are -inf and it
-// stores nothing).  The wave reads each K/V tile once for all 16 columns.
-template <int D, bool BF, int NBUF>
+// buffers kp/vp, for NRB blocks of 16 query columns.  In block j, lane
+// l = 16g + r holds query vector r: row row[j], q head h * G + head[j]
+// (ok[j] == false: an idle column, its scores are -inf and it stores
+// nothing).  Each K/V tile is loaded once into registers and multiplied
+// for all NRB * 16 columns.
+template <int D, bool BF, int NBUF, int NRB>
 __device__ __forceinline__ void split_unit(const SdpaArgs &a, const uint16_t *kp, const uint16_t *vp, int t_begin,
-                                           int t_end, int h, int s, int row, int head, bool ok) {
+                                           int t_end, int h, int s, const int (&row)[NRB],
+                                           const int (&head)[NRB], const bool (&ok)[NRB]) {
     constexpr int NC = D / 32;
     constexpr int NG = (D + 127) / 128;
     const int lane = kq_lane();
     const int g = lane >> 4;
-    const int hq = h * a.G + head;
 
-    SplitState<D, BF> st;
-    // q^T fragments: lane (column r, group g) holds q[32c + 8g .. +7]
-    const uint16_t *qp = a.q + qo_index(a, row, hq) * D;
+    SplitState<D, BF> st[NRB];
 #pragma unroll
-    for (int c = 0; c < NC; ++c) st.qf[c] = __builtin_bit_cast(half8_t, *(const u32x4 *)(qp + 32 * c + 8 * g));
-    if (!ok) {
+    for (int j = 0; j < NRB; ++j) {
+        // q^T fragments: lane (column r, group g) holds q[32c + 8g .. +7]
+        const uint16_t *qp = a.q + qo_index(a, row[j], h * a.G + head[j]) * D;
 #pragma unroll
-        for (int c = 0; c < NC; ++c) st.qf[c] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+        for (int c = 0; c < NC; ++c)
+            st[j].qf[c] = __builtin_bit_cast(half8_t, *(const u32x4 *)(qp + 32 * c + 8 * g));
+        if (!ok[j]) {
+#pragma unroll
+            for (int c = 0; c < NC; ++c) st[j].qf[c] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int dg = 0; dg < NG; ++dg)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) st[j].o[dg][i] = floatx4{0, 0, 0, 0};
+        st[j].m_run = -INFINITY;
+        st[j].l_part = 0.f;
     }
-#pragma unroll
-    for (int dg = 0; dg < NG; ++dg)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) st.o[dg][j] = floatx4{0, 0, 0, 0};
-    st.m_run = -INFINITY;
-    st.l_part = 0.f;
 
     if (t_end > t_begin) {  // wave-uniform
         // Ring of NBUF tiles: tile j + NBUF - 1 is loaded while tile j is
@@ -290,53 +296,60 @@ __device__ __forceinline__ void split_unit(const SdpaArgs &a, const uint16_t *kp
             for (int j = 0; j < NBUF; ++j) {
                 ring[(j + NBUF - 1) % NBUF].load(kp, vp, t0 + 32 * (j + NBUF - 1), t_end);
                 __builtin_amdgcn_sched_barrier(0);
-                if (t0 + 32 * j < t_end) st.tile(ring[j], t0 + 32 * j, t_end, ok, a.scale_log2);
+                if (t0 + 32 * j < t_end) {
+#pragma unroll
+                    for (int k = 0; k < NRB; ++k) st[k].tile(ring[j], t0 + 32 * j, t_end, ok[k], a.scale_log2);
+                }
             }
         }
     }
 
-    // Lane (column r, g) now holds O[d] for d = 128*dg + 32*g + 8*e + j
-    // (element e of o[dg][j]); l is split over the 4 lanes of a column.
-    float l_tot = st.l_part + __shfl_xor(st.l_part, 16);
-    l_tot += __shfl_xor(l_tot, 32);
-    if (!ok) return;
-
-    if (row_nsplit(a, row) == 1) {
-        const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-        uint16_t *op = a.out + qo_index(a, row, hq) * D;
+#pragma unroll
+    for (int j = 0; j < NRB; ++j) {
+        // Lane (column r, g) now holds O[d] for d = 128*dg + 32*g + 8*e + i
+        // (element e of o[dg][i]); l is split over the 4 lanes of a column.
+        float l_tot = st[j].l_part + __shfl_xor(st[j].l_part, 16);
+        l_tot += __shfl_xor(l_tot, 32);
+        if (!ok[j]) continue;
+        const int hq = h * a.G + head[j];
+        if (row_nsplit(a, row[j]) == 1) {
+            const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+            uint16_t *op = a.out + qo_index(a, row[j], hq) * D;
+#pragma unroll
+            for (int dg = 0; dg < NG; ++dg)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int d0 = 128 * dg + 32 * g + 8 * e;
+                    if (d0 >= D) continue;
+                    const floatx4 *o = st[j].o[dg];
+                    u32x4 w;
+                    w.x = (uint32_t)from_f32<BF>(o[0][e] * inv) | ((uint32_t)from_f32<BF>(o[1][e] * inv) << 16);
+                    w.y = (uint32_t)from_f32<BF>(o[2][e] * inv) | ((uint32_t)from_f32<BF>(o[3][e] * inv) << 16);
+                    w.z = (uint32_t)from_f32<BF>(o[4][e] * inv) | ((uint32_t)from_f32<BF>(o[5][e] * inv) << 16);
+                    w.w = (uint32_t)from_f32<BF>(o[6][e] * inv) | ((uint32_t)from_f32<BF>(o[7][e] * inv) << 16);
+                    *(u32x4 *)(op + d0) = w;
+                }
+            continue;
+        }
+        // ---- split partial: O (unnormalised), m, l
+        const int64_t slot = ((int64_t)row[j] * a.Hkv + h) * a.max_splits + s;
+        float *po = a.part + (slot * a.G + head[j]) * D;
 #pragma unroll
         for (int dg = 0; dg < NG; ++dg)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int d0 = 128 * dg + 32 * g + 8 * e;
                 if (d0 >= D) continue;
-                u32x4 w;
-                w.x = (uint32_t)from_f32<BF>(st.o[dg][0][e] * inv) | ((uint32_t)from_f32<BF>(st.o[dg][1][e] * inv) << 16);
-                w.y = (uint32_t)from_f32<BF>(st.o[dg][2][e] * inv) | ((uint32_t)from_f32<BF>(st.o[dg][3][e] * inv) << 16);
-                w.z = (uint32_t)from_f32<BF>(st.o[dg][4][e] * inv) | ((uint32_t)from_f32<BF>(st.o[dg][5][e] * inv) << 16);
-                w.w = (uint32_t)from_f32<BF>(st.o[dg][6][e] * inv) | ((uint32_t)from_f32<BF>(st.o[dg][7][e] * inv) << 16);
-                *(u32x4 *)(op + d0) = w;
+                const floatx4 *o = st[j].o[dg];
+                float4 *dst = (float4 *)(po + d0);
+                dst[0] = make_float4(o[0][e], o[1][e], o[2][e], o[3][e]);
+                dst[1] = make_float4(o[4][e], o[5][e], o[6][e], o[7][e]);
             }
-        return;
-    }
-
-    // ---- split partial: O (unnormalised), m, l
-    const int64_t slot = ((int64_t)row * a.Hkv + h) * a.max_splits + s;
-    float *po = a.part + (slot * a.G + head) * D;
-#pragma unroll
-    for (int dg = 0; dg < NG; ++dg)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int d0 = 128 * dg + 32 * g + 8 * e;
-            if (d0 >= D) continue;
-            float4 *dst = (float4 *)(po + d0);
-            dst[0] = make_float4(st.o[dg][0][e], st.o[dg][1][e], st.o[dg][2][e], st.o[dg][3][e]);
-            dst[1] = make_float4(st.o[dg][4][e], st.o[dg][5][e], st.o[dg][6][e], st.o[dg][7][e]);
+        if (g == 0) {
+            float *pml = a.ml + (slot * a.G + head[j]) * 2;
+            pml[0] = st[j].m_run;
+            pml[1] = l_tot;
         }
-    if (g == 0) {
-        float *pml = a.ml + (slot * a.G + head) * 2;
-        pml[0] = st.m_run;
-        pml[1] = l_tot;
     }
 }
 
@@ -354,39 +367,49 @@ __global__ __launch_bounds__(64) void kq_sdpa_split_kernel(SdpaArgs a) {
         const int t_begin = s * a.split;
         const int t_end = min(len, t_begin + a.split);
         const int64_t kvbase = a.kv_off[b] + (int64_t)h * a.head_stride[b];
-        split_unit<D, BF, NBUF>(a, a.k + kvbase, a.v + kvbase, t_begin, t_end, h, s, b, r < a.G ? r : 0,
-                                r < a.G);
+        const int rw[1] = {b}, hd[1] = {r < a.G ? r : 0};
+        const bool ok[1] = {r < a.G};
+        split_unit<D, BF, NBUF, 1>(a, a.k + kvbase, a.v + kvbase, t_begin, t_end, h, s, rw, hd, ok);
     }
 }
 
 // Cascade mode, W = blockDim / 64 waves per workgroup.
 //  - Workgroup units [0, Hkv * n1): the shared prefix, unit = (kv head h,
-//    prefix split s).  Wave w takes row blocks w, w + W, ... of R = 16 / G
-//    rows each: the block's R rows x G heads fill the 16 MFMA columns, and
-//    the W waves of one workgroup stream the same tiles on one CU, so a
-//    prefix tile comes from HBM about once for all rows.
+//    prefix split s).  A row block is R = 16 / G rows whose G heads fill
+//    the 16 MFMA columns; a wave takes NRB row blocks and multiplies every
+//    prefix tile it loads for all of them, and wave w of the workgroup
+//    takes block groups w, w + W, ...  With nrb <= NRB (the usual case: up
+//    to 16 rows at G = 4) one wave streams each prefix tile once for all
+//    rows.
 //  - Later workgroup units: the private slabs, W consecutive units (row,
 //    h, split) per workgroup, one per wave, as in ragged mode.  Splits
 //    0..n1-1 of a row are the prefix's, n1.. the slab's.
-template <int D, bool BF, int NBUF>
+template <int D, bool BF, int NBUF, int NRB>
 __global__ __launch_bounds__(256) void kq_sdpa_cascade_kernel(SdpaArgs a) {
     const int r = kq_lane() & 15;
     const int W = blockDim.x >> 6, w = threadIdx.x >> 6;
     const int R = 16 / a.G;
     const int nrb = (a.B + R - 1) / R;
+    const int ngrp = (nrb + NRB - 1) / NRB;
     const int64_t U1 = (int64_t)a.Hkv * a.n1;
+    const int jr = r / a.G;
     for (int64_t bu = blockIdx.x;; bu += gridDim.x) {
         if (bu < U1) {
             const int s = (int)(bu % a.n1), h = (int)(bu / a.n1);
-            const int jr = r / a.G;
             const int64_t kvbase = (int64_t)h * a.shared_head_stride;
             const int t_begin = s * a.split1;
             const int t_end = min(a.P, t_begin + a.split1);
-            for (int rb = w; rb < nrb; rb += W) {
-                const int row = rb * R + jr;
-                const bool ok = jr < R && row < a.B;
-                split_unit<D, BF, NBUF>(a, a.k + kvbase, a.v + kvbase, t_begin, t_end, h, s, ok ? row : 0,
-                                        ok ? r - jr * a.G : 0, ok);
+            for (int grp = w; grp < ngrp; grp += W) {
+                int rw[NRB], hd[NRB];
+                bool ok[NRB];
+#pragma unroll
+                for (int j = 0; j < NRB; ++j) {
+                    const int row = (grp * NRB + j) * R + jr;
+                    ok[j] = jr < R && row < a.B;
+                    rw[j] = ok[j] ? row : 0;
+                    hd[j] = ok[j] ? r - jr * a.G : 0;
+                }
+                split_unit<D, BF, NBUF, NRB>(a, a.k + kvbase, a.v + kvbase, t_begin, t_end, h, s, rw, hd, ok);
             }
         } else {
             const int64_t u2 = (bu - U1) * W + w;
@@ -399,22 +422,25 @@ __global__ __launch_bounds__(256) void kq_sdpa_cascade_kernel(SdpaArgs a) {
             const int t_end = min(cascade_len2(a, b), t_begin + a.split);
             const int64_t kvbase = (int64_t)sq * a.priv_batch_stride + (int64_t)h * a.priv_head_stride +
                                    (int64_t)st * D;
-            split_unit<D, BF, NBUF>(a, a.k2 + kvbase, a.v2 + kvbase, t_begin, t_end, h, a.n1 + s, b,
-                                    r < a.G ? r : 0, r < a.G);
+            const int rw[1] = {b}, hd[1] = {r < a.G ? r : 0};
+            const bool ok[1] = {r < a.G};
+            split_unit<D, BF, NBUF, 1>(a, a.k2 + kvbase, a.v2 + kvbase, t_begin, t_end, h, a.n1 + s, rw, hd, ok);
         }
     }
 }
 
 // One 256-thread workgroup per (row b, q head hq); rows with a single split
-// were finished by the split pass.  Thread t handles output element
-// d = t % D for the splits s = p, p + P, ... (p = t / D, P = 256 / D parts),
-// then the P partial sums are added in part order through LDS: a fixed
-// summation order, so the merge is deterministic.
+// were finished by the split pass.  Thread t handles the float4 of output
+// elements 4q .. 4q + 3 (q = t % (D/4)) for the splits s = p, p + P, ...
+// (p = t / (D/4), P = 256 / (D/4) parts), then the P partial sums are added
+// in part order through LDS: a fixed summation order, so the merge is
+// deterministic.
 template <int D, bool BF>
 __global__ __launch_bounds__(256) void kq_sdpa_merge_kernel(SdpaArgs a) {
-    constexpr int P = 256 / D;
+    constexpr int Q = D / 4;    // float4 lanes per split
+    constexpr int P = 256 / Q;  // splits summed side by side
     __shared__ float red_m[4];
-    __shared__ float red_acc[P][D];
+    __shared__ float4 red_acc[P][Q];
     __shared__ float red_l[P];
     const int b = blockIdx.x / a.Hq;
     const int hq = blockIdx.x - b * a.Hq;
@@ -422,11 +448,11 @@ __global__ __launch_bounds__(256) void kq_sdpa_merge_kernel(SdpaArgs a) {
     if (nsplit == 1) return;  // uniform over the workgroup
     const int h = hq / a.G, r = hq - h * a.G;
     const int t = threadIdx.x;
-    const int d = t % D, part = t / D;
+    const int q = t % Q, part = t / Q;
     const int64_t slot0 = ((int64_t)b * a.Hkv + h) * a.max_splits;
-    const float *ml = a.ml + (slot0 * a.G + r) * 2;        // split s at ml[s * G * 2]
-    const float *po = a.part + (slot0 * a.G + r) * D + d;  // split s at po[s * G * D]
-    const int64_t ml_stride = (int64_t)a.G * 2, po_stride = (int64_t)a.G * D;
+    const float *ml = a.ml + (slot0 * a.G + r) * 2;                          // split s at ml[s * G * 2]
+    const float4 *po = (const float4 *)(a.part + (slot0 * a.G + r) * D) + q;  // split s at po[s * G * Q]
+    const int64_t ml_stride = (int64_t)a.G * 2, po_stride = (int64_t)a.G * Q;
     // common max over the splits
     float M = -INFINITY;
     for (int s = t; s < nsplit; s += 256) M = fmaxf(M, ml[s * ml_stride]);
@@ -434,31 +460,42 @@ __global__ __launch_bounds__(256) void kq_sdpa_merge_kernel(SdpaArgs a) {
     if ((t & 63) == 0) red_m[t >> 6] = M;
     __syncthreads();
     M = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
-    // D = 96: threads 192..255 hold no (d, part) pair
-    const bool active = part < P;
-    float acc = 0.f, L = 0.f;
-    if (active) {
+    // D = 96: threads 240..255 hold no (q, part) pair
+    if (part < P) {
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        float L = 0.f;
 #pragma unroll 4
         for (int s = part; s < nsplit; s += P) {
             const float ms = ml[s * ml_stride], ls = ml[s * ml_stride + 1];
             const float f = (ms == -INFINITY) ? 0.f : exp2f(ms - M);
+            const float4 o = po[s * po_stride];
             L += ls * f;
-            acc += f * po[s * po_stride];
+            acc.x += f * o.x;
+            acc.y += f * o.y;
+            acc.z += f * o.z;
+            acc.w += f * o.w;
         }
-        red_acc[part][d] = acc;
-        if (d == 0) red_l[part] = L;
+        red_acc[part][q] = acc;
+        if (q == 0) red_l[part] = L;
     }
     __syncthreads();
     if (part != 0) return;
-    acc = red_acc[0][d];
-    L = red_l[0];
+    float4 acc = red_acc[0][q];
+    float L = red_l[0];
 #pragma unroll
-    for (int q = 1; q < P; ++q) {
-        acc += red_acc[q][d];
-        L += red_l[q];
+    for (int p = 1; p < P; ++p) {
+        const float4 o = red_acc[p][q];
+        acc.x += o.x;
+        acc.y += o.y;
+        acc.z += o.z;
+        acc.w += o.w;
+        L += red_l[p];
     }
     const float inv = L > 0.f ? 1.f / L : 0.f;
-    a.out[qo_index(a, b, hq) * D + d] = from_f32<BF>(acc * inv);
+    uint2 w;
+    w.x = (uint32_t)from_f32<BF>(acc.x * inv) | ((uint32_t)from_f32<BF>(acc.y * inv) << 16);
+    w.y = (uint32_t)from_f32<BF>(acc.z * inv) | ((uint32_t)from_f32<BF>(acc.w * inv) << 16);
+    *(uint2 *)(a.out + qo_index(a, b, hq) * D + 4 * q) = w;
 }
 
 int env_int(const char *name, int dflt) {
@@ -490,11 +527,27 @@ WsLayout ws_layout(int B, int Hq, int Hkv, int D, int max_len) {
     return w;
 }
 
+// Row blocks per prefix wave: 2 (GMLX_KQ_CASCADE_NRB=1 selects one).  Four
+// spill; D = 256 keeps one, its tile alone being 128 VGPRs.
+int cascade_nrb(int D, int nrb) {
+    const int cap = D == 256 ? 1 : env_int("GMLX_KQ_CASCADE_NRB", 2);
+    return nrb >= 2 && cap >= 2 ? 2 : 1;
+}
+
 template <int D, bool BF, int NBUF>
 void launch_n(const SdpaArgs &a, int grid, int block, bool merge, hipStream_t s) {
-    if (a.cascade)
-        hipLaunchKernelGGL((kq_sdpa_cascade_kernel<D, BF, NBUF>), dim3(grid), dim3(block), 0, s, a);
-    else
+    if (a.cascade) {
+        const int R = 16 / a.G;
+        switch (cascade_nrb(D, (a.B + R - 1) / R)) {
+        case 2:
+            if constexpr (D != 256)
+                hipLaunchKernelGGL((kq_sdpa_cascade_kernel<D, BF, NBUF, 2>), dim3(grid), dim3(block), 0, s, a);
+            break;
+        default:
+            hipLaunchKernelGGL((kq_sdpa_cascade_kernel<D, BF, NBUF, 1>), dim3(grid), dim3(block), 0, s, a);
+            break;
+        }
+    } else
         hipLaunchKernelGGL((kq_sdpa_split_kernel<D, BF, NBUF>), dim3(grid), dim3(64), 0, s, a);
     if (merge) hipLaunchKernelGGL((kq_sdpa_merge_kernel<D, BF>), dim3(a.B * a.Hq), dim3(256), 0, s, a);
 }
@@ -571,28 +624,54 @@ int kq_sdpa_decode_ragged(const void *q, const void *k, const void *v, const int
     return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
 }
 
-// Tokens per prefix split (GMLX_KQ_CASCADE_SPLIT, else the ragged split).
-// Shorter prefix splits give more waves but cost partials
-// (rows * G * D * 4 bytes written and merged per split); measured on
-// B 2..16, P 16k-32k, 512 tokens was fastest.
-static int cascade_split1(int P, int rows, int Hkv, int G) {
-    (void)P, (void)rows, (void)Hkv, (void)G;
-    const int env = env_int("GMLX_KQ_CASCADE_SPLIT", 0);
-    if (env > 0) return env < 32 ? 32 : (env + 31) / 32 * 32;
-    return split_tokens();
+// Cascade launch plan.  A wave's tiles form one chain of dependent loads
+// (about 1.5 us per 32-token tile when few waves run), so short batches
+// want short splits, while every split costs a partial (G * D * 4 bytes
+// per row and kv head, written and merged).  Chosen from a sweep of
+// B 2..16, qL 1..4, P 4k-32k, private 256-1024 tokens (Hq 32, Hkv 8, D 128):
+//   prefix split 512 tokens, 256 when that leaves under 384 prefix waves;
+//   private split 512 tokens, 256 when that leaves under 256 private
+//   waves, 128 when 256 leaves under 128.
+// GMLX_KQ_CASCADE_SPLIT / GMLX_KQ_CASCADE_PSPLIT override the two splits.
+struct CascadePlan {
+    int split1, split2;  // tokens per prefix / private split
+    int per_wave;        // row blocks per prefix wave
+    int ngrp;            // prefix waves per (kv head, split)
+};
+
+static int env_split(const char *name) {
+    const int env = env_int(name, 0);
+    return env > 0 ? (env < 32 ? 32 : (env + 31) / 32 * 32) : 0;
+}
+
+static CascadePlan cascade_plan(int P, int S, int rows, int Hkv, int G, int D) {
+    CascadePlan p;
+    const int R = 16 / G;
+    const int nrb = (rows + R - 1) / R;
+    p.per_wave = cascade_nrb(D, nrb);
+    p.ngrp = (nrb + p.per_wave - 1) / p.per_wave;
+    const int64_t prefix_waves_512 = (int64_t)Hkv * ((P + 511) / 512) * p.ngrp;
+    p.split1 = env_split("GMLX_KQ_CASCADE_SPLIT");
+    if (!p.split1) p.split1 = prefix_waves_512 < 384 ? 256 : 512;
+    p.split2 = env_split("GMLX_KQ_CASCADE_PSPLIT");
+    if (!p.split2) {
+        const int64_t per_row = (int64_t)rows * Hkv;
+        p.split2 = per_row * ((S + 511) / 512) >= 256 ? 512 : (per_row * ((S + 255) / 256) >= 128 ? 256 : 128);
+    }
+    return p;
 }
 
 // Cascade splits per (row, kv head): the prefix's, then the private slab's.
-static int cascade_max_splits(int P, int S, int rows, int Hkv, int G) {
-    const int C = split_tokens(), C1 = cascade_split1(P, rows, Hkv, G);
-    const int n = (P + C1 - 1) / C1 + (S + C - 1) / C;
+static int cascade_max_splits(const CascadePlan &p, int P, int S) {
+    const int n = (P + p.split1 - 1) / p.split1 + (S + p.split2 - 1) / p.split2;
     return n > 0 ? n : 1;
 }
 
 size_t kq_sdpa_cascade_workspace_bytes(int32_t B, int32_t qL, int32_t Hq, int32_t Hkv, int32_t D, int32_t P,
                                        int32_t S) {
     if (B <= 0 || qL <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv || D <= 0 || P < 0 || S < 0) return 0;
-    const int64_t slots = (int64_t)B * qL * Hkv * cascade_max_splits(P, S, B * qL, Hkv, Hq / Hkv) * (Hq / Hkv);
+    const CascadePlan plan = cascade_plan(P, S, B * qL, Hkv, Hq / Hkv, D);
+    const int64_t slots = (int64_t)B * qL * Hkv * cascade_max_splits(plan, P, S) * (Hq / Hkv);
     return (((size_t)slots * D * 4 + 255) & ~(size_t)255) + (size_t)slots * 2 * 4;
 }
 
@@ -640,10 +719,11 @@ int kq_sdpa_decode_gqa_cascade(const void *q, const void *k_shared, const void *
     a.Hq = Hq;
     a.Hkv = Hkv;
     a.G = Hq / Hkv;
-    a.split = split_tokens();
-    a.split1 = cascade_split1(P, rows, Hkv, a.G);
+    const CascadePlan plan = cascade_plan(P, S, rows, Hkv, a.G, D);
+    a.split = plan.split2;
+    a.split1 = plan.split1;
     a.n1 = (P + a.split1 - 1) / a.split1;
-    a.max_splits = cascade_max_splits(P, S, rows, Hkv, a.G);
+    a.max_splits = cascade_max_splits(plan, P, S);
     a.max_len = P > S ? P : S;
     a.part = (float *)workspace;
     const int64_t slots = (int64_t)rows * Hkv * a.max_splits * a.G;
@@ -652,9 +732,7 @@ int kq_sdpa_decode_gqa_cascade(const void *q, const void *k_shared, const void *
     // W waves per workgroup: up to 4 row blocks of a prefix split share a
     // workgroup.  Grid: the prefix's Hkv * n1 units, then the private
     // units W at a time (an upper bound; extra waves exit at once).
-    const int R = 16 / a.G;
-    const int nrb = (rows + R - 1) / R;
-    const int W = nrb < 4 ? nrb : 4;
+    const int W = plan.ngrp < 4 ? plan.ngrp : 4;
     const int64_t priv = (int64_t)rows * Hkv * (a.max_splits - a.n1 > 0 ? a.max_splits - a.n1 : 1);
     const int64_t upper = (int64_t)Hkv * a.n1 + (priv + W - 1) / W;
     const int grid = (int)(upper < (1 << 22) ? upper : (1 << 22));
