@@ -19,7 +19,8 @@ algorithmic bytes per launch / average launch duration, both over the timed
 region; `traffic` = HBM bytes per launch of the same family from the
 FETCH_SIZE / WRITE_SIZE counters.  Extra fields: the per-B sweep (B = 1..64, same
 stack), ragged GQA decode attention at BASELINE config 3 (KV GB/s, KV tokens/s),
-one MoE decode layer at BASELINE configs 4 and 5 (GB/s over the touched
+cascade shared-prefix decode attention beside the ragged kernel on the same
+buffer, one MoE decode layer at BASELINE configs 4 and 5 (GB/s over the touched
 experts' bytes) and the CPU baseline (the repository's OpenMP C restatement of the same
 dequant-fused matmul, timed on a bounded sample of the same workload).
 
@@ -247,6 +248,75 @@ def bench_sdpa(torch, ops, iters=20):
     }
 
 
+def bench_cascade(torch, ops, iters=30):
+    """Cascade shared-prefix decode (kq.sdpa_decode_gqa_cascade, the claim of
+    gmlx/cascade_sdpa.py:136-260): B = 8 sequences share a P = 16384-token
+    prefix, then 512 private tokens each after ragged left pads; qL 1,
+    32 q / 8 kv heads, D 128, fp16.  Timed beside the ragged kernel over the
+    same left-padded buffer (what runs without the stamp).  GB/s counts the
+    bytes the cascade must read: the prefix once plus every row's private
+    keys and values."""
+    import numpy as np
+    B, Hq, Hkv, D, P, sp = 8, 32, 8, 128, 16384, 512
+    pads = [0, 64, 128, 32, 5, 0, 17, 3]
+    L = max(pads) + P + sp
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    kb = torch.randn(B, Hkv, L, D, generator=gen, device="cuda", dtype=torch.float32).half()
+    vb = torch.randn(B, Hkv, L, D, generator=gen, device="cuda", dtype=torch.float32).half()
+    for b in range(1, B):  # every row holds row 0's copy of the prefix
+        kb[b, :, pads[b]:pads[b] + P] = kb[0, :, pads[0]:pads[0] + P]
+        vb[b, :, pads[b]:pads[b] + P] = vb[0, :, pads[0]:pads[0] + P]
+    q = torch.randn(B, Hq, 1, D, generator=gen, device="cuda", dtype=torch.float32).half()
+    scale = 1.0 / math.sqrt(D)
+    c0 = min(pads) + P
+    starts = torch.tensor([p + P - c0 for p in pads], dtype=torch.int32, device="cuda")
+    l0 = pads[0]
+    casc = lambda: ops.sdpa_decode_gqa_cascade(  # noqa: E731
+        q, kb[0:1, :, l0:l0 + P], vb[0:1, :, l0:l0 + P], kb[:, :, c0:], vb[:, :, c0:], scale, starts=starts)
+    rag = lambda: ops.ragged_decode_attention(q, kb, vb, pads, scale)  # noqa: E731
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / iters
+
+    out = casc()
+    ms_c = timed(casc)
+    ms_r = timed(rag)
+    tok_bytes = Hkv * D * 2 * 2
+    need = P * tok_bytes + sum(L - c0 - int(s) for s in starts.tolist()) * tok_bytes
+    # spot-check two (row, head) pairs against fp64 over the row's keys
+    chk = 0.0
+    for b, hq in ((0, 0), (B - 1, Hq - 1)):
+        h = hq // (Hq // Hkv)
+        kr = kb[b, h, pads[b]:].double().cpu().numpy()
+        vr = vb[b, h, pads[b]:].double().cpu().numpy()
+        sc = kr @ q[b, hq, 0].double().cpu().numpy() * scale
+        pr = np.exp(sc - sc.max())
+        ref = pr @ vr / pr.sum()
+        got = out[b, hq, 0].double().cpu().numpy()
+        chk = max(chk, float(np.abs(got - ref).max() / np.abs(ref).max()))
+    del kb, vb
+    return {
+        "workload": "cascade: B=8 sequences sharing a 16384-token prefix + 512 private tokens (pads 0..128), "
+                    "qL 1, 32q/8kv heads, D=128, fp16",
+        "ms": round(ms_c, 4),
+        "gbs": round(need / ms_c / 1e6, 1),
+        "frac_hbm": round(need / ms_c / 1e6 / HBM_PEAK_GBS, 4),
+        "bytes_read_once": need,
+        "ragged_same_buffer_ms": round(ms_r, 4),
+        "speedup_vs_ragged": round(ms_r / ms_c, 2),
+        "max_rel_spot": chk,
+    }
+
+
 # ------------------------------------------------------------------- MoE
 
 MOE_CONFIGS = {
@@ -421,6 +491,7 @@ def main():
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-sdpa", action="store_true")
+    ap.add_argument("--no-cascade", action="store_true")
     ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 --pmc passes")
@@ -524,6 +595,12 @@ def main():
         sdpa = bench_sdpa(torch, ops)
         log(f"[bench] sdpa C3: {sdpa['ms']} ms, {sdpa['kv_gbs']} GB/s, {sdpa['kv_tokens_per_s']:.3e} tok/s")
 
+    cascade = None
+    if not args.no_cascade:
+        cascade = bench_cascade(torch, ops)
+        log(f"[bench] cascade: {cascade['ms']} ms, {cascade['gbs']} GB/s on bytes read once, "
+            f"{cascade['speedup_vs_ragged']}x the ragged kernel on the same buffer")
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline({k: v.cpu().numpy() for k, v in stack[0].items()}, B)
@@ -564,6 +641,7 @@ def main():
         "cpu_baseline": cpu,
         "per_batch": per_batch,
         "sdpa": sdpa,
+        "cascade": cascade,
         "moe": moe,
     }
     print(json.dumps(res), flush=True)

@@ -61,28 +61,30 @@ __device__ __forceinline__ void store_tile(void *y, int y_dtype, int64_t y_strid
     }
 }
 
-// Wave `wave` of the workgroup takes super-blocks wave, wave + WV, ...
-template <int CODEC, int MT, int XT, int WV>
-__device__ __forceinline__ void dense_tile(const DenseProblem &p, int nt, int wave, floatx4 (&acc)[MT],
+// Wave `wave` of the workgroup takes super-blocks wave, wave + WV, ... of
+// NW column tiles (16 * NW output columns); the activation fragments of a
+// super-block are loaded once for all NW tiles.
+template <int CODEC, int MT, int XT, int WV, int NW>
+__device__ __forceinline__ void dense_tile(const DenseProblem &p, int nt, int wave, floatx4 (&acc)[NW][MT],
                                            const Iq2Tables &tab) {
     const int lane = kq_lane();
     const int r = lane & 15;
     const int m0 = blockIdx.y * kMaxChunk;
-    const int n = min(nt * 16 + r, p.N - 1);
     const int nb = p.K / KQ_QK;
-    const uint8_t *wrow[1] = {p.w + (int64_t)n * p.w_row_bytes};
+    const uint8_t *wrow[NW];
+#pragma unroll
+    for (int i = 0; i < NW; ++i) wrow[i] = p.w + (int64_t)min((nt * NW + i) * 16 + r, p.N - 1) * p.w_row_bytes;
     const XRowsBuf<MT> xrow = x_rows_buf<MT, XT>(p.x, p.x_stride, p.M, p.K, m0, r);
-    floatx4 a1[1][MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) a1[0][mt] = floatx4{0, 0, 0, 0};
-    tile_accumulate<CODEC, MT, XT, 1, XRowsBuf<MT>, (WV < 16)>(wrow, wave, WV, nb, xrow, a1, tab);
+    for (int i = 0; i < NW; ++i)
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[mt] = a1[0][mt];
+        for (int mt = 0; mt < MT; ++mt) acc[i][mt] = floatx4{0, 0, 0, 0};
+    tile_accumulate<CODEC, MT, XT, NW, XRowsBuf<MT>, (WV < 16)>(wrow, wave, WV, nb, xrow, acc, tab);
 }
 
-template <int MT, int XT, int WV>
+template <int MT, int XT, int WV, int NW>
 __global__ __launch_bounds__(64 * WV) void kq_dense_grouped_kernel(DenseArgs a) {
-    __shared__ floatx4 red[WV - 1][MT][64];
+    __shared__ floatx4 red[WV - 1][NW * MT][64];
     __shared__ Iq2Tables iq2_tab;
     const int unit = blockIdx.x;
     // Select the problem with static indices only: dynamic indexing of the
@@ -96,29 +98,36 @@ __global__ __launch_bounds__(64 * WV) void kq_dense_grouped_kernel(DenseArgs a) 
     const int lane = kq_lane();
     const int m0 = blockIdx.y * kMaxChunk;
     if (m0 >= p.M) return;  // uniform over the workgroup
-    floatx4 acc[MT];
+    floatx4 acc[NW][MT];
     switch (p.codec) {
-    case KQ_CODEC_Q4_K: dense_tile<KQ_CODEC_Q4_K, MT, XT, WV>(p, nt, wave, acc, iq2_tab); break;
-    case KQ_CODEC_Q6_K: dense_tile<KQ_CODEC_Q6_K, MT, XT, WV>(p, nt, wave, acc, iq2_tab); break;
+    case KQ_CODEC_Q4_K: dense_tile<KQ_CODEC_Q4_K, MT, XT, WV, NW>(p, nt, wave, acc, iq2_tab); break;
+    case KQ_CODEC_Q6_K: dense_tile<KQ_CODEC_Q6_K, MT, XT, WV, NW>(p, nt, wave, acc, iq2_tab); break;
     default:
         load_iq2_tables(iq2_tab);
-        dense_tile<KQ_CODEC_IQ2_XXS, MT, XT, WV>(p, nt, wave, acc, iq2_tab);
+        dense_tile<KQ_CODEC_IQ2_XXS, MT, XT, WV, NW>(p, nt, wave, acc, iq2_tab);
         break;
     }
     if (wave > 0) {
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) red[wave - 1][mt][lane] = acc[mt];
+        for (int i = 0; i < NW; ++i)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) red[wave - 1][i * MT + mt][lane] = acc[i][mt];
     }
     __syncthreads();
     if (wave != 0) return;
 #pragma unroll
     for (int w = 0; w < WV - 1; ++w)
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[mt] += red[w][mt][lane];
-    const int n = nt * 16 + (lane & 15);
+        for (int i = 0; i < NW; ++i)
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-        store_tile(p.y, a.y_dtype, p.y_stride, m0 + 16 * mt, p.M, n, n < p.N, acc[mt]);
+            for (int mt = 0; mt < MT; ++mt) acc[i][mt] += red[w][i * MT + mt][lane];
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+        const int n = (nt * NW + i) * 16 + (lane & 15);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+            store_tile(p.y, a.y_dtype, p.y_stride, m0 + 16 * mt, p.M, n, n < p.N, acc[i][mt]);
+    }
 }
 
 // ---------------------------------------------------------------- MoE
@@ -465,6 +474,11 @@ int env_flag(const char *name, int dflt) {
     return !(s[0] == '0' && s[1] == 0);
 }
 
+int env_int(const char *name, int dflt) {
+    const char *s = getenv(name);
+    return (s && *s) ? atoi(s) : dflt;
+}
+
 // "0" -> 0, "2" -> 2, anything else set -> 1, unset -> dflt
 int env_int_flag(const char *name, int dflt) {
     const char *s = getenv(name);
@@ -488,10 +502,30 @@ bool qmv_eligible(const kq_matmul_problem *ps, const int *idx, int n) {
 }
 
 // 16 waves per tile for one m-tile, 4 waves for wider chunks
-template <int MT, int XT>
+template <int MT, int XT, int NW>
 void launch_dense(const DenseArgs &a, int units, int chunks, hipStream_t s) {
     constexpr int WV = MT == 1 ? 16 : 4;
-    hipLaunchKernelGGL((kq_dense_grouped_kernel<MT, XT, WV>), dim3(units, chunks), dim3(64 * WV), 0, s, a);
+    hipLaunchKernelGGL((kq_dense_grouped_kernel<MT, XT, WV, NW>), dim3(units, chunks), dim3(64 * WV), 0, s, a);
+}
+
+// Column tiles per dense workgroup: one m-tile keeps 1; wider chunks read
+// their activation fragments once per super-block for NW tiles
+// (GMLX_KQ_DENSE_NW: 1, 2 or 4).
+int dense_nw(int mt) {
+    if (mt == 1) return 1;
+    const int nw = env_int("GMLX_KQ_DENSE_NW", 2);
+    return nw >= 4 ? 4 : (nw >= 2 ? 2 : 1);
+}
+
+template <int MT, int XT>
+void launch_dense_nw(int nw, const DenseArgs &a, int units, int chunks, hipStream_t s) {
+    if constexpr (MT == 1) {
+        launch_dense<MT, XT, 1>(a, units, chunks, s);
+    } else {
+        if (nw == 4) launch_dense<MT, XT, 4>(a, units, chunks, s);
+        else if (nw == 2) launch_dense<MT, XT, 2>(a, units, chunks, s);
+        else launch_dense<MT, XT, 1>(a, units, chunks, s);
+    }
 }
 
 template <int CODEC, int XT, int NW>
@@ -671,6 +705,8 @@ int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problem
     }
     DenseArgs a;
     int units = 0, max_chunks = 0, np = 0;
+    const int mt = group_mt(problems, n_problems);
+    const int nw = dense_nw(mt);
     for (int i = 0; i < n_problems; ++i) {
         const kq_matmul_problem &q = problems[i];
         if (q.M == 0 || q.N == 0) continue;
@@ -686,9 +722,9 @@ int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problem
         p.N = q.N;
         p.K = q.K;
         p.codec = q.codec;
-        p.n_tiles = pl.n_tiles;
+        p.n_tiles = (pl.n_tiles + nw - 1) / nw;
         p.unit_begin = units;
-        units += pl.n_tiles;
+        units += p.n_tiles;
         if (pl.chunks > max_chunks) max_chunks = pl.chunks;
     }
     if (np == 0) return KQ_OK;
@@ -697,10 +733,13 @@ int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problem
     a.y_dtype = y_dtype;
     hipStream_t s = (hipStream_t)stream;
     const bool bf = x_dtype == KQ_DTYPE_BF16;
-    const int mt = group_mt(problems, n_problems);
-    if (mt == 1) bf ? launch_dense<1, 1>(a, units, max_chunks, s) : launch_dense<1, 0>(a, units, max_chunks, s);
-    else if (mt == 2) bf ? launch_dense<2, 1>(a, units, max_chunks, s) : launch_dense<2, 0>(a, units, max_chunks, s);
-    else bf ? launch_dense<4, 1>(a, units, max_chunks, s) : launch_dense<4, 0>(a, units, max_chunks, s);
+    if (mt == 1) {
+        bf ? launch_dense_nw<1, 1>(nw, a, units, max_chunks, s) : launch_dense_nw<1, 0>(nw, a, units, max_chunks, s);
+    } else if (mt == 2) {
+        bf ? launch_dense_nw<2, 1>(nw, a, units, max_chunks, s) : launch_dense_nw<2, 0>(nw, a, units, max_chunks, s);
+    } else {
+        bf ? launch_dense_nw<4, 1>(nw, a, units, max_chunks, s) : launch_dense_nw<4, 0>(nw, a, units, max_chunks, s);
+    }
     return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
 }
 
