@@ -29,9 +29,11 @@ namespace kqmma {
 // ---- IQ2_XXS tables in fp16 form, built at compile time ------------------
 constexpr uint32_t mag_to_f16_bits(uint32_t b) { return b == 0x08 ? 0x4800u : b == 0x19 ? 0x4E40u : 0x5160u; }
 
-struct Iq2Tables {
-    uint32_t grid_h2[256][4];  // 8 fp16 magnitudes per grid entry
-    uint32_t sign_x2[128][4];  // XOR masks (0x8000 per negative value)
+// 16-byte aligned rows: an entry is one ds_read_b128 (with 4-byte alignment
+// the compiler splits it into two ds_read2_b32).
+struct alignas(16) Iq2Tables {
+    alignas(16) uint32_t grid_h2[256][4];  // 8 fp16 magnitudes per grid entry
+    alignas(16) uint32_t sign_x2[128][4];  // XOR masks (0x8000 per negative value)
 };
 
 constexpr Iq2Tables make_iq2_tables() {
