@@ -33,6 +33,11 @@ using namespace kqmma;
 
 constexpr int kMaxChunk = 64;  // batch rows per grid.y chunk (4 m-tiles)
 
+int env_int(const char *name, int dflt) {
+    const char *s = getenv(name);
+    return (s && *s) ? atoi(s) : dflt;
+}
+
 
 struct DenseProblem {
     const uint8_t *w;
@@ -157,14 +162,22 @@ __device__ __forceinline__ float act_apply(int act, float g) {
 // 16 * MT rows is walked in chunks.
 constexpr int kGatherWaves = 4;
 
-// Register budget: four waves per SIMD (128 VGPRs) up to two m-tiles, two
-// (256) for four m-tiles.
-template <int MT>
-constexpr int gather_waves_per_simd() { return MT <= 2 ? 4 : 2; }
+// Register budget (tighter budgets spill to scratch): four waves per SIMD
+// (128 VGPRs) for one 16-row tile of one matrix with fp16/bf16 rows; three
+// (168) up to two such tiles or fp32 rows; two (256) up to four tiles (and
+// Q6_K pairs of fp32 rows); one (AGPRs too) beyond, and for four tiles of
+// fp32 rows.
+template <int CODEC, int MT, int NW, int XT>
+constexpr int gather_waves_per_simd() {
+    constexpr int t = MT * NW;
+    if (t == 1 && XT != 2) return 4;
+    if (t <= 2 && !(CODEC == KQ_CODEC_Q6_K && XT == 2 && t == 2)) return 3;
+    return (t <= 4 && !(XT == 2 && t == 4)) ? 2 : 1;
+}
 
 template <int CODEC, int MT, int XT, int NW>
 __global__ __launch_bounds__(64 * kGatherWaves)
-__attribute__((amdgpu_waves_per_eu(gather_waves_per_simd<MT>()))) void kq_gather_kernel(GatherArgs a) {
+__attribute__((amdgpu_waves_per_eu(gather_waves_per_simd<CODEC, MT, NW, XT>()))) void kq_gather_kernel(GatherArgs a) {
     __shared__ floatx4 red[kGatherWaves - 1][NW][MT][64];
     __shared__ Iq2Tables iq2_tab;
     if constexpr (CODEC == KQ_CODEC_IQ2_XXS) load_iq2_tables(iq2_tab);
@@ -240,6 +253,72 @@ __attribute__((amdgpu_waves_per_eu(gather_waves_per_simd<MT>()))) void kq_gather
     }
 }
 
+
+// Short K: one wave per (segment slot, tile) unit, kGatherWaves units per
+// workgroup (consecutive tiles of one expert), the whole K in the wave; no
+// cross-wave reduction.
+template <int CODEC, int MT, int XT, int NW>
+__global__ __launch_bounds__(64 * kGatherWaves)
+__attribute__((amdgpu_waves_per_eu(gather_waves_per_simd<CODEC, MT, NW, XT>()))) void kq_gather_wave_kernel(GatherArgs a) {
+    __shared__ Iq2Tables iq2_tab;
+    if constexpr (CODEC == KQ_CODEC_IQ2_XXS) load_iq2_tables(iq2_tab);
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = kq_lane();
+    const int r = lane & 15;
+    const int unit = blockIdx.x * kGatherWaves + wave;
+    const int slot = unit / a.n_tiles;
+    const int nt = unit - slot * a.n_tiles;
+    const int S = a.seg_info[0];
+    if (slot == 0) {
+        // pairs whose expert id is out of range (never routed) get zeros in
+        // this tile's columns
+        const int32_t *flag = a.pair_order + a.n_pairs;
+        const int c = nt * 16 + r;
+        if (c < a.N)
+            for (int p = lane >> 4; p < a.n_pairs; p += 4)
+                if (flag[p] < 0) kq_store_out(a.y, a.y_dtype, (int64_t)p * a.y_stride + c, 0.f);
+    }
+    if (slot >= S) return;  // uniform over the wave
+    const int expert = a.seg_info[1 + slot];
+    const int seg_begin = a.seg_info[1 + a.n_experts + slot];
+    const int seg_end = a.seg_info[1 + a.n_experts + slot + 1];
+    const int n = nt * 16 + r;
+    const bool n_valid = n < a.N;
+    const int nc = n_valid ? n : a.N - 1;
+    const int nb = a.K / KQ_QK;
+    const uint8_t *wrow[NW];
+    wrow[0] = a.w0 + (int64_t)expert * a.w_expert_bytes + (int64_t)nc * a.w_row_bytes;
+    if constexpr (NW == 2)
+        wrow[1] = a.w1 + (int64_t)expert * a.w_expert_bytes + (int64_t)nc * a.w_row_bytes;
+    for (int c0 = seg_begin; c0 < seg_end; c0 += 16 * MT) {
+        XRowPtrs<MT> xrow;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const int ri = min(c0 + 16 * mt + r, seg_end - 1);
+            xrow.row[mt] = a.x + (int64_t)(a.pair_order[ri] / a.x_pair_div) * a.x_stride * x_elem_bytes<XT>();
+        }
+        floatx4 acc[NW][MT];
+#pragma unroll
+        for (int i = 0; i < NW; ++i)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc[i][mt] = floatx4{0, 0, 0, 0};
+        // no prefetch stage (two would not fit 128 VGPRs): resident waves hide the latency
+        tile_accumulate<CODEC, MT, XT, NW, XRowPtrs<MT>, false>(wrow, 0, 1, nb, xrow, acc, iq2_tab);
+        if (!n_valid) continue;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int ri = c0 + 16 * mt + 4 * (lane >> 4) + e;
+                if (ri >= seg_end) continue;
+                const int pair = a.pair_order[ri];
+                float v = acc[0][mt][e];
+                if constexpr (NW == 2) v = act_apply(a.act, v) * acc[1][mt][e];
+                kq_store_out(a.y, a.y_dtype, (int64_t)pair * a.y_stride + n, v);
+            }
+        }
+    }
+}
 
 // Routing: one workgroup, counting sort of pairs by expert (stable by pair id).
 // seg_info = [S, seg_expert[E], seg_start[E+1]]; pair_order[n_pairs];
@@ -474,11 +553,6 @@ int env_flag(const char *name, int dflt) {
     return !(s[0] == '0' && s[1] == 0);
 }
 
-int env_int(const char *name, int dflt) {
-    const char *s = getenv(name);
-    return (s && *s) ? atoi(s) : dflt;
-}
-
 // "0" -> 0, "2" -> 2, anything else set -> 1, unset -> dflt
 int env_int_flag(const char *name, int dflt) {
     const char *s = getenv(name);
@@ -528,8 +602,21 @@ void launch_dense_nw(int nw, const DenseArgs &a, int units, int chunks, hipStrea
     }
 }
 
+// Super-blocks per row up to which a wave takes a whole unit
+// (GMLX_KQ_GATHER_WAVE_NB; 0 always splits K over the workgroup's waves).
+int gather_wave_nb() { return env_int("GMLX_KQ_GATHER_WAVE_NB", 8); }
+
 template <int CODEC, int XT, int NW>
 void launch_gather_codec(int mt, const GatherArgs &a, int grid, hipStream_t s) {
+    if (a.K / KQ_QK <= gather_wave_nb()) {
+        const int g = (grid + kGatherWaves - 1) / kGatherWaves;
+        switch (mt) {
+        case 1: hipLaunchKernelGGL((kq_gather_wave_kernel<CODEC, 1, XT, NW>), dim3(g), dim3(64 * kGatherWaves), 0, s, a); break;
+        case 2: hipLaunchKernelGGL((kq_gather_wave_kernel<CODEC, 2, XT, NW>), dim3(g), dim3(64 * kGatherWaves), 0, s, a); break;
+        default: hipLaunchKernelGGL((kq_gather_wave_kernel<CODEC, 4, XT, NW>), dim3(g), dim3(64 * kGatherWaves), 0, s, a); break;
+        }
+        return;
+    }
     switch (mt) {
     case 1: hipLaunchKernelGGL((kq_gather_kernel<CODEC, 1, XT, NW>), dim3(grid), dim3(64 * kGatherWaves), 0, s, a); break;
     case 2: hipLaunchKernelGGL((kq_gather_kernel<CODEC, 2, XT, NW>), dim3(grid), dim3(64 * kGatherWaves), 0, s, a); break;
