@@ -110,17 +110,18 @@ KERNEL_FAMILIES = ("kq_mv_kernel", "kq_qmv_persistent_kernel", "kq_dense_grouped
 
 def kernel_of(launch, B):
     """Kernel (with template arguments) that serves `launch` at B rows."""
-    dense = f"kq_dense_grouped_kernel<{1 if B <= 16 else 2 if B <= 32 else 4}, 0, {16 if B <= 16 else 4}>"
+    mt = 1 if B <= 16 else 2 if B <= 32 else 4
+    dense = f"kq_dense_grouped_kernel<{mt}, 0, {16 if B <= 16 else 4}, {1 if B <= 16 else 2}>"
     if B > 16:
         return dense
-    if launch == "qkv":  # Q4_K q|k with Q6_K v: the mixed form (codec id 127), 1.5 tiles per CU
-        return "kq_mv_kernel<127, 0, 1, 2, false>"
+    if launch == "qkv":  # Q4_K q|k with Q6_K v: the mixed form (codec id 127), 0.75 tiles per 8-wave workgroup
+        return "kq_mv_kernel<127, 0, 2, 1, false, 8>"
     if launch == "o":
-        return "kq_mv_kernel<12, 0, 1, 1, false>"
+        return "kq_mv_kernel<12, 0, 2, 1, false, 8>"
     if launch == "gate_up":
-        return "kq_mv_kernel<12, 0, 1, 3, false>"
+        return "kq_mv_kernel<12, 0, 1, 3, false, 16>"
     if B <= 8:
-        return f"kq_mv_kernel<14, 0, 3, 1, {'true' if B > 4 else 'false'}>"
+        return f"kq_mv_kernel<14, 0, 3, 1, {'true' if B > 4 else 'false'}, 16>"
     return dense
 
 

@@ -44,7 +44,7 @@ namespace {
 
 using namespace kqmma;
 
-constexpr int WV = 16;                 // waves per workgroup
+constexpr int kWaves = 16;             // waves per CU (one 16-wave or two 8-wave workgroups)
 constexpr int kLdsBytes = 160 * 1024;  // LDS of one CU
 constexpr uint32_t kOut = 0x80000000u; // buffer offset past every range (reads 0, writes dropped)
 #define LDSP(T) __attribute__((address_space(3))) T *
@@ -286,11 +286,13 @@ struct Tables<KQ_CODEC_IQ2_XXS> {
 
 // ---- kernel ---------------------------------------------------------------------
 
-// NBW: blocks per wave per tile (K <= 256 * 16 * NBW).  XT: 0 fp16, 1 bf16.
-// DEPTH: register ring depth in tiles.  XR: block NBW - 1 of every wave takes
-// its activations from registers.
-template <int CODEC, int XT, int NBW, int DEPTH, bool XR>
-__global__ __launch_bounds__(64 * WV) void kq_mv_kernel(MvArgs a_) {
+// WV: waves per workgroup (16: one workgroup per CU; 8: two, which are not
+// phase-locked by each other's per-tile barrier).  NBW: blocks per wave per
+// tile (K <= 256 * WV * NBW).  XT: 0 fp16, 1 bf16.  DEPTH: register ring
+// depth in tiles.  XR: block NBW - 1 of every wave takes its activations
+// from registers.
+template <int CODEC, int XT, int NBW, int DEPTH, bool XR, int WV>
+__global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(4))) void kq_mv_kernel(MvArgs a_) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const KArgs A = (KArgs)__builtin_amdgcn_kernarg_segment_ptr();
     const Iq2Tables *tab = Tables<CODEC>::get();
@@ -391,11 +393,12 @@ __global__ __launch_bounds__(64 * WV) void kq_mv_kernel(MvArgs a_) {
     float *red = (float *)(smem + A->red_off);  // [bufs][WV][64 lanes][4]
     const int bufs = A->red_bufs;
     const uint32_t xr_base = (uint32_t)(uintptr_t)(LDSP(const void))(smem + min(r, M - 1) * xrow);
-    // reduction slice of this wave: source lane 4 * wave + lane / 4, element
-    // lane % 4 (lanes 16..63 store nothing)
-    const int src_lane = 4 * wave + ((lane >> 2) & 3), src_e = lane & 3;
+    // reduction slice of this wave: source lane SL * wave + lane / 4, element
+    // lane % 4 (SL = 64 / WV; lanes 4 * SL .. 63 store nothing)
+    constexpr int SL = 64 / WV;
+    const int src_lane = SL * wave + ((lane >> 2) & (SL - 1)), src_e = lane & 3;
     const int out_n = src_lane & 15, out_m = 4 * (src_lane >> 4) + src_e;
-    const bool out_lane = lane < 16 && out_m < M;
+    const bool out_lane = lane < 4 * SL && out_m < M;
 
     const bool y_f32 = A->y_dtype == KQ_DTYPE_F32, y_bf16 = A->y_dtype == KQ_DTYPE_BF16;
     auto compute_tile = [&](WB<CODEC> (&b)[NBW], int k) {
@@ -467,50 +470,54 @@ __global__ __launch_bounds__(64 * WV) void kq_mv_kernel(MvArgs a_) {
 
 // Launch with `lds` bytes of dynamic LDS; the kernel's limit is raised to the
 // CU's LDS once per instantiation (the default limit is lower).
-template <int CODEC, int XT, int NBW, int DEPTH, bool XR>
+template <int CODEC, int XT, int NBW, int DEPTH, bool XR, int WV>
 int launch_one(const MvArgs &a, int grid, size_t lds, hipStream_t s) {
     static bool raised = false;
     if (!raised) {
         const size_t tables = CODEC == KQ_CODEC_IQ2_XXS ? sizeof(Iq2Tables) : 0;
-        if (hipFuncSetAttribute((const void *)kq_mv_kernel<CODEC, XT, NBW, DEPTH, XR>,
+        if (hipFuncSetAttribute((const void *)kq_mv_kernel<CODEC, XT, NBW, DEPTH, XR, WV>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)(kLdsBytes - tables)) != hipSuccess)
             return KQ_ERR_LAUNCH_FAILED;
         raised = true;
     }
-    hipLaunchKernelGGL((kq_mv_kernel<CODEC, XT, NBW, DEPTH, XR>), dim3(grid), dim3(64 * WV), lds, s, a);
+    hipLaunchKernelGGL((kq_mv_kernel<CODEC, XT, NBW, DEPTH, XR, WV>), dim3(grid), dim3(64 * WV), lds, s, a);
     return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
 }
 
 // Instantiated shapes (registers of a lane at 16 waves per CU: 128): one
 // block per wave with rings of 1..3 tiles; two or three blocks per wave with
 // rings of 1..2 tiles, except three Q6_K blocks and the XR form (ring of 1).
-template <int CODEC, int XT>
+template <int CODEC, int XT, int WV>
 int launch_shape(const MvArgs &a, int nbw, int depth, bool xr, int grid, size_t lds, hipStream_t s) {
     if constexpr (CODEC == KQ_MIX) {
         // mixed Q4_K / Q6_K: up to two blocks per wave, x in LDS
         if (xr || nbw > 2) return KQ_ERR_BAD_SHAPE;
-        if (nbw == 2) return depth == 1 ? launch_one<CODEC, XT, 2, 1, false>(a, grid, lds, s)
-                                        : launch_one<CODEC, XT, 2, 2, false>(a, grid, lds, s);
-        if (depth == 1) return launch_one<CODEC, XT, 1, 1, false>(a, grid, lds, s);
-        if (depth == 2) return launch_one<CODEC, XT, 1, 2, false>(a, grid, lds, s);
-        return launch_one<CODEC, XT, 1, 3, false>(a, grid, lds, s);
+        if (nbw == 2) return depth == 1 ? launch_one<CODEC, XT, 2, 1, false, WV>(a, grid, lds, s)
+                                        : launch_one<CODEC, XT, 2, 2, false, WV>(a, grid, lds, s);
+        if (depth == 1) return launch_one<CODEC, XT, 1, 1, false, WV>(a, grid, lds, s);
+        if (depth == 2) return launch_one<CODEC, XT, 1, 2, false, WV>(a, grid, lds, s);
+        return launch_one<CODEC, XT, 1, 3, false, WV>(a, grid, lds, s);
     } else {
         if (nbw == 1) {
-            if (depth == 1) return launch_one<CODEC, XT, 1, 1, false>(a, grid, lds, s);
-            if (depth == 2) return launch_one<CODEC, XT, 1, 2, false>(a, grid, lds, s);
-            return launch_one<CODEC, XT, 1, 3, false>(a, grid, lds, s);
+            if (depth == 1) return launch_one<CODEC, XT, 1, 1, false, WV>(a, grid, lds, s);
+            if (depth == 2) return launch_one<CODEC, XT, 1, 2, false, WV>(a, grid, lds, s);
+            return launch_one<CODEC, XT, 1, 3, false, WV>(a, grid, lds, s);
         }
         if (nbw == 2) {
-            if (xr) return launch_one<CODEC, XT, 2, 1, true>(a, grid, lds, s);
-            if (depth == 1) return launch_one<CODEC, XT, 2, 1, false>(a, grid, lds, s);
-            return launch_one<CODEC, XT, 2, 2, false>(a, grid, lds, s);
-        }
-        if (nbw == 3) {
-            if (xr) return launch_one<CODEC, XT, 3, 1, true>(a, grid, lds, s);
-            if constexpr (CODEC != KQ_CODEC_Q6_K) {
-                if (depth >= 2) return launch_one<CODEC, XT, 3, 2, false>(a, grid, lds, s);
+            if constexpr (WV == kWaves) {
+                if (xr) return launch_one<CODEC, XT, 2, 1, true, WV>(a, grid, lds, s);
             }
-            return launch_one<CODEC, XT, 3, 1, false>(a, grid, lds, s);
+            if (depth == 1) return launch_one<CODEC, XT, 2, 1, false, WV>(a, grid, lds, s);
+            return launch_one<CODEC, XT, 2, 2, false, WV>(a, grid, lds, s);
+        }
+        if constexpr (WV == kWaves) {  // 8-wave workgroups take K <= 4096
+            if (nbw == 3) {
+                if (xr) return launch_one<CODEC, XT, 3, 1, true, WV>(a, grid, lds, s);
+                if constexpr (CODEC != KQ_CODEC_Q6_K) {
+                    if (depth >= 2) return launch_one<CODEC, XT, 3, 2, false, WV>(a, grid, lds, s);
+                }
+                return launch_one<CODEC, XT, 3, 1, false, WV>(a, grid, lds, s);
+            }
         }
     }
     return KQ_ERR_BAD_SHAPE;
@@ -526,15 +533,15 @@ int env_int(const char *name, int dflt) {
 
 // Columns of x staged in LDS: all of K, or with XR all but the last block
 // of every wave.
-int mv_kl(const kq_matmul_problem &q, bool xr) {
-    const int nbw = (q.K / KQ_QK + WV - 1) / WV;
-    return xr ? (nbw - 1) * WV * KQ_QK : q.K;
+int mv_kl(const kq_matmul_problem &q, bool xr, int wv = kWaves) {
+    const int nbw = (q.K / KQ_QK + wv - 1) / wv;
+    return xr ? (nbw - 1) * wv * KQ_QK : q.K;
 }
 
 // Bytes of LDS the launch needs: staged x rows and the reduction buffers.
-size_t mv_lds(const kq_matmul_problem &q, bool xr, int bufs) {
-    const size_t xrow = 2 * (size_t)mv_kl(q, xr) + 16;
-    return (size_t)q.M * xrow + (size_t)bufs * WV * 64 * sizeof(floatx4);
+size_t mv_lds(const kq_matmul_problem &q, bool xr, int bufs, int wv = kWaves) {
+    const size_t xrow = 2 * (size_t)mv_kl(q, xr, wv) + 16;
+    return (size_t)q.M * xrow + (size_t)bufs * wv * 64 * sizeof(floatx4);
 }
 
 size_t mv_tables(const kq_matmul_problem &q) { return q.codec == KQ_CODEC_IQ2_XXS ? sizeof(Iq2Tables) : 0; }
@@ -544,7 +551,7 @@ size_t mv_tables(const kq_matmul_problem &q) { return q.codec == KQ_CODEC_IQ2_XX
 int mv_xr(const kq_matmul_problem &q) {
     const size_t avail = (size_t)kLdsBytes - mv_tables(q);
     if (mv_lds(q, false, 1) <= avail) return 0;
-    if (q.K / KQ_QK > WV && mv_lds(q, true, 1) <= avail) return 1;
+    if (q.K / KQ_QK > kWaves && mv_lds(q, true, 1) <= avail) return 1;
     return -1;
 }
 
@@ -570,11 +577,11 @@ bool kq_mv_eligible(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype
     const kq_matmul_problem &q0 = ps[0];
     if (q0.M < 1 || q0.M > 16) return false;
     const int nb = q0.K / KQ_QK;
-    if (nb > 3 * WV) return false;
+    if (nb > 3 * kWaves) return false;
     const int xr = mv_xr(q0);
     if (xr < 0) return false;
     const bool mixed = mv_mixed(ps, n);
-    if (mixed && (xr || nb > 2 * WV)) return false;
+    if (mixed && (xr || nb > 2 * kWaves)) return false;
     for (int i = 0; i < n; ++i) {
         const kq_matmul_problem &q = ps[i];
         if (q.x != q0.x || q.x_row_stride != q0.x_row_stride || q.M != q0.M || q.K != q0.K) return false;
@@ -615,14 +622,26 @@ int kq_mv_launch(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype, h
     a.total_tiles = tiles;
     a.n_problems = n;
     const bool xr = mv_xr(q0) == 1;
-    a.kl = mv_kl(q0, xr);
+    const bool mixed = mv_mixed(ps, n);
+    const int nb = q0.K / KQ_QK;
+    // two 8-wave workgroups per CU for launches of at most two tiles per CU
+    // (measured: q|k|v and o of a Q4_K_M layer 1-3 % faster, gate|up at six
+    // tiles per CU 7 % slower), when x and one reduction buffer fit in half
+    // the LDS and every wave keeps at most two blocks per tile;
+    // GMLX_KQ_MV_WAVES=8 / 16 forces the choice
+    const size_t half = (size_t)kLdsBytes / 2 - mv_tables(q0);
+    const int want = env_int("GMLX_KQ_MV_WAVES", tiles <= 2 * device_cus() ? 8 : kWaves);
+    const bool w8 = want == 8 && !xr && nb <= 16 && mv_lds(q0, false, 1, 8) <= half;
+    const int wv = w8 ? 8 : kWaves;
+    a.kl = mv_kl(q0, xr, wv);
     a.xrow = 2 * a.kl + 16;
     a.red_off = q0.M * a.xrow;
-    a.red_bufs = mv_lds(q0, xr, 2) + mv_tables(q0) <= (size_t)kLdsBytes ? 2 : 1;
-    const size_t lds = mv_lds(q0, xr, a.red_bufs);
-    int grid = env_int("GMLX_KQ_MV_WGS", device_cus());
+    a.red_bufs = w8 ? (mv_lds(q0, false, 2, 8) <= half ? 2 : 1)
+                    : (mv_lds(q0, xr, 2) + mv_tables(q0) <= (size_t)kLdsBytes ? 2 : 1);
+    const size_t lds = mv_lds(q0, xr, a.red_bufs, wv);
+    int grid = env_int("GMLX_KQ_MV_WGS", device_cus() * (kWaves / wv));
     if (grid > tiles) grid = tiles;
-    const int nbw = (q0.K / KQ_QK + WV - 1) / WV;
+    const int nbw = (nb + wv - 1) / wv;
     // ring depth: the tiles each workgroup walks, at most 3 (one block per
     // wave) or 2 (more blocks: register budget; launch_shape lowers it further
     // where the registers run out)
@@ -630,17 +649,34 @@ int kq_mv_launch(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype, h
     const int depth = env_int("GMLX_KQ_MV_DEPTH", per_wg >= 4 ? 3 : per_wg >= 2 ? 2 : 1);
     const int d = min(depth, nbw == 1 ? 3 : 2);
     const bool bf = x_dtype == KQ_DTYPE_BF16;
-    if (mv_mixed(ps, n))
-        return bf ? launch_shape<KQ_MIX, 1>(a, nbw, d, xr, grid, lds, s) : launch_shape<KQ_MIX, 0>(a, nbw, d, xr, grid, lds, s);
+    if (w8) {
+        if (mixed)
+            return bf ? launch_shape<KQ_MIX, 1, 8>(a, nbw, d, false, grid, lds, s)
+                      : launch_shape<KQ_MIX, 0, 8>(a, nbw, d, false, grid, lds, s);
+        switch (q0.codec) {
+        case KQ_CODEC_Q4_K:
+            return bf ? launch_shape<KQ_CODEC_Q4_K, 1, 8>(a, nbw, d, false, grid, lds, s)
+                      : launch_shape<KQ_CODEC_Q4_K, 0, 8>(a, nbw, d, false, grid, lds, s);
+        case KQ_CODEC_Q6_K:
+            return bf ? launch_shape<KQ_CODEC_Q6_K, 1, 8>(a, nbw, d, false, grid, lds, s)
+                      : launch_shape<KQ_CODEC_Q6_K, 0, 8>(a, nbw, d, false, grid, lds, s);
+        default:
+            return bf ? launch_shape<KQ_CODEC_IQ2_XXS, 1, 8>(a, nbw, d, false, grid, lds, s)
+                      : launch_shape<KQ_CODEC_IQ2_XXS, 0, 8>(a, nbw, d, false, grid, lds, s);
+        }
+    }
+    if (mixed)
+        return bf ? launch_shape<KQ_MIX, 1, 16>(a, nbw, d, xr, grid, lds, s)
+                  : launch_shape<KQ_MIX, 0, 16>(a, nbw, d, xr, grid, lds, s);
     switch (q0.codec) {
     case KQ_CODEC_Q4_K:
-        return bf ? launch_shape<KQ_CODEC_Q4_K, 1>(a, nbw, d, xr, grid, lds, s)
-                  : launch_shape<KQ_CODEC_Q4_K, 0>(a, nbw, d, xr, grid, lds, s);
+        return bf ? launch_shape<KQ_CODEC_Q4_K, 1, 16>(a, nbw, d, xr, grid, lds, s)
+                  : launch_shape<KQ_CODEC_Q4_K, 0, 16>(a, nbw, d, xr, grid, lds, s);
     case KQ_CODEC_Q6_K:
-        return bf ? launch_shape<KQ_CODEC_Q6_K, 1>(a, nbw, d, xr, grid, lds, s)
-                  : launch_shape<KQ_CODEC_Q6_K, 0>(a, nbw, d, xr, grid, lds, s);
+        return bf ? launch_shape<KQ_CODEC_Q6_K, 1, 16>(a, nbw, d, xr, grid, lds, s)
+                  : launch_shape<KQ_CODEC_Q6_K, 0, 16>(a, nbw, d, xr, grid, lds, s);
     default:
-        return bf ? launch_shape<KQ_CODEC_IQ2_XXS, 1>(a, nbw, d, xr, grid, lds, s)
-                  : launch_shape<KQ_CODEC_IQ2_XXS, 0>(a, nbw, d, xr, grid, lds, s);
+        return bf ? launch_shape<KQ_CODEC_IQ2_XXS, 1, 16>(a, nbw, d, xr, grid, lds, s)
+                  : launch_shape<KQ_CODEC_IQ2_XXS, 0, 16>(a, nbw, d, xr, grid, lds, s);
     }
 }
