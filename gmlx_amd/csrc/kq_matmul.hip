@@ -469,7 +469,8 @@ __global__ __launch_bounds__(64) void kq_router_kernel(const void *logits, int l
 #pragma unroll
     for (int i = 0; i < kMaxPerLane; ++i)
         if (lane + 64 * i < E) v[i] = v[i] / sum;
-    float picked_sum = 0.f;
+    float picked_sum = 0.f, my_score = 0.f;
+    int my_ind = 0;
     for (int j = 0; j < k; ++j) {
         float best = -2.f;
         int bi = 0x7FFFFFFF;
@@ -493,13 +494,16 @@ __global__ __launch_bounds__(64) void kq_router_kernel(const void *logits, int l
         for (int i = 0; i < kMaxPerLane; ++i)
             if (lane + 64 * i == bi) v[i] = -1.f;
         picked_sum += best;
-        if (lane == 0) {
-            inds[(int64_t)t * k + j] = bi;
-            scores[(int64_t)t * k + j] = best;
+        // lane j keeps pick j (best / bi are uniform over the wave here)
+        if (lane == j) {
+            my_score = best;
+            my_ind = bi;
         }
     }
-    if (norm && lane == 0) {
-        for (int j = 0; j < k; ++j) scores[(int64_t)t * k + j] = scores[(int64_t)t * k + j] / picked_sum;
+    // one store per output array; picks are renormalised from registers
+    if (lane < k) {
+        inds[(int64_t)t * k + lane] = my_ind;
+        scores[(int64_t)t * k + lane] = norm ? my_score / picked_sum : my_score;
     }
 }
 
