@@ -254,13 +254,30 @@ __attribute__((amdgpu_waves_per_eu(gather_waves_per_simd<CODEC, MT, NW, XT>())))
 }
 
 
+// Activation rows of one segment staged in LDS as fp16 (converted the way the
+// global loaders convert), row i at base + i * stride bytes.
+struct XRowsLds {
+    uint32_t base;  // LDS byte address of the lane's row
+    template <int XT>
+    __device__ __forceinline__ half8_t load(int, int elem) const {
+        return __builtin_bit_cast(half8_t,
+                                  *(const __attribute__((address_space(3))) u32x4 *)(uintptr_t)(base + (uint32_t)elem * 2));
+    }
+};
+
+constexpr int kGatherLdsBytes = 32 * 1024;  // staged activation rows per workgroup
+
 // Short K: one wave per (segment slot, tile) unit, kGatherWaves units per
 // workgroup (consecutive tiles of one expert), the whole K in the wave; no
-// cross-wave reduction.
+// cross-wave reduction.  When the workgroup's units share one segment of at
+// most 16 rows whose activations fit kGatherLdsBytes, the rows are staged in
+// LDS once for the four waves (their fragments are read from LDS instead of
+// once per tile from L2); otherwise each wave loads them from memory.
 template <int CODEC, int MT, int XT, int NW>
 __global__ __launch_bounds__(64 * kGatherWaves)
 __attribute__((amdgpu_waves_per_eu(gather_waves_per_simd<CODEC, MT, NW, XT>()))) void kq_gather_wave_kernel(GatherArgs a) {
     __shared__ Iq2Tables iq2_tab;
+    __shared__ __attribute__((aligned(16))) uint8_t xs_lds[MT == 1 ? kGatherLdsBytes : 16];
     if constexpr (CODEC == KQ_CODEC_IQ2_XXS) load_iq2_tables(iq2_tab);
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lane = kq_lane();
@@ -269,6 +286,32 @@ __attribute__((amdgpu_waves_per_eu(gather_waves_per_simd<CODEC, MT, NW, XT>())))
     const int slot = unit / a.n_tiles;
     const int nt = unit - slot * a.n_tiles;
     const int S = a.seg_info[0];
+    const int nb = a.K / KQ_QK;
+    // ---- staging decision, uniform over the workgroup
+    bool staged = false;
+    uint32_t xrow_bytes = 0;
+    if constexpr (MT == 1) {
+        const int u0 = blockIdx.x * kGatherWaves;
+        const int s0 = u0 / a.n_tiles, s3 = (u0 + kGatherWaves - 1) / a.n_tiles;
+        if (s0 == s3 && s0 < S) {
+            const int rows = a.seg_info[1 + a.n_experts + s0 + 1] - a.seg_info[1 + a.n_experts + s0];
+            xrow_bytes = (uint32_t)a.K * 2 + 16;  // padded: rows start on different banks
+            staged = rows <= 16 && (uint32_t)rows * xrow_bytes <= (uint32_t)kGatherLdsBytes;
+            if (staged) {
+                const int begin = a.seg_info[1 + a.n_experts + s0];
+                const int per_row = a.K / 8;  // 8 activations (16 bytes of fp16) per item
+                for (int i = threadIdx.x; i < rows * per_row; i += 64 * kGatherWaves) {
+                    const int row = i / per_row, c = i - row * per_row;
+                    const char *src = a.x + ((int64_t)(a.pair_order[begin + row] / a.x_pair_div) * a.x_stride +
+                                             (int64_t)c * 8) * x_elem_bytes<XT>();
+                    *(__attribute__((address_space(3))) half8_t *)(uintptr_t)(
+                        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)xs_lds + row * xrow_bytes + c * 16) =
+                        load_x8<XT>(src);
+                }
+            }
+            __syncthreads();
+        }
+    }
     if (slot == 0) {
         // pairs whose expert id is out of range (never routed) get zeros in
         // this tile's columns
@@ -285,11 +328,38 @@ __attribute__((amdgpu_waves_per_eu(gather_waves_per_simd<CODEC, MT, NW, XT>())))
     const int n = nt * 16 + r;
     const bool n_valid = n < a.N;
     const int nc = n_valid ? n : a.N - 1;
-    const int nb = a.K / KQ_QK;
     const uint8_t *wrow[NW];
     wrow[0] = a.w0 + (int64_t)expert * a.w_expert_bytes + (int64_t)nc * a.w_row_bytes;
     if constexpr (NW == 2)
         wrow[1] = a.w1 + (int64_t)expert * a.w_expert_bytes + (int64_t)nc * a.w_row_bytes;
+    auto epilogue = [&](const floatx4 (&acc)[NW][MT], int c0) {
+        if (!n_valid) return;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int ri = c0 + 16 * mt + 4 * (lane >> 4) + e;
+                if (ri >= seg_end) continue;
+                const int pair = a.pair_order[ri];
+                float v = acc[0][mt][e];
+                if constexpr (NW == 2) v = act_apply(a.act, v) * acc[1][mt][e];
+                kq_store_out(a.y, a.y_dtype, (int64_t)pair * a.y_stride + n, v);
+            }
+        }
+    };
+    if constexpr (MT == 1) {
+        if (staged) {
+            XRowsLds xl;
+            xl.base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)xs_lds +
+                      (uint32_t)min(r, seg_end - seg_begin - 1) * xrow_bytes;
+            floatx4 acc[NW][MT];
+#pragma unroll
+            for (int i = 0; i < NW; ++i) acc[i][0] = floatx4{0, 0, 0, 0};
+            tile_accumulate<CODEC, MT, XT, NW, XRowsLds, false>(wrow, 0, 1, nb, xl, acc, iq2_tab);
+            epilogue(acc, seg_begin);
+            return;
+        }
+    }
     for (int c0 = seg_begin; c0 < seg_end; c0 += 16 * MT) {
         XRowPtrs<MT> xrow;
 #pragma unroll
@@ -304,19 +374,7 @@ __attribute__((amdgpu_waves_per_eu(gather_waves_per_simd<CODEC, MT, NW, XT>())))
             for (int mt = 0; mt < MT; ++mt) acc[i][mt] = floatx4{0, 0, 0, 0};
         // no prefetch stage (two would not fit 128 VGPRs): resident waves hide the latency
         tile_accumulate<CODEC, MT, XT, NW, XRowPtrs<MT>, false>(wrow, 0, 1, nb, xrow, acc, iq2_tab);
-        if (!n_valid) continue;
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int ri = c0 + 16 * mt + 4 * (lane >> 4) + e;
-                if (ri >= seg_end) continue;
-                const int pair = a.pair_order[ri];
-                float v = acc[0][mt][e];
-                if constexpr (NW == 2) v = act_apply(a.act, v) * acc[1][mt][e];
-                kq_store_out(a.y, a.y_dtype, (int64_t)pair * a.y_stride + n, v);
-            }
-        }
+        epilogue(acc, c0);
     }
 }
 
