@@ -97,10 +97,11 @@ def make_inputs(torch, rng, B):
 # The launches of one layer: (name, matrices), and the kernel that serves
 # each (kq_quantized_matmul_grouped's routing): at B <= 16 every launch takes
 # the LDS-staged persistent small-batch kernel (q|k|v: Q4_K and Q6_K tiles in
-# one launch, 1.5 tiles per CU, ring of 2; o: one tile per CU, ring of 1;
-# gate|up: six tiles per CU, ring of 3; down: K = 12288 Q6_K, three blocks
-# per wave, the last 4096 columns of x in registers at B > 4, LDS-staged only
-# up to B = 8); at B > 16 every launch takes the general kernel.
+# one launch and o, at most two tiles per CU: two 8-wave workgroups per CU,
+# one tile each; gate|up: six tiles per CU, one 16-wave workgroup, ring of 3;
+# down: K = 12288 Q6_K, three blocks per wave, the last 4096 columns of x in
+# registers at B > 4, LDS-staged only up to B = 8); at B > 16 every launch
+# takes the general kernel (two column tiles per workgroup).
 LAUNCHES = [("qkv", ("q", "k", "v")), ("o", ("o",)), ("gate_up", ("gate", "up")), ("down", ("down",))]
 CODEC = {name: codec for name, _, _, codec in LAYER}
 DIMS = {name: (N, K) for name, N, K, _ in LAYER}
