@@ -24,19 +24,22 @@ KQ_ERR_WORKSPACE_TOO_SMALL = -6
 KQ_ERR_LAUNCH_FAILED = -7
 KQ_ERR_TOO_MANY_PROBLEMS = -8
 KQ_ERR_BAD_ARGUMENT = -9
+KQ_ERR_IO = -10
+KQ_ERR_BAD_FORMAT = -11
 
 CODEC_ID = {"q4_k": 12, "q6_k": 14, "iq2_xxs": 16}
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 OP_DEQUANTIZE, OP_QUANTIZE, OP_MATMUL, OP_GATHER, OP_MOE_GLU, OP_SDPA = range(6)
 MAX_GROUP = 8
 
-# every symbol include/kq_capi.h declares, checked at load
+# every symbol include/kq_capi.h and include/kq_gguf.h declare, checked at load
 EXPORTS = (
     "kq_version", "kq_strerror", "kq_codec_block_bytes", "kq_supports", "kq_iq2xxs_grid_host",
     "kq_dequantize", "kq_quantize", "kq_matmul_workspace_bytes", "kq_quantized_matmul_grouped",
     "kq_moe_route", "kq_gather_qmm", "kq_moe_glu_gather", "kq_moe_mix", "kq_moe_router_topk",
     "kq_sdpa_workspace_bytes", "kq_sdpa_decode_ragged",
     "kq_sdpa_cascade_workspace_bytes", "kq_sdpa_decode_gqa_cascade",
+    "kq_gguf_open", "kq_gguf_close", "kq_gguf_header", "kq_gguf_kv", "kq_gguf_tensor", "kq_gguf_type_size",
 )
 
 
@@ -96,6 +99,15 @@ _SIGS = {
     "kq_sdpa_cascade_workspace_bytes": ([_i32, _i32, _i32, _i32, _i32, _i32, _i32], _sz),
     "kq_sdpa_decode_gqa_cascade": ([_vp, _vp, _vp, _i64, _i32, _vp, _vp, _i64, _i64, _i32, _vp, _i32, _i32,
                                     _i32, _i32, _i32, _f32, _int, _vp, _vp, _sz, _vp], _int),
+    "kq_gguf_open": ([ctypes.c_char_p, ctypes.POINTER(_vp)], _int),
+    "kq_gguf_close": ([_vp], None),
+    "kq_gguf_header": ([_vp, ctypes.POINTER(ctypes.c_uint32)] + [ctypes.POINTER(_i64)] * 6, _int),
+    "kq_gguf_kv": ([_vp, _i64, ctypes.POINTER(_vp), ctypes.POINTER(_i64), ctypes.POINTER(ctypes.c_uint32),
+                    ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(_i64), ctypes.POINTER(_vp)], _int),
+    "kq_gguf_tensor": ([_vp, _i64, ctypes.POINTER(_vp), ctypes.POINTER(_i64), ctypes.POINTER(ctypes.c_uint32),
+                        ctypes.POINTER(_i64), ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(_i64),
+                        ctypes.POINTER(_i64), ctypes.POINTER(_vp)], _int),
+    "kq_gguf_type_size": ([ctypes.c_uint32, ctypes.POINTER(_i32), ctypes.POINTER(_i32)], _int),
 }
 
 

@@ -118,6 +118,8 @@ const char *kq_strerror(int code) {
     case KQ_ERR_LAUNCH_FAILED: return "kernel launch failed";
     case KQ_ERR_TOO_MANY_PROBLEMS: return "too many problems in one grouped call";
     case KQ_ERR_BAD_ARGUMENT: return "bad argument";
+    case KQ_ERR_IO: return "file could not be opened or mapped";
+    case KQ_ERR_BAD_FORMAT: return "malformed GGUF file";
     default: return "unknown kq status";
     }
 }

@@ -39,7 +39,9 @@ typedef enum {
     KQ_ERR_WORKSPACE_TOO_SMALL = -6,
     KQ_ERR_LAUNCH_FAILED = -7,
     KQ_ERR_TOO_MANY_PROBLEMS = -8,
-    KQ_ERR_BAD_ARGUMENT = -9
+    KQ_ERR_BAD_ARGUMENT = -9,
+    KQ_ERR_IO = -10,         /* a file could not be opened or mapped (kq_gguf.h) */
+    KQ_ERR_BAD_FORMAT = -11  /* a malformed GGUF header (kq_gguf.h) */
 } kq_status;
 
 /* Codec ids are the GGML type ids (gguf GGMLQuantizationType). */

@@ -1,5 +1,5 @@
 """Host-side checks that need no GPU: the C-ABI library loads and exports
-every symbol include/kq_capi.h declares, capability probes and error strings,
+every symbol include/kq_capi.h and include/kq_gguf.h declare, capability probes and error strings,
 the ops' CPU-side validation and decline rails, fault injection, the wire-K
 rule, and the leaf-module swap."""
 import os
@@ -13,9 +13,12 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def _header_symbols():
-    text = open(os.path.join(ROOT, "include", "kq_capi.h")).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(kq_[a-z0-9_]+)\s*\(", text)))
+    names = set()
+    for h in ("kq_capi.h", "kq_gguf.h"):
+        text = open(os.path.join(ROOT, "include", h)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names |= set(re.findall(r"\b(kq_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 def test_library_exports_every_declared_symbol():
