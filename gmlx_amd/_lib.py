@@ -36,7 +36,7 @@ MAX_GROUP = 8
 EXPORTS = (
     "kq_version", "kq_strerror", "kq_codec_block_bytes", "kq_supports", "kq_iq2xxs_grid_host",
     "kq_dequantize", "kq_quantize", "kq_matmul_workspace_bytes", "kq_quantized_matmul_grouped",
-    "kq_moe_route", "kq_gather_qmm", "kq_moe_glu_gather", "kq_moe_mix", "kq_moe_router_topk",
+    "kq_moe_route", "kq_gather_qmm", "kq_moe_glu_gather", "kq_moe_gather_rows", "kq_moe_mix", "kq_moe_router_topk",
     "kq_sdpa_workspace_bytes", "kq_sdpa_decode_ragged",
     "kq_sdpa_cascade_workspace_bytes", "kq_sdpa_decode_gqa_cascade",
     "kq_gguf_open", "kq_gguf_close", "kq_gguf_header", "kq_gguf_kv", "kq_gguf_tensor", "kq_gguf_type_size",
@@ -91,6 +91,8 @@ _SIGS = {
                        _vp, _int, _i64, _vp], _int),
     "kq_moe_glu_gather": ([_vp, _int, _i64, _i32, _vp, _vp, _i64, _i64, _i32, _i32, _int, _int, _vp, _vp,
                            _i32, _i32, _vp, _vp], _int),
+    "kq_moe_gather_rows": ([_vp, _int, _i64, _i32, _i32, _vp, _vp, _i64, _i64, _i32, _i32, _int, _int, _vp, _vp,
+                            _i32, _i32, _vp, _int, _i64, _i32, _vp], _int),
     "kq_moe_mix": ([_vp, _vp, _i32, _i32, _i32, _vp, _int, _vp], _int),
     "kq_moe_router_topk": ([_vp, _int, _i32, _i32, _i32, _int, _vp, _vp, _vp], _int),
     "kq_sdpa_workspace_bytes": ([_i32, _i32, _i32, _i32, _i32], _sz),

@@ -145,7 +145,18 @@ struct GatherArgs {
     const int32_t *pair_order;
     int64_t x_stride, w_expert_bytes, w_row_bytes, y_stride;
     int32_t x_pair_div, N, K, n_pairs, n_experts, n_tiles, y_dtype, act;
+    // row of pair p: x  p / x_pair_div + p / x_skip,  y  p + p / y_skip
+    // (a skip of 0 adds nothing): one spare row per x_skip / y_skip pairs,
+    // e.g. the shared expert's slot k of an [t, k + 1, N] block
+    int32_t x_skip, y_skip;
 };
+
+__device__ __forceinline__ int64_t gather_x_row(const GatherArgs &a, int pair) {
+    return pair / a.x_pair_div + (a.x_skip ? pair / a.x_skip : 0);
+}
+__device__ __forceinline__ int64_t gather_y_row(const GatherArgs &a, int pair) {
+    return pair + (a.y_skip ? pair / a.y_skip : 0);
+}
 
 __device__ __forceinline__ float act_apply(int act, float g) {
     if (act == 0) return g / (1.0f + __expf(-g));  // silu
@@ -193,7 +204,7 @@ __attribute__((amdgpu_waves_per_eu(gather_waves_per_simd<CODEC, MT, NW, XT>())))
         const int c = nt * 16 + (threadIdx.x & 15);
         if (c < a.N)
             for (int p = threadIdx.x >> 4; p < a.n_pairs; p += 4 * kGatherWaves)
-                if (flag[p] < 0) kq_store_out(a.y, a.y_dtype, (int64_t)p * a.y_stride + c, 0.f);
+                if (flag[p] < 0) kq_store_out(a.y, a.y_dtype, gather_y_row(a, p) * a.y_stride + c, 0.f);
     }
     const int S = a.seg_info[0];
     if (slot >= S) return;  // uniform over the workgroup
@@ -213,7 +224,7 @@ __attribute__((amdgpu_waves_per_eu(gather_waves_per_simd<CODEC, MT, NW, XT>())))
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
             const int ri = min(c0 + 16 * mt + r, seg_end - 1);
-            xrow.row[mt] = a.x + (int64_t)(a.pair_order[ri] / a.x_pair_div) * a.x_stride * x_elem_bytes<XT>();
+            xrow.row[mt] = a.x + gather_x_row(a, a.pair_order[ri]) * a.x_stride * x_elem_bytes<XT>();
         }
         floatx4 acc[NW][MT];
 #pragma unroll
@@ -245,7 +256,7 @@ __attribute__((amdgpu_waves_per_eu(gather_waves_per_simd<CODEC, MT, NW, XT>())))
                     const int pair = a.pair_order[ri];
                     float v = acc[0][mt][e];
                     if constexpr (NW == 2) v = act_apply(a.act, v) * acc[1][mt][e];
-                    kq_store_out(a.y, a.y_dtype, (int64_t)pair * a.y_stride + n, v);
+                    kq_store_out(a.y, a.y_dtype, gather_y_row(a, pair) * a.y_stride + n, v);
                 }
             }
         }
@@ -302,7 +313,7 @@ __attribute__((amdgpu_waves_per_eu(gather_waves_per_simd<CODEC, MT, NW, XT>())))
                 const int per_row = a.K / 8;  // 8 activations (16 bytes of fp16) per item
                 for (int i = threadIdx.x; i < rows * per_row; i += 64 * kGatherWaves) {
                     const int row = i / per_row, c = i - row * per_row;
-                    const char *src = a.x + ((int64_t)(a.pair_order[begin + row] / a.x_pair_div) * a.x_stride +
+                    const char *src = a.x + (gather_x_row(a, a.pair_order[begin + row]) * a.x_stride +
                                              (int64_t)c * 8) * x_elem_bytes<XT>();
                     *(__attribute__((address_space(3))) half8_t *)(uintptr_t)(
                         (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)xs_lds + row * xrow_bytes + c * 16) =
@@ -319,7 +330,7 @@ __attribute__((amdgpu_waves_per_eu(gather_waves_per_simd<CODEC, MT, NW, XT>())))
         const int c = nt * 16 + r;
         if (c < a.N)
             for (int p = lane >> 4; p < a.n_pairs; p += 4)
-                if (flag[p] < 0) kq_store_out(a.y, a.y_dtype, (int64_t)p * a.y_stride + c, 0.f);
+                if (flag[p] < 0) kq_store_out(a.y, a.y_dtype, gather_y_row(a, p) * a.y_stride + c, 0.f);
     }
     if (slot >= S) return;  // uniform over the wave
     const int expert = a.seg_info[1 + slot];
@@ -343,7 +354,7 @@ __attribute__((amdgpu_waves_per_eu(gather_waves_per_simd<CODEC, MT, NW, XT>())))
                 const int pair = a.pair_order[ri];
                 float v = acc[0][mt][e];
                 if constexpr (NW == 2) v = act_apply(a.act, v) * acc[1][mt][e];
-                kq_store_out(a.y, a.y_dtype, (int64_t)pair * a.y_stride + n, v);
+                kq_store_out(a.y, a.y_dtype, gather_y_row(a, pair) * a.y_stride + n, v);
             }
         }
     };
@@ -365,7 +376,7 @@ __attribute__((amdgpu_waves_per_eu(gather_waves_per_simd<CODEC, MT, NW, XT>())))
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
             const int ri = min(c0 + 16 * mt + r, seg_end - 1);
-            xrow.row[mt] = a.x + (int64_t)(a.pair_order[ri] / a.x_pair_div) * a.x_stride * x_elem_bytes<XT>();
+            xrow.row[mt] = a.x + gather_x_row(a, a.pair_order[ri]) * a.x_stride * x_elem_bytes<XT>();
         }
         floatx4 acc[NW][MT];
 #pragma unroll
@@ -697,14 +708,15 @@ int gather_common(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pa
                   const void *w1, int64_t w_expert_bytes, int64_t w_row_bytes, int32_t N, int32_t K,
                   int codec, int act, const int32_t *seg_info, const int32_t *pair_order,
                   int32_t n_pairs, int32_t n_experts, void *y, int y_dtype, int64_t y_row_stride,
-                  hipStream_t s) {
+                  hipStream_t s, int32_t x_skip = 0, int32_t y_skip = 0) {
     if (!x || !w0 || !seg_info || !pair_order || !y) return KQ_ERR_NULL_POINTER;
     if (kq_block_bytes(codec) == 0) return KQ_ERR_UNSUPPORTED_CODEC;
     if (x_dtype != KQ_DTYPE_F16 && x_dtype != KQ_DTYPE_BF16 && x_dtype != KQ_DTYPE_F32)
         return KQ_ERR_UNSUPPORTED_DTYPE;
     if (y_dtype != KQ_DTYPE_F32 && y_dtype != KQ_DTYPE_F16 && y_dtype != KQ_DTYPE_BF16)
         return KQ_ERR_UNSUPPORTED_DTYPE;
-    if (N <= 0 || K <= 0 || K % KQ_QK || n_pairs < 0 || n_experts <= 0 || x_pair_div <= 0)
+    if (N <= 0 || K <= 0 || K % KQ_QK || n_pairs < 0 || n_experts <= 0 || x_pair_div <= 0 || x_skip < 0 ||
+        y_skip < 0)
         return KQ_ERR_BAD_SHAPE;
     if (n_pairs == 0) return KQ_OK;
     const int64_t need = (int64_t)(K / KQ_QK) * kq_block_bytes(codec);
@@ -727,6 +739,8 @@ int gather_common(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pa
     a.w_row_bytes = w_row_bytes;
     a.y_stride = y_row_stride;
     a.x_pair_div = x_pair_div;
+    a.x_skip = x_skip;
+    a.y_skip = y_skip;
     a.N = N;
     a.K = K;
     a.n_pairs = n_pairs;
@@ -921,6 +935,18 @@ int kq_moe_glu_gather(const void *x, int x_dtype, int64_t x_row_stride, int32_t 
     return gather_common(x, x_dtype, x_row_stride, x_pair_div, w_gate, w_up, w_expert_bytes, w_row_bytes,
                          N, K, codec, act, seg_info, pair_order, n_pairs, n_experts, h, KQ_DTYPE_F32, N,
                          (hipStream_t)stream);
+}
+
+int kq_moe_gather_rows(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pair_div, int32_t x_skip,
+                       const void *w0, const void *w1, int64_t w_expert_bytes, int64_t w_row_bytes, int32_t N,
+                       int32_t K, int codec, int act, const int32_t *seg_info, const int32_t *pair_order,
+                       int32_t n_pairs, int32_t n_experts, void *y, int y_dtype, int64_t y_row_stride,
+                       int32_t y_skip, kq_stream_t stream) {
+    if (w1 && act != 0 && act != 1) return KQ_ERR_BAD_ARGUMENT;
+    if (w1 && y_dtype != KQ_DTYPE_F32) return KQ_ERR_UNSUPPORTED_DTYPE;
+    return gather_common(x, x_dtype, x_row_stride, x_pair_div, w0, w1, w_expert_bytes, w_row_bytes, N, K, codec,
+                         w1 ? act : 0, seg_info, pair_order, n_pairs, n_experts, y, y_dtype, y_row_stride,
+                         (hipStream_t)stream, x_skip, y_skip);
 }
 
 int kq_moe_mix(const float *y_pairs, const float *scores, int32_t T, int32_t top_k, int32_t N, void *y,

@@ -370,6 +370,124 @@ def gather_qmv_mix_ns_kq(h, down_w, codec, idx, scores, out_dtype=torch.float32)
     return y
 
 
+_ONE_EXPERT = OrderedDict()  # (device, rows) -> routing tables sending every row to expert 0
+
+
+def _one_expert_route(device, rows):
+    """seg_info / pair_order (with its flags) of `rows` pairs all routed to
+    expert 0, in kq_moe_route's layout; memoised per device and size."""
+    key = (str(device), rows)
+    hit = _ONE_EXPERT.get(key)
+    if hit is not None:
+        _ONE_EXPERT.move_to_end(key)
+        return hit
+    seg = torch.tensor([1, 0, 0, rows], dtype=torch.int32, device=device)
+    order = torch.cat([torch.arange(rows, dtype=torch.int32), torch.zeros(rows, dtype=torch.int32)]).to(device)
+    _ONE_EXPERT[key] = (seg, order)
+    if len(_ONE_EXPERT) > 64:
+        _ONE_EXPERT.popitem(last=False)
+    return seg, order
+
+
+def _shared_matrix(w, codec, K, name):
+    """A shared expert's wire matrix [N, K/256 * block_bytes] as a one-expert stack."""
+    if w.dim() != 2 or w.dtype != torch.uint8:
+        raise ValueError(f"{name} must be a uint8 wire matrix [N, K/256*block_bytes]")
+    if wire_k(w.shape[-1], codec) != K:
+        raise ValueError(f"{name} rows hold K={wire_k(w.shape[-1], codec)}, activations have K={K}")
+    return w.contiguous().unsqueeze(0)
+
+
+def _gather_rows(x_ptr, x_dt, x_stride, x_pair_div, x_skip, w, w_up, codec, act, seg, order, P, E, y_ptr, y_dt,
+                 y_stride, y_skip, K, stream):
+    rc = lib().kq_moe_gather_rows(x_ptr, x_dt, x_stride, x_pair_div, x_skip, w.data_ptr(),
+                                  None if w_up is None else w_up.data_ptr(), w.stride(0), w.stride(1), w.shape[1],
+                                  K, _codec_id(codec), act, seg.data_ptr(), order.data_ptr(), P, E, y_ptr, y_dt,
+                                  y_stride, y_skip, stream)
+    check("kq_moe_gather_rows", rc)
+
+
+def moe_glu_gather_shexp_kq(x, gate_w, up_w, shexp_gate_w, shexp_up_w, codec, idx, act="silu",
+                            shexp_kquant_type=None):
+    """kq.moe_glu_gather_shexp_kq (gmlx/modules.py:571-574, 777-780): the
+    routed GLU gather of moe_glu_gather_kq plus the shared expert's GLU on
+    every token, h (t, k + 1, I) float32 with the shared expert in slot k.
+    The shared matrices may use another codec (`shexp_kquant_type`); their
+    intermediate size must equal the routed experts'."""
+    _fault("moe_glu_gather_shexp_kq")
+    _require_gpu(x, gate_w, up_w, shexp_gate_w, shexp_up_w, idx)
+    if act not in _ACTS:
+        raise ValueError(f"act {act!r} has no kernel epilogue; have {tuple(_ACTS)}")
+    K = x.shape[-1]
+    t, k = idx.shape[0], idx.shape[-1]
+    x2 = _rows_view(x)
+    if x2.shape[0] != t:
+        raise ValueError(f"x has {x2.shape[0]} rows for {t} index rows")
+    gate_w = _expert_stack(gate_w, codec, K)
+    up_w = _expert_stack(up_w, codec, K)
+    if gate_w.shape != up_w.shape or gate_w.stride() != up_w.stride():
+        raise ValueError("gate and up stacks must share shape and layout")
+    scodec = shexp_kquant_type or codec
+    sg = _shared_matrix(shexp_gate_w, scodec, K, "shexp_gate_w")
+    su = _shared_matrix(shexp_up_w, scodec, K, "shexp_up_w")
+    E, I = gate_w.shape[0], gate_w.shape[1]
+    if sg.shape != su.shape or sg.shape[1] != I:
+        raise ValueError(f"shared gate/up must both have {I} rows (the routed intermediate size)")
+    h = torch.empty((t, k + 1, I), dtype=torch.float32, device=x.device)
+    if t == 0:
+        return h
+    s = _stream(x)
+    xd = _x_dt(x2)
+    if k:
+        seg, order = moe_route(idx.reshape(t, k), E)
+        _gather_rows(x2.data_ptr(), xd, x2.stride(0), k, 0, gate_w, up_w, codec, _ACTS[act], seg, order, t * k, E,
+                     h.data_ptr(), DTYPE_F32, I, k, K, s)
+    seg1, order1 = _one_expert_route(x.device, t)
+    _gather_rows(x2.data_ptr(), xd, x2.stride(0), 1, 0, sg, su, scodec, _ACTS[act], seg1, order1, t, 1,
+                 h.data_ptr() + k * I * 4, DTYPE_F32, (k + 1) * I, 0, K, s)
+    return h
+
+
+def gather_qmv_mix_kq(h, down_w, shexp_down_w, codec, idx, scores, shexp_kquant_type=None,
+                      out_dtype=torch.float32):
+    """kq.gather_qmv_mix_kq (gmlx/modules.py:581-583, 784-786): h (t, k + 1, I)
+    from moe_glu_gather_shexp_kq; y[t] = sum_s scores[t, s] * (Wd[idx[t, s]] .
+    h[t, s]) + scores[t, k] * (Wsd . h[t, k]), the k + 1 products in fp32 and
+    summed in slot order."""
+    _fault("gather_qmv_mix_kq")
+    _require_gpu(h, down_w, shexp_down_w, idx, scores)
+    t, k = idx.shape[0], idx.shape[-1]
+    if h.dim() != 3 or tuple(h.shape[:2]) != (t, k + 1):
+        raise ValueError("h must be (t, k + 1, I): routed slots then the shared expert")
+    if tuple(scores.reshape(t, -1).shape) != (t, k + 1):
+        raise ValueError("scores must hold k + 1 mix weights per token (the shared expert's last)")
+    I = h.shape[-1]
+    h = h.contiguous()
+    down_w = _expert_stack(down_w, codec, I)
+    scodec = shexp_kquant_type or codec
+    sd = _shared_matrix(shexp_down_w, scodec, I, "shexp_down_w")
+    E, D = down_w.shape[0], down_w.shape[1]
+    if sd.shape[1] != D:
+        raise ValueError(f"shared down must have {D} rows (the routed output size)")
+    y = torch.empty((t, D), dtype=out_dtype, device=h.device)
+    if t == 0:
+        return y
+    s = _stream(h)
+    hd = _x_dt(h)
+    yp = torch.empty((t, k + 1, D), dtype=torch.float32, device=h.device)
+    if k:
+        seg, order = moe_route(idx.reshape(t, k), E)
+        _gather_rows(h.data_ptr(), hd, I, 1, k, down_w, None, codec, 0, seg, order, t * k, E, yp.data_ptr(),
+                     DTYPE_F32, D, k, I, s)
+    seg1, order1 = _one_expert_route(h.device, t)
+    _gather_rows(h.data_ptr() + k * I * h.element_size(), hd, (k + 1) * I, 1, 0, sd, None, scodec, 0, seg1, order1,
+                 t, 1, yp.data_ptr() + k * D * 4, DTYPE_F32, (k + 1) * D, 0, I, s)
+    sc = scores.reshape(t, k + 1).to(torch.float32).contiguous()
+    check("kq_moe_mix", lib().kq_moe_mix(yp.data_ptr(), sc.data_ptr(), t, k + 1, D, y.data_ptr(), _dt(out_dtype),
+                                         s))
+    return y
+
+
 def moe_router_topk(logits, k, norm_topk_prob=True):
     """softmax(fp32) -> top-k (descending, ties to the lower expert id) ->
     optional renormalisation (stock form gmlx/modules.py:754-760).

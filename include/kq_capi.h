@@ -160,6 +160,23 @@ int kq_moe_glu_gather(const void *x, int x_dtype, int64_t x_row_stride, int32_t 
                       const int32_t *seg_info, const int32_t *pair_order, int32_t n_pairs,
                       int32_t n_experts, float *h, kq_stream_t stream);
 
+/* The general form of the two gathers above, for pair rows laid out with a
+ * spare row every few pairs: kq.moe_glu_gather_shexp_kq(x, gate_w, up_w,
+ * shexp_gate_w, shexp_up_w, codec, idx, act=) and kq.gather_qmv_mix_kq(h,
+ * down_w, shexp_down_w, codec, idx, scores) (gmlx/modules.py:571-584,
+ * 777-787) keep the shared expert in slot k of [t, k + 1, N] blocks.
+ * Pair p reads x row p / x_pair_div + p / x_skip and writes y row
+ * p + p / y_skip (a skip of 0 adds nothing).  w1 == NULL: plain gather
+ * (y of y_dtype); w1 != NULL: fused GLU with act as in kq_moe_glu_gather
+ * (y fp32).  The shared expert itself is a one-expert gather (n_experts 1,
+ * every pair routed to it). */
+int kq_moe_gather_rows(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pair_div,
+                       int32_t x_skip, const void *w0, const void *w1, int64_t w_expert_bytes,
+                       int64_t w_row_bytes, int32_t N, int32_t K, int codec, int act,
+                       const int32_t *seg_info, const int32_t *pair_order, int32_t n_pairs,
+                       int32_t n_experts, void *y, int y_dtype, int64_t y_row_stride,
+                       int32_t y_skip, kq_stream_t stream);
+
 /* The routing mix of kq.gather_qmv_mix_ns_kq (gmlx/modules.py:591-593):
  * y[t, :] = sum_s scores[t, s] * y_pairs[t*k + s, :], fp32, slots summed in
  * order s = 0..k-1.  y_pairs fp32 [T*k, N]; scores fp32 [T, k]; y of y_dtype. */

@@ -157,3 +157,44 @@ def test_switch_linear_module():
     deq = okq.dequantize(w, "q6_k").astype(np.float64)
     ref = np.stack([[deq[idx[t, s]] @ x[t].astype(np.float64) for s in range(2)] for t in range(4)])
     assert okq.max_rel(got[:, :, 0], ref) <= TOL
+
+
+@pytest.mark.parametrize("codec,scodec,T,k,E", [("q4_k", None, 5, 4, 16), ("q4_k", "q6_k", 3, 8, 64),
+                                                  ("iq2_xxs", None, 8, 8, 32), ("q6_k", "q4_k", 1, 2, 4)])
+def test_shared_expert_glu_and_mix(codec, scodec, T, k, E):
+    """moe_glu_gather_shexp_kq / gather_qmv_mix_kq: the shared expert in slot
+    k of h and of the mix (gmlx/modules.py:571-584, 777-787), a different
+    codec for the shared matrices included; routed slots equal the plain
+    fused ops' results."""
+    import torch
+    from gmlx_amd import ops
+    rng = np.random.default_rng(T * 100 + k)
+    D, I = 512, 256
+    sc_codec = scodec or codec
+    gw, uw = _experts(rng, codec, E, I, D), _experts(rng, codec, E, I, D)
+    dw = _experts(rng, codec, E, D, I)
+    sg, su = _experts(rng, sc_codec, 1, I, D)[0], _experts(rng, sc_codec, 1, I, D)[0]
+    sd = _experts(rng, sc_codec, 1, D, I)[0]
+    x = fp16_rows(rng, T, D)
+    idx = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    sc = rng.uniform(0.05, 1.0, size=(T, k + 1)).astype(np.float32)
+    kw = {"shexp_kquant_type": scodec} if scodec else {}
+    h = ops.moe_glu_gather_shexp_kq(_dev(x), _dev(gw), _dev(uw), _dev(sg), _dev(su), codec, _dev(idx), act="silu",
+                                    **kw)
+    assert h.dtype == torch.float32 and tuple(h.shape) == (T, k + 1, I)
+    deq = lambda w, c: okq.dequantize(w, c).astype(np.float64)  # noqa: E731
+    G, U, Dd = deq(gw, codec), deq(uw, codec), deq(dw, codec)
+    SG, SU, SD = deq(sg, sc_codec), deq(su, sc_codec), deq(sd, sc_codec)
+    xf = x.astype(np.float64)
+    silu = lambda z: z / (1 + np.exp(-z))  # noqa: E731
+    href = np.stack([[silu(G[idx[t, s]] @ xf[t]) * (U[idx[t, s]] @ xf[t]) for s in range(k)]
+                     + [silu(SG @ xf[t]) * (SU @ xf[t])] for t in range(T)])
+    assert okq.max_rel(h.cpu().numpy(), href) <= TOL
+    routed = ops.moe_glu_gather_kq(_dev(x), _dev(gw), _dev(uw), codec, _dev(idx), act="silu")
+    assert torch.equal(h[:, :k], routed)           # same kernel, same bits
+    y = ops.gather_qmv_mix_kq(h, _dev(dw), _dev(sd), codec, _dev(idx), _dev(sc), **kw)
+    assert tuple(y.shape) == (T, D) and y.dtype == torch.float32
+    hh = h.cpu().numpy().astype(np.float64)
+    yref = np.stack([sum(sc[t, s] * (Dd[idx[t, s]] @ hh[t, s]) for s in range(k)) + sc[t, k] * (SD @ hh[t, k])
+                     for t in range(T)])
+    assert okq.max_rel(y.cpu().numpy(), yref) <= TOL
