@@ -37,8 +37,8 @@ EXPORTS = (
     "kq_version", "kq_strerror", "kq_codec_block_bytes", "kq_supports", "kq_iq2xxs_grid_host",
     "kq_dequantize", "kq_quantize", "kq_matmul_workspace_bytes", "kq_quantized_matmul_grouped",
     "kq_moe_route", "kq_gather_qmm", "kq_moe_glu_gather", "kq_moe_gather_rows", "kq_moe_mix", "kq_moe_router_topk",
-    "kq_sdpa_workspace_bytes", "kq_sdpa_decode_ragged",
-    "kq_sdpa_cascade_workspace_bytes", "kq_sdpa_decode_gqa_cascade",
+    "kq_sdpa_workspace_bytes", "kq_sdpa_decode_ragged", "kq_sdpa_decode_ragged_q8",
+    "kq_sdpa_cascade_workspace_bytes", "kq_sdpa_decode_gqa_cascade", "kq_sdpa_decode_gqa_cascade_q8",
     "kq_gguf_open", "kq_gguf_close", "kq_gguf_header", "kq_gguf_kv", "kq_gguf_tensor", "kq_gguf_type_size",
 )
 
@@ -98,7 +98,10 @@ _SIGS = {
     "kq_sdpa_workspace_bytes": ([_i32, _i32, _i32, _i32, _i32], _sz),
     "kq_sdpa_decode_ragged": ([_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _f32, _int, _vp,
                                _vp, _sz, _vp], _int),
+    "kq_sdpa_decode_ragged_q8": ([_vp] * 10 + [_i32, _i32, _i32, _i32, _i32, _f32, _int, _vp, _vp, _sz, _vp], _int),
     "kq_sdpa_cascade_workspace_bytes": ([_i32, _i32, _i32, _i32, _i32, _i32, _i32], _sz),
+    "kq_sdpa_decode_gqa_cascade_q8": ([_vp, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _i64, _i64, _i32, _vp, _i32,
+                                       _i32, _i32, _i32, _i32, _f32, _int, _vp, _vp, _sz, _vp], _int),
     "kq_sdpa_decode_gqa_cascade": ([_vp, _vp, _vp, _i64, _i32, _vp, _vp, _i64, _i64, _i32, _vp, _i32, _i32,
                                     _i32, _i32, _i32, _f32, _int, _vp, _vp, _sz, _vp], _int),
     "kq_gguf_open": ([ctypes.c_char_p, ctypes.POINTER(_vp)], _int),

@@ -52,6 +52,12 @@ struct SdpaArgs {
     float *ml;            // [B][Hkv][max_splits][G][2] (m, l)
     int32_t B, Hq, Hkv, G, split, max_splits, max_len;
     int32_t qL;           // query tokens per sequence: row r is token r % qL of sequence r / qL
+    // 8-bit affine KV (q8 != 0): k / v (k2 / v2) hold uint8 values, token
+    // rows of D bytes, offsets and strides in bytes; ks / kb / vs / vb (and
+    // ks2 .. vb2) the 16-bit scales and biases, one per 64 values, at
+    // element index (byte offset) / 64
+    const uint16_t *ks, *kb, *vs, *vb, *ks2, *kb2, *vs2, *vb2;
+    int32_t q8;
     float scale_log2;     // scale * log2(e)
 };
 
@@ -178,6 +184,82 @@ struct KVTile {
             }
         }
     }
+    __device__ __forceinline__ half8_t kfrag(int ch, int c) const { return __builtin_bit_cast(half8_t, k[ch][c]); }
+    __device__ __forceinline__ void vrows(int dg, u32x4 (&out)[8]) const {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) out[i] = v[dg][i];
+    }
+};
+
+// 16-bit float bits (fp16, or bf16 when BF) -> fp32
+template <bool BF>
+__device__ __forceinline__ float f16bits_to_f32(uint32_t h) {
+    if constexpr (BF) return __builtin_bit_cast(float, h << 16);
+    else return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+// 8 unsigned bytes -> s * q + b in fp32 (exact conversion, one fused
+// multiply-add, one rounding to the 16-bit type): the affine dequantization
+// of an 8-bit group-quantized KV cache, group of 64 (mx.dequantize).
+template <bool BF>
+__device__ __forceinline__ u32x4 deq8(u32x2 q, uint32_t sb) {
+    const float s = f16bits_to_f32<BF>(sb & 0xFFFFu), b = f16bits_to_f32<BF>(sb >> 16);
+    float f[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        f[j] = fmaf((float)((q.x >> (8 * j)) & 0xFFu), s, b);
+        f[4 + j] = fmaf((float)((q.y >> (8 * j)) & 0xFFu), s, b);
+    }
+    return u32x4{pack2<BF>(f[0], f[1]), pack2<BF>(f[2], f[3]), pack2<BF>(f[4], f[5]), pack2<BF>(f[6], f[7])};
+}
+
+// One 32-token tile of an 8-bit affine-quantized KV cache (uint8 values,
+// token rows of D bytes; 16-bit scale and bias per 64 values of a token), in
+// the same lane layout as KVTile; values are dequantized at their use.
+template <int D, bool BF>
+struct KVTileQ8 {
+    static constexpr int NC = D / 32;
+    static constexpr int NG = (D + 127) / 128;
+    static constexpr int SG = D / 64;  // scale groups per token
+    u32x2 k[2][NC];
+    uint32_t ksb[2][NC];  // scale | bias << 16 of the chunk's group
+    u32x2 v[NG][8];
+    uint32_t vsb[NG][8];
+
+    __device__ __forceinline__ void load(const uint8_t *kp, const uint8_t *vp, const uint16_t *ks, const uint16_t *kb,
+                                         const uint16_t *vs, const uint16_t *vb, int t0, int t_end) {
+        const int lane = kq_lane();
+        const int r = lane & 15, g = lane >> 4;
+#pragma unroll
+        for (int ch = 0; ch < 2; ++ch) {
+            const int tok = min(t0 + 16 * ch + r, t_end - 1);
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const int d = 32 * c + 8 * g;
+                k[ch][c] = *(const u32x2 *)(kp + (int64_t)tok * D + d);
+                const int64_t si = (int64_t)tok * SG + (d >> 6);
+                ksb[ch][c] = (uint32_t)ks[si] | ((uint32_t)kb[si] << 16);
+            }
+        }
+#pragma unroll
+        for (int dg = 0; dg < NG; ++dg) {
+            const int d0 = min(128 * dg + 8 * r, D - 8);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int tok = min(t0 + (i < 4 ? 4 * g + i : 16 + 4 * g + (i - 4)), t_end - 1);
+                v[dg][i] = *(const u32x2 *)(vp + (int64_t)tok * D + d0);
+                const int64_t si = (int64_t)tok * SG + (d0 >> 6);
+                vsb[dg][i] = (uint32_t)vs[si] | ((uint32_t)vb[si] << 16);
+            }
+        }
+    }
+    __device__ __forceinline__ half8_t kfrag(int ch, int c) const {
+        return __builtin_bit_cast(half8_t, deq8<BF>(k[ch][c], ksb[ch][c]));
+    }
+    __device__ __forceinline__ void vrows(int dg, u32x4 (&out)[8]) const {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) out[i] = deq8<BF>(v[dg][i], vsb[dg][i]);
+    }
 };
 
 template <int D, bool BF>
@@ -189,7 +271,8 @@ struct SplitState {
     float m_run;   // running max (log2 domain), same on the 4 lanes of a head
     float l_part;  // this lane's share of the running sum
 
-    __device__ __forceinline__ void tile(const KVTile<D> &kv, int t0, int t_end, bool head_ok, float scale_log2) {
+    template <class Tile>
+    __device__ __forceinline__ void tile(const Tile &kv, int t0, int t_end, bool head_ok, float scale_log2) {
         const int lane = kq_lane();
         const int g = lane >> 4;
         // ---- S = K . q^T for tokens t0 + [0, 32)
@@ -198,7 +281,7 @@ struct SplitState {
         for (int ch = 0; ch < 2; ++ch) {
             floatx4 acc = {0, 0, 0, 0};
 #pragma unroll
-            for (int c = 0; c < NC; ++c) acc = mfma<BF>(__builtin_bit_cast(half8_t, kv.k[ch][c]), qf[c], acc);
+            for (int c = 0; c < NC; ++c) acc = mfma<BF>(kv.kfrag(ch, c), qf[c], acc);
             sc[ch] = acc;
         }
         // ---- online softmax over this lane's 8 scores (head r)
@@ -232,14 +315,16 @@ struct SplitState {
         // ---- O^T += V^T . P^T
 #pragma unroll
         for (int dg = 0; dg < NG; ++dg) {
+            u32x4 vr[8];
+            kv.vrows(dg, vr);
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
                 u32x4 f;
-                f.x = __builtin_amdgcn_perm(kv.v[dg][1][j >> 1], kv.v[dg][0][j >> 1], sel);
-                f.y = __builtin_amdgcn_perm(kv.v[dg][3][j >> 1], kv.v[dg][2][j >> 1], sel);
-                f.z = __builtin_amdgcn_perm(kv.v[dg][5][j >> 1], kv.v[dg][4][j >> 1], sel);
-                f.w = __builtin_amdgcn_perm(kv.v[dg][7][j >> 1], kv.v[dg][6][j >> 1], sel);
+                f.x = __builtin_amdgcn_perm(vr[1][j >> 1], vr[0][j >> 1], sel);
+                f.y = __builtin_amdgcn_perm(vr[3][j >> 1], vr[2][j >> 1], sel);
+                f.z = __builtin_amdgcn_perm(vr[5][j >> 1], vr[4][j >> 1], sel);
+                f.w = __builtin_amdgcn_perm(vr[7][j >> 1], vr[6][j >> 1], sel);
                 const floatx4 acc = o[dg][j] * alpha;
                 o[dg][j] = mfma<BF>(__builtin_bit_cast(half8_t, f), pf, acc);
             }
@@ -255,8 +340,52 @@ struct SplitState {
 // (ok[j] == false: an idle column, its scores are -inf and it stores
 // nothing).  Each K/V tile is loaded once into registers and multiplied
 // for all NRB * 16 columns.
-template <int D, bool BF, int NBUF, int NRB>
-__device__ __forceinline__ void split_unit(const SdpaArgs &a, const uint16_t *kp, const uint16_t *vp, int t_begin,
+// Where one unit's K / V rows start: element (fp16 / bf16) or byte (q8)
+// offset `base` into k / v, and for q8 the scale / bias arrays of the
+// segment (index base / 64).
+struct KvSrc {
+    const void *k, *v;
+    const uint16_t *ks, *kb, *vs, *vb;
+};
+
+template <bool Q8>
+__device__ __forceinline__ KvSrc kv_src(const void *k, const void *v, const uint16_t *ks, const uint16_t *kb,
+                                        const uint16_t *vs, const uint16_t *vb, int64_t base) {
+    KvSrc r;
+    if constexpr (Q8) {
+        r.k = (const uint8_t *)k + base;
+        r.v = (const uint8_t *)v + base;
+        r.ks = ks + (base >> 6);
+        r.kb = kb + (base >> 6);
+        r.vs = vs + (base >> 6);
+        r.vb = vb + (base >> 6);
+    } else {
+        r.k = (const uint16_t *)k + base;
+        r.v = (const uint16_t *)v + base;
+        r.ks = r.kb = r.vs = r.vb = nullptr;
+    }
+    return r;
+}
+
+template <int D, bool BF, bool Q8>
+struct TileOf {
+    using type = KVTile<D>;
+};
+template <int D, bool BF>
+struct TileOf<D, BF, true> {
+    using type = KVTileQ8<D, BF>;
+};
+
+template <int D, bool BF, bool Q8>
+__device__ __forceinline__ void load_tile(typename TileOf<D, BF, Q8>::type &t, const KvSrc &src, int t0, int t_end) {
+    if constexpr (Q8)
+        t.load((const uint8_t *)src.k, (const uint8_t *)src.v, src.ks, src.kb, src.vs, src.vb, t0, t_end);
+    else
+        t.load((const uint16_t *)src.k, (const uint16_t *)src.v, t0, t_end);
+}
+
+template <int D, bool BF, int NBUF, int NRB, bool Q8>
+__device__ __forceinline__ void split_unit(const SdpaArgs &a, const KvSrc &src, int t_begin,
                                            int t_end, int h, int s, const int (&row)[NRB],
                                            const int (&head)[NRB], const bool (&ok)[NRB]) {
     constexpr int NC = D / 32;
@@ -288,13 +417,13 @@ __device__ __forceinline__ void split_unit(const SdpaArgs &a, const uint16_t *kp
         // Ring of NBUF tiles: tile j + NBUF - 1 is loaded while tile j is
         // multiplied.  Loads are issued unconditionally (tokens past t_end
         // read the last valid token), so the wait counts are static.
-        KVTile<D> ring[NBUF];
+        typename TileOf<D, BF, Q8>::type ring[NBUF];
 #pragma unroll
-        for (int j = 0; j < NBUF - 1; ++j) ring[j].load(kp, vp, t_begin + 32 * j, t_end);
+        for (int j = 0; j < NBUF - 1; ++j) load_tile<D, BF, Q8>(ring[j], src, t_begin + 32 * j, t_end);
         for (int t0 = t_begin; t0 < t_end; t0 += 32 * NBUF) {
 #pragma unroll
             for (int j = 0; j < NBUF; ++j) {
-                ring[(j + NBUF - 1) % NBUF].load(kp, vp, t0 + 32 * (j + NBUF - 1), t_end);
+                load_tile<D, BF, Q8>(ring[(j + NBUF - 1) % NBUF], src, t0 + 32 * (j + NBUF - 1), t_end);
                 __builtin_amdgcn_sched_barrier(0);
                 if (t0 + 32 * j < t_end) {
 #pragma unroll
@@ -355,7 +484,7 @@ __device__ __forceinline__ void split_unit(const SdpaArgs &a, const uint16_t *kp
 
 // Ragged mode: unit = one wave = (row b, kv head h, split s), the G q heads
 // of the group in columns 0..G-1.
-template <int D, bool BF, int NBUF>
+template <int D, bool BF, int NBUF, bool Q8>
 __global__ __launch_bounds__(64) void kq_sdpa_split_kernel(SdpaArgs a) {
     const int r = kq_lane() & 15;
     for (int u = blockIdx.x;; u += gridDim.x) {
@@ -369,7 +498,8 @@ __global__ __launch_bounds__(64) void kq_sdpa_split_kernel(SdpaArgs a) {
         const int64_t kvbase = a.kv_off[b] + (int64_t)h * a.head_stride[b];
         const int rw[1] = {b}, hd[1] = {r < a.G ? r : 0};
         const bool ok[1] = {r < a.G};
-        split_unit<D, BF, NBUF, 1>(a, a.k + kvbase, a.v + kvbase, t_begin, t_end, h, s, rw, hd, ok);
+        split_unit<D, BF, NBUF, 1, Q8>(a, kv_src<Q8>(a.k, a.v, a.ks, a.kb, a.vs, a.vb, kvbase), t_begin, t_end, h, s,
+                                       rw, hd, ok);
     }
 }
 
@@ -384,7 +514,7 @@ __global__ __launch_bounds__(64) void kq_sdpa_split_kernel(SdpaArgs a) {
 //  - Later workgroup units: the private slabs, W consecutive units (row,
 //    h, split) per workgroup, one per wave, as in ragged mode.  Splits
 //    0..n1-1 of a row are the prefix's, n1.. the slab's.
-template <int D, bool BF, int NBUF, int NRB>
+template <int D, bool BF, int NBUF, int NRB, bool Q8>
 __global__ __launch_bounds__(256) void kq_sdpa_cascade_kernel(SdpaArgs a) {
     const int r = kq_lane() & 15;
     const int W = blockDim.x >> 6, w = threadIdx.x >> 6;
@@ -409,7 +539,8 @@ __global__ __launch_bounds__(256) void kq_sdpa_cascade_kernel(SdpaArgs a) {
                     rw[j] = ok[j] ? row : 0;
                     hd[j] = ok[j] ? r - jr * a.G : 0;
                 }
-                split_unit<D, BF, NBUF, NRB>(a, a.k + kvbase, a.v + kvbase, t_begin, t_end, h, s, rw, hd, ok);
+                split_unit<D, BF, NBUF, NRB, Q8>(a, kv_src<Q8>(a.k, a.v, a.ks, a.kb, a.vs, a.vb, kvbase), t_begin,
+                                                 t_end, h, s, rw, hd, ok);
             }
         } else {
             const int64_t u2 = (bu - U1) * W + w;
@@ -424,7 +555,8 @@ __global__ __launch_bounds__(256) void kq_sdpa_cascade_kernel(SdpaArgs a) {
                                    (int64_t)st * D;
             const int rw[1] = {b}, hd[1] = {r < a.G ? r : 0};
             const bool ok[1] = {r < a.G};
-            split_unit<D, BF, NBUF, 1>(a, a.k2 + kvbase, a.v2 + kvbase, t_begin, t_end, h, a.n1 + s, rw, hd, ok);
+            split_unit<D, BF, NBUF, 1, Q8>(a, kv_src<Q8>(a.k2, a.v2, a.ks2, a.kb2, a.vs2, a.vb2, kvbase), t_begin,
+                                           t_end, h, a.n1 + s, rw, hd, ok);
         }
     }
 }
@@ -534,30 +666,35 @@ int cascade_nrb(int D, int nrb) {
     return nrb >= 2 && cap >= 2 ? 2 : 1;
 }
 
-template <int D, bool BF, int NBUF>
+template <int D, bool BF, int NBUF, bool Q8>
 void launch_n(const SdpaArgs &a, int grid, int block, bool merge, hipStream_t s) {
     if (a.cascade) {
         const int R = 16 / a.G;
         switch (cascade_nrb(D, (a.B + R - 1) / R)) {
         case 2:
             if constexpr (D != 256)
-                hipLaunchKernelGGL((kq_sdpa_cascade_kernel<D, BF, NBUF, 2>), dim3(grid), dim3(block), 0, s, a);
+                hipLaunchKernelGGL((kq_sdpa_cascade_kernel<D, BF, NBUF, 2, Q8>), dim3(grid), dim3(block), 0, s, a);
             break;
         default:
-            hipLaunchKernelGGL((kq_sdpa_cascade_kernel<D, BF, NBUF, 1>), dim3(grid), dim3(block), 0, s, a);
+            hipLaunchKernelGGL((kq_sdpa_cascade_kernel<D, BF, NBUF, 1, Q8>), dim3(grid), dim3(block), 0, s, a);
             break;
         }
     } else
-        hipLaunchKernelGGL((kq_sdpa_split_kernel<D, BF, NBUF>), dim3(grid), dim3(64), 0, s, a);
+        hipLaunchKernelGGL((kq_sdpa_split_kernel<D, BF, NBUF, Q8>), dim3(grid), dim3(64), 0, s, a);
     if (merge) hipLaunchKernelGGL((kq_sdpa_merge_kernel<D, BF>), dim3(a.B * a.Hq), dim3(256), 0, s, a);
 }
 
-// Tiles in flight per wave: 2 (D = 256 tiles are 128 VGPRs: 1).  Deeper
-// rings put tiles in AGPRs, whose copies wait for the loads: measured no
-// faster on the C3 ragged batch and the cascade shapes.
+// Tiles in flight per wave: 2 (D = 256 tiles are 128 VGPRs, 96 in 8 bits:
+// 1).  Deeper rings put tiles in AGPRs, whose copies wait for the loads:
+// measured no faster on the C3 ragged batch and the cascade shapes.  8-bit
+// KV needs whole 64-value scale groups per token (D = 64, 128, 256).
 template <int D, bool BF>
 void launch(const SdpaArgs &a, int grid, int block, bool merge, hipStream_t s) {
-    launch_n<D, BF, D == 256 ? 1 : 2>(a, grid, block, merge, s);
+    if (a.q8) {
+        if constexpr (D % 64 == 0) launch_n<D, BF, D == 256 ? 1 : 2, true>(a, grid, block, merge, s);
+    } else {
+        launch_n<D, BF, D == 256 ? 1 : 2, false>(a, grid, block, merge, s);
+    }
 }
 
 }  // namespace
@@ -570,17 +707,48 @@ size_t kq_sdpa_workspace_bytes(int32_t B, int32_t Hq, int32_t Hkv, int32_t D, in
     return w.part_bytes + w.ml_bytes;
 }
 
-int kq_sdpa_decode_ragged(const void *q, const void *k, const void *v, const int64_t *kv_off,
-                          const int64_t *head_stride, const int32_t *row_len, int32_t B, int32_t Hq,
-                          int32_t Hkv, int32_t D, int32_t max_len, float scale, int dtype, void *out,
-                          void *workspace, size_t workspace_bytes, kq_stream_t stream) {
+}  // extern "C"
+
+namespace {
+
+// The four scale / bias arrays of an 8-bit KV cache (all NULL: 16-bit KV).
+struct Q8Scales {
+    const void *ks, *kb, *vs, *vb;
+};
+
+int q8_check(const Q8Scales *q8, int D) {
+    if (!q8) return KQ_OK;
+    if (!q8->ks || !q8->kb || !q8->vs || !q8->vb) return KQ_ERR_NULL_POINTER;
+    if (D % 64) return KQ_ERR_BAD_SHAPE;
+    if (((uintptr_t)q8->ks | (uintptr_t)q8->kb | (uintptr_t)q8->vs | (uintptr_t)q8->vb) & 1) return KQ_ERR_BAD_ALIGN;
+    return KQ_OK;
+}
+
+void set_q8(SdpaArgs &a, const Q8Scales *q8, const Q8Scales *q8b) {
+    a.q8 = q8 != nullptr;
+    a.ks = q8 ? (const uint16_t *)q8->ks : nullptr;
+    a.kb = q8 ? (const uint16_t *)q8->kb : nullptr;
+    a.vs = q8 ? (const uint16_t *)q8->vs : nullptr;
+    a.vb = q8 ? (const uint16_t *)q8->vb : nullptr;
+    a.ks2 = q8b ? (const uint16_t *)q8b->ks : nullptr;
+    a.kb2 = q8b ? (const uint16_t *)q8b->kb : nullptr;
+    a.vs2 = q8b ? (const uint16_t *)q8b->vs : nullptr;
+    a.vb2 = q8b ? (const uint16_t *)q8b->vb : nullptr;
+}
+
+int ragged_impl(const void *q, const void *k, const void *v, const Q8Scales *q8, const int64_t *kv_off,
+                const int64_t *head_stride, const int32_t *row_len, int32_t B, int32_t Hq, int32_t Hkv, int32_t D,
+                int32_t max_len, float scale, int dtype, void *out, void *workspace, size_t workspace_bytes,
+                kq_stream_t stream) {
     if (B == 0) return KQ_OK;
     if (!q || !k || !v || !kv_off || !head_stride || !row_len || !out) return KQ_ERR_NULL_POINTER;
     if (B < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || Hq / Hkv > 16 || max_len < 0) return KQ_ERR_BAD_SHAPE;
     if (D != 64 && D != 96 && D != 128 && D != 256) return KQ_ERR_BAD_SHAPE;
     if ((int64_t)B * Hq > (1 << 30)) return KQ_ERR_BAD_SHAPE;
     if (dtype != KQ_DTYPE_F16 && dtype != KQ_DTYPE_BF16) return KQ_ERR_UNSUPPORTED_DTYPE;
-    if (((uintptr_t)q & 15) || ((uintptr_t)k & 15) || ((uintptr_t)v & 15) || ((uintptr_t)out & 15))
+    if (const int rc = q8_check(q8, D)) return rc;
+    const uintptr_t kv_align = q8 ? 7 : 15;
+    if (((uintptr_t)q & 15) || ((uintptr_t)k & kv_align) || ((uintptr_t)v & kv_align) || ((uintptr_t)out & 15))
         return KQ_ERR_BAD_ALIGN;
     const size_t need = kq_sdpa_workspace_bytes(B, Hq, Hkv, D, max_len);
     if (!workspace || workspace_bytes < need) return KQ_ERR_WORKSPACE_TOO_SMALL;
@@ -598,6 +766,7 @@ int kq_sdpa_decode_ragged(const void *q, const void *k, const void *v, const int
     a.shared_head_stride = a.priv_batch_stride = a.priv_head_stride = 0;
     a.cascade = a.P = a.S = a.n1 = a.split1 = 0;
     a.qL = 1;
+    set_q8(a, q8, nullptr);
     a.part = (float *)workspace;
     a.ml = (float *)((char *)workspace + w.part_bytes);
     a.B = B;
@@ -622,6 +791,28 @@ int kq_sdpa_decode_ragged(const void *q, const void *k, const void *v, const int
     default: bf ? launch<256, true>(a, grid, 64, merge, s) : launch<256, false>(a, grid, 64, merge, s); break;
     }
     return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kq_sdpa_decode_ragged(const void *q, const void *k, const void *v, const int64_t *kv_off,
+                          const int64_t *head_stride, const int32_t *row_len, int32_t B, int32_t Hq,
+                          int32_t Hkv, int32_t D, int32_t max_len, float scale, int dtype, void *out,
+                          void *workspace, size_t workspace_bytes, kq_stream_t stream) {
+    return ragged_impl(q, k, v, nullptr, kv_off, head_stride, row_len, B, Hq, Hkv, D, max_len, scale, dtype, out,
+                       workspace, workspace_bytes, stream);
+}
+
+int kq_sdpa_decode_ragged_q8(const void *q, const void *k, const void *v, const void *k_scales,
+                             const void *k_biases, const void *v_scales, const void *v_biases,
+                             const int64_t *kv_off, const int64_t *head_stride, const int32_t *row_len, int32_t B,
+                             int32_t Hq, int32_t Hkv, int32_t D, int32_t max_len, float scale, int dtype, void *out,
+                             void *workspace, size_t workspace_bytes, kq_stream_t stream) {
+    const Q8Scales q8{k_scales, k_biases, v_scales, v_biases};
+    return ragged_impl(q, k, v, &q8, kv_off, head_stride, row_len, B, Hq, Hkv, D, max_len, scale, dtype, out,
+                       workspace, workspace_bytes, stream);
 }
 
 // Cascade launch plan.  A wave's tiles form one chain of dependent loads
@@ -675,12 +866,15 @@ size_t kq_sdpa_cascade_workspace_bytes(int32_t B, int32_t qL, int32_t Hq, int32_
     return (((size_t)slots * D * 4 + 255) & ~(size_t)255) + (size_t)slots * 2 * 4;
 }
 
-int kq_sdpa_decode_gqa_cascade(const void *q, const void *k_shared, const void *v_shared,
-                               int64_t shared_head_stride, int32_t P, const void *k_priv, const void *v_priv,
-                               int64_t priv_batch_stride, int64_t priv_head_stride, int32_t S,
-                               const int32_t *starts, int32_t B, int32_t qL, int32_t Hq, int32_t Hkv, int32_t D,
-                               float scale, int dtype, void *out, void *workspace, size_t workspace_bytes,
-                               kq_stream_t stream) {
+}  // extern "C"
+
+namespace {
+
+int cascade_impl(const void *q, const void *k_shared, const void *v_shared, const Q8Scales *q8s,
+                 int64_t shared_head_stride, int32_t P, const void *k_priv, const void *v_priv, const Q8Scales *q8p,
+                 int64_t priv_batch_stride, int64_t priv_head_stride, int32_t S, const int32_t *starts, int32_t B,
+                 int32_t qL, int32_t Hq, int32_t Hkv, int32_t D, float scale, int dtype, void *out, void *workspace,
+                 size_t workspace_bytes, kq_stream_t stream) {
     if (B == 0) return KQ_OK;
     if (!q || !k_shared || !v_shared || !k_priv || !v_priv || !out) return KQ_ERR_NULL_POINTER;
     if (B < 0 || qL < 1 || qL > 64 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || Hq / Hkv > 16 || P < 0 || S < 0)
@@ -691,9 +885,16 @@ int kq_sdpa_decode_gqa_cascade(const void *q, const void *k_shared, const void *
         priv_batch_stride < priv_head_stride * Hkv)
         return KQ_ERR_BAD_SHAPE;
     if (dtype != KQ_DTYPE_F16 && dtype != KQ_DTYPE_BF16) return KQ_ERR_UNSUPPORTED_DTYPE;
-    if (((uintptr_t)q & 15) || ((uintptr_t)k_shared & 15) || ((uintptr_t)v_shared & 15) ||
-        ((uintptr_t)k_priv & 15) || ((uintptr_t)v_priv & 15) || ((uintptr_t)out & 15) ||
-        (shared_head_stride & 7) || (priv_head_stride & 7) || (priv_batch_stride & 7))
+    if ((q8s == nullptr) != (q8p == nullptr)) return KQ_ERR_NULL_POINTER;
+    if (const int rc = q8_check(q8s, D)) return rc;
+    if (const int rc = q8_check(q8p, D)) return rc;
+    // 16-bit KV: 16-byte rows of 8 values; 8-bit KV: 8-byte runs, and token
+    // rows / strides on whole 64-value scale groups
+    const uintptr_t kv_align = q8s ? 7 : 15;
+    const int64_t st_align = q8s ? 63 : 7;
+    if (((uintptr_t)q & 15) || ((uintptr_t)k_shared & kv_align) || ((uintptr_t)v_shared & kv_align) ||
+        ((uintptr_t)k_priv & kv_align) || ((uintptr_t)v_priv & kv_align) || ((uintptr_t)out & 15) ||
+        (shared_head_stride & st_align) || (priv_head_stride & st_align) || (priv_batch_stride & st_align))
         return KQ_ERR_BAD_ALIGN;
     const size_t need = kq_sdpa_cascade_workspace_bytes(B, qL, Hq, Hkv, D, P, S);
     if (!workspace || workspace_bytes < need) return KQ_ERR_WORKSPACE_TOO_SMALL;
@@ -712,6 +913,7 @@ int kq_sdpa_decode_gqa_cascade(const void *q, const void *k_shared, const void *
     a.priv_batch_stride = priv_batch_stride;
     a.priv_head_stride = priv_head_stride;
     a.cascade = 1;
+    set_q8(a, q8s, q8p);
     a.P = P;
     a.S = S;
     a.qL = qL;
@@ -751,6 +953,36 @@ int kq_sdpa_decode_gqa_cascade(const void *q, const void *k_shared, const void *
         break;
     }
     return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kq_sdpa_decode_gqa_cascade(const void *q, const void *k_shared, const void *v_shared,
+                               int64_t shared_head_stride, int32_t P, const void *k_priv, const void *v_priv,
+                               int64_t priv_batch_stride, int64_t priv_head_stride, int32_t S,
+                               const int32_t *starts, int32_t B, int32_t qL, int32_t Hq, int32_t Hkv, int32_t D,
+                               float scale, int dtype, void *out, void *workspace, size_t workspace_bytes,
+                               kq_stream_t stream) {
+    return cascade_impl(q, k_shared, v_shared, nullptr, shared_head_stride, P, k_priv, v_priv, nullptr,
+                        priv_batch_stride, priv_head_stride, S, starts, B, qL, Hq, Hkv, D, scale, dtype, out,
+                        workspace, workspace_bytes, stream);
+}
+
+int kq_sdpa_decode_gqa_cascade_q8(const void *q, const void *k_shared, const void *v_shared,
+                                  const void *const *shared_scales, int64_t shared_head_stride, int32_t P,
+                                  const void *k_priv, const void *v_priv, const void *const *priv_scales,
+                                  int64_t priv_batch_stride, int64_t priv_head_stride, int32_t S,
+                                  const int32_t *starts, int32_t B, int32_t qL, int32_t Hq, int32_t Hkv, int32_t D,
+                                  float scale, int dtype, void *out, void *workspace, size_t workspace_bytes,
+                                  kq_stream_t stream) {
+    if (!shared_scales || !priv_scales) return KQ_ERR_NULL_POINTER;
+    const Q8Scales s8{shared_scales[0], shared_scales[1], shared_scales[2], shared_scales[3]};
+    const Q8Scales p8{priv_scales[0], priv_scales[1], priv_scales[2], priv_scales[3]};
+    return cascade_impl(q, k_shared, v_shared, &s8, shared_head_stride, P, k_priv, v_priv, &p8, priv_batch_stride,
+                        priv_head_stride, S, starts, B, qL, Hq, Hkv, D, scale, dtype, out, workspace,
+                        workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -584,10 +584,16 @@ def sdpa_decode_slabs(q, k_cache, v_cache, row_offsets, row_lens, n_kv_heads, sc
     return _sdpa_launch(q.contiguous(), k_cache, v_cache, tabs, n_kv_heads, scale, max_len, out)
 
 
-def sdpa_decode_gqa(q, k, v, scale, starts=None):
+def sdpa_decode_gqa(q, k, v, scale, starts=None, k_scales=None, k_biases=None, v_scales=None, v_biases=None):
     """kq.sdpa_decode_gqa with per-row `starts` (gmlx/gemma4_batched_sdpa.py:
     210-226): q (B, Hq, 1, D), k/v (B, Hkv, L, D); row b attends keys
-    [starts[b], L).  `starts` may be a host sequence or an int tensor."""
+    [starts[b], L).  `starts` may be a host sequence or an int tensor.
+
+    With k_scales / k_biases / v_scales / v_biases (the quantized-KV form,
+    gmlx/quantized_sdpa_fix.py:170-182): k / v are an 8-bit affine cache,
+    group 64 -- uint32 words of four values, lowest byte first (mlx's wire,
+    (B, Hkv, L, D/4)) or uint8 (B, Hkv, L, D) -- and the scales / biases
+    (B, Hkv, L, D/64) are in q's dtype; value = scale * q + bias."""
     B = q.shape[0]
     if starts is None:
         pads = [0] * B
@@ -595,10 +601,83 @@ def sdpa_decode_gqa(q, k, v, scale, starts=None):
         pads = [int(x) for x in starts.tolist()]
     else:
         pads = [int(x) for x in starts]
+    q8 = (k_scales, k_biases, v_scales, v_biases)
+    if any(t is not None for t in q8):
+        if any(t is None for t in q8):
+            raise ValueError("sdpa_decode_gqa: quantized KV needs k_scales, k_biases, v_scales and v_biases")
+        return _sdpa_q8(q, k, v, q8, pads, scale)
     out = ragged_decode_attention(q, k, v, pads, scale)
     if out is None:
         raise ValueError("sdpa_decode_gqa: unsupported shape/dtype for the ragged kernel")
     return out
+
+
+def _q8_values(w, D, name):
+    """An 8-bit KV wire tensor as uint8 (..., D): mlx's int32 / uint32 words
+    (four values each, lowest byte first) or bytes."""
+    if w.dtype in (torch.int32, getattr(torch, "uint32", torch.int32)):
+        if w.stride(-1) != 1:
+            w = w.contiguous()
+        w = w.view(torch.uint8)
+    elif w.dtype != torch.uint8:
+        raise ValueError(f"{name}: 8-bit KV is uint8 or 32-bit words, got {w.dtype}")
+    if w.shape[-1] != D:
+        raise ValueError(f"{name}: rows of {w.shape[-1]} values, queries have D={D}")
+    return w
+
+
+def _q8_pair(w, sc, bi, D, dt, name):
+    """(values, scales, biases) in layouts the kernel addresses together: the
+    values' byte strides 64 x the scales' element strides, rows contiguous."""
+    w = _q8_values(w, D, name)
+    if D % 64 or sc.shape[-1] != D // 64 or tuple(sc.shape) != tuple(bi.shape) or \
+            tuple(sc.shape[:-1]) != tuple(w.shape[:-1]):
+        raise ValueError(f"{name}: scales / biases must be (..., D/64) beside (..., D) values (group 64)")
+    if sc.dtype != dt or bi.dtype != dt:
+        raise ValueError(f"{name}: scales / biases must be in the queries' dtype {dt}")
+
+    def lined_up(a, b):
+        return a.stride(-1) == 1 and b.stride(-1) == 1 and all(
+            a.stride(i) == 64 * b.stride(i) for i in range(a.dim() - 1))
+    if not (lined_up(w, sc) and lined_up(w, bi) and sc.stride() == bi.stride()):
+        w, sc, bi = w.contiguous(), sc.contiguous(), bi.contiguous()
+    if w.data_ptr() % 8:
+        raise ValueError(f"{name}: 8-bit KV must be 8-byte aligned")
+    return w, sc, bi
+
+
+def _sdpa_q8(q, k, v, q8, pads, scale):
+    _fault("sdpa_decode_gqa")
+    _require_gpu(q, k, v, *q8)
+    if q.dim() != 4 or q.shape[2] != 1 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("sdpa_decode_gqa: q (B, Hq, 1, D), k / v (B, Hkv, L, .)")
+    B, Hq, _, D = q.shape
+    dt = q.dtype
+    if dt not in (torch.float16, torch.bfloat16):
+        raise ValueError("queries must be float16 or bfloat16")
+    k8, ks, kb = _q8_pair(k, q8[0], q8[1], D, dt, "k")
+    v8, vs, vb = _q8_pair(v, q8[2], q8[3], D, dt, "v")
+    if k8.shape != v8.shape or k8.stride() != v8.stride() or ks.stride() != vs.stride():
+        k8, v8, ks, kb, vs, vb = (t.contiguous() for t in (k8, v8, ks, kb, vs, vb))
+    Hkv, L = k8.shape[1], k8.shape[2]
+    if len(pads) != B or any(p < 0 or p >= max(L, 1) for p in pads):
+        raise ValueError("one start per row, each inside the cache")
+    if Hq % Hkv or Hq // Hkv > 16 or D not in (64, 128, 256):
+        raise ValueError("unsupported quantized-KV attention shape")
+    kv_off = [b * k8.stride(0) + p * k8.stride(2) for b, p in enumerate(pads)]
+    tabs = _row_tables(q.device, kv_off, [k8.stride(1)] * B, [L - p for p in pads])
+    q3 = q.reshape(B, Hq, D).contiguous()
+    out = torch.empty_like(q3)
+    Lb = lib()
+    need = Lb.kq_sdpa_workspace_bytes(B, Hq, Hkv, D, L)
+    s = _stream(q)
+    ws = _WS.get("sdpa", q.device, s.value, need)
+    rc = Lb.kq_sdpa_decode_ragged_q8(q3.data_ptr(), k8.data_ptr(), v8.data_ptr(), ks.data_ptr(), kb.data_ptr(),
+                                     vs.data_ptr(), vb.data_ptr(), tabs[0].data_ptr(), tabs[1].data_ptr(),
+                                     tabs[2].data_ptr(), B, Hq, Hkv, D, L, float(scale), _dt(dt), out.data_ptr(),
+                                     ws.data_ptr(), ws.numel(), s)
+    check("kq_sdpa_decode_ragged_q8", rc)
+    return out.reshape(B, Hq, 1, D)
 
 
 def ragged_decode_attention(queries, keys, values, pads, scale):
@@ -674,10 +753,14 @@ def _kv_pair(k, v, name):
     return k, v
 
 
+_CASCADE_Q8_KEYS = ("k_shared_scales", "k_shared_biases", "v_shared_scales", "v_shared_biases",
+                    "k_priv_scales", "k_priv_biases", "v_priv_scales", "v_priv_biases")
+
+
 def sdpa_decode_gqa_cascade(queries, k_shared, v_shared, k_priv, v_priv, scale, starts=None,
                             **quant_kv):
-    """kq.sdpa_decode_gqa_cascade (gmlx/cascade_sdpa.py:238-248): decode with a
-    prefix shared by every sequence, held once.
+    """kq.sdpa_decode_gqa_cascade (gmlx/cascade_sdpa.py:216-248): decode with
+    a prefix shared by every sequence, held once.
 
     queries (B, Hq, qL, D); k_shared/v_shared (1, Hkv, P, D), the common
     prefix; k_priv/v_priv (B, Hkv, S, D), each sequence's keys after it.
@@ -687,19 +770,34 @@ def sdpa_decode_gqa_cascade(queries, k_shared, v_shared, k_priv, v_priv, scale, 
     tensor (read on the device, no host sync) or a host sequence; None = 0.
     Strided views (slices of a larger cache, as the reference passes) are
     used in place when the last two dims are contiguous.  Returns
-    (B, Hq, qL, D) in the queries' dtype.  The reference's affine-quantised
-    KV form (the *_scales / *_biases keywords) is not implemented here and
-    raises NotImplementedError, which the reference's claim treats as a
-    decline."""
-    if quant_kv:
-        raise NotImplementedError("sdpa_decode_gqa_cascade: quantised KV is not supported")
+    (B, Hq, qL, D) in the queries' dtype.
+
+    The quantized-KV form takes k_shared_scales, k_shared_biases,
+    v_shared_scales, v_shared_biases, k_priv_scales, k_priv_biases,
+    v_priv_scales, v_priv_biases: K / V are then an 8-bit affine cache,
+    group 64, as sdpa_decode_gqa's quantized form describes."""
+    unknown = set(quant_kv) - set(_CASCADE_Q8_KEYS)
+    if unknown:
+        raise TypeError(f"sdpa_decode_gqa_cascade: unexpected keywords {sorted(unknown)}")
+    q8 = bool(quant_kv)
+    if q8 and any(quant_kv.get(k_) is None for k_ in _CASCADE_Q8_KEYS):
+        raise ValueError("sdpa_decode_gqa_cascade: quantized KV needs all eight scale / bias tensors")
     _fault("sdpa_decode_gqa_cascade")
-    _require_gpu(queries, k_shared, v_shared, k_priv, v_priv)
+    _require_gpu(queries, k_shared, v_shared, k_priv, v_priv, *(quant_kv.values()))
     if queries.dim() != 4 or k_shared.dim() != 4 or k_priv.dim() != 4:
         raise ValueError("queries, k_shared, k_priv must be 4-D")
     B, Hq, qL, D = queries.shape
     dt = queries.dtype
-    if dt not in (torch.float16, torch.bfloat16) or any(t.dtype != dt for t in (k_shared, v_shared, k_priv, v_priv)):
+    if dt not in (torch.float16, torch.bfloat16):
+        raise ValueError("queries must be float16 or bfloat16")
+    if q8:
+        ks, kb, vs, vb = (quant_kv[k_] for k_ in _CASCADE_Q8_KEYS[:4])
+        kps, kpb, vps, vpb = (quant_kv[k_] for k_ in _CASCADE_Q8_KEYS[4:])
+        k_shared, ks, kb = _q8_pair(k_shared, ks, kb, D, dt, "k_shared")
+        v_shared, vs, vb = _q8_pair(v_shared, vs, vb, D, dt, "v_shared")
+        k_priv, kps, kpb = _q8_pair(k_priv, kps, kpb, D, dt, "k_priv")
+        v_priv, vps, vpb = _q8_pair(v_priv, vps, vpb, D, dt, "v_priv")
+    elif any(t.dtype != dt for t in (k_shared, v_shared, k_priv, v_priv)):
         raise ValueError("queries and K/V must share dtype float16 or bfloat16")
     if tuple(v_shared.shape) != tuple(k_shared.shape) or tuple(v_priv.shape) != tuple(k_priv.shape):
         raise ValueError("K and V shapes differ")
@@ -709,12 +807,19 @@ def sdpa_decode_gqa_cascade(queries, k_shared, v_shared, k_priv, v_priv, scale, 
     S = k_priv.shape[2]
     if k_priv.shape[1] != Hkv or k_shared.shape[3] != D or k_priv.shape[3] != D:
         raise ValueError("head count / head dim mismatch")
-    if Hq % Hkv or Hq // Hkv > 16 or D not in (64, 96, 128, 256) or not 1 <= qL <= 64:
+    if Hq % Hkv or Hq // Hkv > 16 or D not in ((64, 128, 256) if q8 else (64, 96, 128, 256)) or not 1 <= qL <= 64:
         raise ValueError("unsupported cascade shape")
     if S < qL:
         raise ValueError("the private slab must hold the query block (S >= qL)")
-    ks, vs = _kv_pair(k_shared, v_shared, "sdpa_decode_gqa_cascade")
-    kp, vp = _kv_pair(k_priv, v_priv, "sdpa_decode_gqa_cascade")
+    if q8:
+        if k_shared.stride() != v_shared.stride() or ks.stride() != vs.stride():
+            k_shared, v_shared, ks, kb, vs, vb = (t.contiguous() for t in (k_shared, v_shared, ks, kb, vs, vb))
+        if k_priv.stride() != v_priv.stride() or kps.stride() != vps.stride():
+            k_priv, v_priv, kps, kpb, vps, vpb = (t.contiguous() for t in (k_priv, v_priv, kps, kpb, vps, vpb))
+        kS, vS, kP, vP = k_shared, v_shared, k_priv, v_priv
+    else:
+        kS, vS = _kv_pair(k_shared, v_shared, "sdpa_decode_gqa_cascade")
+        kP, vP = _kv_pair(k_priv, v_priv, "sdpa_decode_gqa_cascade")
     if starts is None:
         st = None
     elif isinstance(starts, torch.Tensor):
@@ -736,12 +841,20 @@ def sdpa_decode_gqa_cascade(queries, k_shared, v_shared, k_priv, v_priv, scale, 
     s = _stream(q)
     ws = _WS.get("sdpa_cascade", q.device, s.value, need)
     # strides of size-1 dims are never used: give them their packed values
-    shs = ks.stride(1) if Hkv > 1 else P * D
-    phs = kp.stride(1) if Hkv > 1 else S * D
-    pbs = kp.stride(0) if B > 1 else Hkv * phs
-    rc = L.kq_sdpa_decode_gqa_cascade(
-        q.data_ptr(), ks.data_ptr(), vs.data_ptr(), shs, P, kp.data_ptr(), vp.data_ptr(),
-        pbs, phs, S, None if st is None else st.data_ptr(), B, qL, Hq, Hkv, D,
-        float(scale), _dt(dt), out.data_ptr(), ws.data_ptr(), ws.numel(), s)
+    shs = kS.stride(1) if Hkv > 1 else P * D
+    phs = kP.stride(1) if Hkv > 1 else S * D
+    pbs = kP.stride(0) if B > 1 else Hkv * phs
+    common = (B, qL, Hq, Hkv, D, float(scale), _dt(dt), out.data_ptr(), ws.data_ptr(), ws.numel(), s)
+    stp = None if st is None else st.data_ptr()
+    if q8:
+        sh = (ctypes.c_void_p * 4)(ks.data_ptr(), kb.data_ptr(), vs.data_ptr(), vb.data_ptr())
+        pr = (ctypes.c_void_p * 4)(kps.data_ptr(), kpb.data_ptr(), vps.data_ptr(), vpb.data_ptr())
+        rc = L.kq_sdpa_decode_gqa_cascade_q8(q.data_ptr(), kS.data_ptr(), vS.data_ptr(), ctypes.cast(sh, ctypes.c_void_p),
+                                             shs, P, kP.data_ptr(), vP.data_ptr(), ctypes.cast(pr, ctypes.c_void_p),
+                                             pbs, phs, S, stp, *common)
+        check("kq_sdpa_decode_gqa_cascade_q8", rc)
+        return out
+    rc = L.kq_sdpa_decode_gqa_cascade(q.data_ptr(), kS.data_ptr(), vS.data_ptr(), shs, P, kP.data_ptr(),
+                                      vP.data_ptr(), pbs, phs, S, stp, *common)
     check("kq_sdpa_decode_gqa_cascade", rc)
     return out

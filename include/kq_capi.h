@@ -214,6 +214,22 @@ int kq_sdpa_decode_ragged(const void *q, const void *k, const void *v, const int
                           int dtype, void *out, void *workspace, size_t workspace_bytes,
                           kq_stream_t stream);
 
+/* 8-bit affine KV cache, group 64 (the quantized-KV form of
+ * kq.sdpa_decode_gqa(q, kw, vw, scale, starts=, k_scales=, k_biases=,
+ * v_scales=, v_biases=), gmlx/quantized_sdpa_fix.py:170-182, as mlx's
+ * BatchQuantizedKVCache holds it: bits 8, group_size 64): k / v hold uint8
+ * values (an mlx uint32 word packs four, lowest byte first), a token row is
+ * D bytes; value = scale * q + bias with one 16-bit (q's dtype) scale and
+ * bias per 64 values, at element index (byte offset) / 64 of k_scales /
+ * k_biases (v_*).  kv_off and head_stride are in bytes and multiples of 64;
+ * D in {64, 128, 256}; k / v 8-byte aligned.  Same workspace as above. */
+int kq_sdpa_decode_ragged_q8(const void *q, const void *k, const void *v, const void *k_scales,
+                             const void *k_biases, const void *v_scales, const void *v_biases,
+                             const int64_t *kv_off, const int64_t *head_stride,
+                             const int32_t *row_len, int32_t B, int32_t Hq, int32_t Hkv,
+                             int32_t D, int32_t max_len, float scale, int dtype, void *out,
+                             void *workspace, size_t workspace_bytes, kq_stream_t stream);
+
 /* ---- cascade (shared-prefix) decode attention ---------------------------- */
 /* kq.sdpa_decode_gqa_cascade(q, k_shared, v_shared, k_priv, v_priv, scale,
  * starts=) as called at gmlx/cascade_sdpa.py:238-248 (claim gates :171-215):
@@ -238,6 +254,20 @@ int kq_sdpa_decode_gqa_cascade(const void *q, const void *k_shared, const void *
                                int32_t B, int32_t qL, int32_t Hq, int32_t Hkv, int32_t D,
                                float scale, int dtype, void *out, void *workspace,
                                size_t workspace_bytes, kq_stream_t stream);
+
+/* The 8-bit affine KV form of the cascade (gmlx/cascade_sdpa.py:216-236:
+ * bits 8, group 64, wire plus scales / biases for the shared prefix and the
+ * private slab), as kq_sdpa_decode_ragged_q8 describes the format:
+ * shared_scales / priv_scales = {k_scales, k_biases, v_scales, v_biases} of
+ * the prefix and of the slabs; strides in bytes, multiples of 64. */
+int kq_sdpa_decode_gqa_cascade_q8(const void *q, const void *k_shared, const void *v_shared,
+                                  const void *const *shared_scales, int64_t shared_head_stride,
+                                  int32_t P, const void *k_priv, const void *v_priv,
+                                  const void *const *priv_scales, int64_t priv_batch_stride,
+                                  int64_t priv_head_stride, int32_t S, const int32_t *starts,
+                                  int32_t B, int32_t qL, int32_t Hq, int32_t Hkv, int32_t D,
+                                  float scale, int dtype, void *out, void *workspace,
+                                  size_t workspace_bytes, kq_stream_t stream);
 
 #ifdef __cplusplus
 }

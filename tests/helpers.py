@@ -39,3 +39,26 @@ def attention_ref(q, k_rows, v_rows, scale):
         p = np.exp(s)
         out[hq] = (p @ v_rows[h].astype(np.float64)) / p.sum()
     return out
+
+
+def q8_affine(x, dtype_name="float16", group=64):
+    """8-bit affine group quantization of x (..., D) as mlx stores a
+    quantized KV cache (bits 8, group 64): q = round((x - bias) / scale) in
+    0..255 with scale = (max - min) / 255 and bias = min per group, scale and
+    bias rounded to `dtype_name`.  Returns (words int32 (..., D/4) with four
+    values per word lowest byte first, scales, biases as torch tensors of
+    that dtype, and the dequantized values scale * q + bias rounded to the
+    dtype, as float64 numpy)."""
+    import torch
+    tdt = getattr(torch, dtype_name)
+    x = np.asarray(x, np.float32)
+    *lead, D = x.shape
+    g = x.reshape(*lead, D // group, group)
+    lo, hi = g.min(-1), g.max(-1)
+    sc = torch.from_numpy(np.maximum(hi - lo, 1e-6) / 255.0).to(tdt)
+    bi = torch.from_numpy(lo).to(tdt)
+    scf, bif = sc.float().numpy()[..., None], bi.float().numpy()[..., None]
+    q = np.clip(np.rint((g - bif) / scf), 0, 255).astype(np.uint8)
+    deq = torch.from_numpy((scf * q.astype(np.float32) + bif).reshape(*lead, D)).to(tdt).double().numpy()
+    words = torch.from_numpy(q.reshape(*lead, D).copy()).view(torch.int32)
+    return words, sc, bi, deq

@@ -123,3 +123,31 @@ def test_sdpa_decode_gqa_starts():
     got = ops.sdpa_decode_gqa(q.cuda(), k.cuda(), v.cuda(), 0.125, starts=starts)
     ref = ops.ragged_decode_attention(q.cuda(), k.cuda(), v.cuda(), [0, 100], 0.125)
     assert torch.equal(got.cpu(), ref.cpu())
+
+
+@pytest.mark.parametrize("D,Hq,Hkv,dtype_name", [(128, 32, 8, "float16"), (64, 8, 8, "float16"),
+                                                 (256, 16, 2, "float16"), (128, 16, 4, "bfloat16")])
+def test_sdpa_decode_gqa_q8_kv(D, Hq, Hkv, dtype_name):
+    """Quantized-KV form of sdpa_decode_gqa (gmlx/quantized_sdpa_fix.py:170-182):
+    an 8-bit affine cache (bits 8, group 64, mlx's uint32 wire) against fp64
+    attention over the dequantized keys and values, ragged starts included."""
+    import torch
+    from gmlx_amd import ops
+    from helpers import q8_affine
+    rng = np.random.default_rng(D + Hq)
+    B, L = 5, 1300
+    kf = rng.normal(0, 1, size=(B, Hkv, L, D)).astype(np.float32)
+    vf = rng.normal(0, 1, size=(B, Hkv, L, D)).astype(np.float32)
+    kw, ks, kb, kd = q8_affine(kf, dtype_name)
+    vw, vs, vb, vd = q8_affine(vf, dtype_name)
+    tdt = getattr(torch, dtype_name)
+    q = torch.from_numpy(rng.normal(0, 1, size=(B, Hq, 1, D)).astype(np.float32)).to(tdt)
+    starts = [0, 17, 600, 1299, 3]
+    scale = D ** -0.5
+    out = ops.sdpa_decode_gqa(q.cuda(), kw.cuda(), vw.cuda(), scale, starts=starts, k_scales=ks.cuda(),
+                              k_biases=kb.cuda(), v_scales=vs.cuda(), v_biases=vb.cuda())
+    assert out.dtype == tdt and tuple(out.shape) == (B, Hq, 1, D)
+    qd = q.double().numpy()[:, :, 0]
+    ref = np.stack([attention_ref(qd[b], kd[b][:, starts[b]:], vd[b][:, starts[b]:], scale) for b in range(B)])
+    tol = BF16_TOL if dtype_name == "bfloat16" else TOL
+    assert okq.max_rel(out.float().cpu().numpy()[:, :, 0], ref) <= tol

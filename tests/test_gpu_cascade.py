@@ -152,8 +152,10 @@ def test_rejects_bad_shapes():
         ops.sdpa_decode_gqa_cascade(q, ks, ks, kp[:1], kp[:1], 0.1)         # batch mismatch
     with pytest.raises(ValueError):
         ops.sdpa_decode_gqa_cascade(q[..., :80], ks[..., :80], ks[..., :80], kp[..., :80], kp[..., :80], 0.1)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError):   # the quantized form needs all eight scale / bias tensors
         ops.sdpa_decode_gqa_cascade(q, ks, ks, kp, kp, 0.1, k_shared_scales=ks)
+    with pytest.raises(TypeError):
+        ops.sdpa_decode_gqa_cascade(q, ks, ks, kp, kp, 0.1, k_scales=ks)
 
 
 # ------------------------------------------------ through the host route
@@ -206,3 +208,36 @@ def test_left_padded_route_order():
     assert dr.claims() == n0 + 1
     for out in (casc, rag):
         assert okq.max_rel(out.float().cpu().numpy(), ref) <= TOL
+
+
+@pytest.mark.parametrize("qL,pads,dtype_name", [(1, [0, 64, 128, 32], "float16"), (4, [0, 64, 32], "float16"),
+                                                (1, [5, 0, 9], "bfloat16")])
+def test_quantized_kv_cascade(qL, pads, dtype_name):
+    """The 8-bit affine KV form (gmlx/cascade_sdpa.py:216-236): wire, scales
+    and biases sliced from one quantized buffer the way the claim slices
+    them; against the masked fp64 reference over the dequantized buffer."""
+    import torch
+    from gmlx_amd import ops
+    from helpers import q8_affine
+    rng = np.random.default_rng(qL + len(pads))
+    B, Hkv, Hq, D, P, sp = len(pads), 8, 16, 128, 1024, 96
+    kb_, vb_, L = _shared_batch(rng, B, Hkv, P, sp, pads, D, np.float32)
+    kw, ks, kbias, kd = q8_affine(kb_, dtype_name)
+    vw, vs, vbias, vd = q8_affine(vb_, dtype_name)
+    for b in range(1, B):   # the prefix copies must stay identical after quantization
+        assert np.array_equal(kd[b, :, pads[b]:pads[b] + P], kd[0, :, pads[0]:pads[0] + P])
+    tdt = getattr(torch, dtype_name)
+    q = torch.from_numpy(rng.normal(0, 1, size=(B, Hq, qL, D)).astype(np.float32)).to(tdt)
+    c0 = min(pads) + P
+    starts = torch.tensor([p + P - c0 for p in pads], dtype=torch.int32, device="cuda")
+    l0 = pads[0]
+    kw, ks, kbias, vw, vs, vbias = (t.cuda() for t in (kw, ks, kbias, vw, vs, vbias))
+    sl = lambda t: t[0:1, :, l0:l0 + P]  # noqa: E731
+    pr = lambda t: t[:, :, c0:]  # noqa: E731
+    out = ops.sdpa_decode_gqa_cascade(
+        q.cuda(), sl(kw), sl(vw), pr(kw), pr(vw), 0.125, starts=starts,
+        k_shared_scales=sl(ks), k_shared_biases=sl(kbias), v_shared_scales=sl(vs), v_shared_biases=sl(vbias),
+        k_priv_scales=pr(ks), k_priv_biases=pr(kbias), v_priv_scales=pr(vs), v_priv_biases=pr(vbias))
+    ref = _masked_ref(q.double().numpy(), kd, vd, pads, 0.125)
+    tol = BF16_TOL if dtype_name == "bfloat16" else TOL
+    assert okq.max_rel(out.float().cpu().numpy(), ref) <= tol
