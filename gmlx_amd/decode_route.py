@@ -174,21 +174,30 @@ def cascade_claim(queries, keys, values, cache, scale, mask=None, sinks=None):
     info = cache.__dict__.get("_gmlx_cascade") if cache is not None and hasattr(cache, "__dict__") else None
     if info is None:
         return _decline("no-stamp")
-    if getattr(cache, "bits", None) is not None or isinstance(keys, (tuple, list)):
-        return _decline("quantized-kv")
-    if not all(isinstance(t, torch.Tensor) for t in (queries, keys, values)):
+    # 8-bit affine caches (bits 8, group 64) present K / V as (wire, scales,
+    # biases); other quantized configurations decline
+    quant = (isinstance(keys, (tuple, list)) and len(keys) == 3 and isinstance(values, (tuple, list))
+             and len(values) == 3 and getattr(cache, "bits", None) == 8
+             and getattr(cache, "group_size", None) == 64)
+    if not quant and (isinstance(keys, (tuple, list)) or getattr(cache, "bits", None) is not None):
+        return _decline("quant-config", bits=getattr(cache, "bits", None), gs=getattr(cache, "group_size", None))
+    ka = keys[0] if quant else keys
+    va = values[0] if quant else values
+    if not all(isinstance(t, torch.Tensor) for t in (queries, ka, va)):
         return _decline("not-tensors")
-    if queries.dim() != 4 or keys.dim() != 4 or values.dim() != 4:
+    if queries.dim() != 4 or ka.dim() != 4 or va.dim() != 4:
         return _decline("rank")
     B, Hq, qL, D = queries.shape
-    Hkv, kL = keys.shape[1], keys.shape[2]
+    Hkv, kL = ka.shape[1], ka.shape[2]
+    kv_last = D // 4 if quant else D
+    dt_ok = ((ka.dtype in (torch.int32, getattr(torch, "uint32", torch.int32)) and keys[1].dtype == queries.dtype)
+             if quant else (ka.dtype == queries.dtype and va.dtype == queries.dtype))
     if not (sinks is None and B > 1 and 1 <= qL <= 8 and D in CASCADE_HEAD_DIMS
-            and keys.shape[0] == B and tuple(values.shape) == tuple(keys.shape) and keys.shape[3] == D
+            and ka.shape[0] == B and tuple(va.shape) == tuple(ka.shape) and ka.shape[3] == kv_last
             and Hkv >= 1 and Hq % Hkv == 0
-            and queries.dtype in (torch.float16, torch.bfloat16)
-            and keys.dtype == queries.dtype and values.dtype == queries.dtype
+            and queries.dtype in (torch.float16, torch.bfloat16) and dt_ok
             and getattr(cache, "_right_padding", None) is None and mask_claimable(mask, qL)):
-        return _decline("shape/dtype/mask", B=B, qL=qL, D=D, dtype=str(queries.dtype))
+        return _decline("shape/dtype/mask", B=B, qL=qL, D=D, dtype=str(queries.dtype), quant=quant)
     G = Hq // Hkv
     if G > 16 or B * G * qL > 64:
         return _decline("width", G=G, B=B, qL=qL)
@@ -209,8 +218,18 @@ def cascade_claim(queries, keys, values, cache, scale, mask=None, sinks=None):
     try:
         starts, c0 = cascade_starts(cache, pads, P, queries.device)
         l0 = pads[0]
-        out = ops.sdpa_decode_gqa_cascade(queries, keys[0:1, :, l0:l0 + P], values[0:1, :, l0:l0 + P],
-                                          keys[:, :, c0:], values[:, :, c0:], scale, starts=starts)
+        sh = lambda t: t[0:1, :, l0:l0 + P]  # noqa: E731  row 0's prefix copy
+        pr = lambda t: t[:, :, c0:]  # noqa: E731  the private slab
+        if quant:
+            kw, ks, kb = keys
+            vw, vs, vb = values
+            out = ops.sdpa_decode_gqa_cascade(
+                queries, sh(kw), sh(vw), pr(kw), pr(vw), scale, starts=starts,
+                k_shared_scales=sh(ks), k_shared_biases=sh(kb), v_shared_scales=sh(vs), v_shared_biases=sh(vb),
+                k_priv_scales=pr(ks), k_priv_biases=pr(kb), v_priv_scales=pr(vs), v_priv_biases=pr(vb))
+        else:
+            out = ops.sdpa_decode_gqa_cascade(queries, sh(keys), sh(values), pr(keys), pr(values), scale,
+                                              starts=starts)
     except KQLibraryError:
         raise  # a missing library is a broken install, not a declined call
     except Exception as e:  # the route only declines

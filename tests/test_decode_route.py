@@ -220,7 +220,10 @@ def test_claim_declines(monkeypatch, case):
     elif case == "geometry":
         cache = _Cache([0, 4, 180, 2], P=1024)           # max(pads) + P > L - qL + 1
     elif case == "quant":
-        cache.bits = 8
+        cache.bits = 4                                    # only 8-bit group-64 caches are claimed
+        cache.group_size = 64
+        k = (k, torch.zeros(4, 8, 1200, 2, dtype=torch.float16), torch.zeros(4, 8, 1200, 2, dtype=torch.float16))
+        v = k
     elif case == "mask-None-verify":
         q, k, v = _qkv(qL=4)
     elif case == "sinks":

@@ -241,3 +241,25 @@ def test_quantized_kv_cascade(qL, pads, dtype_name):
     ref = _masked_ref(q.double().numpy(), kd, vd, pads, 0.125)
     tol = BF16_TOL if dtype_name == "bfloat16" else TOL
     assert okq.max_rel(out.float().cpu().numpy(), ref) <= tol
+
+
+def test_route_claims_quantized_cache():
+    """An 8-bit group-64 cache's (wire, scales, biases) K / V go through the
+    claim into the quantized cascade (gmlx/cascade_sdpa.py:146-162)."""
+    import torch
+    from gmlx_amd import decode_route as dr
+    from helpers import q8_affine
+    rng = np.random.default_rng(31)
+    pads, P, sp = [0, 64, 128, 32], 1024, 96
+    kb_, vb_, L = _shared_batch(rng, 4, 8, P, sp, pads, 128, np.float32)
+    kw, ks, kbias, kd = q8_affine(kb_)
+    vw, vs, vbias, vd = q8_affine(vb_)
+    q = torch.from_numpy(rng.normal(0, 1, size=(4, 16, 1, 128)).astype(np.float32)).half()
+    cache = _StampedCache(pads, P=1024)
+    cache.bits, cache.group_size = 8, 64
+    n0 = dr.claims()
+    out = dr.cascade_claim(q.cuda(), (kw.cuda(), ks.cuda(), kbias.cuda()), (vw.cuda(), vs.cuda(), vbias.cuda()),
+                           cache, 0.125)
+    assert out is not None and dr.claims() == n0 + 1
+    ref = _masked_ref(q.double().numpy(), kd, vd, pads, 0.125)
+    assert okq.max_rel(out.float().cpu().numpy(), ref) <= TOL
