@@ -198,19 +198,32 @@ __device__ __forceinline__ float f16bits_to_f32(uint32_t h) {
     else return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
-// 8 unsigned bytes -> s * q + b in fp32 (exact conversion, one fused
-// multiply-add, one rounding to the 16-bit type): the affine dequantization
-// of an 8-bit group-quantized KV cache, group of 64 (mx.dequantize).
+// 8 unsigned bytes -> s * q + b with one rounding to the 16-bit type: the
+// affine dequantization of an 8-bit group-quantized KV cache, group of 64
+// (mx.dequantize).  fp16: a byte becomes 1024 + q exactly (byte under an
+// 0x64 high byte), 1024 is subtracted exactly, and a packed fp16 FMA rounds
+// q * s + b once; bf16: exact byte -> fp32, fp32 FMA, rounding to bf16.
 template <bool BF>
 __device__ __forceinline__ u32x4 deq8(u32x2 q, uint32_t sb) {
-    const float s = f16bits_to_f32<BF>(sb & 0xFFFFu), b = f16bits_to_f32<BF>(sb >> 16);
-    float f[8];
+    if constexpr (!BF) {
+        const half2_t s2 = kq_as_h2(__builtin_amdgcn_perm(sb, sb, 0x01000100u));  // (s, s)
+        const half2_t b2 = kq_as_h2(__builtin_amdgcn_perm(sb, sb, 0x03020302u));  // (b, b)
+        const half2_t k1024 = {(_Float16)1024.f, (_Float16)1024.f};
+        auto pair = [&](uint32_t w, uint32_t sel) {
+            const half2_t qv = kq_as_h2(kq_bytes_to_h2_biased(w, sel)) - k1024;
+            return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(qv, s2, b2));
+        };
+        return u32x4{pair(q.x, KQ_SEL_B01), pair(q.x, KQ_SEL_B23), pair(q.y, KQ_SEL_B01), pair(q.y, KQ_SEL_B23)};
+    } else {
+        const float s = f16bits_to_f32<BF>(sb & 0xFFFFu), b = f16bits_to_f32<BF>(sb >> 16);
+        float f[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        f[j] = fmaf((float)((q.x >> (8 * j)) & 0xFFu), s, b);
-        f[4 + j] = fmaf((float)((q.y >> (8 * j)) & 0xFFu), s, b);
+        for (int j = 0; j < 4; ++j) {
+            f[j] = fmaf((float)((q.x >> (8 * j)) & 0xFFu), s, b);
+            f[4 + j] = fmaf((float)((q.y >> (8 * j)) & 0xFFu), s, b);
+        }
+        return u32x4{pack2<BF>(f[0], f[1]), pack2<BF>(f[2], f[3]), pack2<BF>(f[4], f[5]), pack2<BF>(f[6], f[7])};
     }
-    return u32x4{pack2<BF>(f[0], f[1]), pack2<BF>(f[2], f[3]), pack2<BF>(f[4], f[5]), pack2<BF>(f[6], f[7])};
 }
 
 // One 32-token tile of an 8-bit affine-quantized KV cache (uint8 values,
