@@ -236,8 +236,36 @@ def bench_sdpa(torch, ops, iters=20):
             ref = p @ vb / p.sum()
             got = out[b, hq].double().cpu().numpy()
             chk = max(chk, float(np.abs(got - ref).max() / np.abs(ref).max()))
+    # the same batch over an 8-bit affine KV cache (group 64): half the KV bytes
+    q8 = {}
+    kq8, vq8, scs = [], [], []
+    for t in (k, v):
+        g = t.view(-1, 64).float()
+        lo, hi = g.min(1, keepdim=True).values, g.max(1, keepdim=True).values
+        sc_ = ((hi - lo).clamp_min(1e-6) / 255.0).half()
+        bi_ = lo.half()
+        qv = ((g - bi_.float()) / sc_.float()).round_().clamp_(0, 255).to(torch.uint8).view(-1)
+        (kq8 if t is k else vq8).append(qv)
+        scs += [sc_.view(-1), bi_.view(-1)]
+        del g
     del k, v
+    run8 = lambda: ops.sdpa_decode_slabs(q, kq8[0], vq8[0], offs.tolist(), lens.tolist(), Hkv, scale,  # noqa: E731
+                                         k_scales=scs[0], k_biases=scs[1], v_scales=scs[2], v_biases=scs[3])
+    for _ in range(3):
+        run8()
+    e0.record()
+    for _ in range(iters):
+        run8()
+    e1.record()
+    torch.cuda.synchronize()
+    ms8 = e0.elapsed_time(e1) / iters
+    q8_bytes = 2 * total + 2 * (total // 64) * 4  # values + fp16 scale and bias per 64
+    q8 = {"ms": round(ms8, 4), "kv_gbs": round(q8_bytes / ms8 / 1e6, 1),
+          "frac_hbm": round(q8_bytes / ms8 / 1e6 / HBM_PEAK_GBS, 4),
+          "kv_tokens_per_s": round(int(lens.sum()) / ms8 * 1e3, 1), "kv_bytes": q8_bytes}
+    del kq8, vq8, scs
     return {
+        "q8_kv": q8,
         "workload": "C3 ragged GQA decode, 32q/8kv heads, D=128, B=16, lens log-uniform 1k..128k (seed 0), fp16",
         "kv_tokens": int(lens.sum()),
         "ms": round(ms, 4),
@@ -595,7 +623,9 @@ def main():
     sdpa = None
     if not args.no_sdpa:
         sdpa = bench_sdpa(torch, ops)
-        log(f"[bench] sdpa C3: {sdpa['ms']} ms, {sdpa['kv_gbs']} GB/s, {sdpa['kv_tokens_per_s']:.3e} tok/s")
+        log(f"[bench] sdpa C3: {sdpa['ms']} ms, {sdpa['kv_gbs']} GB/s, {sdpa['kv_tokens_per_s']:.3e} tok/s; "
+            f"8-bit KV {sdpa['q8_kv']['ms']} ms, {sdpa['q8_kv']['kv_gbs']} GB/s, "
+            f"{sdpa['q8_kv']['kv_tokens_per_s']:.3e} tok/s")
 
     cascade = None
     if not args.no_cascade:

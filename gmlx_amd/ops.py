@@ -566,10 +566,14 @@ def _sdpa_launch(q, k, v, tabs, Hkv, scale, max_len, out):
     return out
 
 
-def sdpa_decode_slabs(q, k_cache, v_cache, row_offsets, row_lens, n_kv_heads, scale, max_len=None):
+def sdpa_decode_slabs(q, k_cache, v_cache, row_offsets, row_lens, n_kv_heads, scale, max_len=None,
+                      k_scales=None, k_biases=None, v_scales=None, v_biases=None):
     """C-config layout: row b's KV is a contiguous slab [Hkv, len_b, D] at
     element offset row_offsets[b] of the flat caches.  row_offsets /
-    row_lens are host sequences (memoised to device tables)."""
+    row_lens are host sequences (memoised to device tables).  With the four
+    scale / bias tensors the caches are 8-bit affine (uint8 values, one
+    16-bit scale and bias per 64 consecutive values, flat beside them; slab
+    offsets multiples of 64)."""
     _fault("sdpa_decode_ragged")
     _require_gpu(q, k_cache, v_cache)
     B, Hq, D = q.shape
@@ -580,8 +584,26 @@ def sdpa_decode_slabs(q, k_cache, v_cache, row_offsets, row_lens, n_kv_heads, sc
     hstride = [l * D for l in row_lens]
     tabs = _row_tables(q.device, offs, hstride, row_lens)
     max_len = int(max_len if max_len is not None else (max(row_lens) if row_lens else 0))
-    out = torch.empty_like(q.contiguous())
-    return _sdpa_launch(q.contiguous(), k_cache, v_cache, tabs, n_kv_heads, scale, max_len, out)
+    q = q.contiguous()
+    out = torch.empty_like(q)
+    q8 = (k_scales, k_biases, v_scales, v_biases)
+    if all(t is None for t in q8):
+        return _sdpa_launch(q, k_cache, v_cache, tabs, n_kv_heads, scale, max_len, out)
+    if any(t is None for t in q8) or k_cache.dtype != torch.uint8 or v_cache.dtype != torch.uint8:
+        raise ValueError("8-bit slabs: uint8 caches and all four scale / bias tensors")
+    if any(o % 64 for o in offs) or D % 64 or any(t.dtype != q.dtype or not t.is_contiguous() for t in q8):
+        raise ValueError("8-bit slabs: offsets and D multiples of 64, contiguous scales in q's dtype")
+    _require_gpu(*q8)
+    L = lib()
+    need = L.kq_sdpa_workspace_bytes(B, Hq, n_kv_heads, D, max_len)
+    s = _stream(q)
+    ws = _WS.get("sdpa", q.device, s.value, need)
+    rc = L.kq_sdpa_decode_ragged_q8(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), *(t.data_ptr() for t in q8),
+                                    tabs[0].data_ptr(), tabs[1].data_ptr(), tabs[2].data_ptr(), B, Hq, n_kv_heads,
+                                    D, max_len, float(scale), _dt(q.dtype), out.data_ptr(), ws.data_ptr(), ws.numel(),
+                                    s)
+    check("kq_sdpa_decode_ragged_q8", rc)
+    return out
 
 
 def sdpa_decode_gqa(q, k, v, scale, starts=None, k_scales=None, k_biases=None, v_scales=None, v_biases=None):
