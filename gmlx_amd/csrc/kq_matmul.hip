@@ -25,6 +25,10 @@ int kq_mv_launch(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype, h
 int kq_qmv_persistent_launch(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype, hipStream_t s);
 // workgroups one persistent launch of this problem's codec / K would use
 int kq_qmv_persistent_grid(const kq_matmul_problem &q);
+// kq_mm.hip: batches of 17..64 rows (problems validated, all live, Q4_K /
+// Q6_K, sharing x / M / K).
+bool kq_mm_eligible(const kq_matmul_problem *ps, int n, int x_dtype);
+int kq_mm_launch(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype, hipStream_t s);
 int device_cus();
 
 namespace {
@@ -840,6 +844,16 @@ int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problem
             }
             return KQ_OK;
         }
+    }
+    // 17..64 rows sharing their activations: one launch with the activations
+    // streamed through LDS once per group of weight tiles (GMLX_KQ_MM=0: the
+    // dense kernel instead)
+    if (live > 0 && env_int_flag("GMLX_KQ_MM", 1)) {
+        kq_matmul_problem all[KQ_MAX_GROUP];
+        int na = 0;
+        for (int i = 0; i < n_problems; ++i)
+            if (problems[i].M != 0 && problems[i].N != 0) all[na++] = problems[i];
+        if (kq_mm_eligible(all, na, x_dtype)) return kq_mm_launch(all, na, x_dtype, y_dtype, (hipStream_t)stream);
     }
     // small batches: one persistent launch per codec when every codec's
     // problems share their activations (q|k|v, gate|up of one layer)
