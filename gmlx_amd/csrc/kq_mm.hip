@@ -14,12 +14,16 @@
 //   - wave w takes super-blocks w, w + 4, ... of every tile of the group, so
 //     each activation byte is loaded by one wave of the CU once per group and
 //     multiplied against T tiles;
-//   - a wave streams its activations in quarter-block stages (the fragments
-//     of two MFMA steps for every m-tile) through a register ring of 4
-//     stages, requesting each stage three quarters before its multiply, and
-//     its weights through the register lane views of kq_mma.h one super-block
-//     ahead.  All of these are ordinary vector loads, so the compiler's wait
-//     counts follow the ring exactly and no barrier runs in the K loop;
+//   - a wave streams its activations in quarter-block stages (64 columns of
+//     every activation row): each stage is read with row-contiguous loads
+//     (8 rows x 128 bytes per instruction; the MFMA fragment layout would
+//     touch 16 rows per instruction, which measured twice as slow), three
+//     stages ahead through a register ring, then written to a per-wave LDS
+//     double buffer one quarter before its multiply and read back as MFMA
+//     fragments.  The weights go through the register lane views of
+//     kq_mma.h one super-block ahead.  All global reads are ordinary vector
+//     loads, so the compiler's wait counts follow the ring exactly; a wave
+//     reads back only what it wrote itself, so no barrier runs in the K loop;
 //   - after the K loop the four waves' partial tiles are summed through LDS
 //     in wave order (deterministic results) and stored.
 #include <stdlib.h>
@@ -60,7 +64,7 @@ typedef const __attribute__((address_space(4))) MmArgs *KArgs;
 // One group: tiles tile0 .. tile0 + T - 1 of a problem, all M rows.
 template <int CODEC, int MT, int XT, int T>
 __device__ __forceinline__ void mm_group(KArgs A, const uint8_t *w, int64_t w_row_bytes, void *y,
-                                         int64_t y_stride, int N, int tile0, floatx4 *red) {
+                                         int64_t y_stride, int N, int tile0, floatx4 *red, u32x4 *xstage) {
     constexpr int BPB = kq_block_bytes(CODEC);
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lane = kq_lane(), r = lane & 15, g = lane >> 4;
@@ -77,24 +81,53 @@ __device__ __forceinline__ void mm_group(KArgs A, const uint8_t *w, int64_t w_ro
         const uint8_t *wrow[T];
 #pragma unroll
         for (int i = 0; i < T; ++i) wrow[i] = w + (int64_t)min((tile0 + i) * 16 + r, N - 1) * w_row_bytes;
-        // activation rows 16 mt + r (rows past M read zeros without a memory access)
-        const XRowsBuf<MT> xb = x_rows_buf<MT, XT>(A->x, A->x_stride, M, K, 0, r);
+        // coalesced activation loads: instruction (mt, v) reads rows
+        // 16 mt + 8 v + lane / 8, piece lane % 8 (16 B) of the stage's 128 B
+        // per row; rows past M lie outside the buffer and read zeros
+        const __amdgpu_buffer_rsrc_t xrs = kq_buffer(A->x, (uint32_t)(((int64_t)(M - 1) * A->x_stride + K) * 2));
+        const uint32_t x_oob = (uint32_t)(((int64_t)(M - 1) * A->x_stride + K) * 2);
+        uint32_t row_off[MT][2];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int v = 0; v < 2; ++v) {
+                const int m = 16 * mt + 8 * v + (lane >> 3);
+                row_off[mt][v] = m < M ? (uint32_t)((int64_t)m * A->x_stride * 2 + 16 * (lane & 7)) : x_oob;
+            }
         const int n_stages = 4 * my_blocks;
         // stage s: quarter s % 4 (MFMA steps 2q, 2q + 1) of super-block
-        // wave + 4 (s / 4), both steps' fragments of every m-tile.  Stages past
-        // the end re-load the last stage (uniform loads, exact wait counts).
-        half8_t xr[kStages][2][MT];
-        auto load_stage = [&](half8_t (&dst)[2][MT], int s) {
+        // wave + 4 (s / 4).  Stages past the end re-load the last stage
+        // (uniform loads, exact wait counts).
+        u32x4 raw[kStages][MT][2];
+        auto load_stage = [&](u32x4 (&dst)[MT][2], int s) {
             const int sc = min(s, n_stages - 1);
-            const int col = (wave + kMmWaves * (sc >> 2)) * KQ_QK + 64 * (sc & 3) + 8 * g;
+            const uint32_t colb = (uint32_t)(((wave + kMmWaves * (sc >> 2)) * KQ_QK + 64 * (sc & 3)) * 2);
 #pragma unroll
-            for (int u = 0; u < 2; ++u)
+            for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt) dst[u][mt] = xb.template load<XT>(mt, col + 32 * u);
+                for (int v = 0; v < 2; ++v)
+                    dst[mt][v] = __builtin_bit_cast(
+                        u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, row_off[mt][v] + colb, 0, 0));
+        };
+        // LDS stage buffers of this wave: row m at 128 m, piece c at
+        // 16 (c ^ (m & 7)) (conflict-free for the row-wise writes and the
+        // fragment reads)
+        u32x4 *stage_buf = xstage + wave * 2 * (16 * MT * 8);
+        const int wr_row = lane >> 3, wr_piece = lane & 7;
+        auto write_stage = [&](const u32x4 (&src)[MT][2], int buf) {
+            u32x4 *b = stage_buf + buf * (16 * MT * 8);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int v = 0; v < 2; ++v) {
+                    const int m = 16 * mt + 8 * v + wr_row;
+                    b[m * 8 + (wr_piece ^ (m & 7))] = src[mt][v];
+                }
         };
         // super-block bi: the next one's weights requested first (past the
-        // end: this one again), then its four quarters, each requesting the
-        // stage kStages - 1 ahead into the slot the previous quarter freed
+        // end: this one again); quarter q requests stage s + 3 (register
+        // ring), writes stage s + 1 (loaded two quarters ago) to the free LDS
+        // buffer and multiplies stage s (written one quarter ago)
         auto do_block = [&](Block<CODEC> (&cur)[T], Block<CODEC> (&nxt)[T], int bi, auto slot0) {
             constexpr int j0 = decltype(slot0)::value;
             const int kb_next = wave + kMmWaves * min(bi + 1, my_blocks - 1);
@@ -109,18 +142,25 @@ __device__ __forceinline__ void mm_group(KArgs A, const uint8_t *w, int64_t w_ro
                 // the requests stay ahead of this quarter's multiplies (the
                 // scheduler would otherwise sink them next to their use)
                 __builtin_amdgcn_sched_barrier(0);
-                load_stage(xr[(jq + kStages - 1) % kStages], 4 * bi + q + kStages - 1);
+                load_stage(raw[(jq + kStages - 1) % kStages], 4 * bi + q + kStages - 1);
                 __builtin_amdgcn_sched_barrier(0);
-                const int slot = jq % kStages;
+                write_stage(raw[(jq + 1) % kStages], (q + 1) & 1);
+                const u32x4 *b = stage_buf + (q & 1) * (16 * MT * 8);
 #pragma unroll
                 for (int u = 0; u < 2; ++u) {
                     const int t = 2 * q + u;
+                    half8_t xf[MT];
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+                        const int m = 16 * mt + r;
+                        xf[mt] = x8_from_bits<XT>(b[m * 8 + ((4 * u + g) ^ (m & 7))]);
+                    }
 #pragma unroll
                     for (int i = 0; i < T; ++i) {
-                        const half8_t b = cur[i].frag(t, g, kIq2);
+                        const half8_t bw = cur[i].frag(t, g, kIq2);
 #pragma unroll
                         for (int mt = 0; mt < MT; ++mt)
-                            acc[i][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xr[slot][u][mt], b, acc[i][mt], 0, 0, 0);
+                            acc[i][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[mt], bw, acc[i][mt], 0, 0, 0);
                     }
                 }
             }
@@ -129,7 +169,8 @@ __device__ __forceinline__ void mm_group(KArgs A, const uint8_t *w, int64_t w_ro
 #pragma unroll
         for (int i = 0; i < T; ++i) b0[i].load(wrow[i] + (int64_t)wave * BPB, g);
 #pragma unroll
-        for (int s = 0; s < kStages - 1; ++s) load_stage(xr[s], s);
+        for (int s = 0; s < kStages - 1; ++s) load_stage(raw[s], s);
+        write_stage(raw[0], 0);
         for (int bi = 0;;) {
             do_block(b0, b1, bi, std::integral_constant<int, 0>{});
             if (++bi >= my_blocks) {
@@ -173,6 +214,7 @@ __device__ __forceinline__ void mm_group(KArgs A, const uint8_t *w, int64_t w_ro
 template <int SET, int MT, int XT, int T>
 __global__ __launch_bounds__(64 * kMmWaves) __attribute__((amdgpu_waves_per_eu(1, 1))) void kq_mm_kernel(MmArgs a_) {
     __shared__ floatx4 red[kMmWaves * T * MT * 64];
+    __shared__ u32x4 xstage[kMmWaves * 2 * 16 * MT * 8];  // two activation stages per wave
     const KArgs A = (KArgs)__builtin_amdgcn_kernarg_segment_ptr();
     const int total = A->total_groups, np = A->n_problems;
     for (int grp = (int)blockIdx.x; grp < total; grp += (int)gridDim.x) {  // uniform
@@ -185,12 +227,12 @@ __global__ __launch_bounds__(64 * kMmWaves) __attribute__((amdgpu_waves_per_eu(1
         const int N = A->p[pi].N;
         const int tile0 = (grp - A->group_begin[pi]) * T;
         if constexpr (SET == kSetQ4K) {
-            mm_group<KQ_CODEC_Q4_K, MT, XT, T>(A, w, wrb, y, ys, N, tile0, red);
+            mm_group<KQ_CODEC_Q4_K, MT, XT, T>(A, w, wrb, y, ys, N, tile0, red, xstage);
         } else if constexpr (SET == kSetQ6K) {
-            mm_group<KQ_CODEC_Q6_K, MT, XT, T>(A, w, wrb, y, ys, N, tile0, red);
+            mm_group<KQ_CODEC_Q6_K, MT, XT, T>(A, w, wrb, y, ys, N, tile0, red, xstage);
         } else {
-            if (A->p[pi].codec == KQ_CODEC_Q6_K) mm_group<KQ_CODEC_Q6_K, MT, XT, T>(A, w, wrb, y, ys, N, tile0, red);
-            else mm_group<KQ_CODEC_Q4_K, MT, XT, T>(A, w, wrb, y, ys, N, tile0, red);
+            if (A->p[pi].codec == KQ_CODEC_Q6_K) mm_group<KQ_CODEC_Q6_K, MT, XT, T>(A, w, wrb, y, ys, N, tile0, red, xstage);
+            else mm_group<KQ_CODEC_Q4_K, MT, XT, T>(A, w, wrb, y, ys, N, tile0, red, xstage);
         }
     }
 }
@@ -237,7 +279,7 @@ int mm_env_int(const char *name, int dflt) {
 
 // Eligibility: problems validated and live, Q4_K / Q6_K only, fp16 or bf16
 // activations shared by every problem (same x, stride, M, K), 17 <= M <= 64,
-// x and its row stride 16-byte aligned.
+// x and its row stride 16-byte aligned, x addressable with 31-bit offsets.
 bool kq_mm_eligible(const kq_matmul_problem *ps, int n, int x_dtype) {
     if (n <= 0) return false;
     if (x_dtype != KQ_DTYPE_F16 && x_dtype != KQ_DTYPE_BF16) return false;
@@ -245,6 +287,8 @@ bool kq_mm_eligible(const kq_matmul_problem *ps, int n, int x_dtype) {
     if (q0.M < 17 || q0.M > 64) return false;
     // 16-byte activation pieces: x and its row stride 16-byte aligned
     if (((uintptr_t)q0.x & 15) != 0 || q0.x_row_stride % 8 != 0) return false;
+    // activation reads are 32-bit buffer offsets (rows past M sit just past the end)
+    if (((int64_t)(q0.M - 1) * q0.x_row_stride + 2 * (int64_t)q0.K) * 2 >= ((int64_t)1 << 31)) return false;
     for (int i = 0; i < n; ++i) {
         const kq_matmul_problem &q = ps[i];
         if (q.codec != KQ_CODEC_Q4_K && q.codec != KQ_CODEC_Q6_K) return false;
