@@ -106,8 +106,8 @@ __device__ __forceinline__ void mm_group(KArgs A, const uint8_t *w, int64_t w_ro
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
                 for (int v = 0; v < 2; ++v)
-                    dst[mt][v] = __builtin_bit_cast(
-                        u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, row_off[mt][v] + colb, 0, 0));
+                    dst[mt][v] = __builtin_bit_cast(  // lane row offset + wave-uniform column (scalar offset)
+                        u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, row_off[mt][v], (int)colb, 0));
         };
         // LDS stage buffers of this wave: row m at 128 m, piece c at
         // 16 (c ^ (m & 7)) (conflict-free for the row-wise writes and the
