@@ -102,7 +102,8 @@ def make_inputs(torch, rng, B):
 # down: K = 12288 Q6_K, three blocks per wave, the last 4096 columns of x in
 # registers at B > 4, LDS-staged only up to B = 8); at B = 17..64 every
 # launch takes the mid-batch kernel (one 4-wave workgroup per CU over groups
-# of T weight tiles: q|k|v mixed T = 2, o and down T = 1, gate|up T = 3);
+# of T weight tiles: q|k|v mixed T = 2, o and down T = 1, gate|up T = 6 up to
+# 32 rows, 3 above);
 # past 64 rows the general kernel.
 LAUNCHES = [("qkv", ("q", "k", "v")), ("o", ("o",)), ("gate_up", ("gate", "up")), ("down", ("down",))]
 CODEC = {name: codec for name, _, _, codec in LAYER}
@@ -119,7 +120,7 @@ def kernel_of(launch, B):
         return dense
     if B > 16:  # kq_mm_kernel<codec set (0 Q4_K, 1 Q6_K, 2 both), m-tiles, fp16, tiles per group>
         return {"qkv": f"kq_mm_kernel<2, {mt}, 0, 2>", "o": f"kq_mm_kernel<0, {mt}, 0, 1>",
-                "gate_up": f"kq_mm_kernel<0, {mt}, 0, 3>", "down": f"kq_mm_kernel<1, {mt}, 0, 1>"}[launch]
+                "gate_up": f"kq_mm_kernel<0, {mt}, 0, {6 if mt == 2 else 3}>", "down": f"kq_mm_kernel<1, {mt}, 0, 1>"}[launch]
     if launch == "qkv":  # Q4_K q|k with Q6_K v: the mixed form (codec id 127), 0.75 tiles per 8-wave workgroup
         return "kq_mv_kernel<127, 0, 2, 1, false, 8>"
     if launch == "o":

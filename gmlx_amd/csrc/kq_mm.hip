@@ -243,8 +243,9 @@ int mm_launch_one(const MmArgs &a, int grid, hipStream_t s) {
     return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
 }
 
-// Instantiated: Q4_K alone with T = 1..4 (1..3 at four m-tiles); Q6_K alone
-// or mixed with T = 1..2 (a Q6_K super-block holds more registers per tile).
+// Instantiated: Q4_K alone with T = 1..4 and 6 at two m-tiles, 1..3 at four
+// (six spill there); Q6_K alone or mixed with T = 1..2 (a Q6_K super-block
+// holds more registers per tile).
 template <int SET, int MT, int XT>
 int mm_launch_t(const MmArgs &a, int t, int grid, hipStream_t s) {
     if constexpr (SET == kSetQ4K) {
@@ -252,9 +253,12 @@ int mm_launch_t(const MmArgs &a, int t, int grid, hipStream_t s) {
         case 1: return mm_launch_one<SET, MT, XT, 1>(a, grid, s);
         case 2: return mm_launch_one<SET, MT, XT, 2>(a, grid, s);
         case 3: return mm_launch_one<SET, MT, XT, 3>(a, grid, s);
-        default:
-            if constexpr (MT == 2) return mm_launch_one<SET, MT, XT, 4>(a, grid, s);
-            return mm_launch_one<SET, MT, XT, 3>(a, grid, s);
+        default:  // t is 4 or 6 here, and only at two m-tiles (the host caps four m-tiles at 3)
+            if constexpr (MT == 2) {
+                return t == 4 ? mm_launch_one<SET, MT, XT, 4>(a, grid, s) : mm_launch_one<SET, MT, XT, 6>(a, grid, s);
+            } else {
+                return KQ_ERR_BAD_SHAPE;
+            }
         }
     } else {
         return t == 1 ? mm_launch_one<SET, MT, XT, 1>(a, grid, s) : mm_launch_one<SET, MT, XT, 2>(a, grid, s);
@@ -299,8 +303,9 @@ bool kq_mm_eligible(const kq_matmul_problem *ps, int n, int x_dtype) {
 
 // Problems eligible (kq_mm_eligible).  T (tiles per group) from the tiles per
 // CU: as many tiles per group as one round of groups over the CUs needs, up
-// to the register limit; more tiles take several rounds of equal groups
-// (GMLX_KQ_MM_T forces T).
+// to the register limit (Q4_K 6 at M <= 32, 3 above; any Q6_K 2); more tiles
+// take several rounds of equal groups (GMLX_KQ_MM_T forces T; a T between the
+// instantiated sizes takes the next larger one).
 int kq_mm_launch(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype, hipStream_t s) {
     bool any4 = false, any6 = false;
     int tiles = 0;
@@ -311,7 +316,7 @@ int kq_mm_launch(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype, h
     }
     const int set = any4 && any6 ? kSetMix : (any6 ? kSetQ6K : kSetQ4K);
     const int mt = ps[0].M <= 32 ? 2 : 4;
-    const int tmax = set == kSetQ4K ? (mt == 2 ? 4 : 3) : 2;
+    const int tmax = set == kSetQ4K ? (mt == 2 ? 6 : 3) : 2;
     const int cus = device_cus();
     int t = (tiles + cus - 1) / cus;
     if (t > tmax) {
@@ -321,6 +326,7 @@ int kq_mm_launch(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype, h
     t = mm_env_int("GMLX_KQ_MM_T", t);
     if (t < 1) t = 1;
     if (t > tmax) t = tmax;
+    if (t == 5) t = 6;  // instantiated sizes: the groups below use the kernel's own T
 
     MmArgs a;
     int groups = 0;

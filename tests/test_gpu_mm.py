@@ -37,7 +37,7 @@ def test_mid_batch_parity(codec, M, K, monkeypatch):
     x16 = fp16_rows(rng, M, K)
     ref = okq.qmm_ref(x16, wire, codec)
     x, w = _dev(x16), _dev(wire)
-    for t in ("1", "2", "3", "4"):
+    for t in ("1", "2", "3", "4", "6"):
         monkeypatch.setenv("GMLX_KQ_MM_T", t)
         got = ops.quantized_matmul(x, w, None, codec).float().cpu().numpy()
         assert okq.max_rel(got, ref) <= TOL, (t, okq.max_rel(got, ref))
