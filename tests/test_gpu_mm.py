@@ -124,3 +124,31 @@ def test_mid_batch_strided_rows_and_determinism(monkeypatch):
     ga, gb = ops.quantized_matmul_grouped([(x, _dev(wa), "q4_k"), (x, _dev(wb), "q4_k")])
     sb = ops.quantized_matmul(x, _dev(wb), None, "q4_k")
     assert torch.equal(ga, a1) and torch.equal(gb, sb)
+
+
+@pytest.mark.parametrize("M", [8, 17, 64, 80])
+def test_strided_rows_through_the_c_abi(M, monkeypatch):
+    """kq_quantized_matmul_grouped with x rows at a stride of K + 64 and y rows
+    at a stride of N + 40 (outputs written into a wider buffer), on every route
+    (M = 8: LDS-staged small batch; 17, 64: mid-batch; 80: general kernel):
+    the reference in the first N columns, the padding columns untouched."""
+    import torch
+    from gmlx_amd import ops
+    _clear(monkeypatch)
+    rng = np.random.default_rng(40 + M)
+    K, N = 2048, 136
+    wa = quantized_weights(rng, "q4_k", N, K)
+    wb = quantized_weights(rng, "q6_k", N, K)
+    x16 = fp16_rows(rng, M, K)
+    xb = torch.zeros(M, K + 64, dtype=torch.float16)
+    xb[:, :K] = torch.from_numpy(x16)
+    xv = xb.cuda()[:, :K]
+    ys = [torch.full((M, N + 40), 7.0, dtype=torch.float32, device="cuda") for _ in range(2)]
+    wd = [_dev(wa), _dev(wb)]  # the problems hold raw pointers: keep the tensors alive
+    probs = [ops._problem(xv, w, c, y[:, :N]) for w, c, y in zip(wd, ("q4_k", "q6_k"), ys)]
+    ops._launch_grouped(probs, ops._dt(torch.float16), ops._dt(torch.float32), xv.device, ops._stream(xv))
+    torch.cuda.synchronize()
+    for w, c, y in zip((wa, wb), ("q4_k", "q6_k"), ys):
+        ref = okq.qmm_ref(x16, w, c)
+        assert okq.max_rel(y[:, :N].cpu().numpy(), ref) <= TOL, c
+        assert bool((y[:, N:] == 7.0).all()), c
