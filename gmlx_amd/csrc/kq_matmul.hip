@@ -679,13 +679,24 @@ void launch_dense_nw(int nw, const DenseArgs &a, int units, int chunks, hipStrea
     }
 }
 
-// Super-blocks per row up to which a wave takes a whole unit
-// (GMLX_KQ_GATHER_WAVE_NB; 0 always splits K over the workgroup's waves).
-int gather_wave_nb() { return env_int("GMLX_KQ_GATHER_WAVE_NB", 8); }
+// One wave per unit (the whole K of a 16-column tile) for rows of at most 8
+// super-blocks, and for longer rows when the launch's units (its grid: the
+// experts it can touch times the tiles) give every CU 16 waves: the waves
+// then stream their rows without the split's reduction (measured on C5,
+// IQ2_XXS K = 7168, 51 touched experts, alternating in one process: 0.272
+// against 0.285 ms); smaller batches split K over the workgroup's waves for
+// parallelism.
+// GMLX_KQ_GATHER_WAVE_NB = n forces the rule "at most n super-blocks" (0: always split).
+bool gather_use_wave(const GatherArgs &a, int grid) {
+    const int forced = env_int("GMLX_KQ_GATHER_WAVE_NB", -1);
+    const int nb = a.K / KQ_QK;
+    if (forced >= 0) return nb <= forced;
+    return nb <= 8 || grid >= 16 * device_cus();
+}
 
 template <int CODEC, int XT, int NW>
 void launch_gather_codec(int mt, const GatherArgs &a, int grid, hipStream_t s) {
-    if (a.K / KQ_QK <= gather_wave_nb()) {
+    if (gather_use_wave(a, grid)) {
         const int g = (grid + kGatherWaves - 1) / kGatherWaves;
         switch (mt) {
         case 1: hipLaunchKernelGGL((kq_gather_wave_kernel<CODEC, 1, XT, NW>), dim3(g), dim3(64 * kGatherWaves), 0, s, a); break;

@@ -198,3 +198,27 @@ def test_shared_expert_glu_and_mix(codec, scodec, T, k, E):
     yref = np.stack([sum(sc[t, s] * (Dd[idx[t, s]] @ hh[t, s]) for s in range(k)) + sc[t, k] * (SD @ hh[t, k])
                      for t in range(T)])
     assert okq.max_rel(y.cpu().numpy(), yref) <= TOL
+
+
+@pytest.mark.parametrize("codec", ["q4_k", "iq2_xxs"])
+@pytest.mark.parametrize("wave_nb", ["32", "0"])
+def test_glu_gather_long_rows_both_forms(codec, wave_nb, monkeypatch):
+    """GLU gather at K = 7168 (28 super-blocks per row, the C5 gate|up
+    geometry) through one wave per tile (the form large decode batches take)
+    and through K split over the workgroup's waves, against fp64."""
+    from gmlx_amd import ops
+    monkeypatch.setenv("GMLX_KQ_GATHER_WAVE_NB", wave_nb)
+    rng = np.random.default_rng(29)
+    E, D, I, T, k = 6, 7168, 48, 3, 2
+    gw = _experts(rng, codec, E, I, D)
+    uw = _experts(rng, codec, E, I, D)
+    x = fp16_rows(rng, T, D)
+    idx = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    h = ops.moe_glu_gather_kq(_dev(x), _dev(gw), _dev(uw), codec, _dev(idx), act="silu")
+    g_deq = okq.dequantize(gw, codec).astype(np.float64)
+    u_deq = okq.dequantize(uw, codec).astype(np.float64)
+    xf = x.astype(np.float64)
+    silu = lambda z: z / (1 + np.exp(-z))  # noqa: E731
+    href = np.stack([[silu(g_deq[idx[t, s]] @ xf[t]) * (u_deq[idx[t, s]] @ xf[t]) for s in range(k)]
+                     for t in range(T)])
+    assert okq.max_rel(h.cpu().numpy(), href) <= TOL
