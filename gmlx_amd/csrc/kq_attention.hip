@@ -32,6 +32,8 @@
 // No cross-workgroup synchronisation happens inside a launch.
 #include "kq_common.h"
 
+int device_cus();
+
 namespace {
 
 struct SdpaArgs {
@@ -651,9 +653,17 @@ int env_int(const char *name, int dflt) {
     return (end && *end == 0 && v > 0 && v < (1 << 24)) ? (int)v : dflt;
 }
 
-// Tokens per split (a multiple of the 32-token tile).
-int split_tokens() {
-    int c = env_int("GMLX_KQ_SDPA_SPLIT", 512);
+// Tokens per split (a multiple of the 32-token tile): 1024 when the launch's
+// unit bound B * Hkv * ceil(max_len / 1024) gives every CU 8 waves, 512
+// otherwise (longer splits halve the partials and the merge's work; measured
+// on C3: 353 against 372 us); GMLX_KQ_SDPA_SPLIT forces it.  The workspace
+// size follows the same rule from the same arguments.
+int split_tokens(int B, int Hkv, int max_len) {
+    int c = env_int("GMLX_KQ_SDPA_SPLIT", 0);
+    if (c == 0) {
+        const int64_t units = (int64_t)B * Hkv * (((int64_t)(max_len > 0 ? max_len : 1) + 1023) / 1024);
+        c = units >= 8 * (int64_t)device_cus() ? 1024 : 512;
+    }
     c = (c + 31) / 32 * 32;
     return c < 32 ? 32 : c;
 }
@@ -664,7 +674,7 @@ struct WsLayout {
 
 WsLayout ws_layout(int B, int Hq, int Hkv, int D, int max_len) {
     const int G = Hq / Hkv;
-    const int C = split_tokens();
+    const int C = split_tokens(B, Hkv, max_len);
     const int64_t ms = max_len <= 0 ? 1 : (max_len + C - 1) / C;
     WsLayout w;
     w.part_bytes = (((size_t)B * Hkv * ms * G * D * 4) + 255) & ~(size_t)255;
@@ -786,7 +796,7 @@ int ragged_impl(const void *q, const void *k, const void *v, const Q8Scales *q8,
     a.Hq = Hq;
     a.Hkv = Hkv;
     a.G = Hq / Hkv;
-    a.split = split_tokens();
+    a.split = split_tokens(B, Hkv, max_len);
     a.max_splits = max_len <= 0 ? 1 : (max_len + a.split - 1) / a.split;
     a.max_len = max_len;
     a.scale_log2 = scale * 1.4426950408889634f;

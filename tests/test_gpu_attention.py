@@ -63,7 +63,7 @@ def test_split_size_invariance(monkeypatch):
     offs, ks, vs, kf, vf = _slabs(rng, lens, 4, 128)
     q = rng.normal(0, 1, size=(2, 16, 128)).astype(np.float16)
     ref = np.stack([attention_ref(q[b], ks[b], vs[b], 128 ** -0.5) for b in range(2)])
-    for split in ("32", "96", "512", "4096"):
+    for split in ("32", "96", "512", "1024", "4096"):
         monkeypatch.setenv("GMLX_KQ_SDPA_SPLIT", split)
         out = ops.sdpa_decode_slabs(torch.from_numpy(q).cuda(), torch.from_numpy(kf).cuda(),
                                     torch.from_numpy(vf).cuda(), offs, lens, 4, 128 ** -0.5)
