@@ -367,55 +367,79 @@ def bench_moe(torch, ops, which, iters=20):
     """BASELINE configs 4 and 5: one MoE decode layer (router top-k, fused
     gate|up GLU gather, down gather with the routing mix folded in) over
     the tokens' ragged per-expert segments.  Router logits and x are numpy
-    default_rng(0) draws; C4 weights are N(0, 0.02) drawn on the GPU (torch
-    generator, seed 0) and quantised by kq_quantize; C5 weights are random
-    valid IQ2_XXS blocks (d = 1e-3) -- the kernels' work does not depend on
-    the values.  C4 rotates two copies of the expert stacks (783 MB, > 2x the
-    256 MB MALL); C5's touched experts alone exceed it."""
+    default_rng(0) draws; weights are N(0, 0.02) drawn on the GPU (torch
+    generator, seed 0) and quantised by kq_quantize -- every expert for C4,
+    the experts the router touches for C5 (the others hold zero blocks and
+    are never read).  C4 rotates two copies of the expert stacks (783 MB,
+    > 2x the 256 MB MALL); C5's touched experts alone exceed it.  After
+    timing, four tokens' outputs are checked against the fp64 oracle over
+    the same wire bytes."""
     import numpy as np
     E, H, I, topk, T, cgu, cd = MOE_CONFIGS[which]
     rng = np.random.default_rng(0)
     logits = torch.from_numpy(rng.normal(0.0, 1.0, size=(T, E)).astype(np.float32)).cuda()
     x = torch.from_numpy(rng.normal(0.0, 1.0, size=(T, H)).astype(np.float16)).cuda()
     gen = torch.Generator(device="cuda").manual_seed(0)
+    idx0, _ = ops.moe_router_topk(logits, topk, shared_gate=False)
+    touched = sorted(set(idx0.cpu().numpy().reshape(-1).tolist()))
 
     def stack(N, K, codec):
         nb, bpb = K // 256, BLOCK_BYTES[codec]
-        if codec == "iq2_xxs":
-            w = torch.randint(0, 256, (E, N, nb, bpb), generator=gen, device="cuda", dtype=torch.uint8)
-            w[..., 0:2] = torch.full((E, N, nb), 1e-3, device="cuda").half().view(torch.uint8).view(E, N, nb, 2)
-            return w.view(E, N, nb * bpb)
-        out = torch.empty((E, N, nb * bpb), dtype=torch.uint8, device="cuda")
-        for e0 in range(0, E, 32):  # quantise 32 experts at a time
-            w = torch.randn((min(32, E - e0) * N, K), generator=gen, device="cuda") * 0.02
-            out[e0:e0 + 32].view(-1, nb * bpb).copy_(ops.quantize(w, codec)[0])
-            del w
+        out = torch.zeros((E, N, nb * bpb), dtype=torch.uint8, device="cuda")
+        experts = range(E) if codec != "iq2_xxs" else touched
+        per = max(1, (64 << 20) // (N * K * 4))  # quantise ~64 MB of fp32 at a time
+        ex = list(experts)
+        for i in range(0, len(ex), per):
+            chunk = ex[i:i + per]
+            w = torch.randn((len(chunk) * N, K), generator=gen, device="cuda") * 0.02
+            q = ops.quantize(w, codec)[0].view(len(chunk), N, nb * bpb)
+            for j, e in enumerate(chunk):
+                out[e].copy_(q[j])
+            del w, q
         return out
 
     copies = 2 if which == "C4" else 1
     sets = [(stack(I, H, cgu), stack(I, H, cgu), stack(H, I, cd)) for _ in range(copies)]
 
     def step(g, u, d):
-        idx, sc = ops.moe_router_topk(logits, topk)
+        idx, sc = ops.moe_router_topk(logits, topk, shared_gate=False)
         h = ops.moe_glu_gather_kq(x, g, u, cgu, idx)
         return ops.gather_qmv_mix_ns_kq(h, d, cd, idx, sc)
 
-    g, _ = capture(torch, lambda: [step(*st) for st in sets])
+    g, outs = capture(torch, lambda: [step(*st) for st in sets])
     ms = time_graph(torch, g, iters, 3) / copies
     del g
-    idx, _ = ops.moe_router_topk(logits, topk)
+    idx, sc = ops.moe_router_topk(logits, topk, shared_gate=False)
     uniq = int(torch.unique(idx).numel())
     per_expert = 2 * I * (H // 256) * BLOCK_BYTES[cgu] + H * (I // 256) * BLOCK_BYTES[cd]
     act_bytes = T * H * 2 + 2 * T * topk * I * 4 + T * topk * H * 4 * 2 + T * H * 4
     byts = uniq * per_expert + act_bytes
-    del sets
+    # spot check: tokens 0, 1, T/2, T-1 of the first copy against fp64
+    from oracle import kquant as okq
+    from oracle import moe as omoe
+    y = outs[0].cpu().numpy()
+    ids, w = idx.cpu().numpy(), sc.cpu().numpy().astype(np.float64)
+    xf = x.cpu().numpy().astype(np.float64)
+    gs, us, ds = sets[0]
+    deq = {}
+    worst = 0.0
+    for t in sorted({0, 1, T // 2, T - 1}):
+        ref = np.zeros(H)
+        for s_, e in enumerate(ids[t]):
+            if e not in deq:
+                deq[e] = tuple(okq.dequantize(m[e].cpu().numpy(), c).astype(np.float64)
+                               for m, c in ((gs, cgu), (us, cgu), (ds, cd)))
+            G, U, Dn = deq[e]
+            ref += w[t, s_] * (Dn @ omoe.glu(G @ xf[t], U @ xf[t], "silu"))
+        worst = max(worst, okq.max_rel(y[t], ref))
+    del sets, outs
     torch.cuda.empty_cache()
     return {
         "workload": f"{which} MoE decode layer: {E} experts, hidden {H}, expert intermediate {I}, top-{topk}, "
                     f"{T} tokens, gate/up {cgu}, down {cd}",
         "unique_experts": uniq, "ms": round(ms, 4), "algorithmic_bytes": byts,
         "gbs": round(byts / ms / 1e6, 1), "frac_hbm": round(byts / ms / 1e6 / HBM_PEAK_GBS, 4),
-        "tokens_per_s": round(T / ms * 1e3, 1),
+        "tokens_per_s": round(T / ms * 1e3, 1), "max_rel_spot": worst,
     }
 
 

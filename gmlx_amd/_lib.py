@@ -37,7 +37,8 @@ EXPORTS = (
     "kq_version", "kq_strerror", "kq_codec_block_bytes", "kq_supports", "kq_iq2xxs_grid_host",
     "kq_dequantize", "kq_quantize", "kq_matmul_workspace_bytes", "kq_quantized_matmul_grouped",
     "kq_moe_route", "kq_gather_qmm", "kq_moe_glu_gather", "kq_moe_gather_rows", "kq_moe_mix", "kq_moe_router_topk",
-    "kq_sdpa_workspace_bytes", "kq_sdpa_decode_ragged", "kq_sdpa_decode_ragged_q8",
+    "kq_sdpa_workspace_bytes", "kq_sdpa_decode_ragged", "kq_sdpa_decode_ragged_q8", "kq_sdpa_decode_gqa",
+    "kq_sdpa_decode_gqa_q8",
     "kq_sdpa_cascade_workspace_bytes", "kq_sdpa_decode_gqa_cascade", "kq_sdpa_decode_gqa_cascade_q8",
     "kq_gguf_open", "kq_gguf_close", "kq_gguf_header", "kq_gguf_kv", "kq_gguf_tensor", "kq_gguf_type_size",
 )
@@ -70,6 +71,35 @@ class MatmulProblem(ctypes.Structure):
     ]
 
 
+# GLU activations (KQ_ACT_*) and router scoring functions (KQ_SCORE_*)
+ACT_ID = {"silu": 0, "gelu": 1, "silu_limit": 2, "swiglu_clamp": 3}
+SCORE_ID = {"softmax": 0, "sigmoid": 1, "sqrtsoftplus": 2}
+
+
+class GatherEpilogue(ctypes.Structure):
+    _fields_ = [
+        ("act", ctypes.c_int32),
+        ("limit", ctypes.c_float),
+        ("alpha", ctypes.c_float),
+        ("bias0", ctypes.c_void_p),
+        ("bias1", ctypes.c_void_p),
+        ("bias_expert_stride", ctypes.c_int64),
+    ]
+
+
+class RouterOptions(ctypes.Structure):
+    _fields_ = [
+        ("norm_topk_prob", ctypes.c_int32),
+        ("shared_gate", ctypes.c_int32),
+        ("scoring", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("bias", ctypes.c_void_p),
+        ("bias_dtype", ctypes.c_int32),
+        ("per_expert_scale", ctypes.c_void_p),
+        ("per_expert_scale_dtype", ctypes.c_int32),
+    ]
+
+
 _lib = None
 _lock = threading.Lock()
 
@@ -91,14 +121,19 @@ _SIGS = {
                        _vp, _int, _i64, _vp], _int),
     "kq_moe_glu_gather": ([_vp, _int, _i64, _i32, _vp, _vp, _i64, _i64, _i32, _i32, _int, _int, _vp, _vp,
                            _i32, _i32, _vp, _vp], _int),
-    "kq_moe_gather_rows": ([_vp, _int, _i64, _i32, _i32, _vp, _vp, _i64, _i64, _i32, _i32, _int, _int, _vp, _vp,
-                            _i32, _i32, _vp, _int, _i64, _i32, _vp], _int),
+    "kq_moe_gather_rows": ([_vp, _int, _i64, _i32, _i32, _vp, _vp, _i64, _i64, _i32, _i32, _int,
+                            ctypes.POINTER(GatherEpilogue), _vp, _vp, _i32, _i32, _vp, _int, _i64, _i32, _vp], _int),
     "kq_moe_mix": ([_vp, _vp, _i32, _i32, _i32, _vp, _int, _vp], _int),
-    "kq_moe_router_topk": ([_vp, _int, _i32, _i32, _i32, _int, _vp, _vp, _vp], _int),
+    "kq_moe_router_topk": ([_vp, _int, _i64, _i32, _i32, _i32, ctypes.POINTER(RouterOptions), _vp, _vp, _vp],
+                           _int),
     "kq_sdpa_workspace_bytes": ([_i32, _i32, _i32, _i32, _i32], _sz),
     "kq_sdpa_decode_ragged": ([_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _f32, _int, _vp,
                                _vp, _sz, _vp], _int),
     "kq_sdpa_decode_ragged_q8": ([_vp] * 10 + [_i32, _i32, _i32, _i32, _i32, _f32, _int, _vp, _vp, _sz, _vp], _int),
+    "kq_sdpa_decode_gqa": ([_vp, _vp, _vp, _i64, _i64, _i32, _vp, _i32, _i32, _i32, _i32, _f32, _int, _vp, _vp, _sz,
+                            _vp], _int),
+    "kq_sdpa_decode_gqa_q8": ([_vp, _vp, _vp, _vp, _i64, _i64, _i32, _vp, _i32, _i32, _i32, _i32, _f32, _int, _vp,
+                               _vp, _sz, _vp], _int),
     "kq_sdpa_cascade_workspace_bytes": ([_i32, _i32, _i32, _i32, _i32, _i32, _i32], _sz),
     "kq_sdpa_decode_gqa_cascade_q8": ([_vp, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _i64, _i64, _i32, _vp, _i32,
                                        _i32, _i32, _i32, _i32, _f32, _int, _vp, _vp, _sz, _vp], _int),

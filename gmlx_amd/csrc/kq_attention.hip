@@ -61,6 +61,13 @@ struct SdpaArgs {
     const uint16_t *ks, *kb, *vs, *vb, *ks2, *kb2, *vs2, *vb2;
     int32_t q8;
     float scale_log2;     // scale * log2(e)
+    // padded mode (padded != 0, ragged): k / v are [B, Hkv, max_len, D] at
+    // batch / head strides pad_batch_stride / pad_head_stride (elements, or
+    // bytes for 8-bit KV) and row b's keys are [starts[b], max_len) (starts
+    // NULL: 0), so no per-row tables exist: offsets and lengths are derived
+    // here from the device starts
+    int32_t padded;
+    int64_t pad_batch_stride, pad_head_stride;
 };
 
 template <bool BF>
@@ -97,6 +104,25 @@ __device__ __forceinline__ int64_t qo_index(const SdpaArgs &a, int row, int hq) 
     return ((int64_t)sq * a.Hq + hq) * a.qL + i;
 }
 
+// First visible key of padded-mode row b, clamped to [0, max_len].
+__device__ __forceinline__ int padded_start(const SdpaArgs &a, int b) {
+    return a.starts ? min(max(a.starts[b], 0), a.max_len) : 0;
+}
+
+// Keys of ragged row b (rows longer than max_len are clamped to it: the
+// workspace holds max_len / split splits per (row, head)).
+__device__ __forceinline__ int ragged_len(const SdpaArgs &a, int b) {
+    if (a.padded) return a.max_len - padded_start(a, b);
+    return max(min(a.row_len[b], a.max_len), 0);
+}
+
+// Element (byte, 8-bit KV) offset of ragged row b's first visible key of kv head h.
+__device__ __forceinline__ int64_t ragged_base(const SdpaArgs &a, int b, int h, int D) {
+    if (a.padded)
+        return (int64_t)b * a.pad_batch_stride + (int64_t)h * a.pad_head_stride + (int64_t)padded_start(a, b) * D;
+    return a.kv_off[b] + (int64_t)h * a.head_stride[b];
+}
+
 __device__ __forceinline__ int row_splits(int len, int split) {
     return len <= 0 ? 1 : (len + split - 1) / split;
 }
@@ -115,7 +141,7 @@ __device__ __forceinline__ int cascade_len2(const SdpaArgs &a, int r) {
 // splits; cascade mode, the private slab's (the prefix units are counted
 // apart).  A row with no keys keeps one (empty) split.
 __device__ __forceinline__ int row_unit_splits(const SdpaArgs &a, int b) {
-    if (!a.cascade) return row_splits(max(min(a.row_len[b], a.max_len), 0), a.split);
+    if (!a.cascade) return row_splits(ragged_len(a, b), a.split);
     const int n2 = (cascade_len2(a, b) + a.split - 1) / a.split;
     return a.n1 == 0 ? max(n2, 1) : n2;
 }
@@ -505,12 +531,10 @@ __global__ __launch_bounds__(64) void kq_sdpa_split_kernel(SdpaArgs a) {
     for (int u = blockIdx.x;; u += gridDim.x) {
         int b, h, s;
         if (!map_unit(a, u, b, h, s)) return;
-        // rows longer than max_len are clamped to it (the workspace holds
-        // max_len / split splits per (row, head))
-        const int len = max(min(a.row_len[b], a.max_len), 0);
+        const int len = ragged_len(a, b);
         const int t_begin = s * a.split;
         const int t_end = min(len, t_begin + a.split);
-        const int64_t kvbase = a.kv_off[b] + (int64_t)h * a.head_stride[b];
+        const int64_t kvbase = ragged_base(a, b, h, D);
         const int rw[1] = {b}, hd[1] = {r < a.G ? r : 0};
         const bool ok[1] = {r < a.G};
         split_unit<D, BF, NBUF, 1, Q8>(a, kv_src<Q8>(a.k, a.v, a.ks, a.kb, a.vs, a.vb, kvbase), t_begin, t_end, h, s,
@@ -759,12 +783,27 @@ void set_q8(SdpaArgs &a, const Q8Scales *q8, const Q8Scales *q8b) {
     a.vb2 = q8b ? (const uint16_t *)q8b->vb : nullptr;
 }
 
+// Padded layout of kq_sdpa_decode_gqa: strides and device starts instead
+// of per-row tables.
+struct PaddedKv {
+    int64_t batch_stride, head_stride;
+    const int32_t *starts;
+};
+
 int ragged_impl(const void *q, const void *k, const void *v, const Q8Scales *q8, const int64_t *kv_off,
-                const int64_t *head_stride, const int32_t *row_len, int32_t B, int32_t Hq, int32_t Hkv, int32_t D,
-                int32_t max_len, float scale, int dtype, void *out, void *workspace, size_t workspace_bytes,
-                kq_stream_t stream) {
+                const int64_t *head_stride, const int32_t *row_len, const PaddedKv *pad, int32_t B, int32_t Hq,
+                int32_t Hkv, int32_t D, int32_t max_len, float scale, int dtype, void *out, void *workspace,
+                size_t workspace_bytes, kq_stream_t stream) {
     if (B == 0) return KQ_OK;
-    if (!q || !k || !v || !kv_off || !head_stride || !row_len || !out) return KQ_ERR_NULL_POINTER;
+    if (!q || !k || !v || !out) return KQ_ERR_NULL_POINTER;
+    if (!pad && (!kv_off || !head_stride || !row_len)) return KQ_ERR_NULL_POINTER;
+    if (pad) {
+        // token rows of D elements (bytes for 8-bit KV), heads and rows apart
+        if (pad->head_stride < (int64_t)max_len * D || pad->batch_stride < pad->head_stride * Hkv)
+            return KQ_ERR_BAD_SHAPE;
+        const int64_t al = q8 ? 63 : 7;
+        if ((pad->head_stride & al) || (pad->batch_stride & al)) return KQ_ERR_BAD_ALIGN;
+    }
     if (B < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || Hq / Hkv > 16 || max_len < 0) return KQ_ERR_BAD_SHAPE;
     if (D != 64 && D != 96 && D != 128 && D != 256) return KQ_ERR_BAD_SHAPE;
     if ((int64_t)B * Hq > (1 << 30)) return KQ_ERR_BAD_SHAPE;
@@ -784,7 +823,10 @@ int ragged_impl(const void *q, const void *k, const void *v, const Q8Scales *q8,
     a.kv_off = kv_off;
     a.head_stride = head_stride;
     a.row_len = row_len;
-    a.starts = nullptr;
+    a.starts = pad ? pad->starts : nullptr;
+    a.padded = pad ? 1 : 0;
+    a.pad_batch_stride = pad ? pad->batch_stride : 0;
+    a.pad_head_stride = pad ? pad->head_stride : 0;
     a.k2 = a.v2 = nullptr;
     a.shared_head_stride = a.priv_batch_stride = a.priv_head_stride = 0;
     a.cascade = a.P = a.S = a.n1 = a.split1 = 0;
@@ -824,8 +866,27 @@ int kq_sdpa_decode_ragged(const void *q, const void *k, const void *v, const int
                           const int64_t *head_stride, const int32_t *row_len, int32_t B, int32_t Hq,
                           int32_t Hkv, int32_t D, int32_t max_len, float scale, int dtype, void *out,
                           void *workspace, size_t workspace_bytes, kq_stream_t stream) {
-    return ragged_impl(q, k, v, nullptr, kv_off, head_stride, row_len, B, Hq, Hkv, D, max_len, scale, dtype, out,
+    return ragged_impl(q, k, v, nullptr, kv_off, head_stride, row_len, nullptr, B, Hq, Hkv, D, max_len, scale, dtype,
+                       out, workspace, workspace_bytes, stream);
+}
+
+int kq_sdpa_decode_gqa(const void *q, const void *k, const void *v, int64_t batch_stride, int64_t head_stride,
+                       int32_t L, const int32_t *starts, int32_t B, int32_t Hq, int32_t Hkv, int32_t D, float scale,
+                       int dtype, void *out, void *workspace, size_t workspace_bytes, kq_stream_t stream) {
+    const PaddedKv pad{batch_stride, head_stride, starts};
+    return ragged_impl(q, k, v, nullptr, nullptr, nullptr, nullptr, &pad, B, Hq, Hkv, D, L, scale, dtype, out,
                        workspace, workspace_bytes, stream);
+}
+
+int kq_sdpa_decode_gqa_q8(const void *q, const void *k, const void *v, const void *const *kv_scales,
+                          int64_t batch_stride, int64_t head_stride, int32_t L, const int32_t *starts, int32_t B,
+                          int32_t Hq, int32_t Hkv, int32_t D, float scale, int dtype, void *out, void *workspace,
+                          size_t workspace_bytes, kq_stream_t stream) {
+    if (!kv_scales) return KQ_ERR_NULL_POINTER;
+    const Q8Scales q8{kv_scales[0], kv_scales[1], kv_scales[2], kv_scales[3]};
+    const PaddedKv pad{batch_stride, head_stride, starts};
+    return ragged_impl(q, k, v, &q8, nullptr, nullptr, nullptr, &pad, B, Hq, Hkv, D, L, scale, dtype, out, workspace,
+                       workspace_bytes, stream);
 }
 
 int kq_sdpa_decode_ragged_q8(const void *q, const void *k, const void *v, const void *k_scales,
@@ -834,7 +895,7 @@ int kq_sdpa_decode_ragged_q8(const void *q, const void *k, const void *v, const 
                              int32_t Hq, int32_t Hkv, int32_t D, int32_t max_len, float scale, int dtype, void *out,
                              void *workspace, size_t workspace_bytes, kq_stream_t stream) {
     const Q8Scales q8{k_scales, k_biases, v_scales, v_biases};
-    return ragged_impl(q, k, v, &q8, kv_off, head_stride, row_len, B, Hq, Hkv, D, max_len, scale, dtype, out,
+    return ragged_impl(q, k, v, &q8, kv_off, head_stride, row_len, nullptr, B, Hq, Hkv, D, max_len, scale, dtype, out,
                        workspace, workspace_bytes, stream);
 }
 
@@ -936,6 +997,8 @@ int cascade_impl(const void *q, const void *k_shared, const void *v_shared, cons
     a.priv_batch_stride = priv_batch_stride;
     a.priv_head_stride = priv_head_stride;
     a.cascade = 1;
+    a.padded = 0;
+    a.pad_batch_stride = a.pad_head_stride = 0;
     set_q8(a, q8s, q8p);
     a.P = P;
     a.S = S;

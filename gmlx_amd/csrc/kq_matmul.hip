@@ -153,6 +153,11 @@ struct GatherArgs {
     // (a skip of 0 adds nothing): one spare row per x_skip / y_skip pairs,
     // e.g. the shared expert's slot k of an [t, k + 1, N] block
     int32_t x_skip, y_skip;
+    // epilogue: GLU clamp / slope, fp32 biases [expert][N] (b0: gate bias of
+    // the GLU, or the output bias of a plain gather; b1: up bias), or null
+    float limit, alpha;
+    const float *b0, *b1;
+    int64_t b_stride;
 };
 
 __device__ __forceinline__ int64_t gather_x_row(const GatherArgs &a, int pair) {
@@ -162,12 +167,39 @@ __device__ __forceinline__ int64_t gather_y_row(const GatherArgs &a, int pair) {
     return pair + (a.y_skip ? pair / a.y_skip : 0);
 }
 
-__device__ __forceinline__ float act_apply(int act, float g) {
-    if (act == 0) return g / (1.0f + __expf(-g));  // silu
-    // gelu, tanh approximation
-    const float k0 = 0.7978845608028654f, k1 = 0.044715f;
-    const float u = k0 * (g + k1 * g * g * g);
-    return 0.5f * g * (1.0f + tanhf(u));
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+
+// Output of pair rows for weight row n of `expert`: acc[0] (gate, or the
+// plain product) and acc[1] (up) in fp32.
+//   plain          v = g (+ b0[n])
+//   0 silu         silu(g) * u
+//   1 gelu         0.5 g (1 + tanh(0.79788456 (g + 0.044715 g^3)))  * u
+//   2 silu_limit   silu(min(g, limit)) * clamp(u, -limit, limit)
+//                  (gmlx/deepseek_v4_model.py:740-744)
+//   3 swiglu_clamp g' = min(g + b0[n], limit), u' = clamp(u + b1[n], -limit, limit):
+//                  (u' + 1) * g' * sigmoid(alpha g')   (gpt-oss clamped SwiGLU,
+//                  gmlx/minimax_m3_model.py:134-138)
+template <int NW>
+__device__ __forceinline__ float gather_epilogue(const GatherArgs &a, int expert, int n, float g, float u) {
+    if constexpr (NW == 1) {
+        return a.b0 ? g + a.b0[(int64_t)expert * a.b_stride + n] : g;
+    } else {
+        switch (a.act) {
+        case KQ_ACT_SILU: return silu(g) * u;
+        case KQ_ACT_GELU: {
+            const float k0 = 0.7978845608028654f, k1 = 0.044715f;
+            return 0.5f * g * (1.0f + tanhf(k0 * (g + k1 * g * g * g))) * u;
+        }
+        case KQ_ACT_SILU_LIMIT: return silu(fminf(g, a.limit)) * fminf(fmaxf(u, -a.limit), a.limit);
+        default: {
+            if (a.b0) g += a.b0[(int64_t)expert * a.b_stride + n];
+            if (a.b1) u += a.b1[(int64_t)expert * a.b_stride + n];
+            g = fminf(g, a.limit);
+            u = fminf(fmaxf(u, -a.limit), a.limit);
+            return (u + 1.0f) * (g / (1.0f + __expf(-a.alpha * g)));
+        }
+        }
+    }
 }
 
 // One workgroup of kGatherWaves waves per (expert segment, 16-row weight
@@ -258,8 +290,7 @@ __attribute__((amdgpu_waves_per_eu(gather_waves_per_simd<CODEC, MT, NW, XT>())))
                     const int ri = c0 + 16 * mt + 4 * (lane >> 4) + e;
                     if (ri >= seg_end) continue;
                     const int pair = a.pair_order[ri];
-                    float v = acc[0][mt][e];
-                    if constexpr (NW == 2) v = act_apply(a.act, v) * acc[1][mt][e];
+                    const float v = gather_epilogue<NW>(a, expert, n, acc[0][mt][e], acc[NW - 1][mt][e]);
                     kq_store_out(a.y, a.y_dtype, gather_y_row(a, pair) * a.y_stride + n, v);
                 }
             }
@@ -356,8 +387,7 @@ __attribute__((amdgpu_waves_per_eu(gather_waves_per_simd<CODEC, MT, NW, XT>())))
                 const int ri = c0 + 16 * mt + 4 * (lane >> 4) + e;
                 if (ri >= seg_end) continue;
                 const int pair = a.pair_order[ri];
-                float v = acc[0][mt][e];
-                if constexpr (NW == 2) v = act_apply(a.act, v) * acc[1][mt][e];
+                const float v = gather_epilogue<NW>(a, expert, n, acc[0][mt][e], acc[NW - 1][mt][e]);
                 kq_store_out(a.y, a.y_dtype, gather_y_row(a, pair) * a.y_stride + n, v);
             }
         }
@@ -508,75 +538,124 @@ __global__ void kq_mix_kernel(const float *__restrict__ yp, const float *__restr
     kq_store_out(y, y_dtype, (int64_t)t * N + n, acc);
 }
 
-// Router: one wave per token.  softmax over E logits in fp32, top-k by repeated
-// arg-max (ties -> lower expert id), optional renormalisation.
-__global__ __launch_bounds__(64) void kq_router_kernel(const void *logits, int ldt, int32_t E, int32_t k,
-                                                       int norm, int32_t *inds, float *scores) {
+// Router arguments (kq_router_options resolved on the host).
+struct RouterArgs {
+    const void *logits;
+    int64_t ld;              // elements between tokens' logit rows
+    int32_t ldt, E, k;       // logits dtype; routed experts; picks
+    int32_t norm, shared_gate, scoring;
+    float scale;
+    const void *bias;        // [E] selection bias or null
+    const void *pes;         // [E] per-expert scale or null
+    int32_t bias_dt, pes_dt;
+    int32_t *inds;
+    float *scores;           // row stride k + shared_gate
+};
+
+__device__ __forceinline__ float router_load(const void *p, int dt, int64_t i) {
+    return dt == KQ_DTYPE_F32 ? ((const float *)p)[i]
+           : dt == KQ_DTYPE_F16 ? (float)((const _Float16 *)p)[i]
+                                : kq_bf16_bits_to_f32(((const uint16_t *)p)[i]);
+}
+
+// Router: one wave per token, in fp32.
+//   score_e = softmax over the E routed logits (max-subtracted), sigmoid, or
+//             sqrt(softplus) with softplus(x) = max(x, 0) + log1p(exp(-|x|));
+//   picks   = top-k of score_e + bias_e by repeated arg-max (ties -> lower
+//             expert id), reported with their unbiased scores;
+//   weights = picks / (sum of picks + 1e-20) when normalising, then times
+//             per_expert_scale[e] and scale;
+//   shared_gate: logit column E is the shared expert's gate, appended to the
+//             weights as sigmoid(logit) (k + 1 weights per token).
+__global__ __launch_bounds__(64) void kq_router_kernel(RouterArgs a) {
     const int t = blockIdx.x;
     const int lane = kq_lane();
     constexpr int kMaxPerLane = 16;  // E <= 1024
-    float v[kMaxPerLane];
+    const int E = a.E;
+    const int64_t row = (int64_t)t * a.ld;
+    float v[kMaxPerLane], sel[kMaxPerLane];
     float mx = -INFINITY;
 #pragma unroll
     for (int i = 0; i < kMaxPerLane; ++i) {
         const int e = lane + 64 * i;
-        float x = -INFINITY;
-        if (e < E) {
-            const int64_t o = (int64_t)t * E + e;
-            x = ldt == KQ_DTYPE_F32 ? ((const float *)logits)[o]
-                : ldt == KQ_DTYPE_F16 ? (float)((const _Float16 *)logits)[o]
-                                      : kq_bf16_bits_to_f32(((const uint16_t *)logits)[o]);
-        }
+        const float x = e < E ? router_load(a.logits, a.ldt, row + e) : -INFINITY;
         v[i] = x;
         mx = fmaxf(mx, x);
     }
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-    float sum = 0.f;
+    if (a.scoring == KQ_SCORE_SOFTMAX) {
+        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+        float sum = 0.f;
+#pragma unroll
+        for (int i = 0; i < kMaxPerLane; ++i) {
+            const int e = lane + 64 * i;
+            v[i] = e < E ? expf(v[i] - mx) : 0.f;
+            sum += v[i];
+        }
+        for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+#pragma unroll
+        for (int i = 0; i < kMaxPerLane; ++i) v[i] = v[i] / sum;
+    } else if (a.scoring == KQ_SCORE_SIGMOID) {
+#pragma unroll
+        for (int i = 0; i < kMaxPerLane; ++i) v[i] = 1.f / (1.f + expf(-v[i]));
+    } else {
+#pragma unroll
+        for (int i = 0; i < kMaxPerLane; ++i) {
+            const float x = v[i];
+            v[i] = sqrtf(fmaxf(x, 0.f) + log1pf(expf(-fabsf(x))));
+        }
+    }
 #pragma unroll
     for (int i = 0; i < kMaxPerLane; ++i) {
         const int e = lane + 64 * i;
-        v[i] = e < E ? expf(v[i] - mx) : -1.f;
-        if (e < E) sum += v[i];
+        sel[i] = e < E ? v[i] + (a.bias ? router_load(a.bias, a.bias_dt, e) : 0.f) : -INFINITY;
     }
-    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
-#pragma unroll
-    for (int i = 0; i < kMaxPerLane; ++i)
-        if (lane + 64 * i < E) v[i] = v[i] / sum;
     float picked_sum = 0.f, my_score = 0.f;
     int my_ind = 0;
-    for (int j = 0; j < k; ++j) {
-        float best = -2.f;
+    uint32_t taken = 0;  // bit i: expert lane + 64 i already picked
+    for (int j = 0; j < a.k; ++j) {
+        float best = -INFINITY, best_v = 0.f;
         int bi = 0x7FFFFFFF;
 #pragma unroll
         for (int i = 0; i < kMaxPerLane; ++i) {
             const int e = lane + 64 * i;
-            if (e < E && (v[i] > best || (v[i] == best && e < bi))) {
-                best = v[i];
+            if (e < E && !((taken >> i) & 1u) && (sel[i] > best || (sel[i] == best && e < bi))) {
+                best = sel[i];
+                best_v = v[i];
                 bi = e;
             }
         }
         for (int off = 32; off > 0; off >>= 1) {
             const float ob = __shfl_xor(best, off);
+            const float ov = __shfl_xor(best_v, off);
             const int oi = __shfl_xor(bi, off);
             if (ob > best || (ob == best && oi < bi)) {
                 best = ob;
+                best_v = ov;
                 bi = oi;
             }
         }
 #pragma unroll
         for (int i = 0; i < kMaxPerLane; ++i)
-            if (lane + 64 * i == bi) v[i] = -1.f;
-        picked_sum += best;
-        // lane j keeps pick j (best / bi are uniform over the wave here)
+            if (lane + 64 * i == bi) taken |= 1u << i;
+        picked_sum += best_v;
+        // lane j keeps pick j (best_v / bi are uniform over the wave here)
         if (lane == j) {
-            my_score = best;
+            my_score = best_v;
             my_ind = bi;
         }
     }
     // one store per output array; picks are renormalised from registers
-    if (lane < k) {
-        inds[(int64_t)t * k + lane] = my_ind;
-        scores[(int64_t)t * k + lane] = norm ? my_score / picked_sum : my_score;
+    const int sld = a.k + a.shared_gate;
+    if (lane < a.k) {
+        float w = a.norm ? my_score / (picked_sum + 1e-20f) : my_score;
+        if (a.pes) w *= router_load(a.pes, a.pes_dt, my_ind);
+        w *= a.scale;
+        a.inds[(int64_t)t * a.k + lane] = my_ind;
+        a.scores[(int64_t)t * sld + lane] = w;
+    }
+    if (a.shared_gate && lane == 0) {
+        const float g = router_load(a.logits, a.ldt, row + E);
+        a.scores[(int64_t)t * sld + a.k] = 1.f / (1.f + expf(-g));
     }
 }
 
@@ -721,7 +800,7 @@ void launch_gather(int codec, int mt, const GatherArgs &a, int grid, hipStream_t
 
 int gather_common(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pair_div, const void *w0,
                   const void *w1, int64_t w_expert_bytes, int64_t w_row_bytes, int32_t N, int32_t K,
-                  int codec, int act, const int32_t *seg_info, const int32_t *pair_order,
+                  int codec, const kq_gather_epilogue *ep, const int32_t *seg_info, const int32_t *pair_order,
                   int32_t n_pairs, int32_t n_experts, void *y, int y_dtype, int64_t y_row_stride,
                   hipStream_t s, int32_t x_skip = 0, int32_t y_skip = 0) {
     if (!x || !w0 || !seg_info || !pair_order || !y) return KQ_ERR_NULL_POINTER;
@@ -742,6 +821,15 @@ int gather_common(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pa
                                    (w1 && ((uintptr_t)w1 & 15))))
         return KQ_ERR_BAD_ALIGN;
     if (((uintptr_t)w0 & 1) || (w_row_bytes & 1) || (w_expert_bytes & 1)) return KQ_ERR_BAD_ALIGN;
+    const kq_gather_epilogue plain{KQ_ACT_SILU, 0.f, 0.f, nullptr, nullptr, 0};
+    if (!ep) ep = &plain;
+    if (w1 && (ep->act < KQ_ACT_SILU || ep->act > KQ_ACT_SWIGLU_CLAMP)) return KQ_ERR_BAD_ARGUMENT;
+    if (!w1 && ep->bias1) return KQ_ERR_BAD_ARGUMENT;
+    if (w1 && ep->act != KQ_ACT_SWIGLU_CLAMP && (ep->bias0 || ep->bias1)) return KQ_ERR_BAD_ARGUMENT;
+    if ((ep->bias0 || ep->bias1) && ep->bias_expert_stride < N) return KQ_ERR_BAD_SHAPE;
+    if (((uintptr_t)ep->bias0 | (uintptr_t)ep->bias1) & 3) return KQ_ERR_BAD_ALIGN;
+    if ((ep->act == KQ_ACT_SILU_LIMIT || ep->act == KQ_ACT_SWIGLU_CLAMP) && w1 && !(ep->limit > 0.f))
+        return KQ_ERR_BAD_ARGUMENT;
     GatherArgs a;
     a.x = (const char *)x;
     a.w0 = (const uint8_t *)w0;
@@ -762,7 +850,12 @@ int gather_common(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pa
     a.n_experts = n_experts;
     a.n_tiles = (N + 15) / 16;
     a.y_dtype = y_dtype;
-    a.act = act;
+    a.act = w1 ? ep->act : KQ_ACT_SILU;
+    a.limit = ep->limit;
+    a.alpha = ep->alpha;
+    a.b0 = ep->bias0;
+    a.b1 = w1 ? ep->bias1 : nullptr;
+    a.b_stride = ep->bias_expert_stride;
     // m-tiles per chunk from the mean segment length (pairs spread over the
     // experts): decode batches leave a few rows per expert; longer segments
     // are walked in chunks of 16 * mt rows
@@ -946,7 +1039,7 @@ int kq_gather_qmm(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pa
                   const int32_t *seg_info, const int32_t *pair_order, int32_t n_pairs,
                   int32_t n_experts, void *y, int y_dtype, int64_t y_row_stride, kq_stream_t stream) {
     return gather_common(x, x_dtype, x_row_stride, x_pair_div, w, nullptr, w_expert_bytes, w_row_bytes,
-                         N, K, codec, 0, seg_info, pair_order, n_pairs, n_experts, y, y_dtype,
+                         N, K, codec, nullptr, seg_info, pair_order, n_pairs, n_experts, y, y_dtype,
                          y_row_stride, (hipStream_t)stream);
 }
 
@@ -956,21 +1049,21 @@ int kq_moe_glu_gather(const void *x, int x_dtype, int64_t x_row_stride, int32_t 
                       const int32_t *pair_order, int32_t n_pairs, int32_t n_experts, float *h,
                       kq_stream_t stream) {
     if (!w_up) return KQ_ERR_NULL_POINTER;
-    if (act != 0 && act != 1) return KQ_ERR_BAD_ARGUMENT;
+    if (act != KQ_ACT_SILU && act != KQ_ACT_GELU) return KQ_ERR_BAD_ARGUMENT;
+    const kq_gather_epilogue ep{act, 0.f, 0.f, nullptr, nullptr, 0};
     return gather_common(x, x_dtype, x_row_stride, x_pair_div, w_gate, w_up, w_expert_bytes, w_row_bytes,
-                         N, K, codec, act, seg_info, pair_order, n_pairs, n_experts, h, KQ_DTYPE_F32, N,
+                         N, K, codec, &ep, seg_info, pair_order, n_pairs, n_experts, h, KQ_DTYPE_F32, N,
                          (hipStream_t)stream);
 }
 
 int kq_moe_gather_rows(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pair_div, int32_t x_skip,
                        const void *w0, const void *w1, int64_t w_expert_bytes, int64_t w_row_bytes, int32_t N,
-                       int32_t K, int codec, int act, const int32_t *seg_info, const int32_t *pair_order,
-                       int32_t n_pairs, int32_t n_experts, void *y, int y_dtype, int64_t y_row_stride,
-                       int32_t y_skip, kq_stream_t stream) {
-    if (w1 && act != 0 && act != 1) return KQ_ERR_BAD_ARGUMENT;
+                       int32_t K, int codec, const kq_gather_epilogue *ep, const int32_t *seg_info,
+                       const int32_t *pair_order, int32_t n_pairs, int32_t n_experts, void *y, int y_dtype,
+                       int64_t y_row_stride, int32_t y_skip, kq_stream_t stream) {
     if (w1 && y_dtype != KQ_DTYPE_F32) return KQ_ERR_UNSUPPORTED_DTYPE;
     return gather_common(x, x_dtype, x_row_stride, x_pair_div, w0, w1, w_expert_bytes, w_row_bytes, N, K, codec,
-                         w1 ? act : 0, seg_info, pair_order, n_pairs, n_experts, y, y_dtype, y_row_stride,
+                         ep, seg_info, pair_order, n_pairs, n_experts, y, y_dtype, y_row_stride,
                          (hipStream_t)stream, x_skip, y_skip);
 }
 
@@ -986,15 +1079,38 @@ int kq_moe_mix(const float *y_pairs, const float *scores, int32_t T, int32_t top
     return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
 }
 
-int kq_moe_router_topk(const void *logits, int logits_dtype, int32_t T, int32_t E, int32_t k,
-                       int norm_topk_prob, int32_t *inds, float *scores, kq_stream_t stream) {
+int kq_moe_router_topk(const void *logits, int logits_dtype, int64_t logits_row_stride, int32_t T, int32_t E,
+                       int32_t k, const kq_router_options *opts, int32_t *inds, float *scores,
+                       kq_stream_t stream) {
     if (!logits || !inds || !scores) return KQ_ERR_NULL_POINTER;
-    if (T < 0 || E <= 0 || E > 1024 || k <= 0 || k > 32 || k > E) return KQ_ERR_BAD_SHAPE;
-    if (logits_dtype != KQ_DTYPE_F32 && logits_dtype != KQ_DTYPE_F16 && logits_dtype != KQ_DTYPE_BF16)
+    const kq_router_options dflt{1, 0, KQ_SCORE_SOFTMAX, 1.f, nullptr, KQ_DTYPE_F32, nullptr, KQ_DTYPE_F32};
+    const kq_router_options &o = opts ? *opts : dflt;
+    const int sg = o.shared_gate ? 1 : 0;
+    if (T < 0 || E <= 0 || E > 1024 || k <= 0 || k > 32 || k > E || logits_row_stride < E + sg)
+        return KQ_ERR_BAD_SHAPE;
+    auto dt_ok = [](int d) { return d == KQ_DTYPE_F32 || d == KQ_DTYPE_F16 || d == KQ_DTYPE_BF16; };
+    if (!dt_ok(logits_dtype) || (o.bias && !dt_ok(o.bias_dtype)) ||
+        (o.per_expert_scale && !dt_ok(o.per_expert_scale_dtype)))
         return KQ_ERR_UNSUPPORTED_DTYPE;
+    if (o.scoring < KQ_SCORE_SOFTMAX || o.scoring > KQ_SCORE_SQRTSOFTPLUS) return KQ_ERR_BAD_ARGUMENT;
     if (T == 0) return KQ_OK;
-    hipLaunchKernelGGL(kq_router_kernel, dim3(T), dim3(64), 0, (hipStream_t)stream, logits, logits_dtype, E,
-                       k, norm_topk_prob, inds, scores);
+    RouterArgs a;
+    a.logits = logits;
+    a.ld = logits_row_stride;
+    a.ldt = logits_dtype;
+    a.E = E;
+    a.k = k;
+    a.norm = o.norm_topk_prob ? 1 : 0;
+    a.shared_gate = sg;
+    a.scoring = o.scoring;
+    a.scale = o.scale;
+    a.bias = o.bias;
+    a.bias_dt = o.bias_dtype;
+    a.pes = o.per_expert_scale;
+    a.pes_dt = o.per_expert_scale_dtype;
+    a.inds = inds;
+    a.scores = scores;
+    hipLaunchKernelGGL(kq_router_kernel, dim3(T), dim3(64), 0, (hipStream_t)stream, a);
     return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
 }
 

@@ -1,8 +1,8 @@
 // GPU quantizers: fp32 rows -> GGUF Q4_K / Q6_K / IQ2_XXS super-blocks.
 // Stands in for kq.quantize (tests/test_dequant_unattachable.py:36,
 // gmlx/mtp_load.py:290).  Q4_K and Q6_K follow llama.cpp's reference
-// quantizers (make_qkx2_quants / make_qx_quants searches); IQ2_XXS uses an
-// exhaustive grid search.  Every float operation is written in a fixed order
+// quantizers (make_qkx2_quants / make_qx_quants searches); IQ2_XXS uses this
+// build's own nearest-lattice search (below).  Every float operation is written in a fixed order
 // and the file is compiled without contraction, so results are deterministic
 // and reproducible on the host.
 #include "kq_common.h"
@@ -255,8 +255,42 @@ __global__ __launch_bounds__(64) void quant_q6k_kernel(const float *__restrict__
     }
 }
 
-// IQ2_XXS: one thread per 32-value group; the block scale d is computed by
-// every group thread of the block from the same 256 values.
+// IQ2_XXS quantizer (this build's own search).  Grid bytes take the values
+// 8, 25 and 43 (levels 0, 1, 2).  For a scale db, each folded value picks the
+// nearest level by the midpoints (below 16.5 db: 0, below 34 db: 1, else 2);
+// the 8 levels of a sub-group form a lattice point u = sum l_j 3^j, and the
+// grid entry nearest to it in level values (g_iq2_near[u], integer squared
+// distance, ties to the lower entry) is taken.  The scale field s (db =
+// d (0.5 + s) / 4) with the least squared error over the group's 32 values
+// wins (ties to the lower s).
+
+__device__ uint8_t g_iq2_near[6561];
+
+// g_iq2_near[u] for every lattice point u (one thread each).
+__global__ __launch_bounds__(256) void iq2_near_kernel() {
+    const int u = blockIdx.x * blockDim.x + threadIdx.x;
+    if (u >= 6561) return;
+    int lv[8];
+    for (int j = 0, r = u; j < 8; ++j, r /= 3) lv[j] = r % 3;
+    const int val[3] = {8, 25, 43};
+    int best = 0x7FFFFFFF, bk = 0;
+    for (int k = 0; k < 256; ++k) {
+        const uint64_t gv = kGrid[k];
+        int dsum = 0;
+        for (int j = 0; j < 8; ++j) {
+            const int d = val[lv[j]] - (int)((gv >> (8 * j)) & 0xFF);
+            dsum += d * d;
+        }
+        if (dsum < best) {
+            best = dsum;
+            bk = k;
+        }
+    }
+    g_iq2_near[u] = (uint8_t)bk;
+}
+
+// One thread per 32-value group; the block scale d is computed by every
+// group thread of the block from the same 256 values.
 __global__ __launch_bounds__(64) void quant_iq2xxs_kernel(const float *__restrict__ w, int64_t n_rows, int nb,
                                                           int64_t w_stride, uint8_t *__restrict__ out) {
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -307,26 +341,25 @@ __global__ __launch_bounds__(64) void quant_iq2xxs_kernel(const float *__restric
     uint32_t best_s = 0, best_idx = 0;
     for (uint32_t sfield = 0; sfield < 16; ++sfield) {
         const float db = d * (0.5f + (float)sfield) * 0.25f;
+        const float t01 = db * 16.5f, t12 = db * 34.f;
         float err_tot = 0;
         uint32_t idx_word = 0;
         for (int l = 0; l < 4; ++l) {
-            float be = INFINITY;
-            int bk = 0;
-            for (int k = 0; k < 256; ++k) {
-                const uint64_t gv = kGrid[k];
-                float e = 0;
-                for (int j = 0; j < 8; ++j) {
-                    const float q = db * (float)((gv >> (8 * j)) & 0xFF);
-                    const float diff = q - folded[8 * l + j];
-                    e += diff * diff;
-                }
-                if (e < be) {
-                    be = e;
-                    bk = k;
-                }
+            int u = 0;
+            for (int j = 7; j >= 0; --j) {
+                const float f = folded[8 * l + j];
+                u = 3 * u + (f < t01 ? 0 : (f < t12 ? 1 : 2));
             }
-            err_tot += be;
-            idx_word |= (uint32_t)bk << (8 * l);
+            const uint32_t k = g_iq2_near[u];
+            const uint64_t gv = kGrid[k];
+            float e = 0;
+            for (int j = 0; j < 8; ++j) {
+                const float q = db * (float)((gv >> (8 * j)) & 0xFF);
+                const float diff = q - folded[8 * l + j];
+                e += diff * diff;
+            }
+            err_tot += e;
+            idx_word |= k << (8 * l);
         }
         if (err_tot < best_err) {
             best_err = err_tot;
@@ -361,6 +394,9 @@ extern "C" int kq_quantize(const float *w, int64_t n_rows, int64_t K, int64_t w_
         hipLaunchKernelGGL(quant_q6k_kernel, dim3((unsigned)((blocks + 63) / 64)), dim3(64), 0, s, w, n_rows,
                            nb, w_row_stride, (uint8_t *)wire);
     } else {
+        // the nearest-grid table is rebuilt on the stream ahead of every
+        // launch (26 workgroups): no state outlives the call
+        hipLaunchKernelGGL(iq2_near_kernel, dim3((6561 + 255) / 256), dim3(256), 0, s);
         hipLaunchKernelGGL(quant_iq2xxs_kernel, dim3((unsigned)((blocks * 8 + 63) / 64)), dim3(64), 0, s, w,
                            n_rows, nb, w_row_stride, (uint8_t *)wire);
     }

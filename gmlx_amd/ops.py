@@ -10,10 +10,13 @@ Op names and argument orders follow the reference's calls:
   quantize(w, codec) -> (wire, scales)           tests/test_dequant_unattachable.py:36
   quantized_matmul(x, w, scales, codec, transpose=True)   gmlx/occupancy_fuse.py:162-165
   gather_qmm / KQuantSwitchLinear                tests/test_native_fp.py:420-428
-  moe_glu_gather_kq(x, gate_w, up_w, codec, idx, act=)    gmlx/modules.py:557-588
-  gather_qmv_kq(h, down_w, codec, idx)           gmlx/modules.py:595-597
+  moe_glu_gather_kq(x, gate_w, up_w, codec, idx, act=, limit=, alpha=,
+                    gate_bias=, up_bias=)        gmlx/modules.py:557-588
+  gather_qmv_kq(h, down_w, codec, idx, bias=)    gmlx/modules.py:595-597
   gather_qmv_mix_ns_kq(h, down_w, codec, idx, scores)     gmlx/modules.py:591-593
-  moe_router_topk(logits, k, norm_topk_prob)     gmlx/modules.py:750-752
+  moe_router_topk(logits, k, norm_topk_prob, shared_gate=, per_expert_scale=,
+                  bias=, scoring=, scale=)       gmlx/modules.py:750-752, 1043-1046;
+                                                 gmlx/deepseek_v4_model.py:1179-1187
   sdpa_decode_gqa(q, k, v, scale, starts=)       gmlx/gemma4_batched_sdpa.py:221-222
   ragged_decode_attention(q, k, v, pads, scale)  gmlx/qwen35_attn.py:395-493
 """
@@ -256,6 +259,53 @@ def moe_route(idx, n_experts):
     return seg, order
 
 
+class _RouteMemo:
+    """Routing tables handed from one gather to the next.  A MoE layer passes
+    one `idx` to its GLU gather and then to its down gather; grouping the
+    pairs once serves both.  A gather that routes leaves its tables here;
+    the next gather over the same index tensor (same storage, geometry and
+    version counter, so not written in place since, on the same stream and
+    on the same side of a graph capture) takes them and removes the entry,
+    so a third call, or the next layer over a reused buffer, routes afresh.
+    An entry keeps its index tensor alive, so its storage cannot be handed
+    to another tensor while the entry exists."""
+
+    def __init__(self, size=8):
+        self._d = OrderedDict()
+        self._size = size
+
+    @staticmethod
+    def _key(idx, n_experts, stream_handle):
+        return (idx.data_ptr(), tuple(idx.shape), tuple(idx.stride()), idx.dtype, idx._version, n_experts,
+                idx.device.index, stream_handle, torch.cuda.is_current_stream_capturing())
+
+    def take(self, idx, n_experts, stream_handle):
+        hit = self._d.pop(self._key(idx, n_experts, stream_handle), None)
+        if hit is not None:
+            return hit[1], hit[2]
+        return None
+
+    def put(self, idx, n_experts, stream_handle, seg, order):
+        self._d[self._key(idx, n_experts, stream_handle)] = (idx, seg, order)
+        if len(self._d) > self._size:
+            self._d.popitem(last=False)
+
+
+_ROUTES = _RouteMemo()
+
+
+def _routed(idx, n_experts):
+    """(seg_info, pair_order) for idx: the tables the previous gather over
+    the same idx left, else a fresh kq_moe_route (left for the next one)."""
+    sh = _stream(idx).value
+    hit = _ROUTES.take(idx, n_experts, sh)
+    if hit is not None:
+        return hit
+    seg, order = moe_route(idx, n_experts)
+    _ROUTES.put(idx, n_experts, sh, seg, order)
+    return seg, order
+
+
 def _expert_stack(w, codec, K):
     if w.dim() != 3 or w.dtype != torch.uint8:
         raise ValueError("expert weights must be a uint8 wire stack [E, N, K/256*block_bytes]")
@@ -272,23 +322,48 @@ def _x_dt(x):
     return _dt(x.dtype)
 
 
-def _gather(x2, x_pair_div, w, codec, idx2, out, out_dt, w_up=None, act=0):
-    E, N, _ = w.shape
-    K = x2.shape[1]
-    seg, order = moe_route(idx2, E)
-    P = idx2.numel()
-    L = lib()
-    s = _stream(x2)
-    if w_up is None:
-        rc = L.kq_gather_qmm(x2.data_ptr(), _x_dt(x2), x2.stride(0), x_pair_div, w.data_ptr(), w.stride(0),
-                             w.stride(1), N, K, _codec_id(codec), seg.data_ptr(), order.data_ptr(), P, E,
-                             out.data_ptr(), out_dt, out.stride(0), s)
-        check("kq_gather_qmm", rc)
-    else:
-        rc = L.kq_moe_glu_gather(x2.data_ptr(), _x_dt(x2), x2.stride(0), x_pair_div, w.data_ptr(),
-                                 w_up.data_ptr(), w.stride(0), w.stride(1), N, K, _codec_id(codec), act,
-                                 seg.data_ptr(), order.data_ptr(), P, E, out.data_ptr(), s)
-        check("kq_moe_glu_gather", rc)
+def _bias_rows(b, E, N, name, device):
+    """Per-expert fp32 bias rows [E, N] (the reference caches them as float32
+    copies, gmlx/modules.py:625-633)."""
+    if b is None:
+        return None
+    if not isinstance(b, torch.Tensor) or b.device != device:
+        raise ValueError(f"{name} must be a tensor on the activations' device")
+    if tuple(b.shape[-2:] if b.dim() >= 2 else (1,) + tuple(b.shape)) != (E, N):
+        raise ValueError(f"{name} must be [{E}, {N}] (one row of N biases per expert)")
+    return b.reshape(E, N).to(torch.float32).contiguous()
+
+
+def _epilogue(act, limit, alpha, gate_bias, up_bias, E, N, device):
+    """GatherEpilogue for act= / limit= / alpha= / gate_bias= / up_bias= of
+    the fused GLU gathers (gmlx/modules.py:557-566), plus the tensors it
+    points at (kept alive for the launch)."""
+    if act not in _lib.ACT_ID:
+        raise ValueError(f"act {act!r} has no kernel epilogue; have {tuple(_lib.ACT_ID)}")
+    if act in ("silu_limit", "swiglu_clamp"):
+        if limit is None:
+            limit = 7.0 if act == "swiglu_clamp" else None
+        if limit is None or not float(limit) > 0.0:
+            raise ValueError(f"act {act!r} needs limit > 0")
+    elif any(v is not None for v in (limit, alpha, gate_bias, up_bias)):
+        raise ValueError(f"act {act!r} takes no limit / alpha / biases")
+    if act != "swiglu_clamp" and (gate_bias is not None or up_bias is not None):
+        raise ValueError("gate_bias / up_bias belong to act='swiglu_clamp'")
+    gb = _bias_rows(gate_bias, E, N, "gate_bias", device)
+    ub = _bias_rows(up_bias, E, N, "up_bias", device)
+    ep = _lib.GatherEpilogue(_lib.ACT_ID[act], float(limit or 0.0),
+                             float(1.702 if alpha is None and act == "swiglu_clamp" else (alpha or 0.0)),
+                             None if gb is None else gb.data_ptr(), None if ub is None else ub.data_ptr(), N)
+    return ep, (gb, ub)
+
+
+def _gather_rows(x_ptr, x_dt, x_stride, x_pair_div, x_skip, w, w_up, codec, ep, seg, order, P, E, y_ptr, y_dt,
+                 y_stride, y_skip, K, stream):
+    rc = lib().kq_moe_gather_rows(x_ptr, x_dt, x_stride, x_pair_div, x_skip, w.data_ptr(),
+                                  None if w_up is None else w_up.data_ptr(), w.stride(0), w.stride(1), w.shape[1],
+                                  K, _codec_id(codec), None if ep is None else ctypes.byref(ep), seg.data_ptr(),
+                                  order.data_ptr(), P, E, y_ptr, y_dt, y_stride, y_skip, stream)
+    check("kq_moe_gather_rows", rc)
 
 
 def gather_qmm(x, w, scales=None, codec="q4_k", indices=None, sorted_indices=False, out_dtype=None):
@@ -305,22 +380,23 @@ def gather_qmm(x, w, scales=None, codec="q4_k", indices=None, sorted_indices=Fal
         raise ValueError(f"x has {x2.shape[0]} rows for {T} index rows")
     w = _expert_stack(w, codec, K)
     out_dtype = out_dtype or x.dtype
-    y = torch.empty((T * k, w.shape[1]), dtype=out_dtype, device=x.device)
+    E, N = w.shape[0], w.shape[1]
+    y = torch.empty((T * k, N), dtype=out_dtype, device=x.device)
     if T * k:
-        _gather(x2, k, w, codec, indices.reshape(T, k), y, _dt(out_dtype))
-    return y.reshape(T, k, 1, w.shape[1])
+        seg, order = _routed(indices, E)
+        _gather_rows(x2.data_ptr(), _x_dt(x2), x2.stride(0), k, 0, w, None, codec, None, seg, order, T * k, E,
+                     y.data_ptr(), _dt(out_dtype), N, 0, K, _stream(x2))
+    return y.reshape(T, k, 1, N)
 
 
-_ACTS = {"silu": 0, "gelu": 1}
-
-
-def moe_glu_gather_kq(x, gate_w, up_w, codec, idx, act="silu"):
-    """Fused MoE GLU gather: h[t, s] = act(Wg[e] . x[t]) * (Wu[e] . x[t]),
-    e = idx[t, s], fp32 epilogue -> h (t, k, I) float32."""
+def moe_glu_gather_kq(x, gate_w, up_w, codec, idx, act="silu", limit=None, alpha=None, gate_bias=None,
+                      up_bias=None):
+    """Fused MoE GLU gather (gmlx/modules.py:557-588): h[t, s] =
+    act(Wg[e] . x[t], Wu[e] . x[t]), e = idx[t, s], in fp32 -> (t, k, I)
+    float32.  act: "silu", "gelu" (tanh form), "silu_limit" (limit=) or
+    "swiglu_clamp" (limit=, alpha=, gate_bias= / up_bias= fp32 [E, I])."""
     _fault("moe_glu_gather_kq")
     _require_gpu(x, gate_w, up_w, idx)
-    if act not in _ACTS:
-        raise ValueError(f"act {act!r} has no kernel epilogue; have {tuple(_ACTS)}")
     K = x.shape[-1]
     t, k = idx.shape[0], idx.shape[-1]
     x2 = _rows_view(x)
@@ -328,18 +404,22 @@ def moe_glu_gather_kq(x, gate_w, up_w, codec, idx, act="silu"):
     up_w = _expert_stack(up_w, codec, K)
     if gate_w.shape != up_w.shape or gate_w.stride() != up_w.stride():
         raise ValueError("gate and up stacks must share shape and layout")
-    h = torch.empty((t * k, gate_w.shape[1]), dtype=torch.float32, device=x.device)
+    E, I = gate_w.shape[0], gate_w.shape[1]
+    ep, keep = _epilogue(act, limit, alpha, gate_bias, up_bias, E, I, x.device)
+    h = torch.empty((t * k, I), dtype=torch.float32, device=x.device)
     if t * k:
-        _gather(x2, k, gate_w, codec, idx.reshape(t, k), h, DTYPE_F32, w_up=up_w, act=_ACTS[act])
-    return h.reshape(t, k, gate_w.shape[1])
+        seg, order = _routed(idx, E)
+        _gather_rows(x2.data_ptr(), _x_dt(x2), x2.stride(0), k, 0, gate_w, up_w, codec, ep, seg, order, t * k, E,
+                     h.data_ptr(), DTYPE_F32, I, 0, K, _stream(x2))
+    del keep
+    return h.reshape(t, k, I)
 
 
 def gather_qmv_kq(h, down_w, codec, idx, bias=None, out_dtype=torch.float32):
-    """Per-pair down projection: y[t, s] = dequant(Wd[idx[t, s]]) . h[t, s]
-    -> (t, k, N).  h (t, k, I) float32/float16/bfloat16."""
+    """Per-pair down projection (gmlx/modules.py:595-597): y[t, s] =
+    dequant(Wd[idx[t, s]]) . h[t, s] (+ bias[idx[t, s]], fp32 [E, N]) ->
+    (t, k, N).  h (t, k, I) float32/float16/bfloat16."""
     _fault("gather_qmv_kq")
-    if bias is not None:
-        raise ValueError("biased expert stacks are not supported by the K-quant kernels")
     _require_gpu(h, down_w, idx)
     t, k = idx.shape[0], idx.shape[-1]
     I = h.shape[-1]
@@ -347,16 +427,21 @@ def gather_qmv_kq(h, down_w, codec, idx, bias=None, out_dtype=torch.float32):
     if h2.shape[0] != t * k:
         raise ValueError("h must hold one row per (token, slot) pair")
     down_w = _expert_stack(down_w, codec, I)
-    y = torch.empty((t * k, down_w.shape[1]), dtype=out_dtype, device=h.device)
+    E, N = down_w.shape[0], down_w.shape[1]
+    b = _bias_rows(bias, E, N, "bias", h.device)
+    ep = None if b is None else _lib.GatherEpilogue(0, 0.0, 0.0, b.data_ptr(), None, N)
+    y = torch.empty((t * k, N), dtype=out_dtype, device=h.device)
     if t * k:
-        _gather(h2, 1, down_w, codec, idx.reshape(t, k), y, _dt(out_dtype))
-    return y.reshape(t, k, down_w.shape[1])
+        seg, order = _routed(idx, E)
+        _gather_rows(h2.data_ptr(), _x_dt(h2), h2.stride(0), 1, 0, down_w, None, codec, ep, seg, order, t * k, E,
+                     y.data_ptr(), _dt(out_dtype), N, 0, I, _stream(h2))
+    return y.reshape(t, k, N)
 
 
 def gather_qmv_mix_ns_kq(h, down_w, codec, idx, scores, out_dtype=torch.float32):
-    """Down projection with the routing mix folded in:
-    y[t] = sum_s scores[t, s] * (Wd[idx[t, s]] . h[t, s]), fp32, slots summed
-    in order."""
+    """Down projection with the routing mix folded in (gmlx/modules.py:
+    591-593): y[t] = sum_s scores[t, s] * (Wd[idx[t, s]] . h[t, s]), fp32,
+    slots summed in order."""
     _fault("gather_qmv_mix_ns_kq")
     _require_gpu(h, down_w, idx, scores)
     t, k = idx.shape[0], idx.shape[-1]
@@ -398,26 +483,18 @@ def _shared_matrix(w, codec, K, name):
     return w.contiguous().unsqueeze(0)
 
 
-def _gather_rows(x_ptr, x_dt, x_stride, x_pair_div, x_skip, w, w_up, codec, act, seg, order, P, E, y_ptr, y_dt,
-                 y_stride, y_skip, K, stream):
-    rc = lib().kq_moe_gather_rows(x_ptr, x_dt, x_stride, x_pair_div, x_skip, w.data_ptr(),
-                                  None if w_up is None else w_up.data_ptr(), w.stride(0), w.stride(1), w.shape[1],
-                                  K, _codec_id(codec), act, seg.data_ptr(), order.data_ptr(), P, E, y_ptr, y_dt,
-                                  y_stride, y_skip, stream)
-    check("kq_moe_gather_rows", rc)
-
-
 def moe_glu_gather_shexp_kq(x, gate_w, up_w, shexp_gate_w, shexp_up_w, codec, idx, act="silu",
-                            shexp_kquant_type=None):
+                            shexp_kquant_type=None, limit=None, alpha=None):
     """kq.moe_glu_gather_shexp_kq (gmlx/modules.py:571-574, 777-780): the
     routed GLU gather of moe_glu_gather_kq plus the shared expert's GLU on
     every token, h (t, k + 1, I) float32 with the shared expert in slot k.
     The shared matrices may use another codec (`shexp_kquant_type`); their
-    intermediate size must equal the routed experts'."""
+    intermediate size must equal the routed experts'.  Biased acts
+    (swiglu_clamp) have no shared-expert form."""
     _fault("moe_glu_gather_shexp_kq")
     _require_gpu(x, gate_w, up_w, shexp_gate_w, shexp_up_w, idx)
-    if act not in _ACTS:
-        raise ValueError(f"act {act!r} has no kernel epilogue; have {tuple(_ACTS)}")
+    if act == "swiglu_clamp":
+        raise ValueError("act 'swiglu_clamp' (biased experts) has no shared-expert form")
     K = x.shape[-1]
     t, k = idx.shape[0], idx.shape[-1]
     x2 = _rows_view(x)
@@ -433,17 +510,18 @@ def moe_glu_gather_shexp_kq(x, gate_w, up_w, shexp_gate_w, shexp_up_w, codec, id
     E, I = gate_w.shape[0], gate_w.shape[1]
     if sg.shape != su.shape or sg.shape[1] != I:
         raise ValueError(f"shared gate/up must both have {I} rows (the routed intermediate size)")
+    ep, _ = _epilogue(act, limit, alpha, None, None, E, I, x.device)
     h = torch.empty((t, k + 1, I), dtype=torch.float32, device=x.device)
     if t == 0:
         return h
     s = _stream(x)
     xd = _x_dt(x2)
     if k:
-        seg, order = moe_route(idx.reshape(t, k), E)
-        _gather_rows(x2.data_ptr(), xd, x2.stride(0), k, 0, gate_w, up_w, codec, _ACTS[act], seg, order, t * k, E,
+        seg, order = _routed(idx, E)
+        _gather_rows(x2.data_ptr(), xd, x2.stride(0), k, 0, gate_w, up_w, codec, ep, seg, order, t * k, E,
                      h.data_ptr(), DTYPE_F32, I, k, K, s)
     seg1, order1 = _one_expert_route(x.device, t)
-    _gather_rows(x2.data_ptr(), xd, x2.stride(0), 1, 0, sg, su, scodec, _ACTS[act], seg1, order1, t, 1,
+    _gather_rows(x2.data_ptr(), xd, x2.stride(0), 1, 0, sg, su, scodec, ep, seg1, order1, t, 1,
                  h.data_ptr() + k * I * 4, DTYPE_F32, (k + 1) * I, 0, K, s)
     return h
 
@@ -476,34 +554,72 @@ def gather_qmv_mix_kq(h, down_w, shexp_down_w, codec, idx, scores, shexp_kquant_
     hd = _x_dt(h)
     yp = torch.empty((t, k + 1, D), dtype=torch.float32, device=h.device)
     if k:
-        seg, order = moe_route(idx.reshape(t, k), E)
-        _gather_rows(h.data_ptr(), hd, I, 1, k, down_w, None, codec, 0, seg, order, t * k, E, yp.data_ptr(),
+        seg, order = _routed(idx, E)
+        _gather_rows(h.data_ptr(), hd, I, 1, k, down_w, None, codec, None, seg, order, t * k, E, yp.data_ptr(),
                      DTYPE_F32, D, k, I, s)
     seg1, order1 = _one_expert_route(h.device, t)
-    _gather_rows(h.data_ptr() + k * I * h.element_size(), hd, (k + 1) * I, 1, 0, sd, None, scodec, 0, seg1, order1,
-                 t, 1, yp.data_ptr() + k * D * 4, DTYPE_F32, (k + 1) * D, 0, I, s)
+    _gather_rows(h.data_ptr() + k * I * h.element_size(), hd, (k + 1) * I, 1, 0, sd, None, scodec, None, seg1,
+                 order1, t, 1, yp.data_ptr() + k * D * 4, DTYPE_F32, (k + 1) * D, 0, I, s)
     sc = scores.reshape(t, k + 1).to(torch.float32).contiguous()
     check("kq_moe_mix", lib().kq_moe_mix(yp.data_ptr(), sc.data_ptr(), t, k + 1, D, y.data_ptr(), _dt(out_dtype),
                                          s))
     return y
 
 
-def moe_router_topk(logits, k, norm_topk_prob=True):
-    """softmax(fp32) -> top-k (descending, ties to the lower expert id) ->
-    optional renormalisation (stock form gmlx/modules.py:754-760).
-    Returns (inds int32 (t, k), scores float32 (t, k))."""
+def _expert_vector(v, E, name, device):
+    if v is None:
+        return None, None
+    if not isinstance(v, torch.Tensor) or v.device != device or v.numel() != E:
+        raise ValueError(f"{name} must be a tensor of {E} values on the logits' device")
+    v = v.reshape(E)
+    if v.dtype not in _TORCH_DTYPE:
+        v = v.to(torch.float32)
+    return v.contiguous(), _dt(v.dtype if v.dtype in _TORCH_DTYPE else torch.float32)
+
+
+def moe_router_topk(logits, k, norm_topk_prob=True, shared_gate=True, per_expert_scale=None, bias=None,
+                    scoring="softmax", scale=1.0):
+    """kq.moe_router_topk, in fp32 on the device (one wave per token).
+
+    score_e = softmax over the routed logits / sigmoid / sqrt(softplus)
+    (`scoring`, gmlx/deepseek_v4_model.py:690-697); the k experts with the
+    largest score_e + bias[e] are picked (descending, ties to the lower id)
+    with their unbiased scores; weights = picks / (sum + 1e-20) when
+    `norm_topk_prob`, then times per_expert_scale[e] and `scale`
+    (gmlx/deepseek_v4_model.py:700-717, gmlx/modules.py:1029-1046).
+    shared_gate (the default, as gmlx/modules.py:750-752 calls it): the last
+    logit column is the shared expert's gate (router-cat rows,
+    gmlx/modules.py:300-312) and sigmoid(it) is appended as weight k (stock
+    form gmlx/modules.py:754-763).  Returns (inds int32 (..., k), weights
+    float32 (..., k + shared_gate))."""
     _fault("moe_router_topk")
     _require_gpu(logits)
-    E = logits.shape[-1]
-    l2 = logits.reshape(-1, E).contiguous()
+    if scoring not in _lib.SCORE_ID:
+        raise ValueError(f"scoring {scoring!r} not in {tuple(_lib.SCORE_ID)}")
+    C = logits.shape[-1]
+    sg = 1 if shared_gate else 0
+    E = C - sg
+    if E < 1 or not 1 <= k <= min(E, 32) or E > 1024:
+        raise ValueError(f"router of {E} experts, top-{k}: need 1 <= k <= min(E, 32), E <= 1024")
+    l2 = logits.reshape(-1, C)
+    if l2.dtype not in _TORCH_DTYPE:
+        l2 = l2.to(torch.float32)
+    if l2.stride(-1) != 1 or (l2.shape[0] > 1 and l2.stride(0) < C):
+        l2 = l2.contiguous()
     t = l2.shape[0]
+    b, bdt = _expert_vector(bias, E, "bias", logits.device)
+    pes, pdt = _expert_vector(per_expert_scale, E, "per_expert_scale", logits.device)
+    opts = _lib.RouterOptions(int(bool(norm_topk_prob)), sg, _lib.SCORE_ID[scoring], float(scale),
+                              None if b is None else b.data_ptr(), bdt or 0,
+                              None if pes is None else pes.data_ptr(), pdt or 0)
     inds = torch.empty((t, k), dtype=torch.int32, device=logits.device)
-    scores = torch.empty((t, k), dtype=torch.float32, device=logits.device)
+    scores = torch.empty((t, k + sg), dtype=torch.float32, device=logits.device)
     if t:
-        check("kq_moe_router_topk", lib().kq_moe_router_topk(l2.data_ptr(), _dt(l2.dtype), t, E, k,
-                                                             int(bool(norm_topk_prob)), inds.data_ptr(),
-                                                             scores.data_ptr(), _stream(logits)))
-    return inds.reshape(*logits.shape[:-1], k), scores.reshape(*logits.shape[:-1], k)
+        check("kq_moe_router_topk",
+              lib().kq_moe_router_topk(l2.data_ptr(), _dt(l2.dtype), l2.stride(0) if t > 1 else C, t, E, k,
+                                       ctypes.byref(opts), inds.data_ptr(), scores.data_ptr(), _stream(logits)))
+    lead = logits.shape[:-1]
+    return inds.reshape(*lead, k), scores.reshape(*lead, k + sg)
 
 
 # --------------------------------------------------------------- attention
@@ -606,32 +722,91 @@ def sdpa_decode_slabs(q, k_cache, v_cache, row_offsets, row_lens, n_kv_heads, sc
     return out
 
 
+def _device_starts(starts, B, device):
+    """Per-row starts as a device int32 [B] tensor (or None for all zeros)
+    without a host synchronisation: a device tensor is used as is (cast on
+    the device if need be); host sequences and CPU tensors are memoised by
+    value, so a decode loop that keeps its pads copies them once."""
+    if starts is None:
+        return None
+    if isinstance(starts, torch.Tensor) and starts.is_cuda:
+        st = starts.reshape(-1)
+        if st.dtype != torch.int32 or not st.is_contiguous():
+            st = st.to(torch.int32).contiguous()
+        if st.numel() != B:
+            raise ValueError(f"one start per row: got {st.numel()} for {B} rows")
+        return st
+    vals = [int(x) for x in (starts.tolist() if isinstance(starts, torch.Tensor) else starts)]
+    if len(vals) != B:
+        raise ValueError(f"one start per row: got {len(vals)} for {B} rows")
+    return _starts_table(device, vals)
+
+
+def _kv_padded(k, v, name):
+    """k / v [B, Hkv, L, D] as views with D contiguous elements per token,
+    shared strides and 16-byte alignment (copying only when needed)."""
+    if k.stride(3) != 1 or k.stride(2) != k.shape[3]:
+        k = k.contiguous()
+    if v.stride() != k.stride():
+        v = v.contiguous()
+        if v.stride() != k.stride():
+            k = k.contiguous()
+    if k.stride(0) % 8 or k.stride(1) % 8 or k.data_ptr() % 16 or v.data_ptr() % 16:
+        k, v = k.contiguous(), v.contiguous()
+        if k.data_ptr() % 16 or v.data_ptr() % 16:
+            raise ValueError(f"{name}: K/V must be 16-byte aligned")
+    return k, v
+
+
+def _sdpa_padded(q, k, v, st, scale):
+    """q (B, Hq, 1, D); k / v prepared by _kv_padded; st device int32 or None."""
+    B, Hq, _, D = q.shape
+    Hkv, L = k.shape[1], k.shape[2]
+    q3 = q.reshape(B, Hq, D).contiguous()
+    out = torch.empty_like(q3)
+    Lb = lib()
+    need = Lb.kq_sdpa_workspace_bytes(B, Hq, Hkv, D, L)
+    s = _stream(q)
+    ws = _WS.get("sdpa", q.device, s.value, need)
+    # the batch stride of a single row is never used: give it its packed value
+    bs = k.stride(0) if B > 1 else Hkv * k.stride(1)
+    rc = Lb.kq_sdpa_decode_gqa(q3.data_ptr(), k.data_ptr(), v.data_ptr(), bs, k.stride(1), L,
+                               None if st is None else st.data_ptr(), B, Hq, Hkv, D, float(scale), _dt(q.dtype),
+                               out.data_ptr(), ws.data_ptr(), ws.numel(), s)
+    check("kq_sdpa_decode_gqa", rc)
+    return out.reshape(B, Hq, 1, D)
+
+
 def sdpa_decode_gqa(q, k, v, scale, starts=None, k_scales=None, k_biases=None, v_scales=None, v_biases=None):
     """kq.sdpa_decode_gqa with per-row `starts` (gmlx/gemma4_batched_sdpa.py:
     210-226): q (B, Hq, 1, D), k/v (B, Hkv, L, D); row b attends keys
-    [starts[b], L).  `starts` may be a host sequence or an int tensor.
+    [starts[b], L).  `starts` may be an int device tensor (read by the
+    kernel: no host synchronisation, the reference's reason for passing
+    device starts, gmlx/quantized_sdpa_fix.py:37-45, 88-93), a CPU tensor
+    or a host sequence (memoised on the device by value).
 
     With k_scales / k_biases / v_scales / v_biases (the quantized-KV form,
     gmlx/quantized_sdpa_fix.py:170-182): k / v are an 8-bit affine cache,
     group 64 -- uint32 words of four values, lowest byte first (mlx's wire,
     (B, Hkv, L, D/4)) or uint8 (B, Hkv, L, D) -- and the scales / biases
     (B, Hkv, L, D/64) are in q's dtype; value = scale * q + bias."""
-    B = q.shape[0]
-    if starts is None:
-        pads = [0] * B
-    elif isinstance(starts, torch.Tensor):
-        pads = [int(x) for x in starts.tolist()]
-    else:
-        pads = [int(x) for x in starts]
     q8 = (k_scales, k_biases, v_scales, v_biases)
     if any(t is not None for t in q8):
         if any(t is None for t in q8):
             raise ValueError("sdpa_decode_gqa: quantized KV needs k_scales, k_biases, v_scales and v_biases")
-        return _sdpa_q8(q, k, v, q8, pads, scale)
-    out = ragged_decode_attention(q, k, v, pads, scale)
-    if out is None:
-        raise ValueError("sdpa_decode_gqa: unsupported shape/dtype for the ragged kernel")
-    return out
+        return _sdpa_q8(q, k, v, q8, starts, scale)
+    _fault("sdpa_decode_gqa")
+    _require_gpu(q, k, v)
+    if q.dim() != 4 or q.shape[2] != 1 or k.dim() != 4 or v.dim() != 4 or tuple(k.shape) != tuple(v.shape):
+        raise ValueError("sdpa_decode_gqa: q (B, Hq, 1, D), k / v (B, Hkv, L, D) of one shape")
+    B, Hq, _, D = q.shape
+    if q.dtype not in (torch.float16, torch.bfloat16) or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("sdpa_decode_gqa: q, k, v must share dtype float16 or bfloat16")
+    Hkv = k.shape[1]
+    if k.shape[0] != B or k.shape[3] != D or Hq % Hkv or Hq // Hkv > 16 or D not in _SDPA_HEAD_DIMS:
+        raise ValueError("sdpa_decode_gqa: unsupported shape for the decode kernels")
+    kk, vv = _kv_padded(k, v, "sdpa_decode_gqa")
+    return _sdpa_padded(q, kk, vv, _device_starts(starts, B, q.device), scale)
 
 
 def _q8_values(w, D, name):
@@ -668,7 +843,7 @@ def _q8_pair(w, sc, bi, D, dt, name):
     return w, sc, bi
 
 
-def _sdpa_q8(q, k, v, q8, pads, scale):
+def _sdpa_q8(q, k, v, q8, starts, scale):
     _fault("sdpa_decode_gqa")
     _require_gpu(q, k, v, *q8)
     if q.dim() != 4 or q.shape[2] != 1 or k.dim() != 4 or v.dim() != 4:
@@ -682,24 +857,25 @@ def _sdpa_q8(q, k, v, q8, pads, scale):
     if k8.shape != v8.shape or k8.stride() != v8.stride() or ks.stride() != vs.stride():
         k8, v8, ks, kb, vs, vb = (t.contiguous() for t in (k8, v8, ks, kb, vs, vb))
     Hkv, L = k8.shape[1], k8.shape[2]
-    if len(pads) != B or any(p < 0 or p >= max(L, 1) for p in pads):
-        raise ValueError("one start per row, each inside the cache")
-    if Hq % Hkv or Hq // Hkv > 16 or D not in (64, 128, 256):
+    if k8.shape[0] != B or Hq % Hkv or Hq // Hkv > 16 or D not in (64, 128, 256):
         raise ValueError("unsupported quantized-KV attention shape")
-    kv_off = [b * k8.stride(0) + p * k8.stride(2) for b, p in enumerate(pads)]
-    tabs = _row_tables(q.device, kv_off, [k8.stride(1)] * B, [L - p for p in pads])
+    st = _device_starts(starts, B, q.device)
     q3 = q.reshape(B, Hq, D).contiguous()
     out = torch.empty_like(q3)
     Lb = lib()
     need = Lb.kq_sdpa_workspace_bytes(B, Hq, Hkv, D, L)
     s = _stream(q)
     ws = _WS.get("sdpa", q.device, s.value, need)
-    rc = Lb.kq_sdpa_decode_ragged_q8(q3.data_ptr(), k8.data_ptr(), v8.data_ptr(), ks.data_ptr(), kb.data_ptr(),
-                                     vs.data_ptr(), vb.data_ptr(), tabs[0].data_ptr(), tabs[1].data_ptr(),
-                                     tabs[2].data_ptr(), B, Hq, Hkv, D, L, float(scale), _dt(dt), out.data_ptr(),
-                                     ws.data_ptr(), ws.numel(), s)
-    check("kq_sdpa_decode_ragged_q8", rc)
+    sc = (ctypes.c_void_p * 4)(ks.data_ptr(), kb.data_ptr(), vs.data_ptr(), vb.data_ptr())
+    bs = k8.stride(0) if B > 1 else Hkv * k8.stride(1)
+    rc = Lb.kq_sdpa_decode_gqa_q8(q3.data_ptr(), k8.data_ptr(), v8.data_ptr(), ctypes.cast(sc, ctypes.c_void_p), bs,
+                                  k8.stride(1), L, None if st is None else st.data_ptr(), B, Hq, Hkv, D, float(scale),
+                                  _dt(dt), out.data_ptr(), ws.data_ptr(), ws.numel(), s)
+    check("kq_sdpa_decode_gqa_q8", rc)
     return out.reshape(B, Hq, 1, D)
+
+
+_SDPA_HEAD_DIMS = (64, 96, 128, 256)
 
 
 def ragged_decode_attention(queries, keys, values, pads, scale):
@@ -709,7 +885,9 @@ def ragged_decode_attention(queries, keys, values, pads, scale):
     are [pads[b], L).  Declines (returns None) exactly where the reference's
     guard rails do (:412-431): non-4-D inputs, S != 1, dtype other than
     float16/bfloat16 or mismatched, len(pads) != B, negative pads,
-    Hq % Hkv != 0, D != V, D not in (64, 96, 128, 256), pad >= L."""
+    Hq % Hkv != 0, D != V, D not in (64, 96, 128, 256), pad >= L.  The pads
+    become device starts memoised by value, so the decode steps L, L + 1, ...
+    of one batch copy nothing and build no tables."""
     if any(not isinstance(t, torch.Tensor) for t in (queries, keys, values)):
         return None
     if (queries.dim() != 4 or keys.dim() != 4 or values.dim() != 4 or queries.shape[2] != 1
@@ -722,24 +900,15 @@ def ragged_decode_attention(queries, keys, values, pads, scale):
         return None
     Hkv, L = keys.shape[1], keys.shape[2]
     Dv = values.shape[-1]
-    if Hq % Hkv != 0 or D != Dv or D not in (64, 96, 128, 256) or any(p >= L for p in pads):
+    if Hq % Hkv != 0 or D != Dv or D not in _SDPA_HEAD_DIMS or any(p >= L for p in pads):
         return None
-    if Hq // Hkv > 16 or tuple(values.shape) != tuple(keys.shape):
+    if Hq // Hkv > 16 or tuple(values.shape) != tuple(keys.shape) or keys.shape[0] != B:
         return None
     _fault("ragged_decode_attention")
     _require_gpu(queries, keys, values)
-    k = keys if keys.stride(3) == 1 and keys.stride(2) == D else keys.contiguous()
-    v = values if values.stride() == k.stride() else values.contiguous()
-    if v.stride() != k.stride():
-        k, v = k.contiguous(), v.contiguous()
-    kv_off = [b * k.stride(0) + p * D for b, p in enumerate(pads)]
-    hstride = [k.stride(1)] * B
-    lens = [L - p for p in pads]
-    tabs = _row_tables(queries.device, kv_off, hstride, lens)
-    q3 = queries.reshape(B, Hq, D).contiguous()
-    out = torch.empty_like(q3)
-    _sdpa_launch(q3, k, v, tabs, Hkv, scale, L, out)
-    return out.reshape(B, Hq, 1, D)
+    k, v = _kv_padded(keys, values, "ragged_decode_attention")
+    st = None if not any(pads) else _starts_table(queries.device, pads)
+    return _sdpa_padded(queries, k, v, st, scale)
 
 
 _STARTS = OrderedDict()  # memoised device starts rows for host sequences

@@ -160,6 +160,31 @@ int kq_moe_glu_gather(const void *x, int x_dtype, int64_t x_row_stride, int32_t 
                       const int32_t *seg_info, const int32_t *pair_order, int32_t n_pairs,
                       int32_t n_experts, float *h, kq_stream_t stream);
 
+/* GLU activations of the fused gathers (the act= strings of
+ * gmlx/modules.py:263-291, 557-566). */
+enum {
+    KQ_ACT_SILU = 0,        /* silu(g) * u */
+    KQ_ACT_GELU = 1,        /* gelu_tanh(g) * u */
+    KQ_ACT_SILU_LIMIT = 2,  /* silu(min(g, limit)) * clip(u, -limit, limit)
+                               (gmlx/deepseek_v4_model.py:740-744) */
+    KQ_ACT_SWIGLU_CLAMP = 3 /* g' = min(g + gate_bias, limit),
+                               u' = clip(u + up_bias, -limit, limit):
+                               (u' + 1) * g' * sigmoid(alpha * g')
+                               (gmlx/minimax_m3_model.py:134-138) */
+};
+
+/* Epilogue of kq_moe_gather_rows, all in fp32.  Fused GLU (w1 != NULL): act
+ * with limit / alpha, bias0 / bias1 the gate / up biases of swiglu_clamp.
+ * Plain gather (w1 == NULL): bias0 is added to the output (the bias= of
+ * kq.gather_qmv_kq, gmlx/modules.py:595-597).  Biases are fp32 rows of N
+ * values per expert, bias_expert_stride elements apart; NULL for none. */
+typedef struct {
+    int32_t act;
+    float limit, alpha;
+    const float *bias0, *bias1;
+    int64_t bias_expert_stride;
+} kq_gather_epilogue;
+
 /* The general form of the two gathers above, for pair rows laid out with a
  * spare row every few pairs: kq.moe_glu_gather_shexp_kq(x, gate_w, up_w,
  * shexp_gate_w, shexp_up_w, codec, idx, act=) and kq.gather_qmv_mix_kq(h,
@@ -167,15 +192,15 @@ int kq_moe_glu_gather(const void *x, int x_dtype, int64_t x_row_stride, int32_t 
  * 777-787) keep the shared expert in slot k of [t, k + 1, N] blocks.
  * Pair p reads x row p / x_pair_div + p / x_skip and writes y row
  * p + p / y_skip (a skip of 0 adds nothing).  w1 == NULL: plain gather
- * (y of y_dtype); w1 != NULL: fused GLU with act as in kq_moe_glu_gather
- * (y fp32).  The shared expert itself is a one-expert gather (n_experts 1,
- * every pair routed to it). */
+ * (y of y_dtype); w1 != NULL: fused GLU (y fp32).  ep == NULL means silu
+ * and no biases.  The shared expert itself is a one-expert gather
+ * (n_experts 1, every pair routed to it). */
 int kq_moe_gather_rows(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pair_div,
                        int32_t x_skip, const void *w0, const void *w1, int64_t w_expert_bytes,
-                       int64_t w_row_bytes, int32_t N, int32_t K, int codec, int act,
-                       const int32_t *seg_info, const int32_t *pair_order, int32_t n_pairs,
-                       int32_t n_experts, void *y, int y_dtype, int64_t y_row_stride,
-                       int32_t y_skip, kq_stream_t stream);
+                       int64_t w_row_bytes, int32_t N, int32_t K, int codec,
+                       const kq_gather_epilogue *ep, const int32_t *seg_info,
+                       const int32_t *pair_order, int32_t n_pairs, int32_t n_experts, void *y,
+                       int y_dtype, int64_t y_row_stride, int32_t y_skip, kq_stream_t stream);
 
 /* The routing mix of kq.gather_qmv_mix_ns_kq (gmlx/modules.py:591-593):
  * y[t, :] = sum_s scores[t, s] * y_pairs[t*k + s, :], fp32, slots summed in
@@ -183,12 +208,40 @@ int kq_moe_gather_rows(const void *x, int x_dtype, int64_t x_row_stride, int32_t
 int kq_moe_mix(const float *y_pairs, const float *scores, int32_t T, int32_t top_k, int32_t N,
                void *y, int y_dtype, kq_stream_t stream);
 
-/* kq.moe_router_topk(logits, k, norm_topk_prob) (gmlx/modules.py:750-752),
- * stock form gmlx/modules.py:754-760: softmax in fp32 -> top-k (descending,
- * ties to the lower expert id) -> optional renormalisation.  logits [T, E] of
- * logits_dtype; inds int32 [T, k]; scores fp32 [T, k].  E <= 1024, k <= 32. */
-int kq_moe_router_topk(const void *logits, int logits_dtype, int32_t T, int32_t E, int32_t k,
-                       int norm_topk_prob, int32_t *inds, float *scores, kq_stream_t stream);
+/* Scoring functions of the router (gmlx/deepseek_v4_model.py:690-697). */
+enum { KQ_SCORE_SOFTMAX = 0, KQ_SCORE_SIGMOID = 1, KQ_SCORE_SQRTSOFTPLUS = 2 };
+
+/* Keywords of kq.moe_router_topk(logits, k, norm_topk_prob, shared_gate=,
+ * per_expert_scale=, bias=, scoring=, scale=). */
+typedef struct {
+    int32_t norm_topk_prob;   /* divide the k picked scores by their sum (+1e-20) */
+    int32_t shared_gate;      /* logits carry one more column, the shared expert's gate */
+    int32_t scoring;          /* KQ_SCORE_* */
+    float scale;              /* routed scaling factor applied to every pick */
+    const void *bias;         /* [E] selection-only bias (e_score_correction_bias), or NULL */
+    int32_t bias_dtype;
+    const void *per_expert_scale; /* [E] multiplies pick e's weight, or NULL */
+    int32_t per_expert_scale_dtype;
+} kq_router_options;
+
+/* kq.moe_router_topk (gmlx/modules.py:750-752, 1043-1046, 1208-1211;
+ * gmlx/deepseek_v4_model.py:1179-1187), in fp32, per token:
+ *   score_e  = softmax over the E routed logits, sigmoid(logit), or
+ *              sqrt(softplus(logit));
+ *   picks    = the k experts with the largest score_e + bias[e] (descending,
+ *              ties to the lower expert id), weighted by their score_e;
+ *   weights  = picks / (sum of picks + 1e-20) when norm_topk_prob, then
+ *              times per_expert_scale[e] and scale;
+ *   shared_gate: logits [T, E + 1] whose last column is the shared expert's
+ *              gate logit (the router-cat rows of gmlx/modules.py:300-312);
+ *              sigmoid(it) is appended as weight k (the stock form
+ *              gmlx/modules.py:754-763).
+ * logits rows logits_row_stride elements apart (>= E + shared_gate); inds
+ * int32 [T, k]; scores fp32 [T, k + shared_gate].  E <= 1024, k <= 32,
+ * k <= E.  opts == NULL: softmax, renormalised, no shared gate, scale 1. */
+int kq_moe_router_topk(const void *logits, int logits_dtype, int64_t logits_row_stride, int32_t T,
+                       int32_t E, int32_t k, const kq_router_options *opts, int32_t *inds,
+                       float *scores, kq_stream_t stream);
 
 /* ---- ragged GQA decode attention ----------------------------------------- */
 /* Workspace of kq_sdpa_decode_ragged: fp32 split partials (O, m, l) for
@@ -229,6 +282,30 @@ int kq_sdpa_decode_ragged_q8(const void *q, const void *k, const void *v, const 
                              const int32_t *row_len, int32_t B, int32_t Hq, int32_t Hkv,
                              int32_t D, int32_t max_len, float scale, int dtype, void *out,
                              void *workspace, size_t workspace_bytes, kq_stream_t stream);
+
+/* kq.sdpa_decode_gqa(q, k, v, scale, starts=) on the reference's padded
+ * cache layout (gmlx/gemma4_batched_sdpa.py:210-226, the ragged route of
+ * gmlx/qwen35_attn.py:395-493 with pads as starts): k / v [B, Hkv, L, D]
+ * with D contiguous elements per token, batch_stride / head_stride elements
+ * apart (multiples of 8); row b attends keys [starts[b], L) (starts: device
+ * int32 [B], read on the device and clamped to [0, L]; NULL means 0).  No
+ * per-row tables and no host synchronisation: a decode loop passes the same
+ * starts at every L.  Same outputs, dtypes, head dims and workspace
+ * (kq_sdpa_workspace_bytes(B, Hq, Hkv, D, L)) as kq_sdpa_decode_ragged. */
+int kq_sdpa_decode_gqa(const void *q, const void *k, const void *v, int64_t batch_stride,
+                       int64_t head_stride, int32_t L, const int32_t *starts, int32_t B, int32_t Hq,
+                       int32_t Hkv, int32_t D, float scale, int dtype, void *out, void *workspace,
+                       size_t workspace_bytes, kq_stream_t stream);
+
+/* The 8-bit affine form of kq_sdpa_decode_gqa (k_scales=, k_biases=,
+ * v_scales=, v_biases=, gmlx/quantized_sdpa_fix.py:76-93, 170-182): k / v
+ * uint8 [B, Hkv, L, D] with byte strides (multiples of 64), kv_scales =
+ * {k_scales, k_biases, v_scales, v_biases} laid out as
+ * kq_sdpa_decode_ragged_q8 describes (index = byte offset / 64). */
+int kq_sdpa_decode_gqa_q8(const void *q, const void *k, const void *v, const void *const *kv_scales,
+                          int64_t batch_stride, int64_t head_stride, int32_t L, const int32_t *starts,
+                          int32_t B, int32_t Hq, int32_t Hkv, int32_t D, float scale, int dtype,
+                          void *out, void *workspace, size_t workspace_bytes, kq_stream_t stream);
 
 /* ---- cascade (shared-prefix) decode attention ---------------------------- */
 /* kq.sdpa_decode_gqa_cascade(q, k_shared, v_shared, k_priv, v_priv, scale,

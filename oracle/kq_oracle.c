@@ -16,7 +16,7 @@
  *     (make_qkx2_quants / make_qx_quants search).  kq.quantize call sites:
  *     tests/test_dequant_unattachable.py:36, gmlx/mtp_load.py:290.
  *     mlx-kquant's own quantizer choices are NOT pinned (no import possible).
- *   - quantization (IQ2_XXS): this build's own exhaustive-grid search; it
+ *   - quantization (IQ2_XXS): this build's own nearest-lattice search; it
  *     produces valid blocks but is not llama.cpp's iq2xs_init_impl search.
  *   - an OpenMP fp32 dequant-fused GEMM and a ragged decode attention used
  *     only as the reported CPU baseline (the reference's CPU path, MLX CPU /
@@ -417,13 +417,51 @@ void kqo_dequant_iq2_xxs(const uint8_t *wire, int64_t nblocks, float *out) {
     }
 }
 
-/* This build's own IQ2_XXS quantizer: per 32-value group, fold the signs
- * (even parity enforced by flipping the smallest-magnitude element), then for
- * every 4-bit group scale choose each 8-value sub-group's grid point by
- * exhaustive least squares over the 256-entry grid, and keep the
- * scale with the smallest error.  The block scale d is set from the largest
- * per-group optimum.  Produces valid blocks; the search is not llama.cpp's. */
+/* This build's own IQ2_XXS quantizer (the GPU kernel quant_iq2xxs_kernel
+ * runs the same operations in the same order):
+ *   d = fp16(amax / (43 * 15.5 * 0.25)) per block;
+ *   per 32-value group and 8-value sub-group: signs folded so that an even
+ *   number are negative (the smallest magnitude gives way), the 7-bit sign
+ *   index kept, values multiplied by their folded sign;
+ *   per scale field s (db = d (0.5 + s) / 4): every folded value takes the
+ *   nearest grid level (8, 25, 43: below 16.5 db level 0, below 34 db level
+ *   1, else 2), the sub-group's lattice point u = sum l_j 3^j maps to the
+ *   grid entry nearest in level values (integer squared distance, ties to
+ *   the lower entry), and the squared error of the 32 values is summed;
+ *   the least error wins (ties to the lower s). */
+static uint8_t iq2_near[6561];
+static int iq2_near_ready = 0;
+
+static void iq2_build_near(void) {
+    static const int val[3] = {8, 25, 43};
+    for (int u = 0; u < 6561; ++u) {
+        int lv[8];
+        for (int j = 0, r = u; j < 8; ++j, r /= 3) lv[j] = r % 3;
+        int best = 0x7FFFFFFF, bk = 0;
+        for (int k = 0; k < 256; ++k) {
+            const uint64_t gv = KQO_IQ2XXS_GRID[k];
+            int dsum = 0;
+            for (int j = 0; j < 8; ++j) {
+                const int dd = val[lv[j]] - (int)((gv >> (8 * j)) & 0xFF);
+                dsum += dd * dd;
+            }
+            if (dsum < best) {
+                best = dsum;
+                bk = k;
+            }
+        }
+        iq2_near[u] = (uint8_t)bk;
+    }
+    iq2_near_ready = 1;
+}
+
+const uint8_t *kqo_iq2_near_table(void) {
+    if (!iq2_near_ready) iq2_build_near();
+    return iq2_near;
+}
+
 void kqo_quantize_iq2_xxs(const float *xin, int64_t nblocks, uint8_t *wire) {
+    const uint8_t *near = kqo_iq2_near_table();
     for (int64_t b = 0; b < nblocks; ++b) {
         const float *x = xin + b * QK_K;
         uint8_t *blk = wire + b * 66;
@@ -441,9 +479,7 @@ void kqo_quantize_iq2_xxs(const float *xin, int64_t nblocks, uint8_t *wire) {
             const float *xg = x + 32 * g;
             float folded[32], wt[32];
             uint32_t sign_idx[4];
-            for (int i = 0; i < 32; ++i) {
-                                wt[i] = fabsf(xg[i]); /* sign-flip cost; the fit itself is unweighted */
-            }
+            for (int i = 0; i < 32; ++i) wt[i] = fabsf(xg[i]); /* sign-flip cost */
             for (int l = 0; l < 4; ++l) {
                 uint32_t s = 0;
                 int nneg = 0, jmin = 0;
@@ -458,35 +494,31 @@ void kqo_quantize_iq2_xxs(const float *xin, int64_t nblocks, uint8_t *wire) {
                 sign_idx[l] = s & 127u;
                 /* the folded sign of element 7 is implied by parity */
                 const uint8_t full = iq2_signs(sign_idx[l]);
-                for (int j = 0; j < 8; ++j) {
-                    const float v = (full >> j) & 1 ? -xg[8 * l + j] : xg[8 * l + j];
-                    folded[8 * l + j] = v; /* value after sign folding */
-                }
+                for (int j = 0; j < 8; ++j) folded[8 * l + j] = (full >> j) & 1 ? -xg[8 * l + j] : xg[8 * l + j];
             }
             float best_err = INFINITY;
             uint32_t best_s = 0, best_idx = 0;
             for (uint32_t sfield = 0; sfield < 16; ++sfield) {
                 const float db = d * (0.5f + (float)sfield) * 0.25f;
+                const float t01 = db * 16.5f, t12 = db * 34.f;
                 float err_tot = 0;
                 uint32_t idx_word = 0;
                 for (int l = 0; l < 4; ++l) {
-                    float be = INFINITY;
-                    int bk = 0;
-                    for (int k = 0; k < 256; ++k) {
-                        const uint64_t gv = KQO_IQ2XXS_GRID[k];
-                        float e = 0;
-                        for (int j = 0; j < 8; ++j) {
-                            const float q = db * (float)((gv >> (8 * j)) & 0xFF);
-                            const float diff = q - folded[8 * l + j];
-                            e += diff * diff;
-                        }
-                        if (e < be) {
-                            be = e;
-                            bk = k;
-                        }
+                    int u = 0;
+                    for (int j = 7; j >= 0; --j) {
+                        const float f = folded[8 * l + j];
+                        u = 3 * u + (f < t01 ? 0 : (f < t12 ? 1 : 2));
                     }
-                    err_tot += be;
-                    idx_word |= (uint32_t)bk << (8 * l);
+                    const uint32_t k = near[u];
+                    const uint64_t gv = KQO_IQ2XXS_GRID[k];
+                    float e = 0;
+                    for (int j = 0; j < 8; ++j) {
+                        const float q = db * (float)((gv >> (8 * j)) & 0xFF);
+                        const float diff = q - folded[8 * l + j];
+                        e += diff * diff;
+                    }
+                    err_tot += e;
+                    idx_word |= k << (8 * l);
                 }
                 if (err_tot < best_err) {
                     best_err = err_tot;

@@ -114,15 +114,55 @@ def test_pads_are_honored():
     assert torch.equal(clean.cpu(), dirty.cpu())
 
 
-def test_sdpa_decode_gqa_starts():
+@pytest.mark.parametrize("starts_kind", ["device", "host", "cpu_tensor", "none"])
+def test_sdpa_decode_gqa_starts(starts_kind):
+    """kq.sdpa_decode_gqa(starts=) (gmlx/gemma4_batched_sdpa.py:210-226)
+    against the fp64 per-row reference over keys [starts[b], L)."""
     import torch
     from gmlx_amd import ops
     rng = np.random.default_rng(3)
-    q, k, v = _padded(rng, 2, 8, 1, 640, 64, torch.float16)
-    starts = torch.tensor([0, 100], dtype=torch.int32)
-    got = ops.sdpa_decode_gqa(q.cuda(), k.cuda(), v.cuda(), 0.125, starts=starts)
-    ref = ops.ragged_decode_attention(q.cuda(), k.cuda(), v.cuda(), [0, 100], 0.125)
-    assert torch.equal(got.cpu(), ref.cpu())
+    B, Hq, Hkv, L, D = 4, 8, 1, 640, 64
+    q, k, v = _padded(rng, B, Hq, Hkv, L, D, torch.float16)
+    st = [0, 100, 639, 7] if starts_kind != "none" else [0] * B
+    arg = {"device": torch.tensor(st, dtype=torch.int32).cuda(), "host": st,
+           "cpu_tensor": torch.tensor(st, dtype=torch.int64), "none": None}[starts_kind]
+    got = ops.sdpa_decode_gqa(q.cuda(), k.cuda(), v.cuda(), 0.125, starts=arg)
+    qf, kf, vf = q.float().numpy(), k.float().numpy(), v.float().numpy()
+    ref = np.stack([attention_ref(qf[b, :, 0], kf[b, :, st[b]:], vf[b, :, st[b]:], 0.125) for b in range(B)])
+    assert okq.max_rel(got.float().cpu().numpy()[:, :, 0], ref) <= TOL
+
+
+def test_decode_steps_sync_free_and_table_free():
+    """A decode loop (keys L, L + 1, L + 2 with the same pads / device starts)
+    makes no host synchronisation and builds no new device tables: the
+    reference passes device starts for exactly this (gmlx/quantized_sdpa_fix.py:
+    37-45, 88-93) and memoises pads per batch (gmlx/cascade_sdpa.py:79-105)."""
+    import torch
+    from gmlx_amd import ops
+    rng = np.random.default_rng(8)
+    B, Hq, Hkv, Lmax, D = 3, 16, 4, 2100, 128
+    q, k, v = _padded(rng, B, Hq, Hkv, Lmax, D, torch.float16)
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    pads = [5, 0, 1024]
+    dev_starts = torch.tensor(pads, dtype=torch.int32, device="cuda")
+    ops.ragged_decode_attention(qd, kd[:, :, :2000], vd[:, :, :2000], pads, D ** -0.5)  # first sight of the pads
+    torch.cuda.synchronize()
+    n_tables = len(ops._STARTS)
+    outs = []
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        for L in (2001, 2002, 2003):
+            outs.append(ops.ragged_decode_attention(qd, kd[:, :, :L], vd[:, :, :L], pads, D ** -0.5))
+            outs.append(ops.sdpa_decode_gqa(qd, kd[:, :, :L], vd[:, :, :L], D ** -0.5, starts=dev_starts))
+    finally:
+        torch.cuda.set_sync_debug_mode(0)
+    assert len(ops._STARTS) == n_tables
+    qf, kf, vf = q.float().numpy(), k.float().numpy(), v.float().numpy()
+    for i, L in enumerate((2001, 2002, 2003)):
+        ref = np.stack([attention_ref(qf[b, :, 0], kf[b, :, pads[b]:L], vf[b, :, pads[b]:L], D ** -0.5)
+                        for b in range(B)])
+        for o in outs[2 * i:2 * i + 2]:
+            assert okq.max_rel(o.float().cpu().numpy()[:, :, 0], ref) <= TOL
 
 
 @pytest.mark.parametrize("D,Hq,Hkv,dtype_name", [(128, 32, 8, "float16"), (64, 8, 8, "float16"),

@@ -88,7 +88,7 @@ def test_moe_glu_then_down_then_mix(act):
     dw = _experts(rng, "q6_k", E, D, I)
     x = fp16_rows(rng, T, D)
     logits = rng.normal(0, 1, size=(T, E)).astype(np.float32)
-    inds, scores = ops.moe_router_topk(_dev(logits), k, True)
+    inds, scores = ops.moe_router_topk(_dev(logits), k, True, shared_gate=False)
     idx = inds.cpu().numpy()
     sc = scores.cpu().numpy()
     h = ops.moe_glu_gather_kq(_dev(x), _dev(gw), _dev(uw), "q4_k", inds, act=act)
@@ -122,7 +122,7 @@ def test_router_topk_matches_numpy():
     rng = np.random.default_rng(4)
     for E, k, norm in [(128, 8, True), (256, 8, False), (60, 4, True)]:
         logits = rng.normal(0, 1, size=(17, E)).astype(np.float32)
-        inds, scores = ops.moe_router_topk(_dev(logits), k, norm)
+        inds, scores = ops.moe_router_topk(_dev(logits), k, norm, shared_gate=False)
         p = np.exp(logits - logits.max(-1, keepdims=True))
         p /= p.sum(-1, keepdims=True)
         order = np.argsort(-p, axis=-1, kind="stable")[:, :k]
@@ -222,3 +222,110 @@ def test_glu_gather_long_rows_both_forms(codec, wave_nb, monkeypatch):
     href = np.stack([[silu(g_deq[idx[t, s]] @ xf[t]) * (u_deq[idx[t, s]] @ xf[t]) for s in range(k)]
                      for t in range(T)])
     assert okq.max_rel(h.cpu().numpy(), href) <= TOL
+
+
+ROUTER_CASES = [
+    # (E, k, norm, shared_gate, scoring, bias, per_expert_scale, scale, logits dtype)
+    (128, 8, True, True, "softmax", False, False, 1.0, "float32"),     # gmlx/modules.py:750-752
+    (64, 4, False, True, "softmax", False, False, 1.0, "bfloat16"),
+    (256, 8, True, False, "sqrtsoftplus", True, False, 2.5, "float32"),  # deepseek_v4_model.py:1179-1187
+    (128, 8, True, False, "softmax", False, True, 1.0, "bfloat16"),    # gemma4, modules.py:1043-1046
+    (60, 6, True, False, "sigmoid", True, True, 1.5, "float16"),
+    (1024, 32, False, False, "softmax", False, False, 1.0, "float32"),
+]
+
+
+@pytest.mark.parametrize("E,k,norm,sg,scoring,use_bias,use_pes,scale,ldt", ROUTER_CASES)
+def test_router_options_match_oracle(E, k, norm, sg, scoring, use_bias, use_pes, scale, ldt):
+    """moe_router_topk's keywords against the fp64 stock forms
+    (oracle/moe.py): picks exactly, weights within fp32 rounding."""
+    import torch
+    from gmlx_amd import ops
+    from oracle import moe as omoe
+    rng = np.random.default_rng(E + k)
+    T = 19
+    tdt = getattr(torch, ldt)
+    logits = torch.from_numpy(rng.normal(0, 1.5, size=(T, E + sg)).astype(np.float32)).to(tdt)
+    bias = torch.from_numpy(rng.normal(0, 0.3, size=E).astype(np.float32)) if use_bias else None
+    pes = torch.from_numpy(rng.uniform(0.5, 2.0, size=E).astype(np.float32)).to(torch.bfloat16) if use_pes else None
+    inds, w = ops.moe_router_topk(logits.cuda(), k, norm, shared_gate=sg, scoring=scoring, scale=scale,
+                                  bias=None if bias is None else bias.cuda(),
+                                  per_expert_scale=None if pes is None else pes.cuda())
+    assert tuple(inds.shape) == (T, k) and tuple(w.shape) == (T, k + sg)
+    ri, rw = omoe.router_topk(logits.float().numpy(), k, norm, shared_gate=sg, scoring=scoring, scale=scale,
+                              bias=None if bias is None else bias.numpy(),
+                              per_expert_scale=None if pes is None else pes.float().numpy())
+    assert np.array_equal(inds.cpu().numpy(), ri)
+    assert np.allclose(w.cpu().numpy(), rw, rtol=3e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("act,limit", [("silu_limit", 0.3), ("swiglu_clamp", 0.6), ("silu_limit", 1e4)])
+def test_glu_limit_acts_and_biases(act, limit):
+    """silu_limit (gmlx/deepseek_v4_model.py:740-744) and the clamped,
+    biased SwiGLU (gmlx/minimax_m3_model.py:134-138) epilogues, a limit small
+    enough that the clamps bite, then the down gather with its output bias
+    (gather_qmv_kq(bias=), gmlx/modules.py:595-597), against fp64."""
+    import torch
+    from gmlx_amd import ops
+    from oracle import moe as omoe
+    rng = np.random.default_rng(11)
+    E, D, I, T, k = 8, 512, 96, 6, 3
+    gw, uw = _experts(rng, "q4_k", E, I, D), _experts(rng, "q4_k", E, I, D)
+    dw = _experts(rng, "q6_k", E, D, 256)  # the down projection below runs on a 256-wide h
+    x = fp16_rows(rng, T, D)
+    idx = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    kw = {"limit": limit}
+    gb = ub = None
+    if act == "swiglu_clamp":
+        gb = rng.normal(0, 0.2, size=(E, I)).astype(np.float32)
+        ub = rng.normal(0, 0.2, size=(E, I)).astype(np.float32)
+        kw.update(alpha=1.702, gate_bias=_dev(gb), up_bias=_dev(ub))
+    h = ops.moe_glu_gather_kq(_dev(x), _dev(gw), _dev(uw), "q4_k", _dev(idx), act=act, **kw)
+    G = okq.dequantize(gw, "q4_k").astype(np.float64)
+    U = okq.dequantize(uw, "q4_k").astype(np.float64)
+    xf = x.astype(np.float64)
+    href = np.stack([[omoe.glu(G[e] @ xf[t], U[e] @ xf[t], act, limit=limit, alpha=1.702,
+                               gate_bias=None if gb is None else gb[e], up_bias=None if ub is None else ub[e])
+                      for e in idx[t]] for t in range(T)])
+    assert okq.max_rel(h.cpu().numpy(), href) <= TOL
+    if limit < 1:  # the clamps were reached (the limit is small: max|ref| shrinks with it, while the
+        # products keep their fp16-weight rounding, so a tighter limit only inflates max-rel)
+        g_all = np.stack([[G[e] @ xf[t] for e in idx[t]] for t in range(T)])
+        assert (np.abs(g_all) > limit).mean() > 0.05
+    # down projection on a 256-wide h (whole Q6_K blocks) with an output bias
+    h2 = torch.from_numpy(rng.normal(0, 1, size=(T, k, 256)).astype(np.float32)).cuda()
+    db = rng.normal(0, 0.5, size=(E, D)).astype(np.float32)
+    y = ops.gather_qmv_kq(h2, _dev(dw), "q6_k", _dev(idx), bias=_dev(db))
+    Dn = okq.dequantize(dw, "q6_k").astype(np.float64)
+    hh = h2.cpu().numpy().astype(np.float64)
+    yref = np.stack([[Dn[e] @ hh[t, s] + db[e] for s, e in enumerate(idx[t])] for t in range(T)])
+    assert okq.max_rel(y.cpu().numpy(), yref) <= TOL
+
+
+def test_route_reused_once_then_recomputed():
+    """A GLU gather leaves its routing for the down gather over the same idx;
+    an in-place change of idx (a new version) routes afresh."""
+    from gmlx_amd import ops
+    rng = np.random.default_rng(12)
+    E, D, I, T, k = 10, 256, 256, 4, 2
+    gw, uw = _experts(rng, "q4_k", E, I, D), _experts(rng, "q4_k", E, I, D)
+    dw = _experts(rng, "q4_k", E, D, I)
+    x = fp16_rows(rng, T, D)
+    idx_np = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    idx = _dev(idx_np)
+    G, U, Dn = (okq.dequantize(w, "q4_k").astype(np.float64) for w in (gw, uw, dw))
+    xf = x.astype(np.float64)
+    for step in range(3):
+        if step:
+            idx_np = (idx_np + 3) % E
+            idx.copy_(_dev(idx_np))            # in place: bumps the version counter
+        h = ops.moe_glu_gather_kq(_dev(x), _dev(gw), _dev(uw), "q4_k", idx)
+        y = ops.gather_qmv_kq(h, _dev(dw), "q4_k", idx)
+        href = np.stack([[omoe_silu(G[e] @ xf[t]) * (U[e] @ xf[t]) for e in idx_np[t]] for t in range(T)])
+        yref = np.stack([[Dn[e] @ href[t, s] for s, e in enumerate(idx_np[t])] for t in range(T)])
+        assert okq.max_rel(h.cpu().numpy(), href) <= TOL
+        assert okq.max_rel(y.cpu().numpy(), yref) <= TOL
+
+
+def omoe_silu(z):
+    return z / (1 + np.exp(-z))

@@ -87,7 +87,19 @@ def test_host_validation_rejects_before_launch():
                                    1 << 20, None) == _lib.KQ_ERR_BAD_SHAPE
     assert L.kq_sdpa_decode_ragged(16, 16, 16, 16, 16, 16, 2, 8, 2, 128, 100, 0.1, _lib.DTYPE_F16, 16, 16,
                                    16, None) == _lib.KQ_ERR_WORKSPACE_TOO_SMALL
-    assert L.kq_moe_router_topk(16, 0, 4, 2000, 8, 1, 16, 16, None) == _lib.KQ_ERR_BAD_SHAPE
+    assert L.kq_moe_router_topk(16, 0, 2000, 4, 2000, 8, None, 16, 16, None) == _lib.KQ_ERR_BAD_SHAPE
+    # the shared gate needs one more logit column than the routed experts
+    opts = _lib.RouterOptions(1, 1, 0, 1.0, None, 0, None, 0)
+    assert L.kq_moe_router_topk(16, 0, 64, 4, 64, 8, ctypes.byref(opts), 16, 16, None) == _lib.KQ_ERR_BAD_SHAPE
+    opts = _lib.RouterOptions(1, 0, 7, 1.0, None, 0, None, 0)
+    assert L.kq_moe_router_topk(16, 0, 64, 4, 64, 8, ctypes.byref(opts), 16, 16, None) == _lib.KQ_ERR_BAD_ARGUMENT
+    # swiglu_clamp needs a positive limit; a plain gather takes no up bias
+    ep = _lib.GatherEpilogue(3, 0.0, 1.702, None, None, 0)
+    assert L.kq_moe_gather_rows(16, 1, 256, 1, 0, 16, 16, 144 * 16, 144, 16, 256, 12, ctypes.byref(ep), 16, 16,
+                                4, 2, 16, 0, 16, 0, None) == _lib.KQ_ERR_BAD_ARGUMENT
+    ep = _lib.GatherEpilogue(0, 0.0, 0.0, 16, 16, 16)
+    assert L.kq_moe_gather_rows(16, 1, 256, 1, 0, 16, None, 144 * 16, 144, 16, 256, 12, ctypes.byref(ep), 16, 16,
+                                4, 2, 16, 1, 16, 0, None) == _lib.KQ_ERR_BAD_ARGUMENT
     assert L.kq_dequantize(16, 4, 99, 16, 0, None) == _lib.KQ_ERR_UNSUPPORTED_CODEC
     assert L.kq_quantize(16, 2, 100, 100, 12, 16, None) == _lib.KQ_ERR_BAD_SHAPE
     _ = ctypes
