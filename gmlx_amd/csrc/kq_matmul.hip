@@ -20,6 +20,10 @@
 // one codec, sharing x / M <= 16, x rows fitting in LDS).
 bool kq_mv_eligible(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype);
 int kq_mv_launch(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype, hipStream_t s);
+// kq_stream.hip: weight-streaming launch for M <= 8 (problems validated, all
+// live, fp16 x shared, one codec or Q4_K with Q6_K, K as its slab plan allows).
+bool kq_stream_eligible(const kq_matmul_problem *ps, int n);
+int kq_stream_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, int y_dtype, hipStream_t s);
 // kq_qmv.hip: persistent small-batch launch (problems validated, all live,
 // sharing codec / x / M <= 16 / K <= 8192).
 int kq_qmv_persistent_launch(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype, hipStream_t s);
@@ -923,6 +927,8 @@ int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problem
         int na = 0;
         for (int i = 0; i < n_problems; ++i)
             if (problems[i].M != 0 && problems[i].N != 0) all[na++] = problems[i];
+        if (x_dtype == KQ_DTYPE_F16 && kq_stream_eligible(all, na))
+            return kq_stream_launch(all, na, nullptr, y_dtype, (hipStream_t)stream);
         if (kq_mv_eligible(all, na, x_dtype, y_dtype))
             return kq_mv_launch(all, na, x_dtype, y_dtype, (hipStream_t)stream);
     }

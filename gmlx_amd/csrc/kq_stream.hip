@@ -1,0 +1,717 @@
+// Weight-streaming small-batch matmul (M <= 8 activation rows) for problems
+// that share their activations: the decode-step projections at batch 1..8.
+//
+//   y[M, N] = x[M, K] . dequant(W[N, K])^T,  fp32 accumulation
+//
+// Producer / consumer workgroups, one per CU, walking 16-row weight tiles
+// t = blockIdx.x + k gridDim.x:
+//  - 2 producer waves copy whole tiles (16 rows x K) from HBM into a ring of
+//    R tile slots in LDS with direct-to-LDS buffer loads (no registers hold
+//    the data), up to R tiles ahead of the compute;
+//  - C consumer waves each own a K-slab of SB super-blocks for the whole
+//    launch: their activation fragments of that slab are loaded once and stay
+//    in registers; per tile a consumer reads its slab of the 16 rows from the
+//    slot in the MFMA lane layout of kq_mma.h, dequantizes in registers, runs
+//    v_mfma_f32_16x16x32_f16 and leaves its partial tile in LDS.
+// One workgroup barrier per tile hands a landed slot to the consumers and a
+// consumed slot back to the producers (the producers wait for their own loads
+// with explicit vmcnt counts, so the later tiles stay in flight across it).
+// The C partial tiles of a round are summed in consumer order
+// (deterministic) and stored.  Dequantization (about 1.9 VALU instructions
+// per weight per lane) runs on the consumers while the producers keep the HBM
+// stream going; with one kind of wave alternating between loads and math the
+// math added to the stream time instead of hiding under it (measured).
+//
+// Tile slot layout in LDS: row r at r * RC 16-byte chunks, RC = nb * SLOT / 16
+// + 1 (the spare chunk staggers the rows over the LDS banks, so the 16 rows
+// of an MFMA operand are read without conflicts); super-block kb of the row
+// at kb * SLOT bytes.  The copy is row-contiguous: each 1 KB load covers 64
+// consecutive chunks of the slot, one or two long runs of consecutive bytes of
+// one or two weight rows (measured on this part: streaming the gate|up bytes
+// this way takes 10.5 us against 14.1 us for per-lane row views, and 4.1
+// against 8.4 us at q|k|v size).  A Q4_K + Q6_K group (the q|k|v of a Q4_K_M
+// layer) runs in one launch with Q6_K-sized slots.
+#include <stdlib.h>
+
+#include "kq_mma.h"
+
+int device_cus();
+
+namespace {
+
+using namespace kqmma;
+
+#define LDSP(T) __attribute__((address_space(3))) T *
+
+constexpr int KQ_MIX = 0x7F;  // Q4_K and Q6_K problems in one launch
+// x region: per consumer kXRows rows of up to 1 KB at a pitch of kXRowLds
+// bytes (the extra 16 staggers the rows over the LDS banks)
+constexpr int kXRows = 8, kXRowLds = 1040;
+constexpr int kTmax = 8;      // tiles per workgroup per round
+constexpr int kProducers = 2;
+
+// A super-block's LDS slot is SLOT bytes (16-aligned), filled by SLOT / 16
+// chunk loads; chunk cb reads the 16 block bytes from src(cb), always inside
+// the block (a load that crosses the end of a buffer range reads zeros whole).
+//   Q4_K    : the 144 bytes in order.
+//   Q6_K    : bytes 0..207 in order, then 194..209 (d lands at slot 222).
+//   IQ2_XXS : bytes 0..15 (d at slot 0), then the 64 bytes of groups from
+//             byte 2 (slot 16..79, 16-aligned).
+template <int CODEC>
+struct Geo;
+template <>
+struct Geo<KQ_CODEC_Q4_K> {
+    static constexpr int BPB = 144, SLOT = 144;
+    __device__ static constexpr int src(int cb) { return 16 * cb; }
+};
+template <>
+struct Geo<KQ_CODEC_Q6_K> {
+    static constexpr int BPB = 210, SLOT = 224, D_AT = 222;
+    __device__ static constexpr int src(int cb) { return cb < 13 ? 16 * cb : 194; }
+};
+template <>
+struct Geo<KQ_CODEC_IQ2_XXS> {
+    static constexpr int BPB = 66, SLOT = 80;
+    __device__ static constexpr int src(int cb) { return cb == 0 ? 0 : 2 + 16 * (cb - 1); }
+};
+
+__device__ __forceinline__ u32x4 lds128(uint32_t a) { return *(const LDSP(u32x4))(uintptr_t)a; }
+__device__ __forceinline__ u32x2 lds64(uint32_t a) { return *(const LDSP(u32x2))(uintptr_t)a; }
+__device__ __forceinline__ uint32_t lds16(uint32_t a) { return (uint32_t) * (const LDSP(uint16_t))(uintptr_t)a; }
+
+// Lane views of kq_mma.h's Block<> filled from an LDS slot (layout above).
+template <int CODEC>
+__device__ __forceinline__ void load_slot(Block<CODEC> &b, uint32_t slot, int g);
+
+template <>
+__device__ __forceinline__ void load_slot<KQ_CODEC_Q4_K>(Block<KQ_CODEC_Q4_K> &b, uint32_t slot, int g) {
+    b.hdr = lds128(slot);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) b.q[c] = lds64(slot + 16 + 32 * c + 8 * g);
+}
+
+template <>
+__device__ __forceinline__ void load_slot<KQ_CODEC_Q6_K>(Block<KQ_CODEC_Q6_K> &b, uint32_t slot, int g) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) b.ql[i] = lds64(slot + 64 * (i >> 1) + 32 * (i & 1) + 8 * g);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) b.qh[h] = lds64(slot + 128 + 32 * h + 8 * g);
+    b.sc = lds128(slot + 192);
+    b.dbits = lds16(slot + Geo<KQ_CODEC_Q6_K>::D_AT);
+}
+
+template <>
+__device__ __forceinline__ void load_slot<KQ_CODEC_IQ2_XXS>(Block<KQ_CODEC_IQ2_XXS> &b, uint32_t slot, int g) {
+    b.raw = lds128(slot + 16 + 16 * g);
+    b.dbits = lds16(slot);
+}
+
+struct StreamProblem {
+    const uint8_t *w;
+    void *y;
+    int64_t y_stride;   // elements
+    uint32_t w_bytes;   // N * row_bytes (< 2^31)
+    uint32_t row_bytes;
+    int32_t N;
+    int32_t codec;
+};
+
+struct StreamArgs {
+    int32_t tile_begin[KQ_MAX_GROUP];  // first tile of each problem; unused: INT_MAX
+    StreamProblem p[KQ_MAX_GROUP];
+    const char *x;                     // fp16 [M, K]
+    const int32_t *x_exp;              // per-row scale exponents of x (outputs * 2^-e), or null
+    int64_t x_stride;                  // elements
+    int32_t M, K, y_dtype, total_tiles, n_problems;
+};
+
+typedef const __attribute__((address_space(4))) StreamArgs *KArgs;
+
+// Problems per launch (the eligibility test declines larger groups).
+constexpr int kStreamProblems = 4;
+
+// The problem of a tile, from the kernel arguments by constant indices only:
+// the loads have fixed addresses, so they issue together (and then hit the
+// scalar cache) instead of forming a chain of dependent scalar-cache misses
+// (index, then fields) in front of every tile's first load.
+__device__ __forceinline__ int problem_of(KArgs A, int tile) {
+    int pi = 0;
+#pragma unroll
+    for (int i = 1; i < kStreamProblems; ++i) pi += tile >= A->tile_begin[i];  // unused entries: INT_MAX
+    return pi;
+}
+
+__device__ __forceinline__ StreamProblem problem_at(KArgs A, int pi, int32_t &begin) {
+    StreamProblem p;
+#pragma unroll
+    for (int i = 0; i < kStreamProblems; ++i)
+        if (i == 0 || pi == i) {
+            p.w = A->p[i].w;
+            p.y = A->p[i].y;
+            p.y_stride = A->p[i].y_stride;
+            p.w_bytes = A->p[i].w_bytes;
+            p.row_bytes = A->p[i].row_bytes;
+            p.N = A->p[i].N;
+            p.codec = A->p[i].codec;
+            begin = A->tile_begin[i];
+        }
+    return p;
+}
+
+// Slot geometry of one codec for NB super-blocks per row.
+template <int CODEC, int NB>
+struct SlotGeo {
+    static constexpr int CPB = Geo<CODEC>::SLOT / 16;  // chunks per super-block
+    static constexpr int RC = NB * CPB + 1;            // chunks per (padded) row
+    static constexpr int CHUNKS = 16 * RC;
+};
+
+// Byte offset in the weight matrix of slot chunk q of the tile whose first
+// row is row0 (rows past last_row read last_row: their outputs are never
+// stored).  The row pads and the chunks past the codec's geometry (a Q4_K
+// tile in Q6_K-sized slots) are never read: their offset lies past the
+// buffer, so the load writes zeros and makes no memory request (pointing them
+// all at one address made a 16-row copy several times slower, measured).
+template <int CODEC, int NB>
+__device__ __forceinline__ uint32_t slot_src(int q, uint32_t row0, uint32_t last_row, uint32_t row_bytes) {
+    using SG = SlotGeo<CODEC, NB>;
+    const int row = q / SG::RC, w = q - row * SG::RC;
+    if (w >= NB * SG::CPB || row >= 16) return 0x80000000u;
+    const int blk = w / SG::CPB, cb = w - blk * SG::CPB;
+    const uint32_t rr = min(row0 + (uint32_t)row, last_row);
+    return rr * row_bytes + (uint32_t)(blk * Geo<CODEC>::BPB + Geo<CODEC>::src(cb));
+}
+
+// The slot geometry a launch allocates: its codec's, or Q6_K's for Q4_K + Q6_K.
+template <int CODEC>
+struct SlotCodec {
+    static constexpr int C = CODEC;
+};
+template <>
+struct SlotCodec<KQ_MIX> {
+    static constexpr int C = KQ_CODEC_Q6_K;
+};
+
+// Loads per producer per tile: the slot's chunks in 1 KB loads, split evenly
+// over the producers (the slot is allocated for all of them).
+template <int SC, int NB>
+constexpr int producer_loads() {
+    return ((SlotGeo<SC, NB>::CHUNKS + 63) / 64 + kProducers - 1) / kProducers;
+}
+template <int SC, int NB>
+constexpr int slot_bytes() {
+    return producer_loads<SC, NB>() * kProducers * 1024;
+}
+
+// s_waitcnt vmcnt(n) (0 <= n <= 63) leaving the other counters unconstrained
+// (gfx9 encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14).
+#define KQ_VMCNT(n) (((n) & 0xF) | ((((n) >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8))
+
+// IQ2_XXS kernels keep the fp16 grid / sign tables in LDS; other codecs
+// allocate none (their views never read the tables).
+template <int CODEC>
+struct IqTables {
+    __device__ static const Iq2Tables *get() { return nullptr; }
+};
+template <>
+struct IqTables<KQ_CODEC_IQ2_XXS> {
+    __device__ static const Iq2Tables *get() {
+        __shared__ Iq2Tables t;
+        load_iq2_tables(t);
+        return &t;
+    }
+};
+
+// ---- Q4_K with owned sub-blocks (launches of Q4_K problems only) ---------
+// Lane group g owns sub-blocks 2g and 2g+1 of every super-block: qs bytes
+// 32g + l (l = 0..31), whose low nibbles are values 64g + l and high nibbles
+// values 64g + 32 + l.  Step t takes qs dword t of that run: the values
+// l = 4t + (0, 2, 1, 3) of both sub-blocks.  A byte pair (b0, b2) or (b1, b3)
+// becomes two biased fp16 values with one v_and_or_b32:
+//   (w & 0x000F000F) | 0x64006400 = 1024 + low nibble (exponent 10: unit 1)
+//   (w & 0x00F000F0) | 0x54005400 =   64 + high nibble (exponent 6: unit 16/16)
+// and one fma against the exact constant -1024 dsc (-64 dsc) removes the bias
+// with a single rounding: fma(1024 + q, dsc, -1024 dsc) = fp16(q dsc).  The
+// minimum term -dm_j * sum_{l in j} x_l stays out of the weights: one more
+// MFMA per K-slab adds it from per-sub-block activation sums (fp32 sums split
+// into fp16 hi + lo parts, about 22 bits) against the fp16 -dm_j.  With
+// |dsc| >= 32 (weights beyond about +-480) the constant could overflow: a
+// wave that meets such a super-block takes the two-step form (exact q, then
+// q * dsc) for it, with the same rounding.
+struct Q4Prep {
+    half2_t dsc;  // (dsc_2g, dsc_2g+1)
+    half2_t nb;   // (-1024 dsc_2g, -64 dsc_2g+1)
+    half2_t ndm;  // (-dm_2g, -dm_2g+1)
+};
+
+// Constants of the owned view held in VGPRs: gfx9 VOP3 encodings take no
+// literal and at most one SGPR, so v_and_or_b32 needs its mask and bias in
+// vector registers (kept opaque to the compiler, which would otherwise fold
+// them back into literal v_and / v_or pairs).
+struct Q4Consts {
+    uint32_t lo_mask, lo_bias, hi_mask, hi_bias, upper;  // upper: ~0 in lane groups 2, 3
+    uint32_t sel;                                         // perm selector of the lane's scale byte pair
+};
+
+__device__ __forceinline__ Q4Consts q4own_consts(int g) {
+    Q4Consts k = {0x000F000Fu, 0x64006400u, 0x00F000F0u, 0x54005400u, g >= 2 ? ~0u : 0u,
+                  (g & 1) ? KQ_SEL_B23 : KQ_SEL_B01};
+    asm volatile("" : "+v"(k.lo_mask), "+v"(k.lo_bias), "+v"(k.hi_mask), "+v"(k.hi_bias), "+v"(k.upper));
+    return k;
+}
+
+__device__ __forceinline__ Q4Prep q4own_prep(u32x4 hdr, const Q4Consts &k) {
+    const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;  // scale bytes 0..3, 4..7, 8..11
+    // sub-blocks 0..3: sc = s[j] & 63, m = s[j+4] & 63; 4..7: low nibbles from
+    // s[j+4], the two high bits from the top of s[j-4] / s[j]; the lane's
+    // pair is picked by bit masks (a select would become a branch)
+    const uint32_t sc_lo = s0 & 0x3F3F3F3Fu, m_lo = s1 & 0x3F3F3F3Fu;
+    const uint32_t sc_hi = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
+    const uint32_t m_hi = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
+    const uint32_t scw = (sc_hi & k.upper) | (sc_lo & ~k.upper);
+    const uint32_t mw = (m_hi & k.upper) | (m_lo & ~k.upper);
+    const half2_t k1024 = {(_Float16)1024.f, (_Float16)1024.f};
+    const half2_t dd = h2b(hdr.x);  // (d, dmin)
+    Q4Prep p;
+    p.dsc = (h2b(__builtin_amdgcn_perm(0x64646464u, scw, k.sel)) - k1024) * bcast(dd.x);
+    p.ndm = (h2b(__builtin_amdgcn_perm(0x64646464u, mw, k.sel)) - k1024) * bcast(-dd.y);
+    p.nb = p.dsc * half2_t{(_Float16)-1024.f, (_Float16)-64.f};
+    return p;
+}
+
+__device__ __forceinline__ bool q4own_big(const Q4Prep &p) {
+    return __builtin_fabsf((float)p.dsc.x) >= 32.f || __builtin_fabsf((float)p.dsc.y) >= 32.f;
+}
+
+template <bool SAFE>
+__device__ __forceinline__ half8_t q4own_frag(uint32_t w, const Q4Prep &p, const Q4Consts &k) {
+    const uint32_t w8 = w >> 8;
+    const half2_t l0 = h2b((w & k.lo_mask) | k.lo_bias), l1 = h2b((w8 & k.lo_mask) | k.lo_bias);
+    const half2_t u0 = h2b((w & k.hi_mask) | k.hi_bias), u1 = h2b((w8 & k.hi_mask) | k.hi_bias);
+    const half2_t s0 = bcast(p.dsc.x), s1 = bcast(p.dsc.y);
+    if constexpr (SAFE) {
+        const half2_t k1024 = {(_Float16)1024.f, (_Float16)1024.f}, k64 = {(_Float16)64.f, (_Float16)64.f};
+        return cat8((l0 - k1024) * s0, (l1 - k1024) * s0, (u0 - k64) * s1, (u1 - k64) * s1);
+    } else {
+        const half2_t c0 = bcast(p.nb.x), c1 = bcast(p.nb.y);
+        return cat8(__builtin_elementwise_fma(l0, s0, c0), __builtin_elementwise_fma(l1, s0, c0),
+                    __builtin_elementwise_fma(u0, s1, c1), __builtin_elementwise_fma(u1, s1, c1));
+    }
+}
+
+// Activation fragments of the owned view for super-blocks kb0 .. kb0+SB-1:
+// xr[s][t] = x[e + (0, 2, 1, 3)], x[e + 32 + (0, 2, 1, 3)] with e = 256 (kb0 + s)
+// + 64 g + 4 t, and xm = the sub-block sums (2g, 2g+1 of each super-block) as
+// fp16 (hi, lo) pairs in the k slots the minimum MFMA pairs with -dm.
+// Input: the coalesced chunks C[s][t'] = x[256 (kb0 + s) + 32 t' + 8 g .. +7]
+// (the four lane groups of a row hold 64 consecutive bytes).  A 4 x 4
+// transpose of chunks between lane groups (t' = 2u + a: lane group g ends
+// with C[2g + a] of every source group w) follows, in two swap stages:
+// v_permlane32_swap exchanges bit 1 of u with bit 1 of g, v_permlane16_swap
+// bit 0 with bit 0.  Register 2w + a then holds x[64 g + 32 a + 8 w .. +7].
+template <int SB>
+__device__ __forceinline__ void q4own_x(half8_t (&xr)[SB][8], half8_t &xm, u32x4 (&cin)[SB][8]) {
+    static_assert(SB <= 2, "the minimum MFMA holds two super-blocks of sums");
+    float sum[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+#pragma unroll
+    for (int s = 0; s < SB; ++s) {
+        u32x4 (&c)[8] = cin[s];
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+#pragma unroll
+                for (int u0 = 0; u0 < 2; ++u0) {  // registers u = u0 and u0 + 2
+                    const auto r = __builtin_amdgcn_permlane32_swap(c[2 * u0 + a][d], c[2 * u0 + 4 + a][d], false,
+                                                                    false);
+                    c[2 * u0 + a][d] = r[0];
+                    c[2 * u0 + 4 + a][d] = r[1];
+                }
+#pragma unroll
+                for (int u1 = 0; u1 < 2; ++u1) {  // registers u = 2 u1 and 2 u1 + 1
+                    const auto r = __builtin_amdgcn_permlane16_swap(c[4 * u1 + a][d], c[4 * u1 + 2 + a][d], false,
+                                                                    false);
+                    c[4 * u1 + a][d] = r[0];
+                    c[4 * u1 + 2 + a][d] = r[1];
+                }
+            }
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const u32x4 &lo = c[2 * (t >> 1)], &hi = c[2 * (t >> 1) + 1];
+            const int d = 2 * (t & 1);
+            const u32x4 v = {__builtin_amdgcn_perm(lo[d + 1], lo[d], 0x05040100u),
+                             __builtin_amdgcn_perm(lo[d + 1], lo[d], 0x07060302u),
+                             __builtin_amdgcn_perm(hi[d + 1], hi[d], 0x05040100u),
+                             __builtin_amdgcn_perm(hi[d + 1], hi[d], 0x07060302u)};
+            xr[s][t] = __builtin_bit_cast(half8_t, v);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                sum[s][0] += (float)xr[s][t][i];
+                sum[s][1] += (float)xr[s][t][4 + i];
+            }
+        }
+    }
+    _Float16 m[8];
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const _Float16 hi = (_Float16)sum[s][j];
+            m[4 * s + 2 * j] = s < SB ? hi : (_Float16)0.f;
+            m[4 * s + 2 * j + 1] = s < SB ? (_Float16)(sum[s][j] - (float)hi) : (_Float16)0.f;
+        }
+    xm = half8_t{m[0], m[1], m[2], m[3], m[4], m[5], m[6], m[7]};
+}
+
+// One K-slab of a tile in the owned view: row_p points at the lane's row,
+// super-block kb0, in the slot.
+template <int SB>
+__device__ __forceinline__ void q4own_slab(floatx4 &acc, LDSP(const uint8_t) row_p, const half8_t (&xr)[SB][8],
+                                           const half8_t &xm, const Q4Consts &k, int g) {
+    u32x4 hdr[SB], qa[SB], qb[SB];
+#pragma unroll
+    for (int s = 0; s < SB; ++s) {
+        hdr[s] = *(const LDSP(u32x4))(row_p + s * 144);
+        qa[s] = *(const LDSP(u32x4))(row_p + s * 144 + 16 + 32 * g);
+        qb[s] = *(const LDSP(u32x4))(row_p + s * 144 + 32 + 32 * g);
+    }
+    _Float16 bm[8];
+#pragma unroll
+    for (int s = 0; s < SB; ++s) {
+        const Q4Prep p = q4own_prep(hdr[s], k);
+        const uint32_t q[8] = {qa[s].x, qa[s].y, qa[s].z, qa[s].w, qb[s].x, qb[s].y, qb[s].z, qb[s].w};
+        if (__builtin_amdgcn_ballot_w64(q4own_big(p))) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xr[s][t], q4own_frag<true>(q[t], p, k), acc, 0, 0, 0);
+        } else {
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xr[s][t], q4own_frag<false>(q[t], p, k), acc, 0, 0, 0);
+        }
+        bm[4 * s] = bm[4 * s + 1] = p.ndm.x;
+        bm[4 * s + 2] = bm[4 * s + 3] = p.ndm.y;
+    }
+#pragma unroll
+    for (int s = SB; s < 2; ++s) bm[4 * s] = bm[4 * s + 1] = bm[4 * s + 2] = bm[4 * s + 3] = (_Float16)0.f;
+    const half8_t b = {bm[0], bm[1], bm[2], bm[3], bm[4], bm[5], bm[6], bm[7]};
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xm, b, acc, 0, 0, 0);
+}
+
+template <int CODEC, int SB>
+__device__ __forceinline__ void mma_slab(floatx4 &acc, uint32_t row_lds, const half8_t (&xr)[SB][8], int g,
+                                         const Iq2Tables &tab) {
+#pragma unroll
+    for (int s = 0; s < SB; ++s) {
+        Block<CODEC> b;
+        load_slot<CODEC>(b, row_lds + s * Geo<CODEC>::SLOT, g);
+        b.prep(g);
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xr[s][t], b.frag(t, g, tab), acc, 0, 0, 0);
+    }
+}
+
+// CODEC: KQ_CODEC_* or KQ_MIX.  SB: super-blocks per consumer, C consumers
+// (K = 256 SB C).  R: tile slots in the ring.
+template <int CODEC, int SB, int C, int R>
+__global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(StreamArgs a_) {
+    constexpr int NB = SB * C;
+    constexpr int SC = SlotCodec<CODEC>::C;
+    constexpr int PL = producer_loads<SC, NB>();  // loads per producer per tile
+    constexpr int SLOTB = slot_bytes<SC, NB>();
+    constexpr int XC = CODEC == KQ_MIX ? KQ_CODEC_Q4_K : CODEC;  // activation layout (Q4_K / Q6_K alike)
+    static_assert(2 * PL <= 63, "vmcnt counts at most 63 loads");
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const KArgs A = (KArgs)__builtin_amdgcn_kernarg_segment_ptr();
+    const Iq2Tables &iq2_tab = *IqTables<CODEC>::get();
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = kq_lane(), r = lane & 15, g = lane >> 4;
+    const int G = (int)gridDim.x, B0 = (int)blockIdx.x;
+    const int M = A->M;
+    const int my_tiles = (A->total_tiles - B0 + G - 1) / G;
+    const uint32_t ring_lds = (uint32_t)(uintptr_t)(LDSP(void))smem;
+    floatx4 *red = (floatx4 *)(smem + R * SLOTB);  // [kTmax][C][32 lanes]
+
+    if (wave < kProducers) {
+        // ================= producer: tiles into slots, up to R ahead
+        for (int round0 = 0; round0 < my_tiles; round0 += kTmax) {
+            const int nt = min(kTmax, my_tiles - round0);
+            // copy tile j of the round into slot j % R
+            auto copy = [&](int j) {
+                const int tile = B0 + (round0 + j) * G;
+                int32_t begin;
+                const StreamProblem pr = problem_at(A, problem_of(A, tile), begin);
+                const uint32_t rb = pr.row_bytes;
+                const uint32_t row0 = (uint32_t)(tile - begin) * 16;
+                const uint32_t last = (uint32_t)pr.N - 1;
+                const __amdgpu_buffer_rsrc_t rs = kq_buffer(pr.w, pr.w_bytes);
+                const bool q6 = CODEC == KQ_MIX && pr.codec == KQ_CODEC_Q6_K;
+                const uint32_t slot = ring_lds + (uint32_t)(j % R) * SLOTB;
+#pragma unroll
+                for (int i = 0; i < PL; ++i) {
+                    const int li = i * kProducers + wave;  // the producers' loads interleave
+                    const int q = 64 * li + lane;
+                    uint32_t off;
+                    if constexpr (CODEC == KQ_MIX)
+                        off = q6 ? slot_src<KQ_CODEC_Q6_K, NB>(q, row0, last, rb)
+                                 : slot_src<KQ_CODEC_Q4_K, NB>(q, row0, last, rb);
+                    else
+                        off = slot_src<CODEC, NB>(q, row0, last, rb);
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDSP(void))(uintptr_t)(slot + 1024 * li), 16, off, 0,
+                                                             0, 0);
+                }
+            };
+            const int pre = min(R, nt);
+            for (int j = 0; j < pre; ++j) {
+                copy(j);
+                // slot 1 onwards and the partial-tile area hold the consumers'
+                // activation rows until they are in registers
+                if (round0 == 0 && j == 0) __builtin_amdgcn_s_barrier();
+            }
+            for (int b = 0; b < nt; ++b) {
+                // wait for tile b's loads; the tiles copied after it stay in flight
+                const int newer = min(b == 0 ? R - 1 : R - 2, nt - 1 - b);
+                if (newer >= 2) __builtin_amdgcn_s_waitcnt(KQ_VMCNT(2 * PL));
+                else if (newer == 1) __builtin_amdgcn_s_waitcnt(KQ_VMCNT(PL));
+                else __builtin_amdgcn_s_waitcnt(KQ_VMCNT(0));
+                __builtin_amdgcn_s_barrier();  // slot b % R to the consumers; slot (b - 1) % R back
+                if (b >= 1 && b + R - 1 < nt) copy(b + R - 1);
+            }
+            __builtin_amdgcn_s_barrier();  // the consumers' partial tiles are in LDS
+            if (round0 + kTmax < my_tiles)
+                __builtin_amdgcn_s_barrier();  // the round's outputs are summed: red and the ring are free
+        }
+        return;
+    }
+
+    // ================= consumer c: K-slab [c SB, c SB + SB) of every tile
+    const int c = wave - kProducers;
+    const int kb0 = c * SB;
+    half8_t xr[SB][8];
+    [[maybe_unused]] half8_t xm;
+    {
+        // The slab's activation rows arrive by coalesced direct-to-LDS loads
+        // (one row segment of SB * 512 bytes per instruction) in this
+        // consumer's part of the x region, then go into the MFMA fragments.
+        // Lanes of rows >= M take zeros.
+        const uint32_t xbytes = (uint32_t)(((int64_t)(M - 1) * A->x_stride + A->K) * 2);
+        const __amdgpu_buffer_rsrc_t xs = kq_buffer(A->x, xbytes);
+        const uint32_t xreg = ring_lds + SLOTB + (uint32_t)(c * kXRows * kXRowLds);
+        // lanes past the segment read past the buffer (zeros, inside the row's LDS pitch)
+        const uint32_t loff =
+            16u * lane < 512u * SB ? (uint32_t)(kb0 * KQ_QK * 2) + 16u * lane : 0x80000000u;
+#pragma unroll
+        for (int m = 0; m < kXRows; ++m)
+            if (m < M)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xs, (LDSP(void))(uintptr_t)(xreg + m * kXRowLds), 16,
+                                                         loff + (uint32_t)(m * A->x_stride * 2), 0, 0, 0);
+        __builtin_amdgcn_s_waitcnt(KQ_VMCNT(0));
+        const bool live = r < M;
+        const uint32_t rowa = xreg + (uint32_t)(min(r, M - 1) * kXRowLds);
+        const u32x4 zero = {0u, 0u, 0u, 0u};
+        if constexpr (CODEC == KQ_CODEC_Q4_K) {
+            u32x4 ch[SB][8];
+#pragma unroll
+            for (int s = 0; s < SB; ++s)
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    const u32x4 v = lds128(rowa + s * 512 + 64 * t + 16 * g);
+                    ch[s][t] = live ? v : zero;
+                }
+            q4own_x<SB>(xr, xm, ch);
+        } else {
+#pragma unroll
+            for (int s = 0; s < SB; ++s)
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    const u32x4 v = lds128(rowa + s * 512 + 2 * Block<XC>::x_elem(t, g));
+                    xr[s][t] = __builtin_bit_cast(half8_t, live ? v : zero);
+                }
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // the x region reads are done
+    __builtin_amdgcn_s_barrier();                           // the producers may fill slot 1
+    // owned Q4_K view: the lane's row at super-block kb0 in slot 0
+    [[maybe_unused]] const Q4Consts q4k = q4own_consts(g);
+    [[maybe_unused]] LDSP(const uint8_t) own_p =
+        (LDSP(const uint8_t))smem + r * SlotGeo<KQ_CODEC_Q4_K, NB>::RC * 16 + kb0 * 144;
+    for (int round0 = 0; round0 < my_tiles; round0 += kTmax) {
+        const int nt = min(kTmax, my_tiles - round0);
+        for (int b = 0; b < nt; ++b) {
+            __builtin_amdgcn_s_barrier();  // tile b has landed in slot b % R
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+            const int tile = B0 + (round0 + b) * G;
+            const uint32_t slot = ring_lds + (uint32_t)(b % R) * SLOTB;
+            floatx4 acc = {0, 0, 0, 0};
+            if constexpr (CODEC == KQ_MIX) {
+                int32_t begin;
+                if (problem_at(A, problem_of(A, tile), begin).codec == KQ_CODEC_Q6_K)
+                    mma_slab<KQ_CODEC_Q6_K, SB>(acc, slot + r * SlotGeo<KQ_CODEC_Q6_K, NB>::RC * 16 + kb0 * 224, xr, g,
+                                                iq2_tab);
+                else
+                    mma_slab<KQ_CODEC_Q4_K, SB>(acc, slot + r * SlotGeo<KQ_CODEC_Q4_K, NB>::RC * 16 + kb0 * 144, xr, g,
+                                                iq2_tab);
+            } else if constexpr (CODEC == KQ_CODEC_Q4_K) {
+                q4own_slab<SB>(acc, own_p + (b % R) * SLOTB, xr, xm, q4k, g);
+            } else {
+                mma_slab<CODEC, SB>(acc, slot + r * SlotGeo<CODEC, NB>::RC * 16 + kb0 * Geo<CODEC>::SLOT, xr, g,
+                                    iq2_tab);
+            }
+            kq_mfma_drain();
+            // batch rows 4g + e < 8 live in lanes g < 2
+            if (g < 2) red[(b * C + c) * 32 + lane] = acc;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // slot reads and red writes done
+        }
+        __builtin_amdgcn_s_barrier();  // every partial tile of the round is in LDS
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        // ---- sum the C partial tiles in consumer order and store: output f = (b, m, n)
+        for (int f = (int)threadIdx.x - 64 * kProducers; f < nt * 8 * 16; f += 64 * C) {
+            const int b = f >> 7, m = (f >> 4) & 7, n = f & 15;
+            if (m >= M) continue;
+            const int ln = 16 * (m >> 2) + n, e = m & 3;
+            float sum = red[(b * C) * 32 + ln][e];
+#pragma unroll
+            for (int c2 = 1; c2 < C; ++c2) sum += red[(b * C + c2) * 32 + ln][e];
+            if (A->x_exp) sum = ldexpf(sum, -A->x_exp[m]);
+            const int tile = B0 + (round0 + b) * G;
+            int32_t begin;
+            const StreamProblem pr = problem_at(A, problem_of(A, tile), begin);
+            const int nn = (tile - begin) * 16 + n;
+            if (nn < pr.N) kq_store_out(pr.y, A->y_dtype, (int64_t)m * pr.y_stride + nn, sum);
+        }
+        if (round0 + kTmax < my_tiles) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            __builtin_amdgcn_s_barrier();  // red and the ring are free for the next round
+        }
+    }
+}
+
+template <int CODEC, int SB, int C>
+int launch(const StreamArgs &a, int grid, hipStream_t s) {
+    constexpr int NB = SB * C;
+    constexpr int SC = SlotCodec<CODEC>::C;
+    // three tile slots when they fit beside the partial tiles, else two
+    constexpr size_t red = (size_t)kTmax * C * 32 * 16;
+    constexpr size_t budget = 150 * 1024 - (CODEC == KQ_CODEC_IQ2_XXS ? sizeof(Iq2Tables) : 0);
+    constexpr size_t xregion = (size_t)slot_bytes<SC, NB>() + (size_t)C * kXRows * kXRowLds;
+    constexpr auto need = [](size_t ring) { return ring + red > xregion ? ring + red : xregion; };
+    constexpr int R = need(3 * (size_t)slot_bytes<SC, NB>()) <= budget ? 3 : 2;
+    constexpr size_t lds = need((size_t)R * slot_bytes<SC, NB>());
+    static_assert(lds <= budget, "stream kernel LDS");
+    static bool raised = false;
+    if (!raised) {
+        if (hipFuncSetAttribute((const void *)kq_stream_kernel<CODEC, SB, C, R>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+            return KQ_ERR_LAUNCH_FAILED;
+        raised = true;
+    }
+    hipLaunchKernelGGL((kq_stream_kernel<CODEC, SB, C, R>), dim3(grid), dim3(64 * (kProducers + C)), lds, s, a);
+    return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
+}
+
+// Consumers for K = 256 nb: one super-block each for 2 and 4 super-blocks,
+// two each for 8 and 16 (4 and 8 consumers); other K take the other
+// small-batch paths.
+template <int CODEC>
+int launch_codec(const StreamArgs &a, int nb, int grid, hipStream_t s) {
+    switch (nb) {
+    case 2: return launch<CODEC, 1, 2>(a, grid, s);
+    case 4: return launch<CODEC, 1, 4>(a, grid, s);
+    case 8: return launch<CODEC, 2, 4>(a, grid, s);
+    case 16: return launch<CODEC, 2, 8>(a, grid, s);
+    default: return KQ_ERR_BAD_SHAPE;
+    }
+}
+
+bool stream_k_ok(int K) {
+    const int nb = K / KQ_QK;
+    return nb == 2 || nb == 4 || nb == 8 || nb == 16;
+}
+
+}  // namespace
+
+// Eligibility (the dispatcher also requires fp16 activations): M <= 8, at
+// most 4 problems sharing x / stride / M / K, one codec or Q4_K with Q6_K, K
+// of 2, 4, 8 or 16 super-blocks, weights and x addressable with 31-bit buffer
+// offsets.  GMLX_KQ_STREAM=0 declines, =2 forces every eligible launch here;
+// GMLX_KQ_STREAM_WGS=n caps the grid at n workgroups (tests).
+bool kq_stream_eligible(const kq_matmul_problem *ps, int n) {
+    if (n <= 0 || n > kStreamProblems) return false;
+    const char *env = getenv("GMLX_KQ_STREAM");
+    if (env && env[0] == '0' && env[1] == 0) return false;
+    const kq_matmul_problem &q0 = ps[0];
+    if (q0.M < 1 || q0.M > 8 || !stream_k_ok(q0.K)) return false;
+    bool mixed = false;
+    for (int i = 0; i < n; ++i) {
+        const kq_matmul_problem &q = ps[i];
+        if (q.x != q0.x || q.x_row_stride != q0.x_row_stride || q.M != q0.M || q.K != q0.K) return false;
+        if (q.codec != q0.codec) mixed = true;
+        if ((int64_t)(q.N + 16) * q.w_row_bytes >= (int64_t)0x80000000LL) return false;
+    }
+    if (mixed)
+        for (int i = 0; i < n; ++i)
+            if (ps[i].codec != KQ_CODEC_Q4_K && ps[i].codec != KQ_CODEC_Q6_K) return false;
+    if ((int64_t)(q0.M - 1) * q0.x_row_stride * 2 + (int64_t)q0.K * 2 >= (int64_t)0x80000000LL) return false;
+    // Routing (measured at the Qwen3-8B shapes, B = 1..8): the kernel's fixed
+    // cost (ten waves per CU, the activation slab, the partial-tile sums) pays
+    // off from about four tiles per CU (gate|up: 15.4-15.8 us against
+    // 16.4-17.7 us for the LDS-staged path); at one or two tiles per CU (o,
+    // q|k|v) the LDS-staged path is faster, and a Q4_K + Q6_K group is slower
+    // here (its producers keep both slot geometries live and spill).
+    // GMLX_KQ_STREAM=2 takes every eligible launch (tests).
+    if (!(env && env[0] == '2' && env[1] == 0)) {
+        if (mixed) return false;
+        int64_t tiles = 0;
+        for (int i = 0; i < n; ++i) tiles += (ps[i].N + 15) / 16;
+        if (tiles < 4 * (int64_t)device_cus()) return false;
+    }
+    return true;
+}
+
+// Problems validated, eligible and all live; x is fp16, x_exp its per-row
+// exponents or null.
+int kq_stream_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, int y_dtype, hipStream_t s) {
+    StreamArgs a;
+    int tiles = 0;
+    bool mixed = false;
+    for (int i = 0; i < n; ++i) {
+        StreamProblem &p = a.p[i];
+        p.w = (const uint8_t *)ps[i].w;
+        p.y = ps[i].y;
+        p.y_stride = ps[i].y_row_stride;
+        p.row_bytes = (uint32_t)ps[i].w_row_bytes;
+        p.w_bytes = (uint32_t)(ps[i].N * ps[i].w_row_bytes);
+        p.N = ps[i].N;
+        p.codec = ps[i].codec;
+        a.tile_begin[i] = tiles;
+        tiles += (ps[i].N + 15) / 16;
+        if (ps[i].codec != ps[0].codec) mixed = true;
+    }
+    for (int i = n; i < KQ_MAX_GROUP; ++i) {
+        a.p[i] = a.p[0];
+        a.tile_begin[i] = 0x7FFFFFFF;
+    }
+    const kq_matmul_problem &q0 = ps[0];
+    a.x = (const char *)q0.x;
+    a.x_exp = x_exp;
+    a.x_stride = q0.x_row_stride;
+    a.M = q0.M;
+    a.K = q0.K;
+    a.y_dtype = y_dtype;
+    a.total_tiles = tiles;
+    a.n_problems = n;
+    int grid = device_cus();
+    if (const char *e = getenv("GMLX_KQ_STREAM_WGS")) {  // smaller grids: more tiles and rounds per workgroup
+        const int w = atoi(e);
+        if (w > 0 && w < grid) grid = w;
+    }
+    if (grid > tiles) grid = tiles;
+    const int nb = q0.K / KQ_QK;
+    if (mixed) return launch_codec<KQ_MIX>(a, nb, grid, s);
+    switch (q0.codec) {
+    case KQ_CODEC_Q4_K: return launch_codec<KQ_CODEC_Q4_K>(a, nb, grid, s);
+    case KQ_CODEC_Q6_K: return launch_codec<KQ_CODEC_Q6_K>(a, nb, grid, s);
+    default: return launch_codec<KQ_CODEC_IQ2_XXS>(a, nb, grid, s);
+    }
+}

@@ -77,7 +77,8 @@ def test_bf16_activations_and_f32_out():
     assert okq.max_rel(got32.cpu().numpy(), ref) <= TOL
 
 
-@pytest.mark.parametrize("path", [{"GMLX_KQ_MV": "0", "GMLX_KQ_PERSISTENT": "0"}, {"GMLX_KQ_MV": "2"}, {}])
+@pytest.mark.parametrize("path", [{"GMLX_KQ_STREAM": "0", "GMLX_KQ_MV": "0", "GMLX_KQ_PERSISTENT": "0"},
+                                  {"GMLX_KQ_STREAM": "0", "GMLX_KQ_MV": "2"}, {}])
 def test_grouped_equals_separate_bitwise(path, monkeypatch):
     """q|k|v with mixed codecs in one launch == three separate launches:
     bitwise when both take the same kernel (the general or the LDS-staged
@@ -173,19 +174,27 @@ def test_module_forward():
     assert okq.max_rel(got, ref) <= TOL
 
 
-# The three small-batch paths of kq_quantized_matmul_grouped, forced in turn:
-# the LDS-staged persistent path (kq_mv), the register persistent path
-# (kq_qmv) and the general tiled path.  Small grids make every workgroup walk
-# many tiles, with partial ring rounds.
+# The small-batch paths of kq_quantized_matmul_grouped, forced in turn: the
+# producer / consumer weight-streaming kernel (M <= 8, K of 2, 4, 8 or 16
+# super-blocks), the LDS-staged persistent path (kq_mv), the register
+# persistent path (kq_qmv) and the general tiled path.  Small grids make every
+# workgroup walk many tiles, with partial ring rounds.
 SMALL_BATCH_PATHS = [
     ("default routing", {}),
-    ("mv, default grid", {"GMLX_KQ_MV": "2"}),
-    ("mv, 3 workgroups", {"GMLX_KQ_MV": "2", "GMLX_KQ_MV_WGS": "3"}),
-    ("mv, 7 workgroups, ring 2", {"GMLX_KQ_MV": "2", "GMLX_KQ_MV_WGS": "7", "GMLX_KQ_MV_DEPTH": "2"}),
-    ("mv, 5 workgroups, ring 1", {"GMLX_KQ_MV": "2", "GMLX_KQ_MV_WGS": "5", "GMLX_KQ_MV_DEPTH": "1"}),
-    ("persistent, 3 workgroups", {"GMLX_KQ_MV": "0", "GMLX_KQ_QMV_WGS": "3"}),
-    ("general", {"GMLX_KQ_MV": "0", "GMLX_KQ_PERSISTENT": "0"}),
+    ("stream, 3 workgroups", {"GMLX_KQ_STREAM": "2", "GMLX_KQ_STREAM_WGS": "3"}),
+    ("stream, 13 workgroups", {"GMLX_KQ_STREAM": "2", "GMLX_KQ_STREAM_WGS": "13"}),
+    ("stream, full grid", {"GMLX_KQ_STREAM": "2"}),
+    ("mv, default grid", {"GMLX_KQ_STREAM": "0", "GMLX_KQ_MV": "2"}),
+    ("mv, 3 workgroups", {"GMLX_KQ_STREAM": "0", "GMLX_KQ_MV": "2", "GMLX_KQ_MV_WGS": "3"}),
+    ("mv, 7 workgroups, ring 2", {"GMLX_KQ_STREAM": "0", "GMLX_KQ_MV": "2", "GMLX_KQ_MV_WGS": "7",
+                                  "GMLX_KQ_MV_DEPTH": "2"}),
+    ("mv, 5 workgroups, ring 1", {"GMLX_KQ_STREAM": "0", "GMLX_KQ_MV": "2", "GMLX_KQ_MV_WGS": "5",
+                                  "GMLX_KQ_MV_DEPTH": "1"}),
+    ("persistent, 3 workgroups", {"GMLX_KQ_STREAM": "0", "GMLX_KQ_MV": "0", "GMLX_KQ_QMV_WGS": "3"}),
+    ("general", {"GMLX_KQ_STREAM": "0", "GMLX_KQ_MV": "0", "GMLX_KQ_PERSISTENT": "0"}),
 ]
+PATH_KNOBS = ("GMLX_KQ_STREAM", "GMLX_KQ_STREAM_WGS", "GMLX_KQ_MV", "GMLX_KQ_MV_WGS", "GMLX_KQ_MV_DEPTH",
+              "GMLX_KQ_QMV_WGS", "GMLX_KQ_PERSISTENT")
 
 
 @pytest.mark.parametrize("codec,N,K,M", [
@@ -200,6 +209,10 @@ SMALL_BATCH_PATHS = [
     ("q4_k", 500, 12288, 6),
     ("q4_k", 300, 8192, 16),       # two blocks per wave, the second from registers
     ("iq2_xxs", 256, 12288, 7),
+    ("q4_k", 1000, 1024, 8),       # stream: 63 tiles, a partial last tile
+    ("q4_k", 4000, 512, 2),        # stream: 250 tiles, several rounds on small grids
+    ("q6_k", 700, 2048, 7),
+    ("iq2_xxs", 330, 4096, 4),
 ])
 def test_small_batch_paths(codec, N, K, M, monkeypatch):
     """Every small-batch path matches the fp64 reference on the same inputs."""
@@ -211,7 +224,7 @@ def test_small_batch_paths(codec, N, K, M, monkeypatch):
     x = fp16_rows(rng, M, K)
     ref = okq.qmm_ref(x, wire, codec)
     for name, env in SMALL_BATCH_PATHS:
-        for k in ("GMLX_KQ_MV", "GMLX_KQ_MV_WGS", "GMLX_KQ_MV_DEPTH", "GMLX_KQ_QMV_WGS", "GMLX_KQ_PERSISTENT"):
+        for k in PATH_KNOBS:
             monkeypatch.delenv(k, raising=False)
         for k, v in env.items():
             monkeypatch.setenv(k, v)
@@ -236,7 +249,7 @@ def test_mixed_codec_group_paths(K, M, monkeypatch):
     refs = [okq.qmm_ref(x16, w, c) for w, c in mats]
     ref_i = okq.qmm_ref(x16, wi, "iq2_xxs")
     for name, env in SMALL_BATCH_PATHS:
-        for k in ("GMLX_KQ_MV", "GMLX_KQ_MV_WGS", "GMLX_KQ_MV_DEPTH", "GMLX_KQ_QMV_WGS", "GMLX_KQ_PERSISTENT"):
+        for k in PATH_KNOBS:
             monkeypatch.delenv(k, raising=False)
         for k, v in env.items():
             monkeypatch.setenv(k, v)
@@ -266,11 +279,11 @@ def test_small_batch_output_dtypes(y_dtype, monkeypatch):
     assert okq.max_rel(out.float().cpu().numpy(), ref) <= BF16_TOL
 
 
-@pytest.mark.parametrize("mv", ["2", "0"])
+@pytest.mark.parametrize("mv", ["stream", "2", "0"])
 def test_persistent_mixed_codec_group_and_determinism(mv, monkeypatch):
-    """q|k (Q4_K) and v (Q6_K) sharing x: one small-batch launch per codec
-    (LDS-staged path forced, or the register persistent path); repeated calls
-    are bitwise identical."""
+    """q|k (Q4_K) and v (Q6_K) sharing x: one small-batch launch (the
+    streaming kernel, the LDS-staged path forced, or the register persistent
+    path); repeated calls are bitwise identical."""
     from gmlx_amd import ops
     rng = np.random.default_rng(21)
     K = 4096
@@ -279,9 +292,14 @@ def test_persistent_mixed_codec_group_and_determinism(mv, monkeypatch):
     wv = quantized_weights(rng, "q6_k", 128, K)
     x16 = fp16_rows(rng, 8, K)
     x = _dev(x16)
-    monkeypatch.setenv("GMLX_KQ_QMV_WGS", "4")
-    monkeypatch.setenv("GMLX_KQ_MV_WGS", "4")
-    monkeypatch.setenv("GMLX_KQ_MV", mv)
+    if mv == "stream":
+        monkeypatch.setenv("GMLX_KQ_STREAM", "2")
+        monkeypatch.setenv("GMLX_KQ_STREAM_WGS", "4")
+    else:
+        monkeypatch.setenv("GMLX_KQ_STREAM", "0")
+        monkeypatch.setenv("GMLX_KQ_QMV_WGS", "4")
+        monkeypatch.setenv("GMLX_KQ_MV_WGS", "4")
+        monkeypatch.setenv("GMLX_KQ_MV", mv)
     outs = [ops.quantized_matmul_grouped([(x, _dev(wq), "q4_k"), (x, _dev(wk), "q4_k"), (x, _dev(wv), "q6_k")])
             for _ in range(3)]
     for o in outs[1:]:
@@ -289,3 +307,25 @@ def test_persistent_mixed_codec_group_and_determinism(mv, monkeypatch):
             assert np.array_equal(a.cpu().numpy().view(np.uint16), b.cpu().numpy().view(np.uint16))
     for o, (w, c) in zip(outs[0], [(wq, "q4_k"), (wk, "q4_k"), (wv, "q6_k")]):
         assert okq.max_rel(o.float().cpu().numpy(), okq.qmm_ref(x16, w, c)) <= TOL
+
+
+def test_stream_large_scales_take_the_two_step_form(monkeypatch):
+    """Q4_K super-blocks whose sub-block scales reach |d sc| >= 32 (weights of
+    several hundred), next to ordinary ones: a wave that meets one converts
+    that super-block in two exact steps (q, then q * dsc) instead of against
+    the -1024 dsc constant, which would overflow fp16.  Every row group
+    matches the fp64 reference on its own scale."""
+    import torch
+    from gmlx_amd import ops
+    rng = np.random.default_rng(44)
+    N, K, M = 96, 1024, 4
+    w = rng.normal(0, 0.02, size=(N, K)).astype(np.float32)
+    w[5, 256:512] *= 3e4      # one super-block of row 5 (|w| up to about 2e3)
+    w[40:48, :256] *= 1e4     # the first super-block of rows 40..47
+    wire = okq.quantize(w, "q4_k")
+    x = fp16_rows(rng, M, K)
+    ref = okq.qmm_ref(x, wire, "q4_k")
+    monkeypatch.setenv("GMLX_KQ_STREAM", "2")
+    got = ops.quantized_matmul(_dev(x), _dev(wire), None, "q4_k", out_dtype=torch.float32).cpu().numpy()
+    for rows in ([5], list(range(40, 48)), [n for n in range(N) if n != 5 and not 40 <= n < 48]):
+        assert okq.max_rel(got[:, rows], ref[:, rows]) <= TOL, rows
