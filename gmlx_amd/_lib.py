@@ -31,6 +31,7 @@ CODEC_ID = {"q4_k": 12, "q6_k": 14, "iq2_xxs": 16}
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 OP_DEQUANTIZE, OP_QUANTIZE, OP_MATMUL, OP_GATHER, OP_MOE_GLU, OP_SDPA = range(6)
 MAX_GROUP = 8
+SDPA_NOALLOC_SCRATCH_BYTES = 32 << 20  # KQ_SDPA_NOALLOC_SCRATCH_BYTES (include/kq_capi.h)
 
 # every symbol include/kq_capi.h and include/kq_gguf.h declare, checked at load
 EXPORTS = (
@@ -38,7 +39,7 @@ EXPORTS = (
     "kq_dequantize", "kq_quantize", "kq_matmul_workspace_bytes", "kq_quantized_matmul_grouped",
     "kq_moe_route", "kq_gather_qmm", "kq_moe_glu_gather", "kq_moe_gather_rows", "kq_moe_mix", "kq_moe_router_topk",
     "kq_sdpa_workspace_bytes", "kq_sdpa_decode_ragged", "kq_sdpa_decode_ragged_q8", "kq_sdpa_decode_gqa",
-    "kq_sdpa_decode_gqa_q8",
+    "kq_sdpa_decode_gqa_q8", "kq_sdpa_decode_gqa_noalloc",
     "kq_sdpa_cascade_workspace_bytes", "kq_sdpa_decode_gqa_cascade", "kq_sdpa_decode_gqa_cascade_q8",
     "kq_gguf_open", "kq_gguf_close", "kq_gguf_header", "kq_gguf_kv", "kq_gguf_tensor", "kq_gguf_type_size",
 )
@@ -134,6 +135,8 @@ _SIGS = {
                             _vp], _int),
     "kq_sdpa_decode_gqa_q8": ([_vp, _vp, _vp, _vp, _i64, _i64, _i32, _vp, _i32, _i32, _i32, _i32, _f32, _int, _vp,
                                _vp, _sz, _vp], _int),
+    "kq_sdpa_decode_gqa_noalloc": ([_vp, _vp, _vp, _i64, _i64, _i32, _vp, _i32, _i32, _i32, _i32, _f32, _int, _vp,
+                                    _vp], _int),
     "kq_sdpa_cascade_workspace_bytes": ([_i32, _i32, _i32, _i32, _i32, _i32, _i32], _sz),
     "kq_sdpa_decode_gqa_cascade_q8": ([_vp, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _i64, _i64, _i32, _vp, _i32,
                                        _i32, _i32, _i32, _i32, _f32, _int, _vp, _vp, _sz, _vp], _int),

@@ -30,6 +30,8 @@
 // once for all rows; private splits are ragged-mode units.  The merge sees
 // one split list per row: prefix splits, then private ones.
 // No cross-workgroup synchronisation happens inside a launch.
+#include <mutex>
+
 #include "kq_common.h"
 
 int device_cus();
@@ -1072,3 +1074,52 @@ int kq_sdpa_decode_gqa_cascade_q8(const void *q, const void *k_shared, const voi
 }
 
 }  // extern "C"
+
+// ---- allocation-free decode attention ------------------------------------
+// The split partials (fp32 O, m, l) of kq_sdpa_decode_gqa_noalloc live in
+// this file-scope device array: each GPU the library runs on holds its own
+// copy, from the code object's load until the process ends.  On the host the
+// array's name is a stand-in, not a device address: host code uses only the
+// per-device address hipGetSymbolAddress returns (taken once per device, with
+// that device current, on the entry point's first call there).  The partials
+// are written before they are read, so nothing needs clearing between calls;
+// calls that overlap on one GPU (two streams, or two threads) share the array
+// and race.
+static __device__ __align__(256) uint8_t scratch[KQ_SDPA_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kScratchDevices];
+
+int scratch_ptr(void **out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return KQ_ERR_LAUNCH_FAILED;
+    if (dev < 0 || dev >= kScratchDevices) return KQ_ERR_BAD_ARGUMENT;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return KQ_ERR_LAUNCH_FAILED;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return KQ_OK;
+}
+
+}  // namespace
+
+extern "C" int kq_sdpa_decode_gqa_noalloc(const void *q, const void *k, const void *v, int64_t batch_stride,
+                                          int64_t head_stride, int32_t L, const int32_t *starts, int32_t B,
+                                          int32_t Hq, int32_t Hkv, int32_t D, float scale, int dtype, void *out,
+                                          kq_stream_t stream) {
+    if (B == 0) return KQ_OK;
+    if (B < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || D <= 0 || L < 0) return KQ_ERR_BAD_SHAPE;
+    const size_t need = kq_sdpa_workspace_bytes(B, Hq, Hkv, D, L);
+    if (need > KQ_SDPA_NOALLOC_SCRATCH_BYTES) return KQ_ERR_WORKSPACE_TOO_SMALL;
+    void *ws = nullptr;
+    if (const int rc = scratch_ptr(&ws)) return rc;
+    const PaddedKv pad{batch_stride, head_stride, starts};
+    return ragged_impl(q, k, v, nullptr, nullptr, nullptr, nullptr, &pad, B, Hq, Hkv, D, L, scale, dtype, out, ws,
+                       KQ_SDPA_NOALLOC_SCRATCH_BYTES, stream);
+}

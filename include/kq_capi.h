@@ -297,6 +297,21 @@ int kq_sdpa_decode_gqa(const void *q, const void *k, const void *v, int64_t batc
                        int32_t Hkv, int32_t D, float scale, int dtype, void *out, void *workspace,
                        size_t workspace_bytes, kq_stream_t stream);
 
+/* kq_sdpa_decode_gqa with no workspace argument; it allocates nothing.  No
+ * counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The split partials live in a device array the library
+ * holds on each GPU it runs on (KQ_SDPA_NOALLOC_SCRATCH_BYTES, until the
+ * process ends); calls needing more (kq_sdpa_workspace_bytes(B, Hq, Hkv, D,
+ * L) above the limit) return KQ_ERR_WORKSPACE_TOO_SMALL and launch nothing.
+ * Same outputs as kq_sdpa_decode_gqa (the same kernels and split plan).  All
+ * calls on one GPU share the array: calls that overlap there (other streams
+ * or threads) race; order them. */
+#define KQ_SDPA_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int kq_sdpa_decode_gqa_noalloc(const void *q, const void *k, const void *v, int64_t batch_stride,
+                               int64_t head_stride, int32_t L, const int32_t *starts, int32_t B, int32_t Hq,
+                               int32_t Hkv, int32_t D, float scale, int dtype, void *out, kq_stream_t stream);
+
 /* The 8-bit affine form of kq_sdpa_decode_gqa (k_scales=, k_biases=,
  * v_scales=, v_biases=, gmlx/quantized_sdpa_fix.py:76-93, 170-182): k / v
  * uint8 [B, Hkv, L, D] with byte strides (multiples of 64), kv_scales =
