@@ -37,7 +37,8 @@ SDPA_NOALLOC_SCRATCH_BYTES = 32 << 20  # KQ_SDPA_NOALLOC_SCRATCH_BYTES (include/
 EXPORTS = (
     "kq_version", "kq_strerror", "kq_codec_block_bytes", "kq_supports", "kq_iq2xxs_grid_host",
     "kq_dequantize", "kq_quantize", "kq_matmul_workspace_bytes", "kq_quantized_matmul_grouped",
-    "kq_moe_route", "kq_gather_qmm", "kq_moe_glu_gather", "kq_moe_gather_rows", "kq_moe_mix", "kq_moe_router_topk",
+    "kq_moe_route", "kq_gather_qmm", "kq_moe_glu_gather", "kq_moe_gather_rows", "kq_gather_workspace_bytes",
+    "kq_moe_mix", "kq_moe_router_topk",
     "kq_sdpa_workspace_bytes", "kq_sdpa_decode_ragged", "kq_sdpa_decode_ragged_q8", "kq_sdpa_decode_gqa",
     "kq_sdpa_decode_gqa_q8", "kq_sdpa_decode_gqa_noalloc",
     "kq_sdpa_cascade_workspace_bytes", "kq_sdpa_decode_gqa_cascade", "kq_sdpa_decode_gqa_cascade_q8",
@@ -115,15 +116,17 @@ _SIGS = {
     "kq_iq2xxs_grid_host": ([], ctypes.POINTER(ctypes.c_uint64)),
     "kq_dequantize": ([_vp, _i64, _int, _vp, _int, _vp], _int),
     "kq_quantize": ([_vp, _i64, _i64, _i64, _int, _vp, _vp], _int),
-    "kq_matmul_workspace_bytes": ([ctypes.POINTER(MatmulProblem), _int], _sz),
+    "kq_matmul_workspace_bytes": ([ctypes.POINTER(MatmulProblem), _int, _int], _sz),
     "kq_quantized_matmul_grouped": ([ctypes.POINTER(MatmulProblem), _int, _int, _int, _vp, _sz, _vp], _int),
     "kq_moe_route": ([_vp, _i32, _i32, _vp, _vp, _vp], _int),
     "kq_gather_qmm": ([_vp, _int, _i64, _i32, _vp, _i64, _i64, _i32, _i32, _int, _vp, _vp, _i32, _i32,
-                       _vp, _int, _i64, _vp], _int),
+                       _vp, _int, _i64, _vp, _sz, _vp], _int),
     "kq_moe_glu_gather": ([_vp, _int, _i64, _i32, _vp, _vp, _i64, _i64, _i32, _i32, _int, _int, _vp, _vp,
-                           _i32, _i32, _vp, _vp], _int),
+                           _i32, _i32, _vp, _vp, _sz, _vp], _int),
     "kq_moe_gather_rows": ([_vp, _int, _i64, _i32, _i32, _vp, _vp, _i64, _i64, _i32, _i32, _int,
-                            ctypes.POINTER(GatherEpilogue), _vp, _vp, _i32, _i32, _vp, _int, _i64, _i32, _vp], _int),
+                            ctypes.POINTER(GatherEpilogue), _vp, _vp, _i32, _i32, _vp, _int, _i64, _i32, _vp, _sz,
+                            _vp], _int),
+    "kq_gather_workspace_bytes": ([_i32, _i32, _i32, _i32, _int], _sz),
     "kq_moe_mix": ([_vp, _vp, _i32, _i32, _i32, _vp, _int, _vp], _int),
     "kq_moe_router_topk": ([_vp, _int, _i64, _i32, _i32, _i32, ctypes.POINTER(RouterOptions), _vp, _vp, _vp],
                            _int),

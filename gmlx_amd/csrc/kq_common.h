@@ -10,6 +10,13 @@
 #define KQ_QK 256
 
 typedef _Float16 kq_half;
+
+// bf16 / fp32 activations as fp16 rows with a power-of-two scale per row
+// (kq_prepare.hip): bytes for `rows` rows of K, and the launch that fills
+// them (the exponents follow the rows; results scale back by 2^exp[row]).
+size_t kq_prepared_bytes(int64_t rows, int64_t K);
+int kq_prepare_rows(const void *x, int x_dtype, int64_t x_stride, int32_t rows, int32_t K, void *out,
+                    const int32_t **exp_out, const void **x16_out, hipStream_t s);
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));

@@ -19,20 +19,20 @@
 // kq_mv.hip: LDS-staged small-batch launch (problems validated, all live,
 // one codec, sharing x / M <= 16, x rows fitting in LDS).
 bool kq_mv_eligible(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype);
-int kq_mv_launch(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype, hipStream_t s);
+int kq_mv_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, int y_dtype, hipStream_t s);
 // kq_stream.hip: weight-streaming launch for M <= 8 (problems validated, all
 // live, fp16 x shared, one codec or Q4_K with Q6_K, K as its slab plan allows).
 bool kq_stream_eligible(const kq_matmul_problem *ps, int n);
 int kq_stream_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, int y_dtype, hipStream_t s);
 // kq_qmv.hip: persistent small-batch launch (problems validated, all live,
 // sharing codec / x / M <= 16 / K <= 8192).
-int kq_qmv_persistent_launch(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype, hipStream_t s);
+int kq_qmv_persistent_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, int y_dtype, hipStream_t s);
 // workgroups one persistent launch of this problem's codec / K would use
 int kq_qmv_persistent_grid(const kq_matmul_problem &q);
 // kq_mm.hip: batches of 17..64 rows (problems validated, all live, Q4_K /
 // Q6_K, sharing x / M / K).
 bool kq_mm_eligible(const kq_matmul_problem *ps, int n, int x_dtype);
-int kq_mm_launch(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype, hipStream_t s);
+int kq_mm_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, int y_dtype, hipStream_t s);
 int device_cus();
 
 namespace {
@@ -50,6 +50,7 @@ int env_int(const char *name, int dflt) {
 struct DenseProblem {
     const uint8_t *w;
     const char *x;
+    const int32_t *x_exp;  // per-row exponents of prepared activations (results * 2^e), or null
     void *y;
     int64_t w_row_bytes, x_stride, y_stride;
     int32_t M, N, K, codec;
@@ -64,13 +65,13 @@ struct DenseArgs {
 };
 
 __device__ __forceinline__ void store_tile(void *y, int y_dtype, int64_t y_stride, int m0, int M,
-                                           int n, bool n_valid, const floatx4 &c) {
+                                           int n, bool n_valid, const floatx4 &c, const int32_t *x_exp) {
     const int lane = kq_lane();
     if (!n_valid) return;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int m = m0 + 4 * (lane >> 4) + e;
-        if (m < M) kq_store_out(y, y_dtype, (int64_t)m * y_stride + n, c[e]);
+        if (m < M) kq_store_out(y, y_dtype, (int64_t)m * y_stride + n, x_exp ? ldexpf(c[e], x_exp[m]) : c[e]);
     }
 }
 
@@ -139,7 +140,7 @@ __global__ __launch_bounds__(64 * WV) void kq_dense_grouped_kernel(DenseArgs a) 
         const int n = (nt * NW + i) * 16 + (lane & 15);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
-            store_tile(p.y, a.y_dtype, p.y_stride, m0 + 16 * mt, p.M, n, n < p.N, acc[i][mt]);
+            store_tile(p.y, a.y_dtype, p.y_stride, m0 + 16 * mt, p.M, n, n < p.N, acc[i][mt], p.x_exp);
     }
 }
 
@@ -162,6 +163,7 @@ struct GatherArgs {
     float limit, alpha;
     const float *b0, *b1;
     int64_t b_stride;
+    const int32_t *x_exp;  // per-row exponents of prepared activations (results * 2^e), or null
 };
 
 __device__ __forceinline__ int64_t gather_x_row(const GatherArgs &a, int pair) {
@@ -294,7 +296,9 @@ __attribute__((amdgpu_waves_per_eu(gather_waves_per_simd<CODEC, MT, NW, XT>())))
                     const int ri = c0 + 16 * mt + 4 * (lane >> 4) + e;
                     if (ri >= seg_end) continue;
                     const int pair = a.pair_order[ri];
-                    const float v = gather_epilogue<NW>(a, expert, n, acc[0][mt][e], acc[NW - 1][mt][e]);
+                    const int ex = a.x_exp ? a.x_exp[gather_x_row(a, pair)] : 0;
+                    const float v = gather_epilogue<NW>(a, expert, n, ldexpf(acc[0][mt][e], ex),
+                                                        ldexpf(acc[NW - 1][mt][e], ex));
                     kq_store_out(a.y, a.y_dtype, gather_y_row(a, pair) * a.y_stride + n, v);
                 }
             }
@@ -391,7 +395,9 @@ __attribute__((amdgpu_waves_per_eu(gather_waves_per_simd<CODEC, MT, NW, XT>())))
                 const int ri = c0 + 16 * mt + 4 * (lane >> 4) + e;
                 if (ri >= seg_end) continue;
                 const int pair = a.pair_order[ri];
-                const float v = gather_epilogue<NW>(a, expert, n, acc[0][mt][e], acc[NW - 1][mt][e]);
+                const int ex = a.x_exp ? a.x_exp[gather_x_row(a, pair)] : 0;
+                const float v = gather_epilogue<NW>(a, expert, n, ldexpf(acc[0][mt][e], ex),
+                                                    ldexpf(acc[NW - 1][mt][e], ex));
                 kq_store_out(a.y, a.y_dtype, gather_y_row(a, pair) * a.y_stride + n, v);
             }
         }
@@ -802,11 +808,18 @@ void launch_gather(int codec, int mt, const GatherArgs &a, int grid, hipStream_t
     else launch_gather_codec<KQ_CODEC_IQ2_XXS, XT, NW>(mt, a, grid, s);
 }
 
+// Activation rows a gather reads: pair p uses row p / x_pair_div + p / x_skip.
+int32_t gather_x_rows(int32_t n_pairs, int32_t x_pair_div, int32_t x_skip) {
+    if (n_pairs <= 0) return 0;
+    return (n_pairs - 1) / x_pair_div + (x_skip ? (n_pairs - 1) / x_skip : 0) + 1;
+}
+
 int gather_common(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pair_div, const void *w0,
                   const void *w1, int64_t w_expert_bytes, int64_t w_row_bytes, int32_t N, int32_t K,
                   int codec, const kq_gather_epilogue *ep, const int32_t *seg_info, const int32_t *pair_order,
                   int32_t n_pairs, int32_t n_experts, void *y, int y_dtype, int64_t y_row_stride,
-                  hipStream_t s, int32_t x_skip = 0, int32_t y_skip = 0) {
+                  void *workspace, size_t workspace_bytes, hipStream_t s, int32_t x_skip = 0,
+                  int32_t y_skip = 0) {
     if (!x || !w0 || !seg_info || !pair_order || !y) return KQ_ERR_NULL_POINTER;
     if (kq_block_bytes(codec) == 0) return KQ_ERR_UNSUPPORTED_CODEC;
     if (x_dtype != KQ_DTYPE_F16 && x_dtype != KQ_DTYPE_BF16 && x_dtype != KQ_DTYPE_F32)
@@ -834,8 +847,20 @@ int gather_common(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pa
     if (((uintptr_t)ep->bias0 | (uintptr_t)ep->bias1) & 3) return KQ_ERR_BAD_ALIGN;
     if ((ep->act == KQ_ACT_SILU_LIMIT || ep->act == KQ_ACT_SWIGLU_CLAMP) && w1 && !(ep->limit > 0.f))
         return KQ_ERR_BAD_ARGUMENT;
+    // bf16 / fp32 activations: fp16 rows with a power of two per row first
+    const int32_t *x_exp = nullptr;
+    if (x_dtype != KQ_DTYPE_F16) {
+        const int32_t rows = gather_x_rows(n_pairs, x_pair_div, x_skip);
+        if (!workspace || workspace_bytes < kq_prepared_bytes(rows, K)) return KQ_ERR_WORKSPACE_TOO_SMALL;
+        const void *x16 = nullptr;
+        if (const int rc = kq_prepare_rows(x, x_dtype, x_row_stride, rows, K, workspace, &x_exp, &x16, s)) return rc;
+        x = x16;
+        x_row_stride = K;
+        x_dtype = KQ_DTYPE_F16;
+    }
     GatherArgs a;
     a.x = (const char *)x;
+    a.x_exp = x_exp;
     a.w0 = (const uint8_t *)w0;
     a.w1 = (const uint8_t *)w1;
     a.y = y;
@@ -867,15 +892,8 @@ int gather_common(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pa
     const int rows = (n_pairs + slots - 1) / slots;
     const int mt = rows <= 16 ? 1 : rows <= 32 ? 2 : 4;
     const int grid = slots * a.n_tiles;
-    if (w1) {
-        if (x_dtype == KQ_DTYPE_F16) launch_gather<0, 2>(codec, mt, a, grid, s);
-        else if (x_dtype == KQ_DTYPE_BF16) launch_gather<1, 2>(codec, mt, a, grid, s);
-        else launch_gather<2, 2>(codec, mt, a, grid, s);
-    } else {
-        if (x_dtype == KQ_DTYPE_F16) launch_gather<0, 1>(codec, mt, a, grid, s);
-        else if (x_dtype == KQ_DTYPE_BF16) launch_gather<1, 1>(codec, mt, a, grid, s);
-        else launch_gather<2, 1>(codec, mt, a, grid, s);
-    }
+    if (w1) launch_gather<0, 2>(codec, mt, a, grid, s);
+    else launch_gather<0, 1>(codec, mt, a, grid, s);
     return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
 }
 
@@ -883,26 +901,62 @@ int gather_common(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pa
 
 extern "C" {
 
-size_t kq_matmul_workspace_bytes(const kq_matmul_problem *problems, int n_problems) {
-    (void)problems;
-    (void)n_problems;
-    return 0;  // K splits are reduced inside a workgroup
+size_t kq_matmul_workspace_bytes(const kq_matmul_problem *problems, int n_problems, int x_dtype) {
+    if (!problems || n_problems <= 0 || x_dtype == KQ_DTYPE_F16) return 0;
+    size_t b = 0;  // a prepared copy per problem (problems sharing x share one)
+    for (int i = 0; i < n_problems && i < KQ_MAX_GROUP; ++i)
+        if (problems[i].M > 0 && problems[i].N > 0) b += kq_prepared_bytes(problems[i].M, problems[i].K);
+    return b;
 }
 
 int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problems, int x_dtype,
                                 int y_dtype, void *workspace, size_t workspace_bytes,
                                 kq_stream_t stream) {
-    (void)workspace;
-    (void)workspace_bytes;
     if (!problems) return KQ_ERR_NULL_POINTER;
     if (n_problems <= 0) return KQ_ERR_BAD_ARGUMENT;
     if (n_problems > KQ_MAX_GROUP) return KQ_ERR_TOO_MANY_PROBLEMS;
-    if (x_dtype != KQ_DTYPE_F16 && x_dtype != KQ_DTYPE_BF16) return KQ_ERR_UNSUPPORTED_DTYPE;
+    if (x_dtype != KQ_DTYPE_F16 && x_dtype != KQ_DTYPE_BF16 && x_dtype != KQ_DTYPE_F32)
+        return KQ_ERR_UNSUPPORTED_DTYPE;
     if (y_dtype != KQ_DTYPE_F32 && y_dtype != KQ_DTYPE_F16 && y_dtype != KQ_DTYPE_BF16)
         return KQ_ERR_UNSUPPORTED_DTYPE;
     for (int i = 0; i < n_problems; ++i) {
         const int rc = validate_problem(problems[i]);
         if (rc != KQ_OK) return rc;
+    }
+    // bf16 / fp32 activations: fp16 rows with a power of two per row, once per
+    // distinct x; every kernel below then reads fp16 and scales its fp32
+    // results back (x_exp)
+    kq_matmul_problem prep[KQ_MAX_GROUP];
+    const int32_t *exps[KQ_MAX_GROUP] = {};
+    if (x_dtype != KQ_DTYPE_F16) {
+        if (!workspace || workspace_bytes < kq_matmul_workspace_bytes(problems, n_problems, x_dtype))
+            return KQ_ERR_WORKSPACE_TOO_SMALL;
+        size_t off = 0;
+        for (int i = 0; i < n_problems; ++i) {
+            prep[i] = problems[i];
+            if (prep[i].M == 0 || prep[i].N == 0) continue;
+            int j = 0;
+            for (; j < i; ++j)
+                if (exps[j] && problems[j].x == problems[i].x && problems[j].x_row_stride == problems[i].x_row_stride &&
+                    problems[j].M == problems[i].M && problems[j].K == problems[i].K)
+                    break;
+            if (j < i) {
+                prep[i].x = prep[j].x;
+                prep[i].x_row_stride = prep[j].x_row_stride;
+                exps[i] = exps[j];
+                continue;
+            }
+            const void *x16 = nullptr;
+            const int rc = kq_prepare_rows(problems[i].x, x_dtype, problems[i].x_row_stride, problems[i].M,
+                                           problems[i].K, (char *)workspace + off, &exps[i], &x16,
+                                           (hipStream_t)stream);
+            if (rc != KQ_OK) return rc;
+            prep[i].x = x16;
+            prep[i].x_row_stride = problems[i].K;
+            off += kq_prepared_bytes(problems[i].M, problems[i].K);
+        }
+        problems = prep;
+        x_dtype = KQ_DTYPE_F16;
     }
     // live problems by codec (the small-batch paths launch once per codec)
     int by_codec[3][KQ_MAX_GROUP], cnt[3] = {0, 0, 0};
@@ -916,6 +970,12 @@ int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problem
                 if (problems[i].codec == codecs[c]) by_codec[c][cnt[c]++] = i;
         }
     }
+    const int32_t *xe0 = nullptr;  // exponents of the first live problem's rows (shared-x launches)
+    for (int i = 0; i < n_problems; ++i)
+        if (problems[i].M != 0 && problems[i].N != 0) {
+            xe0 = exps[i];
+            break;
+        }
     // small batches with activations that fit in LDS: the LDS-staged path.
     // Other codec mixes (IQ2_XXS with K-quants) take one launch per codec
     // only when every codec's launch is large (four tiles per CU); otherwise
@@ -927,10 +987,8 @@ int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problem
         int na = 0;
         for (int i = 0; i < n_problems; ++i)
             if (problems[i].M != 0 && problems[i].N != 0) all[na++] = problems[i];
-        if (x_dtype == KQ_DTYPE_F16 && kq_stream_eligible(all, na))
-            return kq_stream_launch(all, na, nullptr, y_dtype, (hipStream_t)stream);
-        if (kq_mv_eligible(all, na, x_dtype, y_dtype))
-            return kq_mv_launch(all, na, x_dtype, y_dtype, (hipStream_t)stream);
+        if (kq_stream_eligible(all, na)) return kq_stream_launch(all, na, xe0, y_dtype, (hipStream_t)stream);
+        if (kq_mv_eligible(all, na, x_dtype, y_dtype)) return kq_mv_launch(all, na, xe0, y_dtype, (hipStream_t)stream);
     }
     if (live > 0 && mv_mode) {
         bool ok = true;
@@ -949,7 +1007,7 @@ int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problem
         if (ok) {
             for (int c = 0; c < 3; ++c) {
                 if (!cnt[c]) continue;
-                const int rc = kq_mv_launch(sub[c], cnt[c], x_dtype, y_dtype, (hipStream_t)stream);
+                const int rc = kq_mv_launch(sub[c], cnt[c], exps[by_codec[c][0]], y_dtype, (hipStream_t)stream);
                 if (rc != KQ_OK) return rc;
             }
             return KQ_OK;
@@ -963,7 +1021,7 @@ int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problem
         int na = 0;
         for (int i = 0; i < n_problems; ++i)
             if (problems[i].M != 0 && problems[i].N != 0) all[na++] = problems[i];
-        if (kq_mm_eligible(all, na, x_dtype)) return kq_mm_launch(all, na, x_dtype, y_dtype, (hipStream_t)stream);
+        if (kq_mm_eligible(all, na, x_dtype)) return kq_mm_launch(all, na, xe0, y_dtype, (hipStream_t)stream);
     }
     // small batches: one persistent launch per codec when every codec's
     // problems share their activations (q|k|v, gate|up of one layer)
@@ -984,7 +1042,8 @@ int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problem
                 if (!cnt[c]) continue;
                 kq_matmul_problem sub[KQ_MAX_GROUP];
                 for (int i = 0; i < cnt[c]; ++i) sub[i] = problems[by_codec[c][i]];
-                const int rc = kq_qmv_persistent_launch(sub, cnt[c], x_dtype, y_dtype, (hipStream_t)stream);
+                const int rc =
+                    kq_qmv_persistent_launch(sub, cnt[c], exps[by_codec[c][0]], y_dtype, (hipStream_t)stream);
                 if (rc != KQ_OK) return rc;
             }
             return KQ_OK;
@@ -1001,6 +1060,7 @@ int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problem
         DenseProblem &p = a.p[np++];
         p.w = (const uint8_t *)q.w;
         p.x = (const char *)q.x;
+        p.x_exp = exps[i];
         p.y = q.y;
         p.w_row_bytes = q.w_row_bytes;
         p.x_stride = q.x_row_stride;
@@ -1019,14 +1079,9 @@ int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problem
     a.n_problems = np;
     a.y_dtype = y_dtype;
     hipStream_t s = (hipStream_t)stream;
-    const bool bf = x_dtype == KQ_DTYPE_BF16;
-    if (mt == 1) {
-        bf ? launch_dense_nw<1, 1>(nw, a, units, max_chunks, s) : launch_dense_nw<1, 0>(nw, a, units, max_chunks, s);
-    } else if (mt == 2) {
-        bf ? launch_dense_nw<2, 1>(nw, a, units, max_chunks, s) : launch_dense_nw<2, 0>(nw, a, units, max_chunks, s);
-    } else {
-        bf ? launch_dense_nw<4, 1>(nw, a, units, max_chunks, s) : launch_dense_nw<4, 0>(nw, a, units, max_chunks, s);
-    }
+    if (mt == 1) launch_dense_nw<1, 0>(nw, a, units, max_chunks, s);
+    else if (mt == 2) launch_dense_nw<2, 0>(nw, a, units, max_chunks, s);
+    else launch_dense_nw<4, 0>(nw, a, units, max_chunks, s);
     return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
 }
 
@@ -1043,34 +1098,41 @@ int kq_moe_route(const int32_t *idx, int32_t n_pairs, int32_t n_experts, int32_t
 int kq_gather_qmm(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pair_div, const void *w,
                   int64_t w_expert_bytes, int64_t w_row_bytes, int32_t N, int32_t K, int codec,
                   const int32_t *seg_info, const int32_t *pair_order, int32_t n_pairs,
-                  int32_t n_experts, void *y, int y_dtype, int64_t y_row_stride, kq_stream_t stream) {
+                  int32_t n_experts, void *y, int y_dtype, int64_t y_row_stride, void *workspace,
+                  size_t workspace_bytes, kq_stream_t stream) {
     return gather_common(x, x_dtype, x_row_stride, x_pair_div, w, nullptr, w_expert_bytes, w_row_bytes,
                          N, K, codec, nullptr, seg_info, pair_order, n_pairs, n_experts, y, y_dtype,
-                         y_row_stride, (hipStream_t)stream);
+                         y_row_stride, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 int kq_moe_glu_gather(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pair_div,
                       const void *w_gate, const void *w_up, int64_t w_expert_bytes, int64_t w_row_bytes,
                       int32_t N, int32_t K, int codec, int act, const int32_t *seg_info,
                       const int32_t *pair_order, int32_t n_pairs, int32_t n_experts, float *h,
-                      kq_stream_t stream) {
+                      void *workspace, size_t workspace_bytes, kq_stream_t stream) {
     if (!w_up) return KQ_ERR_NULL_POINTER;
     if (act != KQ_ACT_SILU && act != KQ_ACT_GELU) return KQ_ERR_BAD_ARGUMENT;
     const kq_gather_epilogue ep{act, 0.f, 0.f, nullptr, nullptr, 0};
     return gather_common(x, x_dtype, x_row_stride, x_pair_div, w_gate, w_up, w_expert_bytes, w_row_bytes,
                          N, K, codec, &ep, seg_info, pair_order, n_pairs, n_experts, h, KQ_DTYPE_F32, N,
-                         (hipStream_t)stream);
+                         workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 int kq_moe_gather_rows(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pair_div, int32_t x_skip,
                        const void *w0, const void *w1, int64_t w_expert_bytes, int64_t w_row_bytes, int32_t N,
                        int32_t K, int codec, const kq_gather_epilogue *ep, const int32_t *seg_info,
                        const int32_t *pair_order, int32_t n_pairs, int32_t n_experts, void *y, int y_dtype,
-                       int64_t y_row_stride, int32_t y_skip, kq_stream_t stream) {
+                       int64_t y_row_stride, int32_t y_skip, void *workspace, size_t workspace_bytes,
+                       kq_stream_t stream) {
     if (w1 && y_dtype != KQ_DTYPE_F32) return KQ_ERR_UNSUPPORTED_DTYPE;
     return gather_common(x, x_dtype, x_row_stride, x_pair_div, w0, w1, w_expert_bytes, w_row_bytes, N, K, codec,
-                         ep, seg_info, pair_order, n_pairs, n_experts, y, y_dtype, y_row_stride,
-                         (hipStream_t)stream, x_skip, y_skip);
+                         ep, seg_info, pair_order, n_pairs, n_experts, y, y_dtype, y_row_stride, workspace,
+                         workspace_bytes, (hipStream_t)stream, x_skip, y_skip);
+}
+
+size_t kq_gather_workspace_bytes(int32_t n_pairs, int32_t x_pair_div, int32_t x_skip, int32_t K, int x_dtype) {
+    if (x_dtype == KQ_DTYPE_F16 || n_pairs <= 0 || x_pair_div <= 0 || x_skip < 0 || K <= 0) return 0;
+    return kq_prepared_bytes(gather_x_rows(n_pairs, x_pair_div, x_skip), K);
 }
 
 int kq_moe_mix(const float *y_pairs, const float *scores, int32_t T, int32_t top_k, int32_t N, void *y,

@@ -54,6 +54,7 @@ struct MmArgs {
     int32_t group_begin[KQ_MAX_GROUP];  // first group of each problem; unused: INT_MAX
     MmProblem p[KQ_MAX_GROUP];
     const char *x;
+    const int32_t *x_exp;  // per-row exponents of prepared activations (results * 2^e), or null
     int64_t x_stride;  // elements
     int32_t M, K, y_dtype, total_groups, n_problems;
 };
@@ -201,7 +202,7 @@ __device__ __forceinline__ void mm_group(KArgs A, const uint8_t *w, int64_t w_ro
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int m = 16 * mt + 4 * (fl >> 4) + e;
-                if (m < M) kq_store_out(y, y_dtype, (int64_t)m * y_stride + n, s[e]);
+                if (m < M) kq_store_out(y, y_dtype, (int64_t)m * y_stride + n, A->x_exp ? ldexpf(s[e], A->x_exp[m]) : s[e]);
             }
         }
     }
@@ -266,9 +267,9 @@ int mm_launch_t(const MmArgs &a, int t, int grid, hipStream_t s) {
 }
 
 template <int SET>
-int mm_launch_set(const MmArgs &a, int mt, bool bf, int t, int grid, hipStream_t s) {
-    if (mt == 2) return bf ? mm_launch_t<SET, 2, 1>(a, t, grid, s) : mm_launch_t<SET, 2, 0>(a, t, grid, s);
-    return bf ? mm_launch_t<SET, 4, 1>(a, t, grid, s) : mm_launch_t<SET, 4, 0>(a, t, grid, s);
+int mm_launch_set(const MmArgs &a, int mt, int t, int grid, hipStream_t s) {
+    if (mt == 2) return mm_launch_t<SET, 2, 0>(a, t, grid, s);
+    return mm_launch_t<SET, 4, 0>(a, t, grid, s);
 }
 
 int mm_env_int(const char *name, int dflt) {
@@ -286,7 +287,7 @@ int mm_env_int(const char *name, int dflt) {
 // x and its row stride 16-byte aligned, x addressable with 31-bit offsets.
 bool kq_mm_eligible(const kq_matmul_problem *ps, int n, int x_dtype) {
     if (n <= 0) return false;
-    if (x_dtype != KQ_DTYPE_F16 && x_dtype != KQ_DTYPE_BF16) return false;
+    if (x_dtype != KQ_DTYPE_F16) return false;
     const kq_matmul_problem &q0 = ps[0];
     if (q0.M < 17 || q0.M > 64) return false;
     // 16-byte activation pieces: x and its row stride 16-byte aligned
@@ -306,7 +307,7 @@ bool kq_mm_eligible(const kq_matmul_problem *ps, int n, int x_dtype) {
 // to the register limit (Q4_K 6 at M <= 32, 3 above; any Q6_K 2); more tiles
 // take several rounds of equal groups (GMLX_KQ_MM_T forces T; a T between the
 // instantiated sizes takes the next larger one).
-int kq_mm_launch(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype, hipStream_t s) {
+int kq_mm_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, int y_dtype, hipStream_t s) {
     bool any4 = false, any6 = false;
     int tiles = 0;
     for (int i = 0; i < n; ++i) {
@@ -346,6 +347,7 @@ int kq_mm_launch(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype, h
         a.group_begin[i] = 0x7FFFFFFF;
     }
     a.x = (const char *)ps[0].x;
+    a.x_exp = x_exp;
     a.x_stride = ps[0].x_row_stride;
     a.M = ps[0].M;
     a.K = ps[0].K;
@@ -353,10 +355,9 @@ int kq_mm_launch(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype, h
     a.total_groups = groups;
     a.n_problems = n;
     const int grid = groups < cus ? groups : cus;
-    const bool bf = x_dtype == KQ_DTYPE_BF16;
     switch (set) {
-    case kSetQ4K: return mm_launch_set<kSetQ4K>(a, mt, bf, t, grid, s);
-    case kSetQ6K: return mm_launch_set<kSetQ6K>(a, mt, bf, t, grid, s);
-    default: return mm_launch_set<kSetMix>(a, mt, bf, t, grid, s);
+    case kSetQ4K: return mm_launch_set<kSetQ4K>(a, mt, t, grid, s);
+    case kSetQ6K: return mm_launch_set<kSetQ6K>(a, mt, t, grid, s);
+    default: return mm_launch_set<kSetMix>(a, mt, t, grid, s);
     }
 }

@@ -64,6 +64,7 @@ struct MvArgs {
     int32_t tile_begin[KQ_MAX_GROUP];  // first tile of each problem; unused: INT_MAX
     MvProblem p[KQ_MAX_GROUP];
     const char *x;
+    const int32_t *x_exp;              // per-row exponents of prepared activations (results * 2^e), or null
     int64_t x_stride;                  // elements
     int32_t M, K, y_dtype, total_tiles;
     int32_t n_problems;
@@ -431,6 +432,7 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(4))) vo
         float sum = rb[4 * src_lane + src_e];
 #pragma unroll
         for (int w = 1; w < WV; ++w) sum += rb[4 * (w * 64 + src_lane) + src_e];
+        if (A->x_exp && out_lane) sum = ldexpf(sum, A->x_exp[out_m]);
         const int n = (tile - sc.begin) * 16 + out_n;
         const __amdgpu_buffer_rsrc_t ys = kq_buffer(sc.y, sc.y_bytes);
         const uint32_t yo = (out_lane && n < sc.N) ? (uint32_t)(out_m * sc.y_stride + n) * (y_f32 ? 4u : 2u) : kOut;
@@ -568,12 +570,12 @@ bool mv_mixed(const kq_matmul_problem *ps, int n) {
 
 // Eligibility of a set of problems for the LDS-staged small-batch path: one
 // codec (or Q4_K and Q6_K together, K <= 8192, x all in LDS), shared x /
-// stride / M / K, M <= 16, fp16 or bf16 activations, x rows that fit in LDS
+// stride / M / K, M <= 16, fp16 activations, x rows that fit in LDS
 // (all but the last 4096 columns, when K > 4096), at most 3 blocks per wave,
 // weights and outputs addressable with 31-bit buffer offsets.
 bool kq_mv_eligible(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype) {
     if (n <= 0) return false;
-    if (x_dtype != KQ_DTYPE_F16 && x_dtype != KQ_DTYPE_BF16) return false;
+    if (x_dtype != KQ_DTYPE_F16) return false;
     const kq_matmul_problem &q0 = ps[0];
     if (q0.M < 1 || q0.M > 16) return false;
     const int nb = q0.K / KQ_QK;
@@ -593,7 +595,7 @@ bool kq_mv_eligible(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype
 }
 
 // Problems validated and eligible (kq_mv_eligible), all live.
-int kq_mv_launch(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype, hipStream_t s) {
+int kq_mv_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, int y_dtype, hipStream_t s) {
     MvArgs a;
     int tiles = 0;
     for (int i = 0; i < n; ++i) {
@@ -615,6 +617,7 @@ int kq_mv_launch(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype, h
     }
     const kq_matmul_problem &q0 = ps[0];
     a.x = (const char *)q0.x;
+    a.x_exp = x_exp;
     a.x_stride = q0.x_row_stride;
     a.M = q0.M;
     a.K = q0.K;
@@ -648,35 +651,18 @@ int kq_mv_launch(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype, h
     const int per_wg = (tiles + grid - 1) / grid;
     const int depth = env_int("GMLX_KQ_MV_DEPTH", per_wg >= 4 ? 3 : per_wg >= 2 ? 2 : 1);
     const int d = min(depth, nbw == 1 ? 3 : 2);
-    const bool bf = x_dtype == KQ_DTYPE_BF16;
     if (w8) {
-        if (mixed)
-            return bf ? launch_shape<KQ_MIX, 1, 8>(a, nbw, d, false, grid, lds, s)
-                      : launch_shape<KQ_MIX, 0, 8>(a, nbw, d, false, grid, lds, s);
+        if (mixed) return launch_shape<KQ_MIX, 0, 8>(a, nbw, d, false, grid, lds, s);
         switch (q0.codec) {
-        case KQ_CODEC_Q4_K:
-            return bf ? launch_shape<KQ_CODEC_Q4_K, 1, 8>(a, nbw, d, false, grid, lds, s)
-                      : launch_shape<KQ_CODEC_Q4_K, 0, 8>(a, nbw, d, false, grid, lds, s);
-        case KQ_CODEC_Q6_K:
-            return bf ? launch_shape<KQ_CODEC_Q6_K, 1, 8>(a, nbw, d, false, grid, lds, s)
-                      : launch_shape<KQ_CODEC_Q6_K, 0, 8>(a, nbw, d, false, grid, lds, s);
-        default:
-            return bf ? launch_shape<KQ_CODEC_IQ2_XXS, 1, 8>(a, nbw, d, false, grid, lds, s)
-                      : launch_shape<KQ_CODEC_IQ2_XXS, 0, 8>(a, nbw, d, false, grid, lds, s);
+        case KQ_CODEC_Q4_K: return launch_shape<KQ_CODEC_Q4_K, 0, 8>(a, nbw, d, false, grid, lds, s);
+        case KQ_CODEC_Q6_K: return launch_shape<KQ_CODEC_Q6_K, 0, 8>(a, nbw, d, false, grid, lds, s);
+        default: return launch_shape<KQ_CODEC_IQ2_XXS, 0, 8>(a, nbw, d, false, grid, lds, s);
         }
     }
-    if (mixed)
-        return bf ? launch_shape<KQ_MIX, 1, 16>(a, nbw, d, xr, grid, lds, s)
-                  : launch_shape<KQ_MIX, 0, 16>(a, nbw, d, xr, grid, lds, s);
+    if (mixed) return launch_shape<KQ_MIX, 0, 16>(a, nbw, d, xr, grid, lds, s);
     switch (q0.codec) {
-    case KQ_CODEC_Q4_K:
-        return bf ? launch_shape<KQ_CODEC_Q4_K, 1, 16>(a, nbw, d, xr, grid, lds, s)
-                  : launch_shape<KQ_CODEC_Q4_K, 0, 16>(a, nbw, d, xr, grid, lds, s);
-    case KQ_CODEC_Q6_K:
-        return bf ? launch_shape<KQ_CODEC_Q6_K, 1, 16>(a, nbw, d, xr, grid, lds, s)
-                  : launch_shape<KQ_CODEC_Q6_K, 0, 16>(a, nbw, d, xr, grid, lds, s);
-    default:
-        return bf ? launch_shape<KQ_CODEC_IQ2_XXS, 1, 16>(a, nbw, d, xr, grid, lds, s)
-                  : launch_shape<KQ_CODEC_IQ2_XXS, 0, 16>(a, nbw, d, xr, grid, lds, s);
+    case KQ_CODEC_Q4_K: return launch_shape<KQ_CODEC_Q4_K, 0, 16>(a, nbw, d, xr, grid, lds, s);
+    case KQ_CODEC_Q6_K: return launch_shape<KQ_CODEC_Q6_K, 0, 16>(a, nbw, d, xr, grid, lds, s);
+    default: return launch_shape<KQ_CODEC_IQ2_XXS, 0, 16>(a, nbw, d, xr, grid, lds, s);
     }
 }

@@ -189,6 +189,7 @@ struct QmvProblem {
 struct QmvArgs {
     QmvProblem p[kMaxProblems];
     const char *x;
+    const int32_t *x_exp;  // per-row exponents of prepared activations (results * 2^e), or null
     int64_t x_stride;  // elements
     int32_t n_problems, M, K, y_dtype, total_tiles;
 };
@@ -266,7 +267,9 @@ __global__ __launch_bounds__(64 * max_waves<CODEC>()) void kq_qmv_persistent_ker
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int m = 4 * g + e;
-                    if (m < a.M) kq_store_out(pc.y, a.y_dtype, (int64_t)m * pc.y_stride + n, acc[e]);
+                    if (m < a.M)
+                        kq_store_out(pc.y, a.y_dtype, (int64_t)m * pc.y_stride + n,
+                                     a.x_exp ? ldexpf(acc[e], a.x_exp[m]) : acc[e]);
                 }
             }
         }
@@ -290,7 +293,9 @@ __global__ __launch_bounds__(64 * max_waves<CODEC>()) void kq_qmv_persistent_ker
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int m = 4 * g + e;
-                    if (m < a.M) kq_store_out(pc.y, a.y_dtype, (int64_t)m * pc.y_stride + n, acc[e]);
+                    if (m < a.M)
+                        kq_store_out(pc.y, a.y_dtype, (int64_t)m * pc.y_stride + n,
+                                     a.x_exp ? ldexpf(acc[e], a.x_exp[m]) : acc[e]);
                 }
             }
         }
@@ -310,9 +315,8 @@ int env_int(const char *name, int dflt) {
 }
 
 template <int CODEC>
-void launch_codec(const QmvArgs &a, int S, int grid, bool bf, hipStream_t s) {
-    if (bf) hipLaunchKernelGGL((kq_qmv_persistent_kernel<CODEC, 1>), dim3(grid), dim3(64 * S), 0, s, a);
-    else hipLaunchKernelGGL((kq_qmv_persistent_kernel<CODEC, 0>), dim3(grid), dim3(64 * S), 0, s, a);
+void launch_codec(const QmvArgs &a, int S, int grid, hipStream_t s) {
+    hipLaunchKernelGGL((kq_qmv_persistent_kernel<CODEC, 0>), dim3(grid), dim3(64 * S), 0, s, a);
 }
 
 }  // namespace
@@ -341,7 +345,7 @@ int kq_qmv_persistent_grid(const kq_matmul_problem &q) {
 // Internal entry used by kq_quantized_matmul_grouped: problems already
 // validated, all live, sharing x / x_row_stride / M / K / codec, M <= 16,
 // K <= 8192 (K <= 4096 for Q6_K).  Returns KQ_OK or KQ_ERR_LAUNCH_FAILED.
-int kq_qmv_persistent_launch(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype, hipStream_t s) {
+int kq_qmv_persistent_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, int y_dtype, hipStream_t s) {
     QmvArgs a;
     int tiles = 0;
     for (int i = 0; i < n; ++i) {
@@ -356,6 +360,7 @@ int kq_qmv_persistent_launch(const kq_matmul_problem *ps, int n, int x_dtype, in
     }
     for (int i = n; i < kMaxProblems; ++i) a.p[i] = a.p[0];
     a.x = (const char *)ps[0].x;
+    a.x_exp = x_exp;
     a.x_stride = ps[0].x_row_stride;
     a.n_problems = n;
     a.M = ps[0].M;
@@ -365,11 +370,10 @@ int kq_qmv_persistent_launch(const kq_matmul_problem *ps, int n, int x_dtype, in
     const int S = (ps[0].K / KQ_QK + 3) / 4;
     int grid = kq_qmv_persistent_grid(ps[0]);
     if (grid > tiles) grid = tiles;
-    const bool bf = x_dtype == KQ_DTYPE_BF16;
     switch (ps[0].codec) {
-    case KQ_CODEC_Q4_K: launch_codec<KQ_CODEC_Q4_K>(a, S, grid, bf, s); break;
-    case KQ_CODEC_Q6_K: launch_codec<KQ_CODEC_Q6_K>(a, S, grid, bf, s); break;
-    default: launch_codec<KQ_CODEC_IQ2_XXS>(a, S, grid, bf, s); break;
+    case KQ_CODEC_Q4_K: launch_codec<KQ_CODEC_Q4_K>(a, S, grid, s); break;
+    case KQ_CODEC_Q6_K: launch_codec<KQ_CODEC_Q6_K>(a, S, grid, s); break;
+    default: launch_codec<KQ_CODEC_IQ2_XXS>(a, S, grid, s); break;
     }
     return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
 }

@@ -120,7 +120,7 @@ struct StreamArgs {
     int32_t tile_begin[KQ_MAX_GROUP];  // first tile of each problem; unused: INT_MAX
     StreamProblem p[KQ_MAX_GROUP];
     const char *x;                     // fp16 [M, K]
-    const int32_t *x_exp;              // per-row scale exponents of x (outputs * 2^-e), or null
+    const int32_t *x_exp;              // per-row exponents of prepared activations (results * 2^e), or null
     int64_t x_stride;                  // elements
     int32_t M, K, y_dtype, total_tiles, n_problems;
 };
@@ -309,8 +309,13 @@ __device__ __forceinline__ half8_t q4own_frag(uint32_t w, const Q4Prep &p, const
 // with C[2g + a] of every source group w) follows, in two swap stages:
 // v_permlane32_swap exchanges bit 1 of u with bit 1 of g, v_permlane16_swap
 // bit 0 with bit 0.  Register 2w + a then holds x[64 g + 32 a + 8 w .. +7].
+//
+// The sums enter the MFMA as fp16 scaled by 2^-xs, xs >= 0 the same for the
+// whole wave: large enough that the wave's largest sum stays below 2^14
+// (32 activations near fp16's maximum sum past it), 0 for ordinary
+// magnitudes, so small sums keep their precision.
 template <int SB>
-__device__ __forceinline__ void q4own_x(half8_t (&xr)[SB][8], half8_t &xm, u32x4 (&cin)[SB][8]) {
+__device__ __forceinline__ void q4own_x(half8_t (&xr)[SB][8], half8_t &xm, int &xs, u32x4 (&cin)[SB][8]) {
     static_assert(SB <= 2, "the minimum MFMA holds two super-blocks of sums");
     float sum[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
 #pragma unroll
@@ -351,14 +356,24 @@ __device__ __forceinline__ void q4own_x(half8_t (&xr)[SB][8], half8_t &xm, u32x4
             }
         }
     }
+    float mx = fmaxf(fmaxf(fabsf(sum[0][0]), fabsf(sum[0][1])), fmaxf(fabsf(sum[1][0]), fabsf(sum[1][1])));
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    xs = 0;
+    if (mx >= 16384.f && mx <= 3.402823466e38f) {
+        int E;
+        (void)frexpf(mx, &E);  // mx = f 2^E, f in [0.5, 1): mx 2^-(E-14) < 2^14
+        xs = E - 14;
+    }
     _Float16 m[8];
 #pragma unroll
     for (int s = 0; s < 2; ++s)
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            const _Float16 hi = (_Float16)sum[s][j];
+            const float v = ldexpf(sum[s][j], -xs);
+            const _Float16 hi = (_Float16)v;
             m[4 * s + 2 * j] = s < SB ? hi : (_Float16)0.f;
-            m[4 * s + 2 * j + 1] = s < SB ? (_Float16)(sum[s][j] - (float)hi) : (_Float16)0.f;
+            m[4 * s + 2 * j + 1] = s < SB ? (_Float16)(v - (float)hi) : (_Float16)0.f;
         }
     xm = half8_t{m[0], m[1], m[2], m[3], m[4], m[5], m[6], m[7]};
 }
@@ -367,7 +382,7 @@ __device__ __forceinline__ void q4own_x(half8_t (&xr)[SB][8], half8_t &xm, u32x4
 // super-block kb0, in the slot.
 template <int SB>
 __device__ __forceinline__ void q4own_slab(floatx4 &acc, LDSP(const uint8_t) row_p, const half8_t (&xr)[SB][8],
-                                           const half8_t &xm, const Q4Consts &k, int g) {
+                                           const half8_t &xm, float xm_scale, const Q4Consts &k, int g) {
     u32x4 hdr[SB], qa[SB], qb[SB];
 #pragma unroll
     for (int s = 0; s < SB; ++s) {
@@ -395,7 +410,13 @@ __device__ __forceinline__ void q4own_slab(floatx4 &acc, LDSP(const uint8_t) row
 #pragma unroll
     for (int s = SB; s < 2; ++s) bm[4 * s] = bm[4 * s + 1] = bm[4 * s + 2] = bm[4 * s + 3] = (_Float16)0.f;
     const half8_t b = {bm[0], bm[1], bm[2], bm[3], bm[4], bm[5], bm[6], bm[7]};
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xm, b, acc, 0, 0, 0);
+    if (xm_scale == 1.f) {  // wave-uniform: ordinary magnitudes chain into acc
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xm, b, acc, 0, 0, 0);
+    } else {
+        const floatx4 mn = __builtin_amdgcn_mfma_f32_16x16x32_f16(xm, b, floatx4{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(mn[e], xm_scale, acc[e]);
+    }
 }
 
 template <int CODEC, int SB>
@@ -490,6 +511,7 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
     const int kb0 = c * SB;
     half8_t xr[SB][8];
     [[maybe_unused]] half8_t xm;
+    [[maybe_unused]] float xm_scale = 1.f;  // 2^xs of the owned view's sub-block sums
     {
         // The slab's activation rows arrive by coalesced direct-to-LDS loads
         // (one row segment of SB * 512 bytes per instruction) in this
@@ -519,7 +541,9 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
                     const u32x4 v = lds128(rowa + s * 512 + 64 * t + 16 * g);
                     ch[s][t] = live ? v : zero;
                 }
-            q4own_x<SB>(xr, xm, ch);
+            int xs;
+            q4own_x<SB>(xr, xm, xs, ch);
+            xm_scale = ldexpf(1.f, xs);
         } else {
 #pragma unroll
             for (int s = 0; s < SB; ++s)
@@ -553,7 +577,7 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
                     mma_slab<KQ_CODEC_Q4_K, SB>(acc, slot + r * SlotGeo<KQ_CODEC_Q4_K, NB>::RC * 16 + kb0 * 144, xr, g,
                                                 iq2_tab);
             } else if constexpr (CODEC == KQ_CODEC_Q4_K) {
-                q4own_slab<SB>(acc, own_p + (b % R) * SLOTB, xr, xm, q4k, g);
+                q4own_slab<SB>(acc, own_p + (b % R) * SLOTB, xr, xm, xm_scale, q4k, g);
             } else {
                 mma_slab<CODEC, SB>(acc, slot + r * SlotGeo<CODEC, NB>::RC * 16 + kb0 * Geo<CODEC>::SLOT, xr, g,
                                     iq2_tab);
@@ -573,7 +597,7 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
             float sum = red[(b * C) * 32 + ln][e];
 #pragma unroll
             for (int c2 = 1; c2 < C; ++c2) sum += red[(b * C + c2) * 32 + ln][e];
-            if (A->x_exp) sum = ldexpf(sum, -A->x_exp[m]);
+            if (A->x_exp) sum = ldexpf(sum, A->x_exp[m]);
             const int tile = B0 + (round0 + b) * G;
             int32_t begin;
             const StreamProblem pr = problem_at(A, problem_of(A, tile), begin);

@@ -96,11 +96,11 @@ def _rows_view(x):
 
 
 class _Workspaces:
-    """Zero-filled scratch per (op family, device, stream), grown on demand.
-    Kernels leave their counters zeroed, so a workspace is reusable by later
-    calls of the same family on the same stream.  Families never share one:
-    the matmul's partials would land on the attention's counters and vice
-    versa."""
+    """Scratch per (op family, device, stream), grown on demand.  No kernel
+    needs it cleared (attention split partials and prepared activation rows
+    are written before they are read), so one buffer serves every later call
+    of its family on its stream; families keep their own, so a call of one
+    never overwrites what a queued call of another still reads."""
 
     def __init__(self):
         self._ws = {}
@@ -109,7 +109,7 @@ class _Workspaces:
         key = (kind, device.index, stream_handle)
         cur = self._ws.get(key)
         if cur is None or cur.numel() < nbytes:
-            cur = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+            cur = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
             self._ws[key] = cur
         return cur
 
@@ -187,7 +187,7 @@ def _problem(x2, w, codec, y2):
 def _launch_grouped(probs, x_dt, y_dt, device, stream):
     arr = (MatmulProblem * len(probs))(*probs)
     L = lib()
-    need = L.kq_matmul_workspace_bytes(arr, len(probs))
+    need = L.kq_matmul_workspace_bytes(arr, len(probs), x_dt)
     ws_ptr, ws_len = None, 0
     if need:
         ws = _WS.get("matmul", device, stream.value, need)
@@ -203,8 +203,8 @@ def quantized_matmul(x, w, scales=None, codec="q4_k", transpose=True, out_dtype=
     if not transpose:
         raise ValueError("only transpose=True (y = x . W^T) is supported, as gmlx calls it")
     _require_gpu(x, w)
-    if x.dtype not in (torch.float16, torch.bfloat16):
-        raise ValueError(f"activations must be float16 or bfloat16, got {x.dtype}")
+    if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise ValueError(f"activations must be float16, bfloat16 or float32, got {x.dtype}")
     if w.dim() != 2 or w.dtype != torch.uint8:
         raise ValueError("w must be a uint8 wire matrix [N, K/256*block_bytes]")
     x2 = _rows_view(x)
@@ -219,7 +219,8 @@ def quantized_matmul(x, w, scales=None, codec="q4_k", transpose=True, out_dtype=
 def quantized_matmul_grouped(items, out_dtype=None):
     """Run up to 8 independent quantized matmuls in ONE launch.
 
-    items: sequence of (x, w, codec); every x shares one dtype (f16/bf16).
+    items: sequence of (x, w, codec); every x shares one dtype (f16, bf16 or
+    f32; bf16 / f32 rows are prepared as fp16 with a power of two per row).
     Returns the list of outputs.  This is the launch-level form of the
     reference's occupancy fusion (gmlx/occupancy_fuse.py:141-344, q|k|v and
     gate|up concatenated wires): codecs may differ (Q4_K q/k with Q6_K v) and
@@ -359,10 +360,16 @@ def _epilogue(act, limit, alpha, gate_bias, up_bias, E, N, device):
 
 def _gather_rows(x_ptr, x_dt, x_stride, x_pair_div, x_skip, w, w_up, codec, ep, seg, order, P, E, y_ptr, y_dt,
                  y_stride, y_skip, K, stream):
-    rc = lib().kq_moe_gather_rows(x_ptr, x_dt, x_stride, x_pair_div, x_skip, w.data_ptr(),
-                                  None if w_up is None else w_up.data_ptr(), w.stride(0), w.stride(1), w.shape[1],
-                                  K, _codec_id(codec), None if ep is None else ctypes.byref(ep), seg.data_ptr(),
-                                  order.data_ptr(), P, E, y_ptr, y_dt, y_stride, y_skip, stream)
+    L = lib()
+    need = L.kq_gather_workspace_bytes(P, x_pair_div, x_skip, K, x_dt)
+    ws_ptr, ws_len = None, 0
+    if need:
+        ws = _WS.get("gather", w.device, stream.value, need)
+        ws_ptr, ws_len = ws.data_ptr(), ws.numel()
+    rc = L.kq_moe_gather_rows(x_ptr, x_dt, x_stride, x_pair_div, x_skip, w.data_ptr(),
+                              None if w_up is None else w_up.data_ptr(), w.stride(0), w.stride(1), w.shape[1],
+                              K, _codec_id(codec), None if ep is None else ctypes.byref(ep), seg.data_ptr(),
+                              order.data_ptr(), P, E, y_ptr, y_dt, y_stride, y_skip, ws_ptr, ws_len, stream)
     check("kq_moe_gather_rows", rc)
 
 

@@ -101,11 +101,15 @@ typedef struct {
     int32_t codec;
 } kq_matmul_problem;
 
-/* Workspace bytes kq_quantized_matmul_grouped needs for these problems.
- * This build reduces K splits inside a workgroup and returns 0; the
- * workspace arguments stay in the signature so a later split-K plan can use
- * them without an ABI change (pass NULL / 0). */
-size_t kq_matmul_workspace_bytes(const kq_matmul_problem *problems, int n_problems);
+/* Workspace bytes kq_quantized_matmul_grouped needs for these problems and
+ * activation dtype: 0 for fp16; for bf16 / fp32 activations, room for an
+ * fp16 copy of each problem's rows (problems sharing x share one) and one
+ * int32 exponent per row.  Every kernel computes with fp16 operands: a
+ * bf16 / fp32 row enters as fp16(x * 2^-e) with e chosen per row so its
+ * largest magnitude lands in [2^14, 2^15), and the fp32 results are scaled
+ * back by 2^e before rounding to y_dtype -- no overflow past 65504, no
+ * flush below 2^-14, bf16 values exact.  No zero-fill needed. */
+size_t kq_matmul_workspace_bytes(const kq_matmul_problem *problems, int n_problems, int x_dtype);
 
 /* kq.quantized_matmul(x, w, scales, codec, transpose=True) -- the
  * KQuantLinear forward (gmlx/modules.py:1535-1539; direct calls at
@@ -115,7 +119,8 @@ size_t kq_matmul_workspace_bytes(const kq_matmul_problem *problems, int n_proble
  * gmlx/occupancy_fuse.py:141-344 become one call without concatenating
  * bytes.  The call is one launch, except that problems sharing x with
  * M <= 16 and enough rows for every workgroup to walk several 16-row tiles
- * take one persistent launch per codec.  x_dtype: f16 or bf16.
+ * take one persistent launch per codec.  x_dtype: f16, bf16 or f32 (bf16 /
+ * f32 need the workspace above; one extra launch prepares the rows).
  * y_dtype: f16, bf16 or f32.  Results do not depend on scheduling: repeated
  * calls on the same inputs are bitwise identical. */
 #define KQ_MAX_GROUP 8
@@ -149,7 +154,8 @@ int kq_gather_qmm(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pa
                   const void *w, int64_t w_expert_bytes, int64_t w_row_bytes, int32_t N,
                   int32_t K, int codec, const int32_t *seg_info, const int32_t *pair_order,
                   int32_t n_pairs, int32_t n_experts, void *y, int y_dtype,
-                  int64_t y_row_stride, kq_stream_t stream);
+                  int64_t y_row_stride, void *workspace, size_t workspace_bytes,
+                  kq_stream_t stream);
 
 /* kq.moe_glu_gather_kq(x, gate_w, up_w, codec, idx, act) (gmlx/modules.py:557-588):
  * h[p, :] = act(x_row(p) . Wg[e]^T) * (x_row(p) . Wu[e]^T) in fp32, act 0 =
@@ -158,7 +164,8 @@ int kq_moe_glu_gather(const void *x, int x_dtype, int64_t x_row_stride, int32_t 
                       const void *w_gate, const void *w_up, int64_t w_expert_bytes,
                       int64_t w_row_bytes, int32_t N, int32_t K, int codec, int act,
                       const int32_t *seg_info, const int32_t *pair_order, int32_t n_pairs,
-                      int32_t n_experts, float *h, kq_stream_t stream);
+                      int32_t n_experts, float *h, void *workspace, size_t workspace_bytes,
+                      kq_stream_t stream);
 
 /* GLU activations of the fused gathers (the act= strings of
  * gmlx/modules.py:263-291, 557-566). */
@@ -200,7 +207,17 @@ int kq_moe_gather_rows(const void *x, int x_dtype, int64_t x_row_stride, int32_t
                        int64_t w_row_bytes, int32_t N, int32_t K, int codec,
                        const kq_gather_epilogue *ep, const int32_t *seg_info,
                        const int32_t *pair_order, int32_t n_pairs, int32_t n_experts, void *y,
-                       int y_dtype, int64_t y_row_stride, int32_t y_skip, kq_stream_t stream);
+                       int y_dtype, int64_t y_row_stride, int32_t y_skip, void *workspace,
+                       size_t workspace_bytes, kq_stream_t stream);
+
+/* Workspace of the three gathers above: 0 for fp16 activations; for bf16 /
+ * fp32 ones an fp16 copy of the rows the pairs read (row p / x_pair_div +
+ * p / x_skip) with one int32 exponent per row, prepared as for
+ * kq_quantized_matmul_grouped (x_skip 0 for kq_gather_qmm /
+ * kq_moe_glu_gather).  Results are scaled back in fp32 before the GLU and
+ * biases.  No zero-fill needed. */
+size_t kq_gather_workspace_bytes(int32_t n_pairs, int32_t x_pair_div, int32_t x_skip, int32_t K,
+                                 int x_dtype);
 
 /* The routing mix of kq.gather_qmv_mix_ns_kq (gmlx/modules.py:591-593):
  * y[t, :] = sum_s scores[t, s] * y_pairs[t*k + s, :], fp32, slots summed in

@@ -329,3 +329,75 @@ def test_stream_large_scales_take_the_two_step_form(monkeypatch):
     got = ops.quantized_matmul(_dev(x), _dev(wire), None, "q4_k", out_dtype=torch.float32).cpu().numpy()
     for rows in ([5], list(range(40, 48)), [n for n in range(N) if n != 5 and not 40 <= n < 48]):
         assert okq.max_rel(got[:, rows], ref[:, rows]) <= TOL, rows
+
+
+WIDE_ROUTES = [("default", {}), ("stream", {"GMLX_KQ_STREAM": "2"}),
+               ("dense", {"GMLX_KQ_STREAM": "0", "GMLX_KQ_MV": "0", "GMLX_KQ_PERSISTENT": "0", "GMLX_KQ_MM": "0"}),
+               ("persistent", {"GMLX_KQ_STREAM": "0", "GMLX_KQ_MV": "0", "GMLX_KQ_QMV_WGS": "2"})]
+
+
+@pytest.mark.parametrize("M", [1, 7, 24, 80])
+@pytest.mark.parametrize("codec", ["q4_k", "q6_k", "iq2_xxs"])
+def test_wide_range_activations(M, codec, monkeypatch):
+    """bf16 and fp32 activation rows far outside fp16's range -- entries of a
+    few 1e5, rows scaled by 1e-6 (below fp16's 2^-14 normal limit) -- through
+    every route (M 1 / 7: streaming, LDS-staged, register persistent; 24:
+    mid-batch; 80 and the forced route: general).  Each row enters as fp16
+    with a power of two of its own and its results are scaled back in fp32,
+    so every output row matches the fp64 reference on its own scale
+    (narrowing straight to fp16 turned the first row to inf and the second
+    to zeros).  bf16 values are exact after the scaling; fp32 ones round once
+    to 11 bits."""
+    import torch
+    from gmlx_amd import ops
+    rng = np.random.default_rng(M * 7 + len(codec))
+    N, K = 160, 1024
+    if codec == "iq2_xxs":
+        wire = okq.random_valid_blocks(rng, codec, N * K // 256).reshape(N, -1)
+    else:
+        wire = quantized_weights(rng, codec, N, K)
+    x = rng.normal(0.0, 1.0, size=(M, K)).astype(np.float32)
+    x[0] *= 1e5
+    if M > 1:
+        x[1] *= 1e-6
+        x[-1, 5] = 3.0e5
+    for dt in (torch.bfloat16, torch.float32):
+        xd = torch.from_numpy(x).to(dt)
+        ref = okq.qmm_ref(xd.float().numpy(), wire, codec)
+        for name, env in WIDE_ROUTES:
+            if name == "stream" and M > 8:
+                continue
+            for k in PATH_KNOBS + ("GMLX_KQ_MM",):
+                monkeypatch.delenv(k, raising=False)
+            for k, v in env.items():
+                monkeypatch.setenv(k, v)
+            got = ops.quantized_matmul(xd.cuda(), _dev(wire), None, codec, out_dtype=torch.float32).cpu().numpy()
+            assert np.all(np.isfinite(got)), (name, dt)
+            for m in range(M):
+                err = okq.max_rel(got[m], ref[m])
+                assert err <= TOL, (name, dt, m, err)
+
+
+@pytest.mark.parametrize("codec", ["q4_k", "q6_k"])
+def test_large_fp16_activations_every_route(codec, monkeypatch):
+    """fp16 activations of a few 1e4 (sums of 32 of them pass 65504): the
+    streaming kernel's per-sub-block activation sums (the Q4_K minimum term)
+    are scaled into range per wave; every route stays finite and within
+    tolerance.  Zero-mean rows: the fp16 sub-block scales every route uses
+    err by up to 2^-12 each, an error a strongly one-signed row (mean 2e4,
+    std 1.2e4: 2.6e-3 measured) adds up coherently over the sub-blocks."""
+    import torch
+    from gmlx_amd import ops
+    rng = np.random.default_rng(91)
+    N, K, M = 96, 2048, 4
+    wire = quantized_weights(rng, codec, N, K)
+    x = np.clip(rng.normal(0.0, 1.0, size=(M, K)) * 15000.0, -60000, 60000).astype(np.float16)
+    ref = okq.qmm_ref(x, wire, codec)
+    for name, env in WIDE_ROUTES:
+        for k in PATH_KNOBS + ("GMLX_KQ_MM",):
+            monkeypatch.delenv(k, raising=False)
+        for k, v in env.items():
+            monkeypatch.setenv(k, v)
+        got = ops.quantized_matmul(_dev(x), _dev(wire), None, codec, out_dtype=torch.float32).cpu().numpy()
+        assert np.all(np.isfinite(got)), name
+        assert okq.max_rel(got, ref) <= TOL, (name, okq.max_rel(got, ref))

@@ -329,3 +329,50 @@ def test_route_reused_once_then_recomputed():
 
 def omoe_silu(z):
     return z / (1 + np.exp(-z))
+
+
+def test_wide_range_activations_through_the_moe_layer():
+    """bf16 activations with entries of 1e5 into the fused GLU gather, and its
+    fp32 outputs (above fp16's 65504, and rows near 1e-12) into the down
+    gather: both prepare their rows as fp16 with a power of two per row and
+    scale the fp32 results back before the GLU / the store, so every pair
+    row matches the fp64 reference on its own scale."""
+    import torch
+    from gmlx_amd import ops
+    rng = np.random.default_rng(12)
+    E, D, I, T, k = 8, 512, 256, 4, 2
+    gw = _experts(rng, "q4_k", E, I, D)
+    uw = _experts(rng, "q4_k", E, I, D)
+    dw = _experts(rng, "q6_k", E, D, I)
+    x = rng.normal(0, 1, size=(T, D)).astype(np.float32)
+    x[0] *= 1e5
+    x[1] *= 1e-6
+    xb = torch.from_numpy(x).to(torch.bfloat16)
+    idx = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    inds = _dev(idx)
+    h = ops.moe_glu_gather_kq(xb.cuda(), _dev(gw), _dev(uw), "q4_k", inds, act="silu")
+    g_deq = okq.dequantize(gw, "q4_k").astype(np.float64)
+    u_deq = okq.dequantize(uw, "q4_k").astype(np.float64)
+    d_deq = okq.dequantize(dw, "q6_k").astype(np.float64)
+    xf = xb.float().numpy().astype(np.float64)
+
+    def silu(z):
+        return z / (1 + np.exp(-np.clip(z, -700, 700)))
+
+    href = np.stack([[silu(g_deq[idx[t, s]] @ xf[t]) * (u_deq[idx[t, s]] @ xf[t]) for s in range(k)]
+                     for t in range(T)])
+    hg = h.cpu().numpy()
+    assert np.abs(hg[0]).max() > 65504.0        # the GLU output row leaves fp16's range
+    for t in range(T):
+        for s in range(k):
+            assert okq.max_rel(hg[t, s], href[t, s]) <= TOL, (t, s)
+    # fp32 rows far outside fp16's range into the per-pair down gather
+    hin = href.astype(np.float32)
+    hin[2, 0] *= 1e-10
+    y = ops.gather_qmv_kq(_dev(hin), _dev(dw), "q6_k", inds)
+    yg = y.cpu().numpy()
+    hf = hin.astype(np.float64)
+    for t in range(T):
+        for s in range(k):
+            want = d_deq[idx[t, s]] @ hf[t, s]
+            assert okq.max_rel(yg[t, s], want) <= TOL, (t, s)

@@ -73,14 +73,24 @@ def test_host_validation_rejects_before_launch():
     assert call(x=18) == _lib.KQ_ERR_BAD_ALIGN
     assert call(w=0) == _lib.KQ_ERR_NULL_POINTER
     arr = (P * 1)(P(**good))
+    assert L.kq_quantized_matmul_grouped(arr, 1, 7, _lib.DTYPE_F16, None, 0, None) == _lib.KQ_ERR_UNSUPPORTED_DTYPE
+    # fp32 / bf16 activations are prepared in the workspace first: none given, nothing launched
     assert L.kq_quantized_matmul_grouped(arr, 1, _lib.DTYPE_F32, _lib.DTYPE_F16, None, 0, None) == \
-        _lib.KQ_ERR_UNSUPPORTED_DTYPE
+        _lib.KQ_ERR_WORKSPACE_TOO_SMALL
     assert L.kq_quantized_matmul_grouped(arr, 9, _lib.DTYPE_F16, _lib.DTYPE_F16, None, 0, None) == \
         _lib.KQ_ERR_TOO_MANY_PROBLEMS
-    # K splits are reduced inside a workgroup: the dense matmul needs no workspace
+    # fp16 activations need no workspace; bf16 / fp32 ones an fp16 copy of the
+    # rows (256-byte aligned) and an int32 exponent per row
     small_n = dict(good, N=16, K=4096, w_row_bytes=144 * 16, x_row_stride=4096)
     arr = (P * 1)(P(**small_n))
-    assert L.kq_matmul_workspace_bytes(arr, 1) == 0
+    assert L.kq_matmul_workspace_bytes(arr, 1, _lib.DTYPE_F16) == 0
+    M = small_n["M"]
+    want = -(-M * 4096 * 2 // 256) * 256 + -(-M * 4 // 256) * 256
+    assert L.kq_matmul_workspace_bytes(arr, 1, _lib.DTYPE_BF16) == want
+    # gathers: pair p reads row p / x_pair_div + p / x_skip
+    assert L.kq_gather_workspace_bytes(8, 2, 0, 512, _lib.DTYPE_F16) == 0
+    assert L.kq_gather_workspace_bytes(8, 2, 0, 512, _lib.DTYPE_F32) == 4 * 512 * 2 + 256
+    assert L.kq_gather_workspace_bytes(9, 1, 4, 256, _lib.DTYPE_BF16) == (9 + 2) * 256 * 2 + 256
     assert L.kq_sdpa_decode_ragged(16, 16, 16, 16, 16, 16, 2, 8, 3, 128, 100, 0.1, _lib.DTYPE_F16, 16, 16,
                                    1 << 20, None) == _lib.KQ_ERR_BAD_SHAPE
     assert L.kq_sdpa_decode_ragged(16, 16, 16, 16, 16, 16, 2, 8, 2, 80, 100, 0.1, _lib.DTYPE_F16, 16, 16,
@@ -96,10 +106,10 @@ def test_host_validation_rejects_before_launch():
     # swiglu_clamp needs a positive limit; a plain gather takes no up bias
     ep = _lib.GatherEpilogue(3, 0.0, 1.702, None, None, 0)
     assert L.kq_moe_gather_rows(16, 1, 256, 1, 0, 16, 16, 144 * 16, 144, 16, 256, 12, ctypes.byref(ep), 16, 16,
-                                4, 2, 16, 0, 16, 0, None) == _lib.KQ_ERR_BAD_ARGUMENT
+                                4, 2, 16, 0, 16, 0, None, 0, None) == _lib.KQ_ERR_BAD_ARGUMENT
     ep = _lib.GatherEpilogue(0, 0.0, 0.0, 16, 16, 16)
     assert L.kq_moe_gather_rows(16, 1, 256, 1, 0, 16, None, 144 * 16, 144, 16, 256, 12, ctypes.byref(ep), 16, 16,
-                                4, 2, 16, 1, 16, 0, None) == _lib.KQ_ERR_BAD_ARGUMENT
+                                4, 2, 16, 1, 16, 0, None, 0, None) == _lib.KQ_ERR_BAD_ARGUMENT
     assert L.kq_dequantize(16, 4, 99, 16, 0, None) == _lib.KQ_ERR_UNSUPPORTED_CODEC
     assert L.kq_quantize(16, 2, 100, 100, 12, 16, None) == _lib.KQ_ERR_BAD_SHAPE
     _ = ctypes
