@@ -295,21 +295,25 @@ def load_gguf(path, zero_copy=True, device=None):
 
 
 def find_split_shards(gguf_path):
-    """All shards of a split GGUF (`<name>-00001-of-NNNNN.gguf`) in order, or
-    [gguf_path]; a missing shard is an error (a partial load would leave
-    weights unset)."""
-    gguf_path = os.path.expanduser(str(gguf_path))
-    m = SPLIT_SHARD_RE.search(gguf_path)
-    if not m:
-        return [gguf_path]
-    total = int(m.group(2))
-    prefix = gguf_path[:m.start()]
-    shards = [f"{prefix}-{i:05d}-of-{total:05d}.gguf" for i in range(1, total + 1)]
-    missing = [p for p in shards if not os.path.isfile(p)]
-    if missing:
-        names = ", ".join(os.path.basename(p) for p in missing[:3])
-        more = "" if len(missing) <= 3 else f", +{len(missing) - 3} more"
-        raise FileNotFoundError(f"incomplete split GGUF: {len(missing)}/{total} shard(s) missing ({names}{more})")
+    """The shard files of a model, in load order.
+
+    A split GGUF names its shards `<stem>-<i>-of-<n>.gguf` (five-digit
+    i = 1..n, the split naming of gmlx/preflight.py:75-101): any one shard's
+    path yields all n, in index order.  Any other path is a single-file model
+    and comes back alone.  Every shard must exist -- a missing one would leave
+    its tensors unloaded -- so the absent ones are reported together."""
+    path = os.path.expanduser(str(gguf_path))
+    folder, name = os.path.split(path)
+    m = SPLIT_SHARD_RE.search(name)
+    if m is None:
+        return [path]
+    stem, count = name[:m.start()], int(m.group(2))
+    shards = [os.path.join(folder, f"{stem}-{i:05d}-of-{count:05d}.gguf") for i in range(1, count + 1)]
+    absent = [i + 1 for i, p in enumerate(shards) if not os.path.isfile(p)]
+    if absent:
+        listed = ", ".join(str(i) for i in absent[:8]) + (" ..." if len(absent) > 8 else "")
+        raise FileNotFoundError(f"split GGUF {stem!r} is incomplete: {len(absent)}/{count} shard(s) absent "
+                                f"(index {listed}) in {folder or '.'}")
     return shards
 
 

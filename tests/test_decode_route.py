@@ -125,7 +125,7 @@ def test_carry_stamp():
     dst = _Cache([0, 0])
     dr.carry_stamp(src, dst)
     assert dst._gmlx_cascade == src._gmlx_cascade
-    assert getattr(dst.extend, "_gmlx_cascade_merge", False)
+    assert getattr(dst.extend, dr.HOOK_MARK, False)
     dst2 = _Cache([0, 0])
     dr.carry_stamp(_Cache([0, 0]), dst2)
     assert "_gmlx_cascade" not in dst2.__dict__
@@ -183,13 +183,12 @@ def test_pads_and_starts_memoised_on_pad_identity():
     assert pads == [0, 64, 128, 32] and dr.cache_pads(cache) is pads
     starts, c0 = dr.cascade_starts(cache, pads, 1024, torch.device("cpu"))
     assert c0 == 1024 and starts.tolist() == [0, 64, 128, 32] and starts.dtype == torch.int32
-    memo = cache._gmlx_casc_starts
-    dr.cascade_starts(cache, pads, 1024, torch.device("cpu"))
-    assert cache._gmlx_casc_starts is memo
+    again, _ = dr.cascade_starts(cache, pads, 1024, torch.device("cpu"))
+    assert again is starts                              # the device table is built once
     cache.left_padding = torch.tensor([3, 1, 2, 9])     # a new pads object: recomputed
     pads = dr.cache_pads(cache)
-    starts, c0 = dr.cascade_starts(cache, pads, 1024, torch.device("cpu"))
-    assert cache._gmlx_casc_starts is not memo and c0 == 1025 and starts.tolist() == [2, 0, 1, 8]
+    fresh, c0 = dr.cascade_starts(cache, pads, 1024, torch.device("cpu"))
+    assert fresh is not starts and c0 == 1025 and fresh.tolist() == [2, 0, 1, 8]
 
 
 def _qkv(B=4, Hq=16, Hkv=8, qL=1, L=1200, D=128, dtype=torch.float16):
@@ -250,7 +249,7 @@ def test_route_falls_through_to_orig_on_decline():
     mod = types.SimpleNamespace(scaled_dot_product_attention=stock)
     assert dr.install_cascade_sdpa([mod, types.SimpleNamespace()])
     route = mod.scaled_dot_product_attention
-    assert route._gmlx_orig is stock
+    assert route.orig is stock
     assert dr.install_cascade_sdpa([mod]) and mod.scaled_dot_product_attention is route   # idempotent
     q, k, v = _qkv()
     n0 = dr.claims()
@@ -264,7 +263,7 @@ def test_install_killed_by_env(monkeypatch):
     monkeypatch.setenv("GMLX_CASCADE_SDPA", "0")
     mod = types.SimpleNamespace(scaled_dot_product_attention=lambda *a, **k: None)
     assert not dr.install_cascade_sdpa([mod])
-    assert not getattr(mod.scaled_dot_product_attention, "_gmlx_cascade_route", False)
+    assert not isinstance(mod.scaled_dot_product_attention, dr._CascadeRoute)
 
 
 def test_left_padded_route_declines_without_padding_or_for_quant():
