@@ -185,13 +185,24 @@ __device__ __forceinline__ bool map_unit(const SdpaArgs &a, int u, int &b, int &
     return false;
 }
 
-// One 32-token K/V tile in registers.
+// Tokens per K/V tile: 32, or 16 at head dim 512, where a 32-token tile
+// alone would take 256 VGPRs.  A 16-token tile fills the first half of the
+// P.V MFMA's 32 k values; the other half gets zero P and zero V rows.
+template <int D>
+struct TileTok {
+    static constexpr int TT = D > 256 ? 16 : 32;
+    static constexpr int CH = TT / 16;  // 16-token chunks of the score MFMA
+    static constexpr int VT = TT / 4;   // V rows per lane
+};
+
+// One K/V tile of TT tokens in registers.
 template <int D>
 struct KVTile {
     static constexpr int NC = D / 32;            // 32-wide d chunks for Q.K
     static constexpr int NG = (D + 127) / 128;   // 128-wide d groups for P.V
-    u32x4 k[2][NC];   // token t0 + 16*ch + r, d = 32c + 8g .. +7
-    u32x4 v[NG][8];   // token t0 + {4g+i | 16+4g+i-4}, d = 128dg + 8r .. +7
+    static constexpr int CH = TileTok<D>::CH, VT = TileTok<D>::VT;
+    u32x4 k[CH][NC];  // token t0 + 16*ch + r, d = 32c + 8g .. +7
+    u32x4 v[NG][VT];  // token t0 + {4g+i | 16+4g+i-4}, d = 128dg + 8r .. +7
 
     // Tokens past t_end are read from the row's last token (a valid address);
     // their scores are masked to -inf, so they contribute p = 0.
@@ -199,7 +210,7 @@ struct KVTile {
         const int lane = kq_lane();
         const int r = lane & 15, g = lane >> 4;
 #pragma unroll
-        for (int ch = 0; ch < 2; ++ch) {
+        for (int ch = 0; ch < CH; ++ch) {
             const int tok = min(t0 + 16 * ch + r, t_end - 1);
 #pragma unroll
             for (int c = 0; c < NC; ++c) k[ch][c] = *(const u32x4 *)(kp + (int64_t)tok * D + 32 * c + 8 * g);
@@ -208,7 +219,7 @@ struct KVTile {
         for (int dg = 0; dg < NG; ++dg) {
             const int d0 = min(128 * dg + 8 * r, D - 8);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
+            for (int i = 0; i < VT; ++i) {
                 const int tok = min(t0 + (i < 4 ? 4 * g + i : 16 + 4 * g + (i - 4)), t_end - 1);
                 v[dg][i] = *(const u32x4 *)(vp + (int64_t)tok * D + d0);
             }
@@ -217,7 +228,7 @@ struct KVTile {
     __device__ __forceinline__ half8_t kfrag(int ch, int c) const { return __builtin_bit_cast(half8_t, k[ch][c]); }
     __device__ __forceinline__ void vrows(int dg, u32x4 (&out)[8]) const {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) out[i] = v[dg][i];
+        for (int i = 0; i < 8; ++i) out[i] = i < VT ? v[dg][i] : u32x4{0u, 0u, 0u, 0u};
     }
 };
 
@@ -264,17 +275,18 @@ struct KVTileQ8 {
     static constexpr int NC = D / 32;
     static constexpr int NG = (D + 127) / 128;
     static constexpr int SG = D / 64;  // scale groups per token
-    u32x2 k[2][NC];
-    uint32_t ksb[2][NC];  // scale | bias << 16 of the chunk's group
-    u32x2 v[NG][8];
-    uint32_t vsb[NG][8];
+    static constexpr int CH = TileTok<D>::CH, VT = TileTok<D>::VT;
+    u32x2 k[CH][NC];
+    uint32_t ksb[CH][NC];  // scale | bias << 16 of the chunk's group
+    u32x2 v[NG][VT];
+    uint32_t vsb[NG][VT];
 
     __device__ __forceinline__ void load(const uint8_t *kp, const uint8_t *vp, const uint16_t *ks, const uint16_t *kb,
                                          const uint16_t *vs, const uint16_t *vb, int t0, int t_end) {
         const int lane = kq_lane();
         const int r = lane & 15, g = lane >> 4;
 #pragma unroll
-        for (int ch = 0; ch < 2; ++ch) {
+        for (int ch = 0; ch < CH; ++ch) {
             const int tok = min(t0 + 16 * ch + r, t_end - 1);
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
@@ -288,7 +300,7 @@ struct KVTileQ8 {
         for (int dg = 0; dg < NG; ++dg) {
             const int d0 = min(128 * dg + 8 * r, D - 8);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
+            for (int i = 0; i < VT; ++i) {
                 const int tok = min(t0 + (i < 4 ? 4 * g + i : 16 + 4 * g + (i - 4)), t_end - 1);
                 v[dg][i] = *(const u32x2 *)(vp + (int64_t)tok * D + d0);
                 const int64_t si = (int64_t)tok * SG + (d0 >> 6);
@@ -301,7 +313,7 @@ struct KVTileQ8 {
     }
     __device__ __forceinline__ void vrows(int dg, u32x4 (&out)[8]) const {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) out[i] = deq8<BF>(v[dg][i], vsb[dg][i]);
+        for (int i = 0; i < 8; ++i) out[i] = i < VT ? deq8<BF>(v[dg][i], vsb[dg][i]) : u32x4{0u, 0u, 0u, 0u};
     }
 };
 
@@ -318,22 +330,24 @@ struct SplitState {
     __device__ __forceinline__ void tile(const Tile &kv, int t0, int t_end, bool head_ok, float scale_log2) {
         const int lane = kq_lane();
         const int g = lane >> 4;
-        // ---- S = K . q^T for tokens t0 + [0, 32)
+        // ---- S = K . q^T for tokens t0 + [0, TT)
+        constexpr int CH = TileTok<D>::CH;
         floatx4 sc[2];
 #pragma unroll
-        for (int ch = 0; ch < 2; ++ch) {
+        for (int ch = 0; ch < CH; ++ch) {
             floatx4 acc = {0, 0, 0, 0};
 #pragma unroll
             for (int c = 0; c < NC; ++c) acc = mfma<BF>(kv.kfrag(ch, c), qf[c], acc);
             sc[ch] = acc;
         }
-        // ---- online softmax over this lane's 8 scores (head r)
+        // ---- online softmax over this lane's 8 scores (head r); a
+        // 16-token tile has no second chunk (its scores are -inf, p = 0)
         float sv[8];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int ta = t0 + 4 * g + e, tb = t0 + 16 + 4 * g + e;
             sv[e] = (ta < t_end && head_ok) ? sc[0][e] * scale_log2 : -INFINITY;
-            sv[4 + e] = (tb < t_end && head_ok) ? sc[1][e] * scale_log2 : -INFINITY;
+            sv[4 + e] = (CH == 2 && tb < t_end && head_ok) ? sc[CH - 1][e] * scale_log2 : -INFINITY;
         }
         float tmax = sv[0];
 #pragma unroll
@@ -460,17 +474,18 @@ __device__ __forceinline__ void split_unit(const SdpaArgs &a, const KvSrc &src, 
         // Ring of NBUF tiles: tile j + NBUF - 1 is loaded while tile j is
         // multiplied.  Loads are issued unconditionally (tokens past t_end
         // read the last valid token), so the wait counts are static.
+        constexpr int TT = TileTok<D>::TT;
         typename TileOf<D, BF, Q8>::type ring[NBUF];
 #pragma unroll
-        for (int j = 0; j < NBUF - 1; ++j) load_tile<D, BF, Q8>(ring[j], src, t_begin + 32 * j, t_end);
-        for (int t0 = t_begin; t0 < t_end; t0 += 32 * NBUF) {
+        for (int j = 0; j < NBUF - 1; ++j) load_tile<D, BF, Q8>(ring[j], src, t_begin + TT * j, t_end);
+        for (int t0 = t_begin; t0 < t_end; t0 += TT * NBUF) {
 #pragma unroll
             for (int j = 0; j < NBUF; ++j) {
-                load_tile<D, BF, Q8>(ring[(j + NBUF - 1) % NBUF], src, t0 + 32 * (j + NBUF - 1), t_end);
+                load_tile<D, BF, Q8>(ring[(j + NBUF - 1) % NBUF], src, t0 + TT * (j + NBUF - 1), t_end);
                 __builtin_amdgcn_sched_barrier(0);
-                if (t0 + 32 * j < t_end) {
+                if (t0 + TT * j < t_end) {
 #pragma unroll
-                    for (int k = 0; k < NRB; ++k) st[k].tile(ring[j], t0 + 32 * j, t_end, ok[k], a.scale_log2);
+                    for (int k = 0; k < NRB; ++k) st[k].tile(ring[j], t0 + TT * j, t_end, ok[k], a.scale_log2);
                 }
             }
         }
@@ -711,7 +726,7 @@ WsLayout ws_layout(int B, int Hq, int Hkv, int D, int max_len) {
 // Row blocks per prefix wave: 2 (GMLX_KQ_CASCADE_NRB=1 selects one).  Four
 // spill; D = 256 keeps one, its tile alone being 128 VGPRs.
 int cascade_nrb(int D, int nrb) {
-    const int cap = D == 256 ? 1 : env_int("GMLX_KQ_CASCADE_NRB", 2);
+    const int cap = D >= 256 ? 1 : env_int("GMLX_KQ_CASCADE_NRB", 2);
     return nrb >= 2 && cap >= 2 ? 2 : 1;
 }
 
@@ -721,7 +736,7 @@ void launch_n(const SdpaArgs &a, int grid, int block, bool merge, hipStream_t s)
         const int R = 16 / a.G;
         switch (cascade_nrb(D, (a.B + R - 1) / R)) {
         case 2:
-            if constexpr (D != 256)
+            if constexpr (D < 256)
                 hipLaunchKernelGGL((kq_sdpa_cascade_kernel<D, BF, NBUF, 2, Q8>), dim3(grid), dim3(block), 0, s, a);
             break;
         default:
@@ -740,9 +755,9 @@ void launch_n(const SdpaArgs &a, int grid, int block, bool merge, hipStream_t s)
 template <int D, bool BF>
 void launch(const SdpaArgs &a, int grid, int block, bool merge, hipStream_t s) {
     if (a.q8) {
-        if constexpr (D % 64 == 0) launch_n<D, BF, D == 256 ? 1 : 2, true>(a, grid, block, merge, s);
+        if constexpr (D % 64 == 0) launch_n<D, BF, D >= 256 ? 1 : 2, true>(a, grid, block, merge, s);
     } else {
-        launch_n<D, BF, D == 256 ? 1 : 2, false>(a, grid, block, merge, s);
+        launch_n<D, BF, D >= 256 ? 1 : 2, false>(a, grid, block, merge, s);
     }
 }
 
@@ -807,7 +822,7 @@ int ragged_impl(const void *q, const void *k, const void *v, const Q8Scales *q8,
         if ((pad->head_stride & al) || (pad->batch_stride & al)) return KQ_ERR_BAD_ALIGN;
     }
     if (B < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || Hq / Hkv > 16 || max_len < 0) return KQ_ERR_BAD_SHAPE;
-    if (D != 64 && D != 96 && D != 128 && D != 256) return KQ_ERR_BAD_SHAPE;
+    if (D != 64 && D != 96 && D != 128 && D != 256 && D != 512) return KQ_ERR_BAD_SHAPE;
     if ((int64_t)B * Hq > (1 << 30)) return KQ_ERR_BAD_SHAPE;
     if (dtype != KQ_DTYPE_F16 && dtype != KQ_DTYPE_BF16) return KQ_ERR_UNSUPPORTED_DTYPE;
     if (const int rc = q8_check(q8, D)) return rc;
@@ -855,7 +870,8 @@ int ragged_impl(const void *q, const void *k, const void *v, const Q8Scales *q8,
     case 64: bf ? launch<64, true>(a, grid, 64, merge, s) : launch<64, false>(a, grid, 64, merge, s); break;
     case 96: bf ? launch<96, true>(a, grid, 64, merge, s) : launch<96, false>(a, grid, 64, merge, s); break;
     case 128: bf ? launch<128, true>(a, grid, 64, merge, s) : launch<128, false>(a, grid, 64, merge, s); break;
-    default: bf ? launch<256, true>(a, grid, 64, merge, s) : launch<256, false>(a, grid, 64, merge, s); break;
+    case 256: bf ? launch<256, true>(a, grid, 64, merge, s) : launch<256, false>(a, grid, 64, merge, s); break;
+    default: bf ? launch<512, true>(a, grid, 64, merge, s) : launch<512, false>(a, grid, 64, merge, s); break;
     }
     return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
 }
@@ -965,7 +981,7 @@ int cascade_impl(const void *q, const void *k_shared, const void *v_shared, cons
     if (!q || !k_shared || !v_shared || !k_priv || !v_priv || !out) return KQ_ERR_NULL_POINTER;
     if (B < 0 || qL < 1 || qL > 64 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || Hq / Hkv > 16 || P < 0 || S < 0)
         return KQ_ERR_BAD_SHAPE;
-    if (D != 64 && D != 96 && D != 128 && D != 256) return KQ_ERR_BAD_SHAPE;
+    if (D != 64 && D != 96 && D != 128 && D != 256 && D != 512) return KQ_ERR_BAD_SHAPE;
     if ((int64_t)B * qL * Hq > (1 << 24)) return KQ_ERR_BAD_SHAPE;
     if (shared_head_stride < (int64_t)P * D || priv_head_stride < (int64_t)S * D ||
         priv_batch_stride < priv_head_stride * Hkv)
@@ -1036,8 +1052,11 @@ int cascade_impl(const void *q, const void *k_shared, const void *v_shared, cons
     case 128:
         bf ? launch<128, true>(a, grid, block, merge, s) : launch<128, false>(a, grid, block, merge, s);
         break;
-    default:
+    case 256:
         bf ? launch<256, true>(a, grid, block, merge, s) : launch<256, false>(a, grid, block, merge, s);
+        break;
+    default:
+        bf ? launch<512, true>(a, grid, block, merge, s) : launch<512, false>(a, grid, block, merge, s);
         break;
     }
     return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;

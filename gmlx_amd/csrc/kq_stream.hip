@@ -410,13 +410,11 @@ __device__ __forceinline__ void q4own_slab(floatx4 &acc, LDSP(const uint8_t) row
 #pragma unroll
     for (int s = SB; s < 2; ++s) bm[4 * s] = bm[4 * s + 1] = bm[4 * s + 2] = bm[4 * s + 3] = (_Float16)0.f;
     const half8_t b = {bm[0], bm[1], bm[2], bm[3], bm[4], bm[5], bm[6], bm[7]};
-    if (xm_scale == 1.f) {  // wave-uniform: ordinary magnitudes chain into acc
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xm, b, acc, 0, 0, 0);
-    } else {
-        const floatx4 mn = __builtin_amdgcn_mfma_f32_16x16x32_f16(xm, b, floatx4{0, 0, 0, 0}, 0, 0, 0);
+    // straight-line on purpose: with a branch here (chaining into acc when
+    // xm_scale == 1) the results came out wrong on multi-round launches
+    const floatx4 mn = __builtin_amdgcn_mfma_f32_16x16x32_f16(xm, b, floatx4{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(mn[e], xm_scale, acc[e]);
-    }
+    for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(mn[e], xm_scale, acc[e]);
 }
 
 template <int CODEC, int SB>

@@ -810,7 +810,7 @@ def sdpa_decode_gqa(q, k, v, scale, starts=None, k_scales=None, k_biases=None, v
     if q.dtype not in (torch.float16, torch.bfloat16) or k.dtype != q.dtype or v.dtype != q.dtype:
         raise ValueError("sdpa_decode_gqa: q, k, v must share dtype float16 or bfloat16")
     Hkv = k.shape[1]
-    if k.shape[0] != B or k.shape[3] != D or Hq % Hkv or Hq // Hkv > 16 or D not in _SDPA_HEAD_DIMS:
+    if k.shape[0] != B or k.shape[3] != D or Hq % Hkv or Hq // Hkv > 16 or D not in _GQA_HEAD_DIMS:
         raise ValueError("sdpa_decode_gqa: unsupported shape for the decode kernels")
     kk, vv = _kv_padded(k, v, "sdpa_decode_gqa")
     return _sdpa_padded(q, kk, vv, _device_starts(starts, B, q.device), scale)
@@ -864,7 +864,7 @@ def _sdpa_q8(q, k, v, q8, starts, scale):
     if k8.shape != v8.shape or k8.stride() != v8.stride() or ks.stride() != vs.stride():
         k8, v8, ks, kb, vs, vb = (t.contiguous() for t in (k8, v8, ks, kb, vs, vb))
     Hkv, L = k8.shape[1], k8.shape[2]
-    if k8.shape[0] != B or Hq % Hkv or Hq // Hkv > 16 or D not in (64, 128, 256):
+    if k8.shape[0] != B or Hq % Hkv or Hq // Hkv > 16 or D not in _Q8_HEAD_DIMS:
         raise ValueError("unsupported quantized-KV attention shape")
     st = _device_starts(starts, B, q.device)
     q3 = q.reshape(B, Hq, D).contiguous()
@@ -882,7 +882,13 @@ def _sdpa_q8(q, k, v, q8, starts, scale):
     return out.reshape(B, Hq, 1, D)
 
 
+# Head dims per route, as the reference's guards have them: the ragged route
+# (gmlx/qwen35_attn.py:425-428), the batched starts= route and the cascade
+# (512 too: gmlx/gemma4_batched_sdpa.py:172-177, gmlx/cascade_sdpa.py:66), the
+# 8-bit KV route (whole 64-value scale groups: gmlx/quantized_sdpa_fix.py:66).
 _SDPA_HEAD_DIMS = (64, 96, 128, 256)
+_GQA_HEAD_DIMS = (64, 96, 128, 256, 512)
+_Q8_HEAD_DIMS = (64, 128, 256, 512)
 
 
 def ragged_decode_attention(queries, keys, values, pads, scale):
@@ -1005,7 +1011,7 @@ def sdpa_decode_gqa_cascade(queries, k_shared, v_shared, k_priv, v_priv, scale, 
     S = k_priv.shape[2]
     if k_priv.shape[1] != Hkv or k_shared.shape[3] != D or k_priv.shape[3] != D:
         raise ValueError("head count / head dim mismatch")
-    if Hq % Hkv or Hq // Hkv > 16 or D not in ((64, 128, 256) if q8 else (64, 96, 128, 256)) or not 1 <= qL <= 64:
+    if Hq % Hkv or Hq // Hkv > 16 or D not in (_Q8_HEAD_DIMS if q8 else _GQA_HEAD_DIMS) or not 1 <= qL <= 64:
         raise ValueError("unsupported cascade shape")
     if S < qL:
         raise ValueError("the private slab must hold the query block (S >= qL)")

@@ -275,7 +275,8 @@ int kq_moe_router_topk(const void *logits, int logits_dtype, int64_t logits_row_
  * ([Hkv, len_b, D] at a row offset) and the reference's padded
  * [B, Hkv, L, D] + per-row start layout are expressible.
  * q [B, Hq, D] (contiguous), out [B, Hq, D]; q/k/v/out share dtype (f16 or
- * bf16).  D in {64, 96, 128, 256}; Hq % Hkv == 0; Hq/Hkv <= 16.
+ * bf16).  D in {64, 96, 128, 256, 512} (512 walks 16-token tiles); Hq % Hkv
+ * == 0; Hq/Hkv <= 16.
  * max_len >= every row_len[b] (sizes the split table and workspace). */
 size_t kq_sdpa_workspace_bytes(int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t max_len);
 int kq_sdpa_decode_ragged(const void *q, const void *k, const void *v, const int64_t *kv_off,
@@ -292,7 +293,7 @@ int kq_sdpa_decode_ragged(const void *q, const void *k, const void *v, const int
  * D bytes; value = scale * q + bias with one 16-bit (q's dtype) scale and
  * bias per 64 values, at element index (byte offset) / 64 of k_scales /
  * k_biases (v_*).  kv_off and head_stride are in bytes and multiples of 64;
- * D in {64, 128, 256}; k / v 8-byte aligned.  Same workspace as above. */
+ * D in {64, 128, 256, 512}; k / v 8-byte aligned.  Same workspace as above. */
 int kq_sdpa_decode_ragged_q8(const void *q, const void *k, const void *v, const void *k_scales,
                              const void *k_biases, const void *v_scales, const void *v_biases,
                              const int64_t *kv_off, const int64_t *head_stride,
@@ -350,7 +351,7 @@ int kq_sdpa_decode_gqa_q8(const void *q, const void *k, const void *v, const voi
  * left padding plus the end-aligned causal mask of the query block.
  * starts == NULL means 0 for every sequence; starts are clamped to [0, S].
  * q, out [B, Hq, qL, D] contiguous; all tensors share dtype (f16 or bf16).
- * qL in 1..64, D in {64, 96, 128, 256}, Hq % Hkv == 0, Hq/Hkv <= 16.
+ * qL in 1..64, D in {64, 96, 128, 256, 512}, Hq % Hkv == 0, Hq/Hkv <= 16.
  * Each prefix tile is loaded once per 16 / (Hq/Hkv) query rows (the rows'
  * heads share the MFMA's 16 columns), so the prefix costs P, not B * P,
  * bytes per head in the common case (B * qL * Hq / Hkv <= 16). */

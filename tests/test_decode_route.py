@@ -197,7 +197,7 @@ def _qkv(B=4, Hq=16, Hkv=8, qL=1, L=1200, D=128, dtype=torch.float16):
 
 
 @pytest.mark.parametrize("case", ["no-stamp", "B1", "qL9", "D96", "fp32", "short-prefix", "geometry",
-                                  "quant", "mask-None-verify", "sinks", "gqa17", "wide", "right-pad"])
+                                  "quant", "mask-None-verify", "sinks", "gqa17", "wide", "wide512", "right-pad"])
 def test_claim_declines(monkeypatch, case):
     q, k, v = _qkv()
     cache = _Cache([0, 4, 8, 2], P=1024)
@@ -231,6 +231,9 @@ def test_claim_declines(monkeypatch, case):
         q, k, v = _qkv(Hq=17 * 8)
     elif case == "wide":
         q, k, v = _qkv(B=8, Hq=32, qL=4)                 # B * G * qL = 128 > 64
+        kw["mask"] = "causal"
+    elif case == "wide512":
+        q, k, v = _qkv(B=8, Hq=16, Hkv=8, qL=4, D=512)   # B * G * qL = 64 > 32 at head dim 512
         kw["mask"] = "causal"
     elif case == "right-pad":
         cache._right_padding = [0, 1, 0, 0]

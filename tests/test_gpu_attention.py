@@ -191,3 +191,42 @@ def test_sdpa_decode_gqa_q8_kv(D, Hq, Hkv, dtype_name):
     ref = np.stack([attention_ref(qd[b], kd[b][:, starts[b]:], vd[b][:, starts[b]:], scale) for b in range(B)])
     tol = BF16_TOL if dtype_name == "bfloat16" else TOL
     assert okq.max_rel(out.float().cpu().numpy()[:, :, 0], ref) <= tol
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,dtype_name", [(2, 16, 1, "float16"), (16, 8, 2, "float16"),
+                                                 (5, 32, 4, "bfloat16"), (16, 16, 16, "bfloat16")])
+def test_head_dim_512(B, Hq, Hkv, dtype_name):
+    """Head dim 512, the only one the reference's batched starts= route claims
+    (gmlx/gemma4_batched_sdpa.py:172-177), at B 2..16 and G 1..16: the
+    16-bit and the 8-bit affine KV forms of sdpa_decode_gqa against the fp64
+    per-row reference over keys [starts[b], L) (a 16-token tile per step at
+    this head dim)."""
+    import torch
+    from gmlx_amd import ops
+    from helpers import q8_affine
+    rng = np.random.default_rng(B * 7 + Hq)
+    D, L = 512, 900
+    tdt = getattr(torch, dtype_name)
+    tol = BF16_TOL if dtype_name == "bfloat16" else TOL
+    kf = rng.normal(0, 1, size=(B, Hkv, L, D)).astype(np.float32)
+    vf = rng.normal(0, 1, size=(B, Hkv, L, D)).astype(np.float32)
+    q = torch.from_numpy(rng.normal(0, 1, size=(B, Hq, 1, D)).astype(np.float32)).to(tdt)
+    starts = rng.integers(0, L - 1, size=B).tolist()
+    starts[0] = 0
+    scale = D ** -0.5
+    dev_st = torch.tensor(starts, dtype=torch.int32, device="cuda")
+    print(f"hd512 B={B} Hq={Hq} Hkv={Hkv} {dtype_name}", flush=True)
+    k16, v16 = torch.from_numpy(kf).to(tdt), torch.from_numpy(vf).to(tdt)
+    out = ops.sdpa_decode_gqa(q.cuda(), k16.cuda(), v16.cuda(), scale, starts=dev_st)
+    qd = q.double().numpy()[:, :, 0]
+    kd16, vd16 = k16.double().numpy(), v16.double().numpy()
+    ref = np.stack([attention_ref(qd[b], kd16[b][:, starts[b]:], vd16[b][:, starts[b]:], scale) for b in range(B)])
+    assert okq.max_rel(out.float().cpu().numpy()[:, :, 0], ref) <= tol
+    kw, ks, kb, kd = q8_affine(kf, dtype_name)
+    vw, vs, vb, vd = q8_affine(vf, dtype_name)
+    out8 = ops.sdpa_decode_gqa(q.cuda(), kw.cuda(), vw.cuda(), scale, starts=dev_st, k_scales=ks.cuda(),
+                               k_biases=kb.cuda(), v_scales=vs.cuda(), v_biases=vb.cuda())
+    ref8 = np.stack([attention_ref(qd[b], kd[b][:, starts[b]:], vd[b][:, starts[b]:], scale) for b in range(B)])
+    assert okq.max_rel(out8.float().cpu().numpy()[:, :, 0], ref8) <= tol
+    # the ragged route keeps the reference's head dims and declines 512
+    assert ops.ragged_decode_attention(q.cuda(), k16.cuda(), v16.cuda(), starts, scale) is None

@@ -263,3 +263,41 @@ def test_route_claims_quantized_cache():
     assert out is not None and dr.claims() == n0 + 1
     ref = _masked_ref(q.double().numpy(), kd, vd, pads, 0.125)
     assert okq.max_rel(out.float().cpu().numpy(), ref) <= TOL
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,qL,dtype_name", [(8, 8, 2, 1, "float16"), (4, 16, 4, 2, "float16"),
+                                                    (2, 16, 1, 1, "bfloat16")])
+def test_head_dim_512(B, Hq, Hkv, qL, dtype_name):
+    """Head dim 512 inside the claim's width gate for it (B * G * qL <= 32,
+    gmlx/cascade_sdpa.py:66, 194): 16-bit KV against the masked fp64
+    reference."""
+    pads = [3 * b % 11 for b in range(B)]
+    out, ref = _run(B, Hq, Hkv, 512, 1100, 70, pads, qL, dtype_name, seed=B + qL)
+    tol = BF16_TOL if dtype_name == "bfloat16" else TOL
+    assert okq.max_rel(out.float().cpu().numpy(), ref) <= tol
+
+
+def test_quantized_kv_cascade_head_dim_512():
+    """The 8-bit affine KV cascade at head dim 512 (whole 64-value groups)."""
+    import torch
+    from gmlx_amd import ops
+    from helpers import q8_affine
+    rng = np.random.default_rng(512)
+    pads = [0, 40, 12, 7]
+    B, Hkv, Hq, D, P, sp, qL = len(pads), 2, 8, 512, 1024, 80, 1
+    kb_, vb_, L = _shared_batch(rng, B, Hkv, P, sp, pads, D, np.float32)
+    kw, ks, kbias, kd = q8_affine(kb_, "float16")
+    vw, vs, vbias, vd = q8_affine(vb_, "float16")
+    q = torch.from_numpy(rng.normal(0, 1, size=(B, Hq, qL, D)).astype(np.float32)).half()
+    c0 = min(pads) + P
+    starts = torch.tensor([p + P - c0 for p in pads], dtype=torch.int32, device="cuda")
+    l0 = pads[0]
+    kw, ks, kbias, vw, vs, vbias = (t.cuda() for t in (kw, ks, kbias, vw, vs, vbias))
+    sl = lambda t: t[0:1, :, l0:l0 + P]  # noqa: E731
+    pr = lambda t: t[:, :, c0:]  # noqa: E731
+    out = ops.sdpa_decode_gqa_cascade(
+        q.cuda(), sl(kw), sl(vw), pr(kw), pr(vw), D ** -0.5, starts=starts,
+        k_shared_scales=sl(ks), k_shared_biases=sl(kbias), v_shared_scales=sl(vs), v_shared_biases=sl(vbias),
+        k_priv_scales=pr(ks), k_priv_biases=pr(kbias), v_priv_scales=pr(vs), v_priv_biases=pr(vbias))
+    ref = _masked_ref(q.double().numpy(), kd, vd, pads, D ** -0.5)
+    assert okq.max_rel(out.float().cpu().numpy(), ref) <= TOL
