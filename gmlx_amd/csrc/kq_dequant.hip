@@ -136,7 +136,8 @@ int kq_supports(int op, int codec, int dtype) {
     case KQ_OP_QUANTIZE: return codec_ok && dtype == KQ_DTYPE_F32;
     case KQ_OP_MATMUL:
     case KQ_OP_GATHER:
-    case KQ_OP_MOE_GLU: return codec_ok && (dtype == KQ_DTYPE_F16 || dtype == KQ_DTYPE_BF16);
+    case KQ_OP_MOE_GLU:  // activations; bf16 / fp32 rows are prepared as scaled fp16
+        return codec_ok && (dtype == KQ_DTYPE_F16 || dtype == KQ_DTYPE_BF16 || dtype == KQ_DTYPE_F32);
     case KQ_OP_SDPA: return dtype == KQ_DTYPE_F16 || dtype == KQ_DTYPE_BF16;
     default: return 0;
     }

@@ -373,9 +373,10 @@ def _gather_rows(x_ptr, x_dt, x_stride, x_pair_div, x_skip, w, w_up, codec, ep, 
     check("kq_moe_gather_rows", rc)
 
 
-def gather_qmm(x, w, scales=None, codec="q4_k", indices=None, sorted_indices=False, out_dtype=None):
+def gather_qmm(x, w, scales=None, codec="q4_k", indices=None, sorted_indices=False, out_dtype=None, bias=None):
     """KQuantSwitchLinear forward: x (T, 1, 1, K) or (T, K), indices (T, k)
-    -> (T, k, 1, N) with y[t, s] = dequant(w[indices[t, s]]) . x[t].
+    -> (T, k, 1, N) with y[t, s] = dequant(w[indices[t, s]]) . x[t]
+    (+ bias[indices[t, s]], fp32 [E, N], added in the fp32 epilogue).
     `sorted_indices` is accepted for signature parity; grouping by expert
     always happens on the device."""
     _fault("gather_qmm")
@@ -389,9 +390,11 @@ def gather_qmm(x, w, scales=None, codec="q4_k", indices=None, sorted_indices=Fal
     out_dtype = out_dtype or x.dtype
     E, N = w.shape[0], w.shape[1]
     y = torch.empty((T * k, N), dtype=out_dtype, device=x.device)
+    b = _bias_rows(bias, E, N, "bias", x.device)
+    ep = None if b is None else _lib.GatherEpilogue(_lib.ACT_ID["silu"], 0.0, 0.0, b.data_ptr(), None, N)
     if T * k:
         seg, order = _routed(indices, E)
-        _gather_rows(x2.data_ptr(), _x_dt(x2), x2.stride(0), k, 0, w, None, codec, None, seg, order, T * k, E,
+        _gather_rows(x2.data_ptr(), _x_dt(x2), x2.stride(0), k, 0, w, None, codec, ep, seg, order, T * k, E,
                      y.data_ptr(), _dt(out_dtype), N, 0, K, _stream(x2))
     return y.reshape(T, k, 1, N)
 

@@ -376,3 +376,50 @@ def test_wide_range_activations_through_the_moe_layer():
         for s in range(k):
             want = d_deq[idx[t, s]] @ hf[t, s]
             assert okq.max_rel(yg[t, s], want) <= TOL, (t, s)
+
+
+def test_biased_switch_linear_module():
+    """KQuantSwitchLinear with a bias: each pair adds its expert's fp32 bias
+    row in the kernel's epilogue."""
+    import torch
+    from gmlx_amd.nn import KQuantSwitchLinear
+    rng = np.random.default_rng(16)
+    w = _experts(rng, "q4_k", 5, 48, 512)
+    mod = KQuantSwitchLinear(5, 48, 512, True, "q4_k").cuda()
+    mod.weight.copy_(_dev(w))
+    b = rng.normal(0, 1, size=(5, 48)).astype(np.float32)
+    mod.bias.copy_(torch.from_numpy(b))
+    x = fp16_rows(rng, 3, 512)
+    idx = np.array([[0, 4], [2, 2 + 1], [4, 1]], np.int32)
+    got = mod(_dev(x).reshape(3, 1, 1, 512), _dev(idx)).float().cpu().numpy()
+    deq = okq.dequantize(w, "q4_k").astype(np.float64)
+    ref = np.stack([[deq[idx[t, s]] @ x[t].astype(np.float64) + b[idx[t, s]] for s in range(2)] for t in range(3)])
+    assert okq.max_rel(got[:, :, 0], ref) <= TOL
+
+
+@pytest.mark.parametrize("codec,dtype_name", [("q4_k", "bfloat16"), ("q6_k", "float16"), ("iq2_xxs", "float32")])
+def test_kquant_embedding(codec, dtype_name):
+    """KQuantEmbedding: forward(ids) gives the GGML dequantization of the ids'
+    rows (bit-exact in fp32, one rounding otherwise); as_linear(x) is the
+    tied head x . dequant(W)^T."""
+    import torch
+    from gmlx_amd.nn import KQuantEmbedding
+    rng = np.random.default_rng(21)
+    V, D = 300, 512
+    if codec == "iq2_xxs":
+        wire = okq.random_valid_blocks(rng, codec, V * D // 256).reshape(V, -1)
+    else:
+        wire = quantized_weights(rng, codec, V, D)
+    tdt = getattr(torch, dtype_name)
+    emb = KQuantEmbedding(V, D, codec, out_dtype=tdt).cuda()
+    emb.weight.copy_(_dev(wire))
+    ids = rng.integers(0, V, size=(2, 7))
+    got = emb(torch.from_numpy(ids).cuda())
+    assert got.dtype == tdt and tuple(got.shape) == (2, 7, D)
+    deq = okq.dequantize(wire, codec)                                  # fp32, the GGML definition
+    want = torch.from_numpy(deq[ids.reshape(-1)].reshape(2, 7, D)).to(tdt)
+    assert torch.equal(got.cpu(), want)
+    x = fp16_rows(rng, 3, D)
+    logits = emb.as_linear(_dev(x)).float().cpu().numpy()
+    ref = x.astype(np.float64) @ deq.astype(np.float64).T
+    assert okq.max_rel(logits, ref) <= TOL

@@ -43,6 +43,9 @@ def test_version_strerror_and_capabilities():
     assert all(ops.codec_has_matmul(c) and ops.codec_has_moe_glu(c) for c in ops.codecs())
     assert not ops.codec_has_matmul("q8_0")
     assert L.kq_supports(_lib.OP_SDPA, 0, _lib.DTYPE_F32) == 0
+    # matmul / gather activations: fp16, bf16 and fp32 (prepared as scaled fp16)
+    assert all(L.kq_supports(op, 12, dt) == 1 for op in (_lib.OP_MATMUL, _lib.OP_GATHER, _lib.OP_MOE_GLU)
+               for dt in (_lib.DTYPE_F16, _lib.DTYPE_BF16, _lib.DTYPE_F32))
 
 
 def test_library_grid_table_is_pinned():
@@ -179,3 +182,42 @@ def test_install_kquant_modules_swaps_linear_leaves():
     with pytest.raises(ValueError, match="no recognized module"):
         install_kquant_modules(model, {"1.weight": "q4_k"})
     _ = np
+
+
+def test_install_kquant_modules_swaps_embeddings_and_expert_stacks(monkeypatch):
+    """The leaf swap's three kinds (gmlx/modules.py:1539-1552): nn.Embedding
+    -> KQuantEmbedding with the activation dtype out, a 3-D expert stack
+    (registered class, or a class named *SwitchLinear) -> KQuantSwitchLinear
+    with its bias carried over."""
+    from gmlx_amd import nn as knn
+
+    class SwitchLinear(torch.nn.Module):
+        def __init__(self, e, o, i, bias):
+            super().__init__()
+            self.weight = torch.nn.Parameter(torch.zeros(e, o, i))
+            self.bias = torch.nn.Parameter(torch.zeros(e, o)) if bias else None
+
+    class Experts(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.weight = torch.nn.Parameter(torch.zeros(4, 32, 256))
+            self.bias = None
+
+    model = torch.nn.ModuleDict({"emb": torch.nn.Embedding(100, 512), "sw": SwitchLinear(8, 64, 512, True),
+                                 "ex": Experts(), "out": torch.nn.Linear(512, 16)})
+    with pytest.raises(ValueError, match="no recognized module"):
+        knn.install_kquant_modules(model, {"ex.weight": "q4_k"})
+    knn.register_switch_linear(Experts)
+    monkeypatch.setenv("GMLX_ACTIVATION_DTYPE", "float16")
+    n = knn.install_kquant_modules(model, {"emb.weight": "q6_k", "sw.weight": "q4_k", "ex.weight": "q4_k"})
+    assert n == 3
+    assert isinstance(model["emb"], knn.KQuantEmbedding) and model["emb"].out_dtype == torch.float16
+    assert tuple(model["emb"].weight.shape) == (100, 2 * 210)
+    sw = model["sw"]
+    assert isinstance(sw, knn.KQuantSwitchLinear) and tuple(sw.weight.shape) == (8, 64, 2 * 144)
+    assert sw.bias is not None and tuple(sw.bias.shape) == (8, 64)
+    assert isinstance(model["ex"], knn.KQuantSwitchLinear) and model["ex"].bias is None
+    assert isinstance(model["out"], torch.nn.Linear)
+    assert knn.install_kquant_modules(model, {"emb.weight": "q6_k"}) == 0   # already swapped
+    monkeypatch.setenv("GMLX_ACTIVATION_DTYPE", "auto")
+    assert knn.activation_dtype() == torch.bfloat16
