@@ -450,29 +450,68 @@ def bench_moe(torch, ops, which, iters=20):
 
 # -------------------------------------------------------------- CPU baseline
 
-def cpu_baseline(layer_wires, B, budget_s=12.0):
-    """The oracle's OpenMP dequant-fused fp32 matmul (oracle/kq_oracle.c
-    kqo_qmm_f32) on one C2 layer at B rows, repeated until ~budget_s.
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(layer_wires, B, budget_s=12.0, numpy_budget_s=8.0):
+    """The CPU figures of BASELINE section 4, on one C2 layer (7 matrices,
+    122.6 MB of wire) at B rows:
+      value: the oracle's OpenMP dequant-fused fp32 matmul (oracle/kq_oracle.c
+             kqo_qmm_f32), repeated until ~budget_s, on the host threads this
+             process may use (the affinity set, capped by OMP_NUM_THREADS: the
+             GPU box grants one GPU's CPU share);
+      numpy: numpy's vectorised dequantization (oracle/kquant.py) to fp32,
+             then x @ W^T through numpy's BLAS, matrix by matrix until
+             ~numpy_budget_s.
     layer_wires: {name: uint8 numpy wire} of one layer."""
     import numpy as np
     from oracle import kquant as okq
     rng = np.random.default_rng(1)
-    layer = [(layer_wires[name], K, codec) for name, N, K, codec in LAYER]
+    layer = [(layer_wires[name], N, K, codec) for name, N, K, codec in LAYER]
     xs = {K: rng.normal(0, 1, size=(B, K)).astype(np.float16) for K in (HIDDEN, INTER)}
-    cores = len(os.sched_getaffinity(0))
-    nthreads = min(cores, 16)
+    affinity = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS", "").strip()
+    nthreads = min(affinity, int(omp)) if omp.isdigit() and int(omp) > 0 else affinity
     done, t0 = 0, time.perf_counter()
     while True:
-        for wire, K, codec in layer:
+        for wire, _, K, codec in layer:
             okq.qmm_f32_cpu(xs[K], wire, codec, nthreads=nthreads)
         done += 1
         el = time.perf_counter() - t0
         if el >= budget_s or done >= 50:
             break
     gbs = done * layer_bytes(B) / el / 1e9
+    # numpy dequant + BLAS, one matrix at a time, smallest first, until the
+    # budget (at least one matrix; the vectorised dequantization runs near
+    # 1 MB/s of wire, so a whole layer would take minutes)
+    deq = {"q4_k": okq.dequant_q4_k_np, "q6_k": okq.dequant_q6_k_np, "iq2_xxs": okq.dequant_iq2_xxs_np}
+    order = sorted(layer, key=lambda m: m[0].nbytes)
+    nbytes, mats, t1 = 0, 0, time.perf_counter()
+    while True:
+        wire, N, K, codec = order[mats % len(order)]
+        w = deq[codec](wire).reshape(N, K)
+        _ = xs[K].astype(np.float32) @ w.T
+        nbytes += wire.nbytes
+        mats += 1
+        el_np = time.perf_counter() - t1
+        if el_np >= numpy_budget_s:
+            break
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": nthreads, "kind": "port",
             "sample": f"{done} pass(es) of one C2 layer (7 matrices, 122.6 MB of wire) at B={B}, "
-                      f"{el:.1f} s, oracle/kq_oracle.c kqo_qmm_f32 (OpenMP, fp32)"}
+                      f"{el:.1f} s, oracle/kq_oracle.c kqo_qmm_f32 (OpenMP, fp32)",
+            "cpu_model": _cpu_model(), "host_threads_available": affinity,
+            "numpy_blas": {"value": round(nbytes / el_np / 1e9, 4), "unit": "GB/s",
+                           "sample": f"{mats} of the layer's matrices, smallest first ({nbytes / 1e6:.1f} MB of "
+                                     f"wire), numpy dequantization to fp32 then x @ W^T (numpy BLAS), "
+                                     f"{el_np:.1f} s"}}
 
 
 # ------------------------------------------------------------ HBM traffic
@@ -671,7 +710,8 @@ def main():
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline({k: v.cpu().numpy() for k, v in stack[0].items()}, B)
-        log(f"[bench] cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads")
+        log(f"[bench] cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads ({cpu['cpu_model']}); "
+            f"numpy dequant + BLAS {cpu['numpy_blas']['value']} GB/s")
 
     dk = per_kernel[dominant]
     achieved = dk["bytes_per_launch"] / dk["avg_launch_us"] / 1e3
