@@ -1,7 +1,7 @@
 """IQ2_XXS constant tables for the oracle (test infrastructure only).
 
 Two independent transcriptions of public GGML data, checked against each
-other and against the E8-lattice invariants in tests/test_oracle_tables.py:
+other and against the E8-lattice invariants in tests/test_oracle.py:
 
 - ``KGRID_2BIT_256``: the 256 16-bit codes of ggml-quants.c
   (``kgrid_2bit_256`` in ``iq2xs_init_impl``), each holding eight 2-bit digits
