@@ -98,11 +98,12 @@ def make_inputs(torch, rng, B):
 # each (kq_quantized_matmul_grouped's routing): at B <= 8 gate|up (six tiles
 # per CU) takes the producer / consumer weight-streaming kernel (two waves copy
 # whole 16-row tiles into an LDS ring with direct-to-LDS loads, eight waves
-# dequantize and run the MFMA on one K-slab each); q|k|v (Q4_K and Q6_K tiles
-# in one launch) and o (at most two tiles per CU) take the LDS-staged
-# persistent kernel as two 8-wave workgroups per CU, one tile each; down
-# (K = 12288 Q6_K) takes it with three blocks per wave, the last 4096 columns
-# of x in registers at B > 4; at B = 9..16 the LDS-staged kernel serves every
+# dequantize and run the MFMA on one K-slab each), and so does down (K = 12288
+# Q6_K) in six K slices of 8 super-blocks, the last slice of each tile to
+# finish summing the six partial tiles; q|k|v (Q4_K and Q6_K tiles in one
+# launch) and o (at most two tiles per CU) take the LDS-staged persistent
+# kernel as two 8-wave workgroups per CU, one tile each; at B = 9..16 the
+# LDS-staged kernel serves every
 # launch but down, which takes the general kernel; at B = 17..64 every launch
 # takes the mid-batch kernel (one 4-wave workgroup per CU over groups of T
 # weight tiles: q|k|v mixed T = 2, o and down T = 1, gate|up T = 6 up to 32
@@ -126,6 +127,8 @@ def kernel_of(launch, B):
                 "gate_up": f"kq_mm_kernel<0, {mt}, 0, {6 if mt == 2 else 3}>", "down": f"kq_mm_kernel<1, {mt}, 0, 1>"}[launch]
     if B <= 8 and launch == "gate_up":  # kq_stream_kernel<codec, blocks per consumer, consumers, slots>
         return "kq_stream_kernel<12, 2, 8, 3>"
+    if B <= 8 and launch == "down":  # K = 12288 in six slices of 8 super-blocks, one per consumer
+        return "kq_stream_kernel<14, 1, 8, 3>"
     if launch == "qkv":  # Q4_K q|k with Q6_K v: the mixed form (codec id 127), 0.75 tiles per 8-wave workgroup
         return "kq_mv_kernel<127, 0, 2, 1, false, 8>"
     if launch == "o":

@@ -32,6 +32,9 @@ DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 OP_DEQUANTIZE, OP_QUANTIZE, OP_MATMUL, OP_GATHER, OP_MOE_GLU, OP_SDPA = range(6)
 MAX_GROUP = 8
 SDPA_NOALLOC_SCRATCH_BYTES = 32 << 20  # KQ_SDPA_NOALLOC_SCRATCH_BYTES (include/kq_capi.h)
+# KQ_MATMUL_COUNTER_BYTES: arrival counters at the start of every matmul / gather
+# workspace (zero when allocated; the library leaves them zero)
+MATMUL_COUNTER_BYTES = 16 << 10
 
 # every symbol include/kq_capi.h and include/kq_gguf.h declare, checked at load
 EXPORTS = (

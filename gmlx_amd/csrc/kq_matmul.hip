@@ -22,8 +22,11 @@ bool kq_mv_eligible(const kq_matmul_problem *ps, int n, int x_dtype, int y_dtype
 int kq_mv_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, int y_dtype, hipStream_t s);
 // kq_stream.hip: weight-streaming launch for M <= 8 (problems validated, all
 // live, fp16 x shared, one codec or Q4_K with Q6_K, K as its slab plan allows).
-bool kq_stream_eligible(const kq_matmul_problem *ps, int n);
-int kq_stream_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, int y_dtype, hipStream_t s);
+int kq_stream_split_want(const kq_matmul_problem *ps, int n);
+size_t kq_stream_part_bytes(const kq_matmul_problem *ps, int n, int split);
+bool kq_stream_eligible(const kq_matmul_problem *ps, int n, int split);
+int kq_stream_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, int y_dtype, int split,
+                     uint32_t *ctr, float *part, hipStream_t s);
 // kq_qmv.hip: persistent small-batch launch (problems validated, all live,
 // sharing codec / x / M <= 16 / K <= 8192).
 int kq_qmv_persistent_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, int y_dtype, hipStream_t s);
@@ -851,9 +854,12 @@ int gather_common(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pa
     const int32_t *x_exp = nullptr;
     if (x_dtype != KQ_DTYPE_F16) {
         const int32_t rows = gather_x_rows(n_pairs, x_pair_div, x_skip);
-        if (!workspace || workspace_bytes < kq_prepared_bytes(rows, K)) return KQ_ERR_WORKSPACE_TOO_SMALL;
+        if (!workspace || workspace_bytes < KQ_MATMUL_COUNTER_BYTES + kq_prepared_bytes(rows, K))
+            return KQ_ERR_WORKSPACE_TOO_SMALL;
         const void *x16 = nullptr;
-        if (const int rc = kq_prepare_rows(x, x_dtype, x_row_stride, rows, K, workspace, &x_exp, &x16, s)) return rc;
+        if (const int rc = kq_prepare_rows(x, x_dtype, x_row_stride, rows, K,
+                                           (char *)workspace + KQ_MATMUL_COUNTER_BYTES, &x_exp, &x16, s))
+            return rc;
         x = x16;
         x_row_stride = K;
         x_dtype = KQ_DTYPE_F16;
@@ -897,16 +903,33 @@ int gather_common(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pa
     return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
 }
 
+// Bytes of prepared activation rows (a copy per problem; problems sharing x share one).
+size_t prepared_total(const kq_matmul_problem *problems, int n_problems, int x_dtype) {
+    if (x_dtype == KQ_DTYPE_F16) return 0;
+    size_t b = 0;
+    for (int i = 0; i < n_problems && i < KQ_MAX_GROUP; ++i)
+        if (problems[i].M > 0 && problems[i].N > 0) b += kq_prepared_bytes(problems[i].M, problems[i].K);
+    return b;
+}
+
+// Partial-tile bytes of a split launch of the group's live problems (0: none).
+size_t split_bytes(const kq_matmul_problem *problems, int n_problems) {
+    kq_matmul_problem all[KQ_MAX_GROUP];
+    int na = 0;
+    for (int i = 0; i < n_problems && i < KQ_MAX_GROUP; ++i)
+        if (problems[i].M > 0 && problems[i].N > 0) all[na++] = problems[i];
+    if (na == 0) return 0;
+    return kq_stream_part_bytes(all, na, kq_stream_split_want(all, na));
+}
+
 }  // namespace
 
 extern "C" {
 
 size_t kq_matmul_workspace_bytes(const kq_matmul_problem *problems, int n_problems, int x_dtype) {
-    if (!problems || n_problems <= 0 || x_dtype == KQ_DTYPE_F16) return 0;
-    size_t b = 0;  // a prepared copy per problem (problems sharing x share one)
-    for (int i = 0; i < n_problems && i < KQ_MAX_GROUP; ++i)
-        if (problems[i].M > 0 && problems[i].N > 0) b += kq_prepared_bytes(problems[i].M, problems[i].K);
-    return b;
+    if (!problems || n_problems <= 0) return 0;
+    const size_t b = prepared_total(problems, n_problems, x_dtype) + split_bytes(problems, n_problems);
+    return b ? KQ_MATMUL_COUNTER_BYTES + b : 0;
 }
 
 int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problems, int x_dtype,
@@ -928,10 +951,12 @@ int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problem
     // results back (x_exp)
     kq_matmul_problem prep[KQ_MAX_GROUP];
     const int32_t *exps[KQ_MAX_GROUP] = {};
+    // workspace: arrival counters, prepared rows, then split partial tiles
+    size_t used = KQ_MATMUL_COUNTER_BYTES;
     if (x_dtype != KQ_DTYPE_F16) {
-        if (!workspace || workspace_bytes < kq_matmul_workspace_bytes(problems, n_problems, x_dtype))
+        if (!workspace || workspace_bytes < used + prepared_total(problems, n_problems, x_dtype))
             return KQ_ERR_WORKSPACE_TOO_SMALL;
-        size_t off = 0;
+        size_t off = used;
         for (int i = 0; i < n_problems; ++i) {
             prep[i] = problems[i];
             if (prep[i].M == 0 || prep[i].N == 0) continue;
@@ -955,6 +980,7 @@ int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problem
             prep[i].x_row_stride = problems[i].K;
             off += kq_prepared_bytes(problems[i].M, problems[i].K);
         }
+        used = off;
         problems = prep;
         x_dtype = KQ_DTYPE_F16;
     }
@@ -987,7 +1013,14 @@ int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problem
         int na = 0;
         for (int i = 0; i < n_problems; ++i)
             if (problems[i].M != 0 && problems[i].N != 0) all[na++] = problems[i];
-        if (kq_stream_eligible(all, na)) return kq_stream_launch(all, na, xe0, y_dtype, (hipStream_t)stream);
+        // K past 16 super-blocks: K slices, given room for their partial tiles
+        int split = kq_stream_split_want(all, na);
+        if (split > 1 && (!workspace || ((uintptr_t)workspace & 255) ||
+                          workspace_bytes < used + kq_stream_part_bytes(all, na, split)))
+            split = 1;
+        if (kq_stream_eligible(all, na, split))
+            return kq_stream_launch(all, na, xe0, y_dtype, split, (uint32_t *)workspace,
+                                    split > 1 ? (float *)((char *)workspace + used) : nullptr, (hipStream_t)stream);
         if (kq_mv_eligible(all, na, x_dtype, y_dtype)) return kq_mv_launch(all, na, xe0, y_dtype, (hipStream_t)stream);
     }
     if (live > 0 && mv_mode) {
@@ -1132,7 +1165,7 @@ int kq_moe_gather_rows(const void *x, int x_dtype, int64_t x_row_stride, int32_t
 
 size_t kq_gather_workspace_bytes(int32_t n_pairs, int32_t x_pair_div, int32_t x_skip, int32_t K, int x_dtype) {
     if (x_dtype == KQ_DTYPE_F16 || n_pairs <= 0 || x_pair_div <= 0 || x_skip < 0 || K <= 0) return 0;
-    return kq_prepared_bytes(gather_x_rows(n_pairs, x_pair_div, x_skip), K);
+    return KQ_MATMUL_COUNTER_BYTES + kq_prepared_bytes(gather_x_rows(n_pairs, x_pair_div, x_skip), K);
 }
 
 int kq_moe_mix(const float *y_pairs, const float *scores, int32_t T, int32_t top_k, int32_t N, void *y,

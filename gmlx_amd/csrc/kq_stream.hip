@@ -121,9 +121,15 @@ struct StreamArgs {
     StreamProblem p[KQ_MAX_GROUP];
     const char *x;                     // fp16 [M, K]
     const int32_t *x_exp;              // per-row exponents of prepared activations (results * 2^e), or null
+    uint32_t *ctr;                     // split launches: arrivals per tile (zero on entry, left zero)
+    float *part;                       // split launches: partial tiles [tile][slice][8 rows][16 columns]
     int64_t x_stride;                  // elements
     int32_t M, K, y_dtype, total_tiles, n_problems;
+    int32_t split;                     // K slices per tile (1: the whole K in one item)
 };
+
+// K slices per tile at most (the last arrival loads them all at once).
+constexpr int kMaxSplit = 8;
 
 typedef const __attribute__((address_space(4))) StreamArgs *KArgs;
 
@@ -206,6 +212,18 @@ constexpr int slot_bytes() {
 // s_waitcnt vmcnt(n) (0 <= n <= 63) leaving the other counters unconstrained
 // (gfx9 encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14).
 #define KQ_VMCNT(n) (((n) & 0xF) | ((((n) >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8))
+
+// Wait until at most `newer` tiles of PL loads each are still in flight
+// (K: the most the ring can hold, within the counter's 63).
+template <int PL, int K>
+__device__ __forceinline__ void wait_tiles_left(int newer) {
+    if constexpr (K <= 0) {
+        __builtin_amdgcn_s_waitcnt(KQ_VMCNT(0));
+    } else {
+        if (newer >= K) __builtin_amdgcn_s_waitcnt(KQ_VMCNT(K * PL));
+        else wait_tiles_left<PL, K - 1>(newer);
+    }
+}
 
 // IQ2_XXS kernels keep the fp16 grid / sign tables in LDS; other codecs
 // allocate none (their views never read the tables).
@@ -440,7 +458,7 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
     constexpr int PL = producer_loads<SC, NB>();  // loads per producer per tile
     constexpr int SLOTB = slot_bytes<SC, NB>();
     constexpr int XC = CODEC == KQ_MIX ? KQ_CODEC_Q4_K : CODEC;  // activation layout (Q4_K / Q6_K alike)
-    static_assert(2 * PL <= 63, "vmcnt counts at most 63 loads");
+    static_assert(PL <= 63, "vmcnt counts at most 63 loads");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const KArgs A = (KArgs)__builtin_amdgcn_kernarg_segment_ptr();
     const Iq2Tables &iq2_tab = *IqTables<CODEC>::get();
@@ -448,7 +466,10 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
     const int lane = kq_lane(), r = lane & 15, g = lane >> 4;
     const int G = (int)gridDim.x, B0 = (int)blockIdx.x;
     const int M = A->M;
-    const int my_tiles = (A->total_tiles - B0 + G - 1) / G;
+    // item i = (tile i / S, K-slice i % S); workgroup B0 takes items B0 + j G,
+    // which with G a multiple of S are slice q of tiles T0 + j Gs
+    const int S = A->split, q = B0 % S, Gs = G / S, T0 = B0 / S;
+    const int my_tiles = (A->total_tiles - T0 + Gs - 1) / Gs;
     const uint32_t ring_lds = (uint32_t)(uintptr_t)(LDSP(void))smem;
     floatx4 *red = (floatx4 *)(smem + R * SLOTB);  // [kTmax][C][32 lanes]
 
@@ -458,7 +479,7 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
             const int nt = min(kTmax, my_tiles - round0);
             // copy tile j of the round into slot j % R
             auto copy = [&](int j) {
-                const int tile = B0 + (round0 + j) * G;
+                const int tile = T0 + (round0 + j) * Gs;
                 int32_t begin;
                 const StreamProblem pr = problem_at(A, problem_of(A, tile), begin);
                 const uint32_t rb = pr.row_bytes;
@@ -467,33 +488,36 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
                 const __amdgpu_buffer_rsrc_t rs = kq_buffer(pr.w, pr.w_bytes);
                 const bool q6 = CODEC == KQ_MIX && pr.codec == KQ_CODEC_Q6_K;
                 const uint32_t slot = ring_lds + (uint32_t)(j % R) * SLOTB;
+                // the slice's first super-block in each row (offsets past the
+                // buffer stay past it: row bytes < 2^31)
+                const uint32_t kofs = (uint32_t)(q * NB) * (uint32_t)(q6 ? Geo<KQ_CODEC_Q6_K>::BPB : Geo<XC>::BPB);
 #pragma unroll
                 for (int i = 0; i < PL; ++i) {
                     const int li = i * kProducers + wave;  // the producers' loads interleave
-                    const int q = 64 * li + lane;
+                    const int ch = 64 * li + lane;  // slot chunk
                     uint32_t off;
                     if constexpr (CODEC == KQ_MIX)
-                        off = q6 ? slot_src<KQ_CODEC_Q6_K, NB>(q, row0, last, rb)
-                                 : slot_src<KQ_CODEC_Q4_K, NB>(q, row0, last, rb);
+                        off = q6 ? slot_src<KQ_CODEC_Q6_K, NB>(ch, row0, last, rb)
+                                 : slot_src<KQ_CODEC_Q4_K, NB>(ch, row0, last, rb);
                     else
-                        off = slot_src<CODEC, NB>(q, row0, last, rb);
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDSP(void))(uintptr_t)(slot + 1024 * li), 16, off, 0,
-                                                             0, 0);
+                        off = slot_src<CODEC, NB>(ch, row0, last, rb);
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDSP(void))(uintptr_t)(slot + 1024 * li), 16,
+                                                             off + kofs, 0, 0, 0);
                 }
             };
             const int pre = min(R, nt);
             for (int j = 0; j < pre; ++j) {
                 copy(j);
                 // slot 1 onwards and the partial-tile area hold the consumers'
-                // activation rows until they are in registers
+                // activation rows until they are in registers (a start that
+                // also issued tiles 1 .. R-2 before them was slower: the
+                // first tile, which the consumers wait for, landed later)
                 if (round0 == 0 && j == 0) __builtin_amdgcn_s_barrier();
             }
             for (int b = 0; b < nt; ++b) {
                 // wait for tile b's loads; the tiles copied after it stay in flight
                 const int newer = min(b == 0 ? R - 1 : R - 2, nt - 1 - b);
-                if (newer >= 2) __builtin_amdgcn_s_waitcnt(KQ_VMCNT(2 * PL));
-                else if (newer == 1) __builtin_amdgcn_s_waitcnt(KQ_VMCNT(PL));
-                else __builtin_amdgcn_s_waitcnt(KQ_VMCNT(0));
+                wait_tiles_left<PL, (R - 1 < 63 / PL ? R - 1 : 63 / PL)>(newer);
                 __builtin_amdgcn_s_barrier();  // slot b % R to the consumers; slot (b - 1) % R back
                 if (b >= 1 && b + R - 1 < nt) copy(b + R - 1);
             }
@@ -520,7 +544,7 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
         const uint32_t xreg = ring_lds + SLOTB + (uint32_t)(c * kXRows * kXRowLds);
         // lanes past the segment read past the buffer (zeros, inside the row's LDS pitch)
         const uint32_t loff =
-            16u * lane < 512u * SB ? (uint32_t)(kb0 * KQ_QK * 2) + 16u * lane : 0x80000000u;
+            16u * lane < 512u * SB ? (uint32_t)((q * NB + kb0) * KQ_QK * 2) + 16u * lane : 0x80000000u;
 #pragma unroll
         for (int m = 0; m < kXRows; ++m)
             if (m < M)
@@ -563,7 +587,7 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
         for (int b = 0; b < nt; ++b) {
             __builtin_amdgcn_s_barrier();  // tile b has landed in slot b % R
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-            const int tile = B0 + (round0 + b) * G;
+            const int tile = T0 + (round0 + b) * Gs;
             const uint32_t slot = ring_lds + (uint32_t)(b % R) * SLOTB;
             floatx4 acc = {0, 0, 0, 0};
             if constexpr (CODEC == KQ_MIX) {
@@ -587,20 +611,79 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
         }
         __builtin_amdgcn_s_barrier();  // every partial tile of the round is in LDS
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-        // ---- sum the C partial tiles in consumer order and store: output f = (b, m, n)
-        for (int f = (int)threadIdx.x - 64 * kProducers; f < nt * 8 * 16; f += 64 * C) {
-            const int b = f >> 7, m = (f >> 4) & 7, n = f & 15;
-            if (m >= M) continue;
-            const int ln = 16 * (m >> 2) + n, e = m & 3;
-            float sum = red[(b * C) * 32 + ln][e];
-#pragma unroll
-            for (int c2 = 1; c2 < C; ++c2) sum += red[(b * C + c2) * 32 + ln][e];
+        // ---- consumer c sums tiles b = c, c + C, ... of the round over the C
+        // partial tiles in consumer order (deterministic).  Lane l holds
+        // outputs o = l and 64 + l of the tile: row m = o >> 4, column l & 15.
+        const int n = lane & 15, mq = lane >> 4;
+        auto store = [&](int tile, int m, float sum) {
+            if (m >= M) return;
             if (A->x_exp) sum = ldexpf(sum, A->x_exp[m]);
-            const int tile = B0 + (round0 + b) * G;
             int32_t begin;
             const StreamProblem pr = problem_at(A, problem_of(A, tile), begin);
             const int nn = (tile - begin) * 16 + n;
             if (nn < pr.N) kq_store_out(pr.y, A->y_dtype, (int64_t)m * pr.y_stride + nn, sum);
+        };
+        for (int b = c; b < nt; b += C) {
+            const int tile = T0 + (round0 + b) * Gs;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int ln = 16 * h + n;
+                float sum = red[(b * C) * 32 + ln][mq];
+#pragma unroll
+                for (int c2 = 1; c2 < C; ++c2) sum += red[(b * C + c2) * 32 + ln][mq];
+                if (S == 1) store(tile, 4 * h + mq, sum);
+                else if (4 * h + mq < M)
+                    __hip_atomic_store(A->part + ((size_t)tile * S + q) * 128 + 64 * h + lane, sum, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        if (S > 1) {
+            // Split launches: the slice's partial tiles out, then one arrival
+            // per tile (lane i: the wave's i-th tile of the round); the last
+            // of a tile's S arrivals sums the S partials in slice order
+            // (deterministic), stores, and clears the count for the next call.
+            // The partials move by agent-scope stores and loads, which are
+            // coherent across the XCDs' L2s by themselves; an agent-scope
+            // fence would write back and invalidate whole L2s instead (it
+            // made a split launch slower than the unsplit one, measured).
+            // Ordering: the stores have completed (vmcnt 0) before the
+            // arrival is counted, and the loads issue only after the count
+            // returns.
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            __builtin_amdgcn_s_waitcnt(KQ_VMCNT(0));
+            const int bl = c + lane * C;
+            bool last = false;
+            if (bl < nt) {
+                uint32_t *ctr = A->ctr + (T0 + (round0 + bl) * Gs);
+                last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(S - 1);
+                if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            uint64_t mine = __builtin_amdgcn_ballot_w64(last);
+            if (mine) {
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+                while (mine) {
+                    const int i = __builtin_ctzll(mine);
+                    mine &= mine - 1;
+                    const int tile = T0 + (round0 + c + i * C) * Gs;
+                    const float *pp = A->part + (size_t)tile * S * 128;
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const int o = 64 * h + lane;
+                        if (4 * h + mq >= M) continue;
+                        float v[kMaxSplit];
+#pragma unroll
+                        for (int s2 = 0; s2 < kMaxSplit; ++s2)
+                            v[s2] = s2 < S ? __hip_atomic_load(pp + s2 * 128 + o, __ATOMIC_RELAXED,
+                                                               __HIP_MEMORY_SCOPE_AGENT)
+                                           : 0.f;
+                        float sum = v[0];
+#pragma unroll
+                        for (int s2 = 1; s2 < kMaxSplit; ++s2)
+                            if (s2 < S) sum += v[s2];
+                        store(tile, 4 * h + mq, sum);
+                    }
+                }
+            }
         }
         if (round0 + kTmax < my_tiles) {
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
@@ -613,13 +696,21 @@ template <int CODEC, int SB, int C>
 int launch(const StreamArgs &a, int grid, hipStream_t s) {
     constexpr int NB = SB * C;
     constexpr int SC = SlotCodec<CODEC>::C;
-    // three tile slots when they fit beside the partial tiles, else two
+    // as many tile slots as fit beside the partial tiles, 2 to 6: the bytes a
+    // CU keeps in flight set its share of the bandwidth, so small slots (K
+    // slices, short K) take deeper rings
     constexpr size_t red = (size_t)kTmax * C * 32 * 16;
     constexpr size_t budget = 150 * 1024 - (CODEC == KQ_CODEC_IQ2_XXS ? sizeof(Iq2Tables) : 0);
-    constexpr size_t xregion = (size_t)slot_bytes<SC, NB>() + (size_t)C * kXRows * kXRowLds;
+    // the activation rows are staged from slot 1 on
+    constexpr size_t sb = slot_bytes<SC, NB>();
+    constexpr size_t xregion = sb + (size_t)C * kXRows * kXRowLds;
     constexpr auto need = [](size_t ring) { return ring + red > xregion ? ring + red : xregion; };
-    constexpr int R = need(3 * (size_t)slot_bytes<SC, NB>()) <= budget ? 3 : 2;
-    constexpr size_t lds = need((size_t)R * slot_bytes<SC, NB>());
+    constexpr int R = need(6 * sb) <= budget   ? 6
+                      : need(5 * sb) <= budget ? 5
+                      : need(4 * sb) <= budget ? 4
+                      : need(3 * sb) <= budget ? 3
+                                               : 2;
+    constexpr size_t lds = need((size_t)R * sb);
     static_assert(lds <= budget, "stream kernel LDS");
     static bool raised = false;
     if (!raised) {
@@ -632,15 +723,25 @@ int launch(const StreamArgs &a, int grid, hipStream_t s) {
     return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
 }
 
-// Consumers for K = 256 nb: one super-block each for 2 and 4 super-blocks,
-// two each for 8 and 16 (4 and 8 consumers); other K take the other
-// small-batch paths.
+// Consumers for K = 256 nb (one K-slab of SB super-blocks each): as many as
+// the slab count allows up to 12, so that two or more share each SIMD and
+// hide each other's LDS and MFMA latency (8 consumers of one super-block beat
+// 4 of two by 1-2 us on the 8-block slices of a split down projection,
+// measured); 16 blocks take 8 consumers of two.  The mixed Q4_K + Q6_K form
+// keeps two super-blocks per consumer where one would spill.
 template <int CODEC>
 int launch_codec(const StreamArgs &a, int nb, int grid, hipStream_t s) {
+    constexpr bool mix = CODEC == KQ_MIX;
     switch (nb) {
     case 2: return launch<CODEC, 1, 2>(a, grid, s);
     case 4: return launch<CODEC, 1, 4>(a, grid, s);
-    case 8: return launch<CODEC, 2, 4>(a, grid, s);
+    case 6: return launch<CODEC, 1, 6>(a, grid, s);
+    case 8:
+        if constexpr (mix) return launch<CODEC, 2, 4>(a, grid, s);
+        else return launch<CODEC, 1, 8>(a, grid, s);
+    case 12:
+        if constexpr (mix) return launch<CODEC, 2, 6>(a, grid, s);
+        else return launch<CODEC, 1, 12>(a, grid, s);
     case 16: return launch<CODEC, 2, 8>(a, grid, s);
     default: return KQ_ERR_BAD_SHAPE;
     }
@@ -648,22 +749,52 @@ int launch_codec(const StreamArgs &a, int nb, int grid, hipStream_t s) {
 
 bool stream_k_ok(int K) {
     const int nb = K / KQ_QK;
-    return nb == 2 || nb == 4 || nb == 8 || nb == 16;
+    return nb == 2 || nb == 4 || nb == 6 || nb == 8 || nb == 12 || nb == 16;
+}
+
+int64_t group_tiles(const kq_matmul_problem *ps, int n) {
+    int64_t tiles = 0;
+    for (int i = 0; i < n; ++i) tiles += (ps[i].N + 15) / 16;
+    return tiles;
 }
 
 }  // namespace
 
+// K slices a launch of this group would take given the workspace (1: whole
+// K).  K past 16 super-blocks (the down projections) is cut into at most 8
+// slices of 8 super-blocks, else 12, 6 or 4 (the first that divides K);
+// GMLX_KQ_SPLITK=s asks for s slices (tests and tuning; 1 turns splitting
+// off).
+int kq_stream_split_want(const kq_matmul_problem *ps, int n) {
+    if (n <= 0 || n > kStreamProblems || ps[0].M < 1 || ps[0].M > 8 || ps[0].K % KQ_QK) return 1;
+    const int nb = ps[0].K / KQ_QK;
+    if (group_tiles(ps, n) * 4 > (int64_t)KQ_MATMUL_COUNTER_BYTES) return 1;
+    if (const char *e = getenv("GMLX_KQ_SPLITK")) {
+        const int s = atoi(e);
+        return s >= 1 && s <= kMaxSplit && nb % s == 0 && stream_k_ok(ps[0].K / s) ? s : 1;
+    }
+    if (stream_k_ok(ps[0].K)) return 1;
+    for (const int w : {8, 12, 6, 4})
+        if (nb % w == 0 && nb / w <= kMaxSplit) return nb / w;
+    return 1;
+}
+
+// Bytes of partial tiles a split launch writes (after the counter region).
+size_t kq_stream_part_bytes(const kq_matmul_problem *ps, int n, int split) {
+    return split > 1 ? ((size_t)group_tiles(ps, n) * split * 512 + 255) & ~(size_t)255 : 0;
+}
+
 // Eligibility (the dispatcher also requires fp16 activations): M <= 8, at
-// most 4 problems sharing x / stride / M / K, one codec or Q4_K with Q6_K, K
-// of 2, 4, 8 or 16 super-blocks, weights and x addressable with 31-bit buffer
-// offsets.  GMLX_KQ_STREAM=0 declines, =2 forces every eligible launch here;
-// GMLX_KQ_STREAM_WGS=n caps the grid at n workgroups (tests).
-bool kq_stream_eligible(const kq_matmul_problem *ps, int n) {
-    if (n <= 0 || n > kStreamProblems) return false;
+// most 4 problems sharing x / stride / M / K, one codec or Q4_K with Q6_K,
+// K / split of 2, 4, 8 or 16 super-blocks, weights and x addressable with
+// 31-bit buffer offsets.  GMLX_KQ_STREAM=0 declines, =2 forces every eligible
+// launch here; GMLX_KQ_STREAM_WGS=n caps the grid at n workgroups (tests).
+bool kq_stream_eligible(const kq_matmul_problem *ps, int n, int split) {
+    if (n <= 0 || n > kStreamProblems || split < 1 || split > kMaxSplit) return false;
     const char *env = getenv("GMLX_KQ_STREAM");
     if (env && env[0] == '0' && env[1] == 0) return false;
     const kq_matmul_problem &q0 = ps[0];
-    if (q0.M < 1 || q0.M > 8 || !stream_k_ok(q0.K)) return false;
+    if (q0.M < 1 || q0.M > 8 || q0.K % (KQ_QK * split) || !stream_k_ok(q0.K / split)) return false;
     bool mixed = false;
     for (int i = 0; i < n; ++i) {
         const kq_matmul_problem &q = ps[i];
@@ -675,25 +806,29 @@ bool kq_stream_eligible(const kq_matmul_problem *ps, int n) {
         for (int i = 0; i < n; ++i)
             if (ps[i].codec != KQ_CODEC_Q4_K && ps[i].codec != KQ_CODEC_Q6_K) return false;
     if ((int64_t)(q0.M - 1) * q0.x_row_stride * 2 + (int64_t)q0.K * 2 >= (int64_t)0x80000000LL) return false;
+    const int64_t tiles = group_tiles(ps, n);
+    if (split > 1 && tiles * 4 > (int64_t)KQ_MATMUL_COUNTER_BYTES) return false;
     // Routing (measured at the Qwen3-8B shapes, B = 1..8): the kernel's fixed
     // cost (ten waves per CU, the activation slab, the partial-tile sums) pays
-    // off from about four tiles per CU (gate|up: 15.4-15.8 us against
-    // 16.4-17.7 us for the LDS-staged path); at one or two tiles per CU (o,
-    // q|k|v) the LDS-staged path is faster, and a Q4_K + Q6_K group is slower
-    // here (its producers keep both slot geometries live and spill).
-    // GMLX_KQ_STREAM=2 takes every eligible launch (tests).
+    // off from about four items (tiles, or tile slices of a split launch) per
+    // CU (gate|up: 15.4-15.8 us against 16.4-17.7 us for the LDS-staged
+    // path); at one or two per CU (o, q|k|v) the LDS-staged path is faster,
+    // and a Q4_K + Q6_K group is slower here (its producers keep both slot
+    // geometries live and spill).  GMLX_KQ_STREAM=2 takes every eligible
+    // launch (tests).
     if (!(env && env[0] == '2' && env[1] == 0)) {
         if (mixed) return false;
-        int64_t tiles = 0;
-        for (int i = 0; i < n; ++i) tiles += (ps[i].N + 15) / 16;
-        if (tiles < 4 * (int64_t)device_cus()) return false;
+        if (tiles * split < 4 * (int64_t)device_cus()) return false;
     }
     return true;
 }
 
-// Problems validated, eligible and all live; x is fp16, x_exp its per-row
-// exponents or null.
-int kq_stream_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, int y_dtype, hipStream_t s) {
+// Problems validated, eligible (for this split) and all live; x is fp16,
+// x_exp its per-row exponents or null.  Split launches (split > 1) take the
+// arrival counters ctr (one per tile, zero on entry; left zero) and room for
+// kq_stream_part_bytes at part.
+int kq_stream_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, int y_dtype, int split,
+                     uint32_t *ctr, float *part, hipStream_t s) {
     StreamArgs a;
     int tiles = 0;
     bool mixed = false;
@@ -717,19 +852,25 @@ int kq_stream_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, i
     const kq_matmul_problem &q0 = ps[0];
     a.x = (const char *)q0.x;
     a.x_exp = x_exp;
+    a.ctr = ctr;
+    a.part = part;
     a.x_stride = q0.x_row_stride;
     a.M = q0.M;
     a.K = q0.K;
     a.y_dtype = y_dtype;
     a.total_tiles = tiles;
     a.n_problems = n;
+    a.split = split;
     int grid = device_cus();
     if (const char *e = getenv("GMLX_KQ_STREAM_WGS")) {  // smaller grids: more tiles and rounds per workgroup
         const int w = atoi(e);
         if (w > 0 && w < grid) grid = w;
     }
-    if (grid > tiles) grid = tiles;
-    const int nb = q0.K / KQ_QK;
+    // a multiple of the split (each workgroup keeps one K slice), at most one item each
+    grid = grid / split * split;
+    if (grid < split) grid = split;
+    if (grid > tiles * split) grid = tiles * split;
+    const int nb = q0.K / KQ_QK / split;
     if (mixed) return launch_codec<KQ_MIX>(a, nb, grid, s);
     switch (q0.codec) {
     case KQ_CODEC_Q4_K: return launch_codec<KQ_CODEC_Q4_K>(a, nb, grid, s);

@@ -96,11 +96,14 @@ def _rows_view(x):
 
 
 class _Workspaces:
-    """Scratch per (op family, device, stream), grown on demand.  No kernel
-    needs it cleared (attention split partials and prepared activation rows
-    are written before they are read), so one buffer serves every later call
-    of its family on its stream; families keep their own, so a call of one
-    never overwrites what a queued call of another still reads."""
+    """Scratch per (op family, device, stream), grown on demand.  Buffers
+    start zeroed: a matmul / gather workspace begins with per-tile arrival
+    counters that must be zero on a buffer's first use and that every call
+    leaves zero; the rest (attention split partials, prepared activation
+    rows, partial tiles) is written before it is read.  So one buffer serves
+    every later call of its family on its stream; families keep their own,
+    so a call of one never overwrites what a queued call of another still
+    reads."""
 
     def __init__(self):
         self._ws = {}
@@ -109,7 +112,7 @@ class _Workspaces:
         key = (kind, device.index, stream_handle)
         cur = self._ws.get(key)
         if cur is None or cur.numel() < nbytes:
-            cur = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+            cur = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
             self._ws[key] = cur
         return cur
 

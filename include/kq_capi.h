@@ -101,14 +101,29 @@ typedef struct {
     int32_t codec;
 } kq_matmul_problem;
 
+/* Every non-empty workspace of kq_quantized_matmul_grouped and of the
+ * gathers below begins with KQ_MATMUL_COUNTER_BYTES of arrival counters:
+ * zero them once when the buffer is allocated (any fill); each call leaves
+ * them zero, and nothing else may write them (do not hand such a workspace
+ * to the attention entry points).  Calls sharing a workspace must be
+ * ordered (same stream). */
+#define KQ_MATMUL_COUNTER_BYTES ((size_t)16 << 10)
+
 /* Workspace bytes kq_quantized_matmul_grouped needs for these problems and
- * activation dtype: 0 for fp16; for bf16 / fp32 activations, room for an
- * fp16 copy of each problem's rows (problems sharing x share one) and one
- * int32 exponent per row.  Every kernel computes with fp16 operands: a
- * bf16 / fp32 row enters as fp16(x * 2^-e) with e chosen per row so its
- * largest magnitude lands in [2^14, 2^15), and the fp32 results are scaled
- * back by 2^e before rounding to y_dtype -- no overflow past 65504, no
- * flush below 2^-14, bf16 values exact.  No zero-fill needed. */
+ * activation dtype, 0 when it needs none: the counter region above, then
+ *  - for bf16 / fp32 activations an fp16 copy of each problem's rows
+ *    (problems sharing x share one) and one int32 exponent per row.  Every
+ *    kernel computes with fp16 operands: a bf16 / fp32 row enters as
+ *    fp16(x * 2^-e) with e chosen per row so its largest magnitude lands in
+ *    [2^14, 2^15), and the fp32 results are scaled back by 2^e before
+ *    rounding to y_dtype -- no overflow past 65504, no flush below 2^-14,
+ *    bf16 values exact;
+ *  - for groups of at most 8 rows whose K runs past 16 super-blocks (the
+ *    down projections), fp32 partial tiles of K slices: such a launch cuts K
+ *    into slices of 8 super-blocks, and the last slice of each 16-row tile to
+ *    finish sums the slices in slice order (results stay independent of
+ *    scheduling).  With fp16 activations a workspace smaller than this
+ *    (none included) takes the unsplit kernels instead. */
 size_t kq_matmul_workspace_bytes(const kq_matmul_problem *problems, int n_problems, int x_dtype);
 
 /* kq.quantized_matmul(x, w, scales, codec, transpose=True) -- the
@@ -211,11 +226,12 @@ int kq_moe_gather_rows(const void *x, int x_dtype, int64_t x_row_stride, int32_t
                        size_t workspace_bytes, kq_stream_t stream);
 
 /* Workspace of the three gathers above: 0 for fp16 activations; for bf16 /
- * fp32 ones an fp16 copy of the rows the pairs read (row p / x_pair_div +
- * p / x_skip) with one int32 exponent per row, prepared as for
- * kq_quantized_matmul_grouped (x_skip 0 for kq_gather_qmm /
- * kq_moe_glu_gather).  Results are scaled back in fp32 before the GLU and
- * biases.  No zero-fill needed. */
+ * fp32 ones the counter region (KQ_MATMUL_COUNTER_BYTES, zeroed once, so one
+ * buffer may serve matmuls and gathers), then an fp16 copy of the rows the
+ * pairs read (row p / x_pair_div + p / x_skip) with one int32 exponent per
+ * row, prepared as for kq_quantized_matmul_grouped (x_skip 0 for
+ * kq_gather_qmm / kq_moe_glu_gather).  Results are scaled back in fp32
+ * before the GLU and biases. */
 size_t kq_gather_workspace_bytes(int32_t n_pairs, int32_t x_pair_div, int32_t x_skip, int32_t K,
                                  int x_dtype);
 

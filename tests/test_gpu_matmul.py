@@ -175,15 +175,20 @@ def test_module_forward():
 
 
 # The small-batch paths of kq_quantized_matmul_grouped, forced in turn: the
-# producer / consumer weight-streaming kernel (M <= 8, K of 2, 4, 8 or 16
-# super-blocks), the LDS-staged persistent path (kq_mv), the register
-# persistent path (kq_qmv) and the general tiled path.  Small grids make every
-# workgroup walk many tiles, with partial ring rounds.
+# producer / consumer weight-streaming kernel (M <= 8, K of 2, 4, 6, 8, 12 or
+# 16 super-blocks, or K cut into such slices: by default past 16 super-blocks,
+# GMLX_KQ_SPLITK=s slices where they divide K), the LDS-staged persistent
+# path (kq_mv), the register persistent path (kq_qmv) and the general tiled
+# path.  Small grids make every workgroup walk many tiles, with partial ring
+# rounds.
 SMALL_BATCH_PATHS = [
     ("default routing", {}),
     ("stream, 3 workgroups", {"GMLX_KQ_STREAM": "2", "GMLX_KQ_STREAM_WGS": "3"}),
     ("stream, 13 workgroups", {"GMLX_KQ_STREAM": "2", "GMLX_KQ_STREAM_WGS": "13"}),
     ("stream, full grid", {"GMLX_KQ_STREAM": "2"}),
+    ("stream, split 2, 5 workgroups", {"GMLX_KQ_STREAM": "2", "GMLX_KQ_SPLITK": "2", "GMLX_KQ_STREAM_WGS": "5"}),
+    ("stream, split 3", {"GMLX_KQ_STREAM": "2", "GMLX_KQ_SPLITK": "3"}),
+    ("stream, split 4, 13 workgroups", {"GMLX_KQ_STREAM": "2", "GMLX_KQ_SPLITK": "4", "GMLX_KQ_STREAM_WGS": "13"}),
     ("mv, default grid", {"GMLX_KQ_STREAM": "0", "GMLX_KQ_MV": "2"}),
     ("mv, 3 workgroups", {"GMLX_KQ_STREAM": "0", "GMLX_KQ_MV": "2", "GMLX_KQ_MV_WGS": "3"}),
     ("mv, 7 workgroups, ring 2", {"GMLX_KQ_STREAM": "0", "GMLX_KQ_MV": "2", "GMLX_KQ_MV_WGS": "7",
@@ -193,8 +198,8 @@ SMALL_BATCH_PATHS = [
     ("persistent, 3 workgroups", {"GMLX_KQ_STREAM": "0", "GMLX_KQ_MV": "0", "GMLX_KQ_QMV_WGS": "3"}),
     ("general", {"GMLX_KQ_STREAM": "0", "GMLX_KQ_MV": "0", "GMLX_KQ_PERSISTENT": "0"}),
 ]
-PATH_KNOBS = ("GMLX_KQ_STREAM", "GMLX_KQ_STREAM_WGS", "GMLX_KQ_MV", "GMLX_KQ_MV_WGS", "GMLX_KQ_MV_DEPTH",
-              "GMLX_KQ_QMV_WGS", "GMLX_KQ_PERSISTENT")
+PATH_KNOBS = ("GMLX_KQ_STREAM", "GMLX_KQ_STREAM_WGS", "GMLX_KQ_SPLITK", "GMLX_KQ_MV", "GMLX_KQ_MV_WGS",
+              "GMLX_KQ_MV_DEPTH", "GMLX_KQ_QMV_WGS", "GMLX_KQ_PERSISTENT")
 
 
 @pytest.mark.parametrize("codec,N,K,M", [
@@ -213,6 +218,9 @@ PATH_KNOBS = ("GMLX_KQ_STREAM", "GMLX_KQ_STREAM_WGS", "GMLX_KQ_MV", "GMLX_KQ_MV_
     ("q4_k", 4000, 512, 2),        # stream: 250 tiles, several rounds on small grids
     ("q6_k", 700, 2048, 7),
     ("iq2_xxs", 330, 4096, 4),
+    ("q4_k", 333, 1536, 5),        # stream: 6 blocks, 6 consumers
+    ("q6_k", 200, 3072, 8),        # stream: 12 blocks, 12 consumers
+    ("iq2_xxs", 150, 1536, 3),
 ])
 def test_small_batch_paths(codec, N, K, M, monkeypatch):
     """Every small-batch path matches the fp64 reference on the same inputs."""
@@ -230,6 +238,45 @@ def test_small_batch_paths(codec, N, K, M, monkeypatch):
             monkeypatch.setenv(k, v)
         got = _mm(x, wire, codec).float().cpu().numpy()
         assert okq.max_rel(got, ref) <= TOL, (name, okq.max_rel(got, ref))
+
+
+@pytest.mark.parametrize("codec,N,K,M,x_dtype", [
+    ("q6_k", 4096, 12288, 8, "float16"),    # the Qwen3-8B down projection at batch 8
+    ("q4_k", 1000, 12288, 1, "bfloat16"),
+    ("q6_k", 515, 14336, 5, "float32"),     # 7 slices, a partial last tile
+    ("iq2_xxs", 300, 8192, 3, "float16"),   # 4 slices
+    ("q4_k", 700, 7168, 6, "float16"),      # 28 blocks: 7 slices of 4
+    ("q6_k", 300, 9216, 4, "bfloat16"),     # 36 blocks: 3 slices of 12
+])
+def test_split_k_stream(codec, N, K, M, x_dtype, monkeypatch):
+    """K past 16 super-blocks at <= 8 rows: the K-sliced streaming launch
+    matches the fp64 reference and the unsplit LDS-staged path, repeats
+    bitwise, and leaves the workspace's arrival counters zero."""
+    import torch
+    from gmlx_amd import _lib, ops
+    for k in PATH_KNOBS:
+        monkeypatch.delenv(k, raising=False)
+    rng = np.random.default_rng(N + K + M)
+    if codec == "iq2_xxs":
+        wire = okq.random_valid_blocks(rng, codec, N * K // 256).reshape(N, -1)
+    else:
+        wire = quantized_weights(rng, codec, N, K)
+    x = _dev(fp16_rows(rng, M, K)).to(getattr(torch, x_dtype))
+    ref = okq.qmm_ref(x.float().cpu().numpy(), wire, codec)
+    w = _dev(wire)
+    monkeypatch.setenv("GMLX_KQ_STREAM", "2")
+    outs = [ops.quantized_matmul(x, w, codec=codec, out_dtype=torch.float32) for _ in range(3)]
+    torch.cuda.synchronize()
+    got = outs[0].cpu().numpy()
+    assert okq.max_rel(got, ref) <= TOL, okq.max_rel(got, ref)
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+    ws = ops._WS.get("matmul", x.device, ops._stream(x).value, 0)
+    assert int(ws[:_lib.MATMUL_COUNTER_BYTES].count_nonzero()) == 0
+    monkeypatch.setenv("GMLX_KQ_STREAM", "0")
+    monkeypatch.setenv("GMLX_KQ_MV", "2")
+    unsplit = ops.quantized_matmul(x, w, codec=codec, out_dtype=torch.float32).cpu().numpy()
+    assert okq.max_rel(got, unsplit) <= TOL
 
 
 @pytest.mark.parametrize("K,M", [(4096, 8), (8192, 3), (1280, 16), (2048, 1)])

@@ -31,6 +31,20 @@ def test_library_exports_every_declared_symbol():
     assert set(declared) == set(_lib.EXPORTS)
 
 
+def test_header_sizes_match_the_python_mirror():
+    from gmlx_amd import _lib
+    text = open(os.path.join(ROOT, "include", "kq_capi.h")).read()
+
+    def define(name):
+        m = re.search(r"#define\s+" + name + r"\s+(.+)", text)
+        expr = re.sub(r"\(size_t\)", "", m.group(1))
+        return eval(expr, {})
+
+    assert define("KQ_MATMUL_COUNTER_BYTES") == _lib.MATMUL_COUNTER_BYTES
+    assert define("KQ_SDPA_NOALLOC_SCRATCH_BYTES") == _lib.SDPA_NOALLOC_SCRATCH_BYTES
+    assert define("KQ_MAX_GROUP") == _lib.MAX_GROUP
+
+
 def test_version_strerror_and_capabilities():
     from gmlx_amd import _lib, ops
     assert "gfx950" in _lib.version()
@@ -82,18 +96,20 @@ def test_host_validation_rejects_before_launch():
         _lib.KQ_ERR_WORKSPACE_TOO_SMALL
     assert L.kq_quantized_matmul_grouped(arr, 9, _lib.DTYPE_F16, _lib.DTYPE_F16, None, 0, None) == \
         _lib.KQ_ERR_TOO_MANY_PROBLEMS
-    # fp16 activations need no workspace; bf16 / fp32 ones an fp16 copy of the
-    # rows (256-byte aligned) and an int32 exponent per row
+    # fp16 activations at K <= 16 super-blocks need no workspace; bf16 / fp32
+    # ones the counter region, then an fp16 copy of the rows (256-byte
+    # aligned) and an int32 exponent per row
+    ctr = _lib.MATMUL_COUNTER_BYTES
     small_n = dict(good, N=16, K=4096, w_row_bytes=144 * 16, x_row_stride=4096)
     arr = (P * 1)(P(**small_n))
     assert L.kq_matmul_workspace_bytes(arr, 1, _lib.DTYPE_F16) == 0
     M = small_n["M"]
     want = -(-M * 4096 * 2 // 256) * 256 + -(-M * 4 // 256) * 256
-    assert L.kq_matmul_workspace_bytes(arr, 1, _lib.DTYPE_BF16) == want
+    assert L.kq_matmul_workspace_bytes(arr, 1, _lib.DTYPE_BF16) == ctr + want
     # gathers: pair p reads row p / x_pair_div + p / x_skip
     assert L.kq_gather_workspace_bytes(8, 2, 0, 512, _lib.DTYPE_F16) == 0
-    assert L.kq_gather_workspace_bytes(8, 2, 0, 512, _lib.DTYPE_F32) == 4 * 512 * 2 + 256
-    assert L.kq_gather_workspace_bytes(9, 1, 4, 256, _lib.DTYPE_BF16) == (9 + 2) * 256 * 2 + 256
+    assert L.kq_gather_workspace_bytes(8, 2, 0, 512, _lib.DTYPE_F32) == ctr + 4 * 512 * 2 + 256
+    assert L.kq_gather_workspace_bytes(9, 1, 4, 256, _lib.DTYPE_BF16) == ctr + (9 + 2) * 256 * 2 + 256
     assert L.kq_sdpa_decode_ragged(16, 16, 16, 16, 16, 16, 2, 8, 3, 128, 100, 0.1, _lib.DTYPE_F16, 16, 16,
                                    1 << 20, None) == _lib.KQ_ERR_BAD_SHAPE
     assert L.kq_sdpa_decode_ragged(16, 16, 16, 16, 16, 16, 2, 8, 2, 80, 100, 0.1, _lib.DTYPE_F16, 16, 16,
@@ -116,6 +132,36 @@ def test_host_validation_rejects_before_launch():
     assert L.kq_dequantize(16, 4, 99, 16, 0, None) == _lib.KQ_ERR_UNSUPPORTED_CODEC
     assert L.kq_quantize(16, 2, 100, 100, 12, 16, None) == _lib.KQ_ERR_BAD_SHAPE
     _ = ctypes
+
+
+def test_split_k_workspace(monkeypatch):
+    """K past 16 super-blocks at <= 8 rows (a down projection) cuts K into
+    slices of 8 super-blocks: 512 bytes of fp32 partials per (16-row tile,
+    slice) after the counter region; more rows, or GMLX_KQ_SPLITK=1, none."""
+    from gmlx_amd import _lib
+    L = _lib.lib()
+    P = _lib.MatmulProblem
+    ctr = _lib.MATMUL_COUNTER_BYTES
+    down = dict(w=1 << 20, w_row_bytes=210 * 48, x=1 << 21, x_row_stride=12288, y=1 << 22, y_row_stride=4096,
+                M=8, N=4096, K=12288, codec=_lib.CODEC_ID["q6_k"])
+    arr = (P * 1)(P(**down))
+    tiles, slices = 4096 // 16, 48 // 8
+    assert L.kq_matmul_workspace_bytes(arr, 1, _lib.DTYPE_F16) == ctr + tiles * slices * 512
+    prepared = 8 * 12288 * 2 + 256
+    assert L.kq_matmul_workspace_bytes(arr, 1, _lib.DTYPE_BF16) == ctr + prepared + tiles * slices * 512
+    monkeypatch.setenv("GMLX_KQ_SPLITK", "3")
+    assert L.kq_matmul_workspace_bytes(arr, 1, _lib.DTYPE_F16) == ctr + tiles * 3 * 512
+    monkeypatch.setenv("GMLX_KQ_SPLITK", "1")
+    assert L.kq_matmul_workspace_bytes(arr, 1, _lib.DTYPE_F16) == 0
+    monkeypatch.delenv("GMLX_KQ_SPLITK")
+    arr = (P * 1)(P(**dict(down, M=9)))
+    assert L.kq_matmul_workspace_bytes(arr, 1, _lib.DTYPE_F16) == 0
+    # slices of 8 super-blocks first, then 12, 6, 4: K of 56 -> 7 slices, 36
+    # -> 3 (of 12), 28 -> 7 (of 4); 43 (no width divides it): none
+    for nb, slices in ((56, 7), (36, 3), (28, 7), (43, 0)):
+        arr = (P * 1)(P(**dict(down, K=256 * nb, x_row_stride=256 * nb, w_row_bytes=210 * nb)))
+        want = ctr + tiles * slices * 512 if slices else 0
+        assert L.kq_matmul_workspace_bytes(arr, 1, _lib.DTYPE_F16) == want, nb
 
 
 def test_ops_refuse_cpu_tensors():
