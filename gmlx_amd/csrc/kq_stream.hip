@@ -1,5 +1,7 @@
-// Weight-streaming small-batch matmul (M <= 8 activation rows) for problems
-// that share their activations: the decode-step projections at batch 1..8.
+// Weight-streaming small-batch matmul (M <= 16 activation rows) for problems
+// that share their activations: the decode-step projections at batch 1..16
+// (the MFMA computes 16 rows either way; 8-row launches keep half the
+// partial-tile LDS and epilogue work).
 //
 //   y[M, N] = x[M, K] . dequant(W[N, K])^T,  fp32 accumulation
 //
@@ -47,8 +49,10 @@ constexpr int KQ_MIX = 0x7F;  // Q4_K and Q6_K problems in one launch
 // x region: per consumer kXRows rows of up to 1 KB at a pitch of kXRowLds
 // bytes (the extra 16 staggers the rows over the LDS banks)
 constexpr int kXRows = 8, kXRowLds = 1040;
-constexpr int kTmax = 8;      // tiles per workgroup per round
 constexpr int kProducers = 2;
+// MR activation rows per launch (8, or 16 for M = 9..16): tiles per
+// workgroup per round (the partial tiles of a round fill the same LDS)
+__host__ __device__ constexpr int tiles_per_round(int MR) { return MR == 8 ? 8 : 4; }
 
 // A super-block's LDS slot is SLOT bytes (16-aligned), filled by SLOT / 16
 // chunk loads; chunk cb reads the 16 block bytes from src(cb), always inside
@@ -122,7 +126,7 @@ struct StreamArgs {
     const char *x;                     // fp16 [M, K]
     const int32_t *x_exp;              // per-row exponents of prepared activations (results * 2^e), or null
     uint32_t *ctr;                     // split launches: arrivals per tile (zero on entry, left zero)
-    float *part;                       // split launches: partial tiles [tile][slice][8 rows][16 columns]
+    float *part;                       // split launches: partial tiles [tile][slice][MR rows][16 columns]
     int64_t x_stride;                  // elements
     int32_t M, K, y_dtype, total_tiles, n_problems;
     int32_t split;                     // K slices per tile (1: the whole K in one item)
@@ -450,8 +454,8 @@ __device__ __forceinline__ void mma_slab(floatx4 &acc, uint32_t row_lds, const h
 }
 
 // CODEC: KQ_CODEC_* or KQ_MIX.  SB: super-blocks per consumer, C consumers
-// (K = 256 SB C).  R: tile slots in the ring.
-template <int CODEC, int SB, int C, int R>
+// (K = 256 SB C).  R: tile slots in the ring.  MR: activation rows (8 or 16).
+template <int CODEC, int SB, int C, int R, int MR>
 __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(StreamArgs a_) {
     constexpr int NB = SB * C;
     constexpr int SC = SlotCodec<CODEC>::C;
@@ -459,6 +463,9 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
     constexpr int SLOTB = slot_bytes<SC, NB>();
     constexpr int XC = CODEC == KQ_MIX ? KQ_CODEC_Q4_K : CODEC;  // activation layout (Q4_K / Q6_K alike)
     static_assert(PL <= 63, "vmcnt counts at most 63 loads");
+    constexpr int kTmax = tiles_per_round(MR);
+    constexpr int LR = 4 * MR;  // lanes of a partial tile that hold live rows (MFMA row 4g + e in lane 16g + n)
+    constexpr int kCopyUnroll = CODEC == KQ_MIX ? 1 : PL;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const KArgs A = (KArgs)__builtin_amdgcn_kernarg_segment_ptr();
     const Iq2Tables &iq2_tab = *IqTables<CODEC>::get();
@@ -471,15 +478,16 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
     const int S = A->split, q = B0 % S, Gs = G / S, T0 = B0 / S;
     const int my_tiles = (A->total_tiles - T0 + Gs - 1) / Gs;
     const uint32_t ring_lds = (uint32_t)(uintptr_t)(LDSP(void))smem;
-    floatx4 *red = (floatx4 *)(smem + R * SLOTB);  // [kTmax][C][32 lanes]
+    floatx4 *red = (floatx4 *)(smem + R * SLOTB);  // [kTmax][C][LR lanes]
 
     if (wave < kProducers) {
-        // ================= producer: tiles into slots, up to R ahead
-        for (int round0 = 0; round0 < my_tiles; round0 += kTmax) {
-            const int nt = min(kTmax, my_tiles - round0);
-            // copy tile j of the round into slot j % R
+        // ================= producer: tiles into slots, up to R ahead.  The
+        // ring runs across rounds: the workgroup's tile j goes to slot j % R,
+        // and the next round's first tiles are in flight while the consumers
+        // sum a round's partial tiles.
+        {
             auto copy = [&](int j) {
-                const int tile = T0 + (round0 + j) * Gs;
+                const int tile = T0 + j * Gs;
                 int32_t begin;
                 const StreamProblem pr = problem_at(A, problem_of(A, tile), begin);
                 const uint32_t rb = pr.row_bytes;
@@ -491,39 +499,50 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
                 // the slice's first super-block in each row (offsets past the
                 // buffer stay past it: row bytes < 2^31)
                 const uint32_t kofs = (uint32_t)(q * NB) * (uint32_t)(q6 ? Geo<KQ_CODEC_Q6_K>::BPB : Geo<XC>::BPB);
-#pragma unroll
-                for (int i = 0; i < PL; ++i) {
-                    const int li = i * kProducers + wave;  // the producers' loads interleave
-                    const int ch = 64 * li + lane;  // slot chunk
-                    uint32_t off;
-                    if constexpr (CODEC == KQ_MIX)
-                        off = q6 ? slot_src<KQ_CODEC_Q6_K, NB>(ch, row0, last, rb)
-                                 : slot_src<KQ_CODEC_Q4_K, NB>(ch, row0, last, rb);
-                    else
-                        off = slot_src<CODEC, NB>(ch, row0, last, rb);
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDSP(void))(uintptr_t)(slot + 1024 * li), 16,
-                                                             off + kofs, 0, 0, 0);
+                // the producers' loads interleave: load i of this wave fills
+                // slot chunks 64 (i P + wave) .. +63.  The mixed launch keeps
+                // the loop rolled: unrolled, the offsets of all its loads are
+                // computed ahead and spill.
+                auto issue = [&](auto geo) {
+                    constexpr int GC = decltype(geo)::C;
+#pragma unroll kCopyUnroll
+                    for (int i = 0; i < PL; ++i) {
+                        const int li = i * kProducers + wave;
+                        const uint32_t off = slot_src<GC, NB>(64 * li + lane, row0, last, rb);
+                        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDSP(void))(uintptr_t)(slot + 1024 * li), 16,
+                                                                 off + kofs, 0, 0, 0);
+                    }
+                };
+                // a mixed launch branches once per tile (uniform), so only one
+                // geometry's offsets are live
+                if constexpr (CODEC == KQ_MIX) {
+                    if (q6) issue(SlotCodec<KQ_CODEC_Q6_K>{});
+                    else issue(SlotCodec<KQ_CODEC_Q4_K>{});
+                } else {
+                    issue(SlotCodec<CODEC>{});
                 }
             };
-            const int pre = min(R, nt);
+            const int pre = min(R, my_tiles);
             for (int j = 0; j < pre; ++j) {
                 copy(j);
                 // slot 1 onwards and the partial-tile area hold the consumers'
                 // activation rows until they are in registers (a start that
                 // also issued tiles 1 .. R-2 before them was slower: the
                 // first tile, which the consumers wait for, landed later)
-                if (round0 == 0 && j == 0) __builtin_amdgcn_s_barrier();
+                if (j == 0) __builtin_amdgcn_s_barrier();
             }
-            for (int b = 0; b < nt; ++b) {
+            for (int b = 0; b < my_tiles; ++b) {
                 // wait for tile b's loads; the tiles copied after it stay in flight
-                const int newer = min(b == 0 ? R - 1 : R - 2, nt - 1 - b);
+                const int newer = min(b == 0 ? R - 1 : R - 2, my_tiles - 1 - b);
                 wait_tiles_left<PL, (R - 1 < 63 / PL ? R - 1 : 63 / PL)>(newer);
                 __builtin_amdgcn_s_barrier();  // slot b % R to the consumers; slot (b - 1) % R back
-                if (b >= 1 && b + R - 1 < nt) copy(b + R - 1);
+                if (b >= 1 && b + R - 1 < my_tiles) copy(b + R - 1);
+                if ((b + 1) % kTmax == 0 || b + 1 == my_tiles) {
+                    __builtin_amdgcn_s_barrier();  // the round's partial tiles are in LDS
+                    if (b + 1 < my_tiles)
+                        __builtin_amdgcn_s_barrier();  // the round's outputs are summed: red is free
+                }
             }
-            __builtin_amdgcn_s_barrier();  // the consumers' partial tiles are in LDS
-            if (round0 + kTmax < my_tiles)
-                __builtin_amdgcn_s_barrier();  // the round's outputs are summed: red and the ring are free
         }
         return;
     }
@@ -545,35 +564,40 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
         // lanes past the segment read past the buffer (zeros, inside the row's LDS pitch)
         const uint32_t loff =
             16u * lane < 512u * SB ? (uint32_t)((q * NB + kb0) * KQ_QK * 2) + 16u * lane : 0x80000000u;
-#pragma unroll
-        for (int m = 0; m < kXRows; ++m)
-            if (m < M)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(xs, (LDSP(void))(uintptr_t)(xreg + m * kXRowLds), 16,
-                                                         loff + (uint32_t)(m * A->x_stride * 2), 0, 0, 0);
-        __builtin_amdgcn_s_waitcnt(KQ_VMCNT(0));
-        const bool live = r < M;
-        const uint32_t rowa = xreg + (uint32_t)(min(r, M - 1) * kXRowLds);
         const u32x4 zero = {0u, 0u, 0u, 0u};
+        // rows 8p .. 8p+7 in pass p (16 rows: two passes through the region);
+        // a lane keeps what it read in its row's pass, zeros for rows >= M
+        [[maybe_unused]] u32x4 ch[SB][8];
+#pragma unroll
+        for (int p = 0; p < MR / kXRows; ++p) {
+            if (p > 0) __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the region's reads are done
+#pragma unroll
+            for (int m = 0; m < kXRows; ++m)
+                if (kXRows * p + m < M)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                        xs, (LDSP(void))(uintptr_t)(xreg + m * kXRowLds), 16,
+                        loff + (uint32_t)((kXRows * p + m) * A->x_stride * 2), 0, 0, 0);
+            __builtin_amdgcn_s_waitcnt(KQ_VMCNT(0));
+            const bool mine = (r >> 3) == p && r < M;
+            const uint32_t rowa = xreg + (uint32_t)((r & 7) * kXRowLds);
+#pragma unroll
+            for (int s2 = 0; s2 < SB; ++s2)
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    if constexpr (CODEC == KQ_CODEC_Q4_K) {
+                        const u32x4 v = lds128(rowa + s2 * 512 + 64 * t + 16 * g);
+                        ch[s2][t] = mine ? v : (p == 0 ? zero : ch[s2][t]);
+                    } else {
+                        const u32x4 v = lds128(rowa + s2 * 512 + 2 * Block<XC>::x_elem(t, g));
+                        const u32x4 old = p == 0 ? zero : __builtin_bit_cast(u32x4, xr[s2][t]);
+                        xr[s2][t] = __builtin_bit_cast(half8_t, mine ? v : old);
+                    }
+                }
+        }
         if constexpr (CODEC == KQ_CODEC_Q4_K) {
-            u32x4 ch[SB][8];
-#pragma unroll
-            for (int s = 0; s < SB; ++s)
-#pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    const u32x4 v = lds128(rowa + s * 512 + 64 * t + 16 * g);
-                    ch[s][t] = live ? v : zero;
-                }
-            int xs;
-            q4own_x<SB>(xr, xm, xs, ch);
-            xm_scale = ldexpf(1.f, xs);
-        } else {
-#pragma unroll
-            for (int s = 0; s < SB; ++s)
-#pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    const u32x4 v = lds128(rowa + s * 512 + 2 * Block<XC>::x_elem(t, g));
-                    xr[s][t] = __builtin_bit_cast(half8_t, live ? v : zero);
-                }
+            int xs2;
+            q4own_x<SB>(xr, xm, xs2, ch);
+            xm_scale = ldexpf(1.f, xs2);
         }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // the x region reads are done
@@ -585,10 +609,11 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
     for (int round0 = 0; round0 < my_tiles; round0 += kTmax) {
         const int nt = min(kTmax, my_tiles - round0);
         for (int b = 0; b < nt; ++b) {
-            __builtin_amdgcn_s_barrier();  // tile b has landed in slot b % R
+            const int gb = round0 + b;  // the workgroup's tile count: slot gb % R
+            __builtin_amdgcn_s_barrier();  // tile gb has landed in its slot
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-            const int tile = T0 + (round0 + b) * Gs;
-            const uint32_t slot = ring_lds + (uint32_t)(b % R) * SLOTB;
+            const int tile = T0 + gb * Gs;
+            const uint32_t slot = ring_lds + (uint32_t)(gb % R) * SLOTB;
             floatx4 acc = {0, 0, 0, 0};
             if constexpr (CODEC == KQ_MIX) {
                 int32_t begin;
@@ -599,21 +624,22 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
                     mma_slab<KQ_CODEC_Q4_K, SB>(acc, slot + r * SlotGeo<KQ_CODEC_Q4_K, NB>::RC * 16 + kb0 * 144, xr, g,
                                                 iq2_tab);
             } else if constexpr (CODEC == KQ_CODEC_Q4_K) {
-                q4own_slab<SB>(acc, own_p + (b % R) * SLOTB, xr, xm, xm_scale, q4k, g);
+                q4own_slab<SB>(acc, own_p + (gb % R) * SLOTB, xr, xm, xm_scale, q4k, g);
             } else {
                 mma_slab<CODEC, SB>(acc, slot + r * SlotGeo<CODEC, NB>::RC * 16 + kb0 * Geo<CODEC>::SLOT, xr, g,
                                     iq2_tab);
             }
             kq_mfma_drain();
-            // batch rows 4g + e < 8 live in lanes g < 2
-            if (g < 2) red[(b * C + c) * 32 + lane] = acc;
+            // batch rows 4g + e < MR live in lanes g < MR / 4
+            if (g < MR / 4) red[(b * C + c) * LR + lane] = acc;
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // slot reads and red writes done
         }
         __builtin_amdgcn_s_barrier();  // every partial tile of the round is in LDS
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
         // ---- consumer c sums tiles b = c, c + C, ... of the round over the C
         // partial tiles in consumer order (deterministic).  Lane l holds
-        // outputs o = l and 64 + l of the tile: row m = o >> 4, column l & 15.
+        // outputs o = 64 h + l (h < MR / 4) of the tile: row m = o >> 4,
+        // column l & 15.
         const int n = lane & 15, mq = lane >> 4;
         auto store = [&](int tile, int m, float sum) {
             if (m >= M) return;
@@ -626,15 +652,15 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
         for (int b = c; b < nt; b += C) {
             const int tile = T0 + (round0 + b) * Gs;
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
+            for (int h = 0; h < MR / 4; ++h) {
                 const int ln = 16 * h + n;
-                float sum = red[(b * C) * 32 + ln][mq];
+                float sum = red[(b * C) * LR + ln][mq];
 #pragma unroll
-                for (int c2 = 1; c2 < C; ++c2) sum += red[(b * C + c2) * 32 + ln][mq];
+                for (int c2 = 1; c2 < C; ++c2) sum += red[(b * C + c2) * LR + ln][mq];
                 if (S == 1) store(tile, 4 * h + mq, sum);
                 else if (4 * h + mq < M)
-                    __hip_atomic_store(A->part + ((size_t)tile * S + q) * 128 + 64 * h + lane, sum, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(A->part + ((size_t)tile * S + q) * (16 * MR) + 64 * h + lane, sum,
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
         if (S > 1) {
@@ -665,15 +691,15 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
                     const int i = __builtin_ctzll(mine);
                     mine &= mine - 1;
                     const int tile = T0 + (round0 + c + i * C) * Gs;
-                    const float *pp = A->part + (size_t)tile * S * 128;
+                    const float *pp = A->part + (size_t)tile * S * (16 * MR);
 #pragma unroll
-                    for (int h = 0; h < 2; ++h) {
+                    for (int h = 0; h < MR / 4; ++h) {
                         const int o = 64 * h + lane;
                         if (4 * h + mq >= M) continue;
                         float v[kMaxSplit];
 #pragma unroll
                         for (int s2 = 0; s2 < kMaxSplit; ++s2)
-                            v[s2] = s2 < S ? __hip_atomic_load(pp + s2 * 128 + o, __ATOMIC_RELAXED,
+                            v[s2] = s2 < S ? __hip_atomic_load(pp + s2 * (16 * MR) + o, __ATOMIC_RELAXED,
                                                                __HIP_MEMORY_SCOPE_AGENT)
                                            : 0.f;
                         float sum = v[0];
@@ -687,19 +713,19 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
         }
         if (round0 + kTmax < my_tiles) {
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-            __builtin_amdgcn_s_barrier();  // red and the ring are free for the next round
+            __builtin_amdgcn_s_barrier();  // red is free for the next round
         }
     }
 }
 
-template <int CODEC, int SB, int C>
+template <int CODEC, int SB, int C, int MR>
 int launch(const StreamArgs &a, int grid, hipStream_t s) {
     constexpr int NB = SB * C;
     constexpr int SC = SlotCodec<CODEC>::C;
     // as many tile slots as fit beside the partial tiles, 2 to 6: the bytes a
     // CU keeps in flight set its share of the bandwidth, so small slots (K
     // slices, short K) take deeper rings
-    constexpr size_t red = (size_t)kTmax * C * 32 * 16;
+    constexpr size_t red = (size_t)tiles_per_round(MR) * C * (4 * MR) * 16;
     constexpr size_t budget = 150 * 1024 - (CODEC == KQ_CODEC_IQ2_XXS ? sizeof(Iq2Tables) : 0);
     // the activation rows are staged from slot 1 on
     constexpr size_t sb = slot_bytes<SC, NB>();
@@ -714,12 +740,12 @@ int launch(const StreamArgs &a, int grid, hipStream_t s) {
     static_assert(lds <= budget, "stream kernel LDS");
     static bool raised = false;
     if (!raised) {
-        if (hipFuncSetAttribute((const void *)kq_stream_kernel<CODEC, SB, C, R>,
+        if (hipFuncSetAttribute((const void *)kq_stream_kernel<CODEC, SB, C, R, MR>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
             return KQ_ERR_LAUNCH_FAILED;
         raised = true;
     }
-    hipLaunchKernelGGL((kq_stream_kernel<CODEC, SB, C, R>), dim3(grid), dim3(64 * (kProducers + C)), lds, s, a);
+    hipLaunchKernelGGL((kq_stream_kernel<CODEC, SB, C, R, MR>), dim3(grid), dim3(64 * (kProducers + C)), lds, s, a);
     return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
 }
 
@@ -729,22 +755,27 @@ int launch(const StreamArgs &a, int grid, hipStream_t s) {
 // 4 of two by 1-2 us on the 8-block slices of a split down projection,
 // measured); 16 blocks take 8 consumers of two.  The mixed Q4_K + Q6_K form
 // keeps two super-blocks per consumer where one would spill.
-template <int CODEC>
+template <int CODEC, int MR>
 int launch_codec(const StreamArgs &a, int nb, int grid, hipStream_t s) {
     constexpr bool mix = CODEC == KQ_MIX;
     switch (nb) {
-    case 2: return launch<CODEC, 1, 2>(a, grid, s);
-    case 4: return launch<CODEC, 1, 4>(a, grid, s);
-    case 6: return launch<CODEC, 1, 6>(a, grid, s);
+    case 2: return launch<CODEC, 1, 2, MR>(a, grid, s);
+    case 4: return launch<CODEC, 1, 4, MR>(a, grid, s);
+    case 6: return launch<CODEC, 1, 6, MR>(a, grid, s);
     case 8:
-        if constexpr (mix) return launch<CODEC, 2, 4>(a, grid, s);
-        else return launch<CODEC, 1, 8>(a, grid, s);
+        if constexpr (mix) return launch<CODEC, 2, 4, MR>(a, grid, s);
+        else return launch<CODEC, 1, 8, MR>(a, grid, s);
     case 12:
-        if constexpr (mix) return launch<CODEC, 2, 6>(a, grid, s);
-        else return launch<CODEC, 1, 12>(a, grid, s);
-    case 16: return launch<CODEC, 2, 8>(a, grid, s);
+        if constexpr (mix) return launch<CODEC, 2, 6, MR>(a, grid, s);
+        else return launch<CODEC, 1, 12, MR>(a, grid, s);
+    case 16: return launch<CODEC, 2, 8, MR>(a, grid, s);
     default: return KQ_ERR_BAD_SHAPE;
     }
+}
+
+template <int CODEC>
+int launch_rows(const StreamArgs &a, int nb, int grid, hipStream_t s) {
+    return a.M <= 8 ? launch_codec<CODEC, 8>(a, nb, grid, s) : launch_codec<CODEC, 16>(a, nb, grid, s);
 }
 
 bool stream_k_ok(int K) {
@@ -766,7 +797,7 @@ int64_t group_tiles(const kq_matmul_problem *ps, int n) {
 // GMLX_KQ_SPLITK=s asks for s slices (tests and tuning; 1 turns splitting
 // off).
 int kq_stream_split_want(const kq_matmul_problem *ps, int n) {
-    if (n <= 0 || n > kStreamProblems || ps[0].M < 1 || ps[0].M > 8 || ps[0].K % KQ_QK) return 1;
+    if (n <= 0 || n > kStreamProblems || ps[0].M < 1 || ps[0].M > 16 || ps[0].K % KQ_QK) return 1;
     const int nb = ps[0].K / KQ_QK;
     if (group_tiles(ps, n) * 4 > (int64_t)KQ_MATMUL_COUNTER_BYTES) return 1;
     if (const char *e = getenv("GMLX_KQ_SPLITK")) {
@@ -779,14 +810,16 @@ int kq_stream_split_want(const kq_matmul_problem *ps, int n) {
     return 1;
 }
 
-// Bytes of partial tiles a split launch writes (after the counter region).
+// Bytes of partial tiles a split launch writes (after the counter region):
+// 16 columns of 8 or 16 rows (M <= 8 / 9..16) per tile and slice.
 size_t kq_stream_part_bytes(const kq_matmul_problem *ps, int n, int split) {
-    return split > 1 ? ((size_t)group_tiles(ps, n) * split * 512 + 255) & ~(size_t)255 : 0;
+    const size_t tile_bytes = ps[0].M <= 8 ? 512 : 1024;
+    return split > 1 ? ((size_t)group_tiles(ps, n) * split * tile_bytes + 255) & ~(size_t)255 : 0;
 }
 
-// Eligibility (the dispatcher also requires fp16 activations): M <= 8, at
+// Eligibility (the dispatcher also requires fp16 activations): M <= 16, at
 // most 4 problems sharing x / stride / M / K, one codec or Q4_K with Q6_K,
-// K / split of 2, 4, 8 or 16 super-blocks, weights and x addressable with
+// K / split of 2, 4, 6, 8, 12 or 16 super-blocks, weights and x addressable with
 // 31-bit buffer offsets.  GMLX_KQ_STREAM=0 declines, =2 forces every eligible
 // launch here; GMLX_KQ_STREAM_WGS=n caps the grid at n workgroups (tests).
 bool kq_stream_eligible(const kq_matmul_problem *ps, int n, int split) {
@@ -794,7 +827,7 @@ bool kq_stream_eligible(const kq_matmul_problem *ps, int n, int split) {
     const char *env = getenv("GMLX_KQ_STREAM");
     if (env && env[0] == '0' && env[1] == 0) return false;
     const kq_matmul_problem &q0 = ps[0];
-    if (q0.M < 1 || q0.M > 8 || q0.K % (KQ_QK * split) || !stream_k_ok(q0.K / split)) return false;
+    if (q0.M < 1 || q0.M > 16 || q0.K % (KQ_QK * split) || !stream_k_ok(q0.K / split)) return false;
     bool mixed = false;
     for (int i = 0; i < n; ++i) {
         const kq_matmul_problem &q = ps[i];
@@ -815,9 +848,14 @@ bool kq_stream_eligible(const kq_matmul_problem *ps, int n, int split) {
     // path); at one or two per CU (o, q|k|v) the LDS-staged path is faster,
     // and a Q4_K + Q6_K group is slower here (its producers keep both slot
     // geometries live and spill).  GMLX_KQ_STREAM=2 takes every eligible
-    // launch (tests).
+    // launch (tests).  At 9..16 rows only split launches come here (the down
+    // projection: 21.6 / 23.4 us at 12 / 16 rows against 22.0 / 23.8 for the
+    // general kernel); whole-K gate|up stays on the LDS-staged path (19.2 /
+    // 19.9 us against 20.0 / 21.0: the 16-row form sums its partial tiles in
+    // two rounds).
     if (!(env && env[0] == '2' && env[1] == 0)) {
         if (mixed) return false;
+        if (q0.M > 8 && split == 1) return false;
         if (tiles * split < 4 * (int64_t)device_cus()) return false;
     }
     return true;
@@ -871,10 +909,10 @@ int kq_stream_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, i
     if (grid < split) grid = split;
     if (grid > tiles * split) grid = tiles * split;
     const int nb = q0.K / KQ_QK / split;
-    if (mixed) return launch_codec<KQ_MIX>(a, nb, grid, s);
+    if (mixed) return launch_rows<KQ_MIX>(a, nb, grid, s);
     switch (q0.codec) {
-    case KQ_CODEC_Q4_K: return launch_codec<KQ_CODEC_Q4_K>(a, nb, grid, s);
-    case KQ_CODEC_Q6_K: return launch_codec<KQ_CODEC_Q6_K>(a, nb, grid, s);
-    default: return launch_codec<KQ_CODEC_IQ2_XXS>(a, nb, grid, s);
+    case KQ_CODEC_Q4_K: return launch_rows<KQ_CODEC_Q4_K>(a, nb, grid, s);
+    case KQ_CODEC_Q6_K: return launch_rows<KQ_CODEC_Q6_K>(a, nb, grid, s);
+    default: return launch_rows<KQ_CODEC_IQ2_XXS>(a, nb, grid, s);
     }
 }

@@ -175,7 +175,7 @@ def test_module_forward():
 
 
 # The small-batch paths of kq_quantized_matmul_grouped, forced in turn: the
-# producer / consumer weight-streaming kernel (M <= 8, K of 2, 4, 6, 8, 12 or
+# producer / consumer weight-streaming kernel (M <= 16, K of 2, 4, 6, 8, 12 or
 # 16 super-blocks, or K cut into such slices: by default past 16 super-blocks,
 # GMLX_KQ_SPLITK=s slices where they divide K), the LDS-staged persistent
 # path (kq_mv), the register persistent path (kq_qmv) and the general tiled
@@ -221,6 +221,9 @@ PATH_KNOBS = ("GMLX_KQ_STREAM", "GMLX_KQ_STREAM_WGS", "GMLX_KQ_SPLITK", "GMLX_KQ
     ("q4_k", 333, 1536, 5),        # stream: 6 blocks, 6 consumers
     ("q6_k", 200, 3072, 8),        # stream: 12 blocks, 12 consumers
     ("iq2_xxs", 150, 1536, 3),
+    ("q4_k", 2000, 2048, 16),      # stream: 16 rows, two passes of activation staging
+    ("q6_k", 500, 4096, 12),
+    ("iq2_xxs", 300, 3072, 9),
 ])
 def test_small_batch_paths(codec, N, K, M, monkeypatch):
     """Every small-batch path matches the fp64 reference on the same inputs."""
@@ -247,9 +250,11 @@ def test_small_batch_paths(codec, N, K, M, monkeypatch):
     ("iq2_xxs", 300, 8192, 3, "float16"),   # 4 slices
     ("q4_k", 700, 7168, 6, "float16"),      # 28 blocks: 7 slices of 4
     ("q6_k", 300, 9216, 4, "bfloat16"),     # 36 blocks: 3 slices of 12
+    ("q6_k", 1000, 12288, 13, "float16"),   # 16-row partial tiles
+    ("q4_k", 260, 12288, 16, "float32"),
 ])
 def test_split_k_stream(codec, N, K, M, x_dtype, monkeypatch):
-    """K past 16 super-blocks at <= 8 rows: the K-sliced streaming launch
+    """K past 16 super-blocks at <= 16 rows: the K-sliced streaming launch
     matches the fp64 reference and the unsplit LDS-staged path, repeats
     bitwise, and leaves the workspace's arrival counters zero."""
     import torch
