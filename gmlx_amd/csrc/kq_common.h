@@ -62,6 +62,34 @@ __device__ __forceinline__ void kq_store_out(void *out, int dtype, int64_t i, fl
     }
 }
 
+__device__ __forceinline__ float kq_silu(float g) { return g / (1.0f + __expf(-g)); }
+
+// GLU of a gather epilogue for one output (fp32): g the gate row's product, u
+// the up row's; bias0 / bias1 the expert's bias at this column or 0.
+//   0 silu         silu(g) * u
+//   1 gelu         0.5 g (1 + tanh(0.79788456 (g + 0.044715 g^3)))  * u
+//   2 silu_limit   silu(min(g, limit)) * clamp(u, -limit, limit)
+//                  (gmlx/deepseek_v4_model.py:740-744)
+//   3 swiglu_clamp g' = min(g + bias0, limit), u' = clamp(u + bias1, -limit, limit):
+//                  (u' + 1) * g' * sigmoid(alpha g')   (gpt-oss clamped SwiGLU,
+//                  gmlx/minimax_m3_model.py:134-138)
+__device__ __forceinline__ float kq_glu(int act, float g, float u, float limit, float alpha, float bias0,
+                                        float bias1) {
+    switch (act) {
+    case KQ_ACT_SILU: return kq_silu(g) * u;
+    case KQ_ACT_GELU: {
+        const float k0 = 0.7978845608028654f, k1 = 0.044715f;
+        return 0.5f * g * (1.0f + tanhf(k0 * (g + k1 * g * g * g))) * u;
+    }
+    case KQ_ACT_SILU_LIMIT: return kq_silu(fminf(g, limit)) * fminf(fmaxf(u, -limit), limit);
+    default: {
+        g = fminf(g + bias0, limit);
+        u = fminf(fmaxf(u + bias1, -limit), limit);
+        return (u + 1.0f) * (g / (1.0f + __expf(-alpha * g)));
+    }
+    }
+}
+
 // Packed fp16 pair from two bytes already in [0, 63]: lanes hold 1024 + byte.
 // sel picks the two source bytes (0..3) for the low / high half.
 __device__ __forceinline__ uint32_t kq_bytes_to_h2_biased(uint32_t bytes, uint32_t sel) {

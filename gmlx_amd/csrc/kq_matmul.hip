@@ -27,6 +27,12 @@ size_t kq_stream_part_bytes(const kq_matmul_problem *ps, int n, int split);
 bool kq_stream_eligible(const kq_matmul_problem *ps, int n, int split);
 int kq_stream_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, int y_dtype, int split,
                      uint32_t *ctr, float *part, hipStream_t s);
+bool kq_sgather_eligible(int codec, bool glu, int32_t N, int32_t K, int64_t w_row_bytes, int32_t n_experts);
+int kq_sgather_launch(const void *x, const int32_t *x_exp, int64_t x_row_stride, int32_t x_pair_div, int32_t x_skip,
+                      const void *w0, const void *w1, int64_t w_expert_bytes, int64_t w_row_bytes, int32_t N,
+                      int32_t K, int codec, int act, float limit, float alpha, const float *b0, const float *b1,
+                      int64_t b_stride, const int32_t *seg_info, const int32_t *pair_order, int32_t n_pairs,
+                      int32_t n_experts, void *y, int y_dtype, int64_t y_row_stride, int32_t y_skip, hipStream_t s);
 // kq_qmv.hip: persistent small-batch launch (problems validated, all live,
 // sharing codec / x / M <= 16 / K <= 8192).
 int kq_qmv_persistent_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, int y_dtype, hipStream_t s);
@@ -176,38 +182,17 @@ __device__ __forceinline__ int64_t gather_y_row(const GatherArgs &a, int pair) {
     return pair + (a.y_skip ? pair / a.y_skip : 0);
 }
 
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
-
 // Output of pair rows for weight row n of `expert`: acc[0] (gate, or the
-// plain product) and acc[1] (up) in fp32.
-//   plain          v = g (+ b0[n])
-//   0 silu         silu(g) * u
-//   1 gelu         0.5 g (1 + tanh(0.79788456 (g + 0.044715 g^3)))  * u
-//   2 silu_limit   silu(min(g, limit)) * clamp(u, -limit, limit)
-//                  (gmlx/deepseek_v4_model.py:740-744)
-//   3 swiglu_clamp g' = min(g + b0[n], limit), u' = clamp(u + b1[n], -limit, limit):
-//                  (u' + 1) * g' * sigmoid(alpha g')   (gpt-oss clamped SwiGLU,
-//                  gmlx/minimax_m3_model.py:134-138)
+// plain product) and acc[1] (up) in fp32: plain v = g (+ b0[n]); the GLU
+// forms are kq_glu (kq_common.h).
 template <int NW>
 __device__ __forceinline__ float gather_epilogue(const GatherArgs &a, int expert, int n, float g, float u) {
+    const int64_t bo = (int64_t)expert * a.b_stride + n;
     if constexpr (NW == 1) {
-        return a.b0 ? g + a.b0[(int64_t)expert * a.b_stride + n] : g;
+        return a.b0 ? g + a.b0[bo] : g;
     } else {
-        switch (a.act) {
-        case KQ_ACT_SILU: return silu(g) * u;
-        case KQ_ACT_GELU: {
-            const float k0 = 0.7978845608028654f, k1 = 0.044715f;
-            return 0.5f * g * (1.0f + tanhf(k0 * (g + k1 * g * g * g))) * u;
-        }
-        case KQ_ACT_SILU_LIMIT: return silu(fminf(g, a.limit)) * fminf(fmaxf(u, -a.limit), a.limit);
-        default: {
-            if (a.b0) g += a.b0[(int64_t)expert * a.b_stride + n];
-            if (a.b1) u += a.b1[(int64_t)expert * a.b_stride + n];
-            g = fminf(g, a.limit);
-            u = fminf(fmaxf(u, -a.limit), a.limit);
-            return (u + 1.0f) * (g / (1.0f + __expf(-a.alpha * g)));
-        }
-        }
+        const bool clamp = a.act == KQ_ACT_SWIGLU_CLAMP;
+        return kq_glu(a.act, g, u, a.limit, a.alpha, clamp && a.b0 ? a.b0[bo] : 0.f, clamp && a.b1 ? a.b1[bo] : 0.f);
     }
 }
 
@@ -864,6 +849,13 @@ int gather_common(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pa
         x_row_stride = K;
         x_dtype = KQ_DTYPE_F16;
     }
+    // the streaming gather: weight tiles by row-contiguous direct-to-LDS
+    // copies, one persistent workgroup per CU
+    if (kq_sgather_eligible(codec, w1 != nullptr, N, K, w_row_bytes, n_experts))
+        return kq_sgather_launch(x, x_exp, x_row_stride, x_pair_div, x_skip, w0, w1, w_expert_bytes, w_row_bytes, N,
+                                 K, codec, w1 ? ep->act : KQ_ACT_SILU, ep->limit, ep->alpha, ep->bias0,
+                                 w1 ? ep->bias1 : nullptr, ep->bias_expert_stride, seg_info, pair_order, n_pairs,
+                                 n_experts, y, y_dtype, y_row_stride, y_skip, s);
     GatherArgs a;
     a.x = (const char *)x;
     a.x_exp = x_exp;

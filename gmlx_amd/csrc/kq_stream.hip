@@ -35,6 +35,8 @@
 // layer) runs in one launch with Q6_K-sized slots.
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "kq_mma.h"
 
 int device_cus();
@@ -783,6 +785,417 @@ bool stream_k_ok(int K) {
     return nb == 2 || nb == 4 || nb == 6 || nb == 8 || nb == 12 || nb == 16;
 }
 
+// ---- Streaming expert gather ------------------------------------------------
+// The MoE expert matmuls (kq_gather_qmm, kq_moe_glu_gather, kq_moe_gather_rows)
+// on the same producer / consumer ring: a work item is one 16-row weight tile
+// of one matrix (gate, up, or the plain one) of one expert, against one chunk
+// of at most 16 of the expert's routed rows (a segment of the route's
+// seg_info / pair_order, cut into chunks of 16).  Items are ordered chunk,
+// tile, matrix (gate before up), and each workgroup takes a contiguous range
+// of (chunk, tile) pairs, so it meets few chunk changes.  The consumers load
+// their activation fragments straight from the chunk's rows (fp16, gathered
+// through pair_order) when the chunk changes; the producers stream each
+// item's tile into the ring from its expert's matrix.  A round's partial
+// tiles are summed in consumer order and the epilogue (plain bias, or the GLU
+// of gate and up) writes the pairs' output rows.
+struct SGatherArgs {
+    const uint8_t *w0, *w1;            // expert stacks: gate (or the plain matrix), up
+    const char *x;                     // fp16 activation rows
+    const int32_t *x_exp;              // per-row exponents of prepared activations (results * 2^e), or null
+    void *y;
+    const int32_t *seg_info;           // [0] = S, seg_expert[E], seg_start[E + 1]
+    const int32_t *pair_order;         // pair ids by segment, then per pair its expert or -1
+    const float *b0, *b1;              // GLU biases, or the plain gather's output bias [expert][N], or null
+    int64_t x_stride, w_expert_bytes, y_stride, b_stride;
+    uint32_t w_row_bytes, w_bytes;     // one expert's matrix: N * row bytes (< 2^31)
+    int32_t x_pair_div, x_skip, y_skip, N, K, n_pairs, n_experts, n_tiles, y_dtype, act;
+    float limit, alpha;
+};
+
+typedef const __attribute__((address_space(4))) SGatherArgs *GArgs;
+
+constexpr int kSGatherMaxSegs = 1024;  // experts per launch (the router's bound)
+
+__device__ __forceinline__ int64_t sg_x_row(GArgs A, int pair) {
+    return pair / A->x_pair_div + (A->x_skip ? pair / A->x_skip : 0);
+}
+__device__ __forceinline__ int64_t sg_y_row(GArgs A, int pair) {
+    return pair + (A->y_skip ? pair / A->y_skip : 0);
+}
+
+constexpr int kSgRows = 8;  // activation rows per chunk (MFMA rows 0..7: lane groups 0, 1)
+
+// TM: items per round (a multiple of NW: a gate / up pair shares its round).
+// Items are small (16 rows of 3..28 super-blocks), so the ring is deep: the
+// bytes in flight per CU, not the item count, set its share of the bandwidth.
+// CPB: consumers per super-block (2: each takes four of its eight MFMA
+// steps, for short K, where one wave per super-block left the MFMA chains
+// latency-bound; not the owned Q4_K view, whose minimum term spans the block).
+template <int CODEC, int SB, int C, int R, int NW, int TM, int CPB>
+__global__ __launch_bounds__(64 * (kProducers + C)) void kq_sgather_kernel(SGatherArgs a_) {
+    static_assert(CPB == 1 || (CPB == 2 && SB == 1 && CODEC != KQ_CODEC_Q4_K), "split super-blocks: K-quant views");
+    constexpr int NB = SB * C / CPB;
+    constexpr int TS = 8 / CPB;  // MFMA steps per consumer and super-block
+    constexpr int PL = producer_loads<CODEC, NB>();
+    constexpr int SLOTB = slot_bytes<CODEC, NB>();
+    constexpr int kThreads = 64 * (kProducers + C);
+    static_assert(PL <= 63, "vmcnt counts at most 63 loads");
+    static_assert(TM % NW == 0, "rounds hold whole gate / up pairs");
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    // the route's segments in LDS: chunks before segment s, its first pair
+    // position, its expert (no global loads on the per-item paths)
+    __shared__ int32_t cstart[kSGatherMaxSegs + 1];
+    __shared__ int32_t sbeg[kSGatherMaxSegs + 1];
+    __shared__ int32_t sexp[kSGatherMaxSegs];
+    __shared__ int32_t wsum[16];
+    const GArgs A = (GArgs)__builtin_amdgcn_kernarg_segment_ptr();
+    const Iq2Tables &iq2_tab = *IqTables<CODEC>::get();
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = kq_lane(), r = lane & 15, g = lane >> 4;
+    const int S = A->seg_info[0];
+    const int32_t *sstart = A->seg_info + 1 + A->n_experts;
+    // ---- chunk table (segment s: ceil(len / 8) chunks), a workgroup scan
+    {
+        const int per = (S + kThreads - 1) / kThreads;
+        const int s0 = min(S, (int)threadIdx.x * per), s1 = min(S, s0 + per);
+        int v = 0;
+        for (int s = s0; s < s1; ++s) v += (sstart[s + 1] - sstart[s] + kSgRows - 1) / kSgRows;
+        int incl = v;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int y = __shfl_up(incl, d, 64);
+            if (lane >= d) incl += y;
+        }
+        if (lane == 63) wsum[wave] = incl;
+        __syncthreads();
+        int base = 0, total = 0;
+        for (int w2 = 0; w2 < kProducers + C; ++w2) {
+            base += w2 < wave ? wsum[w2] : 0;
+            total += wsum[w2];
+        }
+        int acc = base + incl - v;
+        for (int s = s0; s < s1; ++s) {
+            cstart[s] = acc;
+            sbeg[s] = sstart[s];
+            sexp[s] = A->seg_info[1 + s];
+            acc += (sstart[s + 1] - sstart[s] + kSgRows - 1) / kSgRows;
+        }
+        if (threadIdx.x == 0) {
+            cstart[S] = total;
+            sbeg[S] = sstart[S];
+        }
+        __syncthreads();
+    }
+    // (chunk, tile) pairs of this workgroup: [p0, p1); item j is pair p0 + j / NW, matrix j % NW
+    const int G = (int)gridDim.x;
+    const int pairs_total = cstart[S] * A->n_tiles;
+    const int per_wg = (pairs_total + G - 1) / G;
+    const int p0 = min(pairs_total, (int)blockIdx.x * per_wg), p1 = min(pairs_total, p0 + per_wg);
+    const int my_items = (p1 - p0) * NW;
+    const uint32_t ring_lds = (uint32_t)(uintptr_t)(LDSP(void))smem;
+    floatx4 *red = (floatx4 *)(smem + R * SLOTB);  // [TM][C][32 lanes]
+    auto chunk_of = [&](int j) { return (p0 + j / NW) / A->n_tiles; };
+    // segment of a chunk, advancing monotonically from the previous answer
+    auto seg_of = [&](int chunk, int &s) {
+        while (s + 1 < S && cstart[s + 1] <= chunk) ++s;
+        return s;
+    };
+    int s_start = 0;
+    {  // first segment by bisection
+        const int chunk0 = p0 / max(A->n_tiles, 1);
+        int lo = 0, hi = max(S - 1, 0);
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (cstart[mid] <= chunk0) lo = mid;
+            else hi = mid - 1;
+        }
+        s_start = lo;
+    }
+
+    if (wave < kProducers) {
+        // ================= producer: item tiles into slots
+        int ps = s_start;
+        auto copy = [&](int j) {
+            const int pt = p0 + j / NW;
+            const int chunk = pt / A->n_tiles, t = pt - chunk * A->n_tiles;
+            const int expert = sexp[seg_of(chunk, ps)];
+            const uint8_t *wm = (NW == 2 && j % NW) ? A->w1 : A->w0;
+            const __amdgpu_buffer_rsrc_t rs = kq_buffer(wm + (int64_t)expert * A->w_expert_bytes, A->w_bytes);
+            const uint32_t row0 = (uint32_t)t * 16, last = (uint32_t)A->N - 1, rb = A->w_row_bytes;
+            const uint32_t slot = ring_lds + (uint32_t)(j % R) * SLOTB;
+#pragma unroll
+            for (int i = 0; i < PL; ++i) {
+                const int li = i * kProducers + wave;
+                const uint32_t off = slot_src<CODEC, NB>(64 * li + lane, row0, last, rb);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDSP(void))(uintptr_t)(slot + 1024 * li), 16, off, 0,
+                                                         0, 0);
+            }
+        };
+        const int pre = min(R, my_items);
+        for (int j = 0; j < pre; ++j) copy(j);
+        for (int b = 0; b < my_items; ++b) {
+            const int newer = min(b == 0 ? R - 1 : R - 2, my_items - 1 - b);
+            wait_tiles_left<PL, (R - 1 < 63 / PL ? R - 1 : 63 / PL)>(newer);
+            __builtin_amdgcn_s_barrier();  // slot b % R to the consumers; slot (b - 1) % R back
+            if (b >= 1 && b + R - 1 < my_items) copy(b + R - 1);
+            if ((b + 1) % TM == 0 || b + 1 == my_items) {
+                __builtin_amdgcn_s_barrier();  // the round's partial tiles are in LDS
+                if (b + 1 < my_items) __builtin_amdgcn_s_barrier();  // the round's outputs are stored: red is free
+            }
+        }
+        return;
+    }
+
+    // ================= consumer c: K-slab [c SB, c SB + SB) of every item (or
+    // steps t0 .. t0 + TS - 1 of super-block c / CPB)
+    const int c = wave - kProducers;
+    const int kb0 = (c / CPB) * SB;
+    const int t0 = (c % CPB) * TS;
+    constexpr int XC = CODEC;
+    half8_t xr[SB][8];
+    [[maybe_unused]] half8_t xm;
+    [[maybe_unused]] float xm_scale = 1.f;
+    [[maybe_unused]] const Q4Consts q4k = q4own_consts(g);
+    [[maybe_unused]] LDSP(const uint8_t) own_p =
+        (LDSP(const uint8_t))smem + r * SlotGeo<KQ_CODEC_Q4_K, NB>::RC * 16 + kb0 * 144;
+    int cs = s_start, es = s_start;
+    int cur_chunk = -1;
+    // the chunk's activation fragments of this consumer's slab, from its rows
+    auto load_x = [&](int chunk) {
+        const int s = seg_of(chunk, cs);
+        const int seg_begin = sbeg[s], seg_len = sbeg[s + 1] - seg_begin;
+        const int row0 = (chunk - cstart[s]) * kSgRows;
+        const int rows = min(kSgRows, seg_len - row0);
+        const bool live = r < rows;
+        const int pair = A->pair_order[seg_begin + row0 + min(r, rows - 1)];
+        const char *xrow = A->x + sg_x_row(A, pair) * A->x_stride * 2;
+        const u32x4 zero = {0u, 0u, 0u, 0u};
+        if constexpr (CODEC == KQ_CODEC_Q4_K) {
+            u32x4 ch[SB][8];
+#pragma unroll
+            for (int s2 = 0; s2 < SB; ++s2)
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    const u32x4 v = *(const u32x4 *)(xrow + (256 * (kb0 + s2) + 32 * t + 8 * g) * 2);
+                    ch[s2][t] = live ? v : zero;
+                }
+            int xs2;
+            q4own_x<SB>(xr, xm, xs2, ch);
+            xm_scale = ldexpf(1.f, xs2);
+        } else {
+#pragma unroll
+            for (int s2 = 0; s2 < SB; ++s2)
+#pragma unroll
+                for (int i = 0; i < TS; ++i) {
+                    const int elem = 256 * (kb0 + s2) + Block<XC>::x_elem(t0 + i, g);
+                    const u32x4 v = *(const u32x4 *)(xrow + elem * 2);
+                    xr[s2][i] = __builtin_bit_cast(half8_t, live ? v : zero);
+                }
+        }
+    };
+    // steps T0 .. T0 + TS - 1 of the consumer's super-block (CPB 2)
+    auto half_slab = [&](floatx4 &acc, uint32_t row_lds, auto t0c) {
+        constexpr int T0 = decltype(t0c)::value;
+        Block<CODEC> blk;
+        load_slot<CODEC>(blk, row_lds, g);
+        blk.prep(g);
+#pragma unroll
+        for (int i = 0; i < TS; ++i)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xr[0][i], blk.frag(T0 + i, g, iq2_tab), acc, 0, 0, 0);
+    };
+    auto slab = [&](floatx4 &acc, int gb) {
+        const uint32_t slot = ring_lds + (uint32_t)(gb % R) * SLOTB;
+        const uint32_t row_lds = slot + r * SlotGeo<CODEC, NB>::RC * 16 + kb0 * Geo<CODEC>::SLOT;
+        if constexpr (CODEC == KQ_CODEC_Q4_K) {
+            q4own_slab<SB>(acc, own_p + (gb % R) * SLOTB, xr, xm, xm_scale, q4k, g);
+        } else if constexpr (CPB == 2) {
+            if (t0 == 0) half_slab(acc, row_lds, std::integral_constant<int, 0>{});  // uniform
+            else half_slab(acc, row_lds, std::integral_constant<int, 4>{});
+        } else {
+            mma_slab<CODEC, SB>(acc, row_lds, xr, g, iq2_tab);
+        }
+    };
+    const int n = lane & 15, mq = lane >> 4;
+    // the epilogue's view of a chunk: lane l stores rows 4h + (l >> 4), h < 2;
+    // their pairs and exponents are loaded once per chunk
+    int ep_chunk = -1, ep_expert = 0, ep_rows = 0;
+    int ep_pair[2], ep_ex[2];
+    auto ep_load = [&](int chunk) {
+        const int s = seg_of(chunk, es);
+        const int seg_begin = sbeg[s];
+        const int row0 = (chunk - cstart[s]) * kSgRows;
+        ep_rows = min(kSgRows, sbeg[s + 1] - seg_begin - row0);
+        ep_expert = sexp[s];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) ep_pair[h] = A->pair_order[seg_begin + row0 + min(4 * h + mq, ep_rows - 1)];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) ep_ex[h] = A->x_exp ? A->x_exp[sg_x_row(A, ep_pair[h])] : 0;
+        ep_chunk = chunk;
+    };
+    const float *redf = (const float *)red;
+    for (int round0 = 0; round0 < my_items; round0 += TM) {
+        const int nt = min(TM, my_items - round0);
+        for (int b = 0; b < nt; ++b) {
+            const int gb = round0 + b;
+            const int chunk = chunk_of(gb);
+            if (chunk != cur_chunk) {  // uniform; before the wait, so the loads overlap the tile's
+                load_x(chunk);
+                cur_chunk = chunk;
+            }
+            __builtin_amdgcn_s_barrier();  // item gb has landed in slot gb % R
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+            floatx4 acc = {0, 0, 0, 0};
+            slab(acc, gb);
+            kq_mfma_drain();
+            if (g < 2) red[(b * C + c) * 32 + lane] = acc;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // slot reads and red writes done
+        }
+        __builtin_amdgcn_s_barrier();  // every partial tile of the round is in LDS
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        // ---- the round's outputs: units (item pair qq, row group h < 2)
+        // spread over the consumers (a unit is 4 rows x 16 columns: one value
+        // per lane); the C partial tiles summed in consumer order, then the
+        // epilogue.  Spreading keeps each consumer's chain of LDS reads short.
+        for (int unit = c; unit < (nt / NW) * 2; unit += C) {
+            const int qq = unit >> 1, h = unit & 1;
+            const int b0 = qq * NW;
+            const int pt = p0 + (round0 + b0) / NW;
+            const int chunk = pt / A->n_tiles, t = pt - chunk * A->n_tiles;
+            if (chunk != ep_chunk) ep_load(chunk);  // uniform
+            const int nn = t * 16 + n;
+            const int m = 4 * h + mq;
+            float v[NW];
+#pragma unroll
+            for (int w2 = 0; w2 < NW; ++w2) {
+                // reads in groups of (at most) 8 in flight, summed in consumer order
+                constexpr int GR = C > 8 ? 4 : C;
+                float sum = 0.f;
+#pragma unroll
+                for (int c0 = 0; c0 < C; c0 += GR) {
+                    float pv[GR];
+#pragma unroll
+                    for (int i = 0; i < GR; ++i)
+                        pv[i] = c0 + i < C ? redf[(((b0 + w2) * C + c0 + i) * 32 + 16 * h + n) * 4 + mq] : 0.f;
+#pragma unroll
+                    for (int i = 0; i < GR; ++i)
+                        if (c0 + i < C) sum = (c0 + i == 0) ? pv[i] : sum + pv[i];
+                }
+                v[w2] = sum;
+            }
+            if (m >= ep_rows || nn >= A->N) continue;
+            const int pair = h ? ep_pair[1] : ep_pair[0];
+            const int ex = h ? ep_ex[1] : ep_ex[0];
+            const int64_t bo = (int64_t)ep_expert * A->b_stride + nn;
+            float out;
+            if constexpr (NW == 1) {
+                out = ldexpf(v[0], ex);
+                if (A->b0) out += A->b0[bo];
+            } else {
+                const bool clamp = A->act == KQ_ACT_SWIGLU_CLAMP;
+                out = kq_glu(A->act, ldexpf(v[0], ex), ldexpf(v[NW - 1], ex), A->limit, A->alpha,
+                             clamp && A->b0 ? A->b0[bo] : 0.f, clamp && A->b1 ? A->b1[bo] : 0.f);
+            }
+            kq_store_out(A->y, A->y_dtype, sg_y_row(A, pair) * A->y_stride + nn, out);
+        }
+        if (round0 + TM < my_items) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            __builtin_amdgcn_s_barrier();  // red is free for the next round
+        }
+    }
+    // pairs whose expert id is out of range (never routed): zeros in their
+    // rows, columns of tiles blockIdx.x, blockIdx.x + G, ...
+    if (c == 0) {
+        const int32_t *flag = A->pair_order + A->n_pairs;
+        for (int t = blockIdx.x; t < A->n_tiles; t += G) {
+            const int nn = t * 16 + n;
+            if (nn >= A->N) continue;
+            for (int p = mq; p < A->n_pairs; p += 4)
+                if (flag[p] < 0) kq_store_out(A->y, A->y_dtype, sg_y_row(A, p) * A->y_stride + nn, 0.f);
+        }
+    }
+}
+
+// Items per round: 8 (a multiple of NW) down to 2, the first whose partial
+// tiles leave room for a ring of four slots (three at 2); 0: no fit.  The
+// ring takes the rest of the LDS, up to 16 slots.  Each round ends in a
+// workgroup-wide epilogue (about 0.8 us), so rounds are as long as fits.
+constexpr int sgather_tm(size_t sb, size_t budget, int C) {
+    for (int tm = 8; tm >= 2; tm -= 2)
+        if ((tm == 2 ? 3 : 4) * sb + (size_t)tm * C * 32 * 16 <= budget) return tm;
+    return 0;
+}
+constexpr int sgather_ring(size_t sb, size_t red, size_t budget) {
+    for (int r = 16; r >= 3; --r)
+        if (r * sb + red <= budget) return r;
+    return 0;
+}
+
+// dry: only report whether this form fits (KQ_OK) or not (KQ_ERR_BAD_SHAPE).
+template <int CODEC, int SB, int C, int NW, int CPB = 1>
+int launch_sgather(const SGatherArgs &a, hipStream_t s, bool dry) {
+    constexpr int NB = SB * C / CPB;
+    constexpr size_t sb = slot_bytes<CODEC, NB>();
+    constexpr size_t budget = 150 * 1024 - (CODEC == KQ_CODEC_IQ2_XXS ? sizeof(Iq2Tables) : 0) -
+                              (3 * kSGatherMaxSegs + 2 + 16) * 4;
+    constexpr int TM = sgather_tm(sb, budget, C);
+    if constexpr (TM == 0) {
+        return KQ_ERR_BAD_SHAPE;
+    } else {
+        constexpr size_t red = (size_t)TM * C * 32 * 16;
+        constexpr int R = sgather_ring(sb, red, budget);
+        constexpr size_t lds = R * sb + red;
+        static_assert(R >= 3 && lds <= budget, "stream gather LDS");
+        if (dry) return KQ_OK;
+        static bool raised = false;
+        if (!raised) {
+            if (hipFuncSetAttribute((const void *)kq_sgather_kernel<CODEC, SB, C, R, NW, TM, CPB>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+                return KQ_ERR_LAUNCH_FAILED;
+            raised = true;
+        }
+        hipLaunchKernelGGL((kq_sgather_kernel<CODEC, SB, C, R, NW, TM, CPB>), dim3(device_cus()),
+                           dim3(64 * (kProducers + C)), lds, s, a);
+        return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
+    }
+}
+
+// Consumers for K = 256 nb: one super-block each up to 12; two for 16 and 28,
+// IQ2_XXS only (the K-quant views of two super-blocks, with their activation
+// reload inside the loop, run out of registers; those calls keep the
+// per-tile gather kernels).
+template <int CODEC, int NW>
+int sgather_codec(const SGatherArgs &a, int nb, hipStream_t s, bool dry) {
+    // up to 4 super-blocks, two consumers share each (Q6_K, IQ2_XXS)
+    constexpr int CPB = CODEC == KQ_CODEC_Q4_K ? 1 : 2;
+    switch (nb) {
+    case 2: return launch_sgather<CODEC, 1, 2 * CPB, NW, CPB>(a, s, dry);
+    case 3: return launch_sgather<CODEC, 1, 3 * CPB, NW, CPB>(a, s, dry);
+    case 4: return launch_sgather<CODEC, 1, 4 * CPB, NW, CPB>(a, s, dry);
+    case 6: return launch_sgather<CODEC, 1, 6, NW>(a, s, dry);
+    case 8: return launch_sgather<CODEC, 1, 8, NW>(a, s, dry);
+    case 12: return launch_sgather<CODEC, 1, 12, NW>(a, s, dry);
+    case 16:
+        if constexpr (CODEC == KQ_CODEC_IQ2_XXS) return launch_sgather<CODEC, 2, 8, NW>(a, s, dry);
+        else return KQ_ERR_BAD_SHAPE;
+    case 28:
+        if constexpr (CODEC == KQ_CODEC_IQ2_XXS) return launch_sgather<CODEC, 2, 14, NW>(a, s, dry);
+        else return KQ_ERR_BAD_SHAPE;
+    default: return KQ_ERR_BAD_SHAPE;
+    }
+}
+
+int sgather_dispatch(const SGatherArgs &a, int codec, bool glu, int nb, hipStream_t s, bool dry) {
+    switch (codec) {
+    case KQ_CODEC_Q4_K:
+        return glu ? sgather_codec<KQ_CODEC_Q4_K, 2>(a, nb, s, dry) : sgather_codec<KQ_CODEC_Q4_K, 1>(a, nb, s, dry);
+    case KQ_CODEC_Q6_K:
+        return glu ? sgather_codec<KQ_CODEC_Q6_K, 2>(a, nb, s, dry) : sgather_codec<KQ_CODEC_Q6_K, 1>(a, nb, s, dry);
+    default:
+        return glu ? sgather_codec<KQ_CODEC_IQ2_XXS, 2>(a, nb, s, dry)
+                   : sgather_codec<KQ_CODEC_IQ2_XXS, 1>(a, nb, s, dry);
+    }
+}
+
 int64_t group_tiles(const kq_matmul_problem *ps, int n) {
     int64_t tiles = 0;
     for (int i = 0; i < n; ++i) tiles += (ps[i].N + 15) / 16;
@@ -915,4 +1328,62 @@ int kq_stream_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, i
     case KQ_CODEC_Q6_K: return launch_rows<KQ_CODEC_Q6_K>(a, nb, grid, s);
     default: return launch_rows<KQ_CODEC_IQ2_XXS>(a, nb, grid, s);
     }
+}
+
+// Streaming expert gather (see kq_sgather_kernel).  Forms: K of 2, 3, 4, 6, 8
+// or 12 super-blocks (16 and 28 for IQ2_XXS), at most 1024 experts, one
+// expert's matrix below 2^31 bytes.  Routing (measured at the C4 / C5
+// layers): the K-quant GLU gathers come here (C4 gate|up 61 us against 67
+// for the per-tile kernels); the per-pair down gathers (C4 67 against 65) and
+// the IQ2_XXS gathers (C5 256 / 116 against 165 / 88) stay on the per-tile
+// kernels.  GMLX_KQ_SGATHER=0 declines every call, =2 takes every form.
+bool kq_sgather_eligible(int codec, bool glu, int32_t N, int32_t K, int64_t w_row_bytes, int32_t n_experts) {
+    const char *env = getenv("GMLX_KQ_SGATHER");
+    if (env && env[0] == '0' && env[1] == 0) return false;
+    if (K % KQ_QK || K <= 0) return false;
+    if (codec != KQ_CODEC_Q4_K && codec != KQ_CODEC_Q6_K && codec != KQ_CODEC_IQ2_XXS) return false;
+    if (n_experts < 1 || n_experts > kSGatherMaxSegs) return false;
+    if ((int64_t)(N + 16) * w_row_bytes >= (int64_t)0x80000000LL) return false;
+    SGatherArgs none{};
+    if (sgather_dispatch(none, codec, glu, K / KQ_QK, nullptr, true) != KQ_OK) return false;
+    if (env && env[0] == '2' && env[1] == 0) return true;
+    return glu && codec != KQ_CODEC_IQ2_XXS;
+}
+
+// x: fp16 rows (16-byte aligned, x_row_stride a multiple of 8), x_exp their
+// exponents or null; the other arguments as for the per-tile gathers.
+int kq_sgather_launch(const void *x, const int32_t *x_exp, int64_t x_row_stride, int32_t x_pair_div, int32_t x_skip,
+                      const void *w0, const void *w1, int64_t w_expert_bytes, int64_t w_row_bytes, int32_t N,
+                      int32_t K, int codec, int act, float limit, float alpha, const float *b0, const float *b1,
+                      int64_t b_stride, const int32_t *seg_info, const int32_t *pair_order, int32_t n_pairs,
+                      int32_t n_experts, void *y, int y_dtype, int64_t y_row_stride, int32_t y_skip, hipStream_t s) {
+    SGatherArgs a;
+    a.w0 = (const uint8_t *)w0;
+    a.w1 = (const uint8_t *)w1;
+    a.x = (const char *)x;
+    a.x_exp = x_exp;
+    a.y = y;
+    a.seg_info = seg_info;
+    a.pair_order = pair_order;
+    a.b0 = b0;
+    a.b1 = b1;
+    a.x_stride = x_row_stride;
+    a.w_expert_bytes = w_expert_bytes;
+    a.y_stride = y_row_stride;
+    a.b_stride = b_stride;
+    a.w_row_bytes = (uint32_t)w_row_bytes;
+    a.w_bytes = (uint32_t)((int64_t)N * w_row_bytes);
+    a.x_pair_div = x_pair_div;
+    a.x_skip = x_skip;
+    a.y_skip = y_skip;
+    a.N = N;
+    a.K = K;
+    a.n_pairs = n_pairs;
+    a.n_experts = n_experts;
+    a.n_tiles = (N + 15) / 16;
+    a.y_dtype = y_dtype;
+    a.act = act;
+    a.limit = limit;
+    a.alpha = alpha;
+    return sgather_dispatch(a, codec, w1 != nullptr, K / KQ_QK, s, false);
 }

@@ -117,6 +117,50 @@ def test_moe_glu_then_down_then_mix(act):
     assert np.allclose(mixed.cpu().numpy(), manual, rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("gcodec,dcodec,D,I,E,T,k", [
+    ("q4_k", "q6_k", 2048, 768, 16, 32, 8),      # C4 shapes: GLU at K = 8 super-blocks, down at K = 3
+    ("q4_k", "q6_k", 1024, 256, 4, 40, 4),       # segments past 16 rows: 40 rows per expert, three chunks
+    ("iq2_xxs", "iq2_xxs", 7168, 256, 6, 8, 4),  # C5 gate|up K = 28 super-blocks, down K = 256
+    ("q6_k", "iq2_xxs", 3072, 512, 8, 5, 8),     # K = 12 super-blocks; every expert touched
+])
+def test_streaming_gather_matches_tile_gather(gcodec, dcodec, D, I, E, T, k, monkeypatch):
+    """The streaming gather (every form forced, GMLX_KQ_SGATHER=2) against
+    the per-tile gather kernels (=0) and the fp64 oracle: the GLU gather then
+    the per-pair down gather, with one never-routed pair (zeros)."""
+    from gmlx_amd import ops
+    rng = np.random.default_rng(D + I + E)
+    gw = _experts(rng, gcodec, E, I, D)
+    uw = _experts(rng, gcodec, E, I, D)
+    dw = _experts(rng, dcodec, E, D, I)
+    x = fp16_rows(rng, T, D)
+    idx = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    idx[-1, 0] = E + 3  # never routed
+    outs = {}
+    for mode in ("stream", "tile"):
+        monkeypatch.setenv("GMLX_KQ_SGATHER", "2" if mode == "stream" else "0")
+        h = ops.moe_glu_gather_kq(_dev(x), _dev(gw), _dev(uw), gcodec, _dev(idx))
+        y = ops.gather_qmv_kq(h, _dev(dw), dcodec, _dev(idx))
+        outs[mode] = (h.cpu().numpy(), y.float().cpu().numpy())
+    g_deq = okq.dequantize(gw, gcodec).astype(np.float64)
+    u_deq = okq.dequantize(uw, gcodec).astype(np.float64)
+    d_deq = okq.dequantize(dw, dcodec).astype(np.float64)
+    xf = x.astype(np.float64)
+    silu = lambda z: z / (1 + np.exp(-z))
+    href = np.zeros((T, k, I))
+    for t in range(T):
+        for s_ in range(k):
+            e = idx[t, s_]
+            if e < E:
+                href[t, s_] = silu(g_deq[e] @ xf[t]) * (u_deq[e] @ xf[t])
+    for mode, (h, y) in outs.items():
+        assert np.all(h[-1, 0] == 0) and np.all(y[-1, 0] == 0), mode
+        assert okq.max_rel(h, href) <= TOL, (mode, okq.max_rel(h, href))
+        yref = np.stack([[d_deq[idx[t, s_]] @ h[t, s_] if idx[t, s_] < E else np.zeros(D) for s_ in range(k)]
+                         for t in range(T)])
+        assert okq.max_rel(y, yref) <= TOL, (mode, okq.max_rel(y, yref))
+    assert okq.max_rel(outs["stream"][0], outs["tile"][0]) <= TOL
+
+
 def test_router_topk_matches_numpy():
     from gmlx_amd import ops
     rng = np.random.default_rng(4)
@@ -284,12 +328,19 @@ def test_glu_limit_acts_and_biases(act, limit):
     G = okq.dequantize(gw, "q4_k").astype(np.float64)
     U = okq.dequantize(uw, "q4_k").astype(np.float64)
     xf = x.astype(np.float64)
-    href = np.stack([[omoe.glu(G[e] @ xf[t], U[e] @ xf[t], act, limit=limit, alpha=1.702,
-                               gate_bias=None if gb is None else gb[e], up_bias=None if ub is None else ub[e])
-                      for e in idx[t]] for t in range(T)])
-    assert okq.max_rel(h.cpu().numpy(), href) <= TOL
-    if limit < 1:  # the clamps were reached (the limit is small: max|ref| shrinks with it, while the
-        # products keep their fp16-weight rounding, so a tighter limit only inflates max-rel)
+    def ref(lim):
+        return np.stack([[omoe.glu(G[e] @ xf[t], U[e] @ xf[t], act, limit=lim, alpha=1.702,
+                                   gate_bias=None if gb is None else gb[e], up_bias=None if ub is None else ub[e])
+                          for e in idx[t]] for t in range(T)])
+
+    href = ref(limit)
+    # Max-rel against the unclamped GLU's magnitude: a small limit shrinks
+    # max|ref| while the gate / up products keep their fp16-weight rounding
+    # (normalised by max|ref| itself, 0.3 gives 2.3e-3 .. 4.2e-3 over seeds on
+    # either gather path); with a large limit the two scales coincide.
+    scale = np.max(np.abs(ref(np.inf)))
+    assert np.max(np.abs(h.cpu().numpy() - href)) / scale <= TOL
+    if limit < 1:  # the clamps were reached
         g_all = np.stack([[G[e] @ xf[t] for e in idx[t]] for t in range(T)])
         assert (np.abs(g_all) > limit).mean() > 0.05
     # down projection on a 256-wide h (whole Q6_K blocks) with an output bias
