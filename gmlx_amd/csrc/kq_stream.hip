@@ -789,8 +789,8 @@ bool stream_k_ok(int K) {
 // The MoE expert matmuls (kq_gather_qmm, kq_moe_glu_gather, kq_moe_gather_rows)
 // on the same producer / consumer ring: a work item is one 16-row weight tile
 // of one matrix (gate, up, or the plain one) of one expert, against one chunk
-// of at most 16 of the expert's routed rows (a segment of the route's
-// seg_info / pair_order, cut into chunks of 16).  Items are ordered chunk,
+// of at most kSgRows (8) of the expert's routed rows (a segment of the
+// route's seg_info / pair_order, cut into chunks of 8).  Items are ordered chunk,
 // tile, matrix (gate before up), and each workgroup takes a contiguous range
 // of (chunk, tile) pairs, so it meets few chunk changes.  The consumers load
 // their activation fragments straight from the chunk's rows (fp16, gathered
