@@ -48,9 +48,6 @@ using namespace kqmma;
 #define LDSP(T) __attribute__((address_space(3))) T *
 
 constexpr int KQ_MIX = 0x7F;  // Q4_K and Q6_K problems in one launch
-// x region: per consumer kXRows rows of up to 1 KB at a pitch of kXRowLds
-// bytes (the extra 16 staggers the rows over the LDS banks)
-constexpr int kXRows = 8, kXRowLds = 1040;
 constexpr int kProducers = 2;
 // MR activation rows per launch (8, or 16 for M = 9..16): tiles per
 // workgroup per round (the partial tiles of a round fill the same LDS)
@@ -194,6 +191,21 @@ __device__ __forceinline__ uint32_t slot_src(int q, uint32_t row0, uint32_t last
     return rr * row_bytes + (uint32_t)(blk * Geo<CODEC>::BPB + Geo<CODEC>::src(cb));
 }
 
+// 1 KB loads per slot row (its NB super-blocks of chunks, without the pad).
+template <int CODEC, int NB>
+constexpr int row_parts() {
+    return (NB * SlotGeo<CODEC, NB>::CPB + 63) / 64;
+}
+
+// Offset within a weight row of slot chunk w of the row (w < valid; others
+// past the buffer, which reads zeros with no memory request).
+template <int CODEC, int NB>
+__device__ __forceinline__ uint32_t row_chunk_src(int w, int valid) {
+    using SG = SlotGeo<CODEC, NB>;
+    const int blk = w / SG::CPB, cb = w - blk * SG::CPB;
+    return w < valid ? (uint32_t)(blk * Geo<CODEC>::BPB + Geo<CODEC>::src(cb)) : 0x80000000u;
+}
+
 // The slot geometry a launch allocates: its codec's, or Q6_K's for Q4_K + Q6_K.
 template <int CODEC>
 struct SlotCodec {
@@ -327,60 +339,47 @@ __device__ __forceinline__ half8_t q4own_frag(uint32_t w, const Q4Prep &p, const
 // xr[s][t] = x[e + (0, 2, 1, 3)], x[e + 32 + (0, 2, 1, 3)] with e = 256 (kb0 + s)
 // + 64 g + 4 t, and xm = the sub-block sums (2g, 2g+1 of each super-block) as
 // fp16 (hi, lo) pairs in the k slots the minimum MFMA pairs with -dm.
-// Input: the coalesced chunks C[s][t'] = x[256 (kb0 + s) + 32 t' + 8 g .. +7]
-// (the four lane groups of a row hold 64 consecutive bytes).  A 4 x 4
-// transpose of chunks between lane groups (t' = 2u + a: lane group g ends
-// with C[2g + a] of every source group w) follows, in two swap stages:
-// v_permlane32_swap exchanges bit 1 of u with bit 1 of g, v_permlane16_swap
-// bit 0 with bit 0.  Register 2w + a then holds x[64 g + 32 a + 8 w .. +7].
+// Input: the lane's runs c[s][2 w + a] = x[256 (kb0 + s) + 64 g + 32 a + 8 w .. +7].
+//
+// The sums come from MFMAs with the fragments as the B operand (column r =
+// batch row r) against a 0 / 1 selection A: row m = 4 g' + e of the result
+// selects sub-block 2 g' + (e & 1) of super-block e >> 1, so lane (g, r)
+// ends with sum[s][j] of its own row in element 2 s + j (exact products,
+// fp32 accumulation).
 //
 // The sums enter the MFMA as fp16 scaled by 2^-xs, xs >= 0 the same for the
 // whole wave: large enough that the wave's largest sum stays below 2^14
 // (32 activations near fp16's maximum sum past it), 0 for ordinary
 // magnitudes, so small sums keep their precision.
 template <int SB>
-__device__ __forceinline__ void q4own_x(half8_t (&xr)[SB][8], half8_t &xm, int &xs, u32x4 (&cin)[SB][8]) {
+__device__ __forceinline__ void q4own_x(half8_t (&xr)[SB][8], half8_t &xm, int &xs, const u32x4 (&cin)[SB][8],
+                                        int lane) {
     static_assert(SB <= 2, "the minimum MFMA holds two super-blocks of sums");
-    float sum[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+    const int g = lane >> 4, m = lane & 15;
+    floatx4 sum = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < SB; ++s) {
-        u32x4 (&c)[8] = cin[s];
-#pragma unroll
-        for (int a = 0; a < 2; ++a)
-#pragma unroll
-            for (int d = 0; d < 4; ++d) {
-#pragma unroll
-                for (int u0 = 0; u0 < 2; ++u0) {  // registers u = u0 and u0 + 2
-                    const auto r = __builtin_amdgcn_permlane32_swap(c[2 * u0 + a][d], c[2 * u0 + 4 + a][d], false,
-                                                                    false);
-                    c[2 * u0 + a][d] = r[0];
-                    c[2 * u0 + 4 + a][d] = r[1];
-                }
-#pragma unroll
-                for (int u1 = 0; u1 < 2; ++u1) {  // registers u = 2 u1 and 2 u1 + 1
-                    const auto r = __builtin_amdgcn_permlane16_swap(c[4 * u1 + a][d], c[4 * u1 + 2 + a][d], false,
-                                                                    false);
-                    c[4 * u1 + a][d] = r[0];
-                    c[4 * u1 + 2 + a][d] = r[1];
-                }
-            }
+        // selection of super-block s: element i of lane (g, m) is 1 where row
+        // m takes sub-block 2 g + (i >= 4) of super-block s
+        const bool mine = (m >> 2) == g && ((m >> 1) & 1) == s;
+        const _Float16 one = (_Float16)1.f, zero = (_Float16)0.f;
+        const _Float16 lo = mine && (m & 1) == 0 ? one : zero, hi = mine && (m & 1) == 1 ? one : zero;
+        const half8_t sel = {lo, lo, lo, lo, hi, hi, hi, hi};
+        const u32x4(&c)[8] = cin[s];
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-            const u32x4 &lo = c[2 * (t >> 1)], &hi = c[2 * (t >> 1) + 1];
+            const u32x4 &l = c[2 * (t >> 1)], &h = c[2 * (t >> 1) + 1];
             const int d = 2 * (t & 1);
-            const u32x4 v = {__builtin_amdgcn_perm(lo[d + 1], lo[d], 0x05040100u),
-                             __builtin_amdgcn_perm(lo[d + 1], lo[d], 0x07060302u),
-                             __builtin_amdgcn_perm(hi[d + 1], hi[d], 0x05040100u),
-                             __builtin_amdgcn_perm(hi[d + 1], hi[d], 0x07060302u)};
+            const u32x4 v = {__builtin_amdgcn_perm(l[d + 1], l[d], 0x05040100u),
+                             __builtin_amdgcn_perm(l[d + 1], l[d], 0x07060302u),
+                             __builtin_amdgcn_perm(h[d + 1], h[d], 0x05040100u),
+                             __builtin_amdgcn_perm(h[d + 1], h[d], 0x07060302u)};
             xr[s][t] = __builtin_bit_cast(half8_t, v);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                sum[s][0] += (float)xr[s][t][i];
-                sum[s][1] += (float)xr[s][t][4 + i];
-            }
+            sum = __builtin_amdgcn_mfma_f32_16x16x32_f16(sel, xr[s][t], sum, 0, 0, 0);
         }
     }
-    float mx = fmaxf(fmaxf(fabsf(sum[0][0]), fabsf(sum[0][1])), fmaxf(fabsf(sum[1][0]), fabsf(sum[1][1])));
+    kq_mfma_drain();
+    float mx = fmaxf(fmaxf(fabsf(sum[0]), fabsf(sum[1])), fmaxf(fabsf(sum[2]), fabsf(sum[3])));
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
     xs = 0;
@@ -389,17 +388,15 @@ __device__ __forceinline__ void q4own_x(half8_t (&xr)[SB][8], half8_t &xm, int &
         (void)frexpf(mx, &E);  // mx = f 2^E, f in [0.5, 1): mx 2^-(E-14) < 2^14
         xs = E - 14;
     }
-    _Float16 m[8];
+    _Float16 mm[8];
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const float v = ldexpf(sum[s][j], -xs);
-            const _Float16 hi = (_Float16)v;
-            m[4 * s + 2 * j] = s < SB ? hi : (_Float16)0.f;
-            m[4 * s + 2 * j + 1] = s < SB ? (_Float16)(v - (float)hi) : (_Float16)0.f;
-        }
-    xm = half8_t{m[0], m[1], m[2], m[3], m[4], m[5], m[6], m[7]};
+    for (int e = 0; e < 4; ++e) {
+        const float v = ldexpf(sum[e], -xs);
+        const _Float16 hi = (_Float16)v;
+        mm[2 * e] = (e >> 1) < SB ? hi : (_Float16)0.f;
+        mm[2 * e + 1] = (e >> 1) < SB ? (_Float16)(v - (float)hi) : (_Float16)0.f;
+    }
+    xm = half8_t{mm[0], mm[1], mm[2], mm[3], mm[4], mm[5], mm[6], mm[7]};
 }
 
 // One K-slab of a tile in the owned view: row_p points at the lane's row,
@@ -461,13 +458,19 @@ template <int CODEC, int SB, int C, int R, int MR>
 __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(StreamArgs a_) {
     constexpr int NB = SB * C;
     constexpr int SC = SlotCodec<CODEC>::C;
-    constexpr int PL = producer_loads<SC, NB>();  // loads per producer per tile
+    // Rows of at least 64 chunks load by rows (PR loads each); shorter ones
+    // by the slot's consecutive 1 KB runs with per-lane row offsets.
+    constexpr int kRowChunks = NB * SlotGeo<SC, NB>::CPB;
+    constexpr bool kByRows = kRowChunks >= 64;
+    constexpr int PR = row_parts<SC, NB>();  // loads per slot row
+    constexpr int PL = kByRows ? (16 / kProducers) * PR : producer_loads<SC, NB>();  // loads per producer per tile
+    // row pitch of a mixed launch's Q4_K tiles: the Q6_K slot's when loading by rows
+    constexpr int kMixQ4Pitch = (kByRows ? SlotGeo<SC, NB>::RC : SlotGeo<KQ_CODEC_Q4_K, NB>::RC) * 16;
     constexpr int SLOTB = slot_bytes<SC, NB>();
     constexpr int XC = CODEC == KQ_MIX ? KQ_CODEC_Q4_K : CODEC;  // activation layout (Q4_K / Q6_K alike)
     static_assert(PL <= 63, "vmcnt counts at most 63 loads");
     constexpr int kTmax = tiles_per_round(MR);
     constexpr int LR = 4 * MR;  // lanes of a partial tile that hold live rows (MFMA row 4g + e in lane 16g + n)
-    constexpr int kCopyUnroll = CODEC == KQ_MIX ? 1 : PL;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const KArgs A = (KArgs)__builtin_amdgcn_kernarg_segment_ptr();
     const Iq2Tables &iq2_tab = *IqTables<CODEC>::get();
@@ -488,7 +491,25 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
         // and the next round's first tiles are in flight while the consumers
         // sum a round's partial tiles.
         {
-            auto copy = [&](int j) {
+            // Rows of 64 chunks or more: one load per (row, 1 KB part of the
+            // row's slot chunks).  The row's offset goes in the load's scalar
+            // offset (rows past N clamped by scalar code) and the lane's
+            // offset within the row comes from a table of PR registers made
+            // once, so a load costs no VALU instruction (per-lane row offsets
+            // cost about ten, much of the launch's start).  The last part
+            // covers the row's last 64 chunks: where it overlaps the part
+            // before, both write the same bytes.  (The tables reach copy as
+            // arguments: captured by the lambda, the host pass dropped the
+            // kernel's instantiations.)
+            uint32_t tab[PR];     // the launch's slot geometry
+            uint32_t tab_q4[PR];  // Q4_K tiles in Q6_K-sized slots (mixed launch)
+#pragma unroll
+            for (int p = 0; p < PR; ++p) {
+                const int w = (p == PR - 1 ? kRowChunks - 64 : 64 * p) + lane;
+                tab[p] = kByRows ? row_chunk_src<SC, NB>(w, kRowChunks) : 0u;
+                tab_q4[p] = kByRows && CODEC == KQ_MIX ? row_chunk_src<KQ_CODEC_Q4_K, NB>(w, NB * 9) : 0u;
+            }
+            auto copy = [&](int j, const uint32_t *tb, const uint32_t *tb4) {
                 const int tile = T0 + j * Gs;
                 int32_t begin;
                 const StreamProblem pr = problem_at(A, problem_of(A, tile), begin);
@@ -498,47 +519,69 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
                 const __amdgpu_buffer_rsrc_t rs = kq_buffer(pr.w, pr.w_bytes);
                 const bool q6 = CODEC == KQ_MIX && pr.codec == KQ_CODEC_Q6_K;
                 const uint32_t slot = ring_lds + (uint32_t)(j % R) * SLOTB;
-                // the slice's first super-block in each row (offsets past the
-                // buffer stay past it: row bytes < 2^31)
+                // the slice's first super-block in each row
                 const uint32_t kofs = (uint32_t)(q * NB) * (uint32_t)(q6 ? Geo<KQ_CODEC_Q6_K>::BPB : Geo<XC>::BPB);
-                // the producers' loads interleave: load i of this wave fills
-                // slot chunks 64 (i P + wave) .. +63.  The mixed launch keeps
-                // the loop rolled: unrolled, the offsets of all its loads are
-                // computed ahead and spill.
-                auto issue = [&](auto geo) {
-                    constexpr int GC = decltype(geo)::C;
-#pragma unroll kCopyUnroll
-                    for (int i = 0; i < PL; ++i) {
-                        const int li = i * kProducers + wave;
-                        const uint32_t off = slot_src<GC, NB>(64 * li + lane, row0, last, rb);
-                        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDSP(void))(uintptr_t)(slot + 1024 * li), 16,
-                                                                 off + kofs, 0, 0, 0);
+                if constexpr (kByRows) {
+                    // producer w copies rows w, w + 2, ...
+                    auto issue = [&](const uint32_t *t) {
+#pragma unroll
+                        for (int i = 0; i < 16 / kProducers; ++i) {
+                            const int row = i * kProducers + wave;
+                            const uint32_t rr = min(row0 + (uint32_t)row, last);
+                            const int soff = (int)(rr * rb + kofs);
+                            const uint32_t m0 = slot + (uint32_t)(row * SlotGeo<SC, NB>::RC * 16);
+#pragma unroll
+                            for (int p2 = 0; p2 < PR; ++p2)
+                                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                                    rs, (LDSP(void))(uintptr_t)(m0 + 16 * (p2 == PR - 1 ? kRowChunks - 64 : 64 * p2)),
+                                    16, t[p2], soff, 0, 0);
+                        }
+                    };
+                    if constexpr (CODEC == KQ_MIX) {
+                        if (q6) issue(tb);
+                        else issue(tb4);
+                    } else {
+                        issue(tb);
                     }
-                };
-                // a mixed launch branches once per tile (uniform), so only one
-                // geometry's offsets are live
-                if constexpr (CODEC == KQ_MIX) {
-                    if (q6) issue(SlotCodec<KQ_CODEC_Q6_K>{});
-                    else issue(SlotCodec<KQ_CODEC_Q4_K>{});
                 } else {
-                    issue(SlotCodec<CODEC>{});
+                    // load i of this wave fills slot chunks 64 (i P + wave) .. +63
+                    auto issue = [&](auto geo) {
+                        constexpr int GC = decltype(geo)::C;
+#pragma unroll
+                        for (int i = 0; i < PL; ++i) {
+                            const int li = i * kProducers + wave;
+                            const uint32_t off = slot_src<GC, NB>(64 * li + lane, row0, last, rb);
+                            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDSP(void))(uintptr_t)(slot + 1024 * li),
+                                                                     16, off + kofs, 0, 0, 0);
+                        }
+                    };
+                    // a mixed launch branches once per tile (uniform), so only
+                    // one geometry's offsets are live
+                    if constexpr (CODEC == KQ_MIX) {
+                        if (q6) issue(SlotCodec<KQ_CODEC_Q6_K>{});
+                        else issue(SlotCodec<KQ_CODEC_Q4_K>{});
+                    } else {
+                        issue(SlotCodec<CODEC>{});
+                    }
                 }
             };
-            const int pre = min(R, my_tiles);
-            for (int j = 0; j < pre; ++j) {
-                copy(j);
-                // slot 1 onwards and the partial-tile area hold the consumers'
-                // activation rows until they are in registers (a start that
-                // also issued tiles 1 .. R-2 before them was slower: the
-                // first tile, which the consumers wait for, landed later)
-                if (j == 0) __builtin_amdgcn_s_barrier();
-            }
+            // The start is bound by the memory system, which every CU floods
+            // at once: the consumers' activation loads go first (they issue
+            // them before this barrier), then tile 0 alone; the rest of the
+            // ring follows once tile 0 is with the consumers (issued together,
+            // the ring's later tiles delayed tile 0 by about 2 us, measured).
+            __builtin_amdgcn_s_barrier();
+            copy(0, tab, tab_q4);
             for (int b = 0; b < my_tiles; ++b) {
                 // wait for tile b's loads; the tiles copied after it stay in flight
-                const int newer = min(b == 0 ? R - 1 : R - 2, my_tiles - 1 - b);
+                const int newer = b == 0 ? 0 : min(R - 2, my_tiles - 1 - b);
                 wait_tiles_left<PL, (R - 1 < 63 / PL ? R - 1 : 63 / PL)>(newer);
                 __builtin_amdgcn_s_barrier();  // slot b % R to the consumers; slot (b - 1) % R back
-                if (b >= 1 && b + R - 1 < my_tiles) copy(b + R - 1);
+                if (b == 0) {
+                    for (int j = 1; j < min(R, my_tiles); ++j) copy(j, tab, tab_q4);
+                } else if (b + R - 1 < my_tiles) {
+                    copy(b + R - 1, tab, tab_q4);
+                }
                 if ((b + 1) % kTmax == 0 || b + 1 == my_tiles) {
                     __builtin_amdgcn_s_barrier();  // the round's partial tiles are in LDS
                     if (b + 1 < my_tiles)
@@ -556,54 +599,42 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
     [[maybe_unused]] half8_t xm;
     [[maybe_unused]] float xm_scale = 1.f;  // 2^xs of the owned view's sub-block sums
     {
-        // The slab's activation rows arrive by coalesced direct-to-LDS loads
-        // (one row segment of SB * 512 bytes per instruction) in this
-        // consumer's part of the x region, then go into the MFMA fragments.
-        // Lanes of rows >= M take zeros.
+        // The slab's activation fragments straight from global memory into
+        // registers (no LDS, no barrier: the producers fill the whole ring
+        // from the start): lane (g, r) reads 16-byte runs of row r, rows >= M
+        // past the buffer (zeros).
         const uint32_t xbytes = (uint32_t)(((int64_t)(M - 1) * A->x_stride + A->K) * 2);
         const __amdgpu_buffer_rsrc_t xs = kq_buffer(A->x, xbytes);
-        const uint32_t xreg = ring_lds + SLOTB + (uint32_t)(c * kXRows * kXRowLds);
-        // lanes past the segment read past the buffer (zeros, inside the row's LDS pitch)
-        const uint32_t loff =
-            16u * lane < 512u * SB ? (uint32_t)((q * NB + kb0) * KQ_QK * 2) + 16u * lane : 0x80000000u;
-        const u32x4 zero = {0u, 0u, 0u, 0u};
-        // rows 8p .. 8p+7 in pass p (16 rows: two passes through the region);
-        // a lane keeps what it read in its row's pass, zeros for rows >= M
-        [[maybe_unused]] u32x4 ch[SB][8];
-#pragma unroll
-        for (int p = 0; p < MR / kXRows; ++p) {
-            if (p > 0) __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the region's reads are done
-#pragma unroll
-            for (int m = 0; m < kXRows; ++m)
-                if (kXRows * p + m < M)
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                        xs, (LDSP(void))(uintptr_t)(xreg + m * kXRowLds), 16,
-                        loff + (uint32_t)((kXRows * p + m) * A->x_stride * 2), 0, 0, 0);
-            __builtin_amdgcn_s_waitcnt(KQ_VMCNT(0));
-            const bool mine = (r >> 3) == p && r < M;
-            const uint32_t rowa = xreg + (uint32_t)((r & 7) * kXRowLds);
+        const uint32_t xrow =
+            r < M ? (uint32_t)((r * A->x_stride + (q * NB + kb0) * KQ_QK) * 2) : 0x80000000u;
+        if constexpr (CODEC == KQ_CODEC_Q4_K) {
+            // owned view: lane group g needs values 64 g .. 64 g + 63 of each
+            // super-block, as 16-byte runs c[2 w + a] = x[64 g + 32 a + 8 w .. +7]
+            u32x4 cin[SB][8];
 #pragma unroll
             for (int s2 = 0; s2 < SB; ++s2)
 #pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    if constexpr (CODEC == KQ_CODEC_Q4_K) {
-                        const u32x4 v = lds128(rowa + s2 * 512 + 64 * t + 16 * g);
-                        ch[s2][t] = mine ? v : (p == 0 ? zero : ch[s2][t]);
-                    } else {
-                        const u32x4 v = lds128(rowa + s2 * 512 + 2 * Block<XC>::x_elem(t, g));
-                        const u32x4 old = p == 0 ? zero : __builtin_bit_cast(u32x4, xr[s2][t]);
-                        xr[s2][t] = __builtin_bit_cast(half8_t, mine ? v : old);
-                    }
-                }
-        }
-        if constexpr (CODEC == KQ_CODEC_Q4_K) {
+                for (int w = 0; w < 4; ++w)
+#pragma unroll
+                    for (int a2 = 0; a2 < 2; ++a2)
+                        cin[s2][2 * w + a2] = __builtin_bit_cast(
+                            u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                       xs, xrow + (uint32_t)(2 * (256 * s2 + 64 * g + 32 * a2 + 8 * w)), 0, 0));
+            __builtin_amdgcn_s_barrier();  // the loads are issued: the producers may start
             int xs2;
-            q4own_x<SB>(xr, xm, xs2, ch);
+            q4own_x<SB>(xr, xm, xs2, cin, lane);
             xm_scale = ldexpf(1.f, xs2);
+        } else {
+#pragma unroll
+            for (int s2 = 0; s2 < SB; ++s2)
+#pragma unroll
+                for (int t = 0; t < 8; ++t)
+                    xr[s2][t] = __builtin_bit_cast(
+                        half8_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                     xs, xrow + (uint32_t)(2 * (256 * s2 + Block<XC>::x_elem(t, g))), 0, 0));
+            __builtin_amdgcn_s_barrier();  // the loads are issued: the producers may start
         }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // the x region reads are done
-    __builtin_amdgcn_s_barrier();                           // the producers may fill slot 1
     // owned Q4_K view: the lane's row at super-block kb0 in slot 0
     [[maybe_unused]] const Q4Consts q4k = q4own_consts(g);
     [[maybe_unused]] LDSP(const uint8_t) own_p =
@@ -623,7 +654,7 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
                     mma_slab<KQ_CODEC_Q6_K, SB>(acc, slot + r * SlotGeo<KQ_CODEC_Q6_K, NB>::RC * 16 + kb0 * 224, xr, g,
                                                 iq2_tab);
                 else
-                    mma_slab<KQ_CODEC_Q4_K, SB>(acc, slot + r * SlotGeo<KQ_CODEC_Q4_K, NB>::RC * 16 + kb0 * 144, xr, g,
+                    mma_slab<KQ_CODEC_Q4_K, SB>(acc, slot + r * kMixQ4Pitch + kb0 * 144, xr, g,
                                                 iq2_tab);
             } else if constexpr (CODEC == KQ_CODEC_Q4_K) {
                 q4own_slab<SB>(acc, own_p + (gb % R) * SLOTB, xr, xm, xm_scale, q4k, g);
@@ -729,10 +760,8 @@ int launch(const StreamArgs &a, int grid, hipStream_t s) {
     // slices, short K) take deeper rings
     constexpr size_t red = (size_t)tiles_per_round(MR) * C * (4 * MR) * 16;
     constexpr size_t budget = 150 * 1024 - (CODEC == KQ_CODEC_IQ2_XXS ? sizeof(Iq2Tables) : 0);
-    // the activation rows are staged from slot 1 on
     constexpr size_t sb = slot_bytes<SC, NB>();
-    constexpr size_t xregion = sb + (size_t)C * kXRows * kXRowLds;
-    constexpr auto need = [](size_t ring) { return ring + red > xregion ? ring + red : xregion; };
+    constexpr auto need = [](size_t ring) { return ring + red; };
     constexpr int R = need(6 * sb) <= budget   ? 6
                       : need(5 * sb) <= budget ? 5
                       : need(4 * sb) <= budget ? 4
@@ -975,12 +1004,15 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_sgather_kernel(SGath
 #pragma unroll
             for (int s2 = 0; s2 < SB; ++s2)
 #pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    const u32x4 v = *(const u32x4 *)(xrow + (256 * (kb0 + s2) + 32 * t + 8 * g) * 2);
-                    ch[s2][t] = live ? v : zero;
-                }
+                for (int w = 0; w < 4; ++w)
+#pragma unroll
+                    for (int a2 = 0; a2 < 2; ++a2) {
+                        const u32x4 v =
+                            *(const u32x4 *)(xrow + (256 * (kb0 + s2) + 64 * g + 32 * a2 + 8 * w) * 2);
+                        ch[s2][2 * w + a2] = live ? v : zero;
+                    }
             int xs2;
-            q4own_x<SB>(xr, xm, xs2, ch);
+            q4own_x<SB>(xr, xm, xs2, ch, lane);
             xm_scale = ldexpf(1.f, xs2);
         } else {
 #pragma unroll

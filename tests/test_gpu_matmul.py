@@ -284,6 +284,39 @@ def test_split_k_stream(codec, N, K, M, x_dtype, monkeypatch):
     assert okq.max_rel(got, unsplit) <= TOL
 
 
+@pytest.mark.parametrize("codec,K,M,env", [
+    ("q4_k", 4096, 8, {}),
+    ("q6_k", 2048, 5, {"GMLX_KQ_STREAM_WGS": "7"}),
+    ("q6_k", 12288, 8, {"GMLX_KQ_SPLITK": "6", "GMLX_KQ_STREAM_WGS": "12"}),
+    ("q4_k", 3072, 16, {"GMLX_KQ_STREAM_WGS": "5"}),
+])
+def test_stream_row_pitches_and_partial_tiles(codec, K, M, env, monkeypatch):
+    """The streaming kernel's producers keep per-lane chunk offsets of full
+    tiles for the first problem's row pitch: a group whose second problem has
+    wider rows (padding after each row's blocks) and whose first ends in a
+    partial tile takes the general offsets where those differ, and both match
+    the fp64 reference."""
+    import torch
+    from gmlx_amd import ops
+    for k in PATH_KNOBS:
+        monkeypatch.delenv(k, raising=False)
+    monkeypatch.setenv("GMLX_KQ_STREAM", "2")
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    rng = np.random.default_rng(K + M)
+    Na, Nb = 1000, 704
+    wa = quantized_weights(rng, codec, Na, K)
+    wb = quantized_weights(rng, codec, Nb, K)
+    x16 = fp16_rows(rng, M, K)
+    x = _dev(x16)
+    wide = torch.zeros(Nb, wb.shape[1] + 48, dtype=torch.uint8)
+    wide[:, :wb.shape[1]] = torch.from_numpy(wb)
+    wbv = wide.cuda()[:, :wb.shape[1]]
+    ya, yb = ops.quantized_matmul_grouped([(x, _dev(wa), codec), (x, wbv, codec)], out_dtype=torch.float32)
+    assert okq.max_rel(ya.cpu().numpy(), okq.qmm_ref(x16, wa, codec)) <= TOL
+    assert okq.max_rel(yb.cpu().numpy(), okq.qmm_ref(x16, wb, codec)) <= TOL
+
+
 @pytest.mark.parametrize("K,M", [(4096, 8), (8192, 3), (1280, 16), (2048, 1)])
 def test_mixed_codec_group_paths(K, M, monkeypatch):
     """q|k (Q4_K) with v (Q6_K) in one launch: the mixed LDS-staged kernel
