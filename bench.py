@@ -103,8 +103,8 @@ def make_inputs(torch, rng, B):
 # finish summing the six partial tiles; q|k|v (Q4_K and Q6_K tiles in one
 # launch) and o (at most two tiles per CU) take the LDS-staged persistent
 # kernel as two 8-wave workgroups per CU, one tile each.  At B = 9..16 down
-# takes the streaming kernel in its 16-row form and the other launches the
-# LDS-staged kernel; at B = 17..64 every launch
+# takes the streaming kernel in its 16-row form (four K slices of 12
+# super-blocks) and the other launches the LDS-staged kernel; at B = 17..64 every launch
 # takes the mid-batch kernel (one 4-wave workgroup per CU over groups of T
 # weight tiles: q|k|v mixed T = 2, o and down T = 1, gate|up T = 6 up to 32
 # rows, 3 above); past 64 rows the general kernel.
@@ -127,12 +127,13 @@ def kernel_of(launch, B):
                 "gate_up": f"kq_mm_kernel<0, {mt}, 0, {6 if mt == 2 else 3}>", "down": f"kq_mm_kernel<1, {mt}, 0, 1>"}[launch]
     if B <= 8 and launch == "gate_up":  # kq_stream_kernel<codec, blocks per consumer, consumers, slots, rows>
         return "kq_stream_kernel<12, 2, 8, 3, 8>"
-    if B <= 16 and launch == "down":  # K = 12288 in six slices of 8 super-blocks, one per consumer
-        return f"kq_stream_kernel<14, 1, 8, 3, {8 if B <= 8 else 16}>"
-    if launch == "qkv":  # Q4_K q|k with Q6_K v: the mixed form (codec id 127), 0.75 tiles per 8-wave workgroup
-        return "kq_mv_kernel<127, 0, 2, 1, false, 8>"
+    if B <= 16 and launch == "down":  # K = 12288 in slices, one super-block per consumer
+        # up to 8 rows: six slices of 8; 9..16 rows: four slices of 12 (two ring slots)
+        return "kq_stream_kernel<14, 1, 8, 3, 8>" if B <= 8 else "kq_stream_kernel<14, 1, 12, 2, 16>"
+    if launch == "qkv":  # Q4_K q|k with Q6_K v: the mixed form (codec id 127)
+        return "kq_mv_kernel<127, 0, 2, 1, false, 8>" if B <= 8 else "kq_mv_kernel<127, 0, 1, 2, false, 16>"
     if launch == "o":
-        return "kq_mv_kernel<12, 0, 2, 1, false, 8>"
+        return "kq_mv_kernel<12, 0, 2, 1, false, 8>" if B <= 8 else "kq_mv_kernel<12, 0, 1, 1, false, 16>"
     return "kq_mv_kernel<12, 0, 1, 3, false, 16>"  # gate|up at 9..16 rows
 
 

@@ -49,6 +49,9 @@ using namespace kqmma;
 
 constexpr int KQ_MIX = 0x7F;  // Q4_K and Q6_K problems in one launch
 constexpr int kProducers = 2;
+#ifndef KQ_STREAM_START_TILES
+#define KQ_STREAM_START_TILES 2
+#endif
 // MR activation rows per launch (8, or 16 for M = 9..16): tiles per
 // workgroup per round (the partial tiles of a round fill the same LDS)
 __host__ __device__ constexpr int tiles_per_round(int MR) { return MR == 8 ? 8 : 4; }
@@ -471,6 +474,7 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
     static_assert(PL <= 63, "vmcnt counts at most 63 loads");
     constexpr int kTmax = tiles_per_round(MR);
     constexpr int LR = 4 * MR;  // lanes of a partial tile that hold live rows (MFMA row 4g + e in lane 16g + n)
+    constexpr int kStartTiles = KQ_STREAM_START_TILES < R ? KQ_STREAM_START_TILES : R;  // tiles issued before the first hand-off
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const KArgs A = (KArgs)__builtin_amdgcn_kernarg_segment_ptr();
     const Iq2Tables &iq2_tab = *IqTables<CODEC>::get();
@@ -567,18 +571,20 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
             };
             // The start is bound by the memory system, which every CU floods
             // at once: the consumers' activation loads go first (they issue
-            // them before this barrier), then tile 0 alone; the rest of the
-            // ring follows once tile 0 is with the consumers (issued together,
-            // the ring's later tiles delayed tile 0 by about 2 us, measured).
+            // them before this barrier), then kStartTiles tiles; the rest of
+            // the ring follows once tile 0 is with the consumers (the whole
+            // ring issued together delayed tile 0 by about 2 us; two tiles
+            // beat one by 0.25 us at gate|up size, measured).
             __builtin_amdgcn_s_barrier();
-            copy(0, tab, tab_q4);
+            const int first = min(kStartTiles, my_tiles);
+            for (int j = 0; j < first; ++j) copy(j, tab, tab_q4);
             for (int b = 0; b < my_tiles; ++b) {
                 // wait for tile b's loads; the tiles copied after it stay in flight
-                const int newer = b == 0 ? 0 : min(R - 2, my_tiles - 1 - b);
+                const int newer = b == 0 ? first - 1 : min(R - 2, my_tiles - 1 - b);
                 wait_tiles_left<PL, (R - 1 < 63 / PL ? R - 1 : 63 / PL)>(newer);
                 __builtin_amdgcn_s_barrier();  // slot b % R to the consumers; slot (b - 1) % R back
                 if (b == 0) {
-                    for (int j = 1; j < min(R, my_tiles); ++j) copy(j, tab, tab_q4);
+                    for (int j = first; j < min(R, my_tiles); ++j) copy(j, tab, tab_q4);
                 } else if (b + R - 1 < my_tiles) {
                     copy(b + R - 1, tab, tab_q4);
                 }
@@ -639,8 +645,43 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
     [[maybe_unused]] const Q4Consts q4k = q4own_consts(g);
     [[maybe_unused]] LDSP(const uint8_t) own_p =
         (LDSP(const uint8_t))smem + r * SlotGeo<KQ_CODEC_Q4_K, NB>::RC * 16 + kb0 * 144;
+    // The epilogue's parameters are read ahead of the tiles: per-row exponents
+    // of prepared activations once, the output of the consumer's first tile of
+    // a round before the round (its kernel-argument loads, a chain of scalar
+    // loads, took about 1 us at the end of a launch, measured).
+    const int n = lane & 15, mq = lane >> 4;
+    const bool has_xe = A->x_exp != nullptr;
+    int xe[MR / 4];
+#pragma unroll
+    for (int h = 0; h < MR / 4; ++h) xe[h] = has_xe && 4 * h + mq < M ? A->x_exp[4 * h + mq] : 0;
+    // (arguments, not captures: a lambda capturing a local array dropped the
+    // kernel's host-side instantiations)
+    // kept in registers (the compiler would reload them at their use)
+    int ydt = A->y_dtype;
+    uint64_t part_b = (uint64_t)(uintptr_t)A->part, ctr_b = (uint64_t)(uintptr_t)A->ctr;
+    asm volatile("" : "+s"(ydt), "+s"(part_b), "+s"(ctr_b));
+    float *const part = (float *)(uintptr_t)part_b;
+    uint32_t *const ctr0 = (uint32_t *)(uintptr_t)ctr_b;
+    auto store = [&](const StreamProblem &pr, int32_t begin, int tile, int m, int e, float sum) {
+        if (m >= M) return;
+        if (has_xe) sum = ldexpf(sum, e);
+        const int nn = (tile - begin) * 16 + n;
+        if (nn < pr.N) kq_store_out(pr.y, ydt, (int64_t)m * pr.y_stride + nn, sum);
+    };
     for (int round0 = 0; round0 < my_tiles; round0 += kTmax) {
         const int nt = min(kTmax, my_tiles - round0);
+        const int etile = T0 + (round0 + c) * Gs;  // this consumer's first tile of the round (if c < nt)
+        int32_t ebegin = 0;
+        StreamProblem epr = problem_at(A, problem_of(A, c < nt ? etile : T0), ebegin);
+        {
+            // held in registers from here (left to itself, the compiler
+            // sinks these kernel-argument loads to their use at the store)
+            uint64_t yb = (uint64_t)(uintptr_t)epr.y;
+            int64_t ys = epr.y_stride;
+            asm volatile("" : "+s"(yb), "+s"(ys), "+s"(epr.N), "+s"(ebegin));
+            epr.y = (void *)(uintptr_t)yb;
+            epr.y_stride = ys;
+        }
         for (int b = 0; b < nt; ++b) {
             const int gb = round0 + b;  // the workgroup's tile count: slot gb % R
             __builtin_amdgcn_s_barrier();  // tile gb has landed in its slot
@@ -673,26 +714,19 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
         // partial tiles in consumer order (deterministic).  Lane l holds
         // outputs o = 64 h + l (h < MR / 4) of the tile: row m = o >> 4,
         // column l & 15.
-        const int n = lane & 15, mq = lane >> 4;
-        auto store = [&](int tile, int m, float sum) {
-            if (m >= M) return;
-            if (A->x_exp) sum = ldexpf(sum, A->x_exp[m]);
-            int32_t begin;
-            const StreamProblem pr = problem_at(A, problem_of(A, tile), begin);
-            const int nn = (tile - begin) * 16 + n;
-            if (nn < pr.N) kq_store_out(pr.y, A->y_dtype, (int64_t)m * pr.y_stride + nn, sum);
-        };
         for (int b = c; b < nt; b += C) {
             const int tile = T0 + (round0 + b) * Gs;
+            int32_t begin = ebegin;
+            const StreamProblem pr = b == c ? epr : problem_at(A, problem_of(A, tile), begin);
 #pragma unroll
             for (int h = 0; h < MR / 4; ++h) {
                 const int ln = 16 * h + n;
                 float sum = red[(b * C) * LR + ln][mq];
 #pragma unroll
                 for (int c2 = 1; c2 < C; ++c2) sum += red[(b * C + c2) * LR + ln][mq];
-                if (S == 1) store(tile, 4 * h + mq, sum);
+                if (S == 1) store(pr, begin, tile, 4 * h + mq, xe[h], sum);
                 else if (4 * h + mq < M)
-                    __hip_atomic_store(A->part + ((size_t)tile * S + q) * (16 * MR) + 64 * h + lane, sum,
+                    __hip_atomic_store(part + ((size_t)tile * S + q) * (16 * MR) + 64 * h + lane, sum,
                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
@@ -713,7 +747,7 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
             const int bl = c + lane * C;
             bool last = false;
             if (bl < nt) {
-                uint32_t *ctr = A->ctr + (T0 + (round0 + bl) * Gs);
+                uint32_t *ctr = ctr0 + (T0 + (round0 + bl) * Gs);
                 last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(S - 1);
                 if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
@@ -724,7 +758,9 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
                     const int i = __builtin_ctzll(mine);
                     mine &= mine - 1;
                     const int tile = T0 + (round0 + c + i * C) * Gs;
-                    const float *pp = A->part + (size_t)tile * S * (16 * MR);
+                    int32_t begin = ebegin;
+                    const StreamProblem pr = i == 0 ? epr : problem_at(A, problem_of(A, tile), begin);
+                    const float *pp = part + (size_t)tile * S * (16 * MR);
 #pragma unroll
                     for (int h = 0; h < MR / 4; ++h) {
                         const int o = 64 * h + lane;
@@ -739,7 +775,7 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
 #pragma unroll
                         for (int s2 = 1; s2 < kMaxSplit; ++s2)
                             if (s2 < S) sum += v[s2];
-                        store(tile, 4 * h + mq, sum);
+                        store(pr, begin, tile, 4 * h + mq, xe[h], sum);
                     }
                 }
             }
@@ -1238,9 +1274,11 @@ int64_t group_tiles(const kq_matmul_problem *ps, int n) {
 
 // K slices a launch of this group would take given the workspace (1: whole
 // K).  K past 16 super-blocks (the down projections) is cut into at most 8
-// slices of 8 super-blocks, else 12, 6 or 4 (the first that divides K);
-// GMLX_KQ_SPLITK=s asks for s slices (tests and tuning; 1 turns splitting
-// off).
+// slices of 8 super-blocks, else 12, 6 or 4 (the first that divides K); at
+// 9..16 rows slices of 12 come first (the Qwen3-8B down projection at 16
+// rows: 19.8 us in 4 slices against 22.8 in 6; at 8 rows 16.7 in 6 against
+// 17.4 in 4, measured).  GMLX_KQ_SPLITK=s asks for s slices (tests and
+// tuning; 1 turns splitting off).
 int kq_stream_split_want(const kq_matmul_problem *ps, int n) {
     if (n <= 0 || n > kStreamProblems || ps[0].M < 1 || ps[0].M > 16 || ps[0].K % KQ_QK) return 1;
     const int nb = ps[0].K / KQ_QK;
@@ -1250,7 +1288,8 @@ int kq_stream_split_want(const kq_matmul_problem *ps, int n) {
         return s >= 1 && s <= kMaxSplit && nb % s == 0 && stream_k_ok(ps[0].K / s) ? s : 1;
     }
     if (stream_k_ok(ps[0].K)) return 1;
-    for (const int w : {8, 12, 6, 4})
+    static constexpr int kWidths[2][4] = {{8, 12, 6, 4}, {12, 8, 6, 4}};
+    for (const int w : kWidths[ps[0].M > 8])
         if (nb % w == 0 && nb / w <= kMaxSplit) return nb / w;
     return 1;
 }

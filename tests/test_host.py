@@ -136,7 +136,7 @@ def test_host_validation_rejects_before_launch():
 
 def test_split_k_workspace(monkeypatch):
     """K past 16 super-blocks at <= 16 rows (a down projection) cuts K into
-    slices of 8 super-blocks: 512 (1024 past 8 rows) bytes of fp32 partials
+    slices of 8 super-blocks (12 past 8 rows): 512 (1024 past 8 rows) bytes of fp32 partials
     per (16-row weight tile, slice) after the counter region; more rows, or
     GMLX_KQ_SPLITK=1, none."""
     from gmlx_amd import _lib
@@ -155,9 +155,10 @@ def test_split_k_workspace(monkeypatch):
     monkeypatch.setenv("GMLX_KQ_SPLITK", "1")
     assert L.kq_matmul_workspace_bytes(arr, 1, _lib.DTYPE_F16) == 0
     monkeypatch.delenv("GMLX_KQ_SPLITK")
-    # 9..16 rows: 16-row partial tiles; past 16 rows no split
+    # 9..16 rows: 16-row partial tiles in slices of 12 super-blocks; past 16
+    # rows no split
     arr = (P * 1)(P(**dict(down, M=9)))
-    assert L.kq_matmul_workspace_bytes(arr, 1, _lib.DTYPE_F16) == ctr + tiles * slices * 1024
+    assert L.kq_matmul_workspace_bytes(arr, 1, _lib.DTYPE_F16) == ctr + tiles * (48 // 12) * 1024
     arr = (P * 1)(P(**dict(down, M=17)))
     assert L.kq_matmul_workspace_bytes(arr, 1, _lib.DTYPE_F16) == 0
     # slices of 8 super-blocks first, then 12, 6, 4: K of 56 -> 7 slices, 36
