@@ -720,10 +720,11 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
             const StreamProblem pr = b == c ? epr : problem_at(A, problem_of(A, tile), begin);
 #pragma unroll
             for (int h = 0; h < MR / 4; ++h) {
-                const int ln = 16 * h + n;
-                float sum = red[(b * C) * LR + ln][mq];
+                // one float per lane and partial tile: element mq of lane 16 h + n
+                const float *rf = (const float *)red + 4 * (b * C * LR + 16 * h + n) + mq;
+                float sum = rf[0];
 #pragma unroll
-                for (int c2 = 1; c2 < C; ++c2) sum += red[(b * C + c2) * LR + ln][mq];
+                for (int c2 = 1; c2 < C; ++c2) sum += rf[4 * c2 * LR];
                 if (S == 1) store(pr, begin, tile, 4 * h + mq, xe[h], sum);
                 else if (4 * h + mq < M)
                     __hip_atomic_store(part + ((size_t)tile * S + q) * (16 * MR) + 64 * h + lane, sum,
