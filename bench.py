@@ -101,10 +101,11 @@ def make_inputs(torch, rng, B):
 # dequantize and run the MFMA on one K-slab each), and so does down (K = 12288
 # Q6_K) in six K slices of 8 super-blocks, the last slice of each tile to
 # finish summing the six partial tiles; q|k|v (Q4_K and Q6_K tiles in one
-# launch) and o (at most two tiles per CU) take the LDS-staged persistent
-# kernel as two 8-wave workgroups per CU, one tile each.  At B = 9..16 down
-# takes the streaming kernel in its 16-row form (four K slices of 12
-# super-blocks) and the other launches the LDS-staged kernel; at B = 17..64 every launch
+# launch) takes it in two K slices (768 items, four consumers of two
+# super-blocks); o (one tile per CU) takes the LDS-staged persistent kernel as
+# two 8-wave workgroups per CU.  At B = 9..16 down takes the streaming kernel
+# in its 16-row form (four K slices of 12 super-blocks), q|k|v its 16-row
+# mixed form, gate|up and o the LDS-staged kernel; at B = 17..64 every launch
 # takes the mid-batch kernel (one 4-wave workgroup per CU over groups of T
 # weight tiles: q|k|v mixed T = 2, o and down T = 1, gate|up T = 6 up to 32
 # rows, 3 above); past 64 rows the general kernel.
@@ -130,8 +131,8 @@ def kernel_of(launch, B):
     if B <= 16 and launch == "down":  # K = 12288 in slices, one super-block per consumer
         # up to 8 rows: six slices of 8; 9..16 rows: four slices of 12 (two ring slots)
         return "kq_stream_kernel<14, 1, 8, 3, 8>" if B <= 8 else "kq_stream_kernel<14, 1, 12, 2, 16>"
-    if launch == "qkv":  # Q4_K q|k with Q6_K v: the mixed form (codec id 127)
-        return "kq_mv_kernel<127, 0, 2, 1, false, 8>" if B <= 8 else "kq_mv_kernel<127, 0, 1, 2, false, 16>"
+    if launch == "qkv":  # Q4_K q|k with Q6_K v: the mixed form (codec id 127) in two K slices
+        return f"kq_stream_kernel<127, 2, 4, 4, {8 if B <= 8 else 16}>"
     if launch == "o":
         return "kq_mv_kernel<12, 0, 2, 1, false, 8>" if B <= 8 else "kq_mv_kernel<12, 0, 1, 1, false, 16>"
     return "kq_mv_kernel<12, 0, 1, 3, false, 16>"  # gate|up at 9..16 rows

@@ -1278,8 +1278,10 @@ int64_t group_tiles(const kq_matmul_problem *ps, int n) {
 // slices of 8 super-blocks, else 12, 6 or 4 (the first that divides K); at
 // 9..16 rows slices of 12 come first (the Qwen3-8B down projection at 16
 // rows: 19.8 us in 4 slices against 22.8 in 6; at 8 rows 16.7 in 6 against
-// 17.4 in 4, measured).  GMLX_KQ_SPLITK=s asks for s slices (tests and
-// tuning; 1 turns splitting off).
+// 17.4 in 4, measured).  A Q4_K + Q6_K group of shorter K is cut in two
+// (q|k|v at 1..16 rows: 9.4-11.7 us against 9.6-12.7 for the LDS-staged
+// path, measured).  GMLX_KQ_SPLITK=s asks for s slices (tests and tuning; 1
+// turns splitting off).
 int kq_stream_split_want(const kq_matmul_problem *ps, int n) {
     if (n <= 0 || n > kStreamProblems || ps[0].M < 1 || ps[0].M > 16 || ps[0].K % KQ_QK) return 1;
     const int nb = ps[0].K / KQ_QK;
@@ -1288,7 +1290,16 @@ int kq_stream_split_want(const kq_matmul_problem *ps, int n) {
         const int s = atoi(e);
         return s >= 1 && s <= kMaxSplit && nb % s == 0 && stream_k_ok(ps[0].K / s) ? s : 1;
     }
-    if (stream_k_ok(ps[0].K)) return 1;
+    if (stream_k_ok(ps[0].K)) {
+        // a Q4_K + Q6_K group (the q|k|v of a Q4_K_M layer) takes two slices
+        bool q4 = false, q6 = false, other = false;
+        for (int i = 0; i < n; ++i) {
+            q4 |= ps[i].codec == KQ_CODEC_Q4_K;
+            q6 |= ps[i].codec == KQ_CODEC_Q6_K;
+            other |= ps[i].codec != KQ_CODEC_Q4_K && ps[i].codec != KQ_CODEC_Q6_K;
+        }
+        return q4 && q6 && !other && nb % 2 == 0 && stream_k_ok(ps[0].K / 2) ? 2 : 1;
+    }
     static constexpr int kWidths[2][4] = {{8, 12, 6, 4}, {12, 8, 6, 4}};
     for (const int w : kWidths[ps[0].M > 8])
         if (nb % w == 0 && nb / w <= kMaxSplit) return nb / w;
@@ -1329,19 +1340,21 @@ bool kq_stream_eligible(const kq_matmul_problem *ps, int n, int split) {
     // Routing (measured at the Qwen3-8B shapes, B = 1..8): the kernel's fixed
     // cost (ten waves per CU, the activation slab, the partial-tile sums) pays
     // off from about four items (tiles, or tile slices of a split launch) per
-    // CU (gate|up: 15.4-15.8 us against 16.4-17.7 us for the LDS-staged
-    // path); at one or two per CU (o, q|k|v) the LDS-staged path is faster,
-    // and a Q4_K + Q6_K group is slower here (its producers keep both slot
-    // geometries live and spill).  GMLX_KQ_STREAM=2 takes every eligible
+    // CU (gate|up: 15.4-16.6 us against 17.5-18.2 us for the LDS-staged
+    // path); at one per CU (o) the LDS-staged path is faster (5.5-7.6 us
+    // against 6.5-8.6 at 1..16 rows).  GMLX_KQ_STREAM=2 takes every eligible
     // launch (tests).  At 9..16 rows only split launches come here (the down
-    // projection: 21.6 / 23.4 us at 12 / 16 rows against 22.0 / 23.8 for the
-    // general kernel); whole-K gate|up stays on the LDS-staged path (19.2 /
-    // 19.9 us against 20.0 / 21.0: the 16-row form sums its partial tiles in
-    // two rounds).
+    // projection in 12-block slices: 18.1 / 19.2 us at 12 / 16 rows against
+    // 22.1 / 23.8 for the general kernel); whole-K gate|up stays on the
+    // LDS-staged path (20.0 against 20.05 at 16 rows).  A Q4_K + Q6_K group
+    // comes here split in two (q|k|v: 768 items, 3 per CU).
     if (!(env && env[0] == '2' && env[1] == 0)) {
-        if (mixed) return false;
-        if (q0.M > 8 && split == 1) return false;
-        if (tiles * split < 4 * (int64_t)device_cus()) return false;
+        if (mixed) {
+            if (split < 2 || tiles * split < 2 * (int64_t)device_cus()) return false;
+        } else {
+            if (q0.M > 8 && split == 1) return false;
+            if (tiles * split < 4 * (int64_t)device_cus()) return false;
+        }
     }
     return true;
 }

@@ -61,6 +61,36 @@ def test_config2_shapes_b8(codec):
         assert okq.max_rel(got, ref) <= TOL
 
 
+@pytest.mark.parametrize("M", [1, 8, 16])
+def test_config2_qkv_group(M, monkeypatch):
+    """The q|k|v group of a Qwen3-8B Q4_K_M layer (Q4_K q, k with Q6_K v) on
+    default routing (two K slices on the streaming kernel) matches the fp64
+    reference, repeats bitwise, agrees with the LDS-staged path and leaves the
+    workspace's arrival counters zero."""
+    import torch
+    from gmlx_amd import _lib, ops
+    for k in PATH_KNOBS:
+        monkeypatch.delenv(k, raising=False)
+    rng = np.random.default_rng(30 + M)
+    K = 4096
+    mats = [(quantized_weights(rng, "q4_k", 4096, K), "q4_k"), (quantized_weights(rng, "q4_k", 1024, K), "q4_k"),
+            (quantized_weights(rng, "q6_k", 1024, K), "q6_k")]
+    x16 = fp16_rows(rng, M, K)
+    x = _dev(x16)
+    items = [(x, _dev(w), c) for w, c in mats]
+    outs = [ops.quantized_matmul_grouped(items, out_dtype=torch.float32) for _ in range(2)]
+    torch.cuda.synchronize()
+    for (w, c), o, o2 in zip(mats, outs[0], outs[1]):
+        assert okq.max_rel(o.cpu().numpy(), okq.qmm_ref(x16, w, c)) <= TOL, c
+        assert torch.equal(o, o2)
+    ws = ops._WS.get("matmul", x.device, ops._stream(x).value, 0)
+    assert int(ws[:_lib.MATMUL_COUNTER_BYTES].count_nonzero()) == 0
+    monkeypatch.setenv("GMLX_KQ_STREAM", "0")
+    staged = ops.quantized_matmul_grouped(items, out_dtype=torch.float32)
+    for o, o2 in zip(outs[0], staged):
+        assert okq.max_rel(o.cpu().numpy(), o2.cpu().numpy()) <= TOL
+
+
 def test_bf16_activations_and_f32_out():
     import torch
     from gmlx_amd import ops

@@ -169,6 +169,24 @@ def test_split_k_workspace(monkeypatch):
         assert L.kq_matmul_workspace_bytes(arr, 1, _lib.DTYPE_F16) == want, nb
 
 
+def test_mixed_group_takes_two_k_slices():
+    """A Q4_K + Q6_K group of K <= 16 super-blocks (the q|k|v of a Q4_K_M
+    layer) is cut into two K slices: its workspace holds the counter region and
+    two 512-byte partial tiles per 16-row tile; a one-codec group of the same
+    K needs none."""
+    from gmlx_amd import _lib
+    L = _lib.lib()
+    P = _lib.MatmulProblem
+    base = dict(w=1 << 20, x=1 << 21, x_row_stride=4096, y=1 << 22, M=8, K=4096)
+    q = P(**base, w_row_bytes=16 * 144, y_row_stride=4096, N=4096, codec=_lib.CODEC_ID["q4_k"])
+    k = P(**base, w_row_bytes=16 * 144, y_row_stride=1024, N=1024, codec=_lib.CODEC_ID["q4_k"])
+    v = P(**base, w_row_bytes=16 * 210, y_row_stride=1024, N=1024, codec=_lib.CODEC_ID["q6_k"])
+    tiles = (4096 + 1024 + 1024) // 16
+    assert L.kq_matmul_workspace_bytes((P * 3)(q, k, v), 3, _lib.DTYPE_F16) == \
+        _lib.MATMUL_COUNTER_BYTES + tiles * 2 * 512
+    assert L.kq_matmul_workspace_bytes((P * 2)(q, k), 2, _lib.DTYPE_F16) == 0
+
+
 def test_ops_refuse_cpu_tensors():
     from gmlx_amd import ops
     x = torch.zeros(2, 256, dtype=torch.float16)
