@@ -474,7 +474,25 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
     static_assert(PL <= 63, "vmcnt counts at most 63 loads");
     constexpr int kTmax = tiles_per_round(MR);
     constexpr int LR = 4 * MR;  // lanes of a partial tile that hold live rows (MFMA row 4g + e in lane 16g + n)
-    constexpr int kStartTiles = KQ_STREAM_START_TILES < R ? KQ_STREAM_START_TILES : R;  // tiles issued before the first hand-off
+    // Activation staging: C regions of 8 rows of kXPitch bytes (1 KB and 16:
+    // rows on different banks) from ring slot kXSlot on, which the producers
+    // fill only after the first hand-off (it may reach into the partial-tile
+    // area, free until the round ends).  Forms where it does not fit load the
+    // fragments straight into registers.
+    constexpr int kXPitch = 1040;
+    constexpr size_t kXRegion = (size_t)C * 8 * kXPitch;
+    constexpr size_t kRedBytes = (size_t)kTmax * C * LR * 16;
+    constexpr int kXSlot = (size_t)(R - 2) * SLOTB + kRedBytes >= kXRegion && R >= 3   ? 2
+                           : (size_t)(R - 1) * SLOTB + kRedBytes >= kXRegion && R >= 2 ? 1
+                                                                                      : 0;
+    // Staging halves a two-block slab's load instructions (one 1 KB row each
+    // instead of eight 16-byte runs per block and lane); a one-block slab
+    // gains nothing at 8 rows and gives up a start tile (the down slices:
+    // 16.0 against 15.4 us, measured).  Two 16-row passes spill.
+    constexpr bool kXStaged = kXSlot > 0 && SB == 2 && MR == 8;
+    // tiles issued before the first hand-off (below the staging region)
+    constexpr int kStartTiles = kXStaged ? (KQ_STREAM_START_TILES < kXSlot ? KQ_STREAM_START_TILES : kXSlot)
+                                         : (KQ_STREAM_START_TILES < R ? KQ_STREAM_START_TILES : R);
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const KArgs A = (KArgs)__builtin_amdgcn_kernarg_segment_ptr();
     const Iq2Tables &iq2_tab = *IqTables<CODEC>::get();
@@ -605,40 +623,85 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
     [[maybe_unused]] half8_t xm;
     [[maybe_unused]] float xm_scale = 1.f;  // 2^xs of the owned view's sub-block sums
     {
-        // The slab's activation fragments straight from global memory into
-        // registers (no LDS, no barrier: the producers fill the whole ring
-        // from the start): lane (g, r) reads 16-byte runs of row r, rows >= M
-        // past the buffer (zeros).
         const uint32_t xbytes = (uint32_t)(((int64_t)(M - 1) * A->x_stride + A->K) * 2);
         const __amdgpu_buffer_rsrc_t xs = kq_buffer(A->x, xbytes);
-        const uint32_t xrow =
-            r < M ? (uint32_t)((r * A->x_stride + (q * NB + kb0) * KQ_QK) * 2) : 0x80000000u;
-        if constexpr (CODEC == KQ_CODEC_Q4_K) {
-            // owned view: lane group g needs values 64 g .. 64 g + 63 of each
-            // super-block, as 16-byte runs c[2 w + a] = x[64 g + 32 a + 8 w .. +7]
-            u32x4 cin[SB][8];
+        const uint32_t col0 = (uint32_t)((q * NB + kb0) * KQ_QK * 2);
+        if constexpr (kXStaged) {
+            // The slab's rows arrive by direct-to-LDS loads, one row (SB x
+            // 512 bytes) per instruction, into ring slots the producers fill
+            // only after the first hand-off; then each lane reads its
+            // fragments.  Lanes past the slab read zeros into the row's unused
+            // bytes.  16 rows take two passes through the region.
+            const uint32_t xreg = ring_lds + kXSlot * SLOTB + (uint32_t)(c * 8 * kXPitch);
+            const uint32_t lsrc = 16u * lane < 512u * SB ? 16u * lane + col0 : 0x80000000u;
+            const uint32_t rowa = xreg + (uint32_t)((r & 7) * kXPitch);
+            [[maybe_unused]] u32x4 cin[SB][8];
+            const u32x4 zero = {0u, 0u, 0u, 0u};
 #pragma unroll
-            for (int s2 = 0; s2 < SB; ++s2)
+            for (int p = 0; p < MR / 8; ++p) {
+                if (p > 0) __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the region's reads are done
 #pragma unroll
-                for (int w = 0; w < 4; ++w)
+                for (int m = 0; m < 8; ++m)
+                    if (8 * p + m < M)
+                        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                            xs, (LDSP(void))(uintptr_t)(xreg + m * kXPitch), 16,
+                            lsrc + (uint32_t)((8 * p + m) * A->x_stride * 2), 0, 0, 0);
+                if (p == 0) __builtin_amdgcn_s_barrier();  // the loads are issued: the producers may start
+                __builtin_amdgcn_s_waitcnt(KQ_VMCNT(0));
+                const bool mine = (r >> 3) == p && r < M;
 #pragma unroll
-                    for (int a2 = 0; a2 < 2; ++a2)
-                        cin[s2][2 * w + a2] = __builtin_bit_cast(
-                            u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                       xs, xrow + (uint32_t)(2 * (256 * s2 + 64 * g + 32 * a2 + 8 * w)), 0, 0));
-            __builtin_amdgcn_s_barrier();  // the loads are issued: the producers may start
-            int xs2;
-            q4own_x<SB>(xr, xm, xs2, cin, lane);
-            xm_scale = ldexpf(1.f, xs2);
+                for (int s2 = 0; s2 < SB; ++s2)
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) {
+                        if constexpr (CODEC == KQ_CODEC_Q4_K) {
+                            // owned view: c[2 w + a] = x[64 g + 32 a + 8 w .. +7]
+                            const u32x4 v =
+                                lds128(rowa + (uint32_t)(2 * (256 * s2 + 64 * g + 32 * (t & 1) + 8 * (t >> 1))));
+                            cin[s2][t] = mine ? v : (p == 0 ? zero : cin[s2][t]);
+                        } else {
+                            const u32x4 v = lds128(rowa + (uint32_t)(2 * (256 * s2 + Block<XC>::x_elem(t, g))));
+                            const u32x4 old = p == 0 ? zero : __builtin_bit_cast(u32x4, xr[s2][t]);
+                            xr[s2][t] = __builtin_bit_cast(half8_t, mine ? v : old);
+                        }
+                    }
+            }
+            if constexpr (CODEC == KQ_CODEC_Q4_K) {
+                int xs2;
+                q4own_x<SB>(xr, xm, xs2, cin, lane);
+                xm_scale = ldexpf(1.f, xs2);
+            }
         } else {
+            // The slab's activation fragments straight from global memory into
+            // registers: lane (g, r) reads 16-byte runs of row r, rows >= M
+            // past the buffer (zeros).
+            const uint32_t xrow = r < M ? (uint32_t)(r * A->x_stride * 2) + col0 : 0x80000000u;
+            if constexpr (CODEC == KQ_CODEC_Q4_K) {
+                // owned view: lane group g needs values 64 g .. 64 g + 63 of each
+                // super-block, as 16-byte runs c[2 w + a] = x[64 g + 32 a + 8 w .. +7]
+                u32x4 cin[SB][8];
 #pragma unroll
-            for (int s2 = 0; s2 < SB; ++s2)
+                for (int s2 = 0; s2 < SB; ++s2)
 #pragma unroll
-                for (int t = 0; t < 8; ++t)
-                    xr[s2][t] = __builtin_bit_cast(
-                        half8_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                     xs, xrow + (uint32_t)(2 * (256 * s2 + Block<XC>::x_elem(t, g))), 0, 0));
-            __builtin_amdgcn_s_barrier();  // the loads are issued: the producers may start
+                    for (int w = 0; w < 4; ++w)
+#pragma unroll
+                        for (int a2 = 0; a2 < 2; ++a2)
+                            cin[s2][2 * w + a2] = __builtin_bit_cast(
+                                u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                           xs, xrow + (uint32_t)(2 * (256 * s2 + 64 * g + 32 * a2 + 8 * w)), 0, 0));
+                __builtin_amdgcn_s_barrier();  // the loads are issued: the producers may start
+                int xs2;
+                q4own_x<SB>(xr, xm, xs2, cin, lane);
+                xm_scale = ldexpf(1.f, xs2);
+            } else {
+#pragma unroll
+                for (int s2 = 0; s2 < SB; ++s2)
+#pragma unroll
+                    for (int t = 0; t < 8; ++t)
+                        xr[s2][t] = __builtin_bit_cast(
+                            half8_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                         xs, xrow + (uint32_t)(2 * (256 * s2 + Block<XC>::x_elem(t, g))), 0, 0));
+                __builtin_amdgcn_s_barrier();  // the loads are issued: the producers may start
+            }
         }
     }
     // owned Q4_K view: the lane's row at super-block kb0 in slot 0
