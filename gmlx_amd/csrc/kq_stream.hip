@@ -725,6 +725,10 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
     asm volatile("" : "+s"(ydt), "+s"(part_b), "+s"(ctr_b));
     float *const part = (float *)(uintptr_t)part_b;
     uint32_t *const ctr0 = (uint32_t *)(uintptr_t)ctr_b;
+    // arrival counters spread over the counter region (up to one per 128-byte
+    // line): the slices of a launch's tiles arrive at nearly the same time
+    const int cstride = min(32, 1 << (31 - __builtin_clz(
+                                          (int)(KQ_MATMUL_COUNTER_BYTES / 4) / max(A->total_tiles, 1))));
     auto store = [&](const StreamProblem &pr, int32_t begin, int tile, int m, int e, float sum) {
         if (m >= M) return;
         if (has_xe) sum = ldexpf(sum, e);
@@ -811,7 +815,7 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
             const int bl = c + lane * C;
             bool last = false;
             if (bl < nt) {
-                uint32_t *ctr = ctr0 + (T0 + (round0 + bl) * Gs);
+                uint32_t *ctr = ctr0 + (T0 + (round0 + bl) * Gs) * cstride;
                 last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(S - 1);
                 if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
