@@ -103,9 +103,9 @@ def make_inputs(torch, rng, B):
 # finish summing the six partial tiles; q|k|v (Q4_K and Q6_K tiles in one
 # launch) takes it in two K slices (768 items, four consumers of two
 # super-blocks); o (one tile per CU) takes the LDS-staged persistent kernel as
-# two 8-wave workgroups per CU.  At B = 9..16 down takes the streaming kernel
-# in its 16-row form (four K slices of 12 super-blocks), q|k|v its 16-row
-# mixed form, gate|up and o the LDS-staged kernel; at B = 17..64 every launch
+# two 8-wave workgroups per CU.  At B = 9..16 the same routing holds with the
+# streaming kernel's 16-row forms (down in four K slices of 12 super-blocks);
+# at B = 17..64 every launch
 # takes the mid-batch kernel (one 4-wave workgroup per CU over groups of T
 # weight tiles: q|k|v mixed T = 2, o and down T = 1, gate|up T = 6 up to 32
 # rows, 3 above); past 64 rows the general kernel.
@@ -126,8 +126,8 @@ def kernel_of(launch, B):
     if B > 16:  # kq_mm_kernel<codec set (0 Q4_K, 1 Q6_K, 2 both), m-tiles, fp16, tiles per group>
         return {"qkv": f"kq_mm_kernel<2, {mt}, 0, 2>", "o": f"kq_mm_kernel<0, {mt}, 0, 1>",
                 "gate_up": f"kq_mm_kernel<0, {mt}, 0, {6 if mt == 2 else 3}>", "down": f"kq_mm_kernel<1, {mt}, 0, 1>"}[launch]
-    if B <= 8 and launch == "gate_up":  # kq_stream_kernel<codec, blocks per consumer, consumers, slots, rows>
-        return "kq_stream_kernel<12, 2, 8, 3, 8>"
+    if launch == "gate_up":  # kq_stream_kernel<codec, blocks per consumer, consumers, slots, rows>
+        return f"kq_stream_kernel<12, 2, 8, 3, {8 if B <= 8 else 16}>"
     if B <= 16 and launch == "down":  # K = 12288 in slices, one super-block per consumer
         # up to 8 rows: six slices of 8; 9..16 rows: four slices of 12 (two ring slots)
         return "kq_stream_kernel<14, 1, 8, 3, 8>" if B <= 8 else "kq_stream_kernel<14, 1, 12, 2, 16>"
@@ -135,7 +135,7 @@ def kernel_of(launch, B):
         return f"kq_stream_kernel<127, 2, 4, 4, {8 if B <= 8 else 16}>"
     if launch == "o":
         return "kq_mv_kernel<12, 0, 2, 1, false, 8>" if B <= 8 else "kq_mv_kernel<12, 0, 1, 1, false, 16>"
-    return "kq_mv_kernel<12, 0, 1, 3, false, 16>"  # gate|up at 9..16 rows
+    raise ValueError(launch)
 
 
 def family(kernel):

@@ -1410,16 +1410,14 @@ bool kq_stream_eligible(const kq_matmul_problem *ps, int n, int split) {
     // CU (gate|up: 15.4-16.6 us against 17.5-18.2 us for the LDS-staged
     // path); at one per CU (o) the LDS-staged path is faster (5.5-7.6 us
     // against 6.5-8.6 at 1..16 rows).  GMLX_KQ_STREAM=2 takes every eligible
-    // launch (tests).  At 9..16 rows only split launches come here (the down
-    // projection in 12-block slices: 18.1 / 19.2 us at 12 / 16 rows against
-    // 22.1 / 23.8 for the general kernel); whole-K gate|up stays on the
-    // LDS-staged path (20.0 against 20.05 at 16 rows).  A Q4_K + Q6_K group
-    // comes here split in two (q|k|v: 768 items, 3 per CU).
+    // launch (tests).  At 9..16 rows likewise (gate|up: 18.4 / 18.7 us at 12
+    // / 16 rows against 19.1 / 20.4; the down projection in 12-block slices:
+    // 18.1 / 19.2 against 22.1 / 23.8 for the general kernel).  A Q4_K + Q6_K
+    // group comes here split in two (q|k|v: 768 items, 3 per CU).
     if (!(env && env[0] == '2' && env[1] == 0)) {
         if (mixed) {
             if (split < 2 || tiles * split < 2 * (int64_t)device_cus()) return false;
         } else {
-            if (q0.M > 8 && split == 1) return false;
             if (tiles * split < 4 * (int64_t)device_cus()) return false;
         }
     }
