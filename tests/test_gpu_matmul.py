@@ -254,6 +254,10 @@ PATH_KNOBS = ("GMLX_KQ_STREAM", "GMLX_KQ_STREAM_WGS", "GMLX_KQ_SPLITK", "GMLX_KQ
     ("q4_k", 2000, 2048, 16),      # stream: 16 rows, two passes of activation staging
     ("q6_k", 500, 4096, 12),
     ("iq2_xxs", 300, 3072, 9),
+    ("q4_k", 16, 4096, 5),         # stream: one tile (one workgroup), staged activations
+    ("q6_k", 8, 4096, 8),          # stream: one partial tile, staged activations, two ring slots
+    ("iq2_xxs", 40, 4096, 2),      # stream: three tiles, the last partial, staged activations
+    ("q4_k", 48, 2048, 1),         # stream: 8 blocks per row, overlapping row loads
 ])
 def test_small_batch_paths(codec, N, K, M, monkeypatch):
     """Every small-batch path matches the fp64 reference on the same inputs."""
