@@ -104,16 +104,19 @@ def make_inputs(torch, rng, B):
 # launch) takes it in two K slices (768 items, four consumers of two
 # super-blocks); o (one tile per CU) takes the LDS-staged persistent kernel as
 # two 8-wave workgroups per CU.  At B = 9..16 the same routing holds with the
-# streaming kernel's 16-row forms (down in four K slices of 12 super-blocks);
-# at B = 17..64 every launch
-# takes the mid-batch kernel (one 4-wave workgroup per CU over groups of T
-# weight tiles: q|k|v mixed T = 2, o and down T = 1, gate|up T = 6 up to 32
-# rows, 3 above); past 64 rows the general kernel.
+# streaming kernel's 16-row forms (down in four K slices of 12 super-blocks).
+# At B = 17..64 q|k|v, gate|up and down take the mid-batch streaming kernel
+# (four waves copy each super-block of the activation rows and of a group of
+# six weight tiles into an LDS ring, six waves each accumulate one tile over
+# the group's K slice): gate|up unsplit (256 groups), down in five K slices,
+# q|k|v in three, the last slice of each tile summing the partial tiles; o
+# takes the 17..64-row tile kernel (one 4-wave workgroup per CU per weight
+# tile); past 64 rows the general kernel.
 LAUNCHES = [("qkv", ("q", "k", "v")), ("o", ("o",)), ("gate_up", ("gate", "up")), ("down", ("down",))]
 CODEC = {name: codec for name, _, _, codec in LAYER}
 DIMS = {name: (N, K) for name, N, K, _ in LAYER}
 # kernel families, as rocprofv3 names them
-KERNEL_FAMILIES = ("kq_stream_kernel", "kq_mv_kernel", "kq_qmv_persistent_kernel", "kq_mm_kernel",
+KERNEL_FAMILIES = ("kq_stream_kernel", "kq_mms_kernel", "kq_mv_kernel", "kq_qmv_persistent_kernel", "kq_mm_kernel",
                    "kq_dense_grouped_kernel")
 
 
@@ -123,9 +126,13 @@ def kernel_of(launch, B):
     dense = f"kq_dense_grouped_kernel<{mt}, 0, {16 if B <= 16 else 4}, {1 if B <= 16 else 2}>"
     if B > 64:
         return dense
-    if B > 16:  # kq_mm_kernel<codec set (0 Q4_K, 1 Q6_K, 2 both), m-tiles, fp16, tiles per group>
-        return {"qkv": f"kq_mm_kernel<2, {mt}, 0, 2>", "o": f"kq_mm_kernel<0, {mt}, 0, 1>",
-                "gate_up": f"kq_mm_kernel<0, {mt}, 0, {6 if mt == 2 else 3}>", "down": f"kq_mm_kernel<1, {mt}, 0, 1>"}[launch]
+    if B > 16:
+        # kq_mms_kernel<codec (12 Q4_K, 14 Q6_K, 127 both), 16-row blocks, tiles per group, ring slots>
+        # (q|k|v in 3 K slices, down in 5, gate|up unsplit); o: kq_mm_kernel<codec set (0 Q4_K),
+        # 16-row blocks, fp16, tiles per group>
+        return {"qkv": f"kq_mms_kernel<127, {mt}, 6, {4 if mt == 2 else 2}>", "o": f"kq_mm_kernel<0, {mt}, 0, 1>",
+                "gate_up": f"kq_mms_kernel<12, {mt}, 6, {4 if mt == 2 else 3}>",
+                "down": f"kq_mms_kernel<14, {mt}, 6, {4 if mt == 2 else 2}>"}[launch]
     if launch == "gate_up":  # kq_stream_kernel<codec, blocks per consumer, consumers, slots, rows>
         return f"kq_stream_kernel<12, 2, 8, 3, {8 if B <= 8 else 16}>"
     if B <= 16 and launch == "down":  # K = 12288 in slices, one super-block per consumer

@@ -40,6 +40,10 @@ int kq_qmv_persistent_launch(const kq_matmul_problem *ps, int n, const int32_t *
 int kq_qmv_persistent_grid(const kq_matmul_problem &q);
 // kq_mm.hip: batches of 17..64 rows (problems validated, all live, Q4_K /
 // Q6_K, sharing x / M / K).
+bool kq_mms_eligible(const kq_matmul_problem *ps, int n, bool room);
+size_t kq_mms_part_bytes(const kq_matmul_problem *ps, int n);
+int kq_mms_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, int y_dtype, uint32_t *ctr,
+                  float *part, hipStream_t s);
 bool kq_mm_eligible(const kq_matmul_problem *ps, int n, int x_dtype);
 int kq_mm_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, int y_dtype, hipStream_t s);
 int device_cus();
@@ -911,7 +915,8 @@ size_t split_bytes(const kq_matmul_problem *problems, int n_problems) {
     for (int i = 0; i < n_problems && i < KQ_MAX_GROUP; ++i)
         if (problems[i].M > 0 && problems[i].N > 0) all[na++] = problems[i];
     if (na == 0) return 0;
-    return kq_stream_part_bytes(all, na, kq_stream_split_want(all, na));
+    const size_t a = kq_stream_part_bytes(all, na, kq_stream_split_want(all, na)), b = kq_mms_part_bytes(all, na);
+    return a > b ? a : b;
 }
 
 }  // namespace
@@ -1038,15 +1043,23 @@ int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problem
             return KQ_OK;
         }
     }
-    // 17..64 rows sharing their activations: one launch with the activations
-    // streamed through LDS once per group of weight tiles (GMLX_KQ_MM=0: the
-    // dense kernel instead)
-    if (live > 0 && env_int_flag("GMLX_KQ_MM", 1)) {
+    // 17..64 rows sharing their activations: the mid-batch streaming kernel
+    // (K in stages, the activations read once per CU and unit; GMLX_KQ_MMS=0
+    // declines); else one launch with the activations streamed through LDS
+    // once per group of weight tiles (GMLX_KQ_MM=0: the dense kernel instead)
+    if (live > 0) {
         kq_matmul_problem all[KQ_MAX_GROUP];
         int na = 0;
         for (int i = 0; i < n_problems; ++i)
             if (problems[i].M != 0 && problems[i].N != 0) all[na++] = problems[i];
-        if (kq_mm_eligible(all, na, x_dtype)) return kq_mm_launch(all, na, xe0, y_dtype, (hipStream_t)stream);
+        // K slices given room for their partial tiles
+        const size_t pb = kq_mms_part_bytes(all, na);
+        const bool room = pb && workspace && !((uintptr_t)workspace & 255) && workspace_bytes >= used + pb;
+        if (kq_mms_eligible(all, na, room))
+            return kq_mms_launch(all, na, xe0, y_dtype, room ? (uint32_t *)workspace : nullptr,
+                                 room ? (float *)((char *)workspace + used) : nullptr, (hipStream_t)stream);
+        if (env_int_flag("GMLX_KQ_MM", 1) && kq_mm_eligible(all, na, x_dtype))
+            return kq_mm_launch(all, na, xe0, y_dtype, (hipStream_t)stream);
     }
     // small batches: one persistent launch per codec when every codec's
     // problems share their activations (q|k|v, gate|up of one layer)

@@ -918,6 +918,529 @@ bool stream_k_ok(int K) {
     return nb == 2 || nb == 4 || nb == 6 || nb == 8 || nb == 12 || nb == 16;
 }
 
+// ---- Mid-batch streaming kernel (17..64 rows) -------------------------------
+// Work units: a group of up to C (six) consecutive 16-row weight tiles of one
+// problem against one K slice (split launches cut K in S slices; unit u is
+// group u mod groups, slice u / groups, so the CUs walk one slice of the
+// activations at a time).  One workgroup per CU walks its units with K in
+// stages of one super-block.  kMmsProducers waves copy each stage into a ring
+// of R stage buffers in LDS with direct-to-LDS loads: the stage's activation
+// rows (two 512-byte rows per 1 KB load, their 16-byte chunks XOR-swizzled by
+// row so the consumers' fragment reads of 16 rows hit different banks) and the
+// group's weight rows of that super-block (RCW chunks per row: odd, so the 16
+// rows of a tile start in different banks).  Consumer c owns tile c of the
+// unit and accumulates its MT 16-row blocks of activations on MFMA, reading
+// every activation byte from HBM / L2 once per CU and unit.  Unsplit launches
+// store the results; split ones write the unit's partial tile, and the last
+// of a tile's S arrivals sums the S partials in slice order (deterministic)
+// and stores.  The weight views are kq_mma.h's Block<> (the minimum folded
+// into the weights), the activation fragments x[32 t + 8 g .. +7] of rows
+// 16 m + r.  The Q4_K + Q6_K form (q|k|v) lays each stage out for the larger
+// Q6_K rows and picks the codec per unit.
+constexpr int kMmsProducers = 4;
+constexpr int kMmsTiles = 6;  // tiles per group: consumers
+constexpr int kMmsMaxSplit = 16;
+
+// Chunks per super-block and per LDS weight row of a codec.
+__host__ __device__ constexpr int mms_cpb(int codec) { return codec == KQ_CODEC_Q6_K ? 14 : 9; }
+__host__ __device__ constexpr int mms_rcw(int codec) { return mms_cpb(codec) | 1; }
+
+template <int CODEC, int MT, int C>
+struct MmsGeo {
+    static constexpr int RCW = mms_rcw(CODEC == KQ_MIX ? KQ_CODEC_Q6_K : CODEC);  // largest row of the form
+    static constexpr int XL = MT * 8;                                             // activation loads per stage
+    static constexpr int WL = (C * 16 * RCW + 63) / 64;                           // weight loads per stage
+    static constexpr int PL = (XL + WL + kMmsProducers - 1) / kMmsProducers;     // loads per producer
+    static constexpr int XB = MT * 16 * 512;                                      // activation bytes per stage
+    static constexpr int SB = XB + WL * 1024;                                     // stage bytes
+};
+
+// Unit u of a launch: problem pi, its tiles t0 .. t0 + nt - 1 (global tile
+// numbers), super-blocks kb0 .. kb1 - 1.  Groups: each problem's tiles in runs
+// of C (its last run partial).
+struct MmsUnit {
+    int pi, t0, nt, kb0, kb1;
+};
+
+__device__ __forceinline__ int mms_ngroups(KArgs A, int C) {
+    int ng = 0;
+    for (int i = 0; i < A->n_problems; ++i)
+        ng += ((i + 1 < A->n_problems ? A->tile_begin[i + 1] : A->total_tiles) - A->tile_begin[i] + C - 1) / C;
+    return ng;
+}
+
+__device__ __forceinline__ MmsUnit mms_unit(KArgs A, int C, int ngroups, int nb, int u) {
+    MmsUnit w{0, 0, 0, 0, 0};
+    const int gp = u % ngroups, q = u / ngroups, S = A->split;
+    w.kb0 = q * nb / S;
+    w.kb1 = (q + 1) * nb / S;
+    int gb = 0;
+    for (int i = 0; i < A->n_problems; ++i) {
+        const int tb = A->tile_begin[i];
+        const int te = i + 1 < A->n_problems ? A->tile_begin[i + 1] : A->total_tiles;
+        const int ng = (te - tb + C - 1) / C;
+        if (gp >= gb && gp < gb + ng) {
+            w.pi = i;
+            w.t0 = tb + (gp - gb) * C;
+            w.nt = min(C, te - w.t0);
+        }
+        gb += ng;
+    }
+    return w;
+}
+
+inline int mms_groups_host(const int32_t *tile_begin, int n, int total, int C) {
+    int ng = 0;
+    for (int i = 0; i < n; ++i) ng += ((i + 1 < n ? tile_begin[i + 1] : total) - tile_begin[i] + C - 1) / C;
+    return ng;
+}
+
+// The producers' place in their unit walk: the unit and its next super-block.
+struct MmsCursor {
+    int u, kb, kb1;
+    uint32_t bpb;  // weight bytes per super-block of the unit's codec
+};
+
+// A producer's per-lane offsets for a unit: activation loads (rows 2 li,
+// 2 li + 1; lane l: row 2 li + l / 32, LDS chunk l % 32 holding activation
+// chunk (l % 32) ^ (row % 16)), weight loads (chunk f = 64 (li - XL) + l of
+// the stage's [tile][row][rcw chunks] block; rows past N clamped, pads, tiles
+// past the unit and chunks past the codec's part of the stage past the buffer).
+template <int CODEC, int MT, int C>
+__device__ __forceinline__ void mms_setup(KArgs A, const MmsUnit &w, int wave, int lane, int M,
+                                          uint32_t (&o)[MmsGeo<CODEC, MT, C>::PL], StreamProblem &pr,
+                                          uint32_t &bpb) {
+    using MG = MmsGeo<CODEC, MT, C>;
+    constexpr int NL = MG::XL + MG::WL;
+    int32_t begin;
+    pr = problem_at(A, w.pi, begin);
+    const bool q6 = CODEC == KQ_CODEC_Q6_K || (CODEC == KQ_MIX && pr.codec == KQ_CODEC_Q6_K);
+    const int cpb = q6 ? mms_cpb(KQ_CODEC_Q6_K) : mms_cpb(KQ_CODEC_Q4_K);
+    const int rcw = q6 ? mms_rcw(KQ_CODEC_Q6_K) : mms_rcw(KQ_CODEC_Q4_K);
+    bpb = q6 ? Geo<KQ_CODEC_Q6_K>::BPB : Geo<KQ_CODEC_Q4_K>::BPB;
+    const uint32_t row0 = (uint32_t)(w.t0 - begin) * 16, last = (uint32_t)pr.N - 1, rb = pr.row_bytes;
+#pragma unroll
+    for (int i = 0; i < MG::PL; ++i) {
+        const int li = min(wave + kMmsProducers * i, NL - 1);
+        if (li < MG::XL) {
+            const int row = 2 * li + (lane >> 5);
+            const int ch = (lane & 31) ^ (row & 15);
+            o[i] = row < M ? (uint32_t)(row * A->x_stride * 2 + 16 * ch) : 0x80000000u;
+        } else {
+            const int f = 64 * (li - MG::XL) + lane;
+            const int tile = f / (16 * rcw), rem = f - tile * (16 * rcw);
+            const int row = rem / rcw, ck = rem - row * rcw;
+            const uint32_t rr = min(row0 + (uint32_t)(tile * 16 + row), last);
+            const uint32_t src = q6 ? (uint32_t)Geo<KQ_CODEC_Q6_K>::src(ck) : (uint32_t)(16 * ck);
+            o[i] = ck < cpb && tile < w.nt ? rr * rb + src : 0x80000000u;
+        }
+    }
+}
+
+// Copy stage j (the cursor's next super-block) into ring slot j % R; moves
+// to the workgroup's next unit when the current one is done.
+template <int CODEC, int MT, int C, int R>
+__device__ __forceinline__ void mms_copy(KArgs A, int j, int wave, int lane, int M, int ngroups, int nb,
+                                         uint32_t ring, uint32_t xbytes, uint32_t (&o)[MmsGeo<CODEC, MT, C>::PL],
+                                         StreamProblem &pr, MmsCursor &cur) {
+    using MG = MmsGeo<CODEC, MT, C>;
+    constexpr int NL = MG::XL + MG::WL;
+    if (cur.kb == cur.kb1) {
+        cur.u += (int)gridDim.x;
+        const MmsUnit w = mms_unit(A, C, ngroups, nb, cur.u);
+        mms_setup<CODEC, MT, C>(A, w, wave, lane, M, o, pr, cur.bpb);
+        cur.kb = w.kb0;
+        cur.kb1 = w.kb1;
+    }
+    const int kb = cur.kb++;
+    const __amdgpu_buffer_rsrc_t ws = kq_buffer(pr.w, pr.w_bytes);
+    const __amdgpu_buffer_rsrc_t xs = kq_buffer(A->x, xbytes);
+    const uint32_t base = ring + (uint32_t)(j % R) * MG::SB;
+#pragma unroll
+    for (int i = 0; i < MG::PL; ++i) {
+        const int li = min(wave + kMmsProducers * i, NL - 1);
+        if (li < MG::XL)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xs, (LDSP(void))(uintptr_t)(base + 1024 * li), 16, o[i],
+                                                     kb * 512, 0, 0);
+        else
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ws, (LDSP(void))(uintptr_t)(base + MG::XB + 1024 * (li - MG::XL)),
+                                                     16, o[i], kb * (int)cur.bpb, 0, 0);
+    }
+}
+
+// One stage of one tile: acc[m] += x rows 16 m .. 16 m + 15 (super-block of
+// the stage) . weight rows of the tile (at wrow, RCW chunks apart).
+template <int CODEC, int MT>
+__device__ __forceinline__ void mms_tile_stage(floatx4 (&acc)[MT], uint32_t base, uint32_t wrow, int r, int g,
+                                               const Iq2Tables &iq2_tab) {
+    // activation fragments one step ahead of their MFMAs (the reads of step
+    // t + 1 in flight while step t multiplies)
+    const uint32_t xrow = base + (uint32_t)(r * 512);
+    u32x4 xq[2][MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+        xq[0][m] = lds128(xrow + (uint32_t)(m * 8192 + 16 * ((Block<CODEC>::x_elem(0, g) / 8) ^ r)));
+    Block<CODEC> blk;
+    load_slot<CODEC>(blk, wrow, g);
+    blk.prep(g);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        if (t < 7) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+                xq[(t + 1) & 1][m] =
+                    lds128(xrow + (uint32_t)(m * 8192 + 16 * ((Block<CODEC>::x_elem(t + 1, g) / 8) ^ r)));
+        }
+        __builtin_amdgcn_sched_barrier(0);  // (left alone, the scheduler sinks the reads to their use)
+        const half8_t wf = blk.frag(t, g, iq2_tab);
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+            acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, xq[t & 1][m]), wf, acc[m], 0,
+                                                             0, 0);
+    }
+}
+
+template <int CODEC, int MT, int C, int R>
+__global__ __launch_bounds__(64 * (kMmsProducers + C)) void kq_mms_kernel(StreamArgs a_) {
+    using MG = MmsGeo<CODEC, MT, C>;
+    constexpr int PL = MG::PL;
+    static_assert(PL * (R - 1) <= 63, "vmcnt counts at most 63 loads");
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const KArgs A = (KArgs)__builtin_amdgcn_kernarg_segment_ptr();
+    const Iq2Tables &iq2_tab = *IqTables<CODEC == KQ_MIX ? KQ_CODEC_Q4_K : CODEC>::get();
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = kq_lane(), r = lane & 15, g = lane >> 4;
+    const int M = A->M, nb = A->K / KQ_QK, S = A->split;
+    const int ngroups = mms_ngroups(A, C);
+    const int U = ngroups * S, G = (int)gridDim.x;
+    int stages = 0;
+    for (int u = (int)blockIdx.x; u < U; u += G) {
+        const int q = u / ngroups;
+        stages += (q + 1) * nb / S - q * nb / S;
+    }
+    const uint32_t ring = (uint32_t)(uintptr_t)(LDSP(void))smem;
+
+    if (wave < kMmsProducers) {
+        // ================= producers: load li = wave + kMmsProducers i of a
+        // stage (activation loads first, then weight loads); a producer with
+        // fewer than PL repeats its last load (the same bytes again)
+        const uint32_t xbytes = (uint32_t)(((int64_t)(M - 1) * A->x_stride + A->K) * 2);
+        uint32_t off[PL];  // per-lane offsets of the producer's loads (weights: for the current unit)
+        StreamProblem prob;  // set by the first unit's set-up
+        MmsCursor cur{(int)blockIdx.x - G, 0, 0, 0};
+        const int pre = min(R, stages);
+        for (int j = 0; j < pre; ++j)
+            mms_copy<CODEC, MT, C, R>(A, j, wave, lane, M, ngroups, nb, ring, xbytes, off, prob, cur);
+        for (int b = 0; b < stages; ++b) {
+            const int newer = min(b == 0 ? R - 1 : R - 2, stages - 1 - b);
+            wait_tiles_left<PL, R - 1>(newer);
+            __builtin_amdgcn_s_barrier();  // stage b to the consumers; stage b - 1 back
+            if (b >= 1 && b + R - 1 < stages)
+                mms_copy<CODEC, MT, C, R>(A, b + R - 1, wave, lane, M, ngroups, nb, ring, xbytes, off, prob, cur);
+        }
+        return;
+    }
+
+    // ================= consumer c: tile c of each unit
+    const int c = wave - kMmsProducers;
+    const bool has_xe = A->x_exp != nullptr;
+    int ydt = A->y_dtype;
+    uint64_t part_b = (uint64_t)(uintptr_t)A->part, ctr_b = (uint64_t)(uintptr_t)A->ctr;
+    asm volatile("" : "+s"(ydt), "+s"(part_b), "+s"(ctr_b));
+    float *const part = (float *)(uintptr_t)part_b;
+    uint32_t *const ctr0 = (uint32_t *)(uintptr_t)ctr_b;
+    // arrival counters spread over the counter region (up to one per 128-byte line)
+    const int cstride = min(32, 1 << (31 - __builtin_clz((int)(KQ_MATMUL_COUNTER_BYTES / 4) / max(A->total_tiles, 1))));
+    int j = 0;
+    for (int u = (int)blockIdx.x; u < U; u += G) {
+        const MmsUnit w = mms_unit(A, C, ngroups, nb, u);
+        int32_t begin;
+        const StreamProblem pr = problem_at(A, w.pi, begin);
+        const bool q6 = CODEC == KQ_CODEC_Q6_K || (CODEC == KQ_MIX && pr.codec == KQ_CODEC_Q6_K);
+        const uint32_t pitch = (uint32_t)(q6 ? mms_rcw(KQ_CODEC_Q6_K) : mms_rcw(KQ_CODEC_Q4_K)) * 16;
+        floatx4 acc[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[m] = floatx4{0, 0, 0, 0};
+        for (int kb = w.kb0; kb < w.kb1; ++kb, ++j) {
+            __builtin_amdgcn_s_barrier();  // stage j has landed
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+            const uint32_t base = ring + (uint32_t)(j % R) * MG::SB;
+            if (c < w.nt) {
+                const uint32_t wrow = base + MG::XB + (uint32_t)(c * 16 + r) * pitch;
+                if constexpr (CODEC == KQ_MIX) {
+                    if (q6) mms_tile_stage<KQ_CODEC_Q6_K, MT>(acc, base, wrow, r, g, iq2_tab);
+                    else mms_tile_stage<KQ_CODEC_Q4_K, MT>(acc, base, wrow, r, g, iq2_tab);
+                } else {
+                    mms_tile_stage<CODEC, MT>(acc, base, wrow, r, g, iq2_tab);
+                }
+                kq_mfma_drain();
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // stage reads done
+        }
+        if (c >= w.nt) continue;
+        const int tile = w.t0 + c;
+        const int nn = (tile - begin) * 16 + r;
+        if (S == 1) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int row = 16 * m + 4 * g + e;
+                    if (row < M && nn < pr.N) {
+                        float v = acc[m][e];
+                        if (has_xe) v = ldexpf(v, A->x_exp[row]);
+                        kq_store_out(pr.y, ydt, (int64_t)row * pr.y_stride + nn, v);
+                    }
+                }
+            continue;
+        }
+        // Split launches: the unit's partial tile out ([m][e][lane] floats),
+        // then one arrival on the tile's counter; the last of its S arrivals
+        // sums the S partials in slice order, stores, and clears the count
+        // for the next call.  The partials move by agent-scope stores and
+        // loads (coherent across the XCDs' L2s by themselves); the stores
+        // have completed (vmcnt 0) before the arrival is counted, and the
+        // loads issue only after the count returns.
+        const int q = u / ngroups;
+        // (an opaque lane offset: left alone, the compiler hoists these
+        // addresses out of the stage loop and holds them in registers)
+        int lo = lane;
+        asm volatile("" : "+v"(lo));
+        float *const pq = part + ((size_t)tile * S + q) * (MT * 256) + lo;
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+            if (16 * m < M)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    __hip_atomic_store(pq + m * 256 + e * 64, acc[m][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_s_waitcnt(KQ_VMCNT(0));
+        uint32_t *const ctr = ctr0 + tile * cstride;
+        uint32_t prev = 0;
+        if (lane == 0) prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        prev = (uint32_t)__builtin_amdgcn_readfirstlane((int)prev);
+        if (prev != (uint32_t)(S - 1)) continue;
+        if (lane == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        // the partials of four slices at a time in flight (one load of each
+        // after another would wait out a round trip per load), summed in
+        // slice order
+        const float *const pt = part + (size_t)tile * S * (MT * 256) + lo;
+        floatx4 sum[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) sum[m] = floatx4{0, 0, 0, 0};
+        for (int s0 = 0; s0 < S; s0 += 4) {
+            floatx4 v[4][MT];
+#pragma unroll
+            for (int d = 0; d < 4; ++d)
+#pragma unroll
+                for (int m = 0; m < MT; ++m)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        v[d][m][e] = s0 + d < S && 16 * m < M
+                                         ? __hip_atomic_load(pt + (s0 + d) * (MT * 256) + m * 256 + e * 64,
+                                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                         : 0.f;
+#pragma unroll
+            for (int d = 0; d < 4; ++d)
+#pragma unroll
+                for (int m = 0; m < MT; ++m) sum[m] += v[d][m];
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int row = 16 * m + 4 * g + e;
+                if (row < M && nn < pr.N) {
+                    float y = sum[m][e];
+                    if (has_xe) y = ldexpf(y, A->x_exp[row]);
+                    kq_store_out(pr.y, ydt, (int64_t)row * pr.y_stride + nn, y);
+                }
+            }
+    }
+}
+
+template <int CODEC, int MT, int C>
+int launch_mms(const StreamArgs &a, int grid, hipStream_t s) {
+    using MG = MmsGeo<CODEC, MT, C>;
+    constexpr size_t budget = 160 * 1024;
+    constexpr int R0 = budget / MG::SB > 4 ? 4 : (int)(budget / MG::SB);
+    constexpr int R = MG::PL * (R0 - 1) <= 63 ? R0 : 63 / MG::PL + 1;
+    static_assert(R >= 2, "mid-batch stream kernel LDS");
+    constexpr size_t lds = (size_t)R * MG::SB;
+    static bool raised = false;
+    if (!raised) {
+        if (hipFuncSetAttribute((const void *)kq_mms_kernel<CODEC, MT, C, R>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+            return KQ_ERR_LAUNCH_FAILED;
+        raised = true;
+    }
+    hipLaunchKernelGGL((kq_mms_kernel<CODEC, MT, C, R>), dim3(grid), dim3(64 * (kMmsProducers + C)), lds, s, a);
+    return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
+}
+
+template <int CODEC>
+int launch_mms_rows(const StreamArgs &a, int grid, hipStream_t s) {
+    return a.M <= 32 ? launch_mms<CODEC, 2, kMmsTiles>(a, grid, s) : launch_mms<CODEC, 4, kMmsTiles>(a, grid, s);
+}
+
+// K slices of a launch: the split that leaves the fewest stages per CU
+// (rounds of units over the CUs, times the super-blocks of a slice plus, for
+// a split launch, about one stage's worth of partial tiles).  GMLX_KQ_MMS_S
+// forces the count (tests and tuning).
+int mms_split(const kq_matmul_problem *ps, int n, int max_split) {
+    const int nb = ps[0].K / KQ_QK, cus = device_cus();
+    int32_t tb[KQ_MAX_GROUP];
+    int tiles = 0;
+    for (int i = 0; i < n; ++i) {
+        tb[i] = tiles;
+        tiles += (ps[i].N + 15) / 16;
+    }
+    const int ng = mms_groups_host(tb, n, tiles, kMmsTiles);
+    const int smax = min(min(max_split, kMmsMaxSplit), nb);
+    if (const char *e = getenv("GMLX_KQ_MMS_S")) {
+        const int s = atoi(e);
+        return s >= 1 && s <= smax ? s : 1;
+    }
+    int64_t best = -1;
+    int split = 1;
+    for (int s = 1; s <= smax; ++s) {
+        const int64_t cost = (int64_t)((ng * s + cus - 1) / cus) * ((nb + s - 1) / s + (s > 1));
+        if (best < 0 || cost < best) {
+            best = cost;
+            split = s;
+        }
+    }
+    return split;
+}
+
+}  // namespace
+
+namespace {
+
+// The shapes the kernel serves: 17..64 rows of fp16 activations (16-byte
+// aligned rows), one codec (Q4_K or Q6_K) or Q4_K with Q6_K, at most 4
+// problems sharing x / stride / M / K, weights and x addressable with 31-bit
+// buffer offsets.
+bool mms_shape_ok(const kq_matmul_problem *ps, int n) {
+    if (n <= 0 || n > kStreamProblems) return false;
+    const kq_matmul_problem &q0 = ps[0];
+    if (q0.M < 17 || q0.M > 64 || q0.K % KQ_QK || q0.K < KQ_QK) return false;
+    // 16-byte activation pieces: x and its row stride 16-byte aligned
+    if (((uintptr_t)q0.x & 15) != 0 || q0.x_row_stride % 8 != 0) return false;
+    for (int i = 0; i < n; ++i) {
+        const kq_matmul_problem &q = ps[i];
+        if (q.codec != KQ_CODEC_Q4_K && q.codec != KQ_CODEC_Q6_K) return false;
+        if (q.x != q0.x || q.x_row_stride != q0.x_row_stride || q.M != q0.M || q.K != q0.K) return false;
+        if ((int64_t)(q.N + 16) * q.w_row_bytes >= (int64_t)0x80000000LL) return false;
+    }
+    if ((int64_t)(q0.M - 1) * q0.x_row_stride * 2 + (int64_t)q0.K * 2 >= (int64_t)0x80000000LL) return false;
+    return true;
+}
+
+int64_t mms_tiles(const kq_matmul_problem *ps, int n) {
+    int64_t tiles = 0;
+    for (int i = 0; i < n; ++i) tiles += (ps[i].N + 15) / 16;
+    return tiles;
+}
+
+// K slices the launch may take: split launches need one arrival counter per
+// tile in the counter region (and room for the partial tiles).
+int mms_max_split(const kq_matmul_problem *ps, int n, bool room) {
+    return room && mms_tiles(ps, n) * 4 <= (int64_t)KQ_MATMUL_COUNTER_BYTES ? kMmsMaxSplit : 1;
+}
+
+// Routing (measured at the Qwen3-8B shapes, 17..64 rows): the kernel pays off
+// when its planned units (tile groups times K slices) cover three quarters of
+// the CUs or more: gate|up (256 groups, unsplit: 21.0-28.9 us against
+// 29.5-44.3 for the tile kernel), the down projection (43 groups in 5 slices:
+// 22.6-27.8 against 24.1-37.1), q|k|v (65 groups in 3 slices: 16.8-19.5
+// against 17.1-21.4); not o (43 groups in 4 slices, 172 units: 11.5-15.6
+// against 9.3-12.8).  GMLX_KQ_MMS=0 declines, =2 takes every shape it serves
+// (tests).
+bool mms_worth(const kq_matmul_problem *ps, int n, bool room) {
+    const char *env = getenv("GMLX_KQ_MMS");
+    if (env && env[0] == '0' && env[1] == 0) return false;
+    if (env && env[0] == '2' && env[1] == 0) return true;
+    int32_t tb[KQ_MAX_GROUP];
+    int tiles = 0;
+    for (int i = 0; i < n; ++i) {
+        tb[i] = tiles;
+        tiles += (ps[i].N + 15) / 16;
+    }
+    const int64_t units = (int64_t)mms_groups_host(tb, n, tiles, kMmsTiles) * mms_split(ps, n, mms_max_split(ps, n, room));
+    return 4 * units >= 3 * (int64_t)device_cus();
+}
+
+}  // namespace
+
+// Whether the mid-batch streaming kernel takes the launch (room: the
+// workspace holds kq_mms_part_bytes after the counter region).
+bool kq_mms_eligible(const kq_matmul_problem *ps, int n, bool room) {
+    return mms_shape_ok(ps, n) && mms_worth(ps, n, room);
+}
+
+// Bytes of partial tiles the launch writes when it is taken and given room
+// for them (after the counter region): MT 1 KB blocks per tile and slice.
+size_t kq_mms_part_bytes(const kq_matmul_problem *ps, int n) {
+    if (!kq_mms_eligible(ps, n, true)) return 0;
+    const int S = mms_split(ps, n, mms_max_split(ps, n, true));
+    const size_t mt = ps[0].M <= 32 ? 2 : 4;
+    return S > 1 ? ((size_t)mms_tiles(ps, n) * S * mt * 1024 + 255) & ~(size_t)255 : 0;
+}
+
+// Problems validated and eligible (for this room); x fp16, x_exp its per-row
+// exponents or null.  ctr / part: the arrival counters (zero on entry; left
+// zero) and room for kq_mms_part_bytes, or null (no split).
+int kq_mms_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, int y_dtype, uint32_t *ctr,
+                  float *part, hipStream_t s) {
+    StreamArgs a;
+    int tiles = 0;
+    bool mixed = false;
+    for (int i = 0; i < n; ++i) {
+        StreamProblem &p = a.p[i];
+        p.w = (const uint8_t *)ps[i].w;
+        p.y = ps[i].y;
+        p.y_stride = ps[i].y_row_stride;
+        p.row_bytes = (uint32_t)ps[i].w_row_bytes;
+        p.w_bytes = (uint32_t)(ps[i].N * ps[i].w_row_bytes);
+        p.N = ps[i].N;
+        p.codec = ps[i].codec;
+        a.tile_begin[i] = tiles;
+        tiles += (ps[i].N + 15) / 16;
+        if (ps[i].codec != ps[0].codec) mixed = true;
+    }
+    for (int i = n; i < KQ_MAX_GROUP; ++i) {
+        a.p[i] = a.p[0];
+        a.tile_begin[i] = 0x7FFFFFFF;
+    }
+    const kq_matmul_problem &q0 = ps[0];
+    const int S = mms_split(ps, n, mms_max_split(ps, n, ctr && part));
+    a.x = (const char *)q0.x;
+    a.x_exp = x_exp;
+    a.ctr = S > 1 ? ctr : nullptr;
+    a.part = S > 1 ? part : nullptr;
+    a.x_stride = q0.x_row_stride;
+    a.M = q0.M;
+    a.K = q0.K;
+    a.y_dtype = y_dtype;
+    a.total_tiles = tiles;
+    a.n_problems = n;
+    a.split = S;
+    const int units = mms_groups_host(a.tile_begin, n, tiles, kMmsTiles) * S;
+    int grid = device_cus();
+    if (const char *e = getenv("GMLX_KQ_STREAM_WGS")) {
+        const int w = atoi(e);
+        if (w > 0 && w < grid) grid = w;
+    }
+    if (grid > units) grid = units;
+    if (mixed) return launch_mms_rows<KQ_MIX>(a, grid, s);
+    return q0.codec == KQ_CODEC_Q6_K ? launch_mms_rows<KQ_CODEC_Q6_K>(a, grid, s)
+                                     : launch_mms_rows<KQ_CODEC_Q4_K>(a, grid, s);
+}
+
+namespace {
+
 // ---- Streaming expert gather ------------------------------------------------
 // The MoE expert matmuls (kq_gather_qmm, kq_moe_glu_gather, kq_moe_gather_rows)
 // on the same producer / consumer ring: a work item is one 16-row weight tile

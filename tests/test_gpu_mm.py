@@ -1,8 +1,9 @@
-"""Parity of the 17..64-row path (kq_mm.hip, reached through
-kq_quantized_matmul_grouped): every tile-group size, both codecs and their
-mix, ragged super-block counts per wave, bf16 activations, strided rows and
-every output dtype, against the fp64 oracle (max-rel <= 2e-3; bf16
-activations 8e-3), plus bitwise determinism and grouped == separate."""
+"""Parity of the 17..64-row tile kernel (kq_mm.hip, reached through
+kq_quantized_matmul_grouped with the mid-batch streaming kernel declined):
+every tile-group size, both codecs and their mix, ragged super-block counts
+per wave, bf16 activations, strided rows and every output dtype, against the
+fp64 oracle (max-rel <= 2e-3; bf16 activations 8e-3), plus bitwise
+determinism and grouped == separate."""
 import numpy as np
 import pytest
 
@@ -22,6 +23,7 @@ def _dev(a):
 def _clear(monkeypatch):
     for k in ENV:
         monkeypatch.delenv(k, raising=False)
+    monkeypatch.setenv("GMLX_KQ_MMS", "0")  # the tile kernel, not the mid-batch streaming one
 
 
 @pytest.mark.parametrize("codec", ["q4_k", "q6_k"])

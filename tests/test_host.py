@@ -137,8 +137,8 @@ def test_host_validation_rejects_before_launch():
 def test_split_k_workspace(monkeypatch):
     """K past 16 super-blocks at <= 16 rows (a down projection) cuts K into
     slices of 8 super-blocks (12 past 8 rows): 512 (1024 past 8 rows) bytes of fp32 partials
-    per (16-row weight tile, slice) after the counter region; more rows, or
-    GMLX_KQ_SPLITK=1, none."""
+    per (16-row weight tile, slice) after the counter region; with
+    GMLX_KQ_SPLITK=1, none (17..64 rows: test_mid_batch_split_workspace)."""
     from gmlx_amd import _lib
     L = _lib.lib()
     P = _lib.MatmulProblem
@@ -155,18 +155,52 @@ def test_split_k_workspace(monkeypatch):
     monkeypatch.setenv("GMLX_KQ_SPLITK", "1")
     assert L.kq_matmul_workspace_bytes(arr, 1, _lib.DTYPE_F16) == 0
     monkeypatch.delenv("GMLX_KQ_SPLITK")
-    # 9..16 rows: 16-row partial tiles in slices of 12 super-blocks; past 16
-    # rows no split
+    # 9..16 rows: 16-row partial tiles in slices of 12 super-blocks
     arr = (P * 1)(P(**dict(down, M=9)))
     assert L.kq_matmul_workspace_bytes(arr, 1, _lib.DTYPE_F16) == ctr + tiles * (48 // 12) * 1024
-    arr = (P * 1)(P(**dict(down, M=17)))
-    assert L.kq_matmul_workspace_bytes(arr, 1, _lib.DTYPE_F16) == 0
     # slices of 8 super-blocks first, then 12, 6, 4: K of 56 -> 7 slices, 36
     # -> 3 (of 12), 28 -> 7 (of 4); 43 (no width divides it): none
     for nb, slices in ((56, 7), (36, 3), (28, 7), (43, 0)):
         arr = (P * 1)(P(**dict(down, K=256 * nb, x_row_stride=256 * nb, w_row_bytes=210 * nb)))
         want = ctr + tiles * slices * 512 if slices else 0
         assert L.kq_matmul_workspace_bytes(arr, 1, _lib.DTYPE_F16) == want, nb
+
+
+def test_mid_batch_split_workspace(monkeypatch):
+    """17..64 rows (the mid-batch streaming kernel): groups of six 16-row
+    tiles in K slices, the split leaving the fewest rounds of (stages + one)
+    per CU on 256 CUs, with 2 KB (17..32 rows) or 4 KB (33..64) of partials per
+    tile and slice: the down projection (43 groups, 48 super-blocks) in 5
+    slices, q|k|v (65 groups) in 3, gate|up (256 groups) unsplit; o (43
+    groups in 4 slices: 172 units, under three quarters of the CUs) is left
+    to the tile kernel and needs none.  GMLX_KQ_MMS=2 takes it anyway;
+    GMLX_KQ_MMS_S forces the count (1: none)."""
+    from gmlx_amd import _lib
+    L = _lib.lib()
+    P = _lib.MatmulProblem
+    ctr = _lib.MATMUL_COUNTER_BYTES
+    q4, q6 = _lib.CODEC_ID["q4_k"], _lib.CODEC_ID["q6_k"]
+
+    def ws(probs):
+        arr = (P * len(probs))(*probs)
+        return L.kq_matmul_workspace_bytes(arr, len(probs), _lib.DTYPE_F16)
+
+    def prob(M, N, K, codec):
+        return P(w=1 << 20, w_row_bytes=(210 if codec == q6 else 144) * (K // 256), x=1 << 21, x_row_stride=K,
+                 y=1 << 22, y_row_stride=N, M=M, N=N, K=K, codec=codec)
+
+    assert ws([prob(17, 4096, 12288, q6)]) == ctr + 256 * 5 * 2048
+    assert ws([prob(64, 4096, 12288, q6)]) == ctr + 256 * 5 * 4096
+    assert ws([prob(40, 4096, 4096, q4)]) == 0
+    qkv = [prob(32, 4096, 4096, q4), prob(32, 1024, 4096, q4), prob(32, 1024, 4096, q6)]
+    assert ws(qkv) == ctr + 384 * 3 * 2048
+    assert ws([prob(64, 12288, 4096, q4), prob(64, 12288, 4096, q4)]) == 0
+    monkeypatch.setenv("GMLX_KQ_MMS", "2")
+    assert ws([prob(40, 4096, 4096, q4)]) == ctr + 256 * 4 * 4096
+    monkeypatch.setenv("GMLX_KQ_MMS_S", "2")
+    assert ws([prob(64, 4096, 4096, q4)]) == ctr + 256 * 2 * 4096
+    monkeypatch.setenv("GMLX_KQ_MMS_S", "1")
+    assert ws([prob(64, 4096, 4096, q4)]) == 0
 
 
 def test_mixed_group_takes_two_k_slices():
