@@ -118,12 +118,16 @@ typedef struct {
  *    [2^14, 2^15), and the fp32 results are scaled back by 2^e before
  *    rounding to y_dtype -- no overflow past 65504, no flush below 2^-14,
  *    bf16 values exact;
- *  - for groups of at most 8 rows whose K runs past 16 super-blocks (the
- *    down projections), fp32 partial tiles of K slices: such a launch cuts K
- *    into slices of 8 super-blocks, and the last slice of each 16-row tile to
- *    finish sums the slices in slice order (results stay independent of
- *    scheduling).  With fp16 activations a workspace smaller than this
- *    (none included) takes the unsplit kernels instead. */
+ *  - fp32 partial tiles of K slices for the launches that cut K: groups of
+ *    at most 16 rows whose K runs past 16 super-blocks (the down
+ *    projections: slices of 8 super-blocks up to 8 rows, 12 past 8) and
+ *    Q4_K + Q6_K groups of at most 16 rows (q|k|v: two slices); 17..64-row
+ *    groups that the mid-batch streaming kernel takes in slices (the down
+ *    projection, q|k|v: 2 or 4 KB per 16-row tile and slice).  The last
+ *    slice of each 16-row tile to finish sums the slices in slice order
+ *    (results stay independent of scheduling).  With fp16 activations a
+ *    workspace smaller than this (none included) takes the unsplit kernels
+ *    instead. */
 size_t kq_matmul_workspace_bytes(const kq_matmul_problem *problems, int n_problems, int x_dtype);
 
 /* kq.quantized_matmul(x, w, scales, codec, transpose=True) -- the
