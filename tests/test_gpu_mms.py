@@ -193,3 +193,31 @@ def test_strided_rows_through_the_c_abi_split(M, monkeypatch):
         ref = okq.qmm_ref(x16, w, c)
         assert okq.max_rel(y[:, :N].cpu().numpy(), ref) <= TOL, c
         assert bool((y[:, N:] == 7.0).all()), c
+
+
+def test_split_launch_graph_replays(monkeypatch):
+    """A split launch (the down projection's shape at 40 rows: 5 K slices)
+    captured in a HIP graph: three replays, with eager calls on other inputs
+    between them, each equal bitwise to the eager result (the arrival
+    counters return to zero every call, inside the graph too)."""
+    import torch
+    from gmlx_amd import ops
+    _clear(monkeypatch)
+    monkeypatch.delenv("GMLX_KQ_MMS")
+    rng = np.random.default_rng(21)
+    K, N, M = 12288, 4096, 40
+    w = _dev(quantized_weights(rng, "q6_k", N, K))
+    x = _dev(fp16_rows(rng, M, K))
+    x2 = _dev(fp16_rows(rng, M, K))
+    eager = ops.quantized_matmul(x, w, None, "q6_k")
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = ops.quantized_matmul(x, w, None, "q6_k")
+    for _ in range(3):
+        other = ops.quantized_matmul(x2, w, None, "q6_k")
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        assert not torch.equal(other, eager)
