@@ -452,7 +452,8 @@ def test_stream_large_scales_take_the_two_step_form(monkeypatch):
 
 WIDE_ROUTES = [("default", {}), ("stream", {"GMLX_KQ_STREAM": "2"}),
                ("dense", {"GMLX_KQ_STREAM": "0", "GMLX_KQ_MV": "0", "GMLX_KQ_PERSISTENT": "0", "GMLX_KQ_MM": "0"}),
-               ("persistent", {"GMLX_KQ_STREAM": "0", "GMLX_KQ_MV": "0", "GMLX_KQ_QMV_WGS": "2"})]
+               ("persistent", {"GMLX_KQ_STREAM": "0", "GMLX_KQ_MV": "0", "GMLX_KQ_QMV_WGS": "2"}),
+               ("mid-batch streaming", {"GMLX_KQ_MMS": "2"})]
 
 
 @pytest.mark.parametrize("M", [1, 7, 24, 80])
@@ -461,7 +462,8 @@ def test_wide_range_activations(M, codec, monkeypatch):
     """bf16 and fp32 activation rows far outside fp16's range -- entries of a
     few 1e5, rows scaled by 1e-6 (below fp16's 2^-14 normal limit) -- through
     every route (M 1 / 7: streaming, LDS-staged, register persistent; 24:
-    mid-batch; 80 and the forced route: general).  Each row enters as fp16
+    the mid-batch tile kernel and, forced, the mid-batch streaming kernel in
+    K slices; 80 and the forced route: general).  Each row enters as fp16
     with a power of two of its own and its results are scaled back in fp32,
     so every output row matches the fp64 reference on its own scale
     (narrowing straight to fp16 turned the first row to inf and the second
@@ -486,7 +488,7 @@ def test_wide_range_activations(M, codec, monkeypatch):
         for name, env in WIDE_ROUTES:
             if name == "stream" and M > 8:
                 continue
-            for k in PATH_KNOBS + ("GMLX_KQ_MM",):
+            for k in PATH_KNOBS + ("GMLX_KQ_MM", "GMLX_KQ_MMS"):
                 monkeypatch.delenv(k, raising=False)
             for k, v in env.items():
                 monkeypatch.setenv(k, v)
@@ -513,7 +515,7 @@ def test_large_fp16_activations_every_route(codec, monkeypatch):
     x = np.clip(rng.normal(0.0, 1.0, size=(M, K)) * 15000.0, -60000, 60000).astype(np.float16)
     ref = okq.qmm_ref(x, wire, codec)
     for name, env in WIDE_ROUTES:
-        for k in PATH_KNOBS + ("GMLX_KQ_MM",):
+        for k in PATH_KNOBS + ("GMLX_KQ_MM", "GMLX_KQ_MMS"):
             monkeypatch.delenv(k, raising=False)
         for k, v in env.items():
             monkeypatch.setenv(k, v)
