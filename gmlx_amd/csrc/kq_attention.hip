@@ -267,34 +267,38 @@ __device__ __forceinline__ u32x4 deq8(u32x2 q, uint32_t sb) {
     }
 }
 
-// One 32-token tile of an 8-bit affine-quantized KV cache (uint8 values,
-// token rows of D bytes; 16-bit scale and bias per 64 values of a token), in
-// the same lane layout as KVTile; values are dequantized at their use.
+// One tile of an 8-bit affine-quantized KV cache (uint8 values, token rows of
+// D bytes; a 16-bit scale and bias per 64 values of a token), in the same
+// lane layout as KVTile; values are dequantized at their use.  The tile's
+// TT x SG (token, group) scale / bias pairs are loaded once, pair p = 64 j +
+// l by lane l into slot j (one 2-byte load of each array per lane and slot,
+// where one load per value chunk made the 8-bit cache as slow as the 16-bit
+// one), and a fragment takes its pair from the owning lane (ds_bpermute).
+// Tokens past the row's end are clamped to its last token, for the values
+// and their pairs alike.
 template <int D, bool BF>
 struct KVTileQ8 {
     static constexpr int NC = D / 32;
     static constexpr int NG = (D + 127) / 128;
     static constexpr int SG = D / 64;  // scale groups per token
-    static constexpr int CH = TileTok<D>::CH, VT = TileTok<D>::VT;
+    static constexpr int TT = TileTok<D>::TT, CH = TileTok<D>::CH, VT = TileTok<D>::VT;
+    static constexpr int NP = TT * SG;         // (token, group) pairs of a tile
+    static constexpr int PJ = (NP + 63) / 64;  // pair slots per lane
     u32x2 k[CH][NC];
-    uint32_t ksb[CH][NC];  // scale | bias << 16 of the chunk's group
     u32x2 v[NG][VT];
-    uint32_t vsb[NG][VT];
+    uint32_t ksb[PJ], vsb[PJ];  // pair 64 j + lane: scale | bias << 16
+    int tlast;                  // the tile's last valid token (local index)
 
     __device__ __forceinline__ void load(const uint8_t *kp, const uint8_t *vp, const uint16_t *ks, const uint16_t *kb,
                                          const uint16_t *vs, const uint16_t *vb, int t0, int t_end) {
         const int lane = kq_lane();
         const int r = lane & 15, g = lane >> 4;
+        tlast = max(t_end - 1 - t0, 0);  // (a prefetched tile past the end: every token is the last)
 #pragma unroll
         for (int ch = 0; ch < CH; ++ch) {
             const int tok = min(t0 + 16 * ch + r, t_end - 1);
 #pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                const int d = 32 * c + 8 * g;
-                k[ch][c] = *(const u32x2 *)(kp + (int64_t)tok * D + d);
-                const int64_t si = (int64_t)tok * SG + (d >> 6);
-                ksb[ch][c] = (uint32_t)ks[si] | ((uint32_t)kb[si] << 16);
-            }
+            for (int c = 0; c < NC; ++c) k[ch][c] = *(const u32x2 *)(kp + (int64_t)tok * D + 32 * c + 8 * g);
         }
 #pragma unroll
         for (int dg = 0; dg < NG; ++dg) {
@@ -303,17 +307,39 @@ struct KVTileQ8 {
             for (int i = 0; i < VT; ++i) {
                 const int tok = min(t0 + (i < 4 ? 4 * g + i : 16 + 4 * g + (i - 4)), t_end - 1);
                 v[dg][i] = *(const u32x2 *)(vp + (int64_t)tok * D + d0);
-                const int64_t si = (int64_t)tok * SG + (d0 >> 6);
-                vsb[dg][i] = (uint32_t)vs[si] | ((uint32_t)vb[si] << 16);
             }
         }
+#pragma unroll
+        for (int j = 0; j < PJ; ++j) {
+            const int p = min(64 * j + lane, NP - 1);  // (lanes past the pairs repeat the last)
+            const int tok = min(t0 + p % TT, t_end - 1);
+            const int64_t si = (int64_t)tok * SG + p / TT;
+            ksb[j] = (uint32_t)ks[si] | ((uint32_t)kb[si] << 16);
+            vsb[j] = (uint32_t)vs[si] | ((uint32_t)vb[si] << 16);
+        }
+    }
+    // The pair of local token tl, group grp: lane (grp TT + tl) % 64 of slot
+    // (grp TT + tl) / 64; the slot is uniform over the wave at every call.
+    __device__ __forceinline__ static uint32_t pair(const uint32_t (&sb)[PJ], int tl, int grp) {
+        const int p = grp * TT + tl;
+        uint32_t w = sb[0];
+#pragma unroll
+        for (int j = 1; j < PJ; ++j)
+            if (p >= 64 * j) w = sb[j];
+        return (uint32_t)__builtin_amdgcn_ds_bpermute((p & 63) * 4, (int)w);
     }
     __device__ __forceinline__ half8_t kfrag(int ch, int c) const {
-        return __builtin_bit_cast(half8_t, deq8<BF>(k[ch][c], ksb[ch][c]));
+        const int r = kq_lane() & 15;
+        // values 32 c + 8 g .. +7 lie in group c / 2
+        return __builtin_bit_cast(half8_t, deq8<BF>(k[ch][c], pair(ksb, min(16 * ch + r, tlast), c >> 1)));
     }
     __device__ __forceinline__ void vrows(int dg, u32x4 (&out)[8]) const {
+        const int lane = kq_lane(), r = lane & 15, g = lane >> 4;
+        const int grp = min(128 * dg + 8 * r, D - 8) >> 6;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) out[i] = i < VT ? deq8<BF>(v[dg][i], vsb[dg][i]) : u32x4{0u, 0u, 0u, 0u};
+        for (int i = 0; i < 8; ++i)
+            out[i] = i < VT ? deq8<BF>(v[dg][i], pair(vsb, min(i < 4 ? 4 * g + i : 16 + 4 * g + (i - 4), tlast), grp))
+                            : u32x4{0u, 0u, 0u, 0u};
     }
 };
 
