@@ -488,8 +488,11 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
     // Staging halves a two-block slab's load instructions (one 1 KB row each
     // instead of eight 16-byte runs per block and lane); a one-block slab
     // gains nothing at 8 rows and gives up a start tile (the down slices:
-    // 16.0 against 15.4 us, measured).  Two 16-row passes spill.
-    constexpr bool kXStaged = kXSlot > 0 && SB == 2 && MR == 8;
+    // 16.0 against 15.4 us, measured).  At 16 rows (two passes through the
+    // region) it pays for Q4_K (gate|up at 9..16 rows: 16.2-17.0 against
+    // 16.9-18.8 us), not for the Q4_K + Q6_K form (q|k|v: 10.4-11.5 against
+    // 10.3-11.3 us); the Q6_K form would spill.
+    constexpr bool kXStaged = kXSlot > 0 && SB == 2 && (MR == 8 || CODEC == KQ_CODEC_Q4_K);
     // tiles issued before the first hand-off (below the staging region)
     constexpr int kStartTiles = kXStaged ? (KQ_STREAM_START_TILES < kXSlot ? KQ_STREAM_START_TILES : kXSlot)
                                          : (KQ_STREAM_START_TILES < R ? KQ_STREAM_START_TILES : R);

@@ -251,7 +251,8 @@ PATH_KNOBS = ("GMLX_KQ_STREAM", "GMLX_KQ_STREAM_WGS", "GMLX_KQ_SPLITK", "GMLX_KQ
     ("q4_k", 333, 1536, 5),        # stream: 6 blocks, 6 consumers
     ("q6_k", 200, 3072, 8),        # stream: 12 blocks, 12 consumers
     ("iq2_xxs", 150, 1536, 3),
-    ("q4_k", 2000, 2048, 16),      # stream: 16 rows, two passes of activation staging
+    ("q4_k", 2000, 2048, 16),      # stream: 16 rows, one block per consumer, activations in registers
+    ("q4_k", 700, 4096, 13),       # stream: 16-row form, two passes of activation staging
     ("q6_k", 500, 4096, 12),
     ("iq2_xxs", 300, 3072, 9),
     ("q4_k", 16, 4096, 5),         # stream: one tile (one workgroup), staged activations
