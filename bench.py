@@ -116,7 +116,7 @@ LAUNCHES = [("qkv", ("q", "k", "v")), ("o", ("o",)), ("gate_up", ("gate", "up"))
 CODEC = {name: codec for name, _, _, codec in LAYER}
 DIMS = {name: (N, K) for name, N, K, _ in LAYER}
 # kernel families, as rocprofv3 names them
-KERNEL_FAMILIES = ("kq_stream_kernel", "kq_mms_kernel", "kq_mv_kernel", "kq_qmv_persistent_kernel", "kq_mm_kernel",
+KERNEL_FAMILIES = ("kq_stream_kernel", "kq_mms_kernel", "kq_mv_kernel", "kq_mm_kernel",
                    "kq_dense_grouped_kernel")
 
 

@@ -33,11 +33,6 @@ int kq_sgather_launch(const void *x, const int32_t *x_exp, int64_t x_row_stride,
                       int32_t K, int codec, int act, float limit, float alpha, const float *b0, const float *b1,
                       int64_t b_stride, const int32_t *seg_info, const int32_t *pair_order, int32_t n_pairs,
                       int32_t n_experts, void *y, int y_dtype, int64_t y_row_stride, int32_t y_skip, hipStream_t s);
-// kq_qmv.hip: persistent small-batch launch (problems validated, all live,
-// sharing codec / x / M <= 16 / K <= 8192).
-int kq_qmv_persistent_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, int y_dtype, hipStream_t s);
-// workgroups one persistent launch of this problem's codec / K would use
-int kq_qmv_persistent_grid(const kq_matmul_problem &q);
 // kq_mm.hip: batches of 17..64 rows (problems validated, all live, Q4_K /
 // Q6_K, sharing x / M / K).
 bool kq_mms_eligible(const kq_matmul_problem *ps, int n, bool room);
@@ -705,32 +700,12 @@ int group_mt(const kq_matmul_problem *ps, int n) {
     return mt <= 1 ? 1 : mt <= 2 ? 2 : 4;
 }
 
-int env_flag(const char *name, int dflt) {
-    const char *s = getenv(name);
-    if (!s || !*s) return dflt;
-    return !(s[0] == '0' && s[1] == 0);
-}
-
 // "0" -> 0, "2" -> 2, anything else set -> 1, unset -> dflt
 int env_int_flag(const char *name, int dflt) {
     const char *s = getenv(name);
     if (!s || !*s) return dflt;
     if (s[1] == 0 && (s[0] == '0' || s[0] == '2')) return s[0] - '0';
     return 1;
-}
-
-// The persistent small-batch path (kq_qmv.hip) serves a set of problems that
-// share one codec, x, x stride, M <= 16 and K <= 8192 (Q6_K: K <= 4096).
-bool qmv_eligible(const kq_matmul_problem *ps, const int *idx, int n) {
-    if (n == 0) return false;
-    const kq_matmul_problem &q0 = ps[idx[0]];
-    if (q0.M > 16 || q0.K > (q0.codec == KQ_CODEC_Q6_K ? 4096 : 8192)) return false;
-    for (int i = 1; i < n; ++i) {
-        const kq_matmul_problem &q = ps[idx[i]];
-        if (q.x != q0.x || q.x_row_stride != q0.x_row_stride || q.M != q0.M || q.K != q0.K || q.codec != q0.codec)
-            return false;
-    }
-    return true;
 }
 
 // 16 waves per tile for one m-tile, 4 waves for wider chunks
@@ -921,6 +896,19 @@ size_t split_bytes(const kq_matmul_problem *problems, int n_problems) {
 
 }  // namespace
 
+// Compute units of the current device (cached per device id; 256 on MI355X).
+int device_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
 extern "C" {
 
 size_t kq_matmul_workspace_bytes(const kq_matmul_problem *problems, int n_problems, int x_dtype) {
@@ -1060,32 +1048,6 @@ int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problem
                                  room ? (float *)((char *)workspace + used) : nullptr, (hipStream_t)stream);
         if (env_int_flag("GMLX_KQ_MM", 1) && kq_mm_eligible(all, na, x_dtype))
             return kq_mm_launch(all, na, xe0, y_dtype, (hipStream_t)stream);
-    }
-    // small batches: one persistent launch per codec when every codec's
-    // problems share their activations (q|k|v, gate|up of one layer)
-    if (env_flag("GMLX_KQ_PERSISTENT", 1)) {
-        bool ok = live > 0;
-        for (int c = 0; c < 3 && ok; ++c)
-            if (cnt[c] && !qmv_eligible(problems, by_codec[c], cnt[c])) ok = false;
-        // persistence pays only when a workgroup walks several tiles: every
-        // codec's launch needs at least two tiles per workgroup
-        for (int c = 0; c < 3 && ok; ++c) {
-            if (!cnt[c]) continue;
-            int tiles = 0;
-            for (int i = 0; i < cnt[c]; ++i) tiles += (problems[by_codec[c][i]].N + 15) / 16;
-            if (tiles < 2 * kq_qmv_persistent_grid(problems[by_codec[c][0]])) ok = false;
-        }
-        if (ok) {
-            for (int c = 0; c < 3; ++c) {
-                if (!cnt[c]) continue;
-                kq_matmul_problem sub[KQ_MAX_GROUP];
-                for (int i = 0; i < cnt[c]; ++i) sub[i] = problems[by_codec[c][i]];
-                const int rc =
-                    kq_qmv_persistent_launch(sub, cnt[c], exps[by_codec[c][0]], y_dtype, (hipStream_t)stream);
-                if (rc != KQ_OK) return rc;
-            }
-            return KQ_OK;
-        }
     }
     DenseArgs a;
     int units = 0, max_chunks = 0, np = 0;

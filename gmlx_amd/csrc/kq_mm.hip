@@ -137,6 +137,8 @@ __device__ __forceinline__ void mm_group(KArgs A, const uint8_t *w, int64_t w_ro
             for (int i = 0; i < T; ++i) nxt[i].load(wrow[i] + (int64_t)kb_next * BPB, g);
 #pragma unroll
             for (int i = 0; i < T; ++i) cur[i].prep(g);
+            floatx4 P[T][MT];                // the super-block's chains (exact integer weights)
+            [[maybe_unused]] floatx4 Sm[MT];  // Q4_K: its activation sub-block sums
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int jq = j0 + q;
@@ -156,13 +158,33 @@ __device__ __forceinline__ void mm_group(KArgs A, const uint8_t *w, int64_t w_ro
                         const int m = 16 * mt + r;
                         xf[mt] = x8_from_bits<XT>(b[m * 8 + ((4 * u + g) ^ (m & 7))]);
                     }
+                    if constexpr (CODEC == KQ_CODEC_Q4_K) {
+                        const half8_t sel = sum_sel(r, sum_row(t, 0));
+#pragma unroll
+                        for (int mt = 0; mt < MT; ++mt)
+                            Sm[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sel, xf[mt], t == 0 ? fzero4() : Sm[mt], 0,
+                                                                            0, 0);
+                    }
 #pragma unroll
                     for (int i = 0; i < T; ++i) {
                         const half8_t bw = cur[i].frag(t, g, kIq2);
 #pragma unroll
                         for (int mt = 0; mt < MT; ++mt)
-                            acc[i][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[mt], bw, acc[i][mt], 0, 0, 0);
+                            P[i][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[mt], bw, t == 0 ? fzero4() : P[i][mt],
+                                                                              0, 0, 0);
                     }
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < T; ++i) {
+                const float f = cur[i].dscale();
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) acc[i][mt] = fold4(f, P[i][mt], acc[i][mt]);
+                if constexpr (CODEC == KQ_CODEC_Q4_K) {
+                    float b0, b1;
+                    cur[i].min_b(g, b0, b1);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) acc[i][mt] = min_accumulate(Sm[mt][0], Sm[mt][1], b0, b1, acc[i][mt]);
                 }
             }
         };

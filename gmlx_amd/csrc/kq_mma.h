@@ -10,16 +10,23 @@
 // contiguous 64-byte run.  IQ2_XXS: lane group g owns the quarter 64g .. 64g+63
 // (one 16-byte load of the block per lane) and feeds 64g + 8t .. +7.  The
 // activation fragment of a step is the 8 activations at the same value
-// indices (Block<>::x_elem).  Every weight fragment is fully scaled before the
-// MFMA (w = dequant(q) in fp16), so the accumulator needs no per-block factor.
+// indices (Block<>::x_elem).
 //
-// Dequant to fp16 in registers, per pair of values:
-//   Q4_K : q = cvt_fp8(nibble byte) exact integer, w = fma(q, dsc, -dm)
-//   Q6_K : h = perm(0x64.., 6-bit byte) (= 1024+q), w = (h - 1056) * dsc
-//   IQ2  : w = (grid ^ signmask) * db
-// each with a single rounding; dsc / dm / db are the sub-block scales rounded
-// once to fp16 (Q4_K: the fp16 product d * sc of an fp16 d and an exact
-// integer sc, the same value as rounding the exact fp32 product).
+// Exact weights.  The MFMA's B operand is an exact integer in fp16, the
+// block's integer codes times its integer sub-block scales:
+//   Q4_K : q * sc                 (q <= 15, sc <= 63: at most 945)
+//   Q6_K : (q - 32) * sc          (|.| <= 4096; exact up to 2048, beyond that
+//                                  an odd product rounds to the nearest even)
+//   IQ2  : +-grid * (2 s + 1)     (grid in {8, 25, 43}, s <= 15: at most 1333)
+// Each super-block's eight steps run as their own MFMA chain P (exact
+// products, fp32 sums), and the chain is folded into the fp32 accumulator
+// with the block's fp32 factor: acc += d * P (IQ2_XXS: d / 8).  The Q4_K
+// minimum term -dmin * m_j * sum_{l in j} x_l takes fp32 sub-block sums of
+// the activations (sub-block j of the super-block, from a 0 / 1 selection
+// MFMA, sum_sel below) against -dmin * m_j (exact in fp32) on the fp32 MFMA
+// v_mfma_f32_16x16x4_f32 (min_accumulate).  No scale is rounded to fp16, so
+// the only rounding left is fp32 accumulation (and Q6_K's even rounding of
+// products past 2048, unbiased and independent per weight).
 #pragma once
 #include "kq_common.h"
 #include "kq_tables.h"
@@ -98,14 +105,17 @@ struct Block;
 //   sub-blocks 0..3: sc = s[j] & 63,                    m = s[j+4] & 63
 //   sub-blocks 4..7: sc = s[j+4] & 15 | (s[j-4] >> 6) << 4,
 //                    m  = s[j+4] >> 4 | (s[j] >> 6) << 4
-// then turned into fp16 through the 1024-bias (exact) and multiplied by d / dmin.
-// A nibble byte q <= 15 read as fp8 E4M3 is q * 2^-9; the converter's scale 2^9
-// (a power of two, the only part of the scale it applies) returns q exactly.
+// and the scales become exact fp16 integers through the 1024-bias.  A nibble
+// byte q <= 15 read as fp8 E4M3 is q * 2^-9; the converter's scale 2^9 (a
+// power of two, the only part of the scale it applies) returns q exactly, and
+// q * sc (at most 945) is exact in fp16.
 template <>
 struct Block<KQ_CODEC_Q4_K> {
     u32x4 hdr;
     u32x2 q[4];
-    half2_t dsc[4], ndm[4];  // [i] = sub-blocks 2i, 2i+1
+    half2_t sc[4];          // [i] = integer scales of sub-blocks 2i, 2i+1
+    uint32_t mlo, mhi;      // integer mins, one byte per sub-block (0..3, 4..7)
+    float d, dmin;
 
     __device__ static constexpr int x_elem(int t, int g) { return 32 * t + 8 * g; }
     __device__ __forceinline__ void load(const uint8_t *blk, int g) {
@@ -116,19 +126,17 @@ struct Block<KQ_CODEC_Q4_K> {
     __device__ __forceinline__ void prep(int g) {
         (void)g;
         const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;  // scale bytes 0..3, 4..7, 8..11
-        const uint32_t sc_lo = s0 & 0x3F3F3F3Fu, m_lo = s1 & 0x3F3F3F3Fu;
+        const uint32_t sc_lo = s0 & 0x3F3F3F3Fu;
         const uint32_t sc_hi = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
-        const uint32_t m_hi = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
+        mlo = s1 & 0x3F3F3F3Fu;
+        mhi = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
         const half2_t k1024 = {(_Float16)1024.f, (_Float16)1024.f};
-        const half2_t dd = h2b(hdr.x);  // (d, dmin)
-        const half2_t d2 = bcast(dd.x), nm2 = bcast(-dd.y);
-        const uint32_t scw[2] = {sc_lo, sc_hi}, mw[2] = {m_lo, m_hi};
+        const uint32_t scw[2] = {sc_lo, sc_hi};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t sel = (i & 1) ? KQ_SEL_B23 : KQ_SEL_B01;
-            dsc[i] = (h2b(__builtin_amdgcn_perm(0x64646464u, scw[i >> 1], sel)) - k1024) * d2;
-            ndm[i] = (h2b(__builtin_amdgcn_perm(0x64646464u, mw[i >> 1], sel)) - k1024) * nm2;
-        }
+        for (int i = 0; i < 4; ++i)
+            sc[i] = h2b(__builtin_amdgcn_perm(0x64646464u, scw[i >> 1], (i & 1) ? KQ_SEL_B23 : KQ_SEL_B01)) - k1024;
+        d = kq_f16_bits_to_f32(hdr.x & 0xFFFFu);
+        dmin = kq_f16_bits_to_f32(hdr.x >> 16);
     }
     __device__ __forceinline__ half8_t frag(int t, int g, const Iq2Tables &) const {
         (void)g;
@@ -139,14 +147,20 @@ struct Block<KQ_CODEC_Q4_K> {
         }
         w0 &= 0x0F0F0F0Fu;
         w1 &= 0x0F0F0F0Fu;
-        const half2_t sc = bcast((t & 1) ? dsc[t >> 1].y : dsc[t >> 1].x);
-        const half2_t mn = bcast((t & 1) ? ndm[t >> 1].y : ndm[t >> 1].x);
+        const half2_t s = bcast((t & 1) ? sc[t >> 1].y : sc[t >> 1].x);
         const half2_t a0 = h2b(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 512.f, false)));
         const half2_t a1 = h2b(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 512.f, true)));
         const half2_t a2 = h2b(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 512.f, false)));
         const half2_t a3 = h2b(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 512.f, true)));
-        return cat8(__builtin_elementwise_fma(a0, sc, mn), __builtin_elementwise_fma(a1, sc, mn),
-                    __builtin_elementwise_fma(a2, sc, mn), __builtin_elementwise_fma(a3, sc, mn));
+        return cat8(a0 * s, a1 * s, a2 * s, a3 * s);
+    }
+    __device__ __forceinline__ float dscale() const { return d; }
+    // -dmin * m of sub-blocks 2g and 2g + 1 (exact in fp32): the B operand of
+    // the minimum MFMAs (min_accumulate)
+    __device__ __forceinline__ void min_b(int g, float &b0, float &b1) const {
+        const uint32_t w = (g >= 2 ? mhi : mlo) >> (16 * (g & 1));
+        b0 = -dmin * (float)(w & 0xFFu);
+        b1 = -dmin * (float)((w >> 8) & 0xFFu);
     }
 };
 
@@ -154,14 +168,16 @@ struct Block<KQ_CODEC_Q4_K> {
 // Step t: half h = t/4, quarter q = t%4 (values 128h + 32q + l, l = 0..31);
 // lane group g takes l = 8g .. 8g+7: ql bytes 64h + 32(q&1) + 8g (high
 // nibbles for q >= 2), qh bytes 32h + 8g (bits 2q, 2q+1), one int8 scale
-// sc[8h + 2q + g/2].
+// sc[8h + 2q + g/2].  The fragment is (q6 - 32) * sc (an integer of at most
+// 4096 in magnitude), times d in fp32 after the chain.
 template <>
 struct Block<KQ_CODEC_Q6_K> {
     u32x2 ql[4];  // [2h + p]
     u32x2 qh[2];  // [h]
     u32x4 sc;     // scales[16]
     uint32_t dbits;
-    half2_t dsc[8];
+    half2_t isc[8];  // the lane's int8 scale of step t, as fp16
+    float d;
 
     __device__ static constexpr int x_elem(int t, int g) { return 32 * t + 8 * g; }
     __device__ __forceinline__ void load(const uint8_t *blk, int g) {
@@ -180,7 +196,7 @@ struct Block<KQ_CODEC_Q6_K> {
         dbits = (uint32_t)*(const uint16_t *)(blk + 208);
     }
     __device__ __forceinline__ void prep(int g) {
-        const float d = kq_f16_bits_to_f32(dbits);
+        d = kq_f16_bits_to_f32(dbits);
         const int sh = 8 * (g >> 1);
         const uint32_t w[4] = {sc.x, sc.y, sc.z, sc.w};
 #pragma unroll
@@ -188,7 +204,7 @@ struct Block<KQ_CODEC_Q6_K> {
             // scale index 8h + 2q + g/2 = 2t + g/2: byte (2t + g/2) of the 16
             const int bi = 2 * t;
             const int8_t s = (int8_t)((w[bi >> 2] >> (8 * (bi & 3) + sh)) & 0xFF);
-            dsc[t] = bcast((_Float16)(d * (float)s));
+            isc[t] = bcast((_Float16)(float)s);
         }
     }
     __device__ __forceinline__ half8_t frag(int t, int g, const Iq2Tables &) const {
@@ -211,21 +227,25 @@ struct Block<KQ_CODEC_Q6_K> {
         }
         const Bias8 b(c0, c1);
         const half2_t k1056 = {(_Float16)1056.f, (_Float16)1056.f};
-        const half2_t s = dsc[t];
+        const half2_t s = isc[t];
         return cat8((b.p0 - k1056) * s, (b.p1 - k1056) * s, (b.p2 - k1056) * s, (b.p3 - k1056) * s);
     }
+    __device__ __forceinline__ float dscale() const { return d; }
 };
 
 // IQ2_XXS (66 B = d + 8 groups of 8 B: 4 grid indices, u32 signs|scale).
 // Lane group g owns groups 2g and 2g+1 (bytes 2 + 16g .. +15: one 16-B load
 // per lane) and the values 64g .. 64g+63; step t covers values 64g + 8t .. +7
 // (group 2g + t/4, grid index t%4).  The grid and sign tables are read from
-// LDS.
+// LDS.  Value = d * (0.5 + s) * 0.25 * grid * sign = (d / 8) * (2s + 1) * grid
+// * sign: the fragment is the integer (2s + 1) * grid * sign, times d / 8 in
+// fp32 after the chain.
 template <>
 struct Block<KQ_CODEC_IQ2_XXS> {
     u32x4 raw;  // index word, sign|scale word of group 2g, then of group 2g+1
     uint32_t dbits;
-    half2_t db[2];
+    half2_t os[2];  // 2 s + 1 of groups 2g, 2g + 1
+    float d8;
 
     __device__ static constexpr int x_elem(int t, int g) { return 64 * g + 8 * t; }
     __device__ __forceinline__ void load(const uint8_t *blk, int g) {
@@ -235,9 +255,9 @@ struct Block<KQ_CODEC_IQ2_XXS> {
     }
     __device__ __forceinline__ void prep(int g) {
         (void)g;
-        const float d = kq_f16_bits_to_f32(dbits);
-        db[0] = bcast((_Float16)(d * (0.5f + (float)(raw.y >> 28)) * 0.25f));
-        db[1] = bcast((_Float16)(d * (0.5f + (float)(raw.w >> 28)) * 0.25f));
+        d8 = kq_f16_bits_to_f32(dbits) * 0.125f;
+        os[0] = bcast((_Float16)(float)(2u * (raw.y >> 28) + 1u));
+        os[1] = bcast((_Float16)(float)(2u * (raw.w >> 28) + 1u));
     }
     __device__ __forceinline__ half8_t frag(int t, int g, const Iq2Tables &tab) const {
         (void)g;
@@ -247,10 +267,59 @@ struct Block<KQ_CODEC_IQ2_XXS> {
         const uint32_t s7 = (aux >> (7 * l)) & 127u;
         const u32x4 gm = *(const u32x4 *)tab.grid_h2[idx];
         const u32x4 sm = *(const u32x4 *)tab.sign_x2[s7];
-        const half2_t s = db[e];
+        const half2_t s = os[e];
         return cat8(h2b(gm.x ^ sm.x) * s, h2b(gm.y ^ sm.y) * s, h2b(gm.z ^ sm.z) * s, h2b(gm.w ^ sm.w) * s);
     }
+    __device__ __forceinline__ float dscale() const { return d8; }
 };
+
+// ---- exact-weight accumulation helpers --------------------------------------
+
+__device__ __forceinline__ floatx4 fzero4() { return floatx4{0.f, 0.f, 0.f, 0.f}; }
+
+// acc += f * p (one rounding per element)
+__device__ __forceinline__ floatx4 fold4(float f, const floatx4 &p, const floatx4 &acc) {
+    return floatx4{__builtin_fmaf(f, p[0], acc[0]), __builtin_fmaf(f, p[1], acc[1]), __builtin_fmaf(f, p[2], acc[2]),
+                   __builtin_fmaf(f, p[3], acc[3])};
+}
+
+// Activation sub-block sums by MFMA: S = mfma(sum_sel(r, row), x fragment, S)
+// with the fragment as the B operand (column = activation row of its lane)
+// and a 0 / 1 selection as A: only A-row `row` takes this step's 32 values,
+// so the lane (g, r) of the result accumulates in element e the sum of
+// activation row r over the values whose steps selected row 4g + e (exact
+// products, fp32 sums).  For the layout above (step t = sub-block t) the
+// selection row of sub-block t in super-block slot s is sum_row(t, s):
+// element e of lane (g, r) is then the sum of sub-block 2g + (e & 1) of slot
+// e >> 1, which is what min_accumulate pairs with min_b.
+__device__ __forceinline__ half8_t sum_sel(int r, int row) {
+    const _Float16 v = r == row ? (_Float16)1.f : (_Float16)0.f;
+    return half8_t{v, v, v, v, v, v, v, v};
+}
+__device__ __forceinline__ constexpr int sum_row(int t, int s) { return 4 * (t >> 1) + (t & 1) + 2 * s; }
+
+// Sub-block sums of SB super-blocks of activation fragments in the layout
+// above (xr[s][t]: step t of super-block slot s): element e of lane (g, r) =
+// sum of activation row r over sub-block 2g + (e & 1) of slot e >> 1.
+template <int SB>
+__device__ __forceinline__ floatx4 xsum_generic(const half8_t (&xr)[SB][8], int r) {
+    static_assert(SB <= 2, "one accumulator holds two super-blocks of sums");
+    floatx4 S = fzero4();
+#pragma unroll
+    for (int s = 0; s < SB; ++s)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) S = __builtin_amdgcn_mfma_f32_16x16x32_f16(sum_sel(r, sum_row(t, s)), xr[s][t], S, 0, 0, 0);
+    return S;
+}
+
+// acc += sum_j S_j * (-dmin m_j) over the 8 sub-blocks of one super-block:
+// two fp32 MFMAs with k = lane group g, A = the sums of sub-blocks 2g + i of
+// the lane's activation row (s0, s1), B = -dmin m of the same sub-blocks of
+// its weight row (b0, b1).
+__device__ __forceinline__ floatx4 min_accumulate(float s0, float s1, float b0, float b1, floatx4 acc) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(s0, b0, acc, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(s1, b1, acc, 0, 0, 0);
+}
 
 // ---- activation fragments -------------------------------------------------
 
@@ -370,14 +439,38 @@ struct Stage {
     __device__ __forceinline__ void compute(floatx4 (&acc)[NW][MT], int g, const Iq2Tables &tab) {
 #pragma unroll
         for (int i = 0; i < NW; ++i) w[i].prep(g);
+        // Q4_K: the activations' sub-block sums, once for the NW tiles
+        [[maybe_unused]] floatx4 sums[MT];
+        if constexpr (CODEC == KQ_CODEC_Q4_K) {
+            const int r = kq_lane() & 15;
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
+            for (int mt = 0; mt < MT; ++mt) sums[mt] = fzero4();
 #pragma unroll
-            for (int i = 0; i < NW; ++i) {
+            for (int t = 0; t < 8; ++t) {
+                const half8_t sel = sum_sel(r, sum_row(t, 0));
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+                    sums[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sel, x[t][mt], sums[mt], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+            floatx4 p[MT];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
                 const half8_t b = w[i].frag(t, g, tab);
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt)
-                    acc[i][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x[t][mt], b, acc[i][mt], 0, 0, 0);
+                    p[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x[t][mt], b, t == 0 ? fzero4() : p[mt], 0, 0, 0);
+            }
+            const float f = w[i].dscale();
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc[i][mt] = fold4(f, p[mt], acc[i][mt]);
+            if constexpr (CODEC == KQ_CODEC_Q4_K) {
+                float b0, b1;
+                w[i].min_b(g, b0, b1);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) acc[i][mt] = min_accumulate(sums[mt][0], sums[mt][1], b0, b1, acc[i][mt]);
             }
         }
     }

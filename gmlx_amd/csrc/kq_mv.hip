@@ -90,9 +90,12 @@ struct WB;
 // Q4_K quarter view: header (d, dmin, scales) + qs bytes 32g .. 32g+31.
 // Sub-block 2g in the low nibbles, 2g+1 in the high nibbles.  Scales and mins
 // are unpacked as bytes four at a time (sub-blocks 0..3 and 4..7), the lane's
-// two are picked with a lane-constant mask, and become fp16 through the
-// 1024-bias (exact) times d / dmin.  Nibble bytes become exact fp16 integers
-// through the fp8 converter (q <= 15 read as E4M3 is q * 2^-9, scale 2^9).
+// two are picked with a lane-constant mask and become exact fp16 integers
+// through the 1024-bias.  Nibble bytes become exact fp16 integers through the
+// fp8 converter (q <= 15 read as E4M3 is q * 2^-9, scale 2^9), and the
+// fragment is q * sc, exact.  The block's chain is folded with d in fp32 and
+// the minimum term comes from the wave's activation sub-block sums xs
+// (sub-blocks 2g, 2g + 1 of the lane's row) on the fp32 MFMA.
 template <>
 struct WB<KQ_CODEC_Q4_K> {
     u32x4 hdr, q0, q1;
@@ -103,7 +106,8 @@ struct WB<KQ_CODEC_Q4_K> {
         q1 = ld128(rs, off + 32 + 32 * g);
     }
     template <class XF>
-    __device__ __forceinline__ void mma(floatx4 &acc, const XF &xf, int g, const Iq2Tables &, bool = false) const {
+    __device__ __forceinline__ void mma(floatx4 &acc, const XF &xf, int g, const Iq2Tables &, bool,
+                                        const float (&xs)[2]) const {
         const uint32_t hmask = g >= 2 ? 0xFFFFFFFFu : 0u;
         const uint32_t ssel = (g & 1) ? KQ_SEL_B23 : KQ_SEL_B01;
         const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;
@@ -112,10 +116,10 @@ struct WB<KQ_CODEC_Q4_K> {
         const uint32_t scb = (sc_hi & hmask) | (s0 & 0x3F3F3F3Fu & ~hmask);
         const uint32_t mb = (m_hi & hmask) | (s1 & 0x3F3F3F3Fu & ~hmask);
         const half2_t k1024 = {(_Float16)1024.f, (_Float16)1024.f};
-        const half2_t dd = h2b(hdr.x);
-        const half2_t dsc = (h2b(__builtin_amdgcn_perm(0x64646464u, scb, ssel)) - k1024) * bcast(dd.x);
-        const half2_t ndm = (h2b(__builtin_amdgcn_perm(0x64646464u, mb, ssel)) - k1024) * bcast(-dd.y);
+        const half2_t sc = h2b(__builtin_amdgcn_perm(0x64646464u, scb, ssel)) - k1024;
+        const half2_t mh = h2b(__builtin_amdgcn_perm(0x64646464u, mb, ssel)) - k1024;
         const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        floatx4 P;
 #pragma unroll
         for (int tp = 0; tp < 4; ++tp) {
             const uint32_t lo0 = qw[2 * tp] & 0x0F0F0F0Fu, lo1 = qw[2 * tp + 1] & 0x0F0F0F0Fu;
@@ -123,24 +127,28 @@ struct WB<KQ_CODEC_Q4_K> {
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
                 const uint32_t w0 = e ? hi0 : lo0, w1 = e ? hi1 : lo1;
-                const half2_t sc = bcast(e ? dsc.y : dsc.x), mn = bcast(e ? ndm.y : ndm.x);
+                const half2_t s = bcast(e ? sc.y : sc.x);
                 const half2_t a0 = h2b(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 512.f, false)));
                 const half2_t a1 = h2b(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 512.f, true)));
                 const half2_t a2 = h2b(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 512.f, false)));
                 const half2_t a3 = h2b(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 512.f, true)));
-                const half8_t bf = cat8(__builtin_elementwise_fma(a0, sc, mn), __builtin_elementwise_fma(a1, sc, mn),
-                                        __builtin_elementwise_fma(a2, sc, mn), __builtin_elementwise_fma(a3, sc, mn));
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf(4 * e + tp, x_elem(4 * e + tp, g)), bf, acc, 0, 0, 0);
+                const half8_t bf = cat8(a0 * s, a1 * s, a2 * s, a3 * s);
+                P = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf(4 * e + tp, x_elem(4 * e + tp, g)), bf,
+                                                           tp == 0 && e == 0 ? fzero4() : P, 0, 0, 0);
             }
         }
+        const float dmin = kq_f16_bits_to_f32(hdr.x >> 16);
+        acc = fold4(kq_f16_bits_to_f32(hdr.x & 0xFFFFu), P, acc);
+        acc = min_accumulate(xs[0], xs[1], -dmin * (float)mh.x, -dmin * (float)mh.y, acc);
     }
 };
 
 // Q6_K half view (210 B: ql[128], qh[64], scales[16], d).  Lane group g:
 // h = g / 2, c = g % 2.  Value 128h + 32q + l (l = 16c .. 16c+15) is
 // (ql[64h + 32(q%2) + l] nibble q/2) | (qh[32h + l] bits 2q, 2q+1) << 4,
-// minus 32, times d * scales[8h + 2q + c].  Loads: the two ql runs and the qh
-// run of the lane (16 B each), the 16 scales and d.
+// minus 32, times scales[8h + 2q + c] (the fragment, an integer), times d in
+// fp32 after the chain.  Loads: the two ql runs and the qh run of the lane
+// (16 B each), the 16 scales and d.
 template <>
 struct WB<KQ_CODEC_Q6_K> {
     u32x4 qa, qb, qh, sc;
@@ -157,19 +165,20 @@ struct WB<KQ_CODEC_Q6_K> {
         dbits = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, off + 208, 0, 0);
     }
     template <class XF>
-    __device__ __forceinline__ void mma(floatx4 &acc, const XF &xf, int g, const Iq2Tables &, bool = false) const {
-        const float d = kq_f16_bits_to_f32(dbits);
+    __device__ __forceinline__ void mma(floatx4 &acc, const XF &xf, int g, const Iq2Tables &, bool = false,
+                                        const float (&)[2] = {}) const {
         // scales 8h + 2q + c: q = 0, 1 in word 2h, q = 2, 3 in word 2h + 1, byte 2(q%2) + c
         const uint32_t sw0 = g >= 2 ? sc.z : sc.x, sw1 = g >= 2 ? sc.w : sc.y;
         const uint32_t cs = 8u * (uint32_t)(g & 1);
-        half2_t dsc[4];
+        half2_t isc[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const uint32_t w = q < 2 ? sw0 : sw1;
             const int s = __builtin_amdgcn_sbfe((int)w, (int)(16u * (q & 1) + cs), 8);
-            dsc[q] = bcast((_Float16)(d * (float)s));
+            isc[q] = bcast((_Float16)(float)s);
         }
         const half2_t k1056 = {(_Float16)1056.f, (_Float16)1056.f};
+        floatx4 P;
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             const int q = t >> 1, sub = t & 1;
@@ -189,15 +198,17 @@ struct WB<KQ_CODEC_Q6_K> {
                 c1 = (l1 & 0x0F0F0F0Fu) | ((h1 >> 2) & 0x30303030u);
             }
             const Bias8 b(c0, c1);
-            const half2_t s = dsc[q];
+            const half2_t s = isc[q];
             const half8_t bf = cat8((b.p0 - k1056) * s, (b.p1 - k1056) * s, (b.p2 - k1056) * s, (b.p3 - k1056) * s);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf(t, x_elem(t, g)), bf, acc, 0, 0, 0);
+            P = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf(t, x_elem(t, g)), bf, t == 0 ? fzero4() : P, 0, 0, 0);
         }
+        acc = fold4(kq_f16_bits_to_f32(dbits), P, acc);
     }
 };
 
 // IQ2_XXS quarter view: groups 2g, 2g+1 (bytes 2 + 16g .. +15) and d; grid and
-// sign tables from LDS.
+// sign tables from LDS.  Fragment (2s + 1) * grid * sign (an integer), times
+// d / 8 in fp32 after the chain.
 template <>
 struct WB<KQ_CODEC_IQ2_XXS> {
     u32x4 raw;
@@ -208,11 +219,12 @@ struct WB<KQ_CODEC_IQ2_XXS> {
         dbits = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0);
     }
     template <class XF>
-    __device__ __forceinline__ void mma(floatx4 &acc, const XF &xf, int g, const Iq2Tables &tab, bool = false) const {
+    __device__ __forceinline__ void mma(floatx4 &acc, const XF &xf, int g, const Iq2Tables &tab, bool = false,
+                                        const float (&)[2] = {}) const {
         (void)g;
-        const float d = kq_f16_bits_to_f32(dbits);
-        const half2_t db0 = bcast((_Float16)(d * (0.5f + (float)(raw.y >> 28)) * 0.25f));
-        const half2_t db1 = bcast((_Float16)(d * (0.5f + (float)(raw.w >> 28)) * 0.25f));
+        const half2_t os0 = bcast((_Float16)(float)(2u * (raw.y >> 28) + 1u));
+        const half2_t os1 = bcast((_Float16)(float)(2u * (raw.w >> 28) + 1u));
+        floatx4 P;
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             const int e = t >> 2, l = t & 3;
@@ -221,11 +233,12 @@ struct WB<KQ_CODEC_IQ2_XXS> {
             const uint32_t s7 = (aux >> (7 * l)) & 127u;
             const u32x4 gm = *(const u32x4 *)tab.grid_h2[idx];
             const u32x4 sm = *(const u32x4 *)tab.sign_x2[s7];
-            const half2_t s = e ? db1 : db0;
+            const half2_t s = e ? os1 : os0;
             const half8_t bf =
                 cat8(h2b(gm.x ^ sm.x) * s, h2b(gm.y ^ sm.y) * s, h2b(gm.z ^ sm.z) * s, h2b(gm.w ^ sm.w) * s);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf(t, x_elem(t, g)), bf, acc, 0, 0, 0);
+            P = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf(t, x_elem(t, g)), bf, t == 0 ? fzero4() : P, 0, 0, 0);
         }
+        acc = fold4(kq_f16_bits_to_f32(dbits) * 0.125f, P, acc);
     }
 };
 
@@ -251,7 +264,8 @@ struct WB<KQ_MIX> {
         dbits = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, q6 && !dead ? off + 208 : kOut, 0, 0);
     }
     template <class XF>
-    __device__ __forceinline__ void mma(floatx4 &acc, const XF &xf, int g, const Iq2Tables &tab, bool q6) const {
+    __device__ __forceinline__ void mma(floatx4 &acc, const XF &xf, int g, const Iq2Tables &tab, bool q6,
+                                        const float (&xs)[2]) const {
         if (q6) {
             WB<KQ_CODEC_Q6_K> b;
             b.qa = v0;
@@ -259,13 +273,13 @@ struct WB<KQ_MIX> {
             b.qh = v2;
             b.sc = v3;
             b.dbits = dbits;
-            b.mma(acc, xf, g, tab);
+            b.mma(acc, xf, g, tab, true, xs);
         } else {
             WB<KQ_CODEC_Q4_K> b;
             b.hdr = v0;
             b.q0 = v1;
             b.q1 = v2;
-            b.mma(acc, xf, g, tab);
+            b.mma(acc, xf, g, tab, false, xs);
         }
     }
 };
@@ -402,6 +416,8 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(4))) vo
     const bool out_lane = lane < 4 * SL && out_m < M;
 
     const bool y_f32 = A->y_dtype == KQ_DTYPE_F32, y_bf16 = A->y_dtype == KQ_DTYPE_BF16;
+    // Q4_K: activation sub-block sums of the wave's blocks (filled below, once x is in LDS)
+    [[maybe_unused]] float xsum[NBW][2] = {};
     auto compute_tile = [&](WB<CODEC> (&b)[NBW], int k) {
         const int tile = B0 + k * G;
         store_at(tile);
@@ -413,13 +429,13 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(4))) vo
             if (kb < nb) {
                 if (XR && i == NBW - 1) {
                     auto xf = [&](int t, int) -> half8_t { return xreg[XR ? t : 0]; };
-                    b[i].mma(acc, xf, g, *tab, q6);
+                    b[i].mma(acc, xf, g, *tab, q6, xsum[i]);
                 } else {
                     // activation fragment at element e of the block: x[r][kb * 256 + e]
                     auto xf = [&](int, int e) -> half8_t {
                         return x8_from_bits<XT>(*(const LDSP(u32x4))(uintptr_t)(xr_base + (kb * KQ_QK + e) * 2));
                     };
-                    b[i].mma(acc, xf, g, *tab, q6);
+                    b[i].mma(acc, xf, g, *tab, q6, xsum[i]);
                 }
             }
         }
@@ -455,6 +471,34 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(4))) vo
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    // Q4_K: the activation sub-block sums of this wave's blocks, once per
+    // launch (the wave's blocks never change): element e of lane (g, r) of an
+    // MFMA whose selection A takes, at step t, the k values of lane group
+    // r / 4 for row r when (r & 1) == (t >= 4), row r = 4g + (r & 3) only in
+    // the first two of each four: sum of row r over sub-block 2g + e
+    if constexpr (CODEC == KQ_CODEC_Q4_K || CODEC == KQ_MIX) {
+        const _Float16 one = (_Float16)1.f, zero = (_Float16)0.f;
+#pragma unroll
+        for (int i = 0; i < NBW; ++i) {
+            const int kb = wave + WV * i;
+            floatx4 S = fzero4();
+            if (kb < nb) {  // uniform over the wave
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    const _Float16 v = (r >> 2) == g && (r & 2) == 0 && (r & 1) == (t >= 4 ? 1 : 0) ? one : zero;
+                    const half8_t sel = {v, v, v, v, v, v, v, v};
+                    const half8_t xf = (XR && i == NBW - 1)
+                                           ? xreg[XR ? t : 0]
+                                           : x8_from_bits<XT>(*(const LDSP(u32x4))(uintptr_t)(
+                                                 xr_base + (kb * KQ_QK + WB<KQ_CODEC_Q4_K>::x_elem(t, g)) * 2));
+                    S = __builtin_amdgcn_mfma_f32_16x16x32_f16(sel, xf, S, 0, 0, 0);
+                }
+                kq_mfma_drain();
+            }
+            xsum[i][0] = S[0];
+            xsum[i][1] = S[1];
+        }
+    }
     // ring step k requests tile k + DEPTH - 1 and multiplies tile k; the loop
     // runs whole rounds of DEPTH steps (steps past the last tile only issue
     // their out-of-range requests)

@@ -269,18 +269,17 @@ struct IqTables<KQ_CODEC_IQ2_XXS> {
 // becomes two biased fp16 values with one v_and_or_b32:
 //   (w & 0x000F000F) | 0x64006400 = 1024 + low nibble (exponent 10: unit 1)
 //   (w & 0x00F000F0) | 0x54005400 =   64 + high nibble (exponent 6: unit 16/16)
-// and one fma against the exact constant -1024 dsc (-64 dsc) removes the bias
-// with a single rounding: fma(1024 + q, dsc, -1024 dsc) = fp16(q dsc).  The
-// minimum term -dm_j * sum_{l in j} x_l stays out of the weights: one more
-// MFMA per K-slab adds it from per-sub-block activation sums (fp32 sums split
-// into fp16 hi + lo parts, about 22 bits) against the fp16 -dm_j.  With
-// |dsc| >= 32 (weights beyond about +-480) the constant could overflow: a
-// wave that meets such a super-block takes the two-step form (exact q, then
-// q * dsc) for it, with the same rounding.
+// and one fma against the exact constant -1024 sc (-64 sc) removes the bias:
+// fma(1024 + q, sc, -1024 sc) = q sc, an integer of at most 945, exact (sc
+// <= 63, so the constant, at most 64512, is exact as well).  The chain of a
+// super-block is folded into the accumulator with d in fp32, and the minimum
+// term -dmin m_j sum_{l in j} x_l enters through two fp32 MFMAs
+// (min_accumulate) from the per-sub-block activation sums (fp32, q4own_x).
 struct Q4Prep {
-    half2_t dsc;  // (dsc_2g, dsc_2g+1)
-    half2_t nb;   // (-1024 dsc_2g, -64 dsc_2g+1)
-    half2_t ndm;  // (-dm_2g, -dm_2g+1)
+    half2_t sc;   // (sc_2g, sc_2g+1), exact integers
+    half2_t nb;   // (-1024 sc_2g, -64 sc_2g+1)
+    float d;
+    float b0, b1; // -dmin m_2g, -dmin m_2g+1
 };
 
 // Constants of the owned view held in VGPRs: gfx9 VOP3 encodings take no
@@ -310,56 +309,42 @@ __device__ __forceinline__ Q4Prep q4own_prep(u32x4 hdr, const Q4Consts &k) {
     const uint32_t scw = (sc_hi & k.upper) | (sc_lo & ~k.upper);
     const uint32_t mw = (m_hi & k.upper) | (m_lo & ~k.upper);
     const half2_t k1024 = {(_Float16)1024.f, (_Float16)1024.f};
-    const half2_t dd = h2b(hdr.x);  // (d, dmin)
     Q4Prep p;
-    p.dsc = (h2b(__builtin_amdgcn_perm(0x64646464u, scw, k.sel)) - k1024) * bcast(dd.x);
-    p.ndm = (h2b(__builtin_amdgcn_perm(0x64646464u, mw, k.sel)) - k1024) * bcast(-dd.y);
-    p.nb = p.dsc * half2_t{(_Float16)-1024.f, (_Float16)-64.f};
+    p.sc = h2b(__builtin_amdgcn_perm(0x64646464u, scw, k.sel)) - k1024;
+    p.nb = p.sc * half2_t{(_Float16)-1024.f, (_Float16)-64.f};
+    const half2_t m = h2b(__builtin_amdgcn_perm(0x64646464u, mw, k.sel)) - k1024;
+    const float dmin = kq_f16_bits_to_f32(hdr.x >> 16);
+    p.d = kq_f16_bits_to_f32(hdr.x & 0xFFFFu);
+    p.b0 = -dmin * (float)m.x;
+    p.b1 = -dmin * (float)m.y;
     return p;
 }
 
-__device__ __forceinline__ bool q4own_big(const Q4Prep &p) {
-    return __builtin_fabsf((float)p.dsc.x) >= 32.f || __builtin_fabsf((float)p.dsc.y) >= 32.f;
-}
-
-template <bool SAFE>
 __device__ __forceinline__ half8_t q4own_frag(uint32_t w, const Q4Prep &p, const Q4Consts &k) {
     const uint32_t w8 = w >> 8;
     const half2_t l0 = h2b((w & k.lo_mask) | k.lo_bias), l1 = h2b((w8 & k.lo_mask) | k.lo_bias);
     const half2_t u0 = h2b((w & k.hi_mask) | k.hi_bias), u1 = h2b((w8 & k.hi_mask) | k.hi_bias);
-    const half2_t s0 = bcast(p.dsc.x), s1 = bcast(p.dsc.y);
-    if constexpr (SAFE) {
-        const half2_t k1024 = {(_Float16)1024.f, (_Float16)1024.f}, k64 = {(_Float16)64.f, (_Float16)64.f};
-        return cat8((l0 - k1024) * s0, (l1 - k1024) * s0, (u0 - k64) * s1, (u1 - k64) * s1);
-    } else {
-        const half2_t c0 = bcast(p.nb.x), c1 = bcast(p.nb.y);
-        return cat8(__builtin_elementwise_fma(l0, s0, c0), __builtin_elementwise_fma(l1, s0, c0),
-                    __builtin_elementwise_fma(u0, s1, c1), __builtin_elementwise_fma(u1, s1, c1));
-    }
+    const half2_t s0 = bcast(p.sc.x), s1 = bcast(p.sc.y);
+    const half2_t c0 = bcast(p.nb.x), c1 = bcast(p.nb.y);
+    return cat8(__builtin_elementwise_fma(l0, s0, c0), __builtin_elementwise_fma(l1, s0, c0),
+                __builtin_elementwise_fma(u0, s1, c1), __builtin_elementwise_fma(u1, s1, c1));
 }
 
 // Activation fragments of the owned view for super-blocks kb0 .. kb0+SB-1:
 // xr[s][t] = x[e + (0, 2, 1, 3)], x[e + 32 + (0, 2, 1, 3)] with e = 256 (kb0 + s)
-// + 64 g + 4 t, and xm = the sub-block sums (2g, 2g+1 of each super-block) as
-// fp16 (hi, lo) pairs in the k slots the minimum MFMA pairs with -dm.
+// + 64 g + 4 t, and the sub-block sums (fp32): element 2 s + i of lane (g, r)
+// = sum of activation row r over sub-block 2g + i of super-block s.
 // Input: the lane's runs c[s][2 w + a] = x[256 (kb0 + s) + 64 g + 32 a + 8 w .. +7].
 //
 // The sums come from MFMAs with the fragments as the B operand (column r =
 // batch row r) against a 0 / 1 selection A: row m = 4 g' + e of the result
 // selects sub-block 2 g' + (e & 1) of super-block e >> 1, so lane (g, r)
-// ends with sum[s][j] of its own row in element 2 s + j (exact products,
-// fp32 accumulation).
-//
-// The sums enter the MFMA as fp16 scaled by 2^-xs, xs >= 0 the same for the
-// whole wave: large enough that the wave's largest sum stays below 2^14
-// (32 activations near fp16's maximum sum past it), 0 for ordinary
-// magnitudes, so small sums keep their precision.
+// ends with the sums of its own row (exact products, fp32 accumulation).
 template <int SB>
-__device__ __forceinline__ void q4own_x(half8_t (&xr)[SB][8], half8_t &xm, int &xs, const u32x4 (&cin)[SB][8],
-                                        int lane) {
-    static_assert(SB <= 2, "the minimum MFMA holds two super-blocks of sums");
+__device__ __forceinline__ void q4own_x(half8_t (&xr)[SB][8], floatx4 &xsum, const u32x4 (&cin)[SB][8], int lane) {
+    static_assert(SB <= 2, "one accumulator holds two super-blocks of sums");
     const int g = lane >> 4, m = lane & 15;
-    floatx4 sum = {0.f, 0.f, 0.f, 0.f};
+    floatx4 sum = fzero4();
 #pragma unroll
     for (int s = 0; s < SB; ++s) {
         // selection of super-block s: element i of lane (g, m) is 1 where row
@@ -381,77 +366,54 @@ __device__ __forceinline__ void q4own_x(half8_t (&xr)[SB][8], half8_t &xm, int &
             sum = __builtin_amdgcn_mfma_f32_16x16x32_f16(sel, xr[s][t], sum, 0, 0, 0);
         }
     }
-    kq_mfma_drain();
-    float mx = fmaxf(fmaxf(fabsf(sum[0]), fabsf(sum[1])), fmaxf(fabsf(sum[2]), fabsf(sum[3])));
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-    xs = 0;
-    if (mx >= 16384.f && mx <= 3.402823466e38f) {
-        int E;
-        (void)frexpf(mx, &E);  // mx = f 2^E, f in [0.5, 1): mx 2^-(E-14) < 2^14
-        xs = E - 14;
-    }
-    _Float16 mm[8];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const float v = ldexpf(sum[e], -xs);
-        const _Float16 hi = (_Float16)v;
-        mm[2 * e] = (e >> 1) < SB ? hi : (_Float16)0.f;
-        mm[2 * e + 1] = (e >> 1) < SB ? (_Float16)(v - (float)hi) : (_Float16)0.f;
-    }
-    xm = half8_t{mm[0], mm[1], mm[2], mm[3], mm[4], mm[5], mm[6], mm[7]};
+    xsum = sum;
 }
 
 // One K-slab of a tile in the owned view: row_p points at the lane's row,
 // super-block kb0, in the slot.
 template <int SB>
 __device__ __forceinline__ void q4own_slab(floatx4 &acc, LDSP(const uint8_t) row_p, const half8_t (&xr)[SB][8],
-                                           const half8_t &xm, float xm_scale, const Q4Consts &k, int g) {
+                                           const floatx4 &xsum, const Q4Consts &k) {
     u32x4 hdr[SB], qa[SB], qb[SB];
 #pragma unroll
     for (int s = 0; s < SB; ++s) {
         hdr[s] = *(const LDSP(u32x4))(row_p + s * 144);
-        qa[s] = *(const LDSP(u32x4))(row_p + s * 144 + 16 + 32 * g);
-        qb[s] = *(const LDSP(u32x4))(row_p + s * 144 + 32 + 32 * g);
+        qa[s] = *(const LDSP(u32x4))(row_p + s * 144 + 16 + 32 * (kq_lane() >> 4));
+        qb[s] = *(const LDSP(u32x4))(row_p + s * 144 + 32 + 32 * (kq_lane() >> 4));
     }
-    _Float16 bm[8];
 #pragma unroll
     for (int s = 0; s < SB; ++s) {
         const Q4Prep p = q4own_prep(hdr[s], k);
         const uint32_t q[8] = {qa[s].x, qa[s].y, qa[s].z, qa[s].w, qb[s].x, qb[s].y, qb[s].z, qb[s].w};
-        if (__builtin_amdgcn_ballot_w64(q4own_big(p))) {
+        floatx4 P;
 #pragma unroll
-            for (int t = 0; t < 8; ++t)
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xr[s][t], q4own_frag<true>(q[t], p, k), acc, 0, 0, 0);
-        } else {
-#pragma unroll
-            for (int t = 0; t < 8; ++t)
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xr[s][t], q4own_frag<false>(q[t], p, k), acc, 0, 0, 0);
-        }
-        bm[4 * s] = bm[4 * s + 1] = p.ndm.x;
-        bm[4 * s + 2] = bm[4 * s + 3] = p.ndm.y;
+        for (int t = 0; t < 8; ++t)
+            P = __builtin_amdgcn_mfma_f32_16x16x32_f16(xr[s][t], q4own_frag(q[t], p, k), t == 0 ? fzero4() : P, 0, 0, 0);
+        acc = fold4(p.d, P, acc);
+        acc = min_accumulate(xsum[2 * s], xsum[2 * s + 1], p.b0, p.b1, acc);
     }
-#pragma unroll
-    for (int s = SB; s < 2; ++s) bm[4 * s] = bm[4 * s + 1] = bm[4 * s + 2] = bm[4 * s + 3] = (_Float16)0.f;
-    const half8_t b = {bm[0], bm[1], bm[2], bm[3], bm[4], bm[5], bm[6], bm[7]};
-    // straight-line on purpose: with a branch here (chaining into acc when
-    // xm_scale == 1) the results came out wrong on multi-round launches
-    const floatx4 mn = __builtin_amdgcn_mfma_f32_16x16x32_f16(xm, b, floatx4{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(mn[e], xm_scale, acc[e]);
 }
 
+// One K-slab of a tile in kq_mma.h's Block<> views (xsum: the slab's
+// activation sub-block sums, read by Q4_K tiles only).
 template <int CODEC, int SB>
-__device__ __forceinline__ void mma_slab(floatx4 &acc, uint32_t row_lds, const half8_t (&xr)[SB][8], int g,
-                                         const Iq2Tables &tab) {
+__device__ __forceinline__ void mma_slab(floatx4 &acc, uint32_t row_lds, const half8_t (&xr)[SB][8],
+                                         const floatx4 &xsum, int g, const Iq2Tables &tab) {
 #pragma unroll
     for (int s = 0; s < SB; ++s) {
         Block<CODEC> b;
         load_slot<CODEC>(b, row_lds + s * Geo<CODEC>::SLOT, g);
         b.prep(g);
+        floatx4 P;
 #pragma unroll
         for (int t = 0; t < 8; ++t)
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xr[s][t], b.frag(t, g, tab), acc, 0, 0, 0);
+            P = __builtin_amdgcn_mfma_f32_16x16x32_f16(xr[s][t], b.frag(t, g, tab), t == 0 ? fzero4() : P, 0, 0, 0);
+        acc = fold4(b.dscale(), P, acc);
+        if constexpr (CODEC == KQ_CODEC_Q4_K) {
+            float b0, b1;
+            b.min_b(g, b0, b1);
+            acc = min_accumulate(xsum[2 * s], xsum[2 * s + 1], b0, b1, acc);
+        }
     }
 }
 
@@ -623,8 +585,8 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
     const int c = wave - kProducers;
     const int kb0 = c * SB;
     half8_t xr[SB][8];
-    [[maybe_unused]] half8_t xm;
-    [[maybe_unused]] float xm_scale = 1.f;  // 2^xs of the owned view's sub-block sums
+    // Q4_K tiles: the slab's activation sub-block sums (fp32)
+    [[maybe_unused]] floatx4 xsum = fzero4();
     {
         const uint32_t xbytes = (uint32_t)(((int64_t)(M - 1) * A->x_stride + A->K) * 2);
         const __amdgpu_buffer_rsrc_t xs = kq_buffer(A->x, xbytes);
@@ -668,11 +630,7 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
                         }
                     }
             }
-            if constexpr (CODEC == KQ_CODEC_Q4_K) {
-                int xs2;
-                q4own_x<SB>(xr, xm, xs2, cin, lane);
-                xm_scale = ldexpf(1.f, xs2);
-            }
+            if constexpr (CODEC == KQ_CODEC_Q4_K) q4own_x<SB>(xr, xsum, cin, lane);
         } else {
             // The slab's activation fragments straight from global memory into
             // registers: lane (g, r) reads 16-byte runs of row r, rows >= M
@@ -692,9 +650,7 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
                                 u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                            xs, xrow + (uint32_t)(2 * (256 * s2 + 64 * g + 32 * a2 + 8 * w)), 0, 0));
                 __builtin_amdgcn_s_barrier();  // the loads are issued: the producers may start
-                int xs2;
-                q4own_x<SB>(xr, xm, xs2, cin, lane);
-                xm_scale = ldexpf(1.f, xs2);
+                q4own_x<SB>(xr, xsum, cin, lane);
             } else {
 #pragma unroll
                 for (int s2 = 0; s2 < SB; ++s2)
@@ -707,6 +663,8 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
             }
         }
     }
+    // a mixed launch's Q4_K tiles: the sums in the Block<> layout
+    if constexpr (CODEC == KQ_MIX) xsum = xsum_generic<SB>(xr, r);
     // owned Q4_K view: the lane's row at super-block kb0 in slot 0
     [[maybe_unused]] const Q4Consts q4k = q4own_consts(g);
     [[maybe_unused]] LDSP(const uint8_t) own_p =
@@ -762,15 +720,15 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_stream_kernel(Stream
             if constexpr (CODEC == KQ_MIX) {
                 int32_t begin;
                 if (problem_at(A, problem_of(A, tile), begin).codec == KQ_CODEC_Q6_K)
-                    mma_slab<KQ_CODEC_Q6_K, SB>(acc, slot + r * SlotGeo<KQ_CODEC_Q6_K, NB>::RC * 16 + kb0 * 224, xr, g,
-                                                iq2_tab);
+                    mma_slab<KQ_CODEC_Q6_K, SB>(acc, slot + r * SlotGeo<KQ_CODEC_Q6_K, NB>::RC * 16 + kb0 * 224, xr,
+                                                xsum, g, iq2_tab);
                 else
-                    mma_slab<KQ_CODEC_Q4_K, SB>(acc, slot + r * kMixQ4Pitch + kb0 * 144, xr, g,
+                    mma_slab<KQ_CODEC_Q4_K, SB>(acc, slot + r * kMixQ4Pitch + kb0 * 144, xr, xsum, g,
                                                 iq2_tab);
             } else if constexpr (CODEC == KQ_CODEC_Q4_K) {
-                q4own_slab<SB>(acc, own_p + (gb % R) * SLOTB, xr, xm, xm_scale, q4k, g);
+                q4own_slab<SB>(acc, own_p + (gb % R) * SLOTB, xr, xsum, q4k);
             } else {
-                mma_slab<CODEC, SB>(acc, slot + r * SlotGeo<CODEC, NB>::RC * 16 + kb0 * Geo<CODEC>::SLOT, xr, g,
+                mma_slab<CODEC, SB>(acc, slot + r * SlotGeo<CODEC, NB>::RC * 16 + kb0 * Geo<CODEC>::SLOT, xr, xsum, g,
                                     iq2_tab);
             }
             kq_mfma_drain();
@@ -1086,6 +1044,8 @@ __device__ __forceinline__ void mms_tile_stage(floatx4 (&acc)[MT], uint32_t base
     Block<CODEC> blk;
     load_slot<CODEC>(blk, wrow, g);
     blk.prep(g);
+    floatx4 P[MT];
+    [[maybe_unused]] floatx4 S[MT];  // Q4_K: the stage's activation sub-block sums
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
         if (t < 7) {
@@ -1098,8 +1058,24 @@ __device__ __forceinline__ void mms_tile_stage(floatx4 (&acc)[MT], uint32_t base
         const half8_t wf = blk.frag(t, g, iq2_tab);
 #pragma unroll
         for (int m = 0; m < MT; ++m)
-            acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, xq[t & 1][m]), wf, acc[m], 0,
-                                                             0, 0);
+            P[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, xq[t & 1][m]), wf,
+                                                          t == 0 ? fzero4() : P[m], 0, 0, 0);
+        if constexpr (CODEC == KQ_CODEC_Q4_K) {
+            const half8_t sel = sum_sel(r, sum_row(t, 0));
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+                S[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sel, __builtin_bit_cast(half8_t, xq[t & 1][m]),
+                                                              t == 0 ? fzero4() : S[m], 0, 0, 0);
+        }
+    }
+    const float f = blk.dscale();
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[m] = fold4(f, P[m], acc[m]);
+    if constexpr (CODEC == KQ_CODEC_Q4_K) {
+        float b0, b1;
+        blk.min_b(g, b0, b1);
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[m] = min_accumulate(S[m][0], S[m][1], b0, b1, acc[m]);
     }
 }
 
@@ -1612,8 +1588,7 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_sgather_kernel(SGath
     const int t0 = (c % CPB) * TS;
     constexpr int XC = CODEC;
     half8_t xr[SB][8];
-    [[maybe_unused]] half8_t xm;
-    [[maybe_unused]] float xm_scale = 1.f;
+    [[maybe_unused]] floatx4 xsum = fzero4();  // Q4_K: the slab's activation sub-block sums
     [[maybe_unused]] const Q4Consts q4k = q4own_consts(g);
     [[maybe_unused]] LDSP(const uint8_t) own_p =
         (LDSP(const uint8_t))smem + r * SlotGeo<KQ_CODEC_Q4_K, NB>::RC * 16 + kb0 * 144;
@@ -1641,9 +1616,7 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_sgather_kernel(SGath
                             *(const u32x4 *)(xrow + (256 * (kb0 + s2) + 64 * g + 32 * a2 + 8 * w) * 2);
                         ch[s2][2 * w + a2] = live ? v : zero;
                     }
-            int xs2;
-            q4own_x<SB>(xr, xm, xs2, ch, lane);
-            xm_scale = ldexpf(1.f, xs2);
+            q4own_x<SB>(xr, xsum, ch, lane);
         } else {
 #pragma unroll
             for (int s2 = 0; s2 < SB; ++s2)
@@ -1661,20 +1634,23 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_sgather_kernel(SGath
         Block<CODEC> blk;
         load_slot<CODEC>(blk, row_lds, g);
         blk.prep(g);
+        floatx4 P;
 #pragma unroll
         for (int i = 0; i < TS; ++i)
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xr[0][i], blk.frag(T0 + i, g, iq2_tab), acc, 0, 0, 0);
+            P = __builtin_amdgcn_mfma_f32_16x16x32_f16(xr[0][i], blk.frag(T0 + i, g, iq2_tab), i == 0 ? fzero4() : P,
+                                                       0, 0, 0);
+        acc = fold4(blk.dscale(), P, acc);
     };
     auto slab = [&](floatx4 &acc, int gb) {
         const uint32_t slot = ring_lds + (uint32_t)(gb % R) * SLOTB;
         const uint32_t row_lds = slot + r * SlotGeo<CODEC, NB>::RC * 16 + kb0 * Geo<CODEC>::SLOT;
         if constexpr (CODEC == KQ_CODEC_Q4_K) {
-            q4own_slab<SB>(acc, own_p + (gb % R) * SLOTB, xr, xm, xm_scale, q4k, g);
+            q4own_slab<SB>(acc, own_p + (gb % R) * SLOTB, xr, xsum, q4k);
         } else if constexpr (CPB == 2) {
             if (t0 == 0) half_slab(acc, row_lds, std::integral_constant<int, 0>{});  // uniform
             else half_slab(acc, row_lds, std::integral_constant<int, 4>{});
         } else {
-            mma_slab<CODEC, SB>(acc, row_lds, xr, g, iq2_tab);
+            mma_slab<CODEC, SB>(acc, row_lds, xr, xsum, g, iq2_tab);
         }
     };
     const int n = lane & 15, mq = lane >> 4;

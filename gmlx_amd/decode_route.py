@@ -354,10 +354,12 @@ class _Call:
 
 
 def _is_q8_cache(call) -> bool:
-    """An 8-bit group-64 quantised cache presents K / V as (wire, scales, biases)."""
+    """An 8-bit group-64 quantised cache presents K / V as (wire, scales,
+    biases); at head dim 512 it is not claimed (the reference's gate,
+    gmlx/cascade_sdpa.py:150-157), so such a call declines as 'quant-config'."""
     trio = lambda t: isinstance(t, (tuple, list)) and len(t) == 3  # noqa: E731
     return (trio(call.keys) and trio(call.values) and getattr(call.cache, "bits", None) == 8
-            and getattr(call.cache, "group_size", None) == 64)
+            and getattr(call.cache, "group_size", None) == 64 and call.queries.shape[-1] != 512)
 
 
 def _shape_call(call) -> Optional[str]:

@@ -103,15 +103,25 @@ class _Workspaces:
     rows, partial tiles) is written before it is read.  So one buffer serves
     every later call of its family on its stream; families keep their own,
     so a call of one never overwrites what a queued call of another still
-    reads."""
+    reads.
+
+    A HIP graph captured from these calls holds the buffer's address, so a
+    buffer is never freed once used: when a family's buffer must grow, the
+    old one is kept (its counters left zero by its last call) for the graphs
+    that replay it, and later calls use the new one.  A capture runs on its
+    own stream, so it gets its own buffer (allocated in the capture, from the
+    graph's pool, and zeroed by a fill kernel, not a memset)."""
 
     def __init__(self):
         self._ws = {}
+        self._retired = []
 
     def get(self, kind, device, stream_handle, nbytes):
         key = (kind, device.index, stream_handle)
         cur = self._ws.get(key)
         if cur is None or cur.numel() < nbytes:
+            if cur is not None:
+                self._retired.append(cur)
             cur = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
             self._ws[key] = cur
         return cur

@@ -242,6 +242,27 @@ def test_claim_declines(monkeypatch, case):
     assert dr.claims() == n0
 
 
+@pytest.mark.parametrize("D,want", [(512, "quant-config"), (128, "kernel")])
+def test_q8_cache_declines_at_head_dim_512(monkeypatch, capsys, D, want):
+    """An 8-bit group-64 cache is claimed at head dims other than 512 and
+    declines at 512 as the reference's gate does (gmlx/cascade_sdpa.py:150-157,
+    'and hd != 512'): the 512 call stops at the quantisation gate, the 128
+    call passes every gate and reaches the op (which rejects CPU tensors)."""
+    monkeypatch.setenv("GMLX_CASCADE_DEBUG", "1")
+    monkeypatch.setenv("GMLX_CASCADE_DEBUG_N", "1000000")
+    B, Hq, Hkv, qL, L = 4, 16, 8, 1, 1200
+    q = torch.zeros(B, Hq, qL, D, dtype=torch.float16)
+    words = torch.zeros(B, Hkv, L, D // 4, dtype=torch.int32)
+    sc = torch.zeros(B, Hkv, L, D // 64, dtype=torch.float16)
+    cache = _Cache([0, 4, 8, 2], P=1024)
+    cache.bits = 8
+    cache.group_size = 64
+    n0 = dr.claims()
+    assert dr.cascade_claim(q, (words, sc, sc), (words, sc, sc), cache, 0.088, None, None) is None
+    assert dr.claims() == n0
+    assert f"declined ({want})" in capsys.readouterr().err
+
+
 def test_route_falls_through_to_orig_on_decline():
     calls = []
 

@@ -107,7 +107,7 @@ def test_bf16_activations_and_f32_out():
     assert okq.max_rel(got32.cpu().numpy(), ref) <= TOL
 
 
-@pytest.mark.parametrize("path", [{"GMLX_KQ_STREAM": "0", "GMLX_KQ_MV": "0", "GMLX_KQ_PERSISTENT": "0"},
+@pytest.mark.parametrize("path", [{"GMLX_KQ_STREAM": "0", "GMLX_KQ_MV": "0"},
                                   {"GMLX_KQ_STREAM": "0", "GMLX_KQ_MV": "2"}, {}])
 def test_grouped_equals_separate_bitwise(path, monkeypatch):
     """q|k|v with mixed codecs in one launch == three separate launches:
@@ -175,6 +175,64 @@ def test_deterministic_split_k():
     assert okq.max_rel(outs[0].astype(np.float32), ref) <= TOL
 
 
+def test_graph_keeps_its_workspace_when_a_later_capture_grows_it():
+    """A split launch (K = 12288 at 8 rows: partial tiles and arrival
+    counters in the workspace) captured in graph A; then graph B, captured
+    on the same capture stream, needs a larger workspace of the same family,
+    which replaces the stream's buffer.  A still holds the buffer it was
+    captured with (kept alive, counters left zero), so its replays, between
+    B's replays and eager calls, equal the eager result bitwise."""
+    import torch
+    from gmlx_amd import ops
+    rng = np.random.default_rng(17)
+    w_small = _dev(quantized_weights(rng, "q6_k", 256, 12288))
+    w_big = _dev(quantized_weights(rng, "q6_k", 4096, 12288))
+    x = _dev(fp16_rows(rng, 8, 12288))
+    eager = ops.quantized_matmul(x, w_small, None, "q6_k")
+    eager_big = ops.quantized_matmul(x, w_big, None, "q6_k")
+    torch.cuda.synchronize()
+    ga, gb = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.graph(ga):
+        out_a = ops.quantized_matmul(x, w_small, None, "q6_k")
+    with torch.cuda.graph(gb):
+        out_b = ops.quantized_matmul(x, w_big, None, "q6_k")
+    torch.cuda.synchronize()
+    for _ in range(3):
+        ga.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_a, eager)
+        gb.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_b, eager_big)
+        assert torch.equal(ops.quantized_matmul(x, w_big, None, "q6_k"), eager_big)
+    ref = okq.qmm_ref(x.cpu().numpy(), w_big.cpu().numpy()[:64], "q6_k")
+    assert okq.max_rel(eager_big[:, :64].float().cpu().numpy(), ref) <= TOL
+
+
+@pytest.mark.parametrize("wgs", ["1", "3"])
+def test_stream_multi_round_wide_range_rows(wgs, monkeypatch):
+    """Q4_K streaming launches on 1 and 3 workgroups (every workgroup walks
+    many rounds of tiles through the ring) with bf16 rows of very different
+    magnitudes (per-row exponents: the sums and the minimum term at large
+    scales): every row matches the fp64 reference on its own scale."""
+    import torch
+    from gmlx_amd import ops
+    monkeypatch.setenv("GMLX_KQ_STREAM", "2")
+    monkeypatch.setenv("GMLX_KQ_STREAM_WGS", wgs)
+    rng = np.random.default_rng(23)
+    N, K, M = 1000, 4096, 6
+    wire = quantized_weights(rng, "q4_k", N, K)
+    x = rng.normal(0.0, 1.0, size=(M, K)).astype(np.float32)
+    x[0] *= 3e4
+    x[1] = np.abs(x[1]) * 5e3 + 2e3
+    x[2] *= 1e-5
+    xd = torch.from_numpy(x).to(torch.bfloat16)
+    ref = okq.qmm_ref(xd.float().numpy(), wire, "q4_k")
+    got = ops.quantized_matmul(xd.cuda(), _dev(wire), None, "q4_k", out_dtype=torch.float32).cpu().numpy()
+    for m in range(M):
+        assert okq.max_rel(got[m], ref[m]) <= TOL, (m, okq.max_rel(got[m], ref[m]))
+
+
 @pytest.mark.parametrize("nb", [1, 2, 3, 4, 5, 8, 16, 17, 48])
 def test_k_block_counts(nb):
     """Every K split shape of the 4-wave workgroup: waves with no step,
@@ -208,8 +266,7 @@ def test_module_forward():
 # producer / consumer weight-streaming kernel (M <= 16, K of 2, 4, 6, 8, 12 or
 # 16 super-blocks, or K cut into such slices: by default past 16 super-blocks,
 # GMLX_KQ_SPLITK=s slices where they divide K), the LDS-staged persistent
-# path (kq_mv), the register persistent path (kq_qmv) and the general tiled
-# path.  Small grids make every workgroup walk many tiles, with partial ring
+# path (kq_mv) and the general tiled path.  Small grids make every workgroup walk many tiles, with partial ring
 # rounds.
 SMALL_BATCH_PATHS = [
     ("default routing", {}),
@@ -225,11 +282,10 @@ SMALL_BATCH_PATHS = [
                                   "GMLX_KQ_MV_DEPTH": "2"}),
     ("mv, 5 workgroups, ring 1", {"GMLX_KQ_STREAM": "0", "GMLX_KQ_MV": "2", "GMLX_KQ_MV_WGS": "5",
                                   "GMLX_KQ_MV_DEPTH": "1"}),
-    ("persistent, 3 workgroups", {"GMLX_KQ_STREAM": "0", "GMLX_KQ_MV": "0", "GMLX_KQ_QMV_WGS": "3"}),
-    ("general", {"GMLX_KQ_STREAM": "0", "GMLX_KQ_MV": "0", "GMLX_KQ_PERSISTENT": "0"}),
+    ("general", {"GMLX_KQ_STREAM": "0", "GMLX_KQ_MV": "0"}),
 ]
 PATH_KNOBS = ("GMLX_KQ_STREAM", "GMLX_KQ_STREAM_WGS", "GMLX_KQ_SPLITK", "GMLX_KQ_MV", "GMLX_KQ_MV_WGS",
-              "GMLX_KQ_MV_DEPTH", "GMLX_KQ_QMV_WGS", "GMLX_KQ_PERSISTENT")
+              "GMLX_KQ_MV_DEPTH")
 
 
 @pytest.mark.parametrize("codec,N,K,M", [
@@ -400,10 +456,10 @@ def test_small_batch_output_dtypes(y_dtype, monkeypatch):
 
 
 @pytest.mark.parametrize("mv", ["stream", "2", "0"])
-def test_persistent_mixed_codec_group_and_determinism(mv, monkeypatch):
+def test_mixed_codec_group_and_determinism(mv, monkeypatch):
     """q|k (Q4_K) and v (Q6_K) sharing x: one small-batch launch (the
-    streaming kernel, the LDS-staged path forced, or the register persistent
-    path); repeated calls are bitwise identical."""
+    streaming kernel, the LDS-staged path forced) or the general kernel;
+    repeated calls are bitwise identical."""
     from gmlx_amd import ops
     rng = np.random.default_rng(21)
     K = 4096
@@ -417,7 +473,6 @@ def test_persistent_mixed_codec_group_and_determinism(mv, monkeypatch):
         monkeypatch.setenv("GMLX_KQ_STREAM_WGS", "4")
     else:
         monkeypatch.setenv("GMLX_KQ_STREAM", "0")
-        monkeypatch.setenv("GMLX_KQ_QMV_WGS", "4")
         monkeypatch.setenv("GMLX_KQ_MV_WGS", "4")
         monkeypatch.setenv("GMLX_KQ_MV", mv)
     outs = [ops.quantized_matmul_grouped([(x, _dev(wq), "q4_k"), (x, _dev(wk), "q4_k"), (x, _dev(wv), "q6_k")])
@@ -429,12 +484,11 @@ def test_persistent_mixed_codec_group_and_determinism(mv, monkeypatch):
         assert okq.max_rel(o.float().cpu().numpy(), okq.qmm_ref(x16, w, c)) <= TOL
 
 
-def test_stream_large_scales_take_the_two_step_form(monkeypatch):
+def test_large_scales_every_route(monkeypatch):
     """Q4_K super-blocks whose sub-block scales reach |d sc| >= 32 (weights of
-    several hundred), next to ordinary ones: a wave that meets one converts
-    that super-block in two exact steps (q, then q * dsc) instead of against
-    the -1024 dsc constant, which would overflow fp16.  Every row group
-    matches the fp64 reference on its own scale."""
+    several hundred), next to ordinary ones: the integer fragments q * sc and
+    the fp32 factors do not depend on the magnitude, so every row group
+    matches the fp64 reference on its own scale on every route."""
     import torch
     from gmlx_amd import ops
     rng = np.random.default_rng(44)
@@ -445,15 +499,20 @@ def test_stream_large_scales_take_the_two_step_form(monkeypatch):
     wire = okq.quantize(w, "q4_k")
     x = fp16_rows(rng, M, K)
     ref = okq.qmm_ref(x, wire, "q4_k")
-    monkeypatch.setenv("GMLX_KQ_STREAM", "2")
-    got = ops.quantized_matmul(_dev(x), _dev(wire), None, "q4_k", out_dtype=torch.float32).cpu().numpy()
-    for rows in ([5], list(range(40, 48)), [n for n in range(N) if n != 5 and not 40 <= n < 48]):
-        assert okq.max_rel(got[:, rows], ref[:, rows]) <= TOL, rows
+    for name, env in WIDE_ROUTES:
+        for k in PATH_KNOBS + ("GMLX_KQ_MM", "GMLX_KQ_MMS"):
+            monkeypatch.delenv(k, raising=False)
+        for k, v in env.items():
+            monkeypatch.setenv(k, v)
+        got = ops.quantized_matmul(_dev(x), _dev(wire), None, "q4_k", out_dtype=torch.float32).cpu().numpy()
+        for rows in ([5], list(range(40, 48)), [n for n in range(N) if n != 5 and not 40 <= n < 48]):
+            assert okq.max_rel(got[:, rows], ref[:, rows]) <= TOL, (name, rows)
 
 
 WIDE_ROUTES = [("default", {}), ("stream", {"GMLX_KQ_STREAM": "2"}),
-               ("dense", {"GMLX_KQ_STREAM": "0", "GMLX_KQ_MV": "0", "GMLX_KQ_PERSISTENT": "0", "GMLX_KQ_MM": "0"}),
-               ("persistent", {"GMLX_KQ_STREAM": "0", "GMLX_KQ_MV": "0", "GMLX_KQ_QMV_WGS": "2"}),
+               ("mv", {"GMLX_KQ_STREAM": "0", "GMLX_KQ_MV": "2"}),
+               ("dense", {"GMLX_KQ_STREAM": "0", "GMLX_KQ_MV": "0", "GMLX_KQ_MM": "0", "GMLX_KQ_MMS": "0"}),
+               ("mid-batch tile", {"GMLX_KQ_MMS": "0"}),
                ("mid-batch streaming", {"GMLX_KQ_MMS": "2"})]
 
 
@@ -462,9 +521,9 @@ WIDE_ROUTES = [("default", {}), ("stream", {"GMLX_KQ_STREAM": "2"}),
 def test_wide_range_activations(M, codec, monkeypatch):
     """bf16 and fp32 activation rows far outside fp16's range -- entries of a
     few 1e5, rows scaled by 1e-6 (below fp16's 2^-14 normal limit) -- through
-    every route (M 1 / 7: streaming, LDS-staged, register persistent; 24:
-    the mid-batch tile kernel and, forced, the mid-batch streaming kernel in
-    K slices; 80 and the forced route: general).  Each row enters as fp16
+    every route (M 1 / 7: streaming, LDS-staged; 24: the mid-batch tile
+    kernel and, forced, the mid-batch streaming kernel in K slices; 80 and
+    the forced route: general).  Each row enters as fp16
     with a power of two of its own and its results are scaled back in fp32,
     so every output row matches the fp64 reference on its own scale
     (narrowing straight to fp16 turned the first row to inf and the second
@@ -487,7 +546,7 @@ def test_wide_range_activations(M, codec, monkeypatch):
         xd = torch.from_numpy(x).to(dt)
         ref = okq.qmm_ref(xd.float().numpy(), wire, codec)
         for name, env in WIDE_ROUTES:
-            if name == "stream" and M > 8:
+            if name in ("stream", "mv") and M > 16:
                 continue
             for k in PATH_KNOBS + ("GMLX_KQ_MM", "GMLX_KQ_MMS"):
                 monkeypatch.delenv(k, raising=False)
@@ -500,26 +559,59 @@ def test_wide_range_activations(M, codec, monkeypatch):
                 assert err <= TOL, (name, dt, m, err)
 
 
-@pytest.mark.parametrize("codec", ["q4_k", "q6_k"])
-def test_large_fp16_activations_every_route(codec, monkeypatch):
+@pytest.mark.parametrize("codec", ["q4_k", "q6_k", "iq2_xxs"])
+@pytest.mark.parametrize("M", [4, 24])
+def test_large_fp16_activations_every_route(codec, M, monkeypatch):
     """fp16 activations of a few 1e4 (sums of 32 of them pass 65504): the
-    streaming kernel's per-sub-block activation sums (the Q4_K minimum term)
-    are scaled into range per wave; every route stays finite and within
-    tolerance.  Zero-mean rows: the fp16 sub-block scales every route uses
-    err by up to 2^-12 each, an error a strongly one-signed row (mean 2e4,
-    std 1.2e4: 2.6e-3 measured) adds up coherently over the sub-blocks."""
+    Q4_K minimum term's activation sub-block sums are fp32; every route
+    stays finite and within tolerance."""
     import torch
     from gmlx_amd import ops
     rng = np.random.default_rng(91)
-    N, K, M = 96, 2048, 4
-    wire = quantized_weights(rng, codec, N, K)
+    N, K = 96, 2048
+    if codec == "iq2_xxs":
+        wire = okq.random_valid_blocks(rng, codec, N * K // 256).reshape(N, -1)
+    else:
+        wire = quantized_weights(rng, codec, N, K)
     x = np.clip(rng.normal(0.0, 1.0, size=(M, K)) * 15000.0, -60000, 60000).astype(np.float16)
     ref = okq.qmm_ref(x, wire, codec)
     for name, env in WIDE_ROUTES:
+        if name in ("stream", "mv") and M > 16:
+            continue
         for k in PATH_KNOBS + ("GMLX_KQ_MM", "GMLX_KQ_MMS"):
             monkeypatch.delenv(k, raising=False)
         for k, v in env.items():
             monkeypatch.setenv(k, v)
         got = ops.quantized_matmul(_dev(x), _dev(wire), None, codec, out_dtype=torch.float32).cpu().numpy()
         assert np.all(np.isfinite(got)), name
+        assert okq.max_rel(got, ref) <= TOL, (name, okq.max_rel(got, ref))
+
+
+@pytest.mark.parametrize("codec", ["q4_k", "q6_k", "iq2_xxs"])
+@pytest.mark.parametrize("M", [1, 8, 16, 24, 64])
+def test_one_signed_rows_every_route(codec, M, monkeypatch):
+    """Strongly one-signed fp16 activation rows (mean 2e4, std 1.2e4): every
+    weight's error adds up coherently over such a row, so a weight that is
+    not the reference's exact value (a scale or minimum rounded to fp16)
+    shows here first.  The MFMA fragments are exact integers and the scales
+    and minima fp32, so every route stays within the north-star max-rel by
+    the reference's metric (max |err| / max |ref|, tests/test_ragged_decode.py:78-81)."""
+    import torch
+    from gmlx_amd import ops
+    rng = np.random.default_rng(1000 + M)
+    N, K = 160, 4096
+    if codec == "iq2_xxs":
+        wire = okq.random_valid_blocks(rng, codec, N * K // 256).reshape(N, -1)
+    else:
+        wire = quantized_weights(rng, codec, N, K)
+    x = np.clip(rng.normal(2e4, 1.2e4, size=(M, K)), -60000, 60000).astype(np.float16)
+    ref = okq.qmm_ref(x, wire, codec)
+    for name, env in WIDE_ROUTES:
+        if name in ("stream", "mv") and M > 16:
+            continue
+        for k in PATH_KNOBS + ("GMLX_KQ_MM", "GMLX_KQ_MMS"):
+            monkeypatch.delenv(k, raising=False)
+        for k, v in env.items():
+            monkeypatch.setenv(k, v)
+        got = ops.quantized_matmul(_dev(x), _dev(wire), None, codec, out_dtype=torch.float32).cpu().numpy()
         assert okq.max_rel(got, ref) <= TOL, (name, okq.max_rel(got, ref))
