@@ -169,6 +169,32 @@ def run_launch(ops, L, launch, x, xd):
     return [ops.quantized_matmul(xd, L["down"], None, "q6_k")]
 
 
+def spot_check_layer(torch, ops, L, x, xd, rows_per_matrix=64, seed=5):
+    """max_rel of one layer's four launches at rows_per_matrix seeded weight
+    rows of each matrix, against fp64 over the library's bit-exact
+    dequantization of the same wire rows (kq_dequantize, pinned to the GGML
+    definitions by the GPU tests)."""
+    import numpy as np
+    outs = {}
+    for launch, mats in LAUNCHES:
+        for m, y in zip(mats, run_launch(ops, L, launch, x, xd)):
+            outs[m] = y.float().cpu().numpy()
+    rng = np.random.default_rng(seed)
+    res = {}
+    for launch, mats in LAUNCHES:
+        worst = 0.0
+        for m in mats:
+            N, K = DIMS[m]
+            rows = np.sort(rng.choice(N, size=min(rows_per_matrix, N), replace=False))
+            wr = ops.dequantize(L[m][torch.from_numpy(rows).cuda()], None, CODEC[m]).double().cpu().numpy()
+            xin = (xd if K == INTER else x).double().cpu().numpy()
+            ref = xin @ wr.T
+            got = outs[m][:, rows]
+            worst = max(worst, float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30)))
+        res[launch] = worst
+    return res
+
+
 def step_fn(ops, stack, x, xd, only=None):
     """One decode step of the linear stack: 4 launches per layer (or only the
     launches named in `only`)."""
@@ -192,6 +218,8 @@ def capture(torch, fn):
 
 
 def time_graph(torch, g, steps, warmup):
+    """Mean ms per replay over `steps` back-to-back replays (one event pair
+    around the whole timed region)."""
     for _ in range(warmup):
         g.replay()
     torch.cuda.synchronize()
@@ -205,6 +233,71 @@ def time_graph(torch, g, steps, warmup):
     return e0.elapsed_time(e1) / steps  # ms per replay
 
 
+def quantiles(samples_ms):
+    """Median and p10 / p90 (ms) of per-iteration timings."""
+    import numpy as np
+    a = np.asarray(samples_ms, np.float64)
+    return {"median_ms": round(float(np.median(a)), 5), "p10_ms": round(float(np.percentile(a, 10)), 5),
+            "p90_ms": round(float(np.percentile(a, 90)), 5), "n": int(a.size)}
+
+
+def replay_samples(torch, g, n, flush=None):
+    """Per-replay timings (ms) of n replays, each bracketed by its own event
+    pair; with `flush`, a callable run before each replay outside the events
+    (a write of more than twice the 256 MB MALL, so every timed replay reads
+    its bytes from HBM)."""
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for a, b in ev:
+        if flush is not None:
+            flush()
+        a.record()
+        g.replay()
+        b.record()
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) for a, b in ev]
+
+
+def mall_flush(torch):
+    """A callable that overwrites 1 GiB of device memory (4x the MALL)."""
+    buf = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    return lambda: buf.fill_(1)
+
+
+def copy_peak(torch, nbytes=1 << 30, iters=20):
+    """On-box HBM references, medians over iters with the MALL cold (each
+    buffer is 4x the MALL): a device-to-device copy of nbytes (read + write
+    2 nbytes), the same copy as a float32 elementwise kernel, and a read-only
+    pass (sum of nbytes).  `gbs_median` is the best of them."""
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    src.fill_(1.0)
+    variants = {
+        "memcpy_d2d": (lambda: dst.copy_(src), 2 * nbytes),
+        "elementwise_copy": (lambda: torch.mul(src, 1.0, out=dst), 2 * nbytes),
+        "read_sum": (lambda: src.sum(), nbytes),
+    }
+    out = {}
+    for name, (fn, moved) in variants.items():
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(iters):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            e1.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        q = quantiles(ts)
+        out[name] = {"bytes_moved": moved, "gbs_median": round(moved / q["median_ms"] / 1e6, 1), **q}
+    del src, dst
+    torch.cuda.empty_cache()
+    best = max(v["gbs_median"] for v in out.values())
+    return {"gbs_median": best, "frac_of_8tbs": round(best / HBM_PEAK_GBS, 4), "variants": out,
+            "what": "best of a 1 GiB device copy (memcpy, elementwise) and a 1 GiB read-only sum"}
+
+
 # ---------------------------------------------------------------- attention
 
 def c3_lengths(seed=C3_LENS_SEED, B=16):
@@ -213,7 +306,24 @@ def c3_lengths(seed=C3_LENS_SEED, B=16):
     return np.exp(rng.uniform(math.log(1024), math.log(131072), B)).astype(np.int64), rng
 
 
-def bench_sdpa(torch, ops, iters=20):
+def timed_calls(torch, fn, n, flush=None):
+    """Per-call timings (ms) of n eager calls, each between its own events;
+    with `flush`, a MALL-overwriting write before each call, outside them."""
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for a, b in ev:
+        if flush is not None:
+            flush()
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) for a, b in ev]
+
+
+def bench_sdpa(torch, ops, iters=50):
     """32 q heads / 8 kv heads, D 128, B 16 ragged rows in
     per-row [Hkv, len, D] slabs (offset table), fp16, scale 1/sqrt(128)."""
     import numpy as np
@@ -226,19 +336,13 @@ def bench_sdpa(torch, ops, iters=20):
     v = torch.randn(total, generator=gen, device="cuda", dtype=torch.float32).half()
     q = torch.from_numpy(rng.normal(0, 1, size=(B, Hq, D)).astype(np.float16)).cuda()
     scale = 1.0 / math.sqrt(D)
-    run = lambda: ops.sdpa_decode_slabs(q, k, v, offs.tolist(), lens.tolist(), Hkv, scale)  # noqa: E731
+    offl, lenl = offs.tolist(), lens.tolist()
+    run = lambda: ops.sdpa_decode_slabs(q, k, v, offl, lenl, Hkv, scale)  # noqa: E731
     out = run()
     torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    for _ in range(3):
-        run()
-    e0.record()
-    for _ in range(iters):
-        run()
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / iters
+    # 2.0 GB of KV per call: every call streams from HBM (8x the MALL)
+    qs16 = quantiles(timed_calls(torch, run, iters))
+    ms = qs16["median_ms"]
     kv_bytes = 2 * total * 2
     qo_bytes = 2 * B * Hq * D * 2
     # spot-check two heads of the shortest and longest rows against fp64
@@ -268,18 +372,12 @@ def bench_sdpa(torch, ops, iters=20):
         scs += [sc_.view(-1), bi_.view(-1)]
         del g
     del k, v
-    run8 = lambda: ops.sdpa_decode_slabs(q, kq8[0], vq8[0], offs.tolist(), lens.tolist(), Hkv, scale,  # noqa: E731
+    run8 = lambda: ops.sdpa_decode_slabs(q, kq8[0], vq8[0], offl, lenl, Hkv, scale,  # noqa: E731
                                          k_scales=scs[0], k_biases=scs[1], v_scales=scs[2], v_biases=scs[3])
-    for _ in range(3):
-        run8()
-    e0.record()
-    for _ in range(iters):
-        run8()
-    e1.record()
-    torch.cuda.synchronize()
-    ms8 = e0.elapsed_time(e1) / iters
+    qs8 = quantiles(timed_calls(torch, run8, iters))
+    ms8 = qs8["median_ms"]
     q8_bytes = 2 * total + 2 * (total // 64) * 4  # values + fp16 scale and bias per 64
-    q8 = {"ms": round(ms8, 4), "kv_gbs": round(q8_bytes / ms8 / 1e6, 1),
+    q8 = {"ms": round(ms8, 4), "timing": qs8, "kv_gbs": round(q8_bytes / ms8 / 1e6, 1),
           "frac_hbm": round(q8_bytes / ms8 / 1e6 / HBM_PEAK_GBS, 4),
           "kv_tokens_per_s": round(int(lens.sum()) / ms8 * 1e3, 1), "kv_bytes": q8_bytes}
     del kq8, vq8, scs
@@ -288,6 +386,7 @@ def bench_sdpa(torch, ops, iters=20):
         "workload": "C3 ragged GQA decode, 32q/8kv heads, D=128, B=16, lens log-uniform 1k..128k (seed 0), fp16",
         "kv_tokens": int(lens.sum()),
         "ms": round(ms, 4),
+        "timing": qs16,
         "kv_gbs": round(kv_bytes / ms / 1e6, 1),
         "frac_hbm": round(kv_bytes / ms / 1e6 / HBM_PEAK_GBS, 4),
         "kv_tokens_per_s": round(int(lens.sum()) / ms * 1e3, 1),
@@ -297,14 +396,15 @@ def bench_sdpa(torch, ops, iters=20):
     }
 
 
-def bench_cascade(torch, ops, iters=30):
+def bench_cascade(torch, ops, iters=50):
     """Cascade shared-prefix decode (kq.sdpa_decode_gqa_cascade, the claim of
     gmlx/cascade_sdpa.py:136-260): B = 8 sequences share a P = 16384-token
     prefix, then 512 private tokens each after ragged left pads; qL 1,
     32 q / 8 kv heads, D 128, fp16.  Timed beside the ragged kernel over the
     same left-padded buffer (what runs without the stamp).  GB/s counts the
     bytes the cascade must read: the prefix once plus every row's private
-    keys and values."""
+    keys and values.  Each timed call follows a 1 GiB write (4x the MALL),
+    so both kernels read their bytes from HBM; medians over `iters` calls."""
     import numpy as np
     B, Hq, Hkv, D, P, sp = 8, 32, 8, 128, 16384, 512
     pads = [0, 64, 128, 32, 5, 0, 17, 3]
@@ -324,21 +424,11 @@ def bench_cascade(torch, ops, iters=30):
         q, kb[0:1, :, l0:l0 + P], vb[0:1, :, l0:l0 + P], kb[:, :, c0:], vb[:, :, c0:], scale, starts=starts)
     rag = lambda: ops.ragged_decode_attention(q, kb, vb, pads, scale)  # noqa: E731
 
-    def timed(fn):
-        for _ in range(3):
-            fn()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(iters):
-            fn()
-        e1.record()
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / iters
-
+    flush = mall_flush(torch)
     out = casc()
-    ms_c = timed(casc)
-    ms_r = timed(rag)
+    qc = quantiles(timed_calls(torch, casc, iters, flush))
+    qr = quantiles(timed_calls(torch, rag, iters, flush))
+    ms_c, ms_r = qc["median_ms"], qr["median_ms"]
     tok_bytes = Hkv * D * 2 * 2
     need = P * tok_bytes + sum(L - c0 - int(s) for s in starts.tolist()) * tok_bytes
     # spot-check two (row, head) pairs against fp64 over the row's keys
@@ -357,10 +447,13 @@ def bench_cascade(torch, ops, iters=30):
         "workload": "cascade: B=8 sequences sharing a 16384-token prefix + 512 private tokens (pads 0..128), "
                     "qL 1, 32q/8kv heads, D=128, fp16",
         "ms": round(ms_c, 4),
+        "timing": qc,
+        "mall": "1 GiB write before every timed call (cold MALL for both kernels)",
         "gbs": round(need / ms_c / 1e6, 1),
         "frac_hbm": round(need / ms_c / 1e6 / HBM_PEAK_GBS, 4),
         "bytes_read_once": need,
         "ragged_same_buffer_ms": round(ms_r, 4),
+        "ragged_timing": qr,
         "speedup_vs_ragged": round(ms_r / ms_c, 2),
         "max_rel_spot": chk,
     }
@@ -376,7 +469,7 @@ MOE_CONFIGS = {
 BLOCK_BYTES = {"q4_k": 144, "q6_k": 210, "iq2_xxs": 66}
 
 
-def bench_moe(torch, ops, which, iters=20):
+def bench_moe(torch, ops, which, iters=50):
     """BASELINE configs 4 and 5: one MoE decode layer (router top-k, fused
     gate|up GLU gather, down gather with the routing mix folded in) over
     the tokens' ragged per-expert segments.  Router logits and x are numpy
@@ -385,8 +478,8 @@ def bench_moe(torch, ops, which, iters=20):
     the experts the router touches for C5 (the others hold zero blocks and
     are never read).  C4 rotates two copies of the expert stacks (783 MB,
     > 2x the 256 MB MALL); C5's touched experts alone exceed it.  After
-    timing, four tokens' outputs are checked against the fp64 oracle over
-    the same wire bytes."""
+    timing, four tokens' outputs are checked against fp64 over the library's
+    bit-exact dequantization of the same wire bytes."""
     import numpy as np
     E, H, I, topk, T, cgu, cd = MOE_CONFIGS[which]
     rng = np.random.default_rng(0)
@@ -421,6 +514,7 @@ def bench_moe(torch, ops, which, iters=20):
 
     g, outs = capture(torch, lambda: [step(*st) for st in sets])
     ms = time_graph(torch, g, iters, 3) / copies
+    qm = quantiles([t / copies for t in replay_samples(torch, g, iters)])
     del g
     idx, sc = ops.moe_router_topk(logits, topk, shared_gate=False)
     uniq = int(torch.unique(idx).numel())
@@ -428,8 +522,6 @@ def bench_moe(torch, ops, which, iters=20):
     act_bytes = T * H * 2 + 2 * T * topk * I * 4 + T * topk * H * 4 * 2 + T * H * 4
     byts = uniq * per_expert + act_bytes
     # spot check: tokens 0, 1, T/2, T-1 of the first copy against fp64
-    from oracle import kquant as okq
-    from oracle import moe as omoe
     y = outs[0].cpu().numpy()
     ids, w = idx.cpu().numpy(), sc.cpu().numpy().astype(np.float64)
     xf = x.cpu().numpy().astype(np.float64)
@@ -440,17 +532,18 @@ def bench_moe(torch, ops, which, iters=20):
         ref = np.zeros(H)
         for s_, e in enumerate(ids[t]):
             if e not in deq:
-                deq[e] = tuple(okq.dequantize(m[e].cpu().numpy(), c).astype(np.float64)
+                deq[e] = tuple(ops.dequantize(m[e], None, c).double().cpu().numpy()
                                for m, c in ((gs, cgu), (us, cgu), (ds, cd)))
             G, U, Dn = deq[e]
-            ref += w[t, s_] * (Dn @ omoe.glu(G @ xf[t], U @ xf[t], "silu"))
-        worst = max(worst, okq.max_rel(y[t], ref))
+            gv, uv = G @ xf[t], U @ xf[t]
+            ref += w[t, s_] * (Dn @ (gv / (1.0 + np.exp(-gv)) * uv))
+        worst = max(worst, float(np.abs(y[t] - ref).max() / max(np.abs(ref).max(), 1e-30)))
     del sets, outs
     torch.cuda.empty_cache()
     return {
         "workload": f"{which} MoE decode layer: {E} experts, hidden {H}, expert intermediate {I}, top-{topk}, "
                     f"{T} tokens, gate/up {cgu}, down {cd}",
-        "unique_experts": uniq, "ms": round(ms, 4), "algorithmic_bytes": byts,
+        "unique_experts": uniq, "ms": round(ms, 4), "timing_per_layer": qm, "algorithmic_bytes": byts,
         "gbs": round(byts / ms / 1e6, 1), "frac_hbm": round(byts / ms / 1e6 / HBM_PEAK_GBS, 4),
         "tokens_per_s": round(T / ms * 1e3, 1), "max_rel_spot": worst,
     }
@@ -498,8 +591,8 @@ def cpu_baseline(layer_wires, B, budget_s=12.0, numpy_budget_s=8.0):
             break
     gbs = done * layer_bytes(B) / el / 1e9
     # numpy dequant + BLAS, one matrix at a time, smallest first, until the
-    # budget (at least one matrix; the vectorised dequantization runs near
-    # 1 MB/s of wire, so a whole layer would take minutes)
+    # budget (at least one matrix: the numpy path covers only part of a layer
+    # within the budget)
     deq = {"q4_k": okq.dequant_q4_k_np, "q6_k": okq.dequant_q6_k_np, "iq2_xxs": okq.dequant_iq2_xxs_np}
     order = sorted(layer, key=lambda m: m[0].nbytes)
     nbytes, mats, t1 = 0, 0, time.perf_counter()
@@ -597,7 +690,7 @@ def measure_traffic(batch, timeout=240):
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--batch", type=int, default=8)
     ap.add_argument("--layers", type=int, default=LAYERS)
@@ -649,8 +742,15 @@ def main():
     step_bytes = args.layers * layer_bytes(B)
     value = step_bytes / ms / 1e6
     launches = 4 * args.layers
-    log(f"[bench] B={B}: {ms:.3f} ms/step, {value:.1f} GB/s")
+    # per-replay distribution (outside the contract's timed region)
+    step_q = quantiles(replay_samples(torch, g, max(50, args.steps)))
+    log(f"[bench] B={B}: {ms:.3f} ms/step, {value:.1f} GB/s (replays: median {step_q['median_ms']:.3f}, "
+        f"p10 {step_q['p10_ms']:.3f}, p90 {step_q['p90_ms']:.3f} ms)")
     del g
+    spot = spot_check_layer(torch, ops, stack[0], x, xd)
+    log(f"[bench] max_rel_spot per launch (layer 0 vs fp64): {spot}")
+    copyp = copy_peak(torch)
+    log(f"[bench] copy peak: {copyp['gbs_median']} GB/s ({copyp['frac_of_8tbs']} of 8 TB/s)")
 
     # per-kernel launch durations: each kernel's launches of the step, alone
     # in a graph, timed with HIP events on the replay stream
@@ -676,7 +776,8 @@ def main():
         msl = time_graph(torch, gl, args.steps, args.warmup)
         byts = args.layers * launch_bytes(launch, B)
         per_launch[launch] = {"kernel": kernel_of(launch, B), "avg_us": round(msl * 1e3 / args.layers, 3),
-                              "bytes": launch_bytes(launch, B), "gbs": round(byts / msl / 1e6, 1)}
+                              "bytes": launch_bytes(launch, B), "gbs": round(byts / msl / 1e6, 1),
+                              "max_rel_spot": spot[launch]}
         log(f"[bench]   {launch}: {msl * 1e3 / args.layers:.2f} us, {byts / msl / 1e6:.1f} GB/s")
         del gl
 
@@ -685,9 +786,11 @@ def main():
         for b in (1, 2, 4, 8, 16, 32, 64):
             xb, xdb = make_inputs(torch, rng, b)
             gb, _ = capture(torch, lambda: step_fn(ops, stack, xb, xdb))
-            msb = time_graph(torch, gb, max(5, args.steps // 2), 2)
+            time_graph(torch, gb, 3, 2)
+            qb = quantiles(replay_samples(torch, gb, 50))
+            msb = qb["median_ms"]
             gbs = args.layers * layer_bytes(b) / msb / 1e6
-            per_batch[str(b)] = {"ms_per_step": round(msb, 4), "gbs": round(gbs, 1),
+            per_batch[str(b)] = {"ms_per_step": round(msb, 4), "timing": qb, "gbs": round(gbs, 1),
                                  "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
                                  "tflops": round(2 * b * args.layers * sum(N * K for _, N, K, _ in LAYER)
                                                  / msb / 1e9, 2)}
@@ -735,6 +838,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 4),
+        "step_replays": step_q,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -750,6 +854,7 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": tr,
                      "algorithmic_bytes_per_launch": dk["bytes_per_launch"],
                      "avg_launch_us": dk["avg_launch_us"]},
+        "copy_peak": copyp,
         "kernels": per_kernel,
         "launches": per_launch,
         "traffic_per_launch": traffic,

@@ -894,10 +894,16 @@ bool stream_k_ok(int K) {
 // every activation byte from HBM / L2 once per CU and unit.  Unsplit launches
 // store the results; split ones write the unit's partial tile, and the last
 // of a tile's S arrivals sums the S partials in slice order (deterministic)
-// and stores.  The weight views are kq_mma.h's Block<> (the minimum folded
-// into the weights), the activation fragments x[32 t + 8 g .. +7] of rows
-// 16 m + r.  The Q4_K + Q6_K form (q|k|v) lays each stage out for the larger
-// Q6_K rows and picks the codec per unit.
+// and stores.  The weight views are kq_mma.h's Block<> (exact integer
+// fragments, the block's chain folded in with d), the activation fragments
+// x[32 t + 8 g .. +7] of rows 16 m + r.  The Q4_K minimum term needs the
+// stage's activation sub-block sums: producer wave p (p < MT) computes those
+// of 16-row block p from the stage in LDS (eight selection MFMAs; the
+// producers are otherwise idle between copies) into one of two LDS buffers
+// (stage parity), and the consumers add -dmin m_j S_j of stage b on the fp32
+// MFMA after the next barrier they pass anyway (stage b + 1's); the last
+// stage of a unit takes one extra barrier before the unit's results leave.  The Q4_K + Q6_K form (q|k|v)
+// lays each stage out for the larger Q6_K rows and picks the codec per unit.
 constexpr int kMmsProducers = 4;
 constexpr int kMmsTiles = 6;  // tiles per group: consumers
 constexpr int kMmsMaxSplit = 16;
@@ -914,6 +920,10 @@ struct MmsGeo {
     static constexpr int PL = (XL + WL + kMmsProducers - 1) / kMmsProducers;     // loads per producer
     static constexpr int XB = MT * 16 * 512;                                      // activation bytes per stage
     static constexpr int SB = XB + WL * 1024;                                     // stage bytes
+    // Q4_K forms: the stage's activation sub-block sums, float2 per lane per
+    // 16-row block (sub-blocks 2g, 2g + 1 of the lane's row), after the ring
+    static constexpr bool SUMS = CODEC != KQ_CODEC_Q6_K;
+    static constexpr int SUMB = SUMS ? 2 * MT * 64 * 8 : 0;  // two stages (parity)
 };
 
 // Unit u of a launch: problem pi, its tiles t0 .. t0 + nt - 1 (global tile
@@ -1029,11 +1039,15 @@ __device__ __forceinline__ void mms_copy(KArgs A, int j, int wave, int lane, int
     }
 }
 
-// One stage of one tile: acc[m] += x rows 16 m .. 16 m + 15 (super-block of
-// the stage) . weight rows of the tile (at wrow, RCW chunks apart).
+// One stage of one tile: the chains P[m] = x rows 16 m .. 16 m + 15
+// (super-block of the stage) . the tile's integer weight fragments (rows at
+// wrow, RCW chunks apart), the block's factor d and, for Q4_K, the minimum
+// term's B operand (-dmin m of sub-blocks 2g, 2g + 1) in b0, b1.  The caller
+// folds them into its accumulators after the next barrier, when the chains
+// have long completed.
 template <int CODEC, int MT>
-__device__ __forceinline__ void mms_tile_stage(floatx4 (&acc)[MT], uint32_t base, uint32_t wrow, int r, int g,
-                                               const Iq2Tables &iq2_tab) {
+__device__ __forceinline__ void mms_tile_stage(floatx4 (&P)[MT], uint32_t base, uint32_t wrow, int r, int g,
+                                               const Iq2Tables &iq2_tab, float &d, float &b0, float &b1) {
     // activation fragments one step ahead of their MFMAs (the reads of step
     // t + 1 in flight while step t multiplies)
     const uint32_t xrow = base + (uint32_t)(r * 512);
@@ -1044,8 +1058,6 @@ __device__ __forceinline__ void mms_tile_stage(floatx4 (&acc)[MT], uint32_t base
     Block<CODEC> blk;
     load_slot<CODEC>(blk, wrow, g);
     blk.prep(g);
-    floatx4 P[MT];
-    [[maybe_unused]] floatx4 S[MT];  // Q4_K: the stage's activation sub-block sums
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
         if (t < 7) {
@@ -1060,23 +1072,25 @@ __device__ __forceinline__ void mms_tile_stage(floatx4 (&acc)[MT], uint32_t base
         for (int m = 0; m < MT; ++m)
             P[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, xq[t & 1][m]), wf,
                                                           t == 0 ? fzero4() : P[m], 0, 0, 0);
-        if constexpr (CODEC == KQ_CODEC_Q4_K) {
-            const half8_t sel = sum_sel(r, sum_row(t, 0));
-#pragma unroll
-            for (int m = 0; m < MT; ++m)
-                S[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sel, __builtin_bit_cast(half8_t, xq[t & 1][m]),
-                                                              t == 0 ? fzero4() : S[m], 0, 0, 0);
-        }
     }
-    const float f = blk.dscale();
+    d = blk.dscale();
+    if constexpr (CODEC == KQ_CODEC_Q4_K) blk.min_b(g, b0, b1);
+}
+
+// Producer side of the Q4_K minimum term: the sub-block sums of 16-row
+// activation block m of the stage at `base` (Block<Q4_K> layout), as float2
+// per lane at `dst` (element e of lane (g, r): sub-block 2g + e of row r).
+__device__ __forceinline__ void mms_stage_sums(uint32_t base, int m, float2 *dst, int r, int g) {
+    const uint32_t xrow = base + (uint32_t)(r * 512 + m * 8192);
+    floatx4 S = fzero4();
 #pragma unroll
-    for (int m = 0; m < MT; ++m) acc[m] = fold4(f, P[m], acc[m]);
-    if constexpr (CODEC == KQ_CODEC_Q4_K) {
-        float b0, b1;
-        blk.min_b(g, b0, b1);
-#pragma unroll
-        for (int m = 0; m < MT; ++m) acc[m] = min_accumulate(S[m][0], S[m][1], b0, b1, acc[m]);
+    for (int t = 0; t < 8; ++t) {
+        const half8_t xf = __builtin_bit_cast(
+            half8_t, lds128(xrow + (uint32_t)(16 * ((Block<KQ_CODEC_Q4_K>::x_elem(t, g) / 8) ^ r))));
+        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(sum_sel(r, sum_row(t, 0)), xf, S, 0, 0, 0);
     }
+    kq_mfma_drain();
+    dst[kq_lane()] = float2{S[0], S[1]};
 }
 
 template <int CODEC, int MT, int C, int R>
@@ -1107,6 +1121,14 @@ __global__ __launch_bounds__(64 * (kMmsProducers + C)) void kq_mms_kernel(Stream
         uint32_t off[PL];  // per-lane offsets of the producer's loads (weights: for the current unit)
         StreamProblem prob;  // set by the first unit's set-up
         MmsCursor cur{(int)blockIdx.x - G, 0, 0, 0};
+        // the consumers' unit walk (the extra barrier after each unit's last stage)
+        [[maybe_unused]] int su = (int)blockIdx.x, unit_left = 0;
+        if constexpr (MG::SUMS) {
+            if (su < U) {
+                const MmsUnit w = mms_unit(A, C, ngroups, nb, su);
+                unit_left = w.kb1 - w.kb0;
+            }
+        }
         const int pre = min(R, stages);
         for (int j = 0; j < pre; ++j)
             mms_copy<CODEC, MT, C, R>(A, j, wave, lane, M, ngroups, nb, ring, xbytes, off, prob, cur);
@@ -1116,6 +1138,25 @@ __global__ __launch_bounds__(64 * (kMmsProducers + C)) void kq_mms_kernel(Stream
             __builtin_amdgcn_s_barrier();  // stage b to the consumers; stage b - 1 back
             if (b >= 1 && b + R - 1 < stages)
                 mms_copy<CODEC, MT, C, R>(A, b + R - 1, wave, lane, M, ngroups, nb, ring, xbytes, off, prob, cur);
+            if constexpr (MG::SUMS) {
+                // the stage's activation sub-block sums (every stage of a
+                // mixed launch: its codec is known to the consumers only),
+                // read by the consumers after the next barrier
+                if (wave < MT) {
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+                    mms_stage_sums(ring + (uint32_t)(b % R) * MG::SB, wave,
+                                   (float2 *)(smem + R * MG::SB) + ((b & 1) * MT + wave) * 64, r, g);
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+                }
+                if (--unit_left == 0) {
+                    __builtin_amdgcn_s_barrier();  // the last stage's sums of the consumers' unit
+                    su += G;
+                    if (su < U) {
+                        const MmsUnit w = mms_unit(A, C, ngroups, nb, su);
+                        unit_left = w.kb1 - w.kb0;
+                    }
+                }
+            }
         }
         return;
     }
@@ -1140,22 +1181,54 @@ __global__ __launch_bounds__(64 * (kMmsProducers + C)) void kq_mms_kernel(Stream
         floatx4 acc[MT];
 #pragma unroll
         for (int m = 0; m < MT; ++m) acc[m] = floatx4{0, 0, 0, 0};
+        // The previous stage's chains, folded in after the next barrier (the
+        // MFMAs have completed by then); Q4_K: its minimum term too, whose
+        // sums the producers wrote during that stage
+        floatx4 P[MT];
+        float pd = 0.f;
+        [[maybe_unused]] float pb0 = 0.f, pb1 = 0.f;
+        bool pending = false;
+        [[maybe_unused]] bool pmin = false;
+        auto fold_prev = [&](int stage) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m) acc[m] = fold4(pd, P[m], acc[m]);
+            if constexpr (MG::SUMS) {
+                if (pmin) {
+                    const float2 *sums = (const float2 *)(smem + R * MG::SB) + (stage & 1) * MT * 64;
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) {
+                        const float2 sv = sums[m * 64 + lane];
+                        acc[m] = min_accumulate(sv.x, sv.y, pb0, pb1, acc[m]);
+                    }
+                }
+            }
+        };
         for (int kb = w.kb0; kb < w.kb1; ++kb, ++j) {
-            __builtin_amdgcn_s_barrier();  // stage j has landed
+            __builtin_amdgcn_s_barrier();  // stage j has landed (and stage j - 1's sums)
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+            if (pending) fold_prev(j - 1);
             const uint32_t base = ring + (uint32_t)(j % R) * MG::SB;
             if (c < w.nt) {
                 const uint32_t wrow = base + MG::XB + (uint32_t)(c * 16 + r) * pitch;
                 if constexpr (CODEC == KQ_MIX) {
-                    if (q6) mms_tile_stage<KQ_CODEC_Q6_K, MT>(acc, base, wrow, r, g, iq2_tab);
-                    else mms_tile_stage<KQ_CODEC_Q4_K, MT>(acc, base, wrow, r, g, iq2_tab);
+                    if (q6) mms_tile_stage<KQ_CODEC_Q6_K, MT>(P, base, wrow, r, g, iq2_tab, pd, pb0, pb1);
+                    else mms_tile_stage<KQ_CODEC_Q4_K, MT>(P, base, wrow, r, g, iq2_tab, pd, pb0, pb1);
                 } else {
-                    mms_tile_stage<CODEC, MT>(acc, base, wrow, r, g, iq2_tab);
+                    mms_tile_stage<CODEC, MT>(P, base, wrow, r, g, iq2_tab, pd, pb0, pb1);
                 }
                 kq_mfma_drain();
             }
+            pending = c < w.nt;
+            pmin = pending && !q6;
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // stage reads done
         }
+        if constexpr (MG::SUMS) {
+            __builtin_amdgcn_s_barrier();  // the unit's last sums
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        }
+        if (pending) fold_prev(j - 1);
+        kq_mfma_drain();
+        if constexpr (MG::SUMS) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         if (c >= w.nt) continue;
         const int tile = w.t0 + c;
         const int nn = (tile - begin) * 16 + r;
@@ -1243,10 +1316,10 @@ template <int CODEC, int MT, int C>
 int launch_mms(const StreamArgs &a, int grid, hipStream_t s) {
     using MG = MmsGeo<CODEC, MT, C>;
     constexpr size_t budget = 160 * 1024;
-    constexpr int R0 = budget / MG::SB > 4 ? 4 : (int)(budget / MG::SB);
+    constexpr int R0 = (budget - MG::SUMB) / MG::SB > 4 ? 4 : (int)((budget - MG::SUMB) / MG::SB);
     constexpr int R = MG::PL * (R0 - 1) <= 63 ? R0 : 63 / MG::PL + 1;
     static_assert(R >= 2, "mid-batch stream kernel LDS");
-    constexpr size_t lds = (size_t)R * MG::SB;
+    constexpr size_t lds = (size_t)R * MG::SB + MG::SUMB;
     static bool raised = false;
     if (!raised) {
         if (hipFuncSetAttribute((const void *)kq_mms_kernel<CODEC, MT, C, R>,
