@@ -781,6 +781,25 @@ def main():
         log(f"[bench]   {launch}: {msl * 1e3 / args.layers:.2f} us, {byts / msl / 1e6:.1f} GB/s")
         del gl
 
+    # the fused MLP (kq_fused_mlp: gmlx's _FusedMLP, gate|up -> SwiGLU -> down
+    # in one launch, down reading the h it produced) against the two split
+    # launches on independent inputs, 36 layers each, graph replay
+    mlp = None
+    if B <= 8:
+        def split_mlp():
+            return step_fn(ops, stack, x, xd, only={"gate_up", "down"})
+
+        def fused_mlp():
+            return [ops.fused_mlp(x, L["gate"], L["up"], L["down"], "q4_k", "q6_k") for L in stack]
+        mlp = {}
+        for name, fn in (("split_us", split_mlp), ("fused_us", fused_mlp)):
+            gm, _ = capture(torch, fn)
+            mlp[name] = round(quantiles(replay_samples(torch, gm, max(50, args.steps)))["median_ms"] * 1e3
+                              / args.layers, 3)
+            del gm
+        mlp["fused_single_launch"] = ops.counts()["fused_mlp_launches"] > 0
+        log(f"[bench] MLP per layer: split gate|up + down {mlp['split_us']} us, fused {mlp['fused_us']} us")
+
     per_batch = {}
     if not args.no_sweep:
         for b in (1, 2, 4, 8, 16, 32, 64):
@@ -857,6 +876,7 @@ def main():
         "copy_peak": copyp,
         "kernels": per_kernel,
         "launches": per_launch,
+        "mlp": mlp,
         "traffic_per_launch": traffic,
         "cpu_baseline": cpu,
         "per_batch": per_batch,

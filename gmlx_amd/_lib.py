@@ -35,11 +35,14 @@ SDPA_NOALLOC_SCRATCH_BYTES = 32 << 20  # KQ_SDPA_NOALLOC_SCRATCH_BYTES (include/
 # KQ_MATMUL_COUNTER_BYTES: arrival counters at the start of every matmul / gather
 # workspace (zero when allocated; the library leaves them zero)
 MATMUL_COUNTER_BYTES = 16 << 10
+# KQ_FUSED_MLP_STATUS_OFFSET: the fused MLP's give-up status word in its workspace
+FUSED_MLP_STATUS_OFFSET = MATMUL_COUNTER_BYTES - 64
 
 # every symbol include/kq_capi.h and include/kq_gguf.h declare, checked at load
 EXPORTS = (
     "kq_version", "kq_strerror", "kq_codec_block_bytes", "kq_supports", "kq_iq2xxs_grid_host",
     "kq_dequantize", "kq_quantize", "kq_matmul_workspace_bytes", "kq_quantized_matmul_grouped",
+    "kq_fused_mlp_workspace_bytes", "kq_fused_mlp",
     "kq_moe_route", "kq_gather_qmm", "kq_moe_glu_gather", "kq_moe_gather_rows", "kq_gather_workspace_bytes",
     "kq_moe_mix", "kq_moe_router_topk",
     "kq_sdpa_workspace_bytes", "kq_sdpa_decode_ragged", "kq_sdpa_decode_ragged_q8", "kq_sdpa_decode_gqa",
@@ -121,6 +124,9 @@ _SIGS = {
     "kq_quantize": ([_vp, _i64, _i64, _i64, _int, _vp, _vp], _int),
     "kq_matmul_workspace_bytes": ([ctypes.POINTER(MatmulProblem), _int, _int], _sz),
     "kq_quantized_matmul_grouped": ([ctypes.POINTER(MatmulProblem), _int, _int, _int, _vp, _sz, _vp], _int),
+    "kq_fused_mlp_workspace_bytes": ([_i32, _i32, _i32, _i32, _int], _sz),
+    "kq_fused_mlp": ([_vp, _int, _i64, _i32, _i32, _vp, _vp, _i64, _int, _i32, _vp, _i64, _int, _i32, _int, _vp,
+                      _int, _i64, _vp, _sz, _vp], _int),
     "kq_moe_route": ([_vp, _i32, _i32, _vp, _vp, _vp], _int),
     "kq_gather_qmm": ([_vp, _int, _i64, _i32, _vp, _i64, _i64, _i32, _i32, _int, _vp, _vp, _i32, _i32,
                        _vp, _int, _i64, _vp, _sz, _vp], _int),

@@ -40,6 +40,14 @@ size_t kq_mms_part_bytes(const kq_matmul_problem *ps, int n);
 int kq_mms_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, int y_dtype, uint32_t *ctr,
                   float *part, hipStream_t s);
 bool kq_mm_eligible(const kq_matmul_problem *ps, int n, int x_dtype);
+// kq_stream.hip: the fused dense MLP (one launch).
+bool kq_mlp_eligible(int32_t M, int32_t K, int32_t I, int32_t N, int gu_codec, int d_codec, int64_t gu_row,
+                     int64_t d_row);
+size_t kq_mlp_work_bytes(int32_t I, int32_t N);
+int kq_mlp_launch(const void *x, const int32_t *x_exp, int64_t x_row_stride, int32_t M, int32_t K,
+                  const void *w_gate, const void *w_up, int64_t gu_row, int32_t I, const void *w_down,
+                  int64_t d_row, int d_codec, int32_t N, int act, void *y, int y_dtype, int64_t y_row_stride,
+                  void *workspace, hipStream_t s);
 int kq_mm_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, int y_dtype, hipStream_t s);
 int device_cus();
 
@@ -1083,6 +1091,45 @@ int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problem
     else if (mt == 2) launch_dense_nw<2, 0>(nw, a, units, max_chunks, s);
     else launch_dense_nw<4, 0>(nw, a, units, max_chunks, s);
     return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
+}
+
+size_t kq_fused_mlp_workspace_bytes(int32_t M, int32_t K, int32_t I, int32_t N, int x_dtype) {
+    (void)x_dtype;
+    if (M <= 0 || K <= 0 || I <= 0 || N <= 0) return 0;
+    return KQ_MATMUL_COUNTER_BYTES + kq_mlp_work_bytes(I, N);
+}
+
+int kq_fused_mlp(const void *x, int x_dtype, int64_t x_row_stride, int32_t M, int32_t K, const void *w_gate,
+                 const void *w_up, int64_t gu_row_bytes, int gu_codec, int32_t I, const void *w_down,
+                 int64_t down_row_bytes, int down_codec, int32_t N, int act, void *y, int y_dtype,
+                 int64_t y_row_stride, void *workspace, size_t workspace_bytes, kq_stream_t stream) {
+    if (!x || !w_gate || !w_up || !w_down || !y) return KQ_ERR_NULL_POINTER;
+    if (kq_block_bytes(gu_codec) == 0 || kq_block_bytes(down_codec) == 0) return KQ_ERR_UNSUPPORTED_CODEC;
+    if (x_dtype != KQ_DTYPE_F16 && x_dtype != KQ_DTYPE_BF16 && x_dtype != KQ_DTYPE_F32)
+        return KQ_ERR_UNSUPPORTED_DTYPE;
+    if (y_dtype != KQ_DTYPE_F32 && y_dtype != KQ_DTYPE_F16 && y_dtype != KQ_DTYPE_BF16)
+        return KQ_ERR_UNSUPPORTED_DTYPE;
+    if (act != KQ_ACT_SILU && act != KQ_ACT_GELU) return KQ_ERR_BAD_ARGUMENT;
+    if (M < 0 || K <= 0 || I <= 0 || N <= 0 || K % KQ_QK || I % KQ_QK) return KQ_ERR_BAD_SHAPE;
+    if (M == 0) return KQ_OK;
+    if (gu_row_bytes < (int64_t)(K / KQ_QK) * kq_block_bytes(gu_codec) ||
+        down_row_bytes < (int64_t)(I / KQ_QK) * kq_block_bytes(down_codec) || x_row_stride < K || y_row_stride < N)
+        return KQ_ERR_BAD_SHAPE;
+    if (((uintptr_t)x & 15) || (x_row_stride & (x_dtype == KQ_DTYPE_F32 ? 3 : 7))) return KQ_ERR_BAD_ALIGN;
+    if (((uintptr_t)w_gate & 15) || ((uintptr_t)w_up & 15) || (gu_row_bytes & 15)) return KQ_ERR_BAD_ALIGN;
+    if (((uintptr_t)w_down & 1) || (down_row_bytes & 1) ||
+        (down_codec == KQ_CODEC_Q4_K && (((uintptr_t)w_down & 15) || (down_row_bytes & 15))))
+        return KQ_ERR_BAD_ALIGN;
+    // h is held as fp16: the single launch serves fp16 activations (other
+    // dtypes keep h in their own dtype, as the reference's swiglu does)
+    if (x_dtype != KQ_DTYPE_F16 ||
+        !kq_mlp_eligible(M, K, I, N, gu_codec, down_codec, gu_row_bytes, down_row_bytes))
+        return KQ_ERR_BAD_SHAPE;
+    if (!workspace || ((uintptr_t)workspace & 255) ||
+        workspace_bytes < kq_fused_mlp_workspace_bytes(M, K, I, N, x_dtype))
+        return KQ_ERR_WORKSPACE_TOO_SMALL;
+    return kq_mlp_launch(x, nullptr, x_row_stride, M, K, w_gate, w_up, gu_row_bytes, I, w_down, down_row_bytes,
+                         down_codec, N, act, y, y_dtype, y_row_stride, workspace, (hipStream_t)stream);
 }
 
 int kq_moe_route(const int32_t *idx, int32_t n_pairs, int32_t n_experts, int32_t *seg_info,

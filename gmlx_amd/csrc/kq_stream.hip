@@ -2112,3 +2112,446 @@ int kq_sgather_launch(const void *x, const int32_t *x_exp, int64_t x_row_stride,
     a.alpha = alpha;
     return sgather_dispatch(a, codec, w1 != nullptr, K / KQ_QK, s, false);
 }
+
+// ---- Fused dense MLP at M <= 8 ----------------------------------------------
+// gmlx's _FusedMLP (gmlx/occupancy_fuse.py:270-316): the grouped gate|up call,
+// the SwiGLU h = act(gate . x) * (up . x), then the down projection -- here in
+// one persistent launch of one producer / consumer workgroup per CU, so the
+// down projection's weight stream starts while gate|up is finishing instead
+// of after a launch boundary and a fresh ramp.
+//  Phase A (gate|up): items are 16-row tile pairs (gate tile p, then up tile
+//    p), workgroup b taking pairs b, b + G, ...; the consumers own K-slabs of
+//    the Q4_K rows as in the streaming kernel (owned view), and a round's
+//    epilogue forms h[m][16p + n] = act(g, u) in fp32 and stores it as fp16
+//    with device-coherent stores (they reach the point of coherence past the
+//    XCDs' L2s), then counts one arrival per (pair, row group) on the counter
+//    of the down K-slice the columns belong to.
+//  Phase B (down): K = I is cut into S slices of 8 super-blocks; workgroup b
+//    keeps slice q = b mod S and walks down tiles b / S + j G_q (G_q: the
+//    workgroups of slice q, G / S or one more), like a
+//    split launch of the streaming kernel (partial tiles, per-tile arrival
+//    counters, the last slice sums in slice order).  The producers copy the
+//    first down tiles into the ring while the consumers finish phase A; the
+//    consumers wait once, before their first down tile, until the h columns
+//    of their own super-block of the slice have all arrived (a bounded spin
+//    on its counter), then load their h fragments with device-coherent loads.
+// Every phase-A item is finished by a running workgroup that never waits
+// before it, and the grid is at most one workgroup per CU (LDS), so every
+// wait ends; past kMlpSpinLimit polls a wait gives up and sets the status
+// word instead of hanging (the results are then invalid).  The slice counters
+// return to zero: the last of a slice's waiting workgroups to pass its wait
+// clears them.
+namespace {
+
+constexpr int kMlpC = 8;           // consumer waves
+constexpr int kMlpRows = 8;        // activation rows (M <= 8)
+constexpr int kMlpSliceNb = 8;     // down super-blocks per slice (one per consumer)
+constexpr uint32_t kMlpSpinLimit = 1u << 22;
+// counter region (uint32 index): per-tile split counters below kMlpSbBase;
+// per h super-block sb (sb < I / 256 <= 64) the arrivals at kMlpSbBase + 32 sb
+// and, for the slice's first super-block, the slice's readers at + 16; the
+// status word at kMlpStatus
+constexpr int kMlpSbBase = (int)(KQ_MATMUL_COUNTER_BYTES / 4) - 2048 - 32;
+constexpr int kMlpStatus = (int)(KQ_MATMUL_COUNTER_BYTES / 4) - 16;
+
+struct MlpArgs {
+    const uint8_t *wg, *wu, *wd;
+    const char *x;           // fp16 [M, K]
+    const int32_t *x_exp;    // per-row exponents of prepared activations, or null
+    uint16_t *h;             // fp16 bits [kMlpRows][I]
+    uint32_t *ctr;           // counter region
+    float *part;             // partial tiles [tiles][S][8 rows][16 columns]
+    void *y;
+    int64_t x_stride, y_stride;
+    uint32_t gu_bytes, gu_row, d_bytes, d_row;
+    int32_t M, K, I, N, y_dtype, act, S, pairs, tiles;
+};
+
+typedef const __attribute__((address_space(4))) MlpArgs *MArgs;
+
+template <int SBA, int CD>
+struct MlpGeo {
+    static constexpr int NBA = SBA * kMlpC;                          // gate / up super-blocks (K / 256)
+    static constexpr int RCA = SlotGeo<KQ_CODEC_Q4_K, NBA>::RC;      // chunks per slot row
+    static constexpr int RCB = SlotGeo<CD, kMlpSliceNb>::RC;
+    static constexpr int ROWA = NBA * SlotGeo<KQ_CODEC_Q4_K, NBA>::CPB;  // chunks a row copies
+    static constexpr int ROWB = kMlpSliceNb * SlotGeo<CD, kMlpSliceNb>::CPB;
+    static constexpr int PRA = row_parts<KQ_CODEC_Q4_K, NBA>(), PRB = row_parts<CD, kMlpSliceNb>();
+    static constexpr int PR = PRA > PRB ? PRA : PRB;                 // 1 KB loads per row, both phases
+    static constexpr int PL = (16 / kProducers) * PR;                // loads per producer per tile
+    static constexpr int SLOTB = 16 * 16 * (RCA > RCB ? RCA : RCB);
+    static constexpr int RED = 8 * kMlpC * 32 * 16;                  // a round's partial tiles
+    static constexpr int JUNK = 1024;                                // target of padding loads
+};
+
+template <int SBA, int CD, int R>
+__global__ __launch_bounds__(64 * (kProducers + kMlpC)) void kq_mlp_kernel(MlpArgs a_) {
+    using MG = MlpGeo<SBA, CD>;
+    constexpr int C = kMlpC, LR = 32, kTmax = 8;
+    static_assert(MG::PL * (R - 1) <= 63, "vmcnt counts at most 63 loads");
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const MArgs A = (MArgs)__builtin_amdgcn_kernarg_segment_ptr();
+    const Iq2Tables &iq2_tab = *IqTables<CD>::get();
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = kq_lane(), r = lane & 15, g = lane >> 4;
+    const int G = (int)gridDim.x, B0 = (int)blockIdx.x, S = A->S;
+    const int M = A->M;
+    const int nA = B0 < A->pairs ? 2 * ((A->pairs - B0 + G - 1) / G) : 0;  // phase-A tiles (gate, up alternating)
+    // slice q = B0 mod S has Gs workgroups (G need not be a multiple of S)
+    const int q = B0 % S, Gs = G / S + (q < G % S ? 1 : 0), T0 = B0 / S;
+    const int nB = T0 < A->tiles ? (A->tiles - T0 + Gs - 1) / Gs : 0;     // phase-B tiles
+    const int n = nA + nB;
+    const uint32_t ring_lds = (uint32_t)(uintptr_t)(LDSP(void))smem;
+    floatx4 *red = (floatx4 *)(smem + R * MG::SLOTB);
+    const uint32_t junk = ring_lds + R * MG::SLOTB + MG::RED;
+    // a workgroup's round boundaries: rounds of kTmax tiles within each phase
+    auto round_end = [&](int b) { return b < nA ? ((b + 1) % kTmax == 0 || b + 1 == nA) : ((b + 1 - nA) % kTmax == 0 || b + 1 == n); };
+
+    if (wave < kProducers) {
+        uint32_t tabA[MG::PR], tabB[MG::PR];
+#pragma unroll
+        for (int p = 0; p < MG::PR; ++p) {
+            tabA[p] = p < MG::PRA ? row_chunk_src<KQ_CODEC_Q4_K, MG::NBA>(
+                                        (p == MG::PRA - 1 ? MG::ROWA - 64 : 64 * p) + lane, MG::ROWA)
+                                  : 0x80000000u;
+            tabB[p] = p < MG::PRB ? row_chunk_src<CD, kMlpSliceNb>(
+                                        (p == MG::PRB - 1 ? MG::ROWB - 64 : 64 * p) + lane, MG::ROWB)
+                                  : 0x80000000u;
+        }
+        const uint32_t kofsB = (uint32_t)(q * kMlpSliceNb) * (uint32_t)Geo<CD>::BPB;
+        // (the tables reach copy as arguments: a lambda capturing a local
+        // array made the host pass drop the kernel's instantiations)
+        auto copy = [&](int j, const uint32_t *ta, const uint32_t *tb) {
+            const uint32_t slot = ring_lds + (uint32_t)(j % R) * MG::SLOTB;
+            if (j < nA) {
+                const int pair = B0 + (j >> 1) * G;
+                const __amdgpu_buffer_rsrc_t rs = kq_buffer((j & 1) ? A->wu : A->wg, A->gu_bytes);
+                const uint32_t row0 = (uint32_t)pair * 16, last = (uint32_t)A->I - 1, rb = A->gu_row;
+#pragma unroll
+                for (int i = 0; i < 16 / kProducers; ++i) {
+                    const int row = i * kProducers + wave;
+                    const int soff = (int)(min(row0 + (uint32_t)row, last) * rb);
+                    const uint32_t m0 = slot + (uint32_t)(row * MG::RCA * 16);
+#pragma unroll
+                    for (int p = 0; p < MG::PR; ++p)
+                        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                            rs,
+                            (LDSP(void))(uintptr_t)(p < MG::PRA ? m0 + 16 * (p == MG::PRA - 1 ? MG::ROWA - 64 : 64 * p)
+                                                                : junk),
+                            16, ta[p], soff, 0, 0);
+                }
+            } else {
+                const int tile = T0 + (j - nA) * Gs;
+                const __amdgpu_buffer_rsrc_t rs = kq_buffer(A->wd, A->d_bytes);
+                const uint32_t row0 = (uint32_t)tile * 16, last = (uint32_t)A->N - 1, rb = A->d_row;
+#pragma unroll
+                for (int i = 0; i < 16 / kProducers; ++i) {
+                    const int row = i * kProducers + wave;
+                    const int soff = (int)(min(row0 + (uint32_t)row, last) * rb + kofsB);
+                    const uint32_t m0 = slot + (uint32_t)(row * MG::RCB * 16);
+#pragma unroll
+                    for (int p = 0; p < MG::PR; ++p)
+                        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                            rs,
+                            (LDSP(void))(uintptr_t)(p < MG::PRB ? m0 + 16 * (p == MG::PRB - 1 ? MG::ROWB - 64 : 64 * p)
+                                                                : junk),
+                            16, tb[p], soff, 0, 0);
+                }
+            }
+        };
+        __builtin_amdgcn_s_barrier();  // the consumers' activation loads are issued
+        const int first = min(2, n);
+        for (int j = 0; j < first; ++j) copy(j, tabA, tabB);
+        for (int b = 0; b < n; ++b) {
+            const int newer = b == 0 ? first - 1 : min(R - 2, n - 1 - b);
+            wait_tiles_left<MG::PL, (R - 1 < 63 / MG::PL ? R - 1 : 63 / MG::PL)>(newer);
+            __builtin_amdgcn_s_barrier();  // tile b to the consumers; tile b - 1's slot back
+            if (b == 0) {
+                for (int j = first; j < min(R, n); ++j) copy(j, tabA, tabB);
+            } else if (b + R - 1 < n) {
+                copy(b + R - 1, tabA, tabB);
+            }
+            if (round_end(b)) {
+                __builtin_amdgcn_s_barrier();  // the round's partial tiles are in LDS
+                if (b + 1 < n) __builtin_amdgcn_s_barrier();  // the round's outputs are out: red is free
+            }
+        }
+        return;
+    }
+
+    // ================= consumers
+    const int c = wave - kProducers;
+    const int n16 = lane & 15, mq = lane >> 4;
+    // phase A: the owned Q4_K view of super-blocks [c SBA, c SBA + SBA) of x
+    half8_t xr[SBA][8];
+    floatx4 xsum;
+    {
+        const uint32_t xbytes = (uint32_t)(((int64_t)(M - 1) * A->x_stride + A->K) * 2);
+        const __amdgpu_buffer_rsrc_t xs = kq_buffer(A->x, xbytes);
+        const uint32_t xrow = r < M ? (uint32_t)(r * A->x_stride * 2) + (uint32_t)(c * SBA * KQ_QK * 2) : 0x80000000u;
+        u32x4 cin[SBA][8];
+#pragma unroll
+        for (int s2 = 0; s2 < SBA; ++s2)
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+#pragma unroll
+                for (int a2 = 0; a2 < 2; ++a2)
+                    cin[s2][2 * w + a2] = __builtin_bit_cast(
+                        u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                   xs, xrow + (uint32_t)(2 * (256 * s2 + 64 * g + 32 * a2 + 8 * w)), 0, 0));
+        __builtin_amdgcn_s_barrier();  // the loads are issued: the producers may start
+        q4own_x<SBA>(xr, xsum, cin, lane);
+    }
+    const Q4Consts q4k = q4own_consts(g);
+    const bool has_xe = A->x_exp != nullptr;
+    int xe[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) xe[h] = has_xe && 4 * h + mq < M ? A->x_exp[4 * h + mq] : 0;
+    const __amdgpu_buffer_rsrc_t hrs = kq_buffer(A->h, (uint32_t)(kMlpRows * A->I * 2));
+    uint32_t *const ctr0 = A->ctr;
+    const float *redf = (const float *)red;
+    for (int round0 = 0; round0 < nA; round0 += kTmax) {
+        const int nt = min(kTmax, nA - round0);
+        for (int b = 0; b < nt; ++b) {
+            const int gb = round0 + b;
+            __builtin_amdgcn_s_barrier();  // tile gb has landed
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+            floatx4 acc = fzero4();
+            q4own_slab<SBA>(acc,
+                            (LDSP(const uint8_t))smem + (gb % R) * MG::SLOTB + r * MG::RCA * 16 + c * SBA * 144, xr,
+                            xsum, q4k);
+            kq_mfma_drain();
+            if (g < 2) red[(b * C + c) * LR + lane] = acc;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        }
+        __builtin_amdgcn_s_barrier();  // the round's partial tiles are in LDS
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        // units (pair qq, row group h): one output per lane, the C partial
+        // tiles of gate and of up summed in consumer order, then act(g, u)
+        for (int unit = c; unit < nt; unit += C) {
+            const int qq = unit >> 1, h = unit & 1;
+            const int pair = B0 + ((round0 >> 1) + qq) * G;
+            float v[2];
+#pragma unroll
+            for (int w2 = 0; w2 < 2; ++w2) {
+                float sum = 0.f;
+#pragma unroll
+                for (int c2 = 0; c2 < C; ++c2) {
+                    const float pv = redf[((((2 * qq + w2) * C + c2) * LR) + 16 * h + n16) * 4 + mq];
+                    sum = c2 == 0 ? pv : sum + pv;
+                }
+                v[w2] = sum;
+            }
+            const int m = 4 * h + mq;
+            const float hv = kq_glu(A->act, ldexpf(v[0], xe[h]), ldexpf(v[1], xe[h]), 0.f, 0.f, 0.f, 0.f);
+            const uint32_t off = m < M ? (uint32_t)((m * A->I + pair * 16 + n16) * 2) : 0x80000000u;
+            __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (_Float16)hv), hrs, off, 0, 16);
+            __builtin_amdgcn_s_waitcnt(KQ_VMCNT(0));  // the stores have reached the point of coherence
+            if (lane == 0)  // the h super-block of the pair's columns
+                __hip_atomic_fetch_add(ctr0 + kMlpSbBase + 32 * ((pair * 16) / KQ_QK), 1u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (round0 + nt < n) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            __builtin_amdgcn_s_barrier();  // red is free for the next round
+        }
+    }
+    if (nB == 0) return;
+    // ---- phase B: wait until slice q's h columns have all arrived (two per
+    // pair: the pair's two row groups), then the consumer's fragments of
+    // super-block q * 8 + c of h
+    // Each consumer waits for its own h super-block sb = q * 8 + c: 16 pairs,
+    // two arrivals each (one lane polls, spaced: every poll is a
+    // device-coherent load of a line the arrivals also write).
+    {
+        const int sb = q * kMlpSliceNb + c;
+        const uint32_t want = (uint32_t)(2 * min(KQ_QK / 16, max(0, A->pairs - sb * (KQ_QK / 16))));
+        uint32_t *const sc = ctr0 + kMlpSbBase + 32 * sb;
+        uint32_t seen = 0, spins = 0;
+        if (lane == 0) {
+            while ((seen = __hip_atomic_load(sc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) < want) {
+                __builtin_amdgcn_s_sleep(4);
+                if (++spins >= kMlpSpinLimit) {
+                    __hip_atomic_store(ctr0 + kMlpStatus, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+            }
+        }
+        (void)__builtin_amdgcn_readfirstlane((int)seen);
+    }
+    half8_t hr[1][8];
+    [[maybe_unused]] floatx4 hsum = fzero4();
+    {
+        const uint32_t hrow = r < M ? (uint32_t)((r * A->I + (q * kMlpSliceNb + c) * KQ_QK) * 2) : 0x80000000u;
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+            hr[0][t] = __builtin_bit_cast(
+                half8_t, __builtin_amdgcn_raw_buffer_load_b128(hrs, hrow + (uint32_t)(2 * Block<CD>::x_elem(t, g)), 0, 16));
+        if constexpr (CD == KQ_CODEC_Q4_K) hsum = xsum_generic<1>(hr, r);
+    }
+    int ydt = A->y_dtype;
+    float *const part = A->part;
+    const int cstride = min(32, 1 << (31 - __builtin_clz(kMlpSbBase / max(A->tiles, 1))));
+    for (int round0 = nA; round0 < n; round0 += kTmax) {
+        const int nt = min(kTmax, n - round0);
+        for (int b = 0; b < nt; ++b) {
+            const int gb = round0 + b;
+            __builtin_amdgcn_s_barrier();  // tile gb has landed
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+            if (gb == nA && c == 0 && lane == 0) {
+                // every consumer of this workgroup has passed its wait: the
+                // last of the slice's waiting workgroups (those with down
+                // tiles: min(Gs, tiles)) clears the slice's counters
+                uint32_t *const sc = ctr0 + kMlpSbBase + 32 * (q * kMlpSliceNb);
+                if (__hip_atomic_fetch_add(sc + 16, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                    (uint32_t)(min(Gs, A->tiles) - 1)) {
+                    __hip_atomic_store(sc + 16, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+                    for (int i = 0; i < kMlpSliceNb; ++i)
+                        __hip_atomic_store(sc + 32 * i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+            floatx4 acc = fzero4();
+            mma_slab<CD, 1>(acc, ring_lds + (uint32_t)(gb % R) * MG::SLOTB + r * MG::RCB * 16 + c * Geo<CD>::SLOT, hr,
+                            hsum, g, iq2_tab);
+            kq_mfma_drain();
+            if (g < 2) red[(b * C + c) * LR + lane] = acc;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        }
+        __builtin_amdgcn_s_barrier();  // the round's partial tiles are in LDS
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        // the round's tiles b = c, c + C, ...: partial of slice q over the C
+        // consumers (consumer order), out with device-coherent stores
+        for (int b = c; b < nt; b += C) {
+            const int tile = T0 + (round0 - nA + b) * Gs;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const float *rf = redf + 4 * (b * C * LR + 16 * h + n16) + mq;
+                float sum = rf[0];
+#pragma unroll
+                for (int c2 = 1; c2 < C; ++c2) sum += rf[4 * c2 * LR];
+                if (4 * h + mq < M)
+                    __hip_atomic_store(part + ((size_t)tile * S + q) * 128 + 64 * h + lane, sum, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_s_waitcnt(KQ_VMCNT(0));
+        const int bl = c + lane * C;
+        bool last = false;
+        if (bl < nt) {
+            uint32_t *const ctr = ctr0 + (T0 + (round0 - nA + bl) * Gs) * cstride;
+            last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(S - 1);
+            if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        uint64_t mine = __builtin_amdgcn_ballot_w64(last);
+        while (mine) {
+            const int i = __builtin_ctzll(mine);
+            mine &= mine - 1;
+            const int tile = T0 + (round0 - nA + c + i * C) * Gs;
+            const float *pp = part + (size_t)tile * S * 128;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int m = 4 * h + mq, col = tile * 16 + n16;
+                if (m >= M) continue;
+                float v[kMaxSplit];
+#pragma unroll
+                for (int s2 = 0; s2 < kMaxSplit; ++s2)
+                    v[s2] = s2 < S ? __hip_atomic_load(pp + s2 * 128 + 64 * h + lane, __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT)
+                                   : 0.f;
+                float sum = v[0];
+#pragma unroll
+                for (int s2 = 1; s2 < kMaxSplit; ++s2)
+                    if (s2 < S) sum += v[s2];
+                if (col < A->N) kq_store_out(A->y, ydt, (int64_t)m * A->y_stride + col, sum);
+            }
+        }
+        if (round0 + nt < n) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            __builtin_amdgcn_s_barrier();  // red is free for the next round
+        }
+    }
+}
+
+template <int SBA, int CD>
+int launch_mlp(const MlpArgs &a, int grid, hipStream_t s) {
+    using MG = MlpGeo<SBA, CD>;
+    constexpr size_t budget = 160 * 1024 - (CD == KQ_CODEC_IQ2_XXS ? sizeof(Iq2Tables) : 0);
+    constexpr size_t fixed = MG::RED + MG::JUNK;
+    constexpr int R = (budget - fixed) / MG::SLOTB >= 4 ? 4 : (int)((budget - fixed) / MG::SLOTB);
+    static_assert(R >= 2, "fused MLP LDS");
+    constexpr size_t lds = (size_t)R * MG::SLOTB + fixed;
+    static bool raised = false;
+    if (!raised) {
+        if (hipFuncSetAttribute((const void *)kq_mlp_kernel<SBA, CD, R>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds) != hipSuccess)
+            return KQ_ERR_LAUNCH_FAILED;
+        raised = true;
+    }
+    hipLaunchKernelGGL((kq_mlp_kernel<SBA, CD, R>), dim3(grid), dim3(64 * (kProducers + kMlpC)), lds, s, a);
+    return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
+}
+
+}  // namespace
+
+// Shapes the fused MLP kernel serves (fp16 activations; the caller prepares
+// bf16 / fp32 rows): M 1..8, Q4_K gate / up with K of 8 or 16 super-blocks,
+// Q6_K or Q4_K down whose K = I is whole slices of 8 super-blocks (at most
+// kMaxSplit), byte offsets within 31 bits.
+bool kq_mlp_eligible(int32_t M, int32_t K, int32_t I, int32_t N, int gu_codec, int d_codec, int64_t gu_row,
+                     int64_t d_row) {
+    if (M < 1 || M > kMlpRows || gu_codec != KQ_CODEC_Q4_K) return false;
+    if (d_codec != KQ_CODEC_Q6_K && d_codec != KQ_CODEC_Q4_K) return false;
+    if (K != 8 * KQ_QK && K != 16 * KQ_QK) return false;  // one or two super-blocks per consumer
+    if (I <= 0 || I % (kMlpSliceNb * KQ_QK) || I / (kMlpSliceNb * KQ_QK) > kMaxSplit) return false;
+    if (N <= 0) return false;
+    const int64_t tiles = (N + 15) / 16;
+    if (tiles > kMlpSbBase) return false;  // one split counter per down tile
+    if ((int64_t)(I + 16) * gu_row >= 0x80000000LL || (int64_t)(N + 16) * d_row >= 0x80000000LL) return false;
+    if ((int64_t)kMlpRows * I * 2 >= 0x80000000LL) return false;
+    return true;
+}
+
+// Workspace after the counter region: fp16 h [8][I], then the partial tiles.
+size_t kq_mlp_work_bytes(int32_t I, int32_t N) {
+    const size_t hb = ((size_t)kMlpRows * I * 2 + 255) & ~(size_t)255;
+    const size_t pb = (size_t)((N + 15) / 16) * (I / (kMlpSliceNb * KQ_QK)) * 512;
+    return hb + pb;
+}
+
+int kq_mlp_launch(const void *x, const int32_t *x_exp, int64_t x_row_stride, int32_t M, int32_t K,
+                  const void *w_gate, const void *w_up, int64_t gu_row, int32_t I, const void *w_down,
+                  int64_t d_row, int d_codec, int32_t N, int act, void *y, int y_dtype, int64_t y_row_stride,
+                  void *workspace, hipStream_t s) {
+    MlpArgs a;
+    a.wg = (const uint8_t *)w_gate;
+    a.wu = (const uint8_t *)w_up;
+    a.wd = (const uint8_t *)w_down;
+    a.x = (const char *)x;
+    a.x_exp = x_exp;
+    a.ctr = (uint32_t *)workspace;
+    a.h = (uint16_t *)((char *)workspace + KQ_MATMUL_COUNTER_BYTES);
+    a.part = (float *)((char *)workspace + KQ_MATMUL_COUNTER_BYTES +
+                       (((size_t)kMlpRows * I * 2 + 255) & ~(size_t)255));
+    a.y = y;
+    a.x_stride = x_row_stride;
+    a.y_stride = y_row_stride;
+    a.gu_row = (uint32_t)gu_row;
+    a.gu_bytes = (uint32_t)(I * gu_row);
+    a.d_row = (uint32_t)d_row;
+    a.d_bytes = (uint32_t)(N * d_row);
+    a.M = M;
+    a.K = K;
+    a.I = I;
+    a.N = N;
+    a.y_dtype = y_dtype;
+    a.act = act;
+    a.S = I / (kMlpSliceNb * KQ_QK);
+    a.pairs = I / 16;
+    a.tiles = (N + 15) / 16;
+    const int grid = device_cus();
+    const bool k16 = K == 16 * KQ_QK;
+    if (d_codec == KQ_CODEC_Q6_K) return k16 ? launch_mlp<2, KQ_CODEC_Q6_K>(a, grid, s) : launch_mlp<1, KQ_CODEC_Q6_K>(a, grid, s);
+    return k16 ? launch_mlp<2, KQ_CODEC_Q4_K>(a, grid, s) : launch_mlp<1, KQ_CODEC_Q4_K>(a, grid, s);
+}

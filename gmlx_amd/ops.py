@@ -5,10 +5,11 @@ device, and launches the gfx950 kernels of libgmlx_amd.so on the current torch
 stream.  There is no CPU path: CPU tensors, a missing library or an
 unsupported shape raise.  Reference call sites are cited per op.
 
-Op names and argument orders follow the reference's calls (SURVEY Appendix B):
+Op names and argument orders follow the reference's calls:
   dequantize(w, scales, codec, dtype)            gmlx/modules.py:1461
   quantize(w, codec) -> (wire, scales)           tests/test_dequant_unattachable.py:36
   quantized_matmul(x, w, scales, codec, transpose=True)   gmlx/occupancy_fuse.py:162-165
+  fused_mlp(x, gate_w, up_w, down_w, codec, down_codec, act)  _FusedMLP, gmlx/occupancy_fuse.py:270-316
   gather_qmm / KQuantSwitchLinear                tests/test_native_fp.py:420-428
   moe_glu_gather_kq(x, gate_w, up_w, codec, idx, act=, limit=, alpha=,
                     gate_bias=, up_bias=)        gmlx/modules.py:557-588
@@ -29,7 +30,7 @@ from collections import OrderedDict
 import torch
 
 from . import _lib
-from ._lib import CODEC_ID, DTYPE_BF16, DTYPE_F16, DTYPE_F32, KQError, MatmulProblem, check, lib
+from ._lib import CODEC_ID, DTYPE_BF16, DTYPE_F16, DTYPE_F32, KQ_OK, KQError, MatmulProblem, check, lib
 
 QK_K = 256
 BLOCK_BYTES = {"q4_k": 144, "q6_k": 210, "iq2_xxs": 66}
@@ -37,7 +38,7 @@ _TORCH_DTYPE = {torch.float32: DTYPE_F32, torch.float16: DTYPE_F16, torch.bfloat
 
 __all__ = [
     "codecs", "codec_has_matmul", "codec_has_moe_glu", "dequantize", "quantize", "quantized_matmul",
-    "quantized_matmul_grouped", "moe_route", "gather_qmm", "moe_glu_gather_kq", "gather_qmv_kq",
+    "quantized_matmul_grouped", "fused_mlp", "fused_mlp_status", "counts", "moe_route", "gather_qmm", "moe_glu_gather_kq", "gather_qmv_kq",
     "gather_qmv_mix_ns_kq", "moe_router_topk", "sdpa_decode_ragged", "sdpa_decode_gqa",
     "ragged_decode_attention", "wire_k",
 ]
@@ -128,6 +129,7 @@ class _Workspaces:
 
 
 _WS = _Workspaces()
+_COUNTS = {"fused_mlp_launches": 0}
 
 
 # ------------------------------------------------------------ capabilities
@@ -227,6 +229,71 @@ def quantized_matmul(x, w, scales=None, codec="q4_k", transpose=True, out_dtype=
         s = _stream(x)
         _launch_grouped([_problem(x2, w, codec, y)], _dt(x.dtype), _dt(out_dtype), x.device, s)
     return y.reshape(*x.shape[:-1], w.shape[0])
+
+
+def fused_mlp(x, gate_w, up_w, down_w, codec="q4_k", down_codec=None, act="silu", out_dtype=None):
+    """gmlx's _FusedMLP forward (gmlx/occupancy_fuse.py:270-316):
+    down_proj(swiglu(gate(x), up(x))), with h = act(x . Wg^T) * (x . Wu^T)
+    computed in fp32 and held in the activation dtype (the dtype the
+    reference's swiglu hands down_proj).  x [..., K]; gate / up wire
+    [I, K/256*bpb] of `codec`; down wire [N, I/256*bpb] of `down_codec`
+    (default `codec`).  fp16 activations of at most 8 rows with the served
+    codecs and shapes (kq_fused_mlp) run in one launch; otherwise the same
+    three steps run as the reference runs them: the grouped gate|up matmul,
+    the GLU, the down matmul.""" 
+    _fault("fused_mlp")
+    _require_gpu(x, gate_w, up_w, down_w)
+    down_codec = down_codec or codec
+    if act not in ("silu", "gelu"):
+        raise ValueError(f"act must be 'silu' or 'gelu', got {act!r}")
+    if gate_w.shape != up_w.shape:
+        raise ValueError("gate and up wires must have the same shape")
+    x2 = _rows_view(x)
+    M, K = x2.shape
+    I, N = gate_w.shape[0], down_w.shape[0]
+    if wire_k(gate_w.shape[-1], codec) != K or wire_k(down_w.shape[-1], down_codec) != I:
+        raise ValueError("wire widths do not match x's K and gate's rows")
+    out_dtype = out_dtype or x.dtype
+    y = torch.empty((M, N), dtype=out_dtype, device=x.device)
+    if M == 0:
+        return y.reshape(*x.shape[:-1], N)
+    L = lib()
+    s = _stream(x)
+    need = L.kq_fused_mlp_workspace_bytes(M, K, I, N, _dt(x.dtype))
+    ws = _WS.get("mlp", x.device, s.value, need)
+    gate_w, up_w, down_w = gate_w.contiguous(), up_w.contiguous(), down_w.contiguous()
+    rc = L.kq_fused_mlp(x2.data_ptr(), _dt(x.dtype), x2.stride(0), M, K, gate_w.data_ptr(), up_w.data_ptr(),
+                        gate_w.stride(0), _codec_id(codec), I, down_w.data_ptr(), down_w.stride(0),
+                        _codec_id(down_codec), N, _lib.ACT_ID[act], y.data_ptr(), _dt(out_dtype), y.stride(0),
+                        ws.data_ptr(), ws.numel(), s)
+    if rc == KQ_OK:
+        _COUNTS["fused_mlp_launches"] += 1
+    elif rc == _lib.KQ_ERR_BAD_SHAPE:
+        g, u = quantized_matmul_grouped([(x2, gate_w, codec), (x2, up_w, codec)], out_dtype=torch.float32)
+        gf = torch.nn.functional.silu(g) if act == "silu" else torch.nn.functional.gelu(g, approximate="tanh")
+        h = (gf * u).to(x.dtype)
+        y = quantized_matmul(h, down_w, None, down_codec, out_dtype=out_dtype)
+    else:
+        check("kq_fused_mlp", rc)
+    return y.reshape(*x.shape[:-1], N)
+
+
+def counts():
+    """Calls that took the single-launch forms since import
+    ({"fused_mlp_launches": n})."""
+    return dict(_COUNTS)
+
+
+def fused_mlp_status(device=None):
+    """1 if a fused MLP launch on this device's current stream gave up a
+    wait (see kq_fused_mlp), else 0.  Synchronises the stream."""
+    device = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    s = torch.cuda.current_stream(device).cuda_stream
+    ws = _WS._ws.get(("mlp", device.index, s))
+    if ws is None:
+        return 0
+    off = _lib.FUSED_MLP_STATUS_OFFSET
+    return int(ws[off:off + 4].view(torch.int32).item())
 
 
 def quantized_matmul_grouped(items, out_dtype=None):

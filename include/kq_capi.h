@@ -136,9 +136,9 @@ size_t kq_matmul_workspace_bytes(const kq_matmul_problem *problems, int n_proble
  * KQ_MAX_GROUP independent problems (any codec mix, shared x_dtype/y_dtype)
  * run in one call: the row-concatenated q|k|v and gate|up wires of
  * gmlx/occupancy_fuse.py:141-344 become one call without concatenating
- * bytes.  The call is one launch, except that problems sharing x with
- * M <= 16 and enough rows for every workgroup to walk several 16-row tiles
- * take one persistent launch per codec.  x_dtype: f16, bf16 or f32 (bf16 /
+ * bytes.  The call is one launch (problems sharing x with M <= 16 whose
+ * codecs mix beyond Q4_K with Q6_K may take one launch per codec).
+ * x_dtype: f16, bf16 or f32 (bf16 /
  * f32 need the workspace above; one extra launch prepares the rows).
  * y_dtype: f16, bf16 or f32.  Results do not depend on scheduling: repeated
  * calls on the same inputs are bitwise identical. */
@@ -146,6 +146,35 @@ size_t kq_matmul_workspace_bytes(const kq_matmul_problem *problems, int n_proble
 int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problems,
                                 int x_dtype, int y_dtype, void *workspace,
                                 size_t workspace_bytes, kq_stream_t stream);
+
+/* ---- Fused dense MLP ----------------------------------------------------- */
+/* gmlx's _FusedMLP forward (gmlx/occupancy_fuse.py:270-316): the grouped
+ * gate|up call kq.quantized_matmul(x, w_gate|w_up), its SwiGLU
+ * h = act(x . Wg^T) * (x . Wu^T), then down_proj(h) = h . Wd^T -- in one
+ * launch: the down projection's weight stream starts while gate|up is
+ * finishing, and h never leaves the device's caches as a separate
+ * activation pass.  x [M, K] fp16, gate / up [I, K] wire rows of gu_codec,
+ * down [N, I] wire rows of down_codec, y [M, N] of y_dtype.  h is computed in
+ * fp32 and held as fp16 (the activation dtype the reference's swiglu feeds
+ * down_proj).  act: KQ_ACT_SILU or KQ_ACT_GELU.
+ * Served: fp16 x, M <= 8, Q4_K gate / up with K of 2048 or 4096, Q6_K or
+ * Q4_K down with I a multiple of 2048 up to 16384.  Other shapes and dtypes
+ * (bf16 / f32 activations keep h in their own dtype) and a workspace
+ * below kq_fused_mlp_workspace_bytes, 256-byte aligned) return
+ * KQ_ERR_BAD_SHAPE / KQ_ERR_WORKSPACE_TOO_SMALL before any launch; callers
+ * then run the three steps as separate calls.  The workspace starts with
+ * the KQ_MATMUL_COUNTER_BYTES counter region (zeroed once, left zero by
+ * every call); the uint32 at byte KQ_FUSED_MLP_STATUS_OFFSET is set to 1 if
+ * a wait for h gave up (the launch then did not complete normally: only
+ * possible when the GPU cannot hold one workgroup per CU of this launch at
+ * once), and is never cleared by the library.  Results do not depend on
+ * scheduling. */
+#define KQ_FUSED_MLP_STATUS_OFFSET (KQ_MATMUL_COUNTER_BYTES - 64)
+size_t kq_fused_mlp_workspace_bytes(int32_t M, int32_t K, int32_t I, int32_t N, int x_dtype);
+int kq_fused_mlp(const void *x, int x_dtype, int64_t x_row_stride, int32_t M, int32_t K, const void *w_gate,
+                 const void *w_up, int64_t gu_row_bytes, int gu_codec, int32_t I, const void *w_down,
+                 int64_t down_row_bytes, int down_codec, int32_t N, int act, void *y, int y_dtype,
+                 int64_t y_row_stride, void *workspace, size_t workspace_bytes, kq_stream_t stream);
 
 /* ---- MoE expert gather ------------------------------------------------- */
 /* Device-side routing of (token, slot) pairs to experts.  idx [n_pairs]

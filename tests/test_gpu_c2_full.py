@@ -3,8 +3,9 @@ layer (q|k|v grouped, o, gate|up grouped, down), with the default routing
 the benchmark uses, at every batch width the metric is quoted on
 (B = 1, 2, 4, 8, 16, 32, 64), against fp64 over the same wire bytes.
 
-Shapes and draws follow the benchmark (the reference's
-occupancy-fused q|k|v and gate|up groups, gmlx/occupancy_fuse.py:141-344):
+Shapes and draws follow the benchmark (bench.py's Qwen3-8B stack; the
+reference's occupancy-fused q|k|v and gate|up groups,
+gmlx/occupancy_fuse.py:141-344):
 N(0, 0.02) weights in the draw order q, k, v, o, gate, up, down, quantised on
 the GPU (kq_quantize, byte-identical to the oracle quantiser), fp16 N(0, 1)
 activations.  Two weight rows of every 16-row tile of every matrix are
