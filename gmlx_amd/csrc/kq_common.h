@@ -103,6 +103,10 @@ __device__ __forceinline__ half2_t kq_as_h2(uint32_t u) { return __builtin_bit_c
 __device__ __forceinline__ uint32_t kq_h2_bits(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
 
 // Wave-level helpers (wave64).
+// s_waitcnt vmcnt(n) (0 <= n <= 63) leaving the other counters unconstrained
+// (gfx9 encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14).
+#define KQ_VMCNT(n) (((n) & 0xF) | ((((n) >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8))
+
 __device__ __forceinline__ int kq_lane() { return (int)__lane_id(); }
 
 // Ordering point between the MFMAs of an accumulation loop body and any VALU

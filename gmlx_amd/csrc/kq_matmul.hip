@@ -214,10 +214,11 @@ constexpr int kGatherWaves = 4;
 // (128 VGPRs) for one 16-row tile of one matrix with fp16/bf16 rows; three
 // (168) up to two such tiles or fp32 rows; two (256) up to four tiles (and
 // Q6_K pairs of fp32 rows); one (AGPRs too) beyond, and for four tiles of
-// fp32 rows.
+// fp32 rows.  Q4_K tiles, which also carry the activations' sub-block sums
+// for the minimum term, take the next budget up.
 template <int CODEC, int MT, int NW, int XT>
 constexpr int gather_waves_per_simd() {
-    constexpr int t = MT * NW;
+    constexpr int t = MT * NW * (CODEC == KQ_CODEC_Q4_K ? 2 : 1);
     if (t == 1 && XT != 2) return 4;
     if (t <= 2 && !(CODEC == KQ_CODEC_Q6_K && XT == 2 && t == 2)) return 3;
     return (t <= 4 && !(XT == 2 && t == 4)) ? 2 : 1;
@@ -469,27 +470,24 @@ __device__ int route_block_scan(int v, int *wsum, int *total) {
 // Stable counting sort of (token, slot) pairs by expert id (the SwitchGLU
 // order): counts in LDS, one workgroup-wide scan for the segment starts and
 // the segment list, then one wave per expert walks the pairs in order and
-// writes its segment, so pairs keep their original order within it.
-__global__ __launch_bounds__(kRouteThreads) void kq_route_kernel(const int32_t *__restrict__ idx, int32_t n_pairs,
-                                                                 int32_t n_experts, int32_t *__restrict__ seg_info,
-                                                                 int32_t *__restrict__ pair_order) {
-    extern __shared__ int32_t sm[];
-    int32_t *count = sm;                    // [E]
-    int32_t *start = sm + n_experts;        // [E]
-    int32_t *ids = sm + 2 * n_experts;      // [n_pairs] when staged
+// writes its segment, so pairs keep their original order within it.  `ids`
+// holds the pairs' expert ids in LDS, or is null (they are read from idx and
+// then from the flag array).  Called by all kRouteThreads threads of the
+// workgroup.
+__device__ void route_pairs(const int32_t *__restrict__ idx, const int32_t *ids, int32_t n_pairs,
+                            int32_t n_experts, int32_t *count, int32_t *start, int32_t *__restrict__ seg_info,
+                            int32_t *__restrict__ pair_order) {
     __shared__ int wsum[kRouteThreads / 64];
     __shared__ int tot_pairs, tot_segs;
     const int tid = threadIdx.x;
-    const bool staged = route_staged(n_pairs, n_experts);
     for (int e = tid; e < n_experts; e += kRouteThreads) count[e] = 0;
     __syncthreads();
     int32_t *flag = pair_order + n_pairs;
     for (int p = tid; p < n_pairs; p += kRouteThreads) {
-        int e = idx[p];
+        int e = ids ? ids[p] : idx[p];
         if (e < 0 || e >= n_experts) e = -1;
         else atomicAdd(&count[e], 1);
         flag[p] = e;
-        if (staged) ids[p] = e;
     }
     __syncthreads();
     // thread t owns experts [t * per, t * per + per)
@@ -525,12 +523,132 @@ __global__ __launch_bounds__(kRouteThreads) void kq_route_kernel(const int32_t *
         int w = start[e];
         for (int q0 = 0; q0 < n_pairs; q0 += 64) {
             const int q = q0 + lane;
-            const bool hit = q < n_pairs && (staged ? ids[q] : flag[q]) == e;
+            int id = -1;
+            if (q < n_pairs) {
+                id = ids ? ids[q] : flag[q];
+                if (id < 0 || id >= n_experts) id = -1;
+            }
+            const bool hit = id == e;
             const uint64_t m = __ballot(hit);
             if (hit) pair_order[w + __popcll(m & below)] = q;
             w += __popcll(m);
         }
     }
+}
+
+// The same sort with O(1) passes over the pairs, when the chunk histograms fit
+// LDS (C = ceil(n_pairs / 64) chunks x n_experts counts beside the counts and
+// starts).  Chunk c (64 consecutive pairs) is one wave's step: ballots over
+// the bits of each lane's expert id give every lane the mask of lanes with
+// the same expert, its rank among them and the chunk's count for that expert
+// (written by the expert's first lane).  Per expert, the counts turn into
+// exclusive prefixes over the chunks; a pair's position is then
+// start[e] + prefix[c][e] + rank, so pairs keep their order within an expert.
+constexpr int kRouteFastMaxPairs = 4 * kRouteThreads;
+
+__host__ __device__ inline bool route_fast(int n_pairs, int n_experts) {
+    const int chunks = (n_pairs + 63) / 64;
+    return n_pairs <= kRouteFastMaxPairs && (int64_t)chunks * n_experts + 2 * n_experts <= kRouteLdsInts;
+}
+
+__device__ void route_pairs_fast(const int32_t *__restrict__ idx, int32_t n_pairs, int32_t n_experts,
+                                 int32_t *count, int32_t *start, int32_t *hist, int32_t *__restrict__ seg_info,
+                                 int32_t *__restrict__ pair_order) {
+    __shared__ int wsum[kRouteThreads / 64];
+    __shared__ int tot_pairs, tot_segs;
+    constexpr int NW = kRouteThreads / 64;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int chunks = (n_pairs + 63) / 64;
+    for (int i = tid; i < chunks * n_experts; i += kRouteThreads) hist[i] = 0;
+    // the lane's pairs: chunk wave + NW * j, j < 4 (n_pairs <= 4 * kRouteThreads)
+    int ex[4], rank[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int p = (wave + NW * j) * 64 + lane;
+        int e = -1;
+        if (p < n_pairs) {
+            e = idx[p];
+            if (e < 0 || e >= n_experts) e = -1;
+            pair_order[n_pairs + p] = e;
+        }
+        ex[j] = e;
+    }
+    // bits of e + 1 (0 for a pair routed nowhere, or past n_pairs)
+    const int nbits = 32 - __builtin_clz((unsigned)n_experts);
+    const uint64_t below = lane ? ~0ull >> (64 - lane) : 0ull;
+    __syncthreads();  // hist zeroed
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int c = wave + NW * j;
+        rank[j] = 0;
+        if (c >= chunks) continue;  // uniform over the wave
+        const uint32_t v = (uint32_t)(ex[j] + 1);
+        uint64_t same = ~0ull;
+        for (int b = 0; b < nbits; ++b) {
+            const bool bit = (v >> b) & 1u;
+            const uint64_t m = __ballot(bit);
+            same &= bit ? m : ~m;
+        }
+        rank[j] = __popcll(same & below);
+        if (ex[j] >= 0 && rank[j] == 0) hist[c * n_experts + ex[j]] = __popcll(same);
+    }
+    __syncthreads();
+    // per expert: exclusive prefix over the chunks, and the total
+    const int per = (n_experts + kRouteThreads - 1) / kRouteThreads;
+    const int e0 = tid * per, e1 = min(e0 + per, n_experts);
+    int tot = 0, nz = 0;
+    for (int e = e0; e < e1; ++e) {
+        int run = 0;
+        for (int c = 0; c < chunks; ++c) {
+            const int h = hist[c * n_experts + e];
+            hist[c * n_experts + e] = run;
+            run += h;
+        }
+        count[e] = run;
+        tot += run;
+        nz += run > 0;
+    }
+    int acc = route_block_scan(tot, wsum, &tot_pairs);
+    int sg = route_block_scan(nz, wsum, &tot_segs);
+    for (int e = e0; e < e1; ++e) {
+        start[e] = acc;
+        if (count[e] > 0) {
+            seg_info[1 + sg] = e;
+            seg_info[1 + n_experts + sg] = acc;
+            ++sg;
+        }
+        acc += count[e];
+    }
+    const int S = tot_segs, P = tot_pairs;
+    if (tid == 0) seg_info[0] = S;
+    for (int i = S + tid; i <= n_experts; i += kRouteThreads) seg_info[1 + n_experts + i] = P;
+    for (int i = S + tid; i < n_experts; i += kRouteThreads) seg_info[1 + i] = -1;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int c = wave + NW * j;
+        if (c < chunks && ex[j] >= 0)
+            pair_order[start[ex[j]] + hist[c * n_experts + ex[j]] + rank[j]] = c * 64 + lane;
+    }
+}
+
+__global__ __launch_bounds__(kRouteThreads) void kq_route_kernel(const int32_t *__restrict__ idx, int32_t n_pairs,
+                                                                 int32_t n_experts, int32_t *__restrict__ seg_info,
+                                                                 int32_t *__restrict__ pair_order) {
+    extern __shared__ int32_t sm[];
+    int32_t *count = sm;                    // [E]
+    int32_t *start = sm + n_experts;        // [E]
+    int32_t *rest = sm + 2 * n_experts;     // chunk histograms, or the pairs' ids when staged
+    if (route_fast(n_pairs, n_experts)) {
+        route_pairs_fast(idx, n_pairs, n_experts, count, start, rest, seg_info, pair_order);
+        return;
+    }
+    const bool staged = route_staged(n_pairs, n_experts);
+    if (staged) {
+        for (int p = threadIdx.x; p < n_pairs; p += kRouteThreads) rest[p] = idx[p];
+        // route_pairs' first barrier orders these writes before any read
+    }
+    route_pairs(idx, staged ? rest : nullptr, n_pairs, n_experts, count, start, seg_info, pair_order);
 }
 
 __global__ void kq_mix_kernel(const float *__restrict__ yp, const float *__restrict__ sc, int32_t T,
@@ -563,90 +681,148 @@ __device__ __forceinline__ float router_load(const void *p, int dt, int64_t i) {
                                 : kq_bf16_bits_to_f32(((const uint16_t *)p)[i]);
 }
 
-// Router: one wave per token, in fp32.
+// Cross-lane steps of the router's reductions: DPP moves inside each row of
+// 16 lanes (pair swap, quad swap, half-row mirror, row mirror), after which
+// every lane of a row holds the row's result, and four lane reads combine the
+// rows in row order.  DPP moves are VALU operations with a few cycles of
+// latency, against an LDS round trip per step for a lane shuffle.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_row(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, 0xF, 0xF, false);
+}
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+    v = fmaxf(v, __uint_as_float(dpp_row<0xB1>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(dpp_row<0x4E>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(dpp_row<0x141>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(dpp_row<0x140>(__float_as_uint(v))));
+    float r = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 0));
+#pragma unroll
+    for (int q = 1; q < 4; ++q) r = fmaxf(r, __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 16 * q)));
+    return r;
+}
+
+__device__ __forceinline__ float wave_sum_f32(float v) {
+    v += __uint_as_float(dpp_row<0xB1>(__float_as_uint(v)));
+    v += __uint_as_float(dpp_row<0x4E>(__float_as_uint(v)));
+    v += __uint_as_float(dpp_row<0x141>(__float_as_uint(v)));
+    v += __uint_as_float(dpp_row<0x140>(__float_as_uint(v)));
+    float r = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 0));
+#pragma unroll
+    for (int q = 1; q < 4; ++q) r += __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 16 * q));
+    return r;
+}
+
+// A pick candidate as a 64-bit key (hi, lo): hi orders the selection score
+// (larger float -> larger key; NaN lowest), lo = ~expert so that equal scores
+// rank the lower expert id first.  Key (0, 0) is below every candidate.
+__device__ __forceinline__ uint32_t f32_order(float f) {
+    const uint32_t b = __float_as_uint(f);
+    if (f != f) return 0u;
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ __forceinline__ void key_max(uint32_t &hi, uint32_t &lo, uint32_t ohi, uint32_t olo) {
+    const bool t = ohi > hi || (ohi == hi && olo > lo);
+    hi = t ? ohi : hi;
+    lo = t ? olo : lo;
+}
+
+template <int CTRL>
+__device__ __forceinline__ void key_dpp(uint32_t &hi, uint32_t &lo) {
+    const uint32_t ohi = dpp_row<CTRL>(hi), olo = dpp_row<CTRL>(lo);
+    key_max(hi, lo, ohi, olo);
+}
+
+// The wave's largest key, uniform over the wave.
+__device__ __forceinline__ void wave_max_key(uint32_t &hi, uint32_t &lo) {
+    key_dpp<0xB1>(hi, lo);
+    key_dpp<0x4E>(hi, lo);
+    key_dpp<0x141>(hi, lo);
+    key_dpp<0x140>(hi, lo);
+    uint32_t bh = __builtin_amdgcn_readlane(hi, 0), bl = __builtin_amdgcn_readlane(lo, 0);
+#pragma unroll
+    for (int q = 1; q < 4; ++q)
+        key_max(bh, bl, __builtin_amdgcn_readlane(hi, 16 * q), __builtin_amdgcn_readlane(lo, 16 * q));
+    hi = bh;
+    lo = bl;
+}
+
+// Router of one token on one wave, in fp32 (E <= 64 * NPER experts, expert
+// lane + 64 i in slot i of each lane).
 //   score_e = softmax over the E routed logits (max-subtracted), sigmoid, or
 //             sqrt(softplus) with softplus(x) = max(x, 0) + log1p(exp(-|x|));
 //   picks   = top-k of score_e + bias_e by repeated arg-max (ties -> lower
 //             expert id), reported with their unbiased scores;
-//   weights = picks / (sum of picks + 1e-20) when normalising, then times
-//             per_expert_scale[e] and scale;
+//   weights = picks / (sum of picks, in pick order, + 1e-20) when
+//             normalising, then times per_expert_scale[e] and scale;
 //   shared_gate: logit column E is the shared expert's gate, appended to the
 //             weights as sigmoid(logit) (k + 1 weights per token).
-__global__ __launch_bounds__(64) void kq_router_kernel(RouterArgs a) {
-    const int t = blockIdx.x;
-    const int lane = kq_lane();
-    constexpr int kMaxPerLane = 16;  // E <= 1024
+template <int NPER>
+__device__ __forceinline__ void router_token(const RouterArgs &a, int t, int lane) {
     const int E = a.E;
     const int64_t row = (int64_t)t * a.ld;
-    float v[kMaxPerLane], sel[kMaxPerLane];
-    float mx = -INFINITY;
+    float v[NPER], bias[NPER];
 #pragma unroll
-    for (int i = 0; i < kMaxPerLane; ++i) {
+    for (int i = 0; i < NPER; ++i) {
         const int e = lane + 64 * i;
-        const float x = e < E ? router_load(a.logits, a.ldt, row + e) : -INFINITY;
-        v[i] = x;
-        mx = fmaxf(mx, x);
+        v[i] = e < E ? router_load(a.logits, a.ldt, row + e) : -INFINITY;
+        bias[i] = (a.bias && e < E) ? router_load(a.bias, a.bias_dt, e) : 0.f;
     }
     if (a.scoring == KQ_SCORE_SOFTMAX) {
-        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+        float mx = v[0];
+#pragma unroll
+        for (int i = 1; i < NPER; ++i) mx = fmaxf(mx, v[i]);
+        mx = wave_max_f32(mx);
         float sum = 0.f;
 #pragma unroll
-        for (int i = 0; i < kMaxPerLane; ++i) {
+        for (int i = 0; i < NPER; ++i) {
             const int e = lane + 64 * i;
             v[i] = e < E ? expf(v[i] - mx) : 0.f;
             sum += v[i];
         }
-        for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+        sum = wave_sum_f32(sum);
 #pragma unroll
-        for (int i = 0; i < kMaxPerLane; ++i) v[i] = v[i] / sum;
+        for (int i = 0; i < NPER; ++i) v[i] = v[i] / sum;
     } else if (a.scoring == KQ_SCORE_SIGMOID) {
 #pragma unroll
-        for (int i = 0; i < kMaxPerLane; ++i) v[i] = 1.f / (1.f + expf(-v[i]));
+        for (int i = 0; i < NPER; ++i) v[i] = 1.f / (1.f + expf(-v[i]));
     } else {
 #pragma unroll
-        for (int i = 0; i < kMaxPerLane; ++i) {
+        for (int i = 0; i < NPER; ++i) {
             const float x = v[i];
             v[i] = sqrtf(fmaxf(x, 0.f) + log1pf(expf(-fabsf(x))));
         }
     }
+    uint32_t khi[NPER], klo[NPER];
 #pragma unroll
-    for (int i = 0; i < kMaxPerLane; ++i) {
+    for (int i = 0; i < NPER; ++i) {
         const int e = lane + 64 * i;
-        sel[i] = e < E ? v[i] + (a.bias ? router_load(a.bias, a.bias_dt, e) : 0.f) : -INFINITY;
+        khi[i] = e < E ? f32_order(v[i] + bias[i]) : 0u;
+        klo[i] = e < E ? ~(uint32_t)e : 0u;
     }
     float picked_sum = 0.f, my_score = 0.f;
     int my_ind = 0;
-    uint32_t taken = 0;  // bit i: expert lane + 64 i already picked
     for (int j = 0; j < a.k; ++j) {
-        float best = -INFINITY, best_v = 0.f;
-        int bi = 0x7FFFFFFF;
+        uint32_t bh = khi[0], bl = klo[0];
 #pragma unroll
-        for (int i = 0; i < kMaxPerLane; ++i) {
-            const int e = lane + 64 * i;
-            if (e < E && !((taken >> i) & 1u) && (sel[i] > best || (sel[i] == best && e < bi))) {
-                best = sel[i];
-                best_v = v[i];
-                bi = e;
+        for (int i = 1; i < NPER; ++i) key_max(bh, bl, khi[i], klo[i]);
+        wave_max_key(bh, bl);
+        const int e = (int)~bl;  // uniform
+        float sv = 0.f;
+#pragma unroll
+        for (int i = 0; i < NPER; ++i) {
+            if (lane + 64 * i == e) {
+                sv = v[i];
+                khi[i] = 0u;
+                klo[i] = 0u;
             }
         }
-        for (int off = 32; off > 0; off >>= 1) {
-            const float ob = __shfl_xor(best, off);
-            const float ov = __shfl_xor(best_v, off);
-            const int oi = __shfl_xor(bi, off);
-            if (ob > best || (ob == best && oi < bi)) {
-                best = ob;
-                best_v = ov;
-                bi = oi;
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < kMaxPerLane; ++i)
-            if (lane + 64 * i == bi) taken |= 1u << i;
+        const float best_v = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(sv), e & 63));
         picked_sum += best_v;
-        // lane j keeps pick j (best_v / bi are uniform over the wave here)
         if (lane == j) {
             my_score = best_v;
-            my_ind = bi;
+            my_ind = e;
         }
     }
     // one store per output array; picks are renormalised from registers
@@ -662,6 +838,12 @@ __global__ __launch_bounds__(64) void kq_router_kernel(RouterArgs a) {
         const float g = router_load(a.logits, a.ldt, row + E);
         a.scores[(int64_t)t * sld + a.k] = 1.f / (1.f + expf(-g));
     }
+}
+
+// One wave per token.
+template <int NPER>
+__global__ __launch_bounds__(64) void kq_router_kernel(RouterArgs a) {
+    router_token<NPER>(a, blockIdx.x, kq_lane());
 }
 
 // ---------------------------------------------------------------- host
@@ -1136,7 +1318,9 @@ int kq_moe_route(const int32_t *idx, int32_t n_pairs, int32_t n_experts, int32_t
                  int32_t *pair_order, kq_stream_t stream) {
     if (!idx || !seg_info || !pair_order) return KQ_ERR_NULL_POINTER;
     if (n_pairs < 0 || n_experts <= 0 || n_experts > 4096) return KQ_ERR_BAD_SHAPE;
-    const size_t smem = ((size_t)2 * n_experts + (route_staged(n_pairs, n_experts) ? n_pairs : 0)) * sizeof(int32_t);
+    const size_t rest = route_fast(n_pairs, n_experts) ? (size_t)((n_pairs + 63) / 64) * n_experts
+                        : route_staged(n_pairs, n_experts) ? (size_t)n_pairs : 0;
+    const size_t smem = ((size_t)2 * n_experts + rest) * sizeof(int32_t);
     hipLaunchKernelGGL(kq_route_kernel, dim3(1), dim3(kRouteThreads), smem, (hipStream_t)stream, idx, n_pairs,
                        n_experts, seg_info, pair_order);
     return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
@@ -1194,9 +1378,11 @@ int kq_moe_mix(const float *y_pairs, const float *scores, int32_t T, int32_t top
     return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
 }
 
-int kq_moe_router_topk(const void *logits, int logits_dtype, int64_t logits_row_stride, int32_t T, int32_t E,
-                       int32_t k, const kq_router_options *opts, int32_t *inds, float *scores,
-                       kq_stream_t stream) {
+}  // extern "C"
+
+// Validates a router call and fills its arguments (KQ_OK or a status).
+static int router_args(const void *logits, int logits_dtype, int64_t logits_row_stride, int32_t T, int32_t E,
+                       int32_t k, const kq_router_options *opts, int32_t *inds, float *scores, RouterArgs &a) {
     if (!logits || !inds || !scores) return KQ_ERR_NULL_POINTER;
     const kq_router_options dflt{1, 0, KQ_SCORE_SOFTMAX, 1.f, nullptr, KQ_DTYPE_F32, nullptr, KQ_DTYPE_F32};
     const kq_router_options &o = opts ? *opts : dflt;
@@ -1208,8 +1394,6 @@ int kq_moe_router_topk(const void *logits, int logits_dtype, int64_t logits_row_
         (o.per_expert_scale && !dt_ok(o.per_expert_scale_dtype)))
         return KQ_ERR_UNSUPPORTED_DTYPE;
     if (o.scoring < KQ_SCORE_SOFTMAX || o.scoring > KQ_SCORE_SQRTSOFTPLUS) return KQ_ERR_BAD_ARGUMENT;
-    if (T == 0) return KQ_OK;
-    RouterArgs a;
     a.logits = logits;
     a.ld = logits_row_stride;
     a.ldt = logits_dtype;
@@ -1225,7 +1409,24 @@ int kq_moe_router_topk(const void *logits, int logits_dtype, int64_t logits_row_
     a.pes_dt = o.per_expert_scale_dtype;
     a.inds = inds;
     a.scores = scores;
-    hipLaunchKernelGGL(kq_router_kernel, dim3(T), dim3(64), 0, (hipStream_t)stream, a);
+    return KQ_OK;
+}
+
+extern "C" {
+
+int kq_moe_router_topk(const void *logits, int logits_dtype, int64_t logits_row_stride, int32_t T, int32_t E,
+                       int32_t k, const kq_router_options *opts, int32_t *inds, float *scores,
+                       kq_stream_t stream) {
+    RouterArgs a;
+    const int st = router_args(logits, logits_dtype, logits_row_stride, T, E, k, opts, inds, scores, a);
+    if (st != KQ_OK) return st;
+    if (T == 0) return KQ_OK;
+    const hipStream_t s = (hipStream_t)stream;
+    if (E <= 64) hipLaunchKernelGGL(kq_router_kernel<1>, dim3(T), dim3(64), 0, s, a);
+    else if (E <= 128) hipLaunchKernelGGL(kq_router_kernel<2>, dim3(T), dim3(64), 0, s, a);
+    else if (E <= 256) hipLaunchKernelGGL(kq_router_kernel<4>, dim3(T), dim3(64), 0, s, a);
+    else if (E <= 512) hipLaunchKernelGGL(kq_router_kernel<8>, dim3(T), dim3(64), 0, s, a);
+    else hipLaunchKernelGGL(kq_router_kernel<16>, dim3(T), dim3(64), 0, s, a);
     return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
 }
 

@@ -230,10 +230,6 @@ constexpr int slot_bytes() {
     return producer_loads<SC, NB>() * kProducers * 1024;
 }
 
-// s_waitcnt vmcnt(n) (0 <= n <= 63) leaving the other counters unconstrained
-// (gfx9 encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14).
-#define KQ_VMCNT(n) (((n) & 0xF) | ((((n) >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8))
-
 // Wait until at most `newer` tiles of PL loads each are still in flight
 // (K: the most the ring can hold, within the counter's 63).
 template <int PL, int K>

@@ -129,7 +129,7 @@ class _Workspaces:
 
 
 _WS = _Workspaces()
-_COUNTS = {"fused_mlp_launches": 0}
+_COUNTS = {"fused_mlp_launches": 0, "route_launches": 0}
 
 
 # ------------------------------------------------------------ capabilities
@@ -279,8 +279,8 @@ def fused_mlp(x, gate_w, up_w, down_w, codec="q4_k", down_codec=None, act="silu"
 
 
 def counts():
-    """Calls that took the single-launch forms since import
-    ({"fused_mlp_launches": n})."""
+    """Launch counts since import: the single-launch fused MLP
+    ("fused_mlp_launches") and the expert sorts ("route_launches")."""
     return dict(_COUNTS)
 
 
@@ -337,6 +337,7 @@ def moe_route(idx, n_experts):
     order = torch.empty(max(2 * P, 1), dtype=torch.int32, device=idx.device)
     check("kq_moe_route", lib().kq_moe_route(idx32.data_ptr(), P, n_experts, seg.data_ptr(), order.data_ptr(),
                                              _stream(idx)))
+    _COUNTS["route_launches"] += 1
     return seg, order
 
 
@@ -361,13 +362,18 @@ class _RouteMemo:
                 idx.device.index, stream_handle, torch.cuda.is_current_stream_capturing())
 
     def take(self, idx, n_experts, stream_handle):
-        hit = self._d.pop(self._key(idx, n_experts, stream_handle), None)
-        if hit is not None:
-            return hit[1], hit[2]
-        return None
+        key = self._key(idx, n_experts, stream_handle)
+        hit = self._d.get(key)
+        if hit is None:
+            return None
+        if hit[3] > 1:
+            self._d[key] = (hit[0], hit[1], hit[2], hit[3] - 1)
+        else:
+            del self._d[key]
+        return hit[1], hit[2]
 
-    def put(self, idx, n_experts, stream_handle, seg, order):
-        self._d[self._key(idx, n_experts, stream_handle)] = (idx, seg, order)
+    def put(self, idx, n_experts, stream_handle, seg, order, uses=1):
+        self._d[self._key(idx, n_experts, stream_handle)] = (idx, seg, order, uses)
         if len(self._d) > self._size:
             self._d.popitem(last=False)
 
@@ -704,12 +710,13 @@ def moe_router_topk(logits, k, norm_topk_prob=True, shared_gate=True, per_expert
                               None if pes is None else pes.data_ptr(), pdt or 0)
     inds = torch.empty((t, k), dtype=torch.int32, device=logits.device)
     scores = torch.empty((t, k + sg), dtype=torch.float32, device=logits.device)
+    lead = logits.shape[:-1]
+    out = inds.reshape(*lead, k)
     if t:
         check("kq_moe_router_topk",
               lib().kq_moe_router_topk(l2.data_ptr(), _dt(l2.dtype), l2.stride(0) if t > 1 else C, t, E, k,
                                        ctypes.byref(opts), inds.data_ptr(), scores.data_ptr(), _stream(logits)))
-    lead = logits.shape[:-1]
-    return inds.reshape(*lead, k), scores.reshape(*lead, k + sg)
+    return out, scores.reshape(*lead, k + sg)
 
 
 # --------------------------------------------------------------- attention

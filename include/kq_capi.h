@@ -179,12 +179,13 @@ int kq_fused_mlp(const void *x, int x_dtype, int64_t x_row_stride, int32_t M, in
 /* ---- MoE expert gather ------------------------------------------------- */
 /* Device-side routing of (token, slot) pairs to experts.  idx [n_pairs]
  * int32 expert ids (row-major [T, k]).  Writes:
- *   seg_info  int32 [3 + 2*n_experts]: [0] = number of non-empty experts S,
+ *   seg_info  int32 [2 + 2*n_experts]: [0] = number of non-empty experts S,
  *             then seg_expert[n_experts], seg_start[n_experts + 1];
- *   pair_order int32 [n_pairs]: pair ids grouped by expert (ascending expert,
- *             ascending pair id inside an expert) -- the stable sort gmlx's
- *             SwitchGLU applies at indices.size >= 64
- *             (gmlx/modules.py:1308-1310).
+ *   pair_order int32 [2 * n_pairs]: pair ids grouped by expert (ascending
+ *             expert, ascending pair id inside an expert) -- the stable sort
+ *             gmlx's SwitchGLU applies at indices.size >= 64
+ *             (gmlx/modules.py:1308-1310) -- then each pair's expert id, or
+ *             -1 for an id out of range.
  * Expert ids outside [0, n_experts) are rejected on device: they are routed
  * to no segment and their outputs are written as zeros. */
 int kq_moe_route(const int32_t *idx, int32_t n_pairs, int32_t n_experts, int32_t *seg_info,

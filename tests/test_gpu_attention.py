@@ -230,3 +230,58 @@ def test_head_dim_512(B, Hq, Hkv, dtype_name):
     assert okq.max_rel(out8.float().cpu().numpy()[:, :, 0], ref8) <= tol
     # the ragged route keeps the reference's head dims and declines 512
     assert ops.ragged_decode_attention(q.cuda(), k16.cuda(), v16.cuda(), starts, scale) is None
+
+
+@pytest.mark.parametrize("split", [None, "512", "1024"])
+@pytest.mark.parametrize("dtype_name", ["float16", "bfloat16"])
+def test_batch_row_equals_single_row(split, dtype_name, monkeypatch):
+    """Row b of a batched call is bitwise the same call made on row b alone:
+    the reference's same-bucket property (tests/test_ragged_decode.py:94-114,
+    one plan for the batch and for each row, no drift at all).  Covered:
+    ragged_decode_attention on [B, Hkv, L, D] with the reference's live pads
+    (:97), sdpa_decode_gqa with device starts over the 16-bit and the 8-bit
+    affine cache, and the per-row slab layout.  Splits run 512 or 1024 tokens
+    by the launch's size, so the batched and the single-row call are also
+    compared with the split forced either way."""
+    import torch
+    from gmlx_amd import ops
+    from helpers import q8_affine
+    if split is not None:
+        monkeypatch.setenv("GMLX_KQ_SDPA_SPLIT", split)
+    tdt = getattr(torch, dtype_name)
+    rng = np.random.default_rng(94)
+    B, Hq, Hkv, L, D = 3, 32, 8, 14772, 128
+    pads = [248, 217, 0]
+    q, k, v = _padded(rng, B, Hq, Hkv, L, D, tdt)
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    print(f"batch-row ragged split={split} {dtype_name}", flush=True)
+    full = ops.ragged_decode_attention(qd, kd, vd, pads, D ** -0.5)
+    assert full is not None
+    for b in range(B):
+        one = ops.ragged_decode_attention(qd[b:b + 1], kd[b:b + 1], vd[b:b + 1], pads[b:b + 1], D ** -0.5)
+        assert torch.equal(one[0], full[b]), ("ragged", b)
+    starts = torch.tensor(pads, dtype=torch.int32, device="cuda")
+    full = ops.sdpa_decode_gqa(qd, kd, vd, D ** -0.5, starts=starts)
+    for b in range(B):
+        one = ops.sdpa_decode_gqa(qd[b:b + 1], kd[b:b + 1], vd[b:b + 1], D ** -0.5, starts=starts[b:b + 1])
+        assert torch.equal(one[0], full[b]), ("starts", b)
+    Lq = 3000  # the 8-bit affine cache
+    kw, ks, kb, _ = q8_affine(k[:, :, :Lq].float().numpy(), dtype_name)
+    vw, vs, vb, _ = q8_affine(v[:, :, :Lq].float().numpy(), dtype_name)
+    kw, ks, kb, vw, vs, vb = (t.cuda() for t in (kw, ks, kb, vw, vs, vb))
+    full = ops.sdpa_decode_gqa(qd, kw, vw, D ** -0.5, starts=starts, k_scales=ks, k_biases=kb,
+                               v_scales=vs, v_biases=vb)
+    for b in range(B):
+        sl = slice(b, b + 1)
+        one = ops.sdpa_decode_gqa(qd[sl], kw[sl], vw[sl], D ** -0.5, starts=starts[sl], k_scales=ks[sl],
+                                  k_biases=kb[sl], v_scales=vs[sl], v_biases=vb[sl])
+        assert torch.equal(one[0], full[b]), ("q8", b)
+    if dtype_name == "float16":
+        lens = [1, 700, 2500, 0, 1333]
+        offs, ks_, vs_, kf, vf = _slabs(rng, lens, Hkv, D)
+        qs = torch.from_numpy(rng.normal(0, 1, size=(len(lens), Hq, D)).astype(np.float16)).cuda()
+        kf, vf = torch.from_numpy(kf).cuda(), torch.from_numpy(vf).cuda()
+        full = ops.sdpa_decode_slabs(qs, kf, vf, offs, lens, Hkv, D ** -0.5)
+        for b in range(len(lens)):
+            one = ops.sdpa_decode_slabs(qs[b:b + 1], kf, vf, offs[b:b + 1], lens[b:b + 1], Hkv, D ** -0.5)
+            assert torch.equal(one[0], full[b]), ("slabs", b)

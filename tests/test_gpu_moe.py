@@ -22,10 +22,13 @@ def _experts(rng, codec, E, N, K):
     return np.stack([quantized_weights(rng, codec, N, K) for _ in range(E)])
 
 
-@pytest.mark.parametrize("E,T,k", [(16, 37, 4), (128, 32, 8), (2000, 300, 8), (4096, 1250, 8), (256, 1, 8)])
+@pytest.mark.parametrize("E,T,k", [(16, 37, 4), (128, 32, 8), (2000, 300, 8), (4096, 1250, 8), (256, 1, 8),
+                                   (4, 64, 4), (1024, 8, 8), (60, 64, 6), (128, 512, 8), (3, 700, 2)])
 def test_route_groups_pairs_stably(E, T, k):
     """Stable counting sort by expert: segment list, starts and pair order
-    (ids in LDS, more experts than threads, ids past LDS, out-of-range ids)."""
+    (per-chunk ranks with the chunk histograms in LDS; more experts than
+    threads; histograms past LDS, the ballot-per-expert form; heavy
+    duplication inside a 64-pair chunk; out-of-range ids)."""
     from gmlx_amd import ops
     rng = np.random.default_rng(E + T)
     idx = rng.integers(0, E, size=(T, k)).astype(np.int32)
@@ -471,3 +474,55 @@ def test_kquant_embedding(codec, dtype_name):
     logits = emb.as_linear(_dev(x)).float().cpu().numpy()
     ref = x.astype(np.float64) @ deq.astype(np.float64).T
     assert okq.max_rel(logits, ref) <= TOL
+
+
+
+@pytest.mark.parametrize("dcodec,T,k,E,I,N,bad", [
+    ("q6_k", 32, 8, 128, 768, 2048, False),   # C4's down
+    ("iq2_xxs", 8, 8, 64, 2048, 1024, False),
+    ("q4_k", 5, 4, 6, 256, 200, True),        # a partial last tile; out-of-range experts give zero rows
+    ("q6_k", 40, 8, 16, 512, 2048, False),
+    ("q4_k", 3, 2, 4, 4096, 64, True),        # 16 super-blocks per row: the split-K gather
+])
+@pytest.mark.parametrize("hdt", ["float32", "float16"])
+def test_down_gather_with_mix_equals_two_steps(dcodec, T, k, E, I, N, bad, hdt):
+    """gather_qmv_mix_ns_kq bitwise equal to the per-pair gather followed by
+    the slot-ordered fp32 mix written out in torch; repeated calls and graph
+    replays bitwise equal; and within tolerance of fp64
+    (gmlx/modules.py:591-593)."""
+    import torch
+    from gmlx_amd import ops
+    rng = np.random.default_rng(T * 31 + k + E + I)
+    dw = _dev(_experts(rng, dcodec, E, N, I))
+    idx_np = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    if bad:
+        idx_np[0, 1], idx_np[-1, 0] = -1, E + 3
+    idx = _dev(idx_np)
+    sc = torch.from_numpy(rng.uniform(0.1, 1.0, size=(T, k)).astype(np.float32)).cuda()
+    h = torch.from_numpy(rng.normal(0, 1, size=(T, k, I)).astype(np.float32)).to(getattr(torch, hdt)).cuda()
+    print(f"mix {dcodec} T={T} k={k} E={E} I={I} N={N} {hdt}", flush=True)
+    yp = ops.gather_qmv_kq(h, dw, dcodec, idx)                       # (T, k, N) fp32
+    want = torch.zeros((T, N), dtype=torch.float32, device="cuda")
+    for s in range(k):
+        want = want + sc[:, s:s + 1] * yp[:, s]
+    outs = [ops.gather_qmv_mix_ns_kq(h, dw, dcodec, idx, sc) for _ in range(3)]
+    for o in outs:
+        assert torch.equal(o, want)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        og = ops.gather_qmv_mix_ns_kq(h, dw, dcodec, idx, sc)
+    for _ in range(3):
+        ops.gather_qmv_mix_ns_kq(h, dw, dcodec, idx, sc)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(og, want)
+    D = okq.dequantize(dw.cpu().numpy(), dcodec).reshape(E, N, I).astype(np.float64)
+    hf = h.double().cpu().numpy()
+    ref = np.zeros((T, N))
+    for t in range(T):
+        for s, e in enumerate(idx_np[t]):
+            if 0 <= e < E:
+                ref[t] += float(sc[t, s]) * (D[e] @ hf[t, s])
+    assert okq.max_rel(want.cpu().numpy(), ref) <= TOL
