@@ -155,6 +155,17 @@ struct Block<KQ_CODEC_Q4_K> {
         return cat8(a0 * s, a1 * s, a2 * s, a3 * s);
     }
     __device__ __forceinline__ float dscale() const { return d; }
+    // The integer minimum m of sub-block t (0..63, exact in fp16) in all eight
+    // values: as the B operand of step t against the activation fragment it
+    // gives m_t * (sum of the step's 32 activations) per row, a chain that
+    // folds in with -dmin.
+    __device__ __forceinline__ half8_t min_frag(int t) const {
+        const uint32_t b = (uint32_t)(t & 3);
+        const half2_t k1024 = {(_Float16)1024.f, (_Float16)1024.f};
+        const uint32_t sel = b | (4u << 8) | (b << 16) | (4u << 24);  // byte t of the word under 0x64 bytes
+        const half2_t m = h2b(__builtin_amdgcn_perm(0x64646464u, t < 4 ? mlo : mhi, sel)) - k1024;
+        return cat8(m, m, m, m);
+    }
     // -dmin * m of sub-blocks 2g and 2g + 1 (exact in fp32): the B operand of
     // the minimum MFMAs (min_accumulate)
     __device__ __forceinline__ void min_b(int g, float &b0, float &b1) const {

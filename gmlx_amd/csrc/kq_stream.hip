@@ -918,7 +918,10 @@ struct MmsGeo {
     static constexpr int SB = XB + WL * 1024;                                     // stage bytes
     // Q4_K forms: the stage's activation sub-block sums, float2 per lane per
     // 16-row block (sub-blocks 2g, 2g + 1 of the lane's row), after the ring
-    static constexpr bool SUMS = CODEC != KQ_CODEC_Q6_K;
+    static constexpr bool SUMS = CODEC != KQ_CODEC_Q6_K && MT == 4;
+    // two-block forms: the minimum term as a second MFMA chain against the
+    // integer minimums (mms_tile_stage), no sums
+    static constexpr bool MINC = CODEC != KQ_CODEC_Q6_K && MT != 4;
     static constexpr int SUMB = SUMS ? 2 * MT * 64 * 8 : 0;  // two stages (parity)
 };
 
@@ -1037,13 +1040,16 @@ __device__ __forceinline__ void mms_copy(KArgs A, int j, int wave, int lane, int
 
 // One stage of one tile: the chains P[m] = x rows 16 m .. 16 m + 15
 // (super-block of the stage) . the tile's integer weight fragments (rows at
-// wrow, RCW chunks apart), the block's factor d and, for Q4_K, the minimum
-// term's B operand (-dmin m of sub-blocks 2g, 2g + 1) in b0, b1.  The caller
+// wrow, RCW chunks apart) and the block's factor d.  Q4_K's minimum term:
+// with MINC, a second chain Pm[m] = the same rows . the integer minimums
+// (Block::min_frag) and its factor nd = -dmin; otherwise the B operand of
+// the sums' form (-dmin m of sub-blocks 2g, 2g + 1) in b0, b1.  The caller
 // folds them into its accumulators after the next barrier, when the chains
 // have long completed.
-template <int CODEC, int MT>
-__device__ __forceinline__ void mms_tile_stage(floatx4 (&P)[MT], uint32_t base, uint32_t wrow, int r, int g,
-                                               const Iq2Tables &iq2_tab, float &d, float &b0, float &b1) {
+template <int CODEC, int MT, bool MINC>
+__device__ __forceinline__ void mms_tile_stage(floatx4 (&P)[MT], floatx4 (&Pm)[MT], uint32_t base, uint32_t wrow,
+                                               int r, int g, const Iq2Tables &iq2_tab, float &d, float &nd, float &b0,
+                                               float &b1) {
     // activation fragments one step ahead of their MFMAs (the reads of step
     // t + 1 in flight while step t multiplies)
     const uint32_t xrow = base + (uint32_t)(r * 512);
@@ -1068,9 +1074,19 @@ __device__ __forceinline__ void mms_tile_stage(floatx4 (&P)[MT], uint32_t base, 
         for (int m = 0; m < MT; ++m)
             P[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, xq[t & 1][m]), wf,
                                                           t == 0 ? fzero4() : P[m], 0, 0, 0);
+        if constexpr (CODEC == KQ_CODEC_Q4_K && MINC) {
+            const half8_t mf = blk.min_frag(t);
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+                Pm[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, xq[t & 1][m]), mf,
+                                                               t == 0 ? fzero4() : Pm[m], 0, 0, 0);
+        }
     }
     d = blk.dscale();
-    if constexpr (CODEC == KQ_CODEC_Q4_K) blk.min_b(g, b0, b1);
+    if constexpr (CODEC == KQ_CODEC_Q4_K) {
+        if constexpr (MINC) nd = -blk.dmin;
+        else blk.min_b(g, b0, b1);
+    }
 }
 
 // Producer side of the Q4_K minimum term: the sub-block sums of 16-row
@@ -1180,14 +1196,20 @@ __global__ __launch_bounds__(64 * (kMmsProducers + C)) void kq_mms_kernel(Stream
         // The previous stage's chains, folded in after the next barrier (the
         // MFMAs have completed by then); Q4_K: its minimum term too, whose
         // sums the producers wrote during that stage
-        floatx4 P[MT];
-        float pd = 0.f;
+        floatx4 P[MT], Pm[MT];
+        float pd = 0.f, pnd = 0.f;
         [[maybe_unused]] float pb0 = 0.f, pb1 = 0.f;
         bool pending = false;
         [[maybe_unused]] bool pmin = false;
         auto fold_prev = [&](int stage) {
 #pragma unroll
             for (int m = 0; m < MT; ++m) acc[m] = fold4(pd, P[m], acc[m]);
+            if constexpr (MG::MINC) {
+                if (pmin) {
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) acc[m] = fold4(pnd, Pm[m], acc[m]);
+                }
+            }
             if constexpr (MG::SUMS) {
                 if (pmin) {
                     const float2 *sums = (const float2 *)(smem + R * MG::SB) + (stage & 1) * MT * 64;
@@ -1207,10 +1229,13 @@ __global__ __launch_bounds__(64 * (kMmsProducers + C)) void kq_mms_kernel(Stream
             if (c < w.nt) {
                 const uint32_t wrow = base + MG::XB + (uint32_t)(c * 16 + r) * pitch;
                 if constexpr (CODEC == KQ_MIX) {
-                    if (q6) mms_tile_stage<KQ_CODEC_Q6_K, MT>(P, base, wrow, r, g, iq2_tab, pd, pb0, pb1);
-                    else mms_tile_stage<KQ_CODEC_Q4_K, MT>(P, base, wrow, r, g, iq2_tab, pd, pb0, pb1);
+                    if (q6)
+                        mms_tile_stage<KQ_CODEC_Q6_K, MT, false>(P, Pm, base, wrow, r, g, iq2_tab, pd, pnd, pb0, pb1);
+                    else
+                        mms_tile_stage<KQ_CODEC_Q4_K, MT, MG::MINC>(P, Pm, base, wrow, r, g, iq2_tab, pd, pnd, pb0,
+                                                                     pb1);
                 } else {
-                    mms_tile_stage<CODEC, MT>(P, base, wrow, r, g, iq2_tab, pd, pb0, pb1);
+                    mms_tile_stage<CODEC, MT, MG::MINC>(P, Pm, base, wrow, r, g, iq2_tab, pd, pnd, pb0, pb1);
                 }
                 kq_mfma_drain();
             }
