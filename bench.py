@@ -100,11 +100,13 @@ def make_inputs(torch, rng, B):
 # whole 16-row tiles into an LDS ring with direct-to-LDS loads, eight waves
 # dequantize and run the MFMA on one K-slab each), and so does down (K = 12288
 # Q6_K) in six K slices of 8 super-blocks, the last slice of each tile to
-# finish summing the six partial tiles; q|k|v (Q4_K and Q6_K tiles in one
-# launch) takes it in two K slices (768 items, four consumers of two
-# super-blocks); o (one tile per CU) takes the LDS-staged persistent kernel as
-# two 8-wave workgroups per CU.  At B = 9..16 the same routing holds with the
-# streaming kernel's 16-row forms (down in four K slices of 12 super-blocks).
+# finish summing the six partial tiles; q|k|v and o (one or two tiles per CU)
+# take the one-shot kernel (every wave copies one super-block column of its
+# workgroup's tiles and its activation slab into LDS at entry and multiplies
+# as soon as its own loads land; one barrier before the partial-tile sum).
+# At B = 9..16 q|k|v and gate|up take the streaming kernel's 16-row forms
+# (q|k|v in two K slices, down in four K slices of 12 super-blocks) and o the
+# LDS-staged persistent kernel (two 8-wave workgroups per CU).
 # At B = 17..64 q|k|v, gate|up and down take the mid-batch streaming kernel
 # (four waves copy each super-block of the activation rows and of a group of
 # six weight tiles into an LDS ring, six waves each accumulate one tile over
@@ -116,7 +118,7 @@ LAUNCHES = [("qkv", ("q", "k", "v")), ("o", ("o",)), ("gate_up", ("gate", "up"))
 CODEC = {name: codec for name, _, _, codec in LAYER}
 DIMS = {name: (N, K) for name, N, K, _ in LAYER}
 # kernel families, as rocprofv3 names them
-KERNEL_FAMILIES = ("kq_stream_kernel", "kq_mms_kernel", "kq_mv_kernel", "kq_mm_kernel",
+KERNEL_FAMILIES = ("kq_stream_kernel", "kq_shot_kernel", "kq_mms_kernel", "kq_mv_kernel", "kq_mm_kernel",
                    "kq_dense_grouped_kernel")
 
 
@@ -138,10 +140,12 @@ def kernel_of(launch, B):
     if B <= 16 and launch == "down":  # K = 12288 in slices, one super-block per consumer
         # up to 8 rows: six slices of 8; 9..16 rows: four slices of 12 (two ring slots)
         return "kq_stream_kernel<14, 1, 8, 3, 8>" if B <= 8 else "kq_stream_kernel<14, 1, 12, 2, 16>"
+    if B <= 8 and launch in ("qkv", "o"):  # kq_shot_kernel<super-blocks per row>
+        return "kq_shot_kernel<16>"
     if launch == "qkv":  # Q4_K q|k with Q6_K v: the mixed form (codec id 127) in two K slices
-        return f"kq_stream_kernel<127, 2, 4, 4, {8 if B <= 8 else 16}>"
+        return "kq_stream_kernel<127, 2, 4, 4, 16>"
     if launch == "o":
-        return "kq_mv_kernel<12, 0, 2, 1, false, 8>" if B <= 8 else "kq_mv_kernel<12, 0, 1, 1, false, 16>"
+        return "kq_mv_kernel<12, 0, 1, 1, false, 16>"
     raise ValueError(launch)
 
 

@@ -27,6 +27,9 @@ size_t kq_stream_part_bytes(const kq_matmul_problem *ps, int n, int split);
 bool kq_stream_eligible(const kq_matmul_problem *ps, int n, int split);
 int kq_stream_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, int y_dtype, int split,
                      uint32_t *ctr, float *part, hipStream_t s);
+// kq_stream.hip: the one-shot kernel (a workgroup's tiles and x in LDS at once).
+bool kq_shot_eligible(const kq_matmul_problem *ps, int n);
+int kq_shot_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, int y_dtype, hipStream_t s);
 bool kq_sgather_eligible(int codec, bool glu, int32_t N, int32_t K, int64_t w_row_bytes, int32_t n_experts);
 int kq_sgather_launch(const void *x, const int32_t *x_exp, int64_t x_row_stride, int32_t x_pair_div, int32_t x_skip,
                       const void *w0, const void *w1, int64_t w_expert_bytes, int64_t w_row_bytes, int32_t N,
@@ -1188,6 +1191,8 @@ int kq_quantized_matmul_grouped(const kq_matmul_problem *problems, int n_problem
         int na = 0;
         for (int i = 0; i < n_problems; ++i)
             if (problems[i].M != 0 && problems[i].N != 0) all[na++] = problems[i];
+        // at most two tiles per CU that fit in LDS with x: every byte at once
+        if (kq_shot_eligible(all, na)) return kq_shot_launch(all, na, xe0, y_dtype, (hipStream_t)stream);
         // K past 16 super-blocks: K slices, given room for their partial tiles
         int split = kq_stream_split_want(all, na);
         if (split > 1 && (!workspace || ((uintptr_t)workspace & 255) ||

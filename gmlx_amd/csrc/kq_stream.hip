@@ -132,6 +132,7 @@ struct StreamArgs {
     int64_t x_stride;                  // elements
     int32_t M, K, y_dtype, total_tiles, n_problems;
     int32_t split;                     // K slices per tile (1: the whole K in one item)
+    int32_t pairs;                     // one-shot launches: workgroups holding two tiles
 };
 
 // K slices per tile at most (the last arrival loads them all at once).
@@ -873,6 +874,276 @@ int launch_rows(const StreamArgs &a, int nb, int grid, hipStream_t s) {
 bool stream_k_ok(int K) {
     const int nb = K / KQ_QK;
     return nb == 2 || nb == 4 || nb == 6 || nb == 8 || nb == 12 || nb == 16;
+}
+
+// ---- One-shot kernel: a workgroup's whole share in LDS at once --------------
+// Launches of at most two 16-row tiles per CU (the o and q|k|v projections of
+// a decode step at up to 8 rows).  Every wave owns one super-block column of
+// the workgroup's tiles (NB = 16: super-block `wave` of each tile; NB = 8:
+// unit `wave` = tile wave / 8, super-block wave % 8): at entry it copies that
+// column of each tile (16 rows) and the 8 activation rows of that
+// super-block into its own LDS region with direct-to-LDS loads, waits for its
+// own loads only, and multiplies at once, so the math of the columns that
+// land first overlaps the loads of the others (after one barrier for the
+// whole tile, the math ran after the last byte: 1-1.9 us more per launch,
+// measured with in-kernel stamps).  The partial tiles are then written into
+// the waves' regions, and after the launch's only barrier 128 threads per
+// tile sum them in super-block order (deterministic) and store.
+// Tiles: T over G = min(CUs, T) workgroups (T <= 2 G): workgroup b < P = T - G
+// takes tiles 2b and 2b + 1, the others tile P + b.  The host orders Q4_K
+// problems before Q6_K ones (a workgroup then holds two Q4_K tiles or one of
+// either codec) and checks that every workgroup fits in LDS.
+// A wave's region: the activation slab (8 rows x 512 bytes, each row's
+// 16-byte chunks XOR-swizzled by the row so the fragment reads of 8 rows hit
+// different banks; rows >= M read as zeros), then its columns: Q4_K rows of
+// 144 bytes, Q6_K rows of 240 (the streaming kernel's 224-byte slot with d at
+// 222, and a spare chunk: 15 chunks, an odd count, so the 16 rows of an MFMA
+// operand hit different banks).
+constexpr int kShotWaves = 16;
+constexpr int kShotRows = 8;
+constexpr int kShotSlab = kShotRows * 512;
+
+__host__ __device__ constexpr int shot_col_bytes(int codec) { return codec == KQ_CODEC_Q6_K ? 16 * 240 : 16 * 144; }
+
+// Bytes of a wave's region for tiles of column sizes c0 and c1 (0: none).
+__host__ __device__ constexpr int shot_region(int nb, int c0, int c1) {
+    return kShotSlab + (nb == 16 ? c0 + c1 : (c0 > c1 ? c0 : c1));
+}
+
+// Column kb of a 16-row tile (codec C) into LDS at dst: 64-chunk loads of 16
+// bytes per lane, then the rest in loads of 4 bytes per lane (a 16-byte load
+// writes 1 KB whatever its range, which would run into the next column).
+// voffset: the row's offset within the tile's rows (row r, clamped to rlast)
+// plus the column's bytes; soff: the tile's first row.
+template <int C, int NB>
+__device__ __forceinline__ void shot_copy_col(__amdgpu_buffer_rsrc_t rs, uint32_t dst, uint32_t row_bytes,
+                                              uint32_t kofs, int rlast, uint32_t soff, int lane) {
+    constexpr int RCH = C == KQ_CODEC_Q6_K ? 15 : 9;  // chunks per LDS row
+    constexpr int CH = 16 * RCH;
+    constexpr int FULL = CH / 64;
+    constexpr int TAIL = (CH - 64 * FULL) * 4 / 64;   // dword loads
+    auto src = [&](int q, int byte) -> uint32_t {
+        const int row = q / RCH, c = q - row * RCH;
+        int off;
+        if constexpr (C == KQ_CODEC_Q6_K) off = c < 13 ? 16 * c : c == 13 ? 194 : -1;
+        else off = 16 * c;
+        return off < 0 ? 0x80000000u
+                       : (uint32_t)min(row, rlast) * row_bytes + kofs + (uint32_t)(off + byte);
+    };
+#pragma unroll
+    for (int p = 0; p < FULL; ++p)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDSP(void))(uintptr_t)(dst + 1024u * p), 16, src(64 * p + lane, 0),
+                                                 (int)soff, 0, 0);
+#pragma unroll
+    for (int t = 0; t < TAIL; ++t) {
+        const int d = 64 * t + lane;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDSP(void))(uintptr_t)(dst + 1024u * FULL + 256u * t), 4,
+                                                 src(64 * FULL + d / 4, 4 * (d & 3)), (int)soff, 0, 0);
+    }
+}
+
+template <int NB>
+__global__ __launch_bounds__(64 * kShotWaves) void kq_shot_kernel(StreamArgs a_) {
+    static_assert(NB == 8 || NB == 16, "one super-block column per wave and tile");
+    constexpr int UPW = NB == 16 ? 2 : 1;  // units per wave at most
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const KArgs A = (KArgs)__builtin_amdgcn_kernarg_segment_ptr();
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = kq_lane(), r = lane & 15, g = lane >> 4;
+    // Every argument the kernel reads, loaded at entry and held in SGPRs:
+    // independent scalar loads at fixed offsets issue together (one round
+    // trip), and each tile's problem is picked by scalar selects.  (Left to
+    // itself, the compiler moved the problems' loads behind the branches that
+    // pick them: a chain of scalar-cache misses ahead of the first vector load.)
+    uint64_t aw[kStreamProblems], ay[kStreamProblems];
+    int64_t ays[kStreamProblems];
+    uint32_t awb[kStreamProblems], arb[kStreamProblems];
+    int32_t an[kStreamProblems], ac[kStreamProblems], tb[kStreamProblems];
+#pragma unroll
+    for (int i = 0; i < kStreamProblems; ++i) {
+        aw[i] = (uint64_t)(uintptr_t)A->p[i].w;
+        ay[i] = (uint64_t)(uintptr_t)A->p[i].y;
+        ays[i] = A->p[i].y_stride;
+        awb[i] = A->p[i].w_bytes;
+        arb[i] = A->p[i].row_bytes;
+        an[i] = A->p[i].N;
+        ac[i] = A->p[i].codec;
+        tb[i] = A->tile_begin[i];
+    }
+    int P = A->pairs, M = A->M, xstride = (int)A->x_stride, K = A->K;
+    uint64_t xb = (uint64_t)(uintptr_t)A->x;
+    asm volatile("" : "+s"(P), "+s"(M), "+s"(xstride), "+s"(K), "+s"(xb));
+    StreamProblem all[kStreamProblems];
+#pragma unroll
+    for (int i = 0; i < kStreamProblems; ++i) {
+        asm volatile("" : "+s"(aw[i]), "+s"(ay[i]), "+s"(ays[i]), "+s"(awb[i]), "+s"(arb[i]), "+s"(an[i]), "+s"(ac[i]),
+                     "+s"(tb[i]));
+        all[i].w = (const uint8_t *)(uintptr_t)aw[i];
+        all[i].y = (void *)(uintptr_t)ay[i];
+        all[i].y_stride = ays[i];
+        all[i].w_bytes = awb[i];
+        all[i].row_bytes = arb[i];
+        all[i].N = an[i];
+        all[i].codec = ac[i];
+    }
+    const int b = (int)blockIdx.x;
+    const int nt = b < P ? 2 : 1;
+    const int t0 = b < P ? 2 * b : P + b;
+    // the workgroup's tiles: problem, first row, codec
+    StreamProblem pr[2];
+    int32_t begin[2];
+    bool q6[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int t = j < nt ? t0 + j : t0;
+        const int pi = (t >= tb[1]) + (t >= tb[2]) + (t >= tb[3]);  // unused entries: INT_MAX
+        pr[j] = all[0];
+        begin[j] = tb[0];
+#pragma unroll
+        for (int i = 1; i < kStreamProblems; ++i)
+            if (pi == i) {
+                pr[j] = all[i];
+                begin[j] = tb[i];
+            }
+        q6[j] = pr[j].codec == KQ_CODEC_Q6_K;
+    }
+    const int cb0 = shot_col_bytes(q6[0] ? KQ_CODEC_Q6_K : KQ_CODEC_Q4_K);
+    const int cb1 = nt > 1 ? shot_col_bytes(q6[1] ? KQ_CODEC_Q6_K : KQ_CODEC_Q4_K) : 0;
+    const uint32_t region = (uint32_t)(uintptr_t)(LDSP(void))smem + (uint32_t)(wave * shot_region(NB, cb0, cb1));
+    // the wave's units: (tile uj[i], super-block kb)
+    const int kb = NB == 16 ? wave : wave % NB;
+    int uj[UPW];
+    bool live[UPW], uq6[UPW];
+    uint32_t ucol[UPW];
+#pragma unroll
+    for (int i = 0; i < UPW; ++i) {
+        uj[i] = NB == 16 ? i : wave / NB;
+        live[i] = uj[i] < nt;
+        uq6[i] = uj[i] == 1 ? q6[1] : q6[0];
+        ucol[i] = region + kShotSlab + (uint32_t)(NB == 16 && i == 1 ? cb0 : 0);
+    }
+    const bool any = live[0];
+
+    // ---- loads: the activation slab of super-block kb, then the columns
+    if (any) {
+        const uint32_t xbytes = (uint32_t)(((int64_t)(M - 1) * xstride + K) * 2);
+        const __amdgpu_buffer_rsrc_t xs = kq_buffer((const void *)(uintptr_t)xb, xbytes);
+#pragma unroll
+        for (int i = 0; i < kShotRows / 2; ++i) {
+            const int m = 2 * i + (lane >> 5), c = (lane & 31) ^ (m & 7);
+            const uint32_t off =
+                m < M ? (uint32_t)m * (uint32_t)xstride * 2u + (uint32_t)(kb * 512 + 16 * c) : 0x80000000u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xs, (LDSP(void))(uintptr_t)(region + 1024u * i), 16, off, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < UPW; ++i) {
+            if (!live[i]) continue;
+            // (selects, not array indices: a runtime index puts the arrays in scratch)
+            const bool u1 = uj[i] == 1;
+            const StreamProblem &pj = u1 ? pr[1] : pr[0];
+            const int row0 = (t0 + uj[i] - (u1 ? begin[1] : begin[0])) * 16;
+            const int rlast = min(15, pj.N - 1 - row0);
+            const __amdgpu_buffer_rsrc_t rs = kq_buffer(pj.w, pj.w_bytes);
+            const uint32_t soff = (uint32_t)row0 * pj.row_bytes;
+            if (u1 ? q6[1] : q6[0])
+                shot_copy_col<KQ_CODEC_Q6_K, NB>(rs, ucol[i], pj.row_bytes, (uint32_t)(kb * Geo<KQ_CODEC_Q6_K>::BPB),
+                                                 rlast, soff, lane);
+            else
+                shot_copy_col<KQ_CODEC_Q4_K, NB>(rs, ucol[i], pj.row_bytes, (uint32_t)(kb * Geo<KQ_CODEC_Q4_K>::BPB),
+                                                 rlast, soff, lane);
+        }
+    }
+    // epilogue parameters ahead of the wait (held in registers)
+    const bool has_xe = A->x_exp != nullptr;
+    int ydt = A->y_dtype;
+    asm volatile("" : "+s"(ydt));
+    // ---- math on the wave's units; the partial tiles into its region.  The
+    // activation part (fragment permutes, the Q4_K sub-block sums) runs as soon
+    // as the slab has landed, while the columns (issued after it) are in flight.
+    if (any) {
+        int col_loads = 0;  // loads issued after the slab (they return in order)
+#pragma unroll
+        for (int i = 0; i < UPW; ++i) col_loads += live[i] ? (uq6[i] ? 6 : 3) : 0;
+        wait_tiles_left<1, 12>(col_loads);
+        const uint32_t xrow = region + (uint32_t)((r & 7) * 512);
+        const int sw = r & 7;
+        const bool use4 = (live[0] && !uq6[0]) || (UPW > 1 && live[UPW - 1] && !uq6[UPW - 1]);
+        const bool use6 = (live[0] && uq6[0]) || (UPW > 1 && live[UPW - 1] && uq6[UPW - 1]);
+        half8_t x4[1][8], x6[1][8];
+        floatx4 xsum = fzero4();
+        if (use4) {
+            u32x4 cin[1][8];
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+#pragma unroll
+                for (int a2 = 0; a2 < 2; ++a2)
+                    cin[0][2 * w + a2] = lds128(xrow + 16u * (uint32_t)((8 * g + 4 * a2 + w) ^ sw));
+            q4own_x<1>(x4, xsum, cin, lane);
+        }
+        if (use6) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+                x6[0][t] = __builtin_bit_cast(half8_t, lds128(xrow + 16u * (uint32_t)((4 * t + g) ^ sw)));
+        }
+        const Q4Consts q4k = q4own_consts(g);
+        const Iq2Tables &no_tab = *IqTables<KQ_CODEC_Q4_K>::get();
+        __builtin_amdgcn_s_waitcnt(KQ_VMCNT(0));  // the columns
+        floatx4 acc[UPW];
+#pragma unroll
+        for (int i = 0; i < UPW; ++i) {
+            acc[i] = fzero4();
+            if (!live[i]) continue;
+            if (uq6[i])
+                mma_slab<KQ_CODEC_Q6_K, 1>(acc[i], ucol[i] + (uint32_t)(r * 240), x6, xsum, g, no_tab);
+            else
+                q4own_slab<1>(acc[i], (LDSP(const uint8_t))(uintptr_t)(ucol[i] + (uint32_t)(r * 144)), x4, xsum, q4k);
+        }
+        kq_mfma_drain();
+        // rows 4 g + e < 8 live in lanes g < 2; partial of tile j at region + 512 j
+#pragma unroll
+        for (int i = 0; i < UPW; ++i)
+            if (live[i] && g < 2) *(LDSP(floatx4))(uintptr_t)(region + 512u * (uint32_t)uj[i] + 16u * lane) = acc[i];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    // ---- tile j: threads 128 j .. 128 j + 127, output (m, n) = (t >> 4, t & 15)
+    // of the tile, summed over its super-blocks in order
+    const int tid = (int)threadIdx.x, j = tid >> 7, tt = tid & 127;
+    if (j < nt) {
+        const int m = tt >> 4, n = tt & 15;
+        const uint32_t at = 512u * (uint32_t)j + 16u * (uint32_t)((m >> 2) * 16 + n) + 4u * (uint32_t)(m & 3);
+        const uint32_t rb = (uint32_t)shot_region(NB, cb0, cb1);
+        const uint32_t base = (uint32_t)(uintptr_t)(LDSP(void))smem + at;
+        float v[NB];
+#pragma unroll
+        for (int k = 0; k < NB; ++k) {
+            const int w = (j * NB + k) & (kShotWaves - 1);  // the wave holding unit (j, k)
+            v[k] = *(const LDSP(float))(uintptr_t)(base + (uint32_t)w * rb);
+        }
+        float sum = v[0];
+#pragma unroll
+        for (int k = 1; k < NB; ++k) sum += v[k];
+        const StreamProblem &p = j == 0 ? pr[0] : pr[1];
+        const int col = (t0 + j - (j == 0 ? begin[0] : begin[1])) * 16 + n;
+        if (m < M && col < p.N) {
+            if (has_xe) sum = ldexpf(sum, A->x_exp[m]);
+            kq_store_out(p.y, ydt, (int64_t)m * p.y_stride + col, sum);
+        }
+    }
+}
+
+template <int NB>
+int launch_shot(const StreamArgs &a, int grid, size_t lds, hipStream_t s) {
+    static bool raised = false;
+    if (!raised) {
+        if (hipFuncSetAttribute((const void *)kq_shot_kernel<NB>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                160 * 1024) != hipSuccess)
+            return KQ_ERR_LAUNCH_FAILED;
+        raised = true;
+    }
+    hipLaunchKernelGGL((kq_shot_kernel<NB>), dim3(grid), dim3(64 * kShotWaves), lds, s, a);
+    return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
 }
 
 // ---- Mid-batch streaming kernel (17..64 rows) -------------------------------
@@ -1934,7 +2205,111 @@ int64_t group_tiles(const kq_matmul_problem *ps, int n) {
     return tiles;
 }
 
+// One-shot plan: the problems with Q4_K ones first (ord), the tiles, the
+// workgroups holding two tiles, the grid and the LDS of the largest
+// workgroup.  False when the launch is not served: more than 8 rows, K not 8
+// or 16 super-blocks, another codec, more than two tiles per CU, a
+// workgroup past 160 KB of LDS (two Q6_K tiles at K = 4096), 31-bit offsets.
+// GMLX_KQ_SHOT=0 declines every launch (tests and comparisons), and so does
+// a route forced with GMLX_KQ_STREAM or GMLX_KQ_MV (tests of those kernels).
+bool shot_plan(const kq_matmul_problem *ps, int n, kq_matmul_problem *ord, int &tiles, int &pairs, int &grid,
+               size_t &lds) {
+    if (n <= 0 || n > kStreamProblems) return false;
+    const char *env = getenv("GMLX_KQ_SHOT");
+    if (env && env[0] == '0' && env[1] == 0) return false;
+    for (const char *forced : {"GMLX_KQ_STREAM", "GMLX_KQ_MV"}) {
+        const char *e = getenv(forced);
+        if (e && *e) return false;
+    }
+    const kq_matmul_problem &q0 = ps[0];
+    if (q0.M < 1 || q0.M > kShotRows || q0.K % KQ_QK) return false;
+    const int nb = q0.K / KQ_QK;
+    if (nb != 8 && nb != 16) return false;
+    if (((uintptr_t)q0.x & 15) != 0 || q0.x_row_stride % 8 != 0) return false;
+    int no = 0;
+    for (const int codec : {KQ_CODEC_Q4_K, KQ_CODEC_Q6_K})
+        for (int i = 0; i < n; ++i)
+            if (ps[i].codec == codec) ord[no++] = ps[i];
+    if (no != n) return false;
+    for (int i = 0; i < n; ++i) {
+        const kq_matmul_problem &q = ord[i];
+        if (q.x != q0.x || q.x_row_stride != q0.x_row_stride || q.M != q0.M || q.K != q0.K) return false;
+        if ((int64_t)(q.N + 16) * q.w_row_bytes >= (int64_t)0x80000000LL) return false;
+    }
+    if ((int64_t)(q0.M - 1) * q0.x_row_stride * 2 + (int64_t)q0.K * 2 >= (int64_t)0x80000000LL) return false;
+    const int64_t t64 = group_tiles(ord, n);
+    if (t64 > 2 * (int64_t)device_cus()) return false;
+    tiles = (int)t64;
+    grid = tiles < device_cus() ? tiles : device_cus();
+    pairs = tiles - grid;
+    auto codec_of = [&](int t) {
+        int first = 0;
+        for (int i = 0; i < n; ++i) {
+            first += (ord[i].N + 15) / 16;
+            if (t < first) return ord[i].codec;
+        }
+        return ord[n - 1].codec;
+    };
+    size_t worst = 0;
+    for (int b = 0; b < grid; ++b) {
+        const int c0 = shot_col_bytes(codec_of(b < pairs ? 2 * b : pairs + b));
+        const int c1 = b < pairs ? shot_col_bytes(codec_of(2 * b + 1)) : 0;
+        const size_t s = (size_t)kShotWaves * (size_t)shot_region(nb, c0, c1);
+        worst = s > worst ? s : worst;
+    }
+    lds = worst;
+    return lds <= (size_t)160 * 1024;
+}
+
 }  // namespace
+
+// Whether the one-shot kernel serves this group (fp16 activations; see shot_plan).
+bool kq_shot_eligible(const kq_matmul_problem *ps, int n) {
+    kq_matmul_problem ord[KQ_MAX_GROUP];
+    int tiles, pairs, grid;
+    size_t lds;
+    return shot_plan(ps, n, ord, tiles, pairs, grid, lds);
+}
+
+// Problems validated, eligible and all live; x fp16, x_exp its per-row
+// exponents or null.
+int kq_shot_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, int y_dtype, hipStream_t s) {
+    kq_matmul_problem ord[KQ_MAX_GROUP];
+    int tiles, pairs, grid;
+    size_t lds;
+    if (!shot_plan(ps, n, ord, tiles, pairs, grid, lds)) return KQ_ERR_BAD_SHAPE;
+    StreamArgs a;
+    int t = 0;
+    for (int i = 0; i < n; ++i) {
+        StreamProblem &p = a.p[i];
+        p.w = (const uint8_t *)ord[i].w;
+        p.y = ord[i].y;
+        p.y_stride = ord[i].y_row_stride;
+        p.row_bytes = (uint32_t)ord[i].w_row_bytes;
+        p.w_bytes = (uint32_t)(ord[i].N * ord[i].w_row_bytes);
+        p.N = ord[i].N;
+        p.codec = ord[i].codec;
+        a.tile_begin[i] = t;
+        t += (ord[i].N + 15) / 16;
+    }
+    for (int i = n; i < KQ_MAX_GROUP; ++i) {
+        a.p[i] = a.p[0];
+        a.tile_begin[i] = 0x7FFFFFFF;
+    }
+    a.x = (const char *)ord[0].x;
+    a.x_exp = x_exp;
+    a.ctr = nullptr;
+    a.part = nullptr;
+    a.x_stride = ord[0].x_row_stride;
+    a.M = ord[0].M;
+    a.K = ord[0].K;
+    a.y_dtype = y_dtype;
+    a.total_tiles = tiles;
+    a.n_problems = n;
+    a.split = 1;
+    a.pairs = pairs;
+    return ord[0].K / KQ_QK == 8 ? launch_shot<8>(a, grid, lds, s) : launch_shot<16>(a, grid, lds, s);
+}
 
 // K slices a launch of this group would take given the workspace (1: whole
 // K).  K past 16 super-blocks (the down projections) is cut into at most 8

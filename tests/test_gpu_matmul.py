@@ -64,9 +64,10 @@ def test_config2_shapes_b8(codec):
 @pytest.mark.parametrize("M", [1, 8, 16])
 def test_config2_qkv_group(M, monkeypatch):
     """The q|k|v group of a Qwen3-8B Q4_K_M layer (Q4_K q, k with Q6_K v) on
-    default routing (two K slices on the streaming kernel) matches the fp64
-    reference, repeats bitwise, agrees with the LDS-staged path and leaves the
-    workspace's arrival counters zero."""
+    default routing (the one-shot kernel at 1 and 8 rows, two K slices on the
+    streaming kernel at 16) matches the fp64 reference, repeats bitwise,
+    agrees with the LDS-staged path and leaves the workspace's arrival
+    counters zero."""
     import torch
     from gmlx_amd import _lib, ops
     for k in PATH_KNOBS:
