@@ -475,7 +475,8 @@ BLOCK_BYTES = {"q4_k": 144, "q6_k": 210, "iq2_xxs": 66}
 
 def bench_moe(torch, ops, which, iters=50):
     """BASELINE configs 4 and 5: one MoE decode layer (router top-k, fused
-    gate|up GLU gather, down gather with the routing mix folded in) over
+    gate|up GLU gather writing h in the activation dtype, down gather with
+    the routing mix folded in) over
     the tokens' ragged per-expert segments.  Router logits and x are numpy
     default_rng(0) draws; weights are N(0, 0.02) drawn on the GPU (torch
     generator, seed 0) and quantised by kq_quantize -- every expert for C4,
@@ -511,9 +512,10 @@ def bench_moe(torch, ops, which, iters=50):
     copies = 2 if which == "C4" else 1
     sets = [(stack(I, H, cgu), stack(I, H, cgu), stack(H, I, cd)) for _ in range(copies)]
 
+    # h in the activation dtype (fp16): the down gather reads it as it is
     def step(g, u, d):
         idx, sc = ops.moe_router_topk(logits, topk, shared_gate=False)
-        h = ops.moe_glu_gather_kq(x, g, u, cgu, idx)
+        h = ops.moe_glu_gather_kq(x, g, u, cgu, idx, out_dtype=x.dtype)
         return ops.gather_qmv_mix_ns_kq(h, d, cd, idx, sc)
 
     g, outs = capture(torch, lambda: [step(*st) for st in sets])
@@ -523,7 +525,7 @@ def bench_moe(torch, ops, which, iters=50):
     idx, sc = ops.moe_router_topk(logits, topk, shared_gate=False)
     uniq = int(torch.unique(idx).numel())
     per_expert = 2 * I * (H // 256) * BLOCK_BYTES[cgu] + H * (I // 256) * BLOCK_BYTES[cd]
-    act_bytes = T * H * 2 + 2 * T * topk * I * 4 + T * topk * H * 4 * 2 + T * H * 4
+    act_bytes = T * H * 2 + 2 * T * topk * I * x.element_size() + T * topk * H * 4 * 2 + T * H * 4
     byts = uniq * per_expert + act_bytes
     # spot check: tokens 0, 1, T/2, T-1 of the first copy against fp64
     y = outs[0].cpu().numpy()

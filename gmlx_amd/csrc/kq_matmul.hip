@@ -1360,7 +1360,6 @@ int kq_moe_gather_rows(const void *x, int x_dtype, int64_t x_row_stride, int32_t
                        const int32_t *pair_order, int32_t n_pairs, int32_t n_experts, void *y, int y_dtype,
                        int64_t y_row_stride, int32_t y_skip, void *workspace, size_t workspace_bytes,
                        kq_stream_t stream) {
-    if (w1 && y_dtype != KQ_DTYPE_F32) return KQ_ERR_UNSUPPORTED_DTYPE;
     return gather_common(x, x_dtype, x_row_stride, x_pair_div, w0, w1, w_expert_bytes, w_row_bytes, N, K, codec,
                          ep, seg_info, pair_order, n_pairs, n_experts, y, y_dtype, y_row_stride, workspace,
                          workspace_bytes, (hipStream_t)stream, x_skip, y_skip);

@@ -486,11 +486,16 @@ def gather_qmm(x, w, scales=None, codec="q4_k", indices=None, sorted_indices=Fal
 
 
 def moe_glu_gather_kq(x, gate_w, up_w, codec, idx, act="silu", limit=None, alpha=None, gate_bias=None,
-                      up_bias=None):
+                      up_bias=None, out_dtype=torch.float32):
     """Fused MoE GLU gather (gmlx/modules.py:557-588): h[t, s] =
-    act(Wg[e] . x[t], Wu[e] . x[t]), e = idx[t, s], in fp32 -> (t, k, I)
-    float32.  act: "silu", "gelu" (tanh form), "silu_limit" (limit=) or
-    "swiglu_clamp" (limit=, alpha=, gate_bias= / up_bias= fp32 [E, I])."""
+    act(Wg[e] . x[t], Wu[e] . x[t]), e = idx[t, s], computed in fp32 -> (t, k, I)
+    of out_dtype.  act: "silu", "gelu" (tanh form), "silu_limit" (limit=) or
+    "swiglu_clamp" (limit=, alpha=, gate_bias= / up_bias= fp32 [E, I]).
+    out_dtype float32 (default) keeps any range; float16 / bfloat16 round h
+    to the activation dtype the stock SwitchGLU path produces, so the down
+    gather reads it without a preparation pass (an fp16 h rounds exactly as
+    the prepared fp32 row does, and past 65504 it is inf, as in the stock
+    fp16 path)."""
     _fault("moe_glu_gather_kq")
     _require_gpu(x, gate_w, up_w, idx)
     K = x.shape[-1]
@@ -501,12 +506,14 @@ def moe_glu_gather_kq(x, gate_w, up_w, codec, idx, act="silu", limit=None, alpha
     if gate_w.shape != up_w.shape or gate_w.stride() != up_w.stride():
         raise ValueError("gate and up stacks must share shape and layout")
     E, I = gate_w.shape[0], gate_w.shape[1]
+    if out_dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise ValueError(f"out_dtype {out_dtype} is not float32, float16 or bfloat16")
     ep, keep = _epilogue(act, limit, alpha, gate_bias, up_bias, E, I, x.device)
-    h = torch.empty((t * k, I), dtype=torch.float32, device=x.device)
+    h = torch.empty((t * k, I), dtype=out_dtype, device=x.device)
     if t * k:
         seg, order = _routed(idx, E)
         _gather_rows(x2.data_ptr(), _x_dt(x2), x2.stride(0), k, 0, gate_w, up_w, codec, ep, seg, order, t * k, E,
-                     h.data_ptr(), DTYPE_F32, I, 0, K, _stream(x2))
+                     h.data_ptr(), _dt(out_dtype), I, 0, K, _stream(x2))
     del keep
     return h.reshape(t, k, I)
 

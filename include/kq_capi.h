@@ -247,10 +247,12 @@ typedef struct {
  * down_w, shexp_down_w, codec, idx, scores) (gmlx/modules.py:571-584,
  * 777-787) keep the shared expert in slot k of [t, k + 1, N] blocks.
  * Pair p reads x row p / x_pair_div + p / x_skip and writes y row
- * p + p / y_skip (a skip of 0 adds nothing).  w1 == NULL: plain gather
- * (y of y_dtype); w1 != NULL: fused GLU (y fp32).  ep == NULL means silu
- * and no biases.  The shared expert itself is a one-expert gather
- * (n_experts 1, every pair routed to it). */
+ * p + p / y_skip (a skip of 0 adds nothing).  w1 == NULL: plain gather;
+ * w1 != NULL: fused GLU, computed in fp32.  Either way y is of y_dtype (f32,
+ * f16 or bf16; an f16 GLU output is what the down gather reads without
+ * preparing its rows).  ep == NULL means silu and no biases.  The shared
+ * expert itself is a one-expert gather (n_experts 1, every pair routed to
+ * it). */
 int kq_moe_gather_rows(const void *x, int x_dtype, int64_t x_row_stride, int32_t x_pair_div,
                        int32_t x_skip, const void *w0, const void *w1, int64_t w_expert_bytes,
                        int64_t w_row_bytes, int32_t N, int32_t K, int codec,

@@ -526,3 +526,39 @@ def test_down_gather_with_mix_equals_two_steps(dcodec, T, k, E, I, N, bad, hdt):
             if 0 <= e < E:
                 ref[t] += float(sc[t, s]) * (D[e] @ hf[t, s])
     assert okq.max_rel(want.cpu().numpy(), ref) <= TOL
+
+
+@pytest.mark.parametrize("gcodec,dcodec", [("q4_k", "q6_k"), ("iq2_xxs", "iq2_xxs")])
+def test_glu_gather_fp16_h_skips_the_prepare_pass(gcodec, dcodec):
+    """moe_glu_gather_kq(out_dtype=float16): h is the fp32 h rounded to fp16,
+    bitwise, on both gather forms' codecs; the layer through the down gather
+    and mix matches the fp32-h layer (whose down gather prepares its rows)
+    and the fp64 reference within tolerance."""
+    import torch
+    from gmlx_amd import ops
+    rng = np.random.default_rng(31)
+    E, D, I, T, k = 32, 2048, 768, 16, 8
+    if gcodec == "iq2_xxs":
+        gw, uw, dw = (okq.random_valid_blocks(rng, "iq2_xxs", E * n * kk // 256).reshape(E, n, -1)
+                      for n, kk in ((I, D), (I, D), (D, I)))
+    else:
+        gw, uw, dw = _experts(rng, gcodec, E, I, D), _experts(rng, gcodec, E, I, D), _experts(rng, dcodec, E, D, I)
+    x = fp16_rows(rng, T, D)
+    logits = rng.normal(0, 1, size=(T, E)).astype(np.float32)
+    inds, scores = ops.moe_router_topk(_dev(logits), k, True, shared_gate=False)
+    args = (_dev(x), _dev(gw), _dev(uw), gcodec, inds)
+    h32 = ops.moe_glu_gather_kq(*args)
+    h16 = ops.moe_glu_gather_kq(*args, out_dtype=torch.float16)
+    assert h16.dtype == torch.float16 and h16.shape == h32.shape
+    assert torch.equal(h16, h32.to(torch.float16))
+    dd = _dev(dw)
+    y32 = ops.gather_qmv_mix_ns_kq(h32, dd, dcodec, inds, scores).cpu().numpy()
+    y16 = ops.gather_qmv_mix_ns_kq(h16, dd, dcodec, inds, scores).cpu().numpy()
+    assert okq.max_rel(y16, y32) <= TOL
+    idx, sc = inds.cpu().numpy(), scores.cpu().numpy().astype(np.float64)
+    d_deq = okq.dequantize(dw.reshape(-1, dw.shape[-1]), dcodec).reshape(E, D, I).astype(np.float64)
+    hf = h16.float().cpu().numpy().astype(np.float64)
+    yref = np.stack([sum(sc[t, s] * (d_deq[idx[t, s]] @ hf[t, s]) for s in range(k)) for t in range(T)])
+    assert okq.max_rel(y16, yref) <= TOL
+    with pytest.raises(ValueError):
+        ops.moe_glu_gather_kq(*args, out_dtype=torch.int32)
