@@ -103,10 +103,10 @@ def make_inputs(torch, rng, B):
 # finish summing the six partial tiles; q|k|v and o (one or two tiles per CU)
 # take the one-shot kernel (every wave copies one super-block column of its
 # workgroup's tiles and its activation slab into LDS at entry and multiplies
-# as soon as its own loads land; one barrier before the partial-tile sum).
-# At B = 9..16 q|k|v and gate|up take the streaming kernel's 16-row forms
-# (q|k|v in two K slices, down in four K slices of 12 super-blocks) and o the
-# LDS-staged persistent kernel (two 8-wave workgroups per CU).
+# as soon as its own loads land; one barrier before the partial-tile sum; at
+# 9..16 rows the activation slab is copied in two passes of 8 rows).
+# At B = 9..16 gate|up and down take the streaming kernel's 16-row forms
+# (down in four K slices of 12 super-blocks).
 # At B = 17..64 q|k|v, gate|up and down take the mid-batch streaming kernel
 # (four waves copy each super-block of the activation rows and of a group of
 # six weight tiles into an LDS ring, six waves each accumulate one tile over
@@ -140,12 +140,8 @@ def kernel_of(launch, B):
     if B <= 16 and launch == "down":  # K = 12288 in slices, one super-block per consumer
         # up to 8 rows: six slices of 8; 9..16 rows: four slices of 12 (two ring slots)
         return "kq_stream_kernel<14, 1, 8, 3, 8>" if B <= 8 else "kq_stream_kernel<14, 1, 12, 2, 16>"
-    if B <= 8 and launch in ("qkv", "o"):  # kq_shot_kernel<super-blocks per row>
-        return "kq_shot_kernel<16>"
-    if launch == "qkv":  # Q4_K q|k with Q6_K v: the mixed form (codec id 127) in two K slices
-        return "kq_stream_kernel<127, 2, 4, 4, 16>"
-    if launch == "o":
-        return "kq_mv_kernel<12, 0, 1, 1, false, 16>"
+    if launch in ("qkv", "o"):  # kq_shot_kernel<super-blocks per row, activation rows>
+        return f"kq_shot_kernel<16, {8 if B <= 8 else 16}>"
     raise ValueError(launch)
 
 

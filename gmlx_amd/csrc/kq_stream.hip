@@ -878,7 +878,7 @@ bool stream_k_ok(int K) {
 
 // ---- One-shot kernel: a workgroup's whole share in LDS at once --------------
 // Launches of at most two 16-row tiles per CU (the o and q|k|v projections of
-// a decode step at up to 8 rows).  Every wave owns one super-block column of
+// a decode step at up to 16 rows).  Every wave owns one super-block column of
 // the workgroup's tiles (NB = 16: super-block `wave` of each tile; NB = 8:
 // unit `wave` = tile wave / 8, super-block wave % 8): at entry it copies that
 // column of each tile (16 rows) and the 8 activation rows of that
@@ -895,7 +895,8 @@ bool stream_k_ok(int K) {
 // either codec) and checks that every workgroup fits in LDS.
 // A wave's region: the activation slab (8 rows x 512 bytes, each row's
 // 16-byte chunks XOR-swizzled by the row so the fragment reads of 8 rows hit
-// different banks; rows >= M read as zeros), then its columns: Q4_K rows of
+// different banks; rows >= M read as zeros; a 16-row launch copies rows
+// 8..15 into it once lanes 0..7 hold theirs), then its columns: Q4_K rows of
 // 144 bytes, Q6_K rows of 240 (the streaming kernel's 224-byte slot with d at
 // 222, and a spare chunk: 15 chunks, an odd count, so the 16 rows of an MFMA
 // operand hit different banks).
@@ -908,6 +909,18 @@ __host__ __device__ constexpr int shot_col_bytes(int codec) { return codec == KQ
 // Bytes of a wave's region for tiles of column sizes c0 and c1 (0: none).
 __host__ __device__ constexpr int shot_region(int nb, int c0, int c1) {
     return kShotSlab + (nb == 16 ? c0 + c1 : (c0 > c1 ? c0 : c1));
+}
+
+// Direct-to-LDS buffer loads of 16 and 4 bytes per lane.  Plain functions, not
+// templates: the builtin exists for the device target only, and the host pass
+// marks a function template whose body uses it invalid after its first
+// instantiation, so a second kernel instance calling the same specialization
+// would not compile.
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rs, uint32_t lds, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDSP(void))(uintptr_t)lds, 16, voff, (int)soff, 0, 0);
+}
+__device__ __forceinline__ void lds_dma4(__amdgpu_buffer_rsrc_t rs, uint32_t lds, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDSP(void))(uintptr_t)lds, 4, voff, (int)soff, 0, 0);
 }
 
 // Column kb of a 16-row tile (codec C) into LDS at dst: 64-chunk loads of 16
@@ -931,20 +944,18 @@ __device__ __forceinline__ void shot_copy_col(__amdgpu_buffer_rsrc_t rs, uint32_
                        : (uint32_t)min(row, rlast) * row_bytes + kofs + (uint32_t)(off + byte);
     };
 #pragma unroll
-    for (int p = 0; p < FULL; ++p)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDSP(void))(uintptr_t)(dst + 1024u * p), 16, src(64 * p + lane, 0),
-                                                 (int)soff, 0, 0);
+    for (int p = 0; p < FULL; ++p) lds_dma16(rs, dst + 1024u * p, src(64 * p + lane, 0), soff);
 #pragma unroll
     for (int t = 0; t < TAIL; ++t) {
         const int d = 64 * t + lane;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDSP(void))(uintptr_t)(dst + 1024u * FULL + 256u * t), 4,
-                                                 src(64 * FULL + d / 4, 4 * (d & 3)), (int)soff, 0, 0);
+        lds_dma4(rs, dst + 1024u * FULL + 256u * t, src(64 * FULL + d / 4, 4 * (d & 3)), soff);
     }
 }
 
-template <int NB>
+template <int NB, int MR>
 __global__ __launch_bounds__(64 * kShotWaves) void kq_shot_kernel(StreamArgs a_) {
     static_assert(NB == 8 || NB == 16, "one super-block column per wave and tile");
+    static_assert(MR == 8 || MR == 16, "8 or 16 activation rows");
     constexpr int UPW = NB == 16 ? 2 : 1;  // units per wave at most
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const KArgs A = (KArgs)__builtin_amdgcn_kernarg_segment_ptr();
@@ -1024,17 +1035,22 @@ __global__ __launch_bounds__(64 * kShotWaves) void kq_shot_kernel(StreamArgs a_)
     }
     const bool any = live[0];
 
-    // ---- loads: the activation slab of super-block kb, then the columns
-    if (any) {
-        const uint32_t xbytes = (uint32_t)(((int64_t)(M - 1) * xstride + K) * 2);
-        const __amdgpu_buffer_rsrc_t xs = kq_buffer((const void *)(uintptr_t)xb, xbytes);
+    // ---- loads: the activation slab of super-block kb (rows 0..7), then the
+    // columns; 16-row launches copy rows 8..15 into the same slab once lanes
+    // 0..7 hold their fragments (two slabs would not fit beside the columns)
+    const uint32_t xbytes = (uint32_t)(((int64_t)(M - 1) * xstride + K) * 2);
+    const __amdgpu_buffer_rsrc_t xs = kq_buffer((const void *)(uintptr_t)xb, xbytes);
+    auto copy_slab = [&](int m0) {
 #pragma unroll
         for (int i = 0; i < kShotRows / 2; ++i) {
-            const int m = 2 * i + (lane >> 5), c = (lane & 31) ^ (m & 7);
+            const int m = m0 + 2 * i + (lane >> 5), c = (lane & 31) ^ (m & 7);
             const uint32_t off =
                 m < M ? (uint32_t)m * (uint32_t)xstride * 2u + (uint32_t)(kb * 512 + 16 * c) : 0x80000000u;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(xs, (LDSP(void))(uintptr_t)(region + 1024u * i), 16, off, 0, 0, 0);
         }
+    };
+    if (any) {
+        copy_slab(0);
 #pragma unroll
         for (int i = 0; i < UPW; ++i) {
             if (!live[i]) continue;
@@ -1071,20 +1087,35 @@ __global__ __launch_bounds__(64 * kShotWaves) void kq_shot_kernel(StreamArgs a_)
         const bool use6 = (live[0] && uq6[0]) || (UPW > 1 && live[UPW - 1] && uq6[UPW - 1]);
         half8_t x4[1][8], x6[1][8];
         floatx4 xsum = fzero4();
-        if (use4) {
-            u32x4 cin[1][8];
+        u32x4 cin[1][8];
+        // the lane's raw fragments from the slab (lanes of rows 8..15 of a
+        // 16-row launch take theirs from the second pass)
+        auto read_slab = [&](bool mine) {
+            if (use4) {
 #pragma unroll
-            for (int w = 0; w < 4; ++w)
+                for (int w = 0; w < 4; ++w)
 #pragma unroll
-                for (int a2 = 0; a2 < 2; ++a2)
-                    cin[0][2 * w + a2] = lds128(xrow + 16u * (uint32_t)((8 * g + 4 * a2 + w) ^ sw));
-            q4own_x<1>(x4, xsum, cin, lane);
+                    for (int a2 = 0; a2 < 2; ++a2) {
+                        const u32x4 v = lds128(xrow + 16u * (uint32_t)((8 * g + 4 * a2 + w) ^ sw));
+                        cin[0][2 * w + a2] = mine ? v : cin[0][2 * w + a2];
+                    }
+            }
+            if (use6) {
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    const u32x4 v = lds128(xrow + 16u * (uint32_t)((4 * t + g) ^ sw));
+                    x6[0][t] = mine ? __builtin_bit_cast(half8_t, v) : x6[0][t];
+                }
+            }
+        };
+        read_slab(true);
+        if constexpr (MR == 16) {
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the first pass's reads are done
+            copy_slab(8);
+            __builtin_amdgcn_s_waitcnt(KQ_VMCNT(0));  // (the columns too: they were issued first)
+            read_slab(r >= 8);
         }
-        if (use6) {
-#pragma unroll
-            for (int t = 0; t < 8; ++t)
-                x6[0][t] = __builtin_bit_cast(half8_t, lds128(xrow + 16u * (uint32_t)((4 * t + g) ^ sw)));
-        }
+        if (use4) q4own_x<1>(x4, xsum, cin, lane);
         const Q4Consts q4k = q4own_consts(g);
         const Iq2Tables &no_tab = *IqTables<KQ_CODEC_Q4_K>::get();
         __builtin_amdgcn_s_waitcnt(KQ_VMCNT(0));  // the columns
@@ -1099,20 +1130,22 @@ __global__ __launch_bounds__(64 * kShotWaves) void kq_shot_kernel(StreamArgs a_)
                 q4own_slab<1>(acc[i], (LDSP(const uint8_t))(uintptr_t)(ucol[i] + (uint32_t)(r * 144)), x4, xsum, q4k);
         }
         kq_mfma_drain();
-        // rows 4 g + e < 8 live in lanes g < 2; partial of tile j at region + 512 j
+        // rows 4 g + e < MR live in lanes g < MR / 4; partial of tile j at region + 64 MR j
 #pragma unroll
         for (int i = 0; i < UPW; ++i)
-            if (live[i] && g < 2) *(LDSP(floatx4))(uintptr_t)(region + 512u * (uint32_t)uj[i] + 16u * lane) = acc[i];
+            if (live[i] && g < MR / 4)
+                *(LDSP(floatx4))(uintptr_t)(region + (uint32_t)(64 * MR) * (uint32_t)uj[i] + 16u * lane) = acc[i];
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    // ---- tile j: threads 128 j .. 128 j + 127, output (m, n) = (t >> 4, t & 15)
-    // of the tile, summed over its super-blocks in order
-    const int tid = (int)threadIdx.x, j = tid >> 7, tt = tid & 127;
+    // ---- tile j: threads 16 MR j .. 16 MR j + 16 MR - 1, output (m, n) =
+    // (t >> 4, t & 15) of the tile, summed over its super-blocks in order
+    const int tid = (int)threadIdx.x, j = tid / (16 * MR), tt = tid % (16 * MR);
     if (j < nt) {
         const int m = tt >> 4, n = tt & 15;
-        const uint32_t at = 512u * (uint32_t)j + 16u * (uint32_t)((m >> 2) * 16 + n) + 4u * (uint32_t)(m & 3);
+        const uint32_t at =
+            (uint32_t)(64 * MR) * (uint32_t)j + 16u * (uint32_t)((m >> 2) * 16 + n) + 4u * (uint32_t)(m & 3);
         const uint32_t rb = (uint32_t)shot_region(NB, cb0, cb1);
         const uint32_t base = (uint32_t)(uintptr_t)(LDSP(void))smem + at;
         float v[NB];
@@ -1133,16 +1166,16 @@ __global__ __launch_bounds__(64 * kShotWaves) void kq_shot_kernel(StreamArgs a_)
     }
 }
 
-template <int NB>
+template <int NB, int MR>
 int launch_shot(const StreamArgs &a, int grid, size_t lds, hipStream_t s) {
     static bool raised = false;
     if (!raised) {
-        if (hipFuncSetAttribute((const void *)kq_shot_kernel<NB>, hipFuncAttributeMaxDynamicSharedMemorySize,
+        if (hipFuncSetAttribute((const void *)kq_shot_kernel<NB, MR>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 160 * 1024) != hipSuccess)
             return KQ_ERR_LAUNCH_FAILED;
         raised = true;
     }
-    hipLaunchKernelGGL((kq_shot_kernel<NB>), dim3(grid), dim3(64 * kShotWaves), lds, s, a);
+    hipLaunchKernelGGL((kq_shot_kernel<NB, MR>), dim3(grid), dim3(64 * kShotWaves), lds, s, a);
     return hipGetLastError() == hipSuccess ? KQ_OK : KQ_ERR_LAUNCH_FAILED;
 }
 
@@ -2207,7 +2240,7 @@ int64_t group_tiles(const kq_matmul_problem *ps, int n) {
 
 // One-shot plan: the problems with Q4_K ones first (ord), the tiles, the
 // workgroups holding two tiles, the grid and the LDS of the largest
-// workgroup.  False when the launch is not served: more than 8 rows, K not 8
+// workgroup.  False when the launch is not served: more than 16 rows, K not 8
 // or 16 super-blocks, another codec, more than two tiles per CU, a
 // workgroup past 160 KB of LDS (two Q6_K tiles at K = 4096), 31-bit offsets.
 // GMLX_KQ_SHOT=0 declines every launch (tests and comparisons), and so does
@@ -2222,7 +2255,7 @@ bool shot_plan(const kq_matmul_problem *ps, int n, kq_matmul_problem *ord, int &
         if (e && *e) return false;
     }
     const kq_matmul_problem &q0 = ps[0];
-    if (q0.M < 1 || q0.M > kShotRows || q0.K % KQ_QK) return false;
+    if (q0.M < 1 || q0.M > 2 * kShotRows || q0.K % KQ_QK) return false;
     const int nb = q0.K / KQ_QK;
     if (nb != 8 && nb != 16) return false;
     if (((uintptr_t)q0.x & 15) != 0 || q0.x_row_stride % 8 != 0) return false;
@@ -2308,7 +2341,9 @@ int kq_shot_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, int
     a.n_problems = n;
     a.split = 1;
     a.pairs = pairs;
-    return ord[0].K / KQ_QK == 8 ? launch_shot<8>(a, grid, lds, s) : launch_shot<16>(a, grid, lds, s);
+    const bool nb8 = ord[0].K / KQ_QK == 8, m8 = ord[0].M <= 8;
+    return nb8 ? (m8 ? launch_shot<8, 8>(a, grid, lds, s) : launch_shot<8, 16>(a, grid, lds, s))
+               : (m8 ? launch_shot<16, 8>(a, grid, lds, s) : launch_shot<16, 16>(a, grid, lds, s));
 }
 
 // K slices a launch of this group would take given the workspace (1: whole
