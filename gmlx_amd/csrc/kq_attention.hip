@@ -343,14 +343,38 @@ struct KVTileQ8 {
     }
 };
 
-template <int D, bool BF>
+// Query rows in LDS (QL): 16 rows of D 16-bit values, 2 D + 16 bytes apart so
+// that a fragment read of 16 rows spans every bank.  The 8-bit kernels at head
+// dim 512 keep the query there instead of in 64 VGPRs, and order each MFMA of
+// the tile math after the one before (scheduling barriers: left free, the
+// scheduler hoisted every dequantized fragment of the tile): with the query
+// in registers they spilled 228 (split) and 284 (cascade) bytes per lane, with
+// either change alone 0-28.
+template <int D>
+constexpr uint32_t q_lds_pitch() { return 2 * D + 16; }
+template <int D>
+constexpr uint32_t q_lds_bytes() { return 16 * q_lds_pitch<D>(); }
+template <int D, bool Q8>
+constexpr bool q_in_lds() { return Q8 && D > 256; }
+
+
+template <int D, bool BF, bool QL = false>
 struct SplitState {
     static constexpr int NC = D / 32;
     static constexpr int NG = (D + 127) / 128;
-    half8_t qf[NC];
+    half8_t qf[QL ? 1 : NC];
+    uint32_t qrow;  // QL: LDS byte address of the lane's query row (column r)
     floatx4 o[NG][8];
     float m_run;   // running max (log2 domain), same on the 4 lanes of a head
     float l_part;  // this lane's share of the running sum
+
+    __device__ __forceinline__ half8_t qfrag(int c, int g) const {
+        if constexpr (QL)
+            return __builtin_bit_cast(
+                half8_t, *(const __attribute__((address_space(3))) u32x4 *)(uintptr_t)(qrow + 2u * (32 * c + 8 * g)));
+        else
+            return qf[c];
+    }
 
     template <class Tile>
     __device__ __forceinline__ void tile(const Tile &kv, int t0, int t_end, bool head_ok, float scale_log2) {
@@ -363,7 +387,10 @@ struct SplitState {
         for (int ch = 0; ch < CH; ++ch) {
             floatx4 acc = {0, 0, 0, 0};
 #pragma unroll
-            for (int c = 0; c < NC; ++c) acc = mfma<BF>(kv.kfrag(ch, c), qf[c], acc);
+            for (int c = 0; c < NC; ++c) {
+                acc = mfma<BF>(kv.kfrag(ch, c), qfrag(c, g), acc);
+                if constexpr (QL) __builtin_amdgcn_sched_barrier(0);  // (see q_lds_pitch)
+            }
             sc[ch] = acc;
         }
         // ---- online softmax over this lane's 8 scores (head r); a
@@ -410,6 +437,7 @@ struct SplitState {
                 f.w = __builtin_amdgcn_perm(vr[7][j >> 1], vr[6][j >> 1], sel);
                 const floatx4 acc = o[dg][j] * alpha;
                 o[dg][j] = mfma<BF>(__builtin_bit_cast(half8_t, f), pf, acc);
+                if constexpr (QL) __builtin_amdgcn_sched_barrier(0);  // (see q_lds_pitch)
             }
         }
         // o is read by VALU at the next tile (rescale) or after the loop
@@ -467,26 +495,43 @@ __device__ __forceinline__ void load_tile(typename TileOf<D, BF, Q8>::type &t, c
         t.load((const uint16_t *)src.k, (const uint16_t *)src.v, t0, t_end);
 }
 
+// q_lds: the wave's query region (q_lds_bytes<D>() of LDS) when
+// q_in_lds<D, Q8>(), else unused.
 template <int D, bool BF, int NBUF, int NRB, bool Q8>
 __device__ __forceinline__ void split_unit(const SdpaArgs &a, const KvSrc &src, int t_begin,
                                            int t_end, int h, int s, const int (&row)[NRB],
-                                           const int (&head)[NRB], const bool (&ok)[NRB]) {
+                                           const int (&head)[NRB], const bool (&ok)[NRB], uint32_t q_lds) {
     constexpr int NC = D / 32;
     constexpr int NG = (D + 127) / 128;
+    constexpr bool QL = q_in_lds<D, Q8>();
+    static_assert(!QL || NRB == 1, "one query block per wave in LDS");
     const int lane = kq_lane();
     const int g = lane >> 4;
 
-    SplitState<D, BF> st[NRB];
+    SplitState<D, BF, QL> st[NRB];
 #pragma unroll
     for (int j = 0; j < NRB; ++j) {
         // q^T fragments: lane (column r, group g) holds q[32c + 8g .. +7]
         const uint16_t *qp = a.q + qo_index(a, row[j], h * a.G + head[j]) * D;
+        if constexpr (QL) {
+            // each lane writes its own fragments of row r; the wave reads
+            // them back after its LDS writes complete
+            st[j].qrow = q_lds + (uint32_t)(lane & 15) * q_lds_pitch<D>();
 #pragma unroll
-        for (int c = 0; c < NC; ++c)
-            st[j].qf[c] = __builtin_bit_cast(half8_t, *(const u32x4 *)(qp + 32 * c + 8 * g));
-        if (!ok[j]) {
+            for (int c = 0; c < NC; ++c) {
+                const u32x4 v = ok[j] ? *(const u32x4 *)(qp + 32 * c + 8 * g) : u32x4{0u, 0u, 0u, 0u};
+                *(__attribute__((address_space(3))) u32x4 *)(uintptr_t)(st[j].qrow + 2u * (32 * c + 8 * g)) = v;
+            }
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+            __builtin_amdgcn_wave_barrier();
+        } else {
 #pragma unroll
-            for (int c = 0; c < NC; ++c) st[j].qf[c] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+            for (int c = 0; c < NC; ++c)
+                st[j].qf[c] = __builtin_bit_cast(half8_t, *(const u32x4 *)(qp + 32 * c + 8 * g));
+            if (!ok[j]) {
+#pragma unroll
+                for (int c = 0; c < NC; ++c) st[j].qf[c] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+            }
         }
 #pragma unroll
         for (int dg = 0; dg < NG; ++dg)
@@ -568,8 +613,21 @@ __device__ __forceinline__ void split_unit(const SdpaArgs &a, const KvSrc &src, 
 
 // Ragged mode: unit = one wave = (row b, kv head h, split s), the G q heads
 // of the group in columns 0..G-1.
+//
+// Register budget: left alone the compiler gives a wave ~290 of the SIMD's
+// 512 registers (one wave per SIMD).  A 16-bit wave keeps one 16 KB tile in
+// flight, enough for the four waves of a CU to stream at HBM rate (C3: 0.71
+// of 8 TB/s); an 8-bit tile is half the bytes, and at one wave per SIMD the
+// 8-bit C3 batch ran at 4.2-4.3 TB/s.  8-bit kernels at head dim <= 128
+// therefore ask for two waves per SIMD (249 VGPRs, no AGPRs, no scratch):
+// 0.250 -> 0.224-0.229 ms on C3 (measured).  Three waves spill 416 B per
+// lane; two waves with a three-tile ring spill 88 B; the 16-bit kernel at two
+// waves measured the same as at one.
 template <int D, bool BF, int NBUF, bool Q8>
-__global__ __launch_bounds__(64) void kq_sdpa_split_kernel(SdpaArgs a) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(Q8 && D <= 128 ? 2 : 1))) void kq_sdpa_split_kernel(
+    SdpaArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t qs[q_in_lds<D, Q8>() ? q_lds_bytes<D>() : 16];
+    const uint32_t q_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)qs;
     const int r = kq_lane() & 15;
     for (int u = blockIdx.x;; u += gridDim.x) {
         int b, h, s;
@@ -581,7 +639,7 @@ __global__ __launch_bounds__(64) void kq_sdpa_split_kernel(SdpaArgs a) {
         const int rw[1] = {b}, hd[1] = {r < a.G ? r : 0};
         const bool ok[1] = {r < a.G};
         split_unit<D, BF, NBUF, 1, Q8>(a, kv_src<Q8>(a.k, a.v, a.ks, a.kb, a.vs, a.vb, kvbase), t_begin, t_end, h, s,
-                                       rw, hd, ok);
+                                       rw, hd, ok, q_lds);
     }
 }
 
@@ -598,8 +656,11 @@ __global__ __launch_bounds__(64) void kq_sdpa_split_kernel(SdpaArgs a) {
 //    0..n1-1 of a row are the prefix's, n1.. the slab's.
 template <int D, bool BF, int NBUF, int NRB, bool Q8>
 __global__ __launch_bounds__(256) void kq_sdpa_cascade_kernel(SdpaArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t qs[q_in_lds<D, Q8>() ? 4 * q_lds_bytes<D>() : 16];
     const int r = kq_lane() & 15;
     const int W = blockDim.x >> 6, w = threadIdx.x >> 6;
+    const uint32_t q_lds =
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)qs + (uint32_t)w * q_lds_bytes<D>();
     const int R = 16 / a.G;
     const int nrb = (a.B + R - 1) / R;
     const int ngrp = (nrb + NRB - 1) / NRB;
@@ -622,7 +683,7 @@ __global__ __launch_bounds__(256) void kq_sdpa_cascade_kernel(SdpaArgs a) {
                     hd[j] = ok[j] ? r - jr * a.G : 0;
                 }
                 split_unit<D, BF, NBUF, NRB, Q8>(a, kv_src<Q8>(a.k, a.v, a.ks, a.kb, a.vs, a.vb, kvbase), t_begin,
-                                                 t_end, h, s, rw, hd, ok);
+                                                 t_end, h, s, rw, hd, ok, q_lds);
             }
         } else {
             const int64_t u2 = (bu - U1) * W + w;
@@ -638,7 +699,7 @@ __global__ __launch_bounds__(256) void kq_sdpa_cascade_kernel(SdpaArgs a) {
             const int rw[1] = {b}, hd[1] = {r < a.G ? r : 0};
             const bool ok[1] = {r < a.G};
             split_unit<D, BF, NBUF, 1, Q8>(a, kv_src<Q8>(a.k2, a.v2, a.ks2, a.kb2, a.vs2, a.vb2, kvbase), t_begin,
-                                           t_end, h, a.n1 + s, rw, hd, ok);
+                                           t_end, h, a.n1 + s, rw, hd, ok, q_lds);
         }
     }
 }
