@@ -2419,7 +2419,8 @@ bool kq_stream_eligible(const kq_matmul_problem *ps, int n, int split) {
     // launch (tests).  At 9..16 rows likewise (gate|up: 18.4 / 18.7 us at 12
     // / 16 rows against 19.1 / 20.4; the down projection in 12-block slices:
     // 18.1 / 19.2 against 22.1 / 23.8 for the general kernel).  A Q4_K + Q6_K
-    // group comes here split in two (q|k|v: 768 items, 3 per CU).
+    // group comes here split in two (768 items, 3 per CU, for a q|k|v group);
+    // the one-shot kernel, tried first, now takes q|k|v and o at 1..16 rows.
     if (!(env && env[0] == '2' && env[1] == 0)) {
         if (mixed) {
             if (split < 2 || tiles * split < 2 * (int64_t)device_cus()) return false;
