@@ -104,16 +104,18 @@ def make_inputs(torch, rng, B):
 # take the one-shot kernel (every wave copies one super-block column of its
 # workgroup's tiles and its activation slab into LDS at entry and multiplies
 # as soon as its own loads land; one barrier before the partial-tile sum; at
-# 9..16 rows the activation slab is copied in two passes of 8 rows).
+# 9..16 rows the activation slab is copied in two passes of 8 rows; at
+# 17..32 rows two 16-row blocks run one after the other through the same
+# slab, the columns staying in LDS).
 # At B = 9..16 gate|up and down take the streaming kernel's 16-row forms
 # (down in four K slices of 12 super-blocks).
-# At B = 17..64 q|k|v, gate|up and down take the mid-batch streaming kernel
+# At B = 17..64 gate|up and down (and q|k|v past 32 rows) take the mid-batch streaming kernel
 # (four waves copy each super-block of the activation rows and of a group of
 # six weight tiles into an LDS ring, six waves each accumulate one tile over
 # the group's K slice): gate|up unsplit (256 groups), down in five K slices,
 # q|k|v in three, the last slice of each tile summing the partial tiles; o
-# takes the 17..64-row tile kernel (one 4-wave workgroup per CU per weight
-# tile); past 64 rows the general kernel.
+# past 32 rows takes the 17..64-row tile kernel (one 4-wave workgroup per CU
+# per weight tile); past 64 rows the general kernel.
 LAUNCHES = [("qkv", ("q", "k", "v")), ("o", ("o",)), ("gate_up", ("gate", "up")), ("down", ("down",))]
 CODEC = {name: codec for name, _, _, codec in LAYER}
 DIMS = {name: (N, K) for name, N, K, _ in LAYER}
@@ -129,9 +131,12 @@ def kernel_of(launch, B):
     if B > 64:
         return dense
     if B > 16:
+        # up to 32 rows q|k|v and o take the one-shot kernel's 32-row form (two 16-row blocks);
         # kq_mms_kernel<codec (12 Q4_K, 14 Q6_K, 127 both), 16-row blocks, tiles per group, ring slots>
         # (q|k|v in 3 K slices, down in 5, gate|up unsplit); o: kq_mm_kernel<codec set (0 Q4_K),
         # 16-row blocks, fp16, tiles per group>
+        if B <= 32 and launch in ("qkv", "o"):
+            return "kq_shot_kernel<16, 32>"
         return {"qkv": f"kq_mms_kernel<127, {mt}, 6, {4 if mt == 2 else 2}>", "o": f"kq_mm_kernel<0, {mt}, 0, 1>",
                 "gate_up": f"kq_mms_kernel<12, {mt}, 6, {4 if mt == 2 else 3}>",
                 "down": f"kq_mms_kernel<14, {mt}, 6, {4 if mt == 2 else 2}>"}[launch]

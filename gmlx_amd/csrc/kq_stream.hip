@@ -878,7 +878,7 @@ bool stream_k_ok(int K) {
 
 // ---- One-shot kernel: a workgroup's whole share in LDS at once --------------
 // Launches of at most two 16-row tiles per CU (the o and q|k|v projections of
-// a decode step at up to 16 rows).  Every wave owns one super-block column of
+// a decode step at up to 32 rows).  Every wave owns one super-block column of
 // the workgroup's tiles (NB = 16: super-block `wave` of each tile; NB = 8:
 // unit `wave` = tile wave / 8, super-block wave % 8): at entry it copies that
 // column of each tile (16 rows) and the 8 activation rows of that
@@ -896,7 +896,9 @@ bool stream_k_ok(int K) {
 // A wave's region: the activation slab (8 rows x 512 bytes, each row's
 // 16-byte chunks XOR-swizzled by the row so the fragment reads of 8 rows hit
 // different banks; rows >= M read as zeros; a 16-row launch copies rows
-// 8..15 into it once lanes 0..7 hold theirs), then its columns: Q4_K rows of
+// 8..15 into it once lanes 0..7 hold theirs; a 32-row launch then runs rows
+// 16..31 as a second block through the same slab after the first block's
+// sums, reading and decoding the columns again), then its columns: Q4_K rows of
 // 144 bytes, Q6_K rows of 240 (the streaming kernel's 224-byte slot with d at
 // 222, and a spare chunk: 15 chunks, an odd count, so the 16 rows of an MFMA
 // operand hit different banks).
@@ -955,7 +957,8 @@ __device__ __forceinline__ void shot_copy_col(__amdgpu_buffer_rsrc_t rs, uint32_
 template <int NB, int MR>
 __global__ __launch_bounds__(64 * kShotWaves) void kq_shot_kernel(StreamArgs a_) {
     static_assert(NB == 8 || NB == 16, "one super-block column per wave and tile");
-    static_assert(MR == 8 || MR == 16, "8 or 16 activation rows");
+    static_assert(MR == 8 || MR == 16 || MR == 32, "8, 16 or 32 activation rows");
+    constexpr int MB = MR == 32 ? 2 : 1;  // 16-row blocks of the MFMA
     constexpr int UPW = NB == 16 ? 2 : 1;  // units per wave at most
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const KArgs A = (KArgs)__builtin_amdgcn_kernarg_segment_ptr();
@@ -1073,95 +1076,157 @@ __global__ __launch_bounds__(64 * kShotWaves) void kq_shot_kernel(StreamArgs a_)
     const bool has_xe = A->x_exp != nullptr;
     int ydt = A->y_dtype;
     asm volatile("" : "+s"(ydt));
-    // ---- math on the wave's units; the partial tiles into its region.  The
-    // activation part (fragment permutes, the Q4_K sub-block sums) runs as soon
-    // as the slab has landed, while the columns (issued after it) are in flight.
+    // ---- the activation fragments of block 0 (rows 0..15)
+    const uint32_t xrow = region + (uint32_t)((r & 7) * 512);
+    const int sw = r & 7;
+    const bool use4 = (live[0] && !uq6[0]) || (UPW > 1 && live[UPW - 1] && !uq6[UPW - 1]);
+    const bool use6 = (live[0] && uq6[0]) || (UPW > 1 && live[UPW - 1] && uq6[UPW - 1]);
+    half8_t x4[1][8], x6[1][8];
+    floatx4 xsum = fzero4();
+    u32x4 cin[1][8];
+    Q4Consts q4k;
+    // 32-row launches: a wave's units share one codec (the host declines
+    // workgroups that pair a Q4_K tile with a Q6_K one), so one register set
+    // holds either codec's fragments (the Q4_K runs, or the Q6_K fragments)
+    [[maybe_unused]] u32x4 xr[1][8];
+    // the lane's raw fragments from the slab (lanes of rows 8..15 of a 16-row
+    // block take theirs from the block's second pass)
+    auto read_slab = [&](bool mine) {
+        if constexpr (MR == 32) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int ch = use6 ? 4 * i + g : 8 * g + 4 * (i & 1) + (i >> 1);
+                const u32x4 v = lds128(xrow + 16u * (uint32_t)(ch ^ sw));
+                xr[0][i] = mine ? v : xr[0][i];
+            }
+            return;
+        }
+        if (use4) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+#pragma unroll
+                for (int a2 = 0; a2 < 2; ++a2) {
+                    const u32x4 v = lds128(xrow + 16u * (uint32_t)((8 * g + 4 * a2 + w) ^ sw));
+                    cin[0][2 * w + a2] = mine ? v : cin[0][2 * w + a2];
+                }
+        }
+        if (use6) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const u32x4 v = lds128(xrow + 16u * (uint32_t)((4 * t + g) ^ sw));
+                x6[0][t] = mine ? __builtin_bit_cast(half8_t, v) : x6[0][t];
+            }
+        }
+    };
     if (any) {
         int col_loads = 0;  // loads issued after the slab (they return in order)
 #pragma unroll
         for (int i = 0; i < UPW; ++i) col_loads += live[i] ? (uq6[i] ? 6 : 3) : 0;
         wait_tiles_left<1, 12>(col_loads);
-        const uint32_t xrow = region + (uint32_t)((r & 7) * 512);
-        const int sw = r & 7;
-        const bool use4 = (live[0] && !uq6[0]) || (UPW > 1 && live[UPW - 1] && !uq6[UPW - 1]);
-        const bool use6 = (live[0] && uq6[0]) || (UPW > 1 && live[UPW - 1] && uq6[UPW - 1]);
-        half8_t x4[1][8], x6[1][8];
-        floatx4 xsum = fzero4();
-        u32x4 cin[1][8];
-        // the lane's raw fragments from the slab (lanes of rows 8..15 of a
-        // 16-row launch take theirs from the second pass)
-        auto read_slab = [&](bool mine) {
-            if (use4) {
-#pragma unroll
-                for (int w = 0; w < 4; ++w)
-#pragma unroll
-                    for (int a2 = 0; a2 < 2; ++a2) {
-                        const u32x4 v = lds128(xrow + 16u * (uint32_t)((8 * g + 4 * a2 + w) ^ sw));
-                        cin[0][2 * w + a2] = mine ? v : cin[0][2 * w + a2];
-                    }
-            }
-            if (use6) {
-#pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    const u32x4 v = lds128(xrow + 16u * (uint32_t)((4 * t + g) ^ sw));
-                    x6[0][t] = mine ? __builtin_bit_cast(half8_t, v) : x6[0][t];
-                }
-            }
-        };
         read_slab(true);
-        if constexpr (MR == 16) {
+        if constexpr (MR >= 16) {
             __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the first pass's reads are done
             copy_slab(8);
             __builtin_amdgcn_s_waitcnt(KQ_VMCNT(0));  // (the columns too: they were issued first)
             read_slab(r >= 8);
         }
-        if (use4) q4own_x<1>(x4, xsum, cin, lane);
-        const Q4Consts q4k = q4own_consts(g);
-        const Iq2Tables &no_tab = *IqTables<KQ_CODEC_Q4_K>::get();
-        __builtin_amdgcn_s_waitcnt(KQ_VMCNT(0));  // the columns
-        floatx4 acc[UPW];
-#pragma unroll
-        for (int i = 0; i < UPW; ++i) {
-            acc[i] = fzero4();
-            if (!live[i]) continue;
-            if (uq6[i])
-                mma_slab<KQ_CODEC_Q6_K, 1>(acc[i], ucol[i] + (uint32_t)(r * 240), x6, xsum, g, no_tab);
-            else
-                q4own_slab<1>(acc[i], (LDSP(const uint8_t))(uintptr_t)(ucol[i] + (uint32_t)(r * 144)), x4, xsum, q4k);
-        }
-        kq_mfma_drain();
-        // rows 4 g + e < MR live in lanes g < MR / 4; partial of tile j at region + 64 MR j
-#pragma unroll
-        for (int i = 0; i < UPW; ++i)
-            if (live[i] && g < MR / 4)
-                *(LDSP(floatx4))(uintptr_t)(region + (uint32_t)(64 * MR) * (uint32_t)uj[i] + 16u * lane) = acc[i];
+        q4k = q4own_consts(g);
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    // ---- tile j: threads 16 MR j .. 16 MR j + 16 MR - 1, output (m, n) =
-    // (t >> 4, t & 15) of the tile, summed over its super-blocks in order
-    const int tid = (int)threadIdx.x, j = tid / (16 * MR), tt = tid % (16 * MR);
-    if (j < nt) {
-        const int m = tt >> 4, n = tt & 15;
-        const uint32_t at =
-            (uint32_t)(64 * MR) * (uint32_t)j + 16u * (uint32_t)((m >> 2) * 16 + n) + 4u * (uint32_t)(m & 3);
-        const uint32_t rb = (uint32_t)shot_region(NB, cb0, cb1);
-        const uint32_t base = (uint32_t)(uintptr_t)(LDSP(void))smem + at;
-        float v[NB];
+    // ---- per 16-row block (two for 32-row launches: rows 16..31 are copied
+    // into the slab once block 0's partial tiles have been summed, then the
+    // columns are read and decoded again): math on the wave's units, the
+    // partial tiles into its region, one barrier, the sums.  The activation
+    // part (fragment permutes, the Q4_K sub-block sums) runs as soon as the
+    // slab has landed, while the columns (issued after it) are in flight.
+    constexpr int RB = MR < 16 ? MR : 16;  // rows per block
 #pragma unroll
-        for (int k = 0; k < NB; ++k) {
-            const int w = (j * NB + k) & (kShotWaves - 1);  // the wave holding unit (j, k)
-            v[k] = *(const LDSP(float))(uintptr_t)(base + (uint32_t)w * rb);
+    for (int mb = 0; mb < MB; ++mb) {
+        // (the scheduler would otherwise mix the blocks' live ranges: spills)
+        __builtin_amdgcn_sched_barrier(0);
+        if (any) {
+            if (mb == 1) {
+                copy_slab(16);
+                __builtin_amdgcn_s_waitcnt(KQ_VMCNT(0));
+                read_slab(true);
+                __builtin_amdgcn_s_waitcnt(0xC07F);
+                copy_slab(24);
+                __builtin_amdgcn_s_waitcnt(KQ_VMCNT(0));
+                read_slab(r >= 8);
+            }
+            const Iq2Tables &no_tab = *IqTables<KQ_CODEC_Q4_K>::get();
+            floatx4 acc[UPW];
+#pragma unroll
+            for (int i = 0; i < UPW; ++i) acc[i] = fzero4();
+            if constexpr (MR == 32) {
+                // one codec per wave: the branch keeps one fragment set live
+                if (use6) {
+                    half8_t xf[1][8];
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) xf[0][t] = __builtin_bit_cast(half8_t, xr[0][t]);
+                    __builtin_amdgcn_s_waitcnt(KQ_VMCNT(0));  // the columns
+#pragma unroll
+                    for (int i = 0; i < UPW; ++i)
+                        if (live[i])
+                            mma_slab<KQ_CODEC_Q6_K, 1>(acc[i], ucol[i] + (uint32_t)(r * 240), xf, xsum, g, no_tab);
+                } else {
+                    q4own_x<1>(x4, xsum, xr, lane);
+                    __builtin_amdgcn_s_waitcnt(KQ_VMCNT(0));  // the columns
+#pragma unroll
+                    for (int i = 0; i < UPW; ++i)
+                        if (live[i])
+                            q4own_slab<1>(acc[i], (LDSP(const uint8_t))(uintptr_t)(ucol[i] + (uint32_t)(r * 144)), x4,
+                                          xsum, q4k);
+                }
+            } else {
+                if (use4) q4own_x<1>(x4, xsum, cin, lane);
+                __builtin_amdgcn_s_waitcnt(KQ_VMCNT(0));  // the columns
+#pragma unroll
+                for (int i = 0; i < UPW; ++i) {
+                    if (!live[i]) continue;
+                    if (uq6[i])
+                        mma_slab<KQ_CODEC_Q6_K, 1>(acc[i], ucol[i] + (uint32_t)(r * 240), x6, xsum, g, no_tab);
+                    else
+                        q4own_slab<1>(acc[i], (LDSP(const uint8_t))(uintptr_t)(ucol[i] + (uint32_t)(r * 144)), x4,
+                                      xsum, q4k);
+                }
+            }
+            kq_mfma_drain();
+            // block rows 4 g + e < RB live in lanes g < RB / 4; partial of tile j
+            // at region + 64 RB j (in the slab, whose fragments are in registers)
+#pragma unroll
+            for (int i = 0; i < UPW; ++i)
+                if (live[i] && g < RB / 4)
+                    *(LDSP(floatx4))(uintptr_t)(region + (uint32_t)(64 * RB) * (uint32_t)uj[i] + 16u * lane) = acc[i];
         }
-        float sum = v[0];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        // ---- tile j: threads 16 RB j .. 16 RB j + 16 RB - 1, output (m, n) =
+        // (16 mb + (t >> 4), t & 15) of the tile, summed over its super-blocks in order
+        const int tid = (int)threadIdx.x, j = tid / (16 * RB), tt = tid % (16 * RB);
+        if (j < nt) {
+            const int mr = tt >> 4, n = tt & 15, m = 16 * mb + mr;
+            const uint32_t at =
+                (uint32_t)(64 * RB) * (uint32_t)j + 16u * (uint32_t)((mr >> 2) * 16 + n) + 4u * (uint32_t)(mr & 3);
+            const uint32_t rb = (uint32_t)shot_region(NB, cb0, cb1);
+            const uint32_t base = (uint32_t)(uintptr_t)(LDSP(void))smem + at;
+            float sum = 0.f;
 #pragma unroll
-        for (int k = 1; k < NB; ++k) sum += v[k];
-        const StreamProblem &p = j == 0 ? pr[0] : pr[1];
-        const int col = (t0 + j - (j == 0 ? begin[0] : begin[1])) * 16 + n;
-        if (m < M && col < p.N) {
-            if (has_xe) sum = ldexpf(sum, A->x_exp[m]);
-            kq_store_out(p.y, ydt, (int64_t)m * p.y_stride + col, sum);
+            for (int k = 0; k < NB; ++k) {
+                const int w = (j * NB + k) & (kShotWaves - 1);  // the wave holding unit (j, k)
+                const float v = *(const LDSP(float))(uintptr_t)(base + (uint32_t)w * rb);
+                sum = k == 0 ? v : sum + v;
+            }
+            const StreamProblem &p = j == 0 ? pr[0] : pr[1];
+            const int col = (t0 + j - (j == 0 ? begin[0] : begin[1])) * 16 + n;
+            if (m < M && col < p.N) {
+                if (has_xe) sum = ldexpf(sum, A->x_exp[m]);
+                kq_store_out(p.y, ydt, (int64_t)m * p.y_stride + col, sum);
+            }
+        }
+        if (mb + 1 < MB) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            __builtin_amdgcn_s_barrier();  // the partial tiles are read: the slab is free
         }
     }
 }
@@ -2240,7 +2305,8 @@ int64_t group_tiles(const kq_matmul_problem *ps, int n) {
 
 // One-shot plan: the problems with Q4_K ones first (ord), the tiles, the
 // workgroups holding two tiles, the grid and the LDS of the largest
-// workgroup.  False when the launch is not served: more than 16 rows, K not 8
+// workgroup.  False when the launch is not served: more than 32 rows (16 at
+// K = 2048), K not 8
 // or 16 super-blocks, another codec, more than two tiles per CU, a
 // workgroup past 160 KB of LDS (two Q6_K tiles at K = 4096), 31-bit offsets.
 // GMLX_KQ_SHOT=0 declines every launch (tests and comparisons), and so does
@@ -2255,9 +2321,10 @@ bool shot_plan(const kq_matmul_problem *ps, int n, kq_matmul_problem *ord, int &
         if (e && *e) return false;
     }
     const kq_matmul_problem &q0 = ps[0];
-    if (q0.M < 1 || q0.M > 2 * kShotRows || q0.K % KQ_QK) return false;
+    if (q0.M < 1 || q0.M > 4 * kShotRows || q0.K % KQ_QK) return false;
     const int nb = q0.K / KQ_QK;
     if (nb != 8 && nb != 16) return false;
+    if (q0.M > 16 && nb != 16) return false;  // 17..32 rows: K = 4096 only
     if (((uintptr_t)q0.x & 15) != 0 || q0.x_row_stride % 8 != 0) return false;
     int no = 0;
     for (const int codec : {KQ_CODEC_Q4_K, KQ_CODEC_Q6_K})
@@ -2285,6 +2352,8 @@ bool shot_plan(const kq_matmul_problem *ps, int n, kq_matmul_problem *ord, int &
     };
     size_t worst = 0;
     for (int b = 0; b < grid; ++b) {
+        // 32-row launches: a workgroup's tiles share one codec
+        if (q0.M > 16 && b < pairs && codec_of(2 * b) != codec_of(2 * b + 1)) return false;
         const int c0 = shot_col_bytes(codec_of(b < pairs ? 2 * b : pairs + b));
         const int c1 = b < pairs ? shot_col_bytes(codec_of(2 * b + 1)) : 0;
         const size_t s = (size_t)kShotWaves * (size_t)shot_region(nb, c0, c1);
@@ -2341,9 +2410,11 @@ int kq_shot_launch(const kq_matmul_problem *ps, int n, const int32_t *x_exp, int
     a.n_problems = n;
     a.split = 1;
     a.pairs = pairs;
-    const bool nb8 = ord[0].K / KQ_QK == 8, m8 = ord[0].M <= 8;
-    return nb8 ? (m8 ? launch_shot<8, 8>(a, grid, lds, s) : launch_shot<8, 16>(a, grid, lds, s))
-               : (m8 ? launch_shot<16, 8>(a, grid, lds, s) : launch_shot<16, 16>(a, grid, lds, s));
+    const bool nb8 = ord[0].K / KQ_QK == 8;
+    const int m = ord[0].M;
+    if (nb8) return m <= 8 ? launch_shot<8, 8>(a, grid, lds, s) : launch_shot<8, 16>(a, grid, lds, s);
+    return m <= 8 ? launch_shot<16, 8>(a, grid, lds, s)
+           : m <= 16 ? launch_shot<16, 16>(a, grid, lds, s) : launch_shot<16, 32>(a, grid, lds, s);
 }
 
 // K slices a launch of this group would take given the workspace (1: whole

@@ -1,6 +1,6 @@
 """The one-shot kernel (kq_shot_kernel: a workgroup's one or two weight tiles
 and the activations in LDS at once) against the fp64 oracle: the o and
-q|k|v launches of a Qwen3-8B decode step at 1..16 rows, single and paired
+q|k|v launches of a Qwen3-8B decode step at 1..32 rows, single and paired
 tiles of each codec, partial last tiles,
 K of 8 and 16 super-blocks, prepared bf16 / fp32 activations, strided rows
 and outputs through the C ABI,
@@ -42,13 +42,13 @@ def _clean(monkeypatch):
 
 # (name, [(codec, N)], K, rows)
 CASES = [
-    ("o", [("q4_k", 4096)], 4096, [1, 3, 8, 9, 16]),
-    ("qkv", [("q4_k", 4096), ("q4_k", 1024), ("q6_k", 1024)], 4096, [1, 5, 8, 12, 16]),
+    ("o", [("q4_k", 4096)], 4096, [1, 3, 8, 9, 16, 20, 32]),
+    ("qkv", [("q4_k", 4096), ("q4_k", 1024), ("q6_k", 1024)], 4096, [1, 5, 8, 12, 16, 17, 25, 32]),
     ("q4 pairs, partial tile, K 2048", [("q4_k", 300 * 16 + 5)], 2048, [2, 8]),
     ("q6 pairs, K 2048", [("q6_k", 400 * 16)], 2048, [4]),
     ("q4 with q6 pairs, K 2048", [("q6_k", 200 * 16 + 3), ("q4_k", 200 * 16)], 2048, [7, 13]),
-    ("q6 singles", [("q6_k", 1000)], 4096, [6]),
-    ("q4 pairs", [("q4_k", 7000)], 4096, [8, 16]),
+    ("q6 singles", [("q6_k", 1000)], 4096, [6, 30]),
+    ("q4 pairs", [("q4_k", 7000)], 4096, [8, 16, 24]),
     ("q4 with q6 singles, K 2048", [("q4_k", 100 * 16 + 7), ("q6_k", 30 * 16)], 2048, [3]),
 ]
 
@@ -91,9 +91,11 @@ def test_shot_wide_range_and_one_signed_rows(monkeypatch):
     K = 4096
     wq = quantized_weights(rng, "q4_k", 1024, K)
     wv = quantized_weights(rng, "q6_k", 512, K)
-    rows = np.stack([rng.normal(0, 1e5, K), rng.normal(0, 1e-6, K), rng.normal(2e4, 1.2e4, K),
-                     rng.normal(0, 1, K)] * 3).astype(np.float32)   # 12 rows: the 16-row form
-    for dt, tol in ((torch.float32, TOL), (torch.bfloat16, TOL)):
+    four = [rng.normal(0, 1e5, K), rng.normal(0, 1e-6, K), rng.normal(2e4, 1.2e4, K), rng.normal(0, 1, K)]
+    # 12 rows: the 16-row form; 28 rows: the 32-row form
+    for rows, dt, tol in ((np.stack(four * 3).astype(np.float32), torch.float32, TOL),
+                          (np.stack(four * 3).astype(np.float32), torch.bfloat16, TOL),
+                          (np.stack(four * 7).astype(np.float32), torch.bfloat16, TOL)):
         xt = torch.from_numpy(rows).to(dt)
         xr = xt.float().numpy()
         xd = xt.cuda()  # one activation tensor shared by both problems
@@ -137,14 +139,15 @@ def test_shot_strided_rows_and_outputs_through_the_c_abi(monkeypatch):
 
 
 def test_shot_declines_past_its_shapes(monkeypatch):
-    """17 rows, K of 12 or 48 super-blocks, more than two tiles per CU and
-    paired Q6_K tiles at K = 4096 (past 160 KB of LDS) take the other kernels
-    (and GMLX_KQ_SHOT=0 declines), with the same numerics."""
+    """33 rows, 17 rows at K = 2048, K of 12 or 48 super-blocks, more than
+    two tiles per CU and paired Q6_K tiles at K = 4096 (past 160 KB of LDS)
+    take the other kernels (and GMLX_KQ_SHOT=0 declines), with the same
+    numerics."""
     import torch
     from gmlx_amd import ops
     _clean(monkeypatch)
     rng = np.random.default_rng(7)
-    for M, N, K, c in ((17, 512, 4096, "q4_k"), (8, 256, 12288, "q4_k"), (8, 16 * 600, 2048, "q4_k"),
+    for M, N, K, c in ((33, 512, 4096, "q4_k"), (17, 512, 2048, "q4_k"), (8, 256, 12288, "q4_k"), (8, 16 * 600, 2048, "q4_k"),
                        (4, 512, 3072, "q4_k"), (8, 16 * 300, 4096, "q6_k")):
         w = quantized_weights(rng, c, N, K)
         x16 = fp16_rows(rng, M, K)
