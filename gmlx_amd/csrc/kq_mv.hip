@@ -532,17 +532,18 @@ int launch_one(const MvArgs &a, int grid, size_t lds, hipStream_t s) {
 
 // Instantiated shapes (registers of a lane at 16 waves per CU: 128): one
 // block per wave with rings of 1..3 tiles; two or three blocks per wave with
-// rings of 1..2 tiles, except three Q6_K blocks and the XR form (ring of 1).
+// rings of 1..2 tiles, except three Q6_K blocks and the XR form (ring of 1);
+// the mixed Q4_K / Q6_K form as below.
 template <int CODEC, int XT, int WV>
 int launch_shape(const MvArgs &a, int nbw, int depth, bool xr, int grid, size_t lds, hipStream_t s) {
     if constexpr (CODEC == KQ_MIX) {
-        // mixed Q4_K / Q6_K: up to two blocks per wave, x in LDS
+        // mixed Q4_K / Q6_K: up to two blocks per wave, x in LDS; rings of
+        // one tile at two blocks and of two at one (deeper rings of both
+        // codecs' views spilled: 20 / 40 bytes per lane)
         if (xr || nbw > 2) return KQ_ERR_BAD_SHAPE;
-        if (nbw == 2) return depth == 1 ? launch_one<CODEC, XT, 2, 1, false, WV>(a, grid, lds, s)
-                                        : launch_one<CODEC, XT, 2, 2, false, WV>(a, grid, lds, s);
+        if (nbw == 2) return launch_one<CODEC, XT, 2, 1, false, WV>(a, grid, lds, s);
         if (depth == 1) return launch_one<CODEC, XT, 1, 1, false, WV>(a, grid, lds, s);
-        if (depth == 2) return launch_one<CODEC, XT, 1, 2, false, WV>(a, grid, lds, s);
-        return launch_one<CODEC, XT, 1, 3, false, WV>(a, grid, lds, s);
+        return launch_one<CODEC, XT, 1, 2, false, WV>(a, grid, lds, s);
     } else {
         if (nbw == 1) {
             if (depth == 1) return launch_one<CODEC, XT, 1, 1, false, WV>(a, grid, lds, s);

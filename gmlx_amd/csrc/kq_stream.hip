@@ -2260,10 +2260,12 @@ int launch_sgather(const SGatherArgs &a, hipStream_t s, bool dry) {
     }
 }
 
-// Consumers for K = 256 nb: one super-block each up to 12; two for 16 and 28,
+// Consumers for K = 256 nb: one super-block each up to 12; two for 16,
 // IQ2_XXS only (the K-quant views of two super-blocks, with their activation
 // reload inside the loop, run out of registers; those calls keep the
-// per-tile gather kernels).
+// per-tile gather kernels).  Forms whose workgroup of 14 or 16 waves (a
+// 128-VGPR cap) spilled to scratch decline as well: Q4_K at 12 super-blocks
+// (116 / 64 bytes per lane, GLU / plain) and IQ2_XXS at 28 (184 / 80).
 template <int CODEC, int NW>
 int sgather_codec(const SGatherArgs &a, int nb, hipStream_t s, bool dry) {
     // up to 4 super-blocks, two consumers share each (Q6_K, IQ2_XXS)
@@ -2274,12 +2276,11 @@ int sgather_codec(const SGatherArgs &a, int nb, hipStream_t s, bool dry) {
     case 4: return launch_sgather<CODEC, 1, 4 * CPB, NW, CPB>(a, s, dry);
     case 6: return launch_sgather<CODEC, 1, 6, NW>(a, s, dry);
     case 8: return launch_sgather<CODEC, 1, 8, NW>(a, s, dry);
-    case 12: return launch_sgather<CODEC, 1, 12, NW>(a, s, dry);
+    case 12:
+        if constexpr (CODEC != KQ_CODEC_Q4_K) return launch_sgather<CODEC, 1, 12, NW>(a, s, dry);
+        else return KQ_ERR_BAD_SHAPE;
     case 16:
         if constexpr (CODEC == KQ_CODEC_IQ2_XXS) return launch_sgather<CODEC, 2, 8, NW>(a, s, dry);
-        else return KQ_ERR_BAD_SHAPE;
-    case 28:
-        if constexpr (CODEC == KQ_CODEC_IQ2_XXS) return launch_sgather<CODEC, 2, 14, NW>(a, s, dry);
         else return KQ_ERR_BAD_SHAPE;
     default: return KQ_ERR_BAD_SHAPE;
     }
