@@ -958,7 +958,7 @@ template <int NB, int MR>
 __global__ __launch_bounds__(64 * kShotWaves) void kq_shot_kernel(StreamArgs a_) {
     static_assert(NB == 8 || NB == 16, "one super-block column per wave and tile");
     static_assert(MR == 8 || MR == 16 || MR == 32, "8, 16 or 32 activation rows");
-    constexpr int MB = MR == 32 ? 2 : 1;  // 16-row blocks of the MFMA
+    constexpr int MB = MR > 16 ? MR / 16 : 1;  // 16-row blocks of the MFMA
     constexpr int UPW = NB == 16 ? 2 : 1;  // units per wave at most
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const KArgs A = (KArgs)__builtin_amdgcn_kernarg_segment_ptr();
@@ -1092,7 +1092,7 @@ __global__ __launch_bounds__(64 * kShotWaves) void kq_shot_kernel(StreamArgs a_)
     // the lane's raw fragments from the slab (lanes of rows 8..15 of a 16-row
     // block take theirs from the block's second pass)
     auto read_slab = [&](bool mine) {
-        if constexpr (MR == 32) {
+        if constexpr (MR > 16) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const int ch = use6 ? 4 * i + g : 8 * g + 4 * (i & 1) + (i >> 1);
@@ -1144,12 +1144,12 @@ __global__ __launch_bounds__(64 * kShotWaves) void kq_shot_kernel(StreamArgs a_)
         // (the scheduler would otherwise mix the blocks' live ranges: spills)
         __builtin_amdgcn_sched_barrier(0);
         if (any) {
-            if (mb == 1) {
-                copy_slab(16);
+            if (mb >= 1) {
+                copy_slab(16 * mb);
                 __builtin_amdgcn_s_waitcnt(KQ_VMCNT(0));
                 read_slab(true);
                 __builtin_amdgcn_s_waitcnt(0xC07F);
-                copy_slab(24);
+                copy_slab(16 * mb + 8);
                 __builtin_amdgcn_s_waitcnt(KQ_VMCNT(0));
                 read_slab(r >= 8);
             }
@@ -1157,7 +1157,11 @@ __global__ __launch_bounds__(64 * kShotWaves) void kq_shot_kernel(StreamArgs a_)
             floatx4 acc[UPW];
 #pragma unroll
             for (int i = 0; i < UPW; ++i) acc[i] = fzero4();
-            if constexpr (MR == 32) {
+            // the lane's row, opaque per block: left to itself, the compiler kept
+            // its products live across the blocks and spilled them
+            int r = lane & 15;
+            asm volatile("" : "+v"(r));
+            if constexpr (MR > 16) {
                 // one codec per wave: the branch keeps one fragment set live
                 if (use6) {
                     half8_t xf[1][8];
@@ -1203,7 +1207,9 @@ __global__ __launch_bounds__(64 * kShotWaves) void kq_shot_kernel(StreamArgs a_)
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
         // ---- tile j: threads 16 RB j .. 16 RB j + 16 RB - 1, output (m, n) =
         // (16 mb + (t >> 4), t & 15) of the tile, summed over its super-blocks in order
-        const int tid = (int)threadIdx.x, j = tid / (16 * RB), tt = tid % (16 * RB);
+        int tid = (int)threadIdx.x;
+        asm volatile("" : "+v"(tid));  // (recomputed per block, as r above)
+        const int j = tid / (16 * RB), tt = tid % (16 * RB);
         if (j < nt) {
             const int mr = tt >> 4, n = tt & 15, m = 16 * mb + mr;
             const uint32_t at =
@@ -1227,6 +1233,7 @@ __global__ __launch_bounds__(64 * kShotWaves) void kq_shot_kernel(StreamArgs a_)
         if (mb + 1 < MB) {
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
             __builtin_amdgcn_s_barrier();  // the partial tiles are read: the slab is free
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 }
@@ -2322,6 +2329,8 @@ bool shot_plan(const kq_matmul_problem *ps, int n, kq_matmul_problem *ord, int &
         if (e && *e) return false;
     }
     const kq_matmul_problem &q0 = ps[0];
+    // (four 16-row blocks measured slower than the mid-batch kernels at 64 rows:
+    // q|k|v 20.5 against 20.4 us, o 16.0 against 14.6)
     if (q0.M < 1 || q0.M > 4 * kShotRows || q0.K % KQ_QK) return false;
     const int nb = q0.K / KQ_QK;
     if (nb != 8 && nb != 16) return false;
@@ -2353,7 +2362,7 @@ bool shot_plan(const kq_matmul_problem *ps, int n, kq_matmul_problem *ord, int &
     };
     size_t worst = 0;
     for (int b = 0; b < grid; ++b) {
-        // 32-row launches: a workgroup's tiles share one codec
+        // 17..32-row launches: a workgroup's tiles share one codec
         if (q0.M > 16 && b < pairs && codec_of(2 * b) != codec_of(2 * b + 1)) return false;
         const int c0 = shot_col_bytes(codec_of(b < pairs ? 2 * b : pairs + b));
         const int c1 = b < pairs ? shot_col_bytes(codec_of(2 * b + 1)) : 0;
