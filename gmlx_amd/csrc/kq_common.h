@@ -109,6 +109,33 @@ __device__ __forceinline__ uint32_t kq_h2_bits(half2_t h) { return __builtin_bit
 
 __device__ __forceinline__ int kq_lane() { return (int)__lane_id(); }
 
+// Calls f(p), uniformly over the wave and in pair order, for every pair p < n
+// whose flag (the routing tables' per-pair expert, -1 when out of range) is
+// negative.  The flags are read 1024 at a time, one independent load per lane
+// and batch slot, and found by ballots: a loop of one dependent load per four
+// pairs and lane took ~7 us for 256 pairs, the tail of a MoE gather.
+template <class F>
+__device__ __forceinline__ void kq_for_unrouted(const int32_t *flag, int n, F &&f) {
+    const int lane = kq_lane();
+    for (int base = 0; base < n; base += 64 * 16) {
+        bool neg[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int p = base + 64 * i + lane;
+            neg[i] = p < n && flag[p] < 0;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            uint64_t m = __builtin_amdgcn_ballot_w64(neg[i]);
+            while (m) {
+                const int j = __builtin_ctzll(m);
+                m &= m - 1;
+                f(base + 64 * i + j);
+            }
+        }
+    }
+}
+
 // Ordering point between the MFMAs of an accumulation loop body and any VALU
 // / accvgpr read of their accumulators after the loop's back edge: 24
 // explicit wait states, more than any 16x16x32 MFMA result latency.  Placed at

@@ -238,14 +238,13 @@ __attribute__((amdgpu_waves_per_eu(gather_waves_per_simd<CODEC, MT, NW, XT>())))
     const int r = lane & 15;
     const int slot = blockIdx.x / a.n_tiles;
     const int nt = blockIdx.x - slot * a.n_tiles;
-    if (slot == 0) {
+    if (slot == 0 && wave == 0) {
         // pairs whose expert id is out of range (never routed) get zeros in
         // this tile's columns
-        const int32_t *flag = a.pair_order + a.n_pairs;
-        const int c = nt * 16 + (threadIdx.x & 15);
-        if (c < a.N)
-            for (int p = threadIdx.x >> 4; p < a.n_pairs; p += 4 * kGatherWaves)
-                if (flag[p] < 0) kq_store_out(a.y, a.y_dtype, gather_y_row(a, p) * a.y_stride + c, 0.f);
+        const int c = nt * 16 + (lane & 15);
+        kq_for_unrouted(a.pair_order + a.n_pairs, a.n_pairs, [&](int p) {
+            if (lane < 16 && c < a.N) kq_store_out(a.y, a.y_dtype, gather_y_row(a, p) * a.y_stride + c, 0.f);
+        });
     }
     const int S = a.seg_info[0];
     if (slot >= S) return;  // uniform over the workgroup
@@ -368,11 +367,10 @@ __attribute__((amdgpu_waves_per_eu(gather_waves_per_simd<CODEC, MT, NW, XT>())))
     if (slot == 0) {
         // pairs whose expert id is out of range (never routed) get zeros in
         // this tile's columns
-        const int32_t *flag = a.pair_order + a.n_pairs;
         const int c = nt * 16 + r;
-        if (c < a.N)
-            for (int p = lane >> 4; p < a.n_pairs; p += 4)
-                if (flag[p] < 0) kq_store_out(a.y, a.y_dtype, gather_y_row(a, p) * a.y_stride + c, 0.f);
+        kq_for_unrouted(a.pair_order + a.n_pairs, a.n_pairs, [&](int p) {
+            if (lane < 16 && c < a.N) kq_store_out(a.y, a.y_dtype, gather_y_row(a, p) * a.y_stride + c, 0.f);
+        });
     }
     if (slot >= S) return;  // uniform over the wave
     const int expert = a.seg_info[1 + slot];

@@ -2212,14 +2212,14 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_sgather_kernel(SGath
     }
     // pairs whose expert id is out of range (never routed): zeros in their
     // rows, columns of tiles blockIdx.x, blockIdx.x + G, ...
-    if (c == 0) {
-        const int32_t *flag = A->pair_order + A->n_pairs;
-        for (int t = blockIdx.x; t < A->n_tiles; t += G) {
-            const int nn = t * 16 + n;
-            if (nn >= A->N) continue;
-            for (int p = mq; p < A->n_pairs; p += 4)
-                if (flag[p] < 0) kq_store_out(A->y, A->y_dtype, sg_y_row(A, p) * A->y_stride + nn, 0.f);
-        }
+    if (c == 0 && (int)blockIdx.x < A->n_tiles) {
+        kq_for_unrouted(A->pair_order + A->n_pairs, A->n_pairs, [&](int p) {
+            if (lane >= 16) return;
+            for (int t = blockIdx.x; t < A->n_tiles; t += G) {
+                const int nn = t * 16 + n;
+                if (nn < A->N) kq_store_out(A->y, A->y_dtype, sg_y_row(A, p) * A->y_stride + nn, 0.f);
+            }
+        });
     }
 }
 
