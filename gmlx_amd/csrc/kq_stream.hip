@@ -2036,13 +2036,20 @@ __global__ __launch_bounds__(64 * (kProducers + C)) void kq_sgather_kernel(SGath
                                                          0, 0);
             }
         };
-        const int pre = min(R, my_items);
+        // KQ_STREAM_START_TILES items first, the rest of the ring once item 0
+        // is with the consumers (every CU issuing its whole ring at once
+        // delayed the first item, as in kq_stream_kernel)
+        const int pre = min(min(KQ_STREAM_START_TILES, R), my_items);
         for (int j = 0; j < pre; ++j) copy(j);
         for (int b = 0; b < my_items; ++b) {
-            const int newer = min(b == 0 ? R - 1 : R - 2, my_items - 1 - b);
+            const int newer = b == 0 ? pre - 1 : min(R - 2, my_items - 1 - b);
             wait_tiles_left<PL, (R - 1 < 63 / PL ? R - 1 : 63 / PL)>(newer);
             __builtin_amdgcn_s_barrier();  // slot b % R to the consumers; slot (b - 1) % R back
-            if (b >= 1 && b + R - 1 < my_items) copy(b + R - 1);
+            if (b == 0) {
+                for (int j = pre; j < min(R, my_items); ++j) copy(j);
+            } else if (b + R - 1 < my_items) {
+                copy(b + R - 1);
+            }
             if ((b + 1) % TM == 0 || b + 1 == my_items) {
                 __builtin_amdgcn_s_barrier();  // the round's partial tiles are in LDS
                 if (b + 1 < my_items) __builtin_amdgcn_s_barrier();  // the round's outputs are stored: red is free
