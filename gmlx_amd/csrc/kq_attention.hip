@@ -267,16 +267,29 @@ __device__ __forceinline__ u32x4 deq8(u32x2 q, uint32_t sb) {
     }
 }
 
+// The head-dim offset of the score MFMA's chunk c in lane group g: 32 c + 8 g,
+// or with wide K loads (WK: 8-bit tiles, whose lanes then load 16 contiguous
+// values of a token per instruction, two chunks) 64 (c / 2) + 16 g + 8 (c % 2):
+// one load instruction covers 64 bytes of each of 16 token rows where
+// chunk-sized loads covered 32 (C3 over an 8-bit cache: 0.225-0.229 ->
+// 0.212-0.214 ms, measured).  The query fragments follow the same order.  The
+// bf16 cascade form with two row blocks keeps chunk-sized loads: its 512
+// registers are full, and the wide loads' 128-bit tuples spilled 12 bytes.
+template <bool WK>
+__device__ __forceinline__ int qk_d(int c, int g) {
+    return WK ? 64 * (c >> 1) + 16 * g + 8 * (c & 1) : 32 * c + 8 * g;
+}
+
 // One tile of an 8-bit affine-quantized KV cache (uint8 values, token rows of
-// D bytes; a 16-bit scale and bias per 64 values of a token), in the same
-// lane layout as KVTile; values are dequantized at their use.  The tile's
-// TT x SG (token, group) scale / bias pairs are loaded once, pair p = 64 j +
-// l by lane l into slot j (one 2-byte load of each array per lane and slot,
-// where one load per value chunk made the 8-bit cache as slow as the 16-bit
-// one), and a fragment takes its pair from the owning lane (ds_bpermute).
-// Tokens past the row's end are clamped to its last token, for the values
-// and their pairs alike.
-template <int D, bool BF>
+// D bytes; a 16-bit scale and bias per 64 values of a token), in the lane
+// layout of KVTile except for K's head-dim order (qk_d<WK>); values are
+// dequantized at their use.  The tile's TT x SG (token, group) scale / bias
+// pairs are loaded once, pair p = 64 j + l by lane l into slot j (one 2-byte
+// load of each array per lane and slot, where one load per value chunk made
+// the 8-bit cache as slow as the 16-bit one), and a fragment takes its pair
+// from the owning lane (ds_bpermute).  Tokens past the row's end are clamped
+// to its last token, for the values and their pairs alike.
+template <int D, bool BF, bool WK>
 struct KVTileQ8 {
     static constexpr int NC = D / 32;
     static constexpr int NG = (D + 127) / 128;
@@ -284,7 +297,7 @@ struct KVTileQ8 {
     static constexpr int TT = TileTok<D>::TT, CH = TileTok<D>::CH, VT = TileTok<D>::VT;
     static constexpr int NP = TT * SG;         // (token, group) pairs of a tile
     static constexpr int PJ = (NP + 63) / 64;  // pair slots per lane
-    u32x2 k[CH][NC];
+    u32x2 k[CH][NC];  // token t0 + 16 ch + r, d = qk_d<WK>(c, g) .. +7
     u32x2 v[NG][VT];
     uint32_t ksb[PJ], vsb[PJ];  // pair 64 j + lane: scale | bias << 16
     int tlast;                  // the tile's last valid token (local index)
@@ -297,8 +310,17 @@ struct KVTileQ8 {
 #pragma unroll
         for (int ch = 0; ch < CH; ++ch) {
             const int tok = min(t0 + 16 * ch + r, t_end - 1);
+            if constexpr (WK) {
 #pragma unroll
-            for (int c = 0; c < NC; ++c) k[ch][c] = *(const u32x2 *)(kp + (int64_t)tok * D + 32 * c + 8 * g);
+                for (int i = 0; i < NC / 2; ++i) {
+                    const u32x4 w = *(const u32x4 *)(kp + (int64_t)tok * D + 64 * i + 16 * g);
+                    k[ch][2 * i] = u32x2{w.x, w.y};
+                    k[ch][2 * i + 1] = u32x2{w.z, w.w};
+                }
+            } else {
+#pragma unroll
+                for (int c = 0; c < NC; ++c) k[ch][c] = *(const u32x2 *)(kp + (int64_t)tok * D + qk_d<WK>(c, g));
+            }
         }
 #pragma unroll
         for (int dg = 0; dg < NG; ++dg) {
@@ -330,7 +352,7 @@ struct KVTileQ8 {
     }
     __device__ __forceinline__ half8_t kfrag(int ch, int c) const {
         const int r = kq_lane() & 15;
-        // values 32 c + 8 g .. +7 lie in group c / 2
+        // values qk_d<WK>(c, g) .. +7 lie in group c / 2
         return __builtin_bit_cast(half8_t, deq8<BF>(k[ch][c], pair(ksb, min(16 * ch + r, tlast), c >> 1)));
     }
     __device__ __forceinline__ void vrows(int dg, u32x4 (&out)[8]) const {
@@ -478,17 +500,17 @@ __device__ __forceinline__ KvSrc kv_src(const void *k, const void *v, const uint
     return r;
 }
 
-template <int D, bool BF, bool Q8>
+template <int D, bool BF, bool Q8, bool WK>
 struct TileOf {
     using type = KVTile<D>;
 };
-template <int D, bool BF>
-struct TileOf<D, BF, true> {
-    using type = KVTileQ8<D, BF>;
+template <int D, bool BF, bool WK>
+struct TileOf<D, BF, true, WK> {
+    using type = KVTileQ8<D, BF, WK>;
 };
 
-template <int D, bool BF, bool Q8>
-__device__ __forceinline__ void load_tile(typename TileOf<D, BF, Q8>::type &t, const KvSrc &src, int t0, int t_end) {
+template <class Tile, bool Q8>
+__device__ __forceinline__ void load_tile(Tile &t, const KvSrc &src, int t0, int t_end) {
     if constexpr (Q8)
         t.load((const uint8_t *)src.k, (const uint8_t *)src.v, src.ks, src.kb, src.vs, src.vb, t0, t_end);
     else
@@ -505,13 +527,16 @@ __device__ __forceinline__ void split_unit(const SdpaArgs &a, const KvSrc &src, 
     constexpr int NG = (D + 127) / 128;
     constexpr bool QL = q_in_lds<D, Q8>();
     static_assert(!QL || NRB == 1, "one query block per wave in LDS");
+    constexpr bool WK = Q8 && !(BF && NRB > 1);  // wide K loads (qk_d)
+    using Tile = typename TileOf<D, BF, Q8, WK>::type;
     const int lane = kq_lane();
     const int g = lane >> 4;
 
     SplitState<D, BF, QL> st[NRB];
 #pragma unroll
     for (int j = 0; j < NRB; ++j) {
-        // q^T fragments: lane (column r, group g) holds q[32c + 8g .. +7]
+        // q^T fragments: lane (column r, group g) holds q[qk_d(c, g) .. +7]
+        // (in LDS: at fragment slot 32 c + 8 g of the lane's row)
         const uint16_t *qp = a.q + qo_index(a, row[j], h * a.G + head[j]) * D;
         if constexpr (QL) {
             // each lane writes its own fragments of row r; the wave reads
@@ -519,7 +544,7 @@ __device__ __forceinline__ void split_unit(const SdpaArgs &a, const KvSrc &src, 
             st[j].qrow = q_lds + (uint32_t)(lane & 15) * q_lds_pitch<D>();
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
-                const u32x4 v = ok[j] ? *(const u32x4 *)(qp + 32 * c + 8 * g) : u32x4{0u, 0u, 0u, 0u};
+                const u32x4 v = ok[j] ? *(const u32x4 *)(qp + qk_d<WK>(c, g)) : u32x4{0u, 0u, 0u, 0u};
                 *(__attribute__((address_space(3))) u32x4 *)(uintptr_t)(st[j].qrow + 2u * (32 * c + 8 * g)) = v;
             }
             __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
@@ -527,7 +552,7 @@ __device__ __forceinline__ void split_unit(const SdpaArgs &a, const KvSrc &src, 
         } else {
 #pragma unroll
             for (int c = 0; c < NC; ++c)
-                st[j].qf[c] = __builtin_bit_cast(half8_t, *(const u32x4 *)(qp + 32 * c + 8 * g));
+                st[j].qf[c] = __builtin_bit_cast(half8_t, *(const u32x4 *)(qp + qk_d<WK>(c, g)));
             if (!ok[j]) {
 #pragma unroll
                 for (int c = 0; c < NC; ++c) st[j].qf[c] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
@@ -546,13 +571,13 @@ __device__ __forceinline__ void split_unit(const SdpaArgs &a, const KvSrc &src, 
         // multiplied.  Loads are issued unconditionally (tokens past t_end
         // read the last valid token), so the wait counts are static.
         constexpr int TT = TileTok<D>::TT;
-        typename TileOf<D, BF, Q8>::type ring[NBUF];
+        Tile ring[NBUF];
 #pragma unroll
-        for (int j = 0; j < NBUF - 1; ++j) load_tile<D, BF, Q8>(ring[j], src, t_begin + TT * j, t_end);
+        for (int j = 0; j < NBUF - 1; ++j) load_tile<Tile, Q8>(ring[j], src, t_begin + TT * j, t_end);
         for (int t0 = t_begin; t0 < t_end; t0 += TT * NBUF) {
 #pragma unroll
             for (int j = 0; j < NBUF; ++j) {
-                load_tile<D, BF, Q8>(ring[(j + NBUF - 1) % NBUF], src, t0 + TT * (j + NBUF - 1), t_end);
+                load_tile<Tile, Q8>(ring[(j + NBUF - 1) % NBUF], src, t0 + TT * (j + NBUF - 1), t_end);
                 __builtin_amdgcn_sched_barrier(0);
                 if (t0 + TT * j < t_end) {
 #pragma unroll
