@@ -211,11 +211,13 @@ def test_left_padded_route_order():
 
 
 @pytest.mark.parametrize("qL,pads,dtype_name", [(1, [0, 64, 128, 32], "float16"), (4, [0, 64, 32], "float16"),
-                                                (1, [5, 0, 9], "bfloat16")])
+                                                (1, [5, 0, 9], "bfloat16"), (4, [5, 0, 9], "bfloat16")])
 def test_quantized_kv_cascade(qL, pads, dtype_name):
     """The 8-bit affine KV form (gmlx/cascade_sdpa.py:216-236): wire, scales
     and biases sliced from one quantized buffer the way the claim slices
-    them; against the masked fp64 reference over the dequantized buffer."""
+    them; against the masked fp64 reference over the dequantized buffer.
+    qL = 4 gives 12 query rows at G = 2: two row blocks per prefix wave (the
+    bf16 form of which keeps chunk-sized K loads)."""
     import torch
     from gmlx_amd import ops
     from helpers import q8_affine
