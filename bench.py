@@ -328,9 +328,41 @@ def timed_calls(torch, fn, n, flush=None):
     return [a.elapsed_time(b) for a, b in ev]
 
 
-def bench_sdpa(torch, ops, iters=50):
+def cpu_sdpa_baseline(q, k, v, offs, lens, Hkv, scale, budget_s=6.0):
+    """CPU figure beside C3: the oracle's OpenMP fp32 online-softmax ragged
+    attention (oracle/kq_oracle.c kqo_ragged_attn_f32) over the whole C3
+    batch (host copies of the same fp16 q, K, V), repeated until ~budget_s on
+    the host threads this process may use (as cpu_baseline)."""
+    import numpy as np
+    from oracle import kquant as okq
+    L = okq.lib()
+    B, Hq, D = q.shape
+    lens32 = np.ascontiguousarray(lens, dtype=np.int32)
+    offs64 = np.ascontiguousarray(offs, dtype=np.int64)
+    hs = lens32.astype(np.int64) * D  # one kv head's slab: len x D elements
+    out = np.empty((B, Hq, D), np.float32)
+    affinity = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS", "").strip()
+    nthreads = min(affinity, int(omp)) if omp.isdigit() and int(omp) > 0 else affinity
+    done, t0 = 0, time.perf_counter()
+    while True:
+        L.kqo_ragged_attn_f32(q.ctypes.data, k.ctypes.data, v.ctypes.data, offs64.ctypes.data, hs.ctypes.data,
+                              lens32.ctypes.data, B, Hq, Hkv, D, scale, out.ctypes.data, nthreads)
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or done >= 20:
+            break
+    kv_bytes = 2 * k.size * 2
+    return {"kv_gbs": round(done * kv_bytes / el / 1e9, 3), "unit": "GB/s",
+            "kv_tokens_per_s": round(done * int(lens.sum()) / el, 1), "cores": nthreads, "kind": "port",
+            "sample": f"{done} pass(es) of the whole C3 batch ({kv_bytes / 1e9:.2f} GB of fp16 K/V), {el:.1f} s, "
+                      f"oracle/kq_oracle.c kqo_ragged_attn_f32 (OpenMP, fp32 online softmax)"}
+
+
+def bench_sdpa(torch, ops, iters=50, cpu=False):
     """32 q heads / 8 kv heads, D 128, B 16 ragged rows in
-    per-row [Hkv, len, D] slabs (offset table), fp16, scale 1/sqrt(128)."""
+    per-row [Hkv, len, D] slabs (offset table), fp16, scale 1/sqrt(128).
+    cpu: also time the CPU restatement on the same batch (cpu_sdpa_baseline)."""
     import numpy as np
     lens, rng = c3_lengths()
     B, Hq, Hkv, D = 16, 32, 8, 128
@@ -364,6 +396,9 @@ def bench_sdpa(torch, ops, iters=50):
             ref = p @ vb / p.sum()
             got = out[b, hq].double().cpu().numpy()
             chk = max(chk, float(np.abs(got - ref).max() / np.abs(ref).max()))
+    cpu_line = None
+    if cpu:
+        cpu_line = cpu_sdpa_baseline(q.cpu().numpy(), k.cpu().numpy(), v.cpu().numpy(), offs, lens, Hkv, scale)
     # the same batch over an 8-bit affine KV cache (group 64): half the KV bytes
     q8 = {}
     kq8, vq8, scs = [], [], []
@@ -398,6 +433,7 @@ def bench_sdpa(torch, ops, iters=50):
         "rows_per_s": round(B / ms * 1e3, 1),
         "algorithmic_bytes": kv_bytes + qo_bytes,
         "max_rel_spot": chk,
+        "cpu_baseline": cpu_line,
     }
 
 
@@ -833,10 +869,13 @@ def main():
 
     sdpa = None
     if not args.no_sdpa:
-        sdpa = bench_sdpa(torch, ops)
+        sdpa = bench_sdpa(torch, ops, cpu=not args.no_cpu)
         log(f"[bench] sdpa C3: {sdpa['ms']} ms, {sdpa['kv_gbs']} GB/s, {sdpa['kv_tokens_per_s']:.3e} tok/s; "
             f"8-bit KV {sdpa['q8_kv']['ms']} ms, {sdpa['q8_kv']['kv_gbs']} GB/s, "
             f"{sdpa['q8_kv']['kv_tokens_per_s']:.3e} tok/s")
+        if sdpa["cpu_baseline"]:
+            log(f"[bench] sdpa C3 cpu baseline: {sdpa['cpu_baseline']['kv_gbs']} GB/s, "
+                f"{sdpa['cpu_baseline']['kv_tokens_per_s']:.3e} tok/s on {sdpa['cpu_baseline']['cores']} threads")
 
     cascade = None
     if not args.no_cascade:
