@@ -3,7 +3,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch B]
 
-Headline: one decode step through the linear layers of a
+Headline (workload C2): one decode step through the linear layers of a
 Qwen3-8B Q4_K_M stack -- 36 layers, each q 4096x4096, k 1024x4096,
 o 4096x4096, gate/up 12288x4096 in Q4_K and v 1024x4096, down 4096x12288 in
 Q6_K -- at B rows of fp16 activations.  Per layer the launches follow the
@@ -18,9 +18,9 @@ step (its launches of the step alone, replayed from a graph): achieved =
 algorithmic bytes per launch / average launch duration, both over the timed
 region; `traffic` = HBM bytes per launch of the same family from the
 FETCH_SIZE / WRITE_SIZE counters.  Extra fields: the per-B sweep (B = 1..64, same
-stack), ragged GQA decode attention at BASELINE config 3 (KV GB/s, KV tokens/s),
+stack), ragged GQA decode attention on workload C3 (KV GB/s, KV tokens/s),
 cascade shared-prefix decode attention beside the ragged kernel on the same
-buffer, one MoE decode layer at BASELINE configs 4 and 5 (GB/s over the touched
+buffer, one MoE decode layer on workloads C4 and C5 (GB/s over the touched
 experts' bytes) and the CPU baseline (the repository's OpenMP C restatement of the same
 dequant-fused matmul, timed on a bounded sample of the same workload).
 
@@ -360,7 +360,7 @@ def cpu_sdpa_baseline(q, k, v, offs, lens, Hkv, scale, budget_s=6.0):
 
 
 def bench_sdpa(torch, ops, iters=50, cpu=False):
-    """32 q heads / 8 kv heads, D 128, B 16 ragged rows in
+    """Workload C3: 32 q heads / 8 kv heads, D 128, B 16 ragged rows in
     per-row [Hkv, len, D] slabs (offset table), fp16, scale 1/sqrt(128).
     cpu: also time the CPU restatement on the same batch (cpu_sdpa_baseline)."""
     import numpy as np
@@ -511,7 +511,7 @@ BLOCK_BYTES = {"q4_k": 144, "q6_k": 210, "iq2_xxs": 66}
 
 
 def bench_moe(torch, ops, which, iters=50):
-    """BASELINE configs 4 and 5: one MoE decode layer (router top-k, fused
+    """Workloads C4 and C5: one MoE decode layer (router top-k, fused
     gate|up GLU gather writing h in the activation dtype, down gather with
     the routing mix folded in) over
     the tokens' ragged per-expert segments.  Router logits and x are numpy
@@ -606,7 +606,7 @@ def _cpu_model():
 
 
 def cpu_baseline(layer_wires, B, budget_s=12.0, numpy_budget_s=8.0):
-    """The CPU figures of BASELINE section 4, on one C2 layer (7 matrices,
+    """The CPU figures beside the C2 line, on one C2 layer (7 matrices,
     122.6 MB of wire) at B rows:
       value: the oracle's OpenMP dequant-fused fp32 matmul (oracle/kq_oracle.c
              kqo_qmm_f32), repeated until ~budget_s, on the host threads this

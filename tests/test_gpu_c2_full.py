@@ -1,4 +1,4 @@
-"""BASELINE config 2 at full size: the four launches of a Qwen3-8B Q4_K_M
+"""Workload C2 at full size: the four launches of a Qwen3-8B Q4_K_M
 layer (q|k|v grouped, o, gate|up grouped, down), with the default routing
 the benchmark uses, at every batch width the metric is quoted on
 (B = 1, 2, 4, 8, 16, 32, 64), against fp64 over the same wire bytes.

@@ -1,4 +1,4 @@
-"""Parity at BASELINE's full workloads, through the default launch plans (no
+"""Parity at the full C3 / C4 / C5 workloads, through the default launch plans (no
 environment overrides), against the fp64 oracle:
 
   C3  ragged GQA decode attention: 32 q heads / 8 kv heads / D 128, B = 16

@@ -25,7 +25,7 @@ def _mm(x16, wire, codec, **kw):
 
 
 def test_config1_q4k_matvec():
-    """Q4_K 3072x1024 from N(0, 0.02), x fp16 [1, 1024] N(0, 1), seed 0."""
+    """Workload C1: Q4_K 3072x1024 from N(0, 0.02), x fp16 [1, 1024] N(0, 1), seed 0."""
     rng = np.random.default_rng(0)
     w = rng.normal(0.0, 0.02, size=(3072, 1024)).astype(np.float32)
     wire = okq.quantize(w, "q4_k")
