@@ -317,19 +317,34 @@ struct XRowsLds {
     }
 };
 
-constexpr int kGatherLdsBytes = 32 * 1024;  // staged activation rows per workgroup
+// Staged activation rows per workgroup: 32 KB, or 24 KB where the kernel runs
+// five waves per SIMD (five workgroups per CU then fit the 160 KB of LDS with
+// the IQ2_XXS tables; at K = 2048 that still stages segments of five rows).
+template <int CODEC, int MT, int NW, int XT>
+constexpr int gather_wave_waves_per_simd() {
+    // single-tile fp16 forms (the per-pair down gathers): five waves in 96
+    // VGPRs, with 20 (IQ2_XXS) and 52 (Q6_K) bytes per lane spilled outside
+    // the block loop; measured 1.5 % (C4 down, Q6_K) and 3 % (C5, IQ2_XXS)
+    // faster than four waves
+    if (MT * NW * (CODEC == KQ_CODEC_Q4_K ? 2 : 1) == 1 && XT == 0) return 5;
+    return gather_waves_per_simd<CODEC, MT, NW, XT>();
+}
+template <int CODEC, int MT, int NW, int XT>
+constexpr int gather_lds_bytes() {
+    return gather_wave_waves_per_simd<CODEC, MT, NW, XT>() == 5 ? 24 * 1024 : 32 * 1024;
+}
 
 // Short K: one wave per (segment slot, tile) unit, kGatherWaves units per
 // workgroup (consecutive tiles of one expert), the whole K in the wave; no
 // cross-wave reduction.  When the workgroup's units share one segment of at
-// most 16 rows whose activations fit kGatherLdsBytes, the rows are staged in
+// most 16 rows whose activations fit gather_lds_bytes, the rows are staged in
 // LDS once for the four waves (their fragments are read from LDS instead of
 // once per tile from L2); otherwise each wave loads them from memory.
 template <int CODEC, int MT, int XT, int NW>
 __global__ __launch_bounds__(64 * kGatherWaves)
-__attribute__((amdgpu_waves_per_eu(gather_waves_per_simd<CODEC, MT, NW, XT>()))) void kq_gather_wave_kernel(GatherArgs a) {
+__attribute__((amdgpu_waves_per_eu(gather_wave_waves_per_simd<CODEC, MT, NW, XT>()))) void kq_gather_wave_kernel(GatherArgs a) {
     __shared__ Iq2Tables iq2_tab;
-    __shared__ __attribute__((aligned(16))) uint8_t xs_lds[MT == 1 ? kGatherLdsBytes : 16];
+    __shared__ __attribute__((aligned(16))) uint8_t xs_lds[MT == 1 ? gather_lds_bytes<CODEC, MT, NW, XT>() : 16];
     if constexpr (CODEC == KQ_CODEC_IQ2_XXS) load_iq2_tables(iq2_tab);
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lane = kq_lane();
@@ -348,7 +363,7 @@ __attribute__((amdgpu_waves_per_eu(gather_waves_per_simd<CODEC, MT, NW, XT>())))
         if (s0 == s3 && s0 < S) {
             const int rows = a.seg_info[1 + a.n_experts + s0 + 1] - a.seg_info[1 + a.n_experts + s0];
             xrow_bytes = (uint32_t)a.K * 2 + 16;  // padded: rows start on different banks
-            staged = rows <= 16 && (uint32_t)rows * xrow_bytes <= (uint32_t)kGatherLdsBytes;
+            staged = rows <= 16 && (uint32_t)rows * xrow_bytes <= (uint32_t)gather_lds_bytes<CODEC, MT, NW, XT>();
             if (staged) {
                 const int begin = a.seg_info[1 + a.n_experts + s0];
                 const int per_row = a.K / 8;  // 8 activations (16 bytes of fp16) per item
